@@ -1,0 +1,160 @@
+/*
+ * ssalaad_amd.h — C ABI of the MI355X (gfx950) sparse-plus-low-rank linear library.
+ *
+ *   y = x · Bᵀ · Aᵀ  +  x · Sᵀ  +  b        (S block-sparse, BSR layout)
+ *
+ * Every entry point takes raw device pointers, sizes and a hipStream_t passed as
+ * `void*`; none allocates device memory. Kernel entry points are asynchronous and
+ * ordered on `stream`. Scratch memory (`workspace`) is supplied by the caller,
+ * sized by the matching *_workspace_size query; its first `ssl_*_counter_bytes`
+ * bytes hold completion counters that must be zero before the first call and are
+ * returned to zero by every call that completes. Calls that share one workspace
+ * must be ordered (same stream); concurrent calls on one workspace race.
+ *
+ * Return value: 0 (SSL_OK) or one of the ssl_status codes below. HIP launch
+ * failures are reported as SSL_ERR_HIP; ssl_last_error() returns a message.
+ *
+ * Tensor conventions (all row-major, last dimension contiguous):
+ *   x       [M, ldx]   activations; the first m columns are used
+ *   out/y   [M, ldy]
+ *   crow    [NB + 1]   int32 block-row pointer            (BSR crow_indices)
+ *   col     [nnz]      int32 block-column index           (BSR col_indices)
+ *   values  [nnz, q, p] block values, each block TRANSPOSED to (q, p) — the layout
+ *                      the reference module stores in S_values
+ *   active  [n_active] int32 block-rows that are updated, ascending
+ *   A       [n_pad, r_pad], B [r_pad, m_pad]  low-rank factors, zero-padded
+ *   bias    [n_pad]
+ */
+#ifndef SSALAAD_AMD_H
+#define SSALAAD_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  SSL_OK = 0,
+  SSL_ERR_INVALID = 1,     /* bad pointer, size or stride (maps to ValueError)   */
+  SSL_ERR_UNSUPPORTED = 2, /* dtype / block shape without a kernel (TypeError)   */
+  SSL_ERR_WORKSPACE = 3,   /* workspace missing or too small                     */
+  SSL_ERR_HIP = 4,         /* HIP runtime error (RuntimeError)                   */
+  SSL_ERR_CAPACITY = 5     /* caller-provided host array too small               */
+} ssl_status;
+
+typedef enum { SSL_F32 = 0, SSL_BF16 = 1, SSL_F16 = 2 } ssl_dtype;
+
+/* Library version and last error message (thread-local, valid until next call). */
+int ssl_version(void);
+const char* ssl_last_error(void);
+
+/* -------------------------------------------------------------------------
+ * Work plans (host side, integer only).
+ *
+ * A plan splits the work of one BSR matrix into workgroup chunks. Each block-row
+ * contributes a list of units: its sparse blocks (cost q each) followed by `lr_units`
+ * low-rank units (cost 32 each, 32 ranks of A per unit). A row whose cost exceeds
+ * `target_cost` is split into nearly equal consecutive chunks that are summed in a
+ * fixed order on the device, so long rows of skewed matrices are spread across
+ * workgroups and results stay deterministic. `rows` lists the block-rows that
+ * get chunks (NULL = every row 0..NB-1).
+ *
+ * Table layout: SSL_PLAN_STRIDE int32 per chunk:
+ *   {row, unit_begin, unit_end, seq, nseq, slot, nblk, blk0}
+ * Returns the chunk count in *n_chunks and the partial-sum slot count in *n_slots.
+ * ------------------------------------------------------------------------- */
+#define SSL_PLAN_STRIDE 8
+int ssl_plan_build(const int32_t* crow_host, int64_t NB, const int32_t* rows_host,
+                   int64_t n_rows, int32_t block_q, int32_t lr_units, int64_t target_cost,
+                   int32_t* table_out, int64_t table_capacity, int64_t* n_chunks,
+                   int64_t* n_slots);
+
+/* -------------------------------------------------------------------------
+ * In-place BSR addmm:  out[:, rows of active block-rows] += x · Sᵀ
+ *
+ * Replaces the TileLang op body
+ *   ssalaad/tilelang_sparse/addmm_inplace.py:41-82 (_bsr_body) and :88-127
+ *   (_tilelang_bsr_addmm_inplace_dense_impl), schema at :130-136,
+ * and computes what the AVX2 kernel ssalaad/cpu_sparse/bsr_addmm_avx2.cpp:67-174
+ * computes: for each planned block-row `by`, acc = out[:, by·p : by·p+p] in fp32,
+ * plus Σ_blocks x[:, col·q : col·q+q] · values[blk]  (values blocks are (q, p)),
+ * stored back in the out dtype. Block-rows without a chunk are not touched.
+ * p = q ∈ {16, 32, 64}; dtype ∈ {f32, bf16, f16} for out, x and values alike.
+ * `plan` is a device copy of a table from ssl_plan_build (lr_units = 0).
+ * ------------------------------------------------------------------------- */
+int64_t ssl_bsr_addmm_workspace_size(int64_t M, int64_t NB, int32_t block_p,
+                                     int64_t n_slots);
+int64_t ssl_bsr_addmm_counter_bytes(int64_t M, int64_t NB);
+int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx,
+                          const int32_t* col, const void* values, const int32_t* plan,
+                          int64_t n_chunks, int64_t n_slots, int64_t M, int64_t N,
+                          int64_t K, int64_t NB, int32_t block_p, int32_t block_q,
+                          int32_t dtype, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+/* -------------------------------------------------------------------------
+ * Fused SLR linear:  y[M, n_pad] = x · Bᵀ · Aᵀ + x · Sᵀ + bias
+ *
+ * Replaces the forward of the reference module
+ *   ssalaad/efficient/ls_linear.py:124-137 (_LRSLinearLRBlockCUDA.forward: two
+ *   F.linear GEMMs :131, the BSR op :132-134, the bias add :41-44, :135-137) and
+ *   ssalaad/efficient/ls_linear.py:50-51 (_LRSLinearLR, S = 0: pass nnz = 0).
+ * The latent t = x·Bᵀ is rounded to the activation dtype, as F.linear does, then
+ * t·Aᵀ, the sparse term and the bias are summed in fp32 and rounded once.
+ * m ≤ ldx columns of x are read; A is [n_pad = NB·p, r_pad], B is [r_pad, m_pad]
+ * with r_pad a multiple of 64 and m_pad ≥ m a multiple of 64; padding is zero.
+ * `plan` comes from ssl_plan_build with lr_units = r_pad / 32 and rows = NULL.
+ * `bias` may be NULL. y must hold M rows of n_pad columns (ldy ≥ n_pad).
+ * ------------------------------------------------------------------------- */
+int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r_pad,
+                               int64_t m_pad, int64_t n_slots, int32_t dtype);
+int64_t ssl_slr_counter_bytes(int64_t M, int64_t NB, int64_t r_pad, int64_t m_pad);
+int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A,
+                    const void* B, const void* bias, const int32_t* col,
+                    const void* values, const int32_t* plan, int64_t n_chunks,
+                    int64_t n_slots, int64_t M, int64_t m, int64_t m_pad, int64_t NB,
+                    int64_t r_pad, int32_t block_p, int32_t block_q, int32_t dtype,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The same call with its two kernels selectable, for per-kernel timing:
+ * phase 0 = both (== ssl_slr_forward), 1 = the latent t = x·Bᵀ only (written to the
+ * workspace), 2 = the streaming kernel only, reading the latent the last phase-1
+ * call on this workspace left there. No reference counterpart: the reference's
+ * forward (ls_linear.py:131-137) is not split this way. */
+int ssl_slr_forward_phase(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A,
+                          const void* B, const void* bias, const int32_t* col,
+                          const void* values, const int32_t* plan, int64_t n_chunks,
+                          int64_t n_slots, int64_t M, int64_t m, int64_t m_pad, int64_t NB,
+                          int64_t r_pad, int32_t block_p, int32_t block_q, int32_t dtype,
+                          void* workspace, int64_t workspace_bytes, int32_t phase, void* stream);
+
+/* -------------------------------------------------------------------------
+ * Dense → BSR encoder (device), the rule of ssalaad/efficient/artifact.py:20-37
+ * (dense_to_bsr) followed by the module conversion of
+ * ssalaad/efficient/ls_linear.py:89-97:
+ *   a (p×q) block is kept iff the sum of |values| over the block is > 0, i.e. it
+ *   holds no NaN and at least one non-zero; kept blocks are listed row-major.
+ * Step 1 (ssl_bsr_encode_count) writes crow [NB+1] (int32), active_rows [NB]
+ *   (ascending; entries past the count are unspecified) and the two totals
+ *   totals[0] = nnz, totals[1] = number of active block-rows (int32, device).
+ * Step 2 (ssl_bsr_encode_fill) writes col [nnz] (int32), values_bsr [nnz, p, q]
+ *   (BSR layout; may be NULL) and values_t [nnz, q, p] (kernel layout; may be NULL).
+ * S is [n, lds] row-major with n = NB·p and NBK·q ≤ lds columns used.
+ * `flags` is a device scratch array of NB·NBK bytes shared by the two steps.
+ * ------------------------------------------------------------------------- */
+int ssl_bsr_encode_count(const void* S, int64_t lds, int64_t NB, int64_t NBK,
+                         int32_t block_p, int32_t block_q, int32_t dtype, uint8_t* flags,
+                         int32_t* crow, int32_t* active_rows, int32_t* totals,
+                         void* stream);
+int ssl_bsr_encode_fill(const void* S, int64_t lds, int64_t NB, int64_t NBK,
+                        int32_t block_p, int32_t block_q, int32_t dtype,
+                        const uint8_t* flags, const int32_t* crow, int32_t* col,
+                        void* values_bsr, void* values_t, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SSALAAD_AMD_H */

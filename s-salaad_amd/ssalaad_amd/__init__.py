@@ -1,0 +1,30 @@
+"""MI355X (gfx950) sparse-plus-low-rank linear: y = x·Bᵀ·Aᵀ + x·Sᵀ + b.
+
+Drop-in for the S-SALAAD hot path:
+  * torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_  (ssalaad_amd.addmm_inplace)
+  * LRSLinear                                              (ssalaad_amd.ls_linear)
+  * dense_to_bsr / factor_from_svd                         (ssalaad_amd.artifact)
+All compute runs in the HIP kernels of libssalaad_amd.so; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+from . import _lib
+from .addmm_inplace import SUPPORTED_BLOCK_SIZES, bsr_addmm_inplace_, get_tuned_config
+from .artifact import dense_to_bsr, encode_for_kernels, factor_from_svd
+from .ls_linear import LRSLinear
+
+__all__ = [
+    "LRSLinear",
+    "SUPPORTED_BLOCK_SIZES",
+    "bsr_addmm_inplace_",
+    "dense_to_bsr",
+    "encode_for_kernels",
+    "factor_from_svd",
+    "get_tuned_config",
+    "library_path",
+]
+
+
+def library_path() -> str:
+    return str(_lib.LIB_PATH)

@@ -1,0 +1,138 @@
+"""ctypes binding of libssalaad_amd.so (the C ABI in include/ssalaad_amd.h).
+
+The library is loaded once, after torch, so that it resolves the HIP runtime
+torch already holds. There is no fallback: if the library is missing or cannot
+be loaded, every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (loads torch's libamdhip64 before ours)
+
+LIB_PATH = Path(__file__).resolve().parent / "libssalaad_amd.so"
+
+SSL_OK = 0
+SSL_ERR_INVALID = 1
+SSL_ERR_UNSUPPORTED = 2
+SSL_ERR_WORKSPACE = 3
+SSL_ERR_HIP = 4
+SSL_ERR_CAPACITY = 5
+
+SSL_F32, SSL_BF16, SSL_F16 = 0, 1, 2
+PLAN_STRIDE = 8
+
+_DTYPE_CODE = {torch.float32: SSL_F32, torch.bfloat16: SSL_BF16, torch.float16: SSL_F16}
+
+_c_i64 = ctypes.c_int64
+_c_i32 = ctypes.c_int32
+_c_p = ctypes.c_void_p
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "ssl_version": (ctypes.c_int, []),
+    "ssl_last_error": (ctypes.c_char_p, []),
+    "ssl_plan_build": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_i64, _c_p, _c_i64, _c_p, _c_p],
+    ),
+    "ssl_bsr_addmm_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i32, _c_i64]),
+    "ssl_bsr_addmm_counter_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "ssl_bsr_addmm_inplace": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p],
+    ),
+    "ssl_slr_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32]),
+    "ssl_slr_counter_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "ssl_slr_forward": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p],
+    ),
+    "ssl_slr_forward_phase": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i32,
+         _c_p],
+    ),
+    "ssl_bsr_encode_count": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p],
+    ),
+    "ssl_bsr_encode_fill": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p],
+    ),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the library (once); raises if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH.name} is not built; run `python s-salaad_amd/build.py` "
+            "(or __graft_entry__.build()) first. There is no non-HIP fallback."
+        )
+    lib = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _check_single_hip_runtime()
+    _lib = lib
+    return lib
+
+
+def _check_single_hip_runtime() -> None:
+    """Two HIP runtimes in one process would split device state; refuse that."""
+    try:
+        maps = Path("/proc/self/maps").read_text()
+    except OSError:
+        return
+    paths = {
+        os.path.realpath(line.split()[-1])
+        for line in maps.splitlines()
+        if "libamdhip64" in line and line.split()[-1].startswith("/")
+    }
+    if len(paths) > 1:
+        raise RuntimeError(f"more than one HIP runtime is loaded: {sorted(paths)}")
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    code = _DTYPE_CODE.get(dtype)
+    if code is None:
+        raise TypeError(f"SLR kernels support float32/bfloat16/float16, got {dtype}")
+    return code
+
+
+def check(rc: int, what: str) -> None:
+    """Map a C-ABI status to the exception type the reference raises."""
+    if rc == SSL_OK:
+        return
+    msg = f"{what}: {load().ssl_last_error().decode(errors='replace')}"
+    if rc in (SSL_ERR_INVALID, SSL_ERR_CAPACITY):
+        raise ValueError(msg)
+    if rc == SSL_ERR_UNSUPPORTED:
+        raise TypeError(msg)
+    raise RuntimeError(msg)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

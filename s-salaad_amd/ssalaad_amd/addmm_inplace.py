@@ -1,0 +1,191 @@
+"""`torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_` on gfx950.
+
+Drop-in for ssalaad/tilelang_sparse/addmm_inplace.py: same op name and schema
+(:130-136), same fake (:139-141), same argument meaning (:88-110) — but the body
+is the hand-written HIP streaming kernel of libssalaad_amd.so instead of a
+TileLang/CUDA JIT kernel:
+
+    out_inplace[:, by·p:(by+1)·p] += Σ_blocks x[:, col·q:(col+1)·q] · values[blk]
+
+for each block-row `by` listed in `active_rows`; values are (nnz, q, p). The
+accumulator starts from out in fp32 and is stored once in out's dtype. Unlike the
+TileLang kernel, M needs no padding to a tile multiple.
+
+The per-structure work plan (which workgroup sums which blocks) is built on the
+host the first time a given crow/col/active_rows triple is seen and cached on the
+crow tensor object (keyed by the tensors' versions); building it validates the structure
+— monotone crow, col within range, active rows ascending — so the kernel never
+reads outside the tensors it is given.
+"""
+
+from __future__ import annotations
+
+import weakref
+
+import numpy as np
+import torch
+
+from . import _lib, _runtime
+
+SUPPORTED_BLOCK_SIZES = (16, 32, 64)
+
+_TORCH_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def get_tuned_config(block_p: int, block_q: int) -> dict:
+    """Row-multiple contract of addmm_inplace.py:36-38.
+
+    The HIP kernel masks token rows itself, so callers need no row padding (BM=1).
+    """
+    return {"BM": 1, "WARP_TILE_M": 16, "WARP_TILE_N": 16}
+
+
+class _StructPlan:
+    __slots__ = ("versions", "col_ref", "act_ref", "plans", "NB_K")
+
+    def __init__(self, versions, col, act, NB_K):
+        self.versions = versions
+        self.col_ref = weakref.ref(col)
+        self.act_ref = weakref.ref(act)
+        self.plans: dict[int, _runtime.DevicePlan] = {}
+        self.NB_K = NB_K
+
+
+_PLAN_ATTR = "_ssl_struct_plan"
+
+
+def _validated_host_structure(crow, col, active_rows, nnz_values, NB_K):
+    crow_h = crow.detach().to("cpu", torch.int64).numpy()
+    col_h = col.detach().to("cpu", torch.int64).numpy()
+    act_h = active_rows.detach().to("cpu", torch.int64).numpy()
+    NB = crow_h.shape[0] - 1
+    if NB < 0 or crow_h[0] != 0 or np.any(np.diff(crow_h) < 0):
+        raise ValueError("crow_indices must start at 0 and be non-decreasing")
+    if crow_h[-1] != col_h.shape[0] or col_h.shape[0] != nnz_values:
+        raise ValueError(
+            f"crow_indices[-1]={int(crow_h[-1])}, col_indices ({col_h.shape[0]}) and "
+            f"values ({nnz_values}) must agree on nnz"
+        )
+    if col_h.size and (col_h.min() < 0 or col_h.max() >= NB_K):
+        raise ValueError(f"col_indices must lie in [0, {NB_K})")
+    if act_h.size and (act_h.min() < 0 or act_h.max() >= NB or np.any(np.diff(act_h) <= 0)):
+        raise ValueError("active_rows must be ascending block-row indices")
+    return crow_h.astype(np.int32), act_h.astype(np.int32)
+
+
+def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_bytes):
+    versions = (crow._version, col._version, active_rows._version, col.data_ptr(),
+                active_rows.data_ptr(), values.shape[0], NB_K)
+    sp = getattr(crow, _PLAN_ATTR, None)
+    if (
+        sp is None
+        or sp.versions != versions
+        or sp.col_ref() is not col
+        or sp.act_ref() is not active_rows
+    ):
+        sp = _StructPlan(versions, col, active_rows, NB_K)
+        setattr(crow, _PLAN_ATTR, sp)
+    target_key = 0 if M > 64 else 1
+    plan = sp.plans.get(target_key)
+    if plan is None:
+        crow_h, act_h = _validated_host_structure(crow, col, active_rows, values.shape[0], NB_K)
+        total = int(crow_h[-1]) * block_q
+        target = _runtime.plan_target_cost(total, block_p, elem_bytes, M)
+        table, n_chunks, n_slots = _runtime.build_plan(crow_h, act_h, block_q, 0, target)
+        plan = _runtime.DevicePlan(table, n_chunks, n_slots, crow.device)
+        sp.plans[target_key] = plan
+    return plan
+
+
+def _aligned_rows(t: torch.Tensor) -> bool:
+    eb = t.element_size()
+    return t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and (t.stride(0) * eb) % 16 == 0
+
+
+def bsr_addmm_inplace_(
+    out_inplace: torch.Tensor,
+    x: torch.Tensor,
+    crow_indices: torch.Tensor,
+    col_indices: torch.Tensor,
+    values: torch.Tensor,
+    active_rows: torch.Tensor,
+) -> None:
+    """In place ``out_inplace += x @ S.T`` on the active block-rows of S."""
+    if out_inplace.dtype not in _TORCH_DTYPES:
+        raise TypeError(
+            f"HIP BSR kernel supports float16/bfloat16/float32, got {out_inplace.dtype}"
+        )
+    if x.dtype != out_inplace.dtype or values.dtype != out_inplace.dtype:
+        raise TypeError("out_inplace, x and values must share one dtype")
+    for name, t in (("crow_indices", crow_indices), ("col_indices", col_indices),
+                    ("active_rows", active_rows)):
+        if t.dtype != torch.int32:
+            raise TypeError(f"{name} must be int32, got {t.dtype}")
+        if t.dim() != 1:
+            raise ValueError(f"{name} must be 1-D")
+    if out_inplace.dim() != 2 or x.dim() != 2 or values.dim() != 3:
+        raise ValueError("out_inplace and x must be 2-D and values (nnz, block_q, block_p)")
+    devs = {t.device for t in (out_inplace, x, crow_indices, col_indices, values, active_rows)}
+    if len(devs) != 1 or out_inplace.device.type != "cuda":
+        raise ValueError("all tensors must be on one ROCm GPU device")
+    block_q = int(values.shape[1])
+    block_p = int(values.shape[2])
+    if block_p != block_q or block_p not in SUPPORTED_BLOCK_SIZES:
+        raise ValueError(
+            f"The HIP BSR kernel needs square {SUPPORTED_BLOCK_SIZES} blocks, "
+            f"got {block_p}x{block_q}."
+        )
+    M, N = out_inplace.shape
+    NB = int(crow_indices.shape[0]) - 1
+    if x.shape[0] != M:
+        raise ValueError(f"x has {x.shape[0]} rows, out_inplace has {M}")
+    if N != NB * block_p:
+        raise ValueError(f"out N={N} does not match crow ({NB} block-rows) x block_p={block_p}")
+    K = int(x.shape[1])
+    if K % block_q:
+        raise ValueError(f"x K={K} must be divisible by block_q={block_q}")
+    NB_K = K // block_q
+    if M == 0 or values.shape[0] == 0 or active_rows.numel() == 0:
+        return
+    plan = _plan_for(crow_indices, col_indices, active_rows, values, NB_K, block_p, block_q,
+                     M, out_inplace.element_size())
+    if plan.n_chunks == 0:
+        return
+    if not _aligned_rows(x):
+        x = x.contiguous()
+        if not _aligned_rows(x):
+            x = x.clone(memory_format=torch.contiguous_format)
+    vals = values if (values.is_contiguous() and values.data_ptr() % 16 == 0) else values.contiguous()
+    col = col_indices.contiguous()
+    target = out_inplace
+    if not _aligned_rows(out_inplace):
+        target = out_inplace.contiguous().clone()
+    lib = _lib.load()
+    dt = _lib.dtype_code(out_inplace.dtype)
+    need = lib.ssl_bsr_addmm_workspace_size(M, NB, block_p, plan.n_slots)
+    ws = _runtime.workspace(out_inplace.device, need)
+    with torch.cuda.device(out_inplace.device):
+        rc = lib.ssl_bsr_addmm_inplace(
+            target.data_ptr(), target.stride(0), x.data_ptr(), x.stride(0), col.data_ptr(),
+            vals.data_ptr(), plan.table.data_ptr(), plan.n_chunks, plan.n_slots, M, N, K, NB,
+            block_p, block_q, dt, ws.data_ptr(), ws.numel(),
+            _lib.stream_ptr(out_inplace.device),
+        )
+    _lib.check(rc, "ssl_bsr_addmm_inplace")
+    if target is not out_inplace:
+        out_inplace.copy_(target)
+
+
+# Same library name, op name and schema as addmm_inplace.py:130-136. A FRAGMENT
+# keeps the namespace open for the fused op registered in ops.py.
+_lib_frag = torch.library.Library("ssalaad", "FRAGMENT")
+_lib_frag.define(
+    "tilelang_bsr_addmm_inplace_dense_(Tensor(a!) out_inplace, Tensor x, "
+    "Tensor crow_indices, Tensor col_indices, Tensor values, Tensor active_rows) -> ()"
+)
+_lib_frag.impl("tilelang_bsr_addmm_inplace_dense_", bsr_addmm_inplace_, "CUDA")
+
+
+@torch.library.register_fake("ssalaad::tilelang_bsr_addmm_inplace_dense_")
+def _fake(out_inplace, x, crow_indices, col_indices, values, active_rows) -> None:
+    return None

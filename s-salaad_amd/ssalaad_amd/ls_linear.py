@@ -1,0 +1,300 @@
+"""`LRSLinear` on gfx950: the low-rank + block-sparse linear as one fused HIP call.
+
+Mirror of ssalaad/efficient/ls_linear.py. The factory keeps the reference's
+signature (:227-239), dispatch on nnz (:247-253) and validation messages; the
+module classes keep the reference's attributes (in_features, out_features, r,
+block_p, block_q, S_nnz, kind) and buffers (A, B, bias, S_crow, S_col, S_values
+(nnz, q, p), S_active_rows — :28-36, :86-97). The forward
+
+    y = x · Bᵀ · Aᵀ + x · Sᵀ + b
+
+is one call of `ssl_slr_forward` (two kernels: the latent t = x·Bᵀ, then a
+streaming kernel that adds t·Aᵀ, the sparse term and the bias in one epilogue)
+instead of the reference's F.linear ×2 + BSR op + bias add (:124-137).
+
+Differences from the reference, all extensions:
+  * fp32 runs on the GPU too (the TileLang class requires fp16/bf16, :118-119);
+  * out/in features that are not multiples of the block (e.g. FFN 5461) are
+    accepted when S is given at the padded shape (ceil(n/p)·p, ceil(m/q)·q);
+    the padding must be zero, and y is returned at the true width;
+  * no CPU path: the library is the GPU kernels, so CPU tensors are rejected
+    (the reference's AVX2 CPU class, :140-164, is the oracle's baseline instead);
+  * N:M (2:4) S is rejected (out of this library's scope).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib, _runtime
+
+SUPPORTED_BLOCK_SIZES = (16, 32, 64)
+_LR_ONLY_BLOCK = 64  # output tile width when S is all zero
+
+
+def _round_up(v: int, a: int) -> int:
+    return (v + a - 1) // a * a
+
+
+class _KernelState:
+    """Device-side view of a module's weights in the layout the kernels read.
+
+    Buffers the kernels can read as they are (aligned, padded dims already
+    multiples) are used in place; otherwise a zero-padded copy is made once.
+    """
+
+    def __init__(self, mod: "_LRSLinearBase", device: torch.device):
+        dtype = mod.A.dtype
+        self.device = device
+        self.dtype_code = _lib.dtype_code(dtype)
+        self.elem = torch.empty((), dtype=dtype).element_size()
+        n, m, r = mod.out_features, mod.in_features, mod.r
+        p = mod._kernel_block
+        self.p = p
+        self.NB = -(-n // p)
+        self.n_pad = self.NB * p
+        self.r_pad = _round_up(max(r, 1), 64)
+        self.m_pad = _round_up(max(m, 1), 64)
+        self.m = m
+        self.A = self._padded(mod.A, self.n_pad, self.r_pad)
+        self.B = self._padded(mod.B, self.r_pad, self.m_pad)
+        self.bias = None
+        if mod.bias is not None:
+            b = mod.bias.to(dtype)
+            self.bias = b if (self.n_pad == n and b.is_contiguous()) else F.pad(b, (0, self.n_pad - n)).contiguous()
+        if mod.S_nnz > 0:
+            self.col = mod.S_col
+            self.values = mod.S_values
+            crow_h = mod.S_crow.detach().to("cpu").numpy().astype(np.int32)
+            self.nblk_total = int(crow_h[-1])
+        else:
+            self.col = torch.zeros(1, dtype=torch.int32, device=device)
+            self.values = torch.zeros(16, dtype=dtype, device=device)
+            crow_h = np.zeros(self.NB + 1, dtype=np.int32)
+            self.nblk_total = 0
+        self.crow_h = crow_h
+        self.lr_units = self.r_pad // 32
+        self.block_q = p
+        self._plans: dict[int, _runtime.DevicePlan] = {}
+
+    def _padded(self, t: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+        if t.shape == (rows, cols) and t.is_contiguous() and t.data_ptr() % 16 == 0:
+            return t
+        out = torch.zeros(rows, cols, dtype=t.dtype, device=t.device)
+        out[: t.shape[0], : t.shape[1]] = t
+        return out
+
+    def plan(self, M: int) -> _runtime.DevicePlan:
+        key = 0 if M > 64 else 1
+        pl = self._plans.get(key)
+        if pl is None:
+            total = self.nblk_total * self.block_q + self.NB * self.lr_units * 32
+            target = _runtime.plan_target_cost(total, self.p, self.elem, M)
+            table, n_chunks, n_slots = _runtime.build_plan(
+                self.crow_h, None, self.block_q, self.lr_units, target
+            )
+            pl = _runtime.DevicePlan(table, n_chunks, n_slots, self.device)
+            self._plans[key] = pl
+        return pl
+
+    def forward(self, x: torch.Tensor, out_features: int, phase: int = 0) -> torch.Tensor:
+        """y = x·Bᵀ·Aᵀ + x·Sᵀ + b. `phase` selects the kernels (0 both, 1 latent
+        only, 2 streaming kernel only) for per-kernel timing; callers use 0."""
+        m = self.m
+        orig = x.shape
+        x2 = x.reshape(-1, orig[-1])
+        if x2.stride(-1) != 1 or x2.data_ptr() % 16 or (x2.stride(0) * self.elem) % 16:
+            # rows must be 16-byte aligned: copy into a row-padded buffer
+            ld = _round_up(m, 16 // self.elem)
+            buf = torch.zeros(x2.shape[0], ld, dtype=x2.dtype, device=x2.device)
+            buf[:, :m] = x2
+            x2 = buf
+        M = x2.shape[0]
+        y = torch.empty(M, self.n_pad, dtype=x.dtype, device=x.device)
+        if M > 0:
+            pl = self.plan(M)
+            lib = _lib.load()
+            need = lib.ssl_slr_workspace_size(
+                M, self.NB, self.p, self.r_pad, self.m_pad, pl.n_slots, self.dtype_code
+            )
+            ws = _runtime.workspace(x.device, need)
+            rc = lib.ssl_slr_forward_phase(
+                y.data_ptr(), y.stride(0), x2.data_ptr(), x2.stride(0), self.A.data_ptr(),
+                self.B.data_ptr(), _lib.ptr(self.bias), self.col.data_ptr(),
+                self.values.data_ptr(), pl.table.data_ptr(), pl.n_chunks, pl.n_slots, M, m,
+                self.m_pad, self.NB, self.r_pad, self.p, self.p, self.dtype_code,
+                ws.data_ptr(), ws.numel(), phase, _lib.stream_ptr(x.device),
+            )
+            _lib.check(rc, "ssl_slr_forward")
+        if self.n_pad != out_features:
+            y = y[:, :out_features]
+        return y.reshape(*orig[:-1], out_features)
+
+
+class _LRSLinearBase(nn.Module):
+    """Buffers and validation of ls_linear.py:7-44."""
+
+    kind: str = ""
+    _kernel_block: int = _LR_ONLY_BLOCK
+
+    def __init__(self, A, B, *, in_features, out_features, bias=None) -> None:
+        super().__init__()
+        (n, r) = A.shape
+        (rB, m) = B.shape
+        if rB != r:
+            raise ValueError(f"A.shape[1]={r} must match B.shape[0]={rB}")
+        if (n, m) != (out_features, in_features):
+            raise ValueError(
+                f"L = A·B shape ({n},{m}) must equal (out_features={out_features}, in_features={in_features})"
+            )
+        self.in_features = in_features
+        self.out_features = out_features
+        self.r = int(r)
+        self.register_buffer("B", B.contiguous())
+        self.register_buffer("A", A.contiguous())
+        if bias is not None:
+            self.register_buffer("bias", bias.contiguous())
+        else:
+            self.bias = None
+        self._state: _KernelState | None = None
+
+    def _apply(self, fn, recurse: bool = True):
+        self._state = None  # weights moved or cast: rebuild the kernel view lazily
+        return super()._apply(fn, recurse=recurse)
+
+    def _kernel(self) -> _KernelState:
+        st = self._state
+        if st is None or st.device != self.A.device:
+            if self.A.device.type != "cuda":
+                raise ValueError("The HIP SLR kernels need the module on a ROCm GPU device.")
+            st = _KernelState(self, self.A.device)
+            self._state = st
+        return st
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.dtype != self.A.dtype:
+            raise TypeError(f"input dtype {x.dtype} does not match the weights' {self.A.dtype}")
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"input has {x.shape[-1]} features, expected {self.in_features}")
+        if x.device != self.A.device:
+            raise ValueError(f"input on {x.device}, weights on {self.A.device}")
+        return self._kernel().forward(x, self.out_features)
+
+
+class _LRSLinearLR(_LRSLinearBase):
+    """S ≡ 0 (ls_linear.py:47-54): the same fused call with no sparse units."""
+
+    kind = "lr_only"
+    S_nnz = 0
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, rank={self.r}, S=zero (skipped), bias={self.bias is not None}"
+
+
+class _LRSLinearLRBlockBase(_LRSLinearBase):
+    """Block-sparse S in BSR layout (ls_linear.py:57-104)."""
+
+    kind = "block_sparse"
+
+    def __init__(self, A, B, S_sparse, *, in_features, out_features, bias, block_p, block_q) -> None:
+        super().__init__(A, B, in_features=in_features, out_features=out_features, bias=bias)
+        p, q = int(block_p), int(block_q)
+        expected = {(out_features, in_features), (_round_up(out_features, p), _round_up(in_features, q))}
+        if tuple(S_sparse.shape) not in expected:
+            raise ValueError(
+                f"S shape {tuple(S_sparse.shape)} must equal "
+                f"(out_features, in_features)=({out_features},{in_features})"
+            )
+        self.block_p = p
+        self.block_q = q
+        self._kernel_block = p
+        self.S_nnz = int(S_sparse._nnz())
+        crow = S_sparse.crow_indices()
+        self.register_buffer("S_crow", crow.to(torch.int32).clone())
+        self.register_buffer("S_col", S_sparse.col_indices().to(torch.int32).clone())
+        self.register_buffer("S_values", S_sparse.values().transpose(1, 2).contiguous().clone())
+        active = (crow[1:] - crow[:-1]).nonzero(as_tuple=False).squeeze(-1)
+        self.register_buffer("S_active_rows", active.to(torch.int32).clone())
+        self._check_structure(S_sparse.shape)
+
+    def _check_structure(self, shape) -> None:
+        """Host check of the BSR structure the kernels index with."""
+        crow = self.S_crow.detach().cpu().numpy().astype(np.int64)
+        col = self.S_col.detach().cpu().numpy().astype(np.int64)
+        nbk = shape[1] // self.block_q
+        if crow[0] != 0 or np.any(np.diff(crow) < 0) or crow[-1] != col.shape[0]:
+            raise ValueError("S has an inconsistent BSR row pointer")
+        if col.size and (col.min() < 0 or col.max() >= nbk):
+            raise ValueError("S has block-column indices out of range")
+        if self.S_values.shape[0] != col.shape[0]:
+            raise ValueError("S values and column indices disagree on nnz")
+
+    def extra_repr(self) -> str:
+        return (
+            f"in_features={self.in_features}, out_features={self.out_features}, "
+            f"rank={self.r}, S_nnz={self.S_nnz}, "
+            f"block=({self.block_p}×{self.block_q}), bias={self.bias is not None}"
+        )
+
+
+class _LRSLinearLRBlockHIP(_LRSLinearLRBlockBase):
+    """Block-sparse S on the gfx950 streaming kernels (replaces ls_linear.py:107-137)."""
+
+    def __init__(self, *args, **kwargs) -> None:
+        super().__init__(*args, **kwargs)
+        if self.S_values.device.type != "cuda":
+            raise ValueError("The HIP block kernel requires a ROCm GPU device.")
+        if self.block_p != self.block_q or self.block_p not in SUPPORTED_BLOCK_SIZES:
+            raise ValueError(
+                f"The HIP block kernel needs square blocks of size "
+                f"{SUPPORTED_BLOCK_SIZES}, got {self.block_p}x{self.block_q}."
+            )
+        if self.S_values.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError("The HIP block kernel requires fp16, bf16 or fp32.")
+
+
+def LRSLinear(
+    A,
+    B,
+    S_sparse,
+    *,
+    in_features,
+    out_features,
+    bias=None,
+    block_p=None,
+    block_q=None,
+    nm_n=None,
+    nm_m=None,
+):
+    """Compute x @ (A @ B + S).T (+ bias) with the gfx950 kernels.
+
+    Same signature and dispatch as ls_linear.py:227-285: S with no stored block
+    gives the low-rank-only module; block-sparse S needs its block shape. There
+    is no dense or CSR fallback, so a pattern the kernels cannot run is rejected.
+    """
+    if S_sparse.layout == torch.strided:
+        nnz = int(torch.count_nonzero(S_sparse))
+    else:
+        nnz = S_sparse._nnz()
+    kwargs = dict(in_features=in_features, out_features=out_features, bias=bias)
+    if nnz == 0:
+        return _LRSLinearLR(A, B, **kwargs)
+    if nm_n is not None:
+        raise ValueError("N:M (2:4) S is not supported by the HIP kernels.")
+    if block_p is None or block_q is None:
+        raise ValueError("Sparse S needs a recorded block shape to pick a kernel.")
+    if block_p != block_q or block_p not in SUPPORTED_BLOCK_SIZES:
+        raise ValueError(
+            f"The HIP kernel supports square {SUPPORTED_BLOCK_SIZES} blocks, "
+            f"got ({block_p}, {block_q})."
+        )
+    if not A.is_cuda:
+        raise ValueError("The HIP kernels need A, B and S on a ROCm GPU device.")
+    if S_sparse.layout == torch.strided:
+        from .artifact import dense_to_bsr
+
+        S_sparse = dense_to_bsr(S_sparse, block_p, block_q)
+    return _LRSLinearLRBlockHIP(A, B, S_sparse, block_p=block_p, block_q=block_q, **kwargs)

@@ -1,0 +1,296 @@
+"""GPU parity of the HIP kernels against the oracle (through the C ABI).
+
+Tolerances (max-abs normalised error, max|y−y_ref| / max|y_ref|):
+  fp32  1e-5   bf16 / fp16  1e-2   structure (crow/col/active/values bits): exact.
+"""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT / "tests" / "golden"))
+
+from golden_inputs import CASES, make_case  # noqa: E402
+from oracle import slr_oracle as orc  # noqa: E402
+from slr_cases import TOL, err, make_problem, make_x, oracle_y, sparse_bsr_tensor, to_dev  # noqa: E402
+
+import ssalaad_amd  # noqa: E402
+from ssalaad_amd import LRSLinear, _runtime  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = np.load(ROOT / "tests" / "golden" / "bsr_addmm_avx2.npz")
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def _op(out, x, crow, col, vt, act):
+    torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_(out, x, crow, col, vt, act)
+
+
+# --------------------------------------------------- in-place BSR op --
+
+
+@pytest.mark.parametrize("name", [c for c in CASES if not c.endswith("_b8") and "_b8_" not in c])
+def test_op_matches_reference_kernel_golden_outputs(name, gpu_device):
+    c = make_case(name)
+    dev = gpu_device
+    out = torch.from_numpy(c["out"].copy()).to(dev)
+    args = [torch.from_numpy(c[k]).to(dev) for k in ("x", "crow", "col", "values_t", "active")]
+    _op(out, *args)
+    torch.cuda.synchronize()
+    ref = GOLDEN[f"{name}__out"]
+    got = out.cpu().numpy()
+    assert orc.max_abs_normalised_error(got, ref) <= 1e-5
+    # block-rows without blocks are bit-identical to the input
+    p = c["block"]
+    for by in range(len(c["crow"]) - 1):
+        if by not in set(c["active"].tolist()):
+            assert np.array_equal(got[:, by * p:(by + 1) * p], c["out"][:, by * p:(by + 1) * p])
+
+
+def test_op_rejects_block_8(gpu_device):
+    c = make_case("reftest_b8")
+    out = torch.from_numpy(c["out"].copy()).to(gpu_device)
+    args = [torch.from_numpy(c[k]).to(gpu_device) for k in ("x", "crow", "col", "values_t", "active")]
+    with pytest.raises(ValueError, match="square"):
+        _op(out, *args)
+
+
+def _op_case(dtype, p, M, skew, seed, dev):
+    prob = make_problem(8 * p, 12 * p, 4, p, 0.1 if skew else 0.5, dtype, seed=seed, skew=skew)
+    crow32, col32, vt, act = orc.module_buffers(prob["crow"], prob["col"], prob["vals"])
+    x = make_x(prob, M, seed=seed + 7)
+    out0 = orc.bf16_round(np.random.default_rng(seed).standard_normal((M, prob["n"]))).astype(np.float64)
+    out0 = torch.from_numpy(out0).to(dtype).double().numpy()
+    want = orc.bsr_addmm_inplace(out0, x, crow32, col32, vt, act)
+    out = to_dev(out0, dtype, dev)
+    _op(out, to_dev(x, dtype, dev), torch.from_numpy(crow32).to(dev), torch.from_numpy(col32).to(dev),
+        to_dev(vt, dtype, dev), torch.from_numpy(act).to(dev))
+    torch.cuda.synchronize()
+    return out, want, out0, act, prob
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("p", [16, 32, 64])
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 40, 64, 65, 200])
+def test_op_matches_oracle(dtype, p, M, gpu_device):
+    out, want, out0, act, prob = _op_case(dtype, p, M, False, 10 * p + M, gpu_device)
+    assert err(out, want) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("p", [16, 64])
+@pytest.mark.parametrize("M", [1, 16, 100])
+def test_op_skewed_rows_and_untouched_rows(dtype, p, M, gpu_device):
+    out, want, out0, act, prob = _op_case(dtype, p, M, True, 3 * p + M, gpu_device)
+    assert err(out, want) <= TOL[dtype]
+    got = out.double().cpu().numpy()
+    inactive = sorted(set(range(prob["NB"])) - set(act.tolist()))
+    for by in inactive:
+        assert np.array_equal(got[:, by * p:(by + 1) * p], out0[:, by * p:(by + 1) * p])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_op_with_every_block_its_own_chunk(dtype, gpu_device, monkeypatch):
+    """Maximal row splitting: every block is a chunk, every row goes through the
+    partial/counter combine. Two calls: the counters must be back at zero."""
+    monkeypatch.setattr(_runtime, "_MIN_CHUNK_BYTES", 1)
+    monkeypatch.setattr(_runtime, "_TARGET_WORKGROUPS", 10**7)
+    p, M = 32, 16
+    prob = make_problem(6 * p, 20 * p, 4, p, 0.6, dtype, seed=99, skew=True)
+    crow32, col32, vt, act = orc.module_buffers(prob["crow"], prob["col"], prob["vals"])
+    x = make_x(prob, M, seed=5)
+    want = orc.bsr_addmm_inplace(np.zeros((M, prob["n"])), x, crow32, col32, vt, act)
+    dev = gpu_device
+    args = (to_dev(x, dtype, dev), torch.from_numpy(crow32).to(dev), torch.from_numpy(col32).to(dev),
+            to_dev(vt, dtype, dev), torch.from_numpy(act).to(dev))
+    outs = []
+    for _ in range(2):
+        out = torch.zeros(M, prob["n"], dtype=dtype, device=dev)
+        _op(out, *args)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert err(outs[0], want) <= TOL[dtype]
+    assert torch.equal(outs[0], outs[1])
+
+
+# ------------------------------------------------------- fused module --
+
+
+def _module(prob, dev, bias=True):
+    dt = prob["dtype"]
+    S = sparse_bsr_tensor(prob, dev)
+    return LRSLinear(
+        to_dev(prob["A"], dt, dev), to_dev(prob["B"], dt, dev), S,
+        in_features=prob["m"], out_features=prob["n"],
+        bias=to_dev(prob["bias"], dt, dev) if (bias and prob["bias"] is not None) else None,
+        block_p=prob["p"], block_q=prob["p"],
+    )
+
+
+def test_single_slr_linear_fp32_config(gpu_device):
+    """fp32 512×512, rank 128, 32×32 blocks at 50%, x[256,512] ~ N(0,1), bias zeros."""
+    prob = make_problem(512, 512, 128, 32, 0.5, torch.float32, seed=0)
+    prob["bias"] = np.zeros(512)
+    mod = _module(prob, gpu_device)
+    x = np.random.default_rng(1).standard_normal((256, 512)).astype(np.float32).astype(np.float64)
+    y = mod(to_dev(x, torch.float32, gpu_device))
+    torch.cuda.synchronize()
+    assert y.shape == (256, 512)
+    assert err(y, oracle_y(prob, x)) <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("shape", [(256, 192, 64, 32), (192, 256, 100, 16), (128, 128, 4, 64)])
+@pytest.mark.parametrize("M", [1, 4, 16, 33, 64, 130])
+def test_module_matches_oracle(dtype, shape, M, gpu_device):
+    n, m, r, p = shape
+    prob = make_problem(n, m, r, p, 0.5, dtype, seed=n + m + r + M)
+    mod = _module(prob, gpu_device)
+    x = make_x(prob, M)
+    y = mod(to_dev(x, dtype, gpu_device))
+    torch.cuda.synchronize()
+    assert y.shape == (M, n) and y.dtype == dtype
+    assert err(y, oracle_y(prob, x)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("M", [1, 16, 70])
+def test_module_ragged_features_and_no_bias(dtype, M, gpu_device):
+    """out/in features that are not block multiples (zero-padded S), no bias."""
+    prob = make_problem(100, 200, 24, 32, 0.5, dtype, seed=M, bias=False, pad=True)
+    mod = _module(prob, gpu_device, bias=False)
+    x = make_x(prob, M)
+    xt = to_dev(x, dtype, gpu_device)
+    y = mod(xt)
+    torch.cuda.synchronize()
+    assert y.shape == (M, 100)
+    assert err(y, oracle_y(prob, x)) <= TOL[dtype]
+    # leading dims are kept (ls_linear.py:125-137)
+    y3 = mod(xt.reshape(1, M, 200))
+    assert y3.shape == (1, M, 100) and torch.equal(y3.reshape(M, 100), y)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_low_rank_only_module(dtype, gpu_device):
+    rng = np.random.default_rng(3)
+    n, m, r = 96, 80, 16
+    A = orc.bf16_round(rng.standard_normal((n, r)) * 0.1).astype(np.float64)
+    B = orc.bf16_round(rng.standard_normal((r, m)) * 0.1).astype(np.float64)
+    b = orc.bf16_round(rng.standard_normal(n)).astype(np.float64)
+    dev = gpu_device
+    mod = LRSLinear(to_dev(A, dtype, dev), to_dev(B, dtype, dev), torch.zeros(n, m, device=dev),
+                    in_features=m, out_features=n, bias=to_dev(b, dtype, dev))
+    assert mod.kind == "lr_only"
+    x = orc.bf16_round(rng.standard_normal((9, m))).astype(np.float64)
+    y = mod(to_dev(x, dtype, dev))
+    torch.cuda.synchronize()
+    assert err(y, orc.slr_linear(x, A, B, np.zeros((n, m)), b)) <= TOL[dtype]
+
+
+def test_module_is_deterministic_and_reuses_workspace(gpu_device):
+    prob = make_problem(4096, 1024, 256, 64, 0.5, torch.bfloat16, seed=4, skew=True)
+    mod = _module(prob, gpu_device)
+    x = to_dev(make_x(prob, 16), torch.bfloat16, gpu_device)
+    y1 = mod(x)
+    y2 = mod(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_llama7b_ffn_shape_decode(M, gpu_device):
+    """Full-size 11008×4096 bf16, rank 256, 64×64 blocks at 50%: split rows,
+    latent split over in_features."""
+    prob = make_problem(11008, 4096, 256, 64, 0.5, torch.bfloat16, seed=7)
+    mod = _module(prob, gpu_device)
+    x = make_x(prob, M)
+    y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= 1e-2
+
+
+def test_llama1b_down_proj_ragged_decode(gpu_device):
+    """2048×5461 bf16 (in_features not a block multiple), 32×32 blocks, rank 256."""
+    prob = make_problem(2048, 5461, 256, 32, 0.5, torch.bfloat16, seed=8, pad=True)
+    mod = _module(prob, gpu_device)
+    x = make_x(prob, 4)
+    y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= 1e-2
+
+
+# ------------------------------------------------------------ encoder --
+
+
+def _special_matrix(n, m, p, q, dtype, seed):
+    rng = np.random.default_rng(seed)
+    S = np.zeros((n, m), dtype=np.float32)
+    NB, NBK = n // p, m // q
+    for s in rng.permutation(NB * NBK)[: (NB * NBK) // 2]:
+        br, bc = divmod(int(s), NBK)
+        S[br * p:(br + 1) * p, bc * q:(bc + 1) * q] = rng.standard_normal((p, q))
+    # special blocks (if the grid has room): NaN, -0 only, inf, a lone subnormal
+    specials = [(0, 0, np.nan), (0, 1, -0.0), (1, 0, np.inf), (1, 1, "sub")]
+    for br, bc, v in specials:
+        if br < NB and bc < NBK:
+            blk = S[br * p:(br + 1) * p, bc * q:(bc + 1) * q]
+            if v == "sub":
+                blk[:] = 0
+                blk[p - 1, q - 1] = {torch.float32: 1e-45, torch.bfloat16: 1e-40,
+                                     torch.float16: 6e-8}[dtype]
+            elif isinstance(v, float) and v == 0.0:
+                blk[:] = -0.0
+            else:
+                blk[p // 2, q // 2] = v
+    return torch.from_numpy(S).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("pq", [(16, 16), (32, 32), (64, 64), (16, 32)])
+def test_encoder_structure_is_bit_exact(dtype, pq, gpu_device):
+    p, q = pq
+    S = _special_matrix(6 * p, 9 * q, p, q, dtype, seed=p + q)
+    crow, col, vals = orc.dense_to_bsr(S.float().numpy(), p, q)
+    crow32, col32, vt, act = orc.module_buffers(crow, col, vals)
+    bits = {torch.float32: torch.int32, torch.bfloat16: torch.int16, torch.float16: torch.int16}[dtype]
+    S_bits = S.view(bits).numpy()
+    dev = gpu_device
+    k_crow, k_col, k_vt, k_act = ssalaad_amd.encode_for_kernels(S.to(dev), p, q)
+    bsr = ssalaad_amd.dense_to_bsr(S.to(dev), p, q)
+    torch.cuda.synchronize()
+    assert np.array_equal(k_crow.cpu().numpy(), crow32)
+    assert np.array_equal(k_col.cpu().numpy(), col32)
+    assert np.array_equal(k_act.cpu().numpy(), act)
+    assert np.array_equal(bsr.crow_indices().cpu().numpy(), crow)
+    assert np.array_equal(bsr.col_indices().cpu().numpy(), col)
+    assert bsr.crow_indices().dtype == torch.int64
+    # values copied bit for bit: gather the kept blocks' bits from S directly
+    rows = np.repeat(np.arange(len(crow) - 1), np.diff(crow))
+    want_bits = np.stack([S_bits[r * p:(r + 1) * p, c * q:(c + 1) * q] for r, c in zip(rows, col)]) \
+        if len(col) else np.zeros((0, p, q), S_bits.dtype)
+    assert np.array_equal(bsr.values().cpu().view(bits).numpy(), want_bits)
+    assert np.array_equal(k_vt.cpu().view(bits).numpy(), want_bits.transpose(0, 2, 1))
+
+
+def test_encoder_feeds_the_module(gpu_device):
+    """Dense S handed to the factory goes through the device encoder."""
+    prob = make_problem(128, 192, 16, 32, 0.4, torch.bfloat16, seed=2)
+    dev = gpu_device
+    from slr_cases import s_dense
+
+    S = to_dev(s_dense(prob), torch.bfloat16, dev)
+    mod = LRSLinear(to_dev(prob["A"], torch.bfloat16, dev), to_dev(prob["B"], torch.bfloat16, dev),
+                    S, in_features=192, out_features=128, bias=to_dev(prob["bias"], torch.bfloat16, dev),
+                    block_p=32, block_q=32)
+    assert mod.S_nnz == len(prob["col"])
+    x = make_x(prob, 5)
+    y = mod(to_dev(x, torch.bfloat16, dev))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= 1e-2

@@ -1,0 +1,129 @@
+"""Host-side behaviour of the reference-mirroring Python layer (no GPU):
+factory dispatch and validation messages, op registration and schema."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import ssalaad_amd
+from ssalaad_amd import LRSLinear
+from ssalaad_amd.ls_linear import _LRSLinearLR
+
+
+def _block_sparse(n, m, block, coords, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    S = torch.zeros(n, m)
+    for br, bc in coords:
+        S[br * block:(br + 1) * block, bc * block:(bc + 1) * block] = torch.randn(block, block, generator=g)
+    return S
+
+
+def test_block_kernel_rejects_unsupported_block_shape():
+    """Mirror of tests/test_ssalaad.py:340-354: non-square blocks fail loudly."""
+    torch.manual_seed(0)
+    A, B = torch.randn(64, 8), torch.randn(8, 96)
+    S = _block_sparse(64, 96, 8, [(0, 1), (1, 0)])
+    with pytest.raises(ValueError, match="square"):
+        LRSLinear(A, B, S.to_sparse_bsr(blocksize=(8, 8)), in_features=96, out_features=64,
+                  block_p=8, block_q=16)
+
+
+@pytest.mark.parametrize("block", [8, 48])
+def test_block_sizes_without_a_kernel_are_rejected(block):
+    A, B = torch.randn(96, 4), torch.randn(4, 96)
+    S = _block_sparse(96, 96, block, [(0, 0)])
+    with pytest.raises(ValueError, match="square"):
+        LRSLinear(A, B, S.to_sparse_bsr(blocksize=(block, block)), in_features=96,
+                  out_features=96, block_p=block, block_q=block)
+
+
+def test_sparse_s_without_block_shape_is_rejected():
+    A, B = torch.randn(32, 4), torch.randn(4, 32)
+    S = _block_sparse(32, 32, 16, [(0, 0)])
+    with pytest.raises(ValueError, match="block shape"):
+        LRSLinear(A, B, S.to_sparse_bsr(blocksize=(16, 16)), in_features=32, out_features=32)
+
+
+def test_cpu_tensors_have_no_fallback():
+    A, B = torch.randn(32, 4), torch.randn(4, 32)
+    S = _block_sparse(32, 32, 16, [(0, 0)])
+    with pytest.raises(ValueError, match="GPU"):
+        LRSLinear(A, B, S.to_sparse_bsr(blocksize=(16, 16)), in_features=32, out_features=32,
+                  block_p=16, block_q=16)
+
+
+def test_nm_is_rejected():
+    A, B = torch.randn(32, 4), torch.randn(4, 32)
+    S = _block_sparse(32, 32, 16, [(0, 0)])
+    with pytest.raises(ValueError, match="N:M"):
+        LRSLinear(A, B, S, in_features=32, out_features=32, nm_n=2, nm_m=4)
+
+
+def test_zero_s_gives_the_low_rank_module():
+    """ls_linear.py:252-253; also the module's shape validation (:20-27)."""
+    A, B = torch.randn(32, 4), torch.randn(4, 48)
+    mod = LRSLinear(A, B, torch.zeros(32, 48), in_features=48, out_features=32)
+    assert isinstance(mod, _LRSLinearLR) and mod.kind == "lr_only" and mod.r == 4
+    assert "S=zero" in mod.extra_repr()
+    with pytest.raises(ValueError, match="must match"):
+        LRSLinear(torch.randn(32, 4), torch.randn(5, 48), torch.zeros(32, 48), in_features=48,
+                  out_features=32)
+    with pytest.raises(ValueError, match="must equal"):
+        LRSLinear(A, B, torch.zeros(32, 48), in_features=40, out_features=32)
+    with pytest.raises(ValueError, match="GPU"):
+        mod(torch.randn(2, 48))
+
+
+def test_op_is_registered_with_the_reference_schema():
+    op = torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_
+    schema = str(op.default._schema)
+    assert schema.startswith("ssalaad::tilelang_bsr_addmm_inplace_dense_(Tensor(a!) out_inplace, Tensor x, Tensor crow_indices, Tensor col_indices, Tensor values, Tensor active_rows) -> ()")
+    assert ssalaad_amd.get_tuned_config(64, 64)["BM"] == 1
+
+
+def test_op_fake_kernel_returns_none():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        out = torch.empty(4, 64)
+        x = torch.empty(4, 64)
+        crow = torch.empty(2, dtype=torch.int32)
+        col = torch.empty(1, dtype=torch.int32)
+        vals = torch.empty(1, 64, 64)
+        act = torch.empty(1, dtype=torch.int32)
+        assert torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_(out, x, crow, col, vals, act) is None
+
+
+def test_op_validates_arguments_on_cpu():
+    out = torch.zeros(4, 64)
+    x = torch.zeros(4, 64)
+    crow = torch.tensor([0, 1], dtype=torch.int32)
+    col = torch.tensor([0], dtype=torch.int32)
+    vals = torch.zeros(1, 64, 64)
+    act = torch.tensor([0], dtype=torch.int32)
+    f = ssalaad_amd.bsr_addmm_inplace_
+    with pytest.raises(TypeError):
+        f(out.long(), x, crow, col, vals, act)
+    with pytest.raises(TypeError):
+        f(out, x.double(), crow, col, vals, act)
+    with pytest.raises(TypeError):
+        f(out, x, crow.long(), col, vals, act)
+    with pytest.raises(ValueError, match="GPU"):
+        f(out, x, crow, col, vals, act)
+
+
+def test_factor_from_svd_mirror():
+    """tests/test_ssalaad.py:276-283 on the mirrored helper (torch ops, any device)."""
+    torch.manual_seed(0)
+    matrix = torch.randn(16, 3) @ torch.randn(3, 32)
+    svd = torch.linalg.svd(matrix, full_matrices=False)
+    A, B = ssalaad_amd.factor_from_svd(*svd, 3)
+    torch.testing.assert_close(A @ B, matrix, atol=1e-4, rtol=1e-4)
+    A0, B0 = ssalaad_amd.factor_from_svd(*svd, 0)
+    assert A0.shape == (16, 0) and B0.shape == (0, 32)
+
+
+def test_encoder_front_end_checks_shape_first():
+    with pytest.raises(ValueError, match="not divisible"):
+        ssalaad_amd.dense_to_bsr(torch.zeros(10, 16), 4, 4)
