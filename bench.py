@@ -11,10 +11,11 @@ Timing: the step is captured once in a HIP graph and replayed; W untimed
 replays, then K replays bracketed by synchronize + HIP events on the replay
 stream. value = M·K / elapsed (tokens/s).
 
-roofline: the dominant kernel is the fused streaming kernel (sparse blocks +
-t·Aᵀ + epilogue). Its average launch duration is measured live with HIP events
-around graph replays that launch only that kernel (168 launches per replay);
-achieved = its algorithmic bytes per launch / that duration.
+roofline: each SLR linear is one launch of the fused kernel (latent, sparse
+blocks, t·Aᵀ and epilogue), so the step's 168 launches are all that kernel; its
+average launch duration = the HIP-event time of the graph replays / 168 (gaps
+between launches included, so this slightly understates the kernel);
+achieved = algorithmic bytes per launch / that duration.
 
 cpu_baseline: the reference AVX2 BSR kernel (oracle/_ref, compiled from the
 reference's own source) plus torch-CPU F.linear ×2 — the reference's CPU
@@ -87,12 +88,8 @@ def algorithmic_bytes(mod, M: int, e: int) -> dict:
     idx = 4 * (nnz + 2 * NB + 1)
     bias = e * n if mod.bias is not None else 0
     total = e * M * (m + n) + e * r * (n + m) + e * nnz * p * p + idx + bias
-    # per kernel: the latent reads B and x, writes t; the streaming kernel reads
-    # x, t, A, S and writes y
-    latent = e * r * m + e * M * m + e * M * r
-    stream = e * M * m + e * M * r + e * n * r + e * nnz * p * p + idx + bias + e * M * n
     flops = 2 * M * r * (m + n) + 2 * M * nnz * p * p
-    return dict(total=total, latent=latent, stream=stream, flops=flops)
+    return dict(total=total, flops=flops)
 
 
 # -------------------------------------------------------------- GPU leg --
@@ -123,59 +120,43 @@ def run_gpu(args):
     bytes_ = [algorithmic_bytes(mod, M, e) for _, mod in mods]
     states = [mod._kernel() for _, mod in mods]
 
-    def step(phase=0):
-        outs = []
-        for (name, mod), st in zip(mods, states):
-            outs.append(st.forward(xin[name], mod.out_features, phase=phase))
-        return outs
+    def step():
+        return [st.forward(xin[name], mod.out_features) for (name, mod), st in zip(mods, states)]
 
     s = torch.cuda.Stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(s):
-        for ph in (0, 1, 2):
-            step(ph)
+        step()
     torch.cuda.synchronize()
-    graphs = {}
-    keep = {}
-    for ph in (0, 2):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            keep[ph] = step(ph)
-        graphs[ph] = g
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        keep = step()
     torch.cuda.synchronize()
 
-    def time_graph(g, reps, warm):
-        with torch.cuda.stream(s):
-            for _ in range(warm):
-                g.replay()
-            torch.cuda.synchronize()
-            ev0 = torch.cuda.Event(enable_timing=True)
-            ev1 = torch.cuda.Event(enable_timing=True)
-            ev0.record(s)
-            for _ in range(reps):
-                g.replay()
-            ev1.record(s)
-            torch.cuda.synchronize()
-        return ev0.elapsed_time(ev1) / reps  # ms per replay
-
-    ms_step = time_graph(graphs[0], args.steps, args.warmup)
-    # the streaming kernel alone (latent left in the workspace by the warmup)
-    ms_stream = time_graph(graphs[2], max(args.steps, 20), max(args.warmup, 3))
+    with torch.cuda.stream(s):
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record(s)
+        for _ in range(args.steps):
+            g.replay()
+        ev1.record(s)
+        torch.cuda.synchronize()
+    ms_step = ev0.elapsed_time(ev1) / args.steps
     n_lin = len(mods)
-    stream_bytes = sum(b["stream"] for b in bytes_)
     total_bytes = sum(b["total"] for b in bytes_)
     total_flops = sum(b["flops"] for b in bytes_)
-    avg_stream_us = ms_stream * 1e3 / n_lin
-    achieved = stream_bytes / n_lin / (avg_stream_us * 1e-6) / 1e9
-    step_gbs = total_bytes / (ms_step * 1e-3) / 1e9
+    avg_us = ms_step * 1e3 / n_lin
+    achieved = total_bytes / n_lin / (avg_us * 1e-6) / 1e9
     res = dict(
         ms_step=ms_step,
         tok_s=M / (ms_step * 1e-3),
-        step_gbs=step_gbs,
         step_tflops=total_flops / (ms_step * 1e-3) / 1e12,
-        stream_avg_us=avg_stream_us,
-        stream_achieved_gbs=achieved,
-        stream_bytes_per_launch=stream_bytes / n_lin,
+        avg_launch_us=avg_us,
+        achieved_gbs=achieved,
+        bytes_per_launch=total_bytes / n_lin,
         total_bytes_per_step=total_bytes,
         n_linears=n_lin,
     )
@@ -183,7 +164,12 @@ def run_gpu(args):
     name, mod = mods[-1]
     ref = mod(xin[name])
     torch.cuda.synchronize()
-    res["graph_matches_eager"] = bool(torch.equal(keep[0][-1], ref))
+    res["graph_matches_eager"] = bool(torch.equal(keep[-1], ref))
+    from ssalaad_amd.ls_linear import latent_wait_status
+
+    with torch.cuda.stream(s):
+        res["status"] = latent_wait_status(dev)
+    res["status"] = max(res["status"], latent_wait_status(dev))
     return res
 
 
@@ -319,22 +305,21 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(g["stream_achieved_gbs"], 1),
+            "achieved": round(g["achieved_gbs"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(g["stream_achieved_gbs"] / HBM_PEAK_GBS, 4),
+            "frac": round(g["achieved_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "bsr_stream_kernel<bf16,p32,MT1,fused>",
-            "avg_launch_us": round(g["stream_avg_us"], 3),
-            "algorithmic_bytes_per_launch": int(g["stream_bytes_per_launch"]),
+            "kernel": "slr_kernel<bf16,p32,MT1,fused>",
+            "avg_launch_us": round(g["avg_launch_us"], 3),
+            "algorithmic_bytes_per_launch": int(g["bytes_per_launch"]),
         },
         "cpu_baseline": cpu,
         "details": {
-            "step_algorithmic_GBps": round(g["step_gbs"], 1),
-            "step_frac_hbm": round(g["step_gbs"] / HBM_PEAK_GBS, 4),
-            "step_TFLOPs": round(g["step_tflops"], 2),
+            "step_TFLOPs": round(g["step_tflops"], 3),
             "bytes_per_step": int(g["total_bytes_per_step"]),
             "graph_matches_eager": g["graph_matches_eager"],
+            "latent_wait_status": g["status"],
         },
     }
     print(json.dumps(line), flush=True)

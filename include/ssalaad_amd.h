@@ -5,11 +5,14 @@
  *
  * Every entry point takes raw device pointers, sizes and a hipStream_t passed as
  * `void*`; none allocates device memory. Kernel entry points are asynchronous and
- * ordered on `stream`. Scratch memory (`workspace`) is supplied by the caller,
- * sized by the matching *_workspace_size query; its first `ssl_*_counter_bytes`
- * bytes hold completion counters that must be zero before the first call and are
- * returned to zero by every call that completes. Calls that share one workspace
- * must be ordered (same stream); concurrent calls on one workspace race.
+ * ordered on `stream`. Scratch is supplied by the caller in two parts:
+ *   counters  int32 array sized by the *_counter_count query. It must be zero
+ *             before the first call; every call that completes leaves it zero.
+ *             Keep it for counters only (never alias it with data).
+ *   workspace bytes sized by the *_workspace_size query (256-byte aligned); no
+ *             initialisation needed.
+ * Calls that share scratch must be ordered (same stream); concurrent calls on the
+ * same scratch race.
  *
  * Return value: 0 (SSL_OK) or one of the ssl_status codes below. HIP launch
  * failures are reported as SSL_ERR_HIP; ssl_last_error() returns a message.
@@ -54,15 +57,18 @@ const char* ssl_last_error(void);
  * Work plans (host side, integer only).
  *
  * A plan splits the work of one BSR matrix into workgroup chunks. Each block-row
- * contributes a list of units: its sparse blocks (cost q each) followed by `lr_units`
- * low-rank units (cost 32 each, 32 ranks of A per unit). A row whose cost exceeds
- * `target_cost` is split into nearly equal consecutive chunks that are summed in a
- * fixed order on the device, so long rows of skewed matrices are spread across
- * workgroups and results stay deterministic. `rows` lists the block-rows that
- * get chunks (NULL = every row 0..NB-1).
+ * owns its sparse blocks (cost q each) and `lr_units` low-rank units (cost 32
+ * each, 32 ranks of A per unit). A row whose cost exceeds `target_cost` is split
+ * into k nearly equal chunks; chunk j takes the j-th consecutive share of the
+ * row's blocks and the j-th share of its low-rank units. The k partial results
+ * are summed in chunk order on the device, so long rows of skewed matrices are
+ * spread across workgroups and results stay deterministic. `rows` lists the
+ * block-rows that get chunks (NULL = every row 0..NB-1). target_cost <= 0 never
+ * splits.
  *
  * Table layout: SSL_PLAN_STRIDE int32 per chunk:
- *   {row, unit_begin, unit_end, seq, nseq, slot, nblk, blk0}
+ *   {row, blk_begin, blk_end, lr_begin, lr_end, seq, nseq, slot}
+ * (blk_* index the BSR block arrays; lr_* count 32-rank units of the row).
  * Returns the chunk count in *n_chunks and the partial-sum slot count in *n_slots.
  * ------------------------------------------------------------------------- */
 #define SSL_PLAN_STRIDE 8
@@ -86,16 +92,16 @@ int ssl_plan_build(const int32_t* crow_host, int64_t NB, const int32_t* rows_hos
  * ------------------------------------------------------------------------- */
 int64_t ssl_bsr_addmm_workspace_size(int64_t M, int64_t NB, int32_t block_p,
                                      int64_t n_slots);
-int64_t ssl_bsr_addmm_counter_bytes(int64_t M, int64_t NB);
+int64_t ssl_bsr_addmm_counter_count(int64_t M, int64_t NB);
 int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx,
                           const int32_t* col, const void* values, const int32_t* plan,
                           int64_t n_chunks, int64_t n_slots, int64_t M, int64_t N,
                           int64_t K, int64_t NB, int32_t block_p, int32_t block_q,
-                          int32_t dtype, void* workspace, int64_t workspace_bytes,
-                          void* stream);
+                          int32_t dtype, int32_t* counters, int64_t n_counters,
+                          void* workspace, int64_t workspace_bytes, void* stream);
 
 /* -------------------------------------------------------------------------
- * Fused SLR linear:  y[M, n_pad] = x · Bᵀ · Aᵀ + x · Sᵀ + bias
+ * Fused SLR linear:  y[M, n_pad] = x · Bᵀ · Aᵀ + x · Sᵀ + bias   (one launch)
  *
  * Replaces the forward of the reference module
  *   ssalaad/efficient/ls_linear.py:124-137 (_LRSLinearLRBlockCUDA.forward: two
@@ -105,30 +111,27 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx,
  * t·Aᵀ, the sparse term and the bias are summed in fp32 and rounded once.
  * m ≤ ldx columns of x are read; A is [n_pad = NB·p, r_pad], B is [r_pad, m_pad]
  * with r_pad a multiple of 64 and m_pad ≥ m a multiple of 64; padding is zero.
- * `plan` comes from ssl_plan_build with lr_units = r_pad / 32 and rows = NULL.
+ * `plan` comes from ssl_plan_build with lr_units = r_pad / 32 and rows = NULL;
+ * `lr_wgs` counts the plan's chunks with low-rank units (lr_end > lr_begin).
  * `bias` may be NULL. y must hold M rows of n_pad columns (ldy ≥ n_pad).
+ * `counters` (ssl_slr_counter_count int32) start at zero and are zero again when
+ * the launch ends; they may be shared by calls ordered on one stream.
+ * `sync` (ssl_slr_sync_count uint64) belongs to one plan: zero when the plan is
+ * made, then advanced by every call with that plan, never reset; calls with one
+ * plan must be ordered on one stream. sync[0] is set to 1 if a workgroup gave up
+ * waiting (never expected; the host may check it after synchronising).
  * ------------------------------------------------------------------------- */
 int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r_pad,
                                int64_t m_pad, int64_t n_slots, int32_t dtype);
-int64_t ssl_slr_counter_bytes(int64_t M, int64_t NB, int64_t r_pad, int64_t m_pad);
+int64_t ssl_slr_counter_count(int64_t M, int64_t NB);
+int64_t ssl_slr_sync_count(int64_t M);
 int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A,
                     const void* B, const void* bias, const int32_t* col,
                     const void* values, const int32_t* plan, int64_t n_chunks,
-                    int64_t n_slots, int64_t M, int64_t m, int64_t m_pad, int64_t NB,
-                    int64_t r_pad, int32_t block_p, int32_t block_q, int32_t dtype,
-                    void* workspace, int64_t workspace_bytes, void* stream);
-
-/* The same call with its two kernels selectable, for per-kernel timing:
- * phase 0 = both (== ssl_slr_forward), 1 = the latent t = x·Bᵀ only (written to the
- * workspace), 2 = the streaming kernel only, reading the latent the last phase-1
- * call on this workspace left there. No reference counterpart: the reference's
- * forward (ls_linear.py:131-137) is not split this way. */
-int ssl_slr_forward_phase(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A,
-                          const void* B, const void* bias, const int32_t* col,
-                          const void* values, const int32_t* plan, int64_t n_chunks,
-                          int64_t n_slots, int64_t M, int64_t m, int64_t m_pad, int64_t NB,
-                          int64_t r_pad, int32_t block_p, int32_t block_q, int32_t dtype,
-                          void* workspace, int64_t workspace_bytes, int32_t phase, void* stream);
+                    int64_t n_slots, int64_t lr_wgs, int64_t M, int64_t m, int64_t m_pad,
+                    int64_t NB, int64_t r_pad, int32_t block_p, int32_t block_q,
+                    int32_t dtype, int32_t* counters, int64_t n_counters, uint64_t* sync,
+                    int64_t n_sync, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* -------------------------------------------------------------------------
  * Dense → BSR encoder (device), the rule of ssalaad/efficient/artifact.py:20-37

@@ -1,200 +1,365 @@
 // Streaming SLR / BSR kernels for gfx950.
 //
-// One workgroup (4 waves) executes one chunk of a work plan (plan.cpp): a
-// consecutive range of the units of one block-row — sparse (q, p) blocks and,
-// for the fused linear, 32-rank slices of A — for a tile of 16·MT token rows.
-// The four waves take the chunk's units round-robin and stream each unit's
-// weights from HBM straight into registers (no LDS staging: every weight byte
-// is used exactly once per token tile), feeding v_mfma_f32_16x16x{32,16,4}.
-// Partial tiles are reduced across the waves in LDS; a block-row split over
-// several chunks is combined through a per-row arrival counter: each chunk
-// writes its fp32 partial, and the last chunk to arrive sums all partials in
-// chunk order (deterministic) and runs the epilogue.
+// Decode-shaped calls (up to 64 token rows per tile) are HBM-bound: every
+// weight byte is read once per token tile and feeds a handful of MFMAs. The
+// kernels are therefore organised around keeping as many weight bytes in
+// flight as possible and around the few cross-workgroup exchanges that the
+// computation needs, because on a loaded device each exchange (a device-coherent
+// store, its acknowledgement and a counter update) costs microseconds.
 //
-// The low-rank latent t = x·Bᵀ is produced by lr_latent_kernel with the same
-// machinery (chunks over the in_features dimension, combined per 64-rank group).
+// Row-resident workgroups. A plan (plan.cpp) gives one workgroup (8 waves) a
+// whole block-row — its sparse (q, p) blocks and, for the fused linear, the
+// 32-rank slices of A — unless the row is long, in which case it is split into
+// a few chunks. The 8 waves take the units round-robin and issue all of their
+// loads before the first MFMA (about 32 blocks of 64×64 in one batch), so a
+// typical row costs one memory round trip. Weights go from HBM straight into
+// registers (no LDS staging: each byte is used once per token tile); the sparse
+// blocks, stored (q, p) as in the reference module, are transposed into MFMA
+// fragments with register byte permutes.
+//
+// Reduction. The 8 wave tiles are summed in LDS in a fixed tree order; wave 0
+// then runs the epilogue (bias, or the in-place add of the op) and stores the
+// row tile once.
+//
+// Split rows. A chunk of a split row stores its fp32 tile with device-coherent
+// (sc1) stores, waits for the acknowledgement and bumps the row's counter. In
+// the fused linear the row's finaliser chunk (the one with the low-rank units,
+// launched after all other chunks) waits for the others and sums the partials in
+// chunk order; in the in-place op the chunk that arrives last does. Results are
+// deterministic either way. Only exchanged data is accessed device-coherently;
+// no workgroup writes back or invalidates a whole L2.
+//
+// The latent. The fused launch starts with one workgroup per 16-rank tile of
+// t = x·Bᵀ and chunk of in_features (one batch of loads each); each stores its
+// fp32 partial device-coherently and bumps the token tile's ready counter. The
+// consumers sum the partials in chunk order and round once. Low-rank units
+// load their A slices first and wait for that counter (bounded spin) only then.
+// Only one thread per workgroup polls. Workgroups of one XCD are dispatched in
+// index order, so every workgroup a chunk may wait for (latent tiles, earlier
+// chunks of its row) is resident or done before it, and every wait ends. The
+// latent counters are monotonic per plan (a consumer's ticket tells it which
+// launch it belongs to), so no launch needs an end-of-launch reset.
 
 #include "abi_internal.h"
 #include "slr_common.h"
 
 namespace ssl {
 
+enum : int { MODE_OP = 0, MODE_FUSED = 1 };
+
+constexpr int kSW = 8;            // waves per streaming workgroup
+constexpr int kST = kSW * kWave;  // threads per streaming workgroup
+
+// Polls of a counter before a wait gives up and flags an error in the status
+// word (seconds; a healthy launch waits microseconds).
+constexpr int kSpinLimit = 1 << 22;
+
 // ---------------------------------------------------------------------------
-// W-wide fp32 vectors in memory (partials) and in the output dtype (epilogue).
+// Device-coherent (agent scope) 32-bit accesses for data exchanged between
+// workgroups of one launch: sc1 loads/stores, no cache-wide maintenance.
 // ---------------------------------------------------------------------------
-template <int W>
-__device__ __forceinline__ void st_f32(float* p, const float (&v)[W]) {
-  if constexpr (W == 4) *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
-  else if constexpr (W == 2) *(float2*)p = make_float2(v[0], v[1]);
-  else p[0] = v[0];
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-template <int W>
-__device__ __forceinline__ void ld_f32(const float* p, float (&v)[W]) {
-  if constexpr (W == 4) {
-    float4 t = *(const float4*)p;
-    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-  } else if constexpr (W == 2) {
-    float2 t = *(const float2*)p;
-    v[0] = t.x; v[1] = t.y;
-  } else {
-    v[0] = p[0];
-  }
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-template <int DT, int W>
-__device__ __forceinline__ void st_elems(void* base, int64_t off, const float (&v)[W]) {
-  if constexpr (DT == DT_F32) {
-    st_f32<W>((float*)base + off, v);
-  } else {
-    uint16_t* p = (uint16_t*)base + off;
-    if constexpr (W == 4) {
-      uint2 u;
-      u.x = to_bits<DT>(v[0]) | (to_bits<DT>(v[1]) << 16);
-      u.y = to_bits<DT>(v[2]) | (to_bits<DT>(v[3]) << 16);
-      *(uint2*)p = u;
-    } else if constexpr (W == 2) {
-      *(uint32_t*)p = to_bits<DT>(v[0]) | (to_bits<DT>(v[1]) << 16);
-    } else {
-      p[0] = (uint16_t)to_bits<DT>(v[0]);
-    }
-  }
+__device__ __forceinline__ void st_dev_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-template <int DT, int W>
-__device__ __forceinline__ void ld_elems(const void* base, int64_t off, float (&v)[W]) {
-  if constexpr (DT == DT_F32) {
-    ld_f32<W>((const float*)base + off, v);
-  } else {
-    const uint16_t* p = (const uint16_t*)base + off;
-    uint32_t w[(W + 1) / 2];
-    if constexpr (W == 4) {
-      uint2 u = *(const uint2*)p;
-      w[0] = u.x; w[1] = u.y;
-    } else if constexpr (W == 2) {
-      w[0] = *(const uint32_t*)p;
-    } else {
-      w[0] = p[0];
-    }
-#pragma unroll
-    for (int s = 0; s < W; ++s) {
-      uint32_t h = (w[s >> 1] >> (16 * (s & 1))) & 0xffffu;
-      v[s] = (DT == DT_BF16) ? bf16_to_f32(h) : f16_to_f32(h);
+__device__ __forceinline__ uint32_t ld_dev_u32(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int rmw_add(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_int(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_int(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// All of this thread's earlier memory operations have completed (stores are
+// acknowledged by the device-coherent level).
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
+typedef unsigned long long u64;
+constexpr int kLatentUnits = 840;  // divisible by every latent split 1..8
+__device__ __forceinline__ u64 rmw_add64(u64* p, u64 v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 ld_u64(const u64* p) {
+  return __hip_atomic_load(const_cast<u64*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_u64(u64* p, u64 v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Spin (one lane) until *flag >= target; bounded, sets *status on timeout.
+template <typename T>
+__device__ __forceinline__ void wait_at_least(const T* flag, T target, u64* status) {
+  int n = 0;
+  while (__hip_atomic_load(const_cast<T*>(flag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+         target) {
+    __builtin_amdgcn_s_sleep(2);
+    if (++n > kSpinLimit) {
+      st_u64(status, 1);
+      break;
     }
   }
 }
 
-// ---------------------------------------------------------------------------
-// Combine the workgroup's tile with the other chunks of the same row and run
-// the epilogue once. Called by wave 0 only; `acc` is the workgroup total.
-//   part_base : partial slot 0 of this row (slots seq = 0..nseq-1 follow)
-//   counter   : arrival counter of this row (zero on entry, zero on exit)
-// ---------------------------------------------------------------------------
-template <int MT, int W, typename Store>
-__device__ __forceinline__ void finish_tile(f32x4 (&acc)[MT][W], int nseq, int seq,
-                                            float* part_base, int* counter, int Mrem, int lane,
-                                            Store&& store) {
-  constexpr int TP = 16 * W;
-  constexpr int TSZ = MT * 16 * TP;
-  if (nseq == 1) {
-    store(acc);
-    return;
+// A KE-element fragment of the latent t: the sum, in chunk order, of the n_kc
+// fp32 partials written by the latent workgroups of this launch (read with
+// device-coherent loads), rounded once to the activation dtype.
+template <int DT, int KE>
+__device__ __forceinline__ typename Mma<DT, KE>::Frag load_latent(const float* base, int64_t off,
+                                                                  int n_kc, int64_t kstride) {
+  float v[KE];
+#pragma unroll
+  for (int e = 0; e < KE; ++e) v[e] = ld_dev(base + off + e);
+  for (int k = 1; k < n_kc; ++k) {
+    const float* p = base + k * kstride + off;
+#pragma unroll
+    for (int e = 0; e < KE; ++e) v[e] += ld_dev(p + e);
   }
+  typename Mma<DT, KE>::Frag f;
+  if constexpr (DT == DT_F32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f.f[e] = v[e];
+  } else {
+#pragma unroll
+    for (int d = 0; d < KE / 2; ++d) f.d[d] = to_bits<DT>(v[2 * d]) | (to_bits<DT>(v[2 * d + 1]) << 16);
+  }
+  return f;
+}
+
+// ---------------------------------------------------------------------------
+// W adjacent elements in the activation dtype.
+// ---------------------------------------------------------------------------
+template <int DT, int W>
+__device__ __forceinline__ void st_w(void* base, int64_t off, const float (&v)[W]) {
+  if constexpr (DT == DT_F32) {
+    float* p = (float*)base + off;
+    if constexpr (W == 4) *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+    else if constexpr (W == 2) *(float2*)p = make_float2(v[0], v[1]);
+    else p[0] = v[0];
+  } else {
+    uint16_t* p = (uint16_t*)base + off;
+    if constexpr (W == 1) {
+      p[0] = (uint16_t)to_bits<DT>(v[0]);
+    } else {
+      uint32_t w[W / 2];
+#pragma unroll
+      for (int i = 0; i < W / 2; ++i) w[i] = to_bits<DT>(v[2 * i]) | (to_bits<DT>(v[2 * i + 1]) << 16);
+      if constexpr (W == 4) *(uint2*)p = make_uint2(w[0], w[1]);
+      else *(uint32_t*)p = w[0];
+    }
+  }
+}
+template <int DT, int W>
+__device__ __forceinline__ void ld_w(const void* base, int64_t off, float (&v)[W]) {
+  if constexpr (DT == DT_F32) {
+    const float* p = (const float*)base + off;
+#pragma unroll
+    for (int s = 0; s < W; ++s) v[s] = p[s];
+  } else {
+    const uint16_t* p = (const uint16_t*)base + off;
+#pragma unroll
+    for (int s = 0; s < W; ++s) v[s] = (DT == DT_BF16) ? bf16_to_f32(p[s]) : f16_to_f32(p[s]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic tree reduction of the kSW wave tiles into wave 0's registers:
+// rounds of halving; in each round wave i (< half) adds wave i + half's tile,
+// passed through LDS in groups of SLOTS tiles.
+// ---------------------------------------------------------------------------
+template <int MT, int W>
+constexpr int red_slots() {
+  return MT * W <= 8 ? 4 : 2;  // LDS: SLOTS × MT·W KiB
+}
+
+template <int MT, int W>
+__device__ __forceinline__ void tree_reduce(f32x4 (&acc)[MT][W], f32x4* red, int wid, int lane) {
+  constexpr int SLOTS = red_slots<MT, W>();
+#pragma unroll
+  for (int half = kSW / 2; half >= 1; half /= 2) {
+#pragma unroll
+    for (int g0 = 0; g0 < half; g0 += SLOTS) {
+      const int g1 = g0 + SLOTS < half ? g0 + SLOTS : half;
+      if (wid >= half + g0 && wid < half + g1) {
+        f32x4* slot = red + (wid - half - g0) * (MT * W * kWave);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int s = 0; s < W; ++s) slot[(mt * W + s) * kWave + lane] = acc[mt][s];
+      }
+      __syncthreads();
+      if (wid >= g0 && wid < g1) {
+        const f32x4* slot = red + (wid - g0) * (MT * W * kWave);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int s = 0; s < W; ++s) acc[mt][s] += slot[(mt * W + s) * kWave + lane];
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Wave-level exchange of a row tile held in registers (lane-native layout:
+// lane (c, g), element e of column tile s -> row 16·mt + 4g + e, column W·c + s).
+// Partial tiles live in memory row-major [16·MT][16·W] fp32.
+template <int MT, int W>
+__device__ __forceinline__ void store_partial(const f32x4 (&acc)[MT][W], float* part, int Mrem,
+                                              int lane) {
+  constexpr int TP = 16 * W;
   const int c = lane & 15, g = lane >> 4;
-  float* mine = part_base + (int64_t)seq * TSZ;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int rr = mt * 16 + 4 * g + e;
       if (rr < Mrem) {
-        float v[W];
 #pragma unroll
-        for (int s = 0; s < W; ++s) v[s] = acc[mt][s][e];
-        st_f32<W>(mine + rr * TP + W * c, v);
+        for (int s = 0; s < W; ++s) st_dev(part + rr * TP + W * c + s, acc[mt][s][e]);
       }
     }
-  fence_agent();
-  int old = 0;
-  if (lane == 0) old = atomic_inc_agent(counter);
-  old = __builtin_amdgcn_readfirstlane(old);
-  if (old != nseq - 1) return;
-  fence_agent();
-  f32x4 tot[MT][W];
+}
+template <int MT, int W>
+__device__ __forceinline__ void add_partial(f32x4 (&tot)[MT][W], const float* part, int Mrem,
+                                            int lane) {
+  constexpr int TP = 16 * W;
+  const int c = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int s = 0; s < W; ++s) tot[mt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < nseq; ++k) {
-    if (k == seq) {
+    for (int e = 0; e < 4; ++e) {
+      const int rr = mt * 16 + 4 * g + e;
+      if (rr < Mrem) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int s = 0; s < W; ++s) tot[mt][s] += acc[mt][s];
-    } else {
-      const float* pk = part_base + (int64_t)k * TSZ;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int rr = mt * 16 + 4 * g + e;
-          if (rr < Mrem) {
-            float v[W];
-            ld_f32<W>(pk + rr * TP + W * c, v);
-#pragma unroll
-            for (int s = 0; s < W; ++s) tot[mt][s][e] += v[s];
-          }
-        }
+        for (int s = 0; s < W; ++s) tot[mt][s][e] += ld_dev(part + rr * TP + W * c + s);
+      }
     }
-  }
-  if (lane == 0) atomic_store_agent(counter, 0);
-  store(tot);
-}
-
-// Sum the four waves' tiles into wave 0 (fixed order). Returns false for waves 1..3.
-template <int MT, int W>
-__device__ __forceinline__ bool reduce_waves(f32x4 (&acc)[MT][W], int wid, int lane) {
-  __shared__ f32x4 red[kWaves - 1][MT][W][kWave];
-  if (wid > 0) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int s = 0; s < W; ++s) red[wid - 1][mt][s][lane] = acc[mt][s];
-  }
-  __syncthreads();
-  if (wid != 0) return false;
-#pragma unroll
-  for (int w2 = 0; w2 < kWaves - 1; ++w2)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int s = 0; s < W; ++s) acc[mt][s] += red[w2][mt][s][lane];
-  return true;
 }
 
 // ---------------------------------------------------------------------------
-// Main streaming kernel.
-//   FUSED = false : out[:, row tile] += Σ blocks           (in-place BSR addmm)
-//   FUSED = true  : y[:, row tile]    = Σ blocks + t·Aᵀ + b (fused SLR linear)
+// Kernel arguments (one struct for every mode).
 // ---------------------------------------------------------------------------
-struct StreamArgs {
-  void* y;
-  int64_t ldy;
+struct SlrArgs {
+  // activations
   const void* x;
   int64_t ldx;
+  int M, m;
+  // output and the streamed part
+  void* y;
+  int64_t ldy;
   const int32_t* col;
   const void* values;
   const int32_t* plan;
+  int n_chunks;
+  int NB;
   const void* A;
   int64_t lda;
-  const void* t;
-  int64_t ldt;
   const void* bias;
-  float* partials;
-  int* counters;
   int64_t n_slots;
-  int NB, M, m;
+  float* part_main;
+  int* cnt_main;  // [MG][NB]
+  // latent
+  const void* B;
+  int64_t ldb;
+  void* t;
+  int64_t ldt;
+  int n_rt;       // 16-rank tiles
+  int n_kc;       // in_features chunks of the latent (fp32 partials summed by the consumers)
+  int ku_total;   // in_features in KM-column units
+  int ku_chunk;   // KM-column units per latent chunk
+  int n_lat_wgs;  // latent workgroups at the start of the grid (n_rt·n_kc·MG)
+  // latent handshake: sync[0] status (1 = a wait gave up), then per token tile
+  // mg two monotonic counters: sync[1 + 2·mg] latent workgroups done,
+  // sync[2 + 2·mg] consumer tickets
+  // Each latent workgroup adds kLatentUnits / n_kc, so one launch adds
+  // n_rt·kLatentUnits per token tile whatever its K split (n_kc ≤ 8 divides 840).
+  u64* sync;
+  int lr_wgs;     // workgroups that consume the latent (per token tile)
+  int lat_weight; // kLatentUnits / n_kc
 };
 
-template <int DT, int P, int MT, bool FUSED, int UNR>
-__global__ __launch_bounds__(kThreads) void bsr_stream_kernel(StreamArgs a) {
+// ---------------------------------------------------------------------------
+// Latent workgroup: t[token tile, 16-rank tile rt] over all of in_features.
+// ---------------------------------------------------------------------------
+template <int DT, int MT>
+__device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) {
+  constexpr int KE = (DT == DT_F32) ? 4 : 8;
+  using MM = Mma<DT, KE>;
+  using Frag = typename MM::Frag;
+  constexpr int KM = MM::KM;
+  constexpr int UNR = MT == 1 ? 16 : (MT == 2 ? 8 : 4);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = wave_uniform(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int per_mg = a.n_rt * a.n_kc;
+  const int mg = wg / per_mg, rt = (wg % per_mg) / a.n_kc, kc = wg % a.n_kc;
+  const int m0 = mg * MT * 16;
+  const int Mrem = min(a.M - m0, MT * 16);
+  const int64_t brow = (int64_t)(rt * 16 + c) * a.ldb;
+  const int ub = kc * a.ku_chunk, ue = min(ub + a.ku_chunk, a.ku_total);
+
+  f32x4 acc[MT][1];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int u0 = ub + wid; u0 < ue; u0 += kSW * UNR) {
+    Frag xf[UNR][MT];
+    Frag bf[UNR];
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int u = u0 + k * kSW;
+      if (u < ue) {
+        const int kcol = u * KM + KE * g;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int rr = mt * 16 + c;
+          const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
+          xf[k][mt] = (valid > 0)
+                          ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol, valid)
+                          : zero_frag<DT, KE>();
+        }
+        bf[k] = load_kfrag<DT, KE>(a.B, brow + kcol, KE);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      if (u0 + k * kSW < ue) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][0], xf[k][mt], bf[k]);
+      }
+    }
+  }
+
+  tree_reduce<MT, 1>(acc, red, wid, lane);
+  if (wid != 0) return;
+  // wave 0: lane (c, g) holds rows 16·mt + 4g + e of rank rt·16 + c; store the
+  // fp32 partial of chunk kc: t[kc][token row][rank]
+  float* tp = (float*)a.t + (int64_t)kc * a.M * a.ldt;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rr = mt * 16 + 4 * g + e;
+      if (rr < Mrem) st_dev(tp + (int64_t)(m0 + rr) * a.ldt + rt * 16 + c, acc[mt][0][e]);
+    }
+  wait_mem();
+  if (lane == 0) rmw_add64(a.sync + 1 + 2 * mg, (u64)a.lat_weight);
+}
+
+// ---------------------------------------------------------------------------
+// Streaming workgroup: one plan chunk for one token tile.
+// ---------------------------------------------------------------------------
+template <int DT, int P, int MT, int MODE, int UNR>
+__device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f32x4* red) {
   constexpr int Q = P;
   constexpr int W = P / 16;
   constexpr int KE = (DT == DT_F32) ? 4 : (Q >= 32 ? 8 : 4);
@@ -208,14 +373,14 @@ __global__ __launch_bounds__(kThreads) void bsr_stream_kernel(StreamArgs a) {
   using FragL = typename ML::Frag;
   constexpr int NLS = 32 / ML::KM;  // macro steps per 32-rank unit
   constexpr int EB = Elem<DT>::bytes;
+  constexpr int TSZ = MT * 16 * P;
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = wave_uniform(threadIdx.x >> 6);
   const int c = lane & 15, g = lane >> 4;
-  const int32_t* d = a.plan + (int64_t)blockIdx.x * SSL_PLAN_STRIDE;
-  const int row = d[0], ubeg = d[1], uend = d[2], seq = d[3], nseq = d[4], slot = d[5];
-  const int nblk = d[6], blk0 = d[7];
-  const int mg = blockIdx.y;
+  const int32_t* d = a.plan + (int64_t)chunk * SSL_PLAN_STRIDE;
+  const int row = d[0], bb = d[1], be = d[2], lb = d[3], le = d[4], seq = d[5], nseq = d[6];
+  const int slot = d[7];
   const int m0 = mg * MT * 16;
   const int Mrem = min(a.M - m0, MT * 16);
 
@@ -225,202 +390,201 @@ __global__ __launch_bounds__(kThreads) void bsr_stream_kernel(StreamArgs a) {
 #pragma unroll
     for (int s = 0; s < W; ++s) acc[mt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // ---- sparse blocks ------------------------------------------------------
-  const int se = min(uend, nblk);
-  for (int u0 = ubeg + wid; u0 < se; u0 += kWaves * UNR) {
+  const bool used_t = (MODE == MODE_FUSED) && lb < le;
+  // A consumer of the latent takes a ticket at once (its latency hides behind
+  // the row's loads). Launch k's consumers hold tickets k·lr_wgs ... and wait
+  // for (k + 1)·(latent workgroups) completions, so no counter is ever reset.
+  u64 ticket = 0;
+  if (used_t && threadIdx.x == 0) ticket = rmw_add64(a.sync + 2 + 2 * mg, 1);
+
+  // ---- sparse blocks: a batch issues all its loads (x, then the block) unit by
+  // unit before the first MFMA, so each unit waits only for its own data.
+  for (int u0 = bb + wid; u0 < be; u0 += kSW * UNR) {
     Raw raw[UNR][NKS];
-    int colb[UNR];
+    Frag xf[UNR][NKS][MT];
 #pragma unroll
     for (int k = 0; k < UNR; ++k) {
-      const int u = u0 + k * kWaves;
-      colb[k] = 0;
-      if (u < se) {
-        const int blk = blk0 + u;
-        colb[k] = a.col[blk] * Q;
-        const char* vb = (const char*)a.values + (int64_t)blk * (P * Q * EB);
+      const int u = u0 + k * kSW;
+      if (u < be) {
+        const int colb = a.col[u] * Q;
+        const char* vb = (const char*)a.values + (int64_t)u * (P * Q * EB);
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) load_vstep<DT, KE, W>(raw[k][ks], vb, P, ks * KM, lane);
+        for (int ks = 0; ks < NKS; ++ks) {
+          const int kcol = colb + ks * KM + KE * g;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int rr = mt * 16 + c;
+            const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
+            xf[k][ks][mt] = (valid > 0) ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol,
+                                                             valid)
+                                        : zero_frag<DT, KE>();
+          }
+          load_vstep<DT, KE, W>(raw[k][ks], vb, P, ks * KM, lane);
+        }
       }
     }
 #pragma unroll
     for (int k = 0; k < UNR; ++k) {
-      const int u = u0 + k * kWaves;
-      if (u < se) {
+      if (u0 + k * kSW < be) {
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const int kcol = colb[k] + ks * KM + KE * g;
-          Frag xf[MT];
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const int rr = mt * 16 + c;
-            int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
-            xf[mt] = (valid > 0) ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol, valid)
-                                 : zero_frag<DT, KE>();
-          }
+        for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
           for (int s = 0; s < W; ++s) {
             const Frag vf = vfrag<DT, KE, W>(raw[k][ks], s);
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][s], xf[mt], vf);
+            for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][s], xf[k][ks][mt], vf);
+          }
+      }
+    }
+  }
+
+  // ---- low-rank units: 32 ranks of A per unit, t·Aᵀ. A does not depend on the
+  // latent, so every wave issues its first A fragments before one thread of
+  // the workgroup waits for the latent.
+  if constexpr (MODE == MODE_FUSED) {
+    if (used_t) {
+      constexpr int ULR = 2;
+      FragL af[ULR][NLS][W];
+      auto load_a = [&](int base) {
+#pragma unroll
+        for (int k = 0; k < ULR; ++k) {
+          const int u = base + k * kSW;
+          if (u < le) {
+#pragma unroll
+            for (int ls = 0; ls < NLS; ++ls)
+#pragma unroll
+              for (int s = 0; s < W; ++s)
+                af[k][ls][s] = load_kfrag<DT, KEL>(
+                    a.A, (int64_t)(row * P + W * c + s) * a.lda + u * 32 + ls * ML::KM + KEL * g,
+                    KEL);
           }
         }
+      };
+      load_a(lb + wid);
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const u64 per_launch = (u64)a.n_rt * kLatentUnits;
+        wait_at_least<u64>(a.sync + 1 + 2 * mg, (ticket / a.lr_wgs + 1) * per_launch, a.sync);
       }
-    }
-  }
-
-  // ---- low-rank units: 32 ranks of A per unit, t·Aᵀ -------------------------
-  if constexpr (FUSED) {
-    const int lb = max(ubeg, nblk);
-    for (int u = lb + wid; u < uend; u += kWaves) {
-      const int r0 = (u - nblk) * 32;
+      __syncthreads();
+      for (int u0 = lb + wid; u0 < le; u0 += kSW * ULR) {
 #pragma unroll
-      for (int ls = 0; ls < NLS; ++ls) {
-        const int kr = r0 + ls * ML::KM + KEL * g;
-        FragL af[W];
+        for (int k = 0; k < ULR; ++k) {
+          const int u = u0 + k * kSW;
+          if (u < le) {
 #pragma unroll
-        for (int s = 0; s < W; ++s)
-          af[s] = load_kfrag<DT, KEL>(a.A, (int64_t)(row * P + W * c + s) * a.lda + kr, KEL);
+            for (int ls = 0; ls < NLS; ++ls) {
+              const int kr = u * 32 + ls * ML::KM + KEL * g;
+              FragL tf[MT];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int rr = mt * 16 + c;
-          const FragL tf = (rr < Mrem)
-                               ? load_kfrag<DT, KEL>(a.t, (int64_t)(m0 + rr) * a.ldt + kr, KEL)
-                               : zero_frag<DT, KEL>();
+              for (int mt = 0; mt < MT; ++mt) {
+                const int rr = mt * 16 + c;
+                tf[mt] = (rr < Mrem) ? load_latent<DT, KEL>((const float*)a.t,
+                                                            (int64_t)(m0 + rr) * a.ldt + kr, a.n_kc,
+                                                            (int64_t)a.M * a.ldt)
+                                     : zero_frag<DT, KEL>();
+              }
 #pragma unroll
-          for (int s = 0; s < W; ++s) ML::run(acc[mt][s], tf, af[s]);
+              for (int s = 0; s < W; ++s)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) ML::run(acc[mt][s], tf[mt], af[k][ls][s]);
+            }
+          }
         }
+        if (u0 + kSW * ULR < le) load_a(u0 + kSW * ULR);
       }
     }
   }
 
-  if (!reduce_waves<MT, W>(acc, wid, lane)) return;
+  tree_reduce<MT, W>(acc, red, wid, lane);
+  if (wid != 0) return;
 
-  auto store = [&](f32x4(&v)[MT][W]) {
-    const int j0 = row * P + W * c;
-    float bv[W];
+  // ---- wave 0: combine (split rows) and epilogue ---------------------------
+  if (nseq > 1) {
+    float* part_base = a.part_main + ((int64_t)mg * a.n_slots + slot) * TSZ;
+    int* counter = a.cnt_main + (int64_t)mg * a.NB + row;
+    const bool finaliser_mode = (MODE == MODE_FUSED) && a.n_rt > 0;
+    if (finaliser_mode && used_t) {
+      // the row's finaliser: wait for the other nseq - 1 chunks
+      if (lane == 0) wait_at_least<int>(counter, nseq - 1, a.sync);
+    } else {
+      store_partial<MT, W>(acc, part_base + (int64_t)seq * TSZ, Mrem, lane);
+      wait_mem();
+      int old = 0;
+      if (lane == 0) old = rmw_add(counter, 1);
+      old = __builtin_amdgcn_readfirstlane(old);
+      if (finaliser_mode || old != nseq - 1) return;
+    }
+    // sum the partials in chunk order, this chunk's tile at its own position
+    f32x4 tot[MT][W];
 #pragma unroll
-    for (int s = 0; s < W; ++s) bv[s] = 0.f;
-    if constexpr (FUSED) {
-      if (a.bias != nullptr) {
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int s = 0; s < W; ++s) bv[s] = load_scalar<DT>(a.bias, j0 + s);
+      for (int s = 0; s < W; ++s) tot[mt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < nseq; ++k) {
+      if (k == seq) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int s = 0; s < W; ++s) tot[mt][s] += acc[mt][s];
+      } else {
+        add_partial<MT, W>(tot, part_base + (int64_t)k * TSZ, Mrem, lane);
       }
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int rr = mt * 16 + 4 * g + e;
-        if (rr < Mrem) {
-          const int64_t off = (int64_t)(m0 + rr) * a.ldy + j0;
-          float o[W];
-          if constexpr (FUSED) {
+      for (int s = 0; s < W; ++s) acc[mt][s] = tot[mt][s];
+    if (lane == 0) st_int(counter, 0);
+  }
+
+  // epilogue: lane (c, g) owns W adjacent output columns of rows 16·mt + 4g + e
+  const int j0 = row * P + W * c;
+  float bv[W];
 #pragma unroll
-            for (int s = 0; s < W; ++s) o[s] = v[mt][s][e] + bv[s];
-          } else {
-            ld_elems<DT, W>(a.y, off, o);
-#pragma unroll
-            for (int s = 0; s < W; ++s) o[s] += v[mt][s][e];
-          }
-          st_elems<DT, W>(a.y, off, o);
-        }
-      }
-  };
-  constexpr int TSZ = MT * 16 * P;
-  finish_tile<MT, W>(acc, nseq, seq, a.partials + ((int64_t)mg * a.n_slots + slot) * TSZ,
-                     a.counters + (int64_t)mg * a.NB + row, Mrem, lane, store);
-}
-
-// ---------------------------------------------------------------------------
-// Latent kernel: t[M, r_pad] = x[M, :m] · B[r_pad, :m_pad]ᵀ, rounded to the
-// activation dtype. Workgroup = (64-rank group, chunk of in_features).
-// ---------------------------------------------------------------------------
-struct LatentArgs {
-  void* t;
-  int64_t ldt;
-  const void* x;
-  int64_t ldx;
-  const void* B;
-  int64_t ldb;
-  float* partials;
-  int* counters;
-  int n_rg, n_kc, ku_total, ku_chunk;
-  int M, m;
-};
-
-template <int DT, int MT, int UNR>
-__global__ __launch_bounds__(kThreads) void lr_latent_kernel(LatentArgs a) {
-  constexpr int KE = (DT == DT_F32) ? 4 : 8;
-  using MM = Mma<DT, KE>;
-  using Frag = typename MM::Frag;
-  constexpr int KM = MM::KM;
-  constexpr int W = 4;
-
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wid = wave_uniform(threadIdx.x >> 6);
-  const int c = lane & 15, g = lane >> 4;
-  const int rg = blockIdx.x / a.n_kc, kc = blockIdx.x % a.n_kc;
-  const int mg = blockIdx.y;
-  const int m0 = mg * MT * 16;
-  const int Mrem = min(a.M - m0, MT * 16);
-  const int ub = kc * a.ku_chunk, ue = min(ub + a.ku_chunk, a.ku_total);
-
-  f32x4 acc[MT][W];
+  for (int s = 0; s < W; ++s) bv[s] = 0.f;
+  if constexpr (MODE == MODE_FUSED) {
+    if (a.bias != nullptr) ld_w<DT, W>(a.bias, j0, bv);
+  }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int s = 0; s < W; ++s) acc[mt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int u0 = ub + wid; u0 < ue; u0 += kWaves * UNR) {
-    Frag bf[UNR][W];
+    for (int e = 0; e < 4; ++e) {
+      const int rr = mt * 16 + 4 * g + e;
+      if (rr < Mrem) {
+        const int64_t off = (int64_t)(m0 + rr) * a.ldy + j0;
+        float o[W];
+        if constexpr (MODE == MODE_FUSED) {
 #pragma unroll
-    for (int k = 0; k < UNR; ++k) {
-      const int u = u0 + k * kWaves;
-      if (u < ue) {
+          for (int s = 0; s < W; ++s) o[s] = acc[mt][s][e] + bv[s];
+        } else {
+          ld_w<DT, W>(a.y, off, o);
 #pragma unroll
-        for (int s = 0; s < W; ++s)
-          bf[k][s] = load_kfrag<DT, KE>(a.B, (int64_t)(rg * 64 + W * c + s) * a.ldb + u * KM + KE * g, KE);
+          for (int s = 0; s < W; ++s) o[s] += acc[mt][s][e];
+        }
+        st_w<DT, W>(a.y, off, o);
       }
     }
-#pragma unroll
-    for (int k = 0; k < UNR; ++k) {
-      const int u = u0 + k * kWaves;
-      if (u < ue) {
-        const int kcol = u * KM + KE * g;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int rr = mt * 16 + c;
-          int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
-          const Frag xf = (valid > 0)
-                              ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol, valid)
-                              : zero_frag<DT, KE>();
-#pragma unroll
-          for (int s = 0; s < W; ++s) MM::run(acc[mt][s], xf, bf[k][s]);
-        }
-      }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel. Grid (1-D): [latent workgroups][stream chunks × token tiles].
+// ---------------------------------------------------------------------------
+template <int DT, int P, int MT, int MODE, int UNR>
+__global__ __launch_bounds__(kST) void slr_kernel(SlrArgs a) {
+  constexpr int W = P / 16;
+  constexpr int SLOTS = red_slots<MT, W>();
+  __shared__ f32x4 red[SLOTS * MT * W * kWave];
+  const int b = blockIdx.x;
+  if constexpr (MODE == MODE_FUSED) {
+    if (b < a.n_lat_wgs) {
+      latent_wg<DT, MT>(a, b, red);
+      return;
     }
   }
-
-  if (!reduce_waves<MT, W>(acc, wid, lane)) return;
-
-  auto store = [&](f32x4(&v)[MT][W]) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int rr = mt * 16 + 4 * g + e;
-        if (rr < Mrem) {
-          float o[W];
-#pragma unroll
-          for (int s = 0; s < W; ++s) o[s] = v[mt][s][e];
-          st_elems<DT, W>(a.t, (int64_t)(m0 + rr) * a.ldt + rg * 64 + W * c, o);
-        }
-      }
-  };
-  constexpr int TSZ = MT * 16 * 64;
-  finish_tile<MT, W>(acc, a.n_kc, kc,
-                     a.partials + ((int64_t)mg * a.n_rg + rg) * a.n_kc * TSZ,
-                     a.counters + (int64_t)mg * a.n_rg + rg, Mrem, lane, store);
+  const int sb = b - (MODE == MODE_FUSED ? a.n_lat_wgs : 0);
+  const int mg = sb / a.n_chunks, chunk = sb % a.n_chunks;
+  stream_wg<DT, P, MT, MODE, UNR>(a, chunk, mg, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -428,26 +592,27 @@ __global__ __launch_bounds__(kThreads) void lr_latent_kernel(LatentArgs a) {
 // ---------------------------------------------------------------------------
 namespace {
 
-template <int DT, int P>
+template <int DT, int P, int MT>
 constexpr int stream_unroll() {
-  // Keep roughly 8–16 KiB of one wave's weight loads in flight.
+  // Units per wave per batch: about 32 KiB of weights per wave for one token
+  // tile (a 32-block row in one batch of the 8 waves), fewer for wide tiles.
   constexpr int bytes = P * P * Elem<DT>::bytes;
-  return bytes >= 16384 ? 1 : (bytes >= 8192 ? 2 : (bytes >= 2048 ? 4 : 8));
+  constexpr int u = bytes >= 16384 ? 2 : (bytes >= 8192 ? 4 : (bytes >= 2048 ? 8 : 16));
+  constexpr int d = MT >= 4 ? 4 : MT;
+  return u / d > 0 ? u / d : 1;
 }
 
-template <int DT, int P, int MT, bool FUSED>
-hipError_t launch_stream(const StreamArgs& a, int64_t n_chunks, int MG, hipStream_t s) {
-  constexpr int UNR = stream_unroll<DT, P>();
-  hipLaunchKernelGGL((bsr_stream_kernel<DT, P, MT, FUSED, UNR>), dim3((unsigned)n_chunks, MG),
-                     dim3(kThreads), 0, s, a);
+template <int DT, int P, int MT, int MODE>
+hipError_t launch(const SlrArgs& a, int64_t blocks, hipStream_t s) {
+  constexpr int UNR = stream_unroll<DT, P, MT>();
+  hipLaunchKernelGGL((slr_kernel<DT, P, MT, MODE, UNR>), dim3((unsigned)blocks), dim3(kST), 0, s, a);
   return hipGetLastError();
 }
 
-template <int DT, bool FUSED>
-hipError_t dispatch_stream(int P, int MT, const StreamArgs& a, int64_t n_chunks, int MG,
-                           hipStream_t s) {
-#define SSL_CASE(PP, MM)                                                  \
-  if (P == PP && MT == MM) return launch_stream<DT, PP, MM, FUSED>(a, n_chunks, MG, s);
+template <int DT, int MODE>
+hipError_t dispatch_p(int P, int MT, const SlrArgs& a, int64_t blocks, hipStream_t s) {
+#define SSL_CASE(PP, MM) \
+  if (P == PP && MT == MM) return launch<DT, PP, MM, MODE>(a, blocks, s);
   SSL_CASE(16, 1) SSL_CASE(16, 2) SSL_CASE(16, 4)
   SSL_CASE(32, 1) SSL_CASE(32, 2) SSL_CASE(32, 4)
   SSL_CASE(64, 1) SSL_CASE(64, 2) SSL_CASE(64, 4)
@@ -455,43 +620,41 @@ hipError_t dispatch_stream(int P, int MT, const StreamArgs& a, int64_t n_chunks,
   return hipErrorInvalidValue;
 }
 
-template <bool FUSED>
-hipError_t dispatch_stream_dt(int dtype, int P, int MT, const StreamArgs& a, int64_t n_chunks,
-                              int MG, hipStream_t s) {
+template <int MODE>
+hipError_t dispatch(int dtype, int P, int MT, const SlrArgs& a, int64_t blocks, hipStream_t s) {
   switch (dtype) {
-    case SSL_F32: return dispatch_stream<DT_F32, FUSED>(P, MT, a, n_chunks, MG, s);
-    case SSL_BF16: return dispatch_stream<DT_BF16, FUSED>(P, MT, a, n_chunks, MG, s);
-    case SSL_F16: return dispatch_stream<DT_F16, FUSED>(P, MT, a, n_chunks, MG, s);
+    case SSL_F32: return dispatch_p<DT_F32, MODE>(P, MT, a, blocks, s);
+    case SSL_BF16: return dispatch_p<DT_BF16, MODE>(P, MT, a, blocks, s);
+    case SSL_F16: return dispatch_p<DT_F16, MODE>(P, MT, a, blocks, s);
   }
   return hipErrorInvalidValue;
 }
 
-template <int DT, int MT>
-hipError_t launch_latent(const LatentArgs& a, int MG, hipStream_t s) {
-  hipLaunchKernelGGL((lr_latent_kernel<DT, MT, 2>), dim3((unsigned)(a.n_rg * a.n_kc), MG),
-                     dim3(kThreads), 0, s, a);
-  return hipGetLastError();
-}
-
-hipError_t dispatch_latent(int dtype, int MT, const LatentArgs& a, int MG, hipStream_t s) {
-#define SSL_CASE(DD, MM) \
-  if (dtype == DD && MT == MM) return launch_latent<DD, MM>(a, MG, s);
-  SSL_CASE(DT_F32, 1) SSL_CASE(DT_F32, 2) SSL_CASE(DT_F32, 4)
-  SSL_CASE(DT_BF16, 1) SSL_CASE(DT_BF16, 2) SSL_CASE(DT_BF16, 4)
-  SSL_CASE(DT_F16, 1) SSL_CASE(DT_F16, 2) SSL_CASE(DT_F16, 4)
-#undef SSL_CASE
-  return hipErrorInvalidValue;
+// In_features chunks of the latent. More chunks put more workgroups (and so
+// more of the device's memory parallelism) on the latent, which every row
+// needs before it can finish; each chunk adds an fp32 partial of t that every
+// row workgroup reads, so the split shrinks as the token count grows.
+int latent_split(int64_t M, int64_t m_pad) {
+  const int64_t by_width = m_pad / 512 > 1 ? m_pad / 512 : 1;  // ≥ 512 columns per chunk
+  const int64_t Mc = M > 0 ? M : 1;
+  int64_t by_tokens = 32 / Mc;
+  if (by_tokens > 8) by_tokens = 8;
+  if (by_tokens < 1) by_tokens = 1;
+  return (int)(by_width < by_tokens ? by_width : by_tokens);
 }
 
 bool supported_block(int p, int q) { return p == q && (p == 16 || p == 32 || p == 64); }
 bool supported_dtype(int dt) { return dt == SSL_F32 || dt == SSL_BF16 || dt == SSL_F16; }
 
-// Workspace layout of one call (offsets in bytes).
+// Scratch layout of one fused call. Counters live in their own int32 array
+// (zero at rest, never shared with data); the data workspace holds the latent
+// and the fp32 partial tiles of split rows (byte offsets).
 struct Layout {
   int MT, MG;
-  int n_rg, n_kc, ku_total, ku_chunk;
-  int64_t counters_main, counters_lat, counter_end;
-  int64_t t_buf, part_lat, part_main, total;
+  int n_rt, n_kc, ku_total, ku_chunk;
+  int64_t cnt_total;  // int32 row counters: [MG][NB]
+  int64_t n_sync;     // u64 sync words: status + 2 per token tile
+  int64_t t_buf, part_main, total;
 };
 
 Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, int64_t n_slots,
@@ -499,30 +662,19 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   Layout L{};
   L.MT = tile_mt(M);
   L.MG = (int)((M + 16 * L.MT - 1) / (16 * L.MT));
-  L.n_rg = (int)(r_pad / 64);
-  const int KM = (dtype == SSL_F32) ? 16 : 32;
+  L.n_rt = (int)(r_pad / 16);
+  const int KM = dtype == SSL_F32 ? 16 : 32;
   L.ku_total = (int)(m_pad / KM);
-  // One token tile: split in_features so the latent kernel covers the device;
-  // several tiles already give enough workgroups.
-  int chunk = L.ku_total;
-  if (L.MG == 1) {
-    chunk = (L.ku_total + 31) / 32;
-    if (chunk < 4) chunk = 4;
-    if (chunk > L.ku_total) chunk = L.ku_total;
-  }
-  if (chunk < 1) chunk = 1;
-  L.ku_chunk = chunk;
-  L.n_kc = L.ku_total > 0 ? (L.ku_total + chunk - 1) / chunk : 1;
+  L.n_kc = latent_split(M, m_pad);  // 1..8
+  L.ku_chunk = (L.ku_total + L.n_kc - 1) / L.n_kc;
+  if (L.ku_chunk < 1) L.ku_chunk = 1;
+  L.n_kc = (L.ku_total + L.ku_chunk - 1) / L.ku_chunk;
+  if (L.n_kc < 1) L.n_kc = 1;
+  L.cnt_total = (int64_t)L.MG * NB;
+  L.n_sync = 1 + 2 * (int64_t)L.MG;
   int64_t off = 0;
-  L.counters_main = off;
-  off = align_up(off + 4 * (int64_t)L.MG * NB, 256);
-  L.counters_lat = off;
-  off = align_up(off + 4 * (int64_t)L.MG * L.n_rg, 256);
-  L.counter_end = off;
   L.t_buf = off;
-  off = align_up(off + (int64_t)elem_bytes(dtype) * M * r_pad, 256);
-  L.part_lat = off;
-  if (L.n_kc > 1) off = align_up(off + 4 * (int64_t)L.MG * L.n_rg * L.n_kc * (16 * L.MT * 64), 256);
+  off = align_up(off + 4 * (int64_t)L.n_kc * M * r_pad, 256);
   L.part_main = off;
   off = align_up(off + 4 * (int64_t)L.MG * n_slots * (16 * L.MT * p), 256);
   L.total = off;
@@ -536,23 +688,25 @@ using namespace ssl;
 
 extern "C" {
 
-int64_t ssl_bsr_addmm_counter_bytes(int64_t M, int64_t NB) {
+int64_t ssl_bsr_addmm_counter_count(int64_t M, int64_t NB) {
   const int MT = tile_mt(M);
   const int64_t MG = (M + 16 * MT - 1) / (16 * MT);
-  return align_up(4 * MG * NB, 256);
+  return MG * NB;
 }
 
 int64_t ssl_bsr_addmm_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t n_slots) {
+  (void)NB;
   const int MT = tile_mt(M);
   const int64_t MG = (M + 16 * MT - 1) / (16 * MT);
-  return ssl_bsr_addmm_counter_bytes(M, NB) + align_up(4 * MG * n_slots * (16 * MT * block_p), 256);
+  return align_up(4 * MG * n_slots * (16 * MT * block_p), 256);
 }
 
 int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, const int32_t* col,
                           const void* values, const int32_t* plan, int64_t n_chunks,
                           int64_t n_slots, int64_t M, int64_t N, int64_t K, int64_t NB,
-                          int32_t block_p, int32_t block_q, int32_t dtype, void* workspace,
-                          int64_t workspace_bytes, void* stream) {
+                          int32_t block_p, int32_t block_q, int32_t dtype, int32_t* counters,
+                          int64_t n_counters, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
   clear_error();
   if (!supported_dtype(dtype)) return fail(SSL_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
   if (!supported_block(block_p, block_q))
@@ -563,7 +717,9 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
   if (N != NB * block_p) return fail(SSL_ERR_INVALID, "out N=%lld does not match crow/block_p", (long long)N);
   if (K % block_q) return fail(SSL_ERR_INVALID, "x K=%lld must be divisible by block_q", (long long)K);
   if (M == 0 || n_chunks == 0) return SSL_OK;
-  if (n_chunks > 0x7fffffff) return fail(SSL_ERR_INVALID, "too many chunks");
+  const int MT = tile_mt(M);
+  const int64_t MG = (M + 16 * MT - 1) / (16 * MT);
+  if (n_chunks * MG > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
   const int eb = elem_bytes(dtype);
   if (!out || !x || !col || !values || !plan) return fail(SSL_ERR_INVALID, "null pointer");
   if (ldx < K || ldo < N) return fail(SSL_ERR_INVALID, "leading dimension smaller than row");
@@ -573,46 +729,51 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
   const int64_t need = ssl_bsr_addmm_workspace_size(M, NB, block_p, n_slots);
   if (workspace_bytes < need || (need > 0 && !workspace))
     return fail(SSL_ERR_WORKSPACE, "workspace of %lld bytes needed", (long long)need);
-  if (!aligned(workspace, 256)) return fail(SSL_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  if (workspace && !aligned(workspace, 256))
+    return fail(SSL_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  if (n_counters < ssl_bsr_addmm_counter_count(M, NB) || !counters)
+    return fail(SSL_ERR_WORKSPACE, "%lld zeroed counters needed",
+                (long long)ssl_bsr_addmm_counter_count(M, NB));
 
-  const int MT = tile_mt(M);
-  const int MG = (int)((M + 16 * MT - 1) / (16 * MT));
-  StreamArgs a{};
-  a.y = out; a.ldy = ldo; a.x = x; a.ldx = ldx; a.col = col; a.values = values; a.plan = plan;
-  a.counters = (int*)workspace;
-  a.partials = (float*)((char*)workspace + ssl_bsr_addmm_counter_bytes(M, NB));
-  a.n_slots = n_slots; a.NB = (int)NB; a.M = (int)M; a.m = (int)K;
-  return check_hip(dispatch_stream_dt<false>(dtype, block_p, MT, a, n_chunks, MG, (hipStream_t)stream),
+  SlrArgs a{};
+  a.x = x; a.ldx = ldx; a.M = (int)M; a.m = (int)K;
+  a.y = out; a.ldy = ldo; a.col = col; a.values = values; a.plan = plan;
+  a.n_chunks = (int)n_chunks; a.NB = (int)NB;
+  a.n_slots = n_slots; a.part_main = (float*)workspace; a.cnt_main = counters;
+  return check_hip(dispatch<MODE_OP>(dtype, block_p, MT, a, n_chunks * MG, (hipStream_t)stream),
                    "bsr_addmm launch");
 }
 
-int64_t ssl_slr_counter_bytes(int64_t M, int64_t NB, int64_t r_pad, int64_t m_pad) {
-  return slr_layout(M, NB, 16, r_pad, m_pad, 0, SSL_BF16).counter_end;
+int64_t ssl_slr_counter_count(int64_t M, int64_t NB) {
+  return slr_layout(M, NB, 16, 0, 64, 0, SSL_BF16).cnt_total;
 }
+
+int64_t ssl_slr_sync_count(int64_t M) { return slr_layout(M, 0, 16, 0, 64, 0, SSL_BF16).n_sync; }
 
 int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r_pad,
                                int64_t m_pad, int64_t n_slots, int32_t dtype) {
   return slr_layout(M, NB, block_p, r_pad, m_pad, n_slots, dtype).total;
 }
 
-int ssl_slr_forward_phase(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A,
-                          const void* B, const void* bias, const int32_t* col, const void* values,
-                          const int32_t* plan, int64_t n_chunks, int64_t n_slots, int64_t M,
-                          int64_t m, int64_t m_pad, int64_t NB, int64_t r_pad, int32_t block_p,
-                          int32_t block_q, int32_t dtype, void* workspace, int64_t workspace_bytes,
-                          int32_t phase, void* stream) {
-  if (phase < 0 || phase > 2) return fail(SSL_ERR_INVALID, "phase must be 0, 1 or 2");
+int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A, const void* B,
+                    const void* bias, const int32_t* col, const void* values, const int32_t* plan,
+                    int64_t n_chunks, int64_t n_slots, int64_t lr_wgs, int64_t M, int64_t m,
+                    int64_t m_pad, int64_t NB, int64_t r_pad, int32_t block_p, int32_t block_q,
+                    int32_t dtype, int32_t* counters, int64_t n_counters, uint64_t* sync,
+                    int64_t n_sync, void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   if (!supported_dtype(dtype)) return fail(SSL_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
   if (!supported_block(block_p, block_q))
     return fail(SSL_ERR_UNSUPPORTED,
                 "SLR kernel needs square 16, 32 or 64 blocks, got %dx%d", block_p, block_q);
-  if (M < 0 || m < 0 || NB < 0 || r_pad < 0 || n_chunks < 0 || n_slots < 0)
+  if (M < 0 || m < 0 || NB < 0 || r_pad < 0 || n_chunks < 0 || n_slots < 0 || lr_wgs < 0)
     return fail(SSL_ERR_INVALID, "negative size");
   if (r_pad % 64 || m_pad % 64 || m_pad < m)
     return fail(SSL_ERR_INVALID, "r_pad and m_pad must be multiples of 64 with m_pad >= m");
   if (M == 0 || NB == 0) return SSL_OK;
   if (n_chunks == 0) return fail(SSL_ERR_INVALID, "empty plan for a non-empty output");
+  if ((r_pad > 0) != (lr_wgs > 0) || lr_wgs > n_chunks)
+    return fail(SSL_ERR_INVALID, "lr_wgs must count the plan's chunks with low-rank units");
   const int eb = elem_bytes(dtype);
   if (!y || !x || !plan || (r_pad > 0 && (!A || !B))) return fail(SSL_ERR_INVALID, "null pointer");
   if (ldx < m || ldy < NB * block_p) return fail(SSL_ERR_INVALID, "leading dimension smaller than row");
@@ -624,36 +785,28 @@ int ssl_slr_forward_phase(void* y, int64_t ldy, const void* x, int64_t ldx, cons
   if (workspace_bytes < L.total || !workspace)
     return fail(SSL_ERR_WORKSPACE, "workspace of %lld bytes needed", (long long)L.total);
   if (!aligned(workspace, 256)) return fail(SSL_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
+  if (n_counters < L.cnt_total || !counters)
+    return fail(SSL_ERR_WORKSPACE, "%lld zeroed counters needed", (long long)L.cnt_total);
+  if (n_sync < L.n_sync || !sync)
+    return fail(SSL_ERR_WORKSPACE, "%lld sync words needed", (long long)L.n_sync);
+  if (!aligned(sync, 8)) return fail(SSL_ERR_WORKSPACE, "sync words must be 8-byte aligned");
+  const int64_t n_lat = (int64_t)L.n_rt * L.n_kc * L.MG;
+  const int64_t blocks = n_lat + n_chunks * L.MG;
+  if (blocks > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
   char* ws = (char*)workspace;
 
-  if (r_pad > 0 && phase != 2) {
-    LatentArgs la{};
-    la.t = ws + L.t_buf; la.ldt = r_pad; la.x = x; la.ldx = ldx; la.B = B; la.ldb = m_pad;
-    la.partials = (float*)(ws + L.part_lat); la.counters = (int*)(ws + L.counters_lat);
-    la.n_rg = L.n_rg; la.n_kc = L.n_kc; la.ku_total = L.ku_total; la.ku_chunk = L.ku_chunk;
-    la.M = (int)M; la.m = (int)m;
-    int rc = check_hip(dispatch_latent(dtype, L.MT, la, L.MG, s), "latent launch");
-    if (rc) return rc;
-  }
-  if (phase == 1) return SSL_OK;
-  StreamArgs a{};
-  a.y = y; a.ldy = ldy; a.x = x; a.ldx = ldx; a.col = col; a.values = values; a.plan = plan;
-  a.A = A; a.lda = r_pad; a.t = ws + L.t_buf; a.ldt = r_pad; a.bias = bias;
-  a.counters = (int*)(ws + L.counters_main); a.partials = (float*)(ws + L.part_main);
-  a.n_slots = n_slots; a.NB = (int)NB; a.M = (int)M; a.m = (int)m;
-  return check_hip(dispatch_stream_dt<true>(dtype, block_p, L.MT, a, n_chunks, L.MG, s),
+  SlrArgs a{};
+  a.x = x; a.ldx = ldx; a.M = (int)M; a.m = (int)m;
+  a.y = y; a.ldy = ldy; a.col = col; a.values = values; a.plan = plan;
+  a.n_chunks = (int)n_chunks; a.NB = (int)NB;
+  a.A = A; a.lda = r_pad; a.bias = bias;
+  a.n_slots = n_slots; a.part_main = (float*)(ws + L.part_main); a.cnt_main = counters;
+  a.B = B; a.ldb = m_pad; a.t = ws + L.t_buf; a.ldt = r_pad;
+  a.n_rt = L.n_rt; a.n_kc = L.n_kc; a.ku_total = L.ku_total; a.ku_chunk = L.ku_chunk;
+  a.n_lat_wgs = (int)n_lat;
+  a.sync = (u64*)sync; a.lr_wgs = (int)lr_wgs; a.lat_weight = kLatentUnits / L.n_kc;
+  return check_hip(dispatch<MODE_FUSED>(dtype, block_p, L.MT, a, blocks, (hipStream_t)stream),
                    "slr launch");
-}
-
-int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A, const void* B,
-                    const void* bias, const int32_t* col, const void* values, const int32_t* plan,
-                    int64_t n_chunks, int64_t n_slots, int64_t M, int64_t m, int64_t m_pad,
-                    int64_t NB, int64_t r_pad, int32_t block_p, int32_t block_q, int32_t dtype,
-                    void* workspace, int64_t workspace_bytes, void* stream) {
-  return ssl_slr_forward_phase(y, ldy, x, ldx, A, B, bias, col, values, plan, n_chunks, n_slots, M,
-                               m, m_pad, NB, r_pad, block_p, block_q, dtype, workspace,
-                               workspace_bytes, 0, stream);
 }
 
 }  // extern "C"

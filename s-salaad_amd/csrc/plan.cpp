@@ -1,11 +1,19 @@
 // Host-side work planning and error reporting for the C ABI.
 //
-// A plan turns a BSR structure into workgroup chunks. Block-row `by` owns the
-// unit list [its nblk sparse blocks][lr_units low-rank units]; units cost q
-// (one q-wide block of p rows) or 32 (32 ranks of p rows of A). Rows costing
-// more than `target_cost` are split into k nearly equal consecutive chunks.
-// This is the load-balancing step for skewed block structures: a row with ten
-// times the mean block count gets ten times as many workgroups.
+// A plan turns a BSR structure into workgroup chunks. Block-row `by` owns
+// `nblk` sparse blocks (cost q each: one q-wide block of p rows) and `lr_units`
+// low-rank units (cost 32 each: 32 ranks of p rows of A). A row costing more
+// than `target_cost` is split into k chunks of nearly equal cost. This is the
+// load-balancing step for skewed block structures: a row with ten times the
+// mean block count gets ten times as many workgroups.
+//
+// Without low-rank units the k chunks take consecutive, equal shares of the
+// row's blocks and are combined by whichever finishes last. With low-rank units
+// the row's last chunk is its finaliser: it takes all the low-rank units (they
+// need the latent, which is ready only later in the launch) and a smaller
+// share of blocks, waits for the other chunks' partial sums and runs the
+// epilogue. Finaliser chunks are listed after every other chunk, so a chunk only
+// ever waits for chunks that precede it in the table (and in launch order).
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -40,7 +48,7 @@ using namespace ssl;
 
 extern "C" {
 
-int ssl_version(void) { return 1; }
+int ssl_version(void) { return 3; }
 
 const char* ssl_last_error(void) { return g_last_error.c_str(); }
 
@@ -54,57 +62,78 @@ int ssl_plan_build(const int32_t* crow_host, int64_t NB, const int32_t* rows_hos
   for (int64_t b = 0; b < NB; ++b)
     if (crow_host[b + 1] < crow_host[b]) return fail(SSL_ERR_INVALID, "crow must be non-decreasing");
   const int64_t nr = rows_host ? n_rows : NB;
-  int64_t chunks = 0, slots = 0;
   int64_t prev = -1;
   for (int64_t i = 0; i < nr; ++i) {
     const int64_t by = rows_host ? rows_host[i] : i;
     if (by < 0 || by >= NB) return fail(SSL_ERR_INVALID, "row %lld out of range", (long long)by);
     if (by <= prev) return fail(SSL_ERR_INVALID, "rows must be strictly ascending");
     prev = by;
-    const int64_t blk0 = crow_host[by];
-    const int64_t nblk = crow_host[by + 1] - blk0;
-    const int64_t units = nblk + lr_units;
-    if (units == 0) {
-      // A listed row without blocks: the in-place kernel would only rewrite the
-      // row with its own value, so it gets no chunk.
-      continue;
-    }
-    const int64_t cost = nblk * block_q + (int64_t)lr_units * 32;
-    int64_t k = 1;
-    if (target_cost > 0) k = (cost + target_cost - 1) / target_cost;
-    if (k < 1) k = 1;
-    if (k > units) k = units;
-    // Chunk boundaries at equal fractions of the row's cost; pc(u) is the cost
-    // of the row's first u units.
-    auto pc = [&](int64_t u) {
-      return u <= nblk ? u * block_q : nblk * block_q + (u - nblk) * 32;
-    };
-    int64_t ub = 0;
-    for (int64_t j = 0; j < k; ++j) {
-      int64_t ue;
-      if (j == k - 1) {
-        ue = units;
-      } else {
-        const int64_t goal = cost * (j + 1) / k;
-        ue = ub + 1;  // every chunk holds at least one unit
-        while (ue < units - (k - 1 - j) && pc(ue) < goal) ue++;
+  }
+  // Two passes: non-finaliser chunks first, then finalisers (pass 1 only when
+  // rows have low-rank units).
+  int64_t chunks = 0, slots = 0;
+  for (int pass = 0; pass < (lr_units > 0 ? 2 : 1); ++pass) {
+    int64_t row_slots = 0;
+    for (int64_t i = 0; i < nr; ++i) {
+      const int64_t by = rows_host ? rows_host[i] : i;
+      const int64_t blk0 = crow_host[by];
+      const int64_t nblk = crow_host[by + 1] - blk0;
+      if (nblk + lr_units == 0) {
+        // A listed row without blocks: the in-place kernel would only rewrite the
+        // row with its own value, so it gets no chunk.
+        continue;
       }
-      if (table_out) {
-        if (chunks >= table_capacity) return fail(SSL_ERR_CAPACITY, "plan table capacity exceeded");
-        int32_t* d = table_out + chunks * SSL_PLAN_STRIDE;
-        d[0] = (int32_t)by;
-        d[1] = (int32_t)ub;
-        d[2] = (int32_t)ue;
-        d[3] = (int32_t)j;
-        d[4] = (int32_t)k;
-        d[5] = (int32_t)(k > 1 ? slots : 0);
-        d[6] = (int32_t)nblk;
-        d[7] = (int32_t)blk0;
+      const int64_t cost = nblk * block_q + (int64_t)lr_units * 32;
+      int64_t k = 1;
+      if (target_cost > 0) k = (cost + target_cost - 1) / target_cost;
+      if (k < 1) k = 1;
+      // Block shares. With low-rank units the finaliser (chunk k-1) takes the
+      // low-rank cost first; the blocks are split so every chunk costs about
+      // cost/k.
+      int64_t nsplit = k;  // chunks that share the blocks
+      int64_t fin_blocks = 0;
+      if (lr_units > 0) {
+        const int64_t share = cost / k;  // cost per chunk
+        const int64_t lr_cost = (int64_t)lr_units * 32;
+        fin_blocks = share > lr_cost ? (share - lr_cost) / block_q : 0;
+        if (fin_blocks > nblk) fin_blocks = nblk;
+        nsplit = k - 1;
+        if (nsplit == 0) fin_blocks = nblk;
+      } else if (k > nblk) {
+        k = nsplit = nblk;
       }
-      ++chunks;
-      ub = ue;
+      const int64_t rest = nblk - fin_blocks;  // blocks for the non-finaliser chunks
+      if (lr_units > 0 && nsplit > rest) nsplit = rest;  // no empty non-finaliser chunk
+      const int64_t kept = nsplit + (lr_units > 0 ? 1 : 0);
+      for (int64_t j = 0; j < kept; ++j) {
+        const bool fin = lr_units > 0 && j == kept - 1;
+        if ((pass == 1) != fin && lr_units > 0) continue;
+        int64_t sb, se, lb = 0, le = 0;
+        if (fin) {
+          sb = blk0 + rest;
+          se = blk0 + nblk;
+          le = lr_units;
+        } else {
+          sb = blk0 + rest * j / nsplit;
+          se = blk0 + rest * (j + 1) / nsplit;
+        }
+        if (table_out) {
+          if (chunks >= table_capacity) return fail(SSL_ERR_CAPACITY, "plan table capacity exceeded");
+          int32_t* d = table_out + chunks * SSL_PLAN_STRIDE;
+          d[0] = (int32_t)by;
+          d[1] = (int32_t)sb;
+          d[2] = (int32_t)se;
+          d[3] = (int32_t)lb;
+          d[4] = (int32_t)le;
+          d[5] = (int32_t)j;
+          d[6] = (int32_t)kept;
+          d[7] = (int32_t)(kept > 1 ? row_slots : 0);
+        }
+        ++chunks;
+      }
+      if (kept > 1) row_slots += kept;
     }
-    if (k > 1) slots += k;
+    slots = row_slots;
   }
   *n_chunks = chunks;
   *n_slots = slots;

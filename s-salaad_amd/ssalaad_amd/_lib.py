@@ -40,24 +40,20 @@ _SIGNATURES = {
         [_c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_i64, _c_p, _c_i64, _c_p, _c_p],
     ),
     "ssl_bsr_addmm_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i32, _c_i64]),
-    "ssl_bsr_addmm_counter_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "ssl_bsr_addmm_counter_count": (_c_i64, [_c_i64, _c_i64]),
     "ssl_bsr_addmm_inplace": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
-         _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p],
+         _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_p],
     ),
     "ssl_slr_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32]),
-    "ssl_slr_counter_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "ssl_slr_counter_count": (_c_i64, [_c_i64, _c_i64]),
+    "ssl_slr_sync_count": (_c_i64, [_c_i64]),
     "ssl_slr_forward": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
-         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p],
-    ),
-    "ssl_slr_forward_phase": (
-        ctypes.c_int,
-        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
-         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i32,
-         _c_p],
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64,
+         _c_p, _c_i64, _c_p, _c_i64, _c_p],
     ),
     "ssl_bsr_encode_count": (
         ctypes.c_int,

@@ -2,38 +2,44 @@
 
 A work plan (built by the C ABI's ssl_plan_build) assigns the units of each
 block-row — its sparse blocks, then its low-rank slices — to workgroup chunks.
-Workspaces hold the kernels' completion counters, the low-rank latent and the
-partial tiles of split rows. Counters are zero at rest (the kernels return them
-to zero), so one zero-initialised workspace per (device, stream) is reused by
-every call on that stream and grown when a call needs more.
+Scratch comes in two pools per (device, stream), shared by every call ordered on
+that stream and grown when a call needs more:
+  * counters: int32, zero-initialised and used for nothing else; the kernels
+    return every counter they touch to zero, so the pool is zero at rest;
+  * workspace: bytes for the low-rank latent and the partial tiles of split
+    rows; no initialisation needed.
+A plan that feeds the fused kernel also owns its latent-handshake words (see
+DevicePlan.sync): those advance monotonically and are never shared.
 """
 
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import numpy as np
 import torch
 
 from . import _lib
 
-# Workgroups the decode plan aims for: two per compute unit of an MI355X.
-_TARGET_WORKGROUPS = 512
-# Smallest chunk worth a workgroup, in weight bytes.
-_MIN_CHUNK_BYTES = 16384
+# Weight bytes one workgroup streams before a row is split: a workgroup's 8
+# waves keep about 256 KiB in flight, so a chunk costs one or two memory round
+# trips. Rows of up to this size are never split and need no cross-workgroup
+# combine; longer rows (skewed structures) are.
+_CHUNK_BYTES = 512 * 1024
 
 
 def plan_target_cost(total_cost: int, block_p: int, elem_bytes: int, M: int) -> int:
     """Chunk cost target for a call with M token rows (0 = never split a row).
 
     Cost units are columns of a p-row block (q per sparse block, 32 per low-rank
-    unit). With one token tile (M ≤ 64) rows are split so the chip has ~512
-    workgroups; with several token tiles the tiles already provide parallelism.
+    unit), i.e. p·elem_bytes weight bytes each. With one token tile (M ≤ 64) a
+    row longer than _CHUNK_BYTES is split; several token tiles already provide
+    the parallelism, so rows stay whole.
     """
     if M > 64:
         return 0
-    min_cost = max(1, _MIN_CHUNK_BYTES // (block_p * elem_bytes))
-    return max(min_cost, -(-total_cost // _TARGET_WORKGROUPS))
+    return max(1, _CHUNK_BYTES // (block_p * elem_bytes))
 
 
 def build_plan(
@@ -69,33 +75,71 @@ def build_plan(
     return table[: n_chunks.value], int(n_chunks.value), int(n_slots.value)
 
 
+_PLANS: "weakref.WeakSet[DevicePlan]" = weakref.WeakSet()
+
+
 class DevicePlan:
     """A plan uploaded to one device."""
 
-    __slots__ = ("table", "n_chunks", "n_slots")
+    __slots__ = ("table", "n_chunks", "n_slots", "lr_wgs", "_sync", "__weakref__")
 
     def __init__(self, table: np.ndarray, n_chunks: int, n_slots: int, device: torch.device):
         t = torch.from_numpy(table if n_chunks else np.zeros((1, _lib.PLAN_STRIDE), np.int32))
         self.table = t.to(device)
         self.n_chunks = n_chunks
         self.n_slots = n_slots
+        # workgroups that read the latent: the chunks with low-rank units
+        lr = (table[:n_chunks, 4] - table[:n_chunks, 3]) if n_chunks else np.zeros(0)
+        self.lr_wgs = int((lr > 0).sum())
+        self._sync: torch.Tensor | None = None
+        _PLANS.add(self)
+
+    def sync(self, count: int) -> torch.Tensor:
+        """The plan's own latent-handshake words (uint64 as int64), at least `count`.
+
+        The kernels advance them monotonically and never reset them, so they
+        belong to this plan alone; calls with one plan are ordered on one
+        stream. Growing replaces them with zeros, which is a consistent state
+        for the next call on that stream.
+        """
+        if self._sync is None or self._sync.numel() < count:
+            self._sync = torch.zeros(max(int(count), 8), dtype=torch.int64,
+                                     device=self.table.device)
+        return self._sync
+
+    def wait_status(self) -> int:
+        """1 if a workgroup of a call with this plan gave up waiting, else 0.
+
+        Synchronises the device.
+        """
+        return 0 if self._sync is None else int(self._sync[0].item())
 
 
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+_COUNTERS: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _key(device: torch.device) -> tuple[int, int]:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return (idx, torch.cuda.current_stream(device).cuda_stream)
+
+
+def _grown(pool, key, n, dtype, device, minimum):
+    buf = pool.get(key)
+    if buf is None or buf.numel() < n:
+        size = max(int(n), minimum)
+        if buf is not None:
+            size = max(size, 2 * buf.numel())
+        buf = torch.zeros(size, dtype=dtype, device=device)
+        pool[key] = buf
+    return buf
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-initialised uint8 workspace of at least `nbytes` for the current stream.
+    """uint8 workspace of at least `nbytes` for the current stream."""
+    return _grown(_WORKSPACES, _key(device), nbytes, torch.uint8, device, 1 << 20)
 
-    Calls ordered on one stream share it; the kernels leave its counters at zero.
-    """
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (idx, torch.cuda.current_stream(device).cuda_stream)
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        size = max(int(nbytes), 1 << 20)
-        if ws is not None:
-            size = max(size, 2 * ws.numel())
-        ws = torch.zeros(size, dtype=torch.uint8, device=device)
-        _WORKSPACES[key] = ws
-    return ws
+
+def counters(device: torch.device, count: int) -> torch.Tensor:
+    """int32 counters (zero at rest) of at least `count` for the current stream."""
+    return _grown(_COUNTERS, _key(device), count, torch.int32, device, 1 << 14)

@@ -162,14 +162,15 @@ def bsr_addmm_inplace_(
         target = out_inplace.contiguous().clone()
     lib = _lib.load()
     dt = _lib.dtype_code(out_inplace.dtype)
-    need = lib.ssl_bsr_addmm_workspace_size(M, NB, block_p, plan.n_slots)
-    ws = _runtime.workspace(out_inplace.device, need)
-    with torch.cuda.device(out_inplace.device):
+    dev = out_inplace.device
+    with torch.cuda.device(dev):
+        ws = _runtime.workspace(dev, lib.ssl_bsr_addmm_workspace_size(M, NB, block_p, plan.n_slots))
+        cnt = _runtime.counters(dev, lib.ssl_bsr_addmm_counter_count(M, NB))
         rc = lib.ssl_bsr_addmm_inplace(
             target.data_ptr(), target.stride(0), x.data_ptr(), x.stride(0), col.data_ptr(),
             vals.data_ptr(), plan.table.data_ptr(), plan.n_chunks, plan.n_slots, M, N, K, NB,
-            block_p, block_q, dt, ws.data_ptr(), ws.numel(),
-            _lib.stream_ptr(out_inplace.device),
+            block_p, block_q, dt, cnt.data_ptr(), cnt.numel(), ws.data_ptr(), ws.numel(),
+            _lib.stream_ptr(dev),
         )
     _lib.check(rc, "ssl_bsr_addmm_inplace")
     if target is not out_inplace:

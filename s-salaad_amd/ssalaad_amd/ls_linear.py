@@ -8,8 +8,8 @@ block_p, block_q, S_nnz, kind) and buffers (A, B, bias, S_crow, S_col, S_values
 
     y = x · Bᵀ · Aᵀ + x · Sᵀ + b
 
-is one call of `ssl_slr_forward` (two kernels: the latent t = x·Bᵀ, then a
-streaming kernel that adds t·Aᵀ, the sparse term and the bias in one epilogue)
+is one call of `ssl_slr_forward` — one kernel launch that computes the latent
+t = x·Bᵀ and streams t·Aᵀ, the sparse term and the bias into one epilogue —
 instead of the reference's F.linear ×2 + BSR op + bias add (:124-137).
 
 Differences from the reference, all extensions:
@@ -100,9 +100,8 @@ class _KernelState:
             self._plans[key] = pl
         return pl
 
-    def forward(self, x: torch.Tensor, out_features: int, phase: int = 0) -> torch.Tensor:
-        """y = x·Bᵀ·Aᵀ + x·Sᵀ + b. `phase` selects the kernels (0 both, 1 latent
-        only, 2 streaming kernel only) for per-kernel timing; callers use 0."""
+    def forward(self, x: torch.Tensor, out_features: int) -> torch.Tensor:
+        """y = x·Bᵀ·Aᵀ + x·Sᵀ + b in one fused launch."""
         m = self.m
         orig = x.shape
         x2 = x.reshape(-1, orig[-1])
@@ -121,17 +120,30 @@ class _KernelState:
                 M, self.NB, self.p, self.r_pad, self.m_pad, pl.n_slots, self.dtype_code
             )
             ws = _runtime.workspace(x.device, need)
-            rc = lib.ssl_slr_forward_phase(
+            cnt = _runtime.counters(x.device, lib.ssl_slr_counter_count(M, self.NB))
+            sync = pl.sync(lib.ssl_slr_sync_count(M))
+            rc = lib.ssl_slr_forward(
                 y.data_ptr(), y.stride(0), x2.data_ptr(), x2.stride(0), self.A.data_ptr(),
                 self.B.data_ptr(), _lib.ptr(self.bias), self.col.data_ptr(),
-                self.values.data_ptr(), pl.table.data_ptr(), pl.n_chunks, pl.n_slots, M, m,
-                self.m_pad, self.NB, self.r_pad, self.p, self.p, self.dtype_code,
-                ws.data_ptr(), ws.numel(), phase, _lib.stream_ptr(x.device),
+                self.values.data_ptr(), pl.table.data_ptr(), pl.n_chunks, pl.n_slots,
+                pl.lr_wgs, M, m, self.m_pad, self.NB, self.r_pad, self.p, self.p,
+                self.dtype_code, cnt.data_ptr(), cnt.numel(), sync.data_ptr(), sync.numel(),
+                ws.data_ptr(), ws.numel(),
+                _lib.stream_ptr(x.device),
             )
             _lib.check(rc, "ssl_slr_forward")
         if self.n_pad != out_features:
             y = y[:, :out_features]
         return y.reshape(*orig[:-1], out_features)
+
+
+def latent_wait_status(device: torch.device) -> int:
+    """1 if a fused call of any live plan on `device` had a workgroup give up
+    waiting (its output tile is then unreliable), else 0. Synchronises.
+    """
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return max([pl.wait_status() for pl in list(_runtime._PLANS)
+                if pl.table.device.index == idx] + [0])
 
 
 class _LRSLinearBase(nn.Module):

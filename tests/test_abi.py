@@ -46,7 +46,7 @@ def test_single_hip_runtime_in_process():
 
 
 def test_version():
-    assert _lib.load().ssl_version() == 1
+    assert _lib.load().ssl_version() == 3
 
 
 # ------------------------------------------------------------------ plans --
@@ -59,46 +59,73 @@ def _plan(crow, rows=None, q=64, lr=0, target=0):
     return table, n, s
 
 
+def _check_plan(crow, lr, table, n, slots):
+    """Every block and low-rank unit of every row is covered exactly once, chunks
+    of a row share one slot base, and finalisers (chunks with low-rank units)
+    come after every other chunk."""
+    rows = {}
+    for idx, (row, bb, be, lb, le, seq, nseq, slot) in enumerate(table):
+        assert crow[row] <= bb <= be <= crow[row + 1]
+        assert 0 <= lb <= le <= lr
+        rows.setdefault(int(row), []).append((seq, nseq, bb, be, lb, le, slot, idx))
+    used = set()
+    last_plain = max([i for *_, lb, le, _s, i in
+                      ((p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]) for v in rows.values() for p in v)
+                      if le == lb] + [-1])
+    for row, parts in rows.items():
+        parts.sort()
+        k = parts[0][1]
+        assert [p[0] for p in parts] == list(range(k)) and all(p[1] == k for p in parts)
+        assert parts[0][2] == crow[row] and parts[-1][3] == crow[row + 1]
+        for a, b in zip(parts, parts[1:]):
+            assert a[3] == b[2]
+        if lr:
+            fin = parts[-1]
+            assert (fin[4], fin[5]) == (0, lr)                 # finaliser holds every unit
+            assert all(p[4] == p[5] for p in parts[:-1])        # others hold none
+            assert fin[7] > last_plain                          # listed after all others
+        if k > 1:
+            base = parts[0][6]
+            assert all(p[6] == base for p in parts)
+            for j in range(k):
+                assert base + j not in used
+                used.add(base + j)
+    assert len(used) == slots
+    return rows
+
+
 def test_plan_covers_every_unit_once():
     rng = np.random.default_rng(0)
     counts = rng.integers(0, 40, 50)
     crow = np.concatenate([[0], np.cumsum(counts)])
-    lr = 8
-    for target in (0, 64, 200, 1000):
-        table, n, slots = _plan(crow, q=64, lr=lr, target=target)
-        seen = {}
-        for row, ub, ue, seq, nseq, slot, nblk, blk0 in table:
-            assert nblk == counts[row] and blk0 == crow[row]
-            assert 0 <= ub < ue <= nblk + lr
-            seen.setdefault(row, []).append((seq, nseq, ub, ue, slot))
-        assert sorted(seen) == list(range(50))  # every row has units (lr > 0)
-        used_slots = set()
-        for row, parts in seen.items():
-            parts.sort()
-            k = parts[0][1]
-            assert [p[0] for p in parts] == list(range(k))
-            assert parts[0][2] == 0 and parts[-1][3] == counts[row] + lr
-            for a, b in zip(parts, parts[1:]):
-                assert a[3] == b[2]  # consecutive, no gap or overlap
-            if k > 1:
-                base = parts[0][4]
-                assert all(p[4] == base for p in parts)
-                for j in range(k):
-                    assert base + j not in used_slots
-                    used_slots.add(base + j)
-        assert len(used_slots) == slots
+    for lr in (0, 8):
+        for target in (0, 64, 200, 1000):
+            table, n, slots = _plan(crow, q=64, lr=lr, target=target)
+            rows = _check_plan(crow, lr, table, n, slots)
+            expect = set(range(50)) if lr else {i for i in range(50) if counts[i]}
+            assert set(rows) == expect
 
 
 def test_plan_splits_long_rows_evenly():
     crow = [0, 4, 4 + 400, 404 + 10]
     table, n, slots = _plan(crow, q=64, lr=0, target=64 * 8)
     per_row = {}
-    for row, ub, ue, *_ in table:
-        per_row.setdefault(row, []).append(ue - ub)
-    assert len(per_row[0]) == 1
+    for row, bb, be, *_ in table:
+        per_row.setdefault(int(row), []).append(int(be - bb))
+    assert per_row[0] == [4]
     assert len(per_row[1]) == 50 and set(per_row[1]) == {8}
-    assert len(per_row[2]) == 2
-    assert 1 not in per_row or True
+    assert per_row[2] == [5, 5]
+    assert slots == 52
+
+
+def test_plan_finaliser_takes_the_low_rank_units():
+    crow = np.array([0, 30, 30, 100], np.int32)
+    table, n, slots = _plan(crow, q=32, lr=8, target=300)
+    rows = _check_plan(crow, 8, table, n, slots)
+    # a row without blocks is a lone finaliser; a single-chunk row is its own finaliser
+    assert [(p[2], p[3], p[4], p[5]) for p in rows[1]] == [(30, 30, 0, 8)]
+    table1, n1, s1 = _plan(crow, q=32, lr=8, target=0)
+    assert n1 == 3 and s1 == 0 and all(int(r[6]) == 1 for r in table1)
 
 
 def test_plan_with_row_list_skips_unlisted_and_empty_rows():
@@ -120,10 +147,9 @@ def test_plan_rejects_bad_structures():
 
 def test_plan_target_cost_policy():
     assert _runtime.plan_target_cost(10**6, 64, 2, M=65) == 0  # several token tiles: no split
-    small = _runtime.plan_target_cost(100, 64, 2, M=1)
-    assert small == 16384 // 128
-    big = _runtime.plan_target_cost(5504 * 64 + 172 * 8 * 32, 64, 2, M=16)
-    assert big == -(-(5504 * 64 + 172 * 8 * 32) // 512)
+    # rows are split beyond 512 KiB of weights: 4096 cost units of a 64-row bf16 block
+    assert _runtime.plan_target_cost(100, 64, 2, M=1) == 4096
+    assert _runtime.plan_target_cost(10**7, 16, 4, M=16) == 512 * 1024 // 64
 
 
 # ---------------------------------------------------- workspace / checks --
@@ -135,33 +161,58 @@ def test_workspace_sizes_are_aligned_and_monotone():
     b = lib.ssl_slr_workspace_size(16, 172, 64, 256, 4096, 100, _lib.SSL_BF16)
     c = lib.ssl_slr_workspace_size(2048, 172, 64, 256, 4096, 0, _lib.SSL_BF16)
     assert a % 256 == 0 and b > a and c > a
-    assert lib.ssl_slr_counter_bytes(16, 172, 256, 4096) <= a
-    assert lib.ssl_bsr_addmm_counter_bytes(16, 172) % 256 == 0
-    assert lib.ssl_bsr_addmm_workspace_size(16, 172, 64, 10) > lib.ssl_bsr_addmm_counter_bytes(16, 172)
+    # counters: one per (token tile, block-row); sync words: the status word,
+    # then latent-done and consumer-ticket counters per token tile
+    assert lib.ssl_slr_counter_count(16, 172) == 172
+    assert lib.ssl_slr_counter_count(2048, 172) == 32 * 172
+    assert lib.ssl_slr_sync_count(16) == 3
+    assert lib.ssl_slr_sync_count(2048) == 1 + 2 * 32
+    assert lib.ssl_bsr_addmm_counter_count(16, 172) == 172
+    assert lib.ssl_bsr_addmm_counter_count(65, 172) == 2 * 172
+    assert lib.ssl_bsr_addmm_workspace_size(16, 172, 64, 0) == 0
+    assert lib.ssl_bsr_addmm_workspace_size(16, 172, 64, 10) == 10 * 16 * 64 * 4
 
 
 def test_entry_points_reject_bad_arguments_before_any_launch():
     lib = _lib.load()
     # unsupported block shape
     rc = lib.ssl_bsr_addmm_inplace(1, 64, 1, 64, 1, 1, 1, 1, 0, 1, 64, 64, 1, 8, 8,
-                                   _lib.SSL_BF16, None, 0, None)
+                                   _lib.SSL_BF16, None, 0, None, 0, None)
     assert rc == _lib.SSL_ERR_UNSUPPORTED and b"square" in lib.ssl_last_error()
     # N inconsistent with NB·p
     rc = lib.ssl_bsr_addmm_inplace(1, 64, 1, 64, 1, 1, 1, 1, 0, 1, 60, 64, 1, 64, 64,
-                                   _lib.SSL_BF16, None, 0, None)
+                                   _lib.SSL_BF16, None, 0, None, 0, None)
     assert rc == _lib.SSL_ERR_INVALID
-    # bad dtype
-    rc = lib.ssl_slr_forward(1, 64, 1, 64, 1, 1, None, 1, 1, 1, 1, 0, 1, 64, 64, 1, 64, 64, 64,
-                             7, None, 0, None)
-    assert rc == _lib.SSL_ERR_UNSUPPORTED
-    # r_pad not a multiple of 64
-    rc = lib.ssl_slr_forward(1, 64, 1, 64, 1, 1, None, 1, 1, 1, 1, 0, 1, 64, 64, 1, 48, 64, 64,
-                             _lib.SSL_BF16, None, 0, None)
-    assert rc == _lib.SSL_ERR_INVALID
-    # missing workspace
-    rc = lib.ssl_slr_forward(16, 64, 16, 64, 16, 16, None, 16, 16, 16, 1, 0, 1, 64, 64, 1, 64, 64,
-                             64, _lib.SSL_BF16, None, 0, None)
+    # missing counters
+    rc = lib.ssl_bsr_addmm_inplace(16, 64, 16, 64, 16, 16, 16, 1, 0, 1, 64, 64, 1, 64, 64,
+                                   _lib.SSL_BF16, None, 0, None, 0, None)
     assert rc == _lib.SSL_ERR_WORKSPACE
+    # bad dtype
+    rc = lib.ssl_slr_forward(1, 64, 1, 64, 1, 1, None, 1, 1, 1, 1, 0, 1, 1, 64, 64, 1, 64, 64,
+                             64, 7, None, 0, None, 0, None, 0, None)
+    assert rc == _lib.SSL_ERR_UNSUPPORTED
+    # lr_wgs inconsistent with r_pad
+    rc = lib.ssl_slr_forward(1, 64, 1, 64, 1, 1, None, 1, 1, 1, 1, 0, 0, 1, 64, 64, 1, 64, 64,
+                             64, _lib.SSL_BF16, None, 0, None, 0, None, 0, None)
+    assert rc == _lib.SSL_ERR_INVALID and b"lr_wgs" in lib.ssl_last_error()
+    # more consuming workgroups than chunks
+    rc = lib.ssl_slr_forward(1, 64, 1, 64, 1, 1, None, 1, 1, 1, 1, 0, 2, 1, 64, 64, 1, 64, 64,
+                             64, _lib.SSL_BF16, None, 0, None, 0, None, 0, None)
+    assert rc == _lib.SSL_ERR_INVALID and b"lr_wgs" in lib.ssl_last_error()
+    # r_pad not a multiple of 64
+    rc = lib.ssl_slr_forward(1, 64, 1, 64, 1, 1, None, 1, 1, 1, 1, 0, 1, 1, 64, 64, 1, 48, 64,
+                             64, _lib.SSL_BF16, None, 0, None, 0, None, 0, None)
+    assert rc == _lib.SSL_ERR_INVALID
+    # missing workspace / counters / sync words
+    rc = lib.ssl_slr_forward(16, 64, 16, 64, 16, 16, None, 16, 16, 16, 1, 0, 1, 1, 64, 64, 1, 64,
+                             64, 64, _lib.SSL_BF16, None, 0, None, 0, None, 0, None)
+    assert rc == _lib.SSL_ERR_WORKSPACE
+    rc = lib.ssl_slr_forward(16, 64, 16, 64, 16, 16, None, 16, 16, 16, 1, 0, 1, 1, 64, 64, 1, 64,
+                             64, 64, _lib.SSL_BF16, None, 0, None, 0, 256, 1 << 20, None)
+    assert rc == _lib.SSL_ERR_WORKSPACE and b"counters" in lib.ssl_last_error()
+    rc = lib.ssl_slr_forward(16, 64, 16, 64, 16, 16, None, 16, 16, 16, 1, 0, 1, 1, 64, 64, 1, 64,
+                             64, 64, _lib.SSL_BF16, 256, 1, None, 0, 256, 1 << 20, None)
+    assert rc == _lib.SSL_ERR_WORKSPACE and b"sync" in lib.ssl_last_error()
     with pytest.raises(ValueError):
         _lib.check(_lib.SSL_ERR_INVALID, "x")
     with pytest.raises(TypeError):

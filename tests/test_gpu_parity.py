@@ -22,6 +22,7 @@ from slr_cases import TOL, err, make_problem, make_x, oracle_y, sparse_bsr_tenso
 
 import ssalaad_amd  # noqa: E402
 from ssalaad_amd import LRSLinear, _runtime  # noqa: E402
+from ssalaad_amd.ls_linear import latent_wait_status  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -100,8 +101,7 @@ def test_op_skewed_rows_and_untouched_rows(dtype, p, M, gpu_device):
 def test_op_with_every_block_its_own_chunk(dtype, gpu_device, monkeypatch):
     """Maximal row splitting: every block is a chunk, every row goes through the
     partial/counter combine. Two calls: the counters must be back at zero."""
-    monkeypatch.setattr(_runtime, "_MIN_CHUNK_BYTES", 1)
-    monkeypatch.setattr(_runtime, "_TARGET_WORKGROUPS", 10**7)
+    monkeypatch.setattr(_runtime, "_CHUNK_BYTES", 1)
     p, M = 32, 16
     prob = make_problem(6 * p, 20 * p, 4, p, 0.6, dtype, seed=99, skew=True)
     crow32, col32, vt, act = orc.module_buffers(prob["crow"], prob["col"], prob["vals"])
@@ -121,6 +121,23 @@ def test_op_with_every_block_its_own_chunk(dtype, gpu_device, monkeypatch):
 
 
 # ------------------------------------------------------- fused module --
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("M", [1, 16, 40])
+def test_module_with_every_unit_its_own_chunk(dtype, M, gpu_device, monkeypatch):
+    """Maximal splitting of the fused linear: every block and every low-rank unit
+    is its own chunk, so each row is combined from many partials and every
+    low-rank chunk waits for the latent."""
+    monkeypatch.setattr(_runtime, "_CHUNK_BYTES", 1)
+    prob = make_problem(256, 2048, 96, 32, 0.3, dtype, seed=M, skew=True)
+    mod = _module(prob, gpu_device)
+    x = make_x(prob, M)
+    ys = [mod(to_dev(x, dtype, gpu_device)) for _ in range(2)]
+    torch.cuda.synchronize()
+    assert err(ys[0], oracle_y(prob, x)) <= TOL[dtype]
+    assert torch.equal(ys[0], ys[1])
+    assert latent_wait_status(gpu_device) == 0
 
 
 def _module(prob, dev, bias=True):
@@ -294,3 +311,13 @@ def test_encoder_feeds_the_module(gpu_device):
     y = mod(to_dev(x, torch.bfloat16, dev))
     torch.cuda.synchronize()
     assert err(y, oracle_y(prob, x)) <= 1e-2
+
+
+def test_no_workgroup_gave_up_waiting_for_the_latent(gpu_device):
+    """Runs after the module tests: every fused call found its latent ready."""
+    prob = make_problem(4096, 1024, 256, 64, 0.5, torch.bfloat16, seed=6)
+    mod = _module(prob, gpu_device)
+    for M in (1, 16, 64, 200):
+        mod(to_dev(make_x(prob, M), torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    assert latent_wait_status(gpu_device) == 0
