@@ -124,7 +124,7 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx,
 int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r_pad,
                                int64_t m_pad, int64_t n_slots, int32_t dtype);
 int64_t ssl_slr_counter_count(int64_t M, int64_t NB);
-int64_t ssl_slr_sync_count(int64_t M);
+int64_t ssl_slr_sync_count(int64_t M, int64_t r_pad);
 int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A,
                     const void* B, const void* bias, const int32_t* col,
                     const void* values, const int32_t* plan, int64_t n_chunks,

@@ -79,6 +79,47 @@ __device__ __forceinline__ int ld_int(const int* p) {
 __device__ __forceinline__ void st_int(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Vector forms of the same device-coherent accesses: buffer loads/stores with
+// the sc1 cache policy (what the relaxed agent-scope atomics above compile to),
+// N = 1, 2 or 4 floats at a wave-uniform base plus a per-lane byte offset below
+// 2 GiB (the host checks the workspace size).
+constexpr int kSc1 = 16;  // cache-policy bit: sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                           0x00020000);
+}
+template <int N>
+__device__ __forceinline__ void ld_dev_vec(__amdgpu_buffer_rsrc_t r, int byte_off, float* v) {
+  if constexpr (N == 4) {
+    const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kSc1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(u[i]);
+  } else if constexpr (N == 2) {
+    const auto u = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, kSc1);
+    v[0] = __uint_as_float(u[0]);
+    v[1] = __uint_as_float(u[1]);
+  } else {
+    static_assert(N == 1, "1, 2 or 4 floats");
+    v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, kSc1));
+  }
+}
+template <int N>
+__device__ __forceinline__ void st_dev_vec(__amdgpu_buffer_rsrc_t r, int byte_off, const float* v) {
+  if constexpr (N == 4) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 u = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                     __float_as_uint(v[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(u, r, byte_off, 0, kSc1);
+  } else if constexpr (N == 2) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 u = {__float_as_uint(v[0]), __float_as_uint(v[1])};
+    __builtin_amdgcn_raw_buffer_store_b64(u, r, byte_off, 0, kSc1);
+  } else {
+    static_assert(N == 1, "1, 2 or 4 floats");
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, byte_off, 0, kSc1);
+  }
+}
+
 // All of this thread's earlier memory operations have completed (stores are
 // acknowledged by the device-coherent level).
 __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
@@ -109,28 +150,15 @@ __device__ __forceinline__ void wait_at_least(const T* flag, T target, u64* stat
   }
 }
 
-// A KE-element fragment of the latent t: the sum, in chunk order, of the n_kc
-// fp32 partials written by the latent workgroups of this launch (read with
-// device-coherent loads), rounded once to the activation dtype.
+// One KE-element fragment (16 bytes) of the final latent, read device-coherently.
 template <int DT, int KE>
-__device__ __forceinline__ typename Mma<DT, KE>::Frag load_latent(const float* base, int64_t off,
-                                                                  int n_kc, int64_t kstride) {
-  float v[KE];
-#pragma unroll
-  for (int e = 0; e < KE; ++e) v[e] = ld_dev(base + off + e);
-  for (int k = 1; k < n_kc; ++k) {
-    const float* p = base + k * kstride + off;
-#pragma unroll
-    for (int e = 0; e < KE; ++e) v[e] += ld_dev(p + e);
-  }
+__device__ __forceinline__ typename Mma<DT, KE>::Frag ld_dev_frag(__amdgpu_buffer_rsrc_t r,
+                                                                  int byte_off) {
+  static_assert(KE * Elem<DT>::bytes == 16, "16-byte fragments");
+  const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kSc1);
   typename Mma<DT, KE>::Frag f;
-  if constexpr (DT == DT_F32) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) f.f[e] = v[e];
-  } else {
-#pragma unroll
-    for (int d = 0; d < KE / 2; ++d) f.d[d] = to_bits<DT>(v[2 * d]) | (to_bits<DT>(v[2 * d + 1]) << 16);
-  }
+  static_assert(sizeof(f) == 16, "fragment image");
+  __builtin_memcpy(&f, &u, 16);
   return f;
 }
 
@@ -216,14 +244,17 @@ __device__ __forceinline__ void store_partial(const f32x4 (&acc)[MT][W], float* 
                                               int lane) {
   constexpr int TP = 16 * W;
   const int c = lane & 15, g = lane >> 4;
+  const auto r = dev_rsrc(part);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int rr = mt * 16 + 4 * g + e;
       if (rr < Mrem) {
+        float v[W];
 #pragma unroll
-        for (int s = 0; s < W; ++s) st_dev(part + rr * TP + W * c + s, acc[mt][s][e]);
+        for (int s = 0; s < W; ++s) v[s] = acc[mt][s][e];
+        st_dev_vec<W>(r, (rr * TP + W * c) * 4, v);
       }
     }
 }
@@ -232,14 +263,17 @@ __device__ __forceinline__ void add_partial(f32x4 (&tot)[MT][W], const float* pa
                                             int lane) {
   constexpr int TP = 16 * W;
   const int c = lane & 15, g = lane >> 4;
+  const auto r = dev_rsrc(part);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int rr = mt * 16 + 4 * g + e;
       if (rr < Mrem) {
+        float v[W];
+        ld_dev_vec<W>(r, (rr * TP + W * c) * 4, v);
 #pragma unroll
-        for (int s = 0; s < W; ++s) tot[mt][s][e] += ld_dev(part + rr * TP + W * c + s);
+        for (int s = 0; s < W; ++s) tot[mt][s][e] += v[s];
       }
     }
 }
@@ -269,22 +303,29 @@ struct SlrArgs {
   // latent
   const void* B;
   int64_t ldb;
-  void* t;
+  void* t;          // final latent [MG·16·MT][ldt], activation dtype
   int64_t ldt;
-  int n_rt;       // 16-rank tiles
-  int n_kc;       // in_features chunks of the latent (fp32 partials summed by the consumers)
-  int ku_total;   // in_features in KM-column units
-  int ku_chunk;   // KM-column units per latent chunk
-  int n_lat_wgs;  // latent workgroups at the start of the grid (n_rt·n_kc·MG)
-  // latent handshake: sync[0] status (1 = a wait gave up), then per token tile
-  // mg two monotonic counters: sync[1 + 2·mg] latent workgroups done,
-  // sync[2 + 2·mg] consumer tickets
-  // Each latent workgroup adds kLatentUnits / n_kc, so one launch adds
-  // n_rt·kLatentUnits per token tile whatever its K split (n_kc ≤ 8 divides 840).
+  float* t_part;    // fp32 partials [n_kc][MG][n_rt][MT·256] (lane-native tiles)
+  int MG;           // token tiles
+  int n_rt;         // 16-rank tiles
+  int n_kc;         // in_features chunks of the latent
+  int ku_total;     // in_features in KM-column units
+  int ku_chunk;     // KM-column units per latent chunk
+  int n_lat_wgs;    // latent workgroups at the start of the grid (n_rt·n_kc·MG)
+  // Handshake words, all monotonic (never reset): sync[0] is the status (1 =
+  // a wait gave up); token tile mg owns sync[1 + mg·(2 + n_rt) ...]:
+  //   [0] final latent tiles written (+1 per rank tile and launch)
+  //   [1] consumer tickets (+1 per consuming workgroup and launch)
+  //   [2 + rt] arrivals of rank tile rt's K chunks (+kLatentUnits/n_kc each,
+  //       so every launch adds exactly kLatentUnits whatever its split)
   u64* sync;
-  int lr_wgs;     // workgroups that consume the latent (per token tile)
-  int lat_weight; // kLatentUnits / n_kc
+  int lr_wgs;       // workgroups that consume the latent (per token tile)
+  int lat_weight;   // kLatentUnits / n_kc
 };
+
+__device__ __forceinline__ u64* tile_sync(const SlrArgs& a, int mg) {
+  return a.sync + 1 + (int64_t)mg * (2 + a.n_rt);
+}
 
 // ---------------------------------------------------------------------------
 // Latent workgroup: t[token tile, 16-rank tile rt] over all of in_features.
@@ -341,18 +382,63 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
 
   tree_reduce<MT, 1>(acc, red, wid, lane);
   if (wid != 0) return;
-  // wave 0: lane (c, g) holds rows 16·mt + 4g + e of rank rt·16 + c; store the
-  // fp32 partial of chunk kc: t[kc][token row][rank]
-  float* tp = (float*)a.t + (int64_t)kc * a.M * a.ldt;
+  // wave 0: lane (c, g) holds rows 16·mt + 4g + e of rank rt·16 + c.
+  u64* sy = tile_sync(a, mg);
+  if (a.n_kc > 1) {
+    // Publish this K chunk's fp32 partial; the last chunk of the rank tile to
+    // arrive sums all of them in chunk order (deterministic) and goes on.
+    const auto pr = dev_rsrc(a.t_part);
+    const int64_t slab = (int64_t)a.MG * a.n_rt * (MT * 256);  // floats per K chunk
+    const int64_t tile = ((int64_t)mg * a.n_rt + rt) * (MT * 256);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float v[4] = {acc[mt][0][0], acc[mt][0][1], acc[mt][0][2], acc[mt][0][3]};
+      st_dev_vec<4>(pr, (int)((kc * slab + tile + (mt * 64 + lane) * 4) * 4), v);
+    }
+    wait_mem();
+    int last = 0;
+    if (lane == 0) {
+      const u64 old = rmw_add64(sy + 2 + rt, (u64)a.lat_weight);
+      last = (old + (u64)a.lat_weight) % kLatentUnits == 0;
+    }
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
+    f32x4 tot[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) tot[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < a.n_kc; ++k) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (k == kc) {
+          tot[mt] += acc[mt][0];
+        } else {
+          float v[4];
+          ld_dev_vec<4>(pr, (int)((k * slab + tile + (mt * 64 + lane) * 4) * 4), v);
+          tot[mt] += f32x4{v[0], v[1], v[2], v[3]};
+        }
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt][0] = tot[mt];
+  }
+  // Final latent tile, rounded once to the activation dtype as F.linear's
+  // output is. Rows past M hold zeros (their x rows were read as zero).
+  const auto tr = dev_rsrc(a.t);
+  constexpr int EB = Elem<DT>::bytes;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int rr = mt * 16 + 4 * g + e;
-      if (rr < Mrem) st_dev(tp + (int64_t)(m0 + rr) * a.ldt + rt * 16 + c, acc[mt][0][e]);
+      const int off = (int)(((int64_t)(m0 + mt * 16 + 4 * g + e) * a.ldt + rt * 16 + c) * EB);
+      if constexpr (DT == DT_F32) {
+        float v = acc[mt][0][e];
+        st_dev_vec<1>(tr, off, &v);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)to_bits<DT>(acc[mt][0][e]), tr, off,
+                                              0, kSc1);
+      }
     }
   wait_mem();
-  if (lane == 0) rmw_add64(a.sync + 1 + 2 * mg, (u64)a.lat_weight);
+  if (lane == 0) rmw_add64(sy, 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -395,7 +481,22 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   // the row's loads). Launch k's consumers hold tickets k·lr_wgs ... and wait
   // for (k + 1)·(latent workgroups) completions, so no counter is ever reset.
   u64 ticket = 0;
-  if (used_t && threadIdx.x == 0) ticket = rmw_add64(a.sync + 2 + 2 * mg, 1);
+  if (used_t && threadIdx.x == 0) ticket = rmw_add64(tile_sync(a, mg) + 1, 1);
+
+  // The wave's first low-rank unit of A does not depend on the latent: its
+  // loads go out ahead of the sparse blocks.
+  FragL af0[NLS][W];
+  if constexpr (MODE == MODE_FUSED) {
+    if (used_t && lb + wid < le) {
+#pragma unroll
+      for (int ls = 0; ls < NLS; ++ls)
+#pragma unroll
+        for (int s = 0; s < W; ++s)
+          af0[ls][s] = load_kfrag<DT, KEL>(
+              a.A, (int64_t)(row * P + W * c + s) * a.lda + (lb + wid) * 32 + ls * ML::KM + KEL * g,
+              KEL);
+    }
+  }
 
   // ---- sparse blocks: a batch issues all its loads (x, then the block) unit by
   // unit before the first MFMA, so each unit waits only for its own data.
@@ -438,60 +539,40 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
     }
   }
 
-  // ---- low-rank units: 32 ranks of A per unit, t·Aᵀ. A does not depend on the
-  // latent, so every wave issues its first A fragments before one thread of
-  // the workgroup waits for the latent.
+  // ---- low-rank units: 32 ranks of A per unit, t·Aᵀ. One thread of the
+  // workgroup waits for this launch's final latent; the barrier releases the
+  // other waves, which then read it device-coherently.
   if constexpr (MODE == MODE_FUSED) {
     if (used_t) {
-      constexpr int ULR = 2;
-      FragL af[ULR][NLS][W];
-      auto load_a = [&](int base) {
-#pragma unroll
-        for (int k = 0; k < ULR; ++k) {
-          const int u = base + k * kSW;
-          if (u < le) {
-#pragma unroll
-            for (int ls = 0; ls < NLS; ++ls)
-#pragma unroll
-              for (int s = 0; s < W; ++s)
-                af[k][ls][s] = load_kfrag<DT, KEL>(
-                    a.A, (int64_t)(row * P + W * c + s) * a.lda + u * 32 + ls * ML::KM + KEL * g,
-                    KEL);
-          }
-        }
-      };
-      load_a(lb + wid);
-      __syncthreads();
       if (threadIdx.x == 0) {
-        const u64 per_launch = (u64)a.n_rt * kLatentUnits;
-        wait_at_least<u64>(a.sync + 1 + 2 * mg, (ticket / a.lr_wgs + 1) * per_launch, a.sync);
+        const u64 target = (ticket / (u64)a.lr_wgs + 1) * (u64)a.n_rt;
+        wait_at_least<u64>(tile_sync(a, mg), target, a.sync);
       }
       __syncthreads();
-      for (int u0 = lb + wid; u0 < le; u0 += kSW * ULR) {
+      const auto tr = dev_rsrc(a.t);
+      for (int u = lb + wid; u < le; u += kSW) {
+        FragL af[NLS][W];
+        FragL tf[NLS][MT];
 #pragma unroll
-        for (int k = 0; k < ULR; ++k) {
-          const int u = u0 + k * kSW;
-          if (u < le) {
+        for (int ls = 0; ls < NLS; ++ls) {
+          const int kr = u * 32 + ls * ML::KM + KEL * g;
 #pragma unroll
-            for (int ls = 0; ls < NLS; ++ls) {
-              const int kr = u * 32 + ls * ML::KM + KEL * g;
-              FragL tf[MT];
+          for (int mt = 0; mt < MT; ++mt)
+            tf[ls][mt] = ld_dev_frag<DT, KEL>(
+                tr, (int)(((int64_t)(m0 + mt * 16 + c) * a.ldt + kr) * EB));
 #pragma unroll
-              for (int mt = 0; mt < MT; ++mt) {
-                const int rr = mt * 16 + c;
-                tf[mt] = (rr < Mrem) ? load_latent<DT, KEL>((const float*)a.t,
-                                                            (int64_t)(m0 + rr) * a.ldt + kr, a.n_kc,
-                                                            (int64_t)a.M * a.ldt)
-                                     : zero_frag<DT, KEL>();
-              }
-#pragma unroll
-              for (int s = 0; s < W; ++s)
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) ML::run(acc[mt][s], tf[mt], af[k][ls][s]);
-            }
-          }
+          for (int s = 0; s < W; ++s)
+            af[ls][s] = (u == lb + wid)
+                            ? af0[ls][s]
+                            : load_kfrag<DT, KEL>(a.A, (int64_t)(row * P + W * c + s) * a.lda + kr,
+                                                  KEL);
         }
-        if (u0 + kSW * ULR < le) load_a(u0 + kSW * ULR);
+#pragma unroll
+        for (int ls = 0; ls < NLS; ++ls)
+#pragma unroll
+          for (int s = 0; s < W; ++s)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) ML::run(acc[mt][s], tf[ls][mt], af[ls][s]);
       }
     }
   }
@@ -630,31 +711,46 @@ hipError_t dispatch(int dtype, int P, int MT, const SlrArgs& a, int64_t blocks, 
   return hipErrorInvalidValue;
 }
 
-// In_features chunks of the latent. More chunks put more workgroups (and so
-// more of the device's memory parallelism) on the latent, which every row
-// needs before it can finish; each chunk adds an fp32 partial of t that every
-// row workgroup reads, so the split shrinks as the token count grows.
-int latent_split(int64_t M, int64_t m_pad) {
-  const int64_t by_width = m_pad / 512 > 1 ? m_pad / 512 : 1;  // ≥ 512 columns per chunk
-  const int64_t Mc = M > 0 ? M : 1;
-  int64_t by_tokens = 32 / Mc;
-  if (by_tokens > 8) by_tokens = 8;
-  if (by_tokens < 1) by_tokens = 1;
-  return (int)(by_width < by_tokens ? by_width : by_tokens);
+// Most in_features chunks of the latent a call may use (the workspace is
+// sized for this many fp32 partials). More chunks put more workgroups, and so
+// more of the device's memory parallelism, on the latent that every row needs
+// before it can finish; chunks stay at least 512 columns wide, and calls with
+// many token rows keep few partials.
+int latent_split_max(int64_t M, int64_t m_pad) {
+  int64_t n = m_pad / 512;
+  const int64_t by_tokens = 128 / (M > 0 ? M : 1);
+  if (n > by_tokens) n = by_tokens;
+  if (n > 8) n = 8;
+  return n < 1 ? 1 : (int)n;
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cache[dev] = v;
+  }
+  return cache[dev];
 }
 
 bool supported_block(int p, int q) { return p == q && (p == 16 || p == 32 || p == 64); }
 bool supported_dtype(int dt) { return dt == SSL_F32 || dt == SSL_BF16 || dt == SSL_F16; }
 
-// Scratch layout of one fused call. Counters live in their own int32 array
-// (zero at rest, never shared with data); the data workspace holds the latent
-// and the fp32 partial tiles of split rows (byte offsets).
+// Scratch layout of one fused call. Row counters live in their own int32 array
+// (zero at rest, never shared with data) and the handshake words in the plan's
+// own uint64 array; the data workspace holds the latent partials, the final
+// latent and the fp32 partial tiles of split rows (byte offsets).
 struct Layout {
   int MT, MG;
-  int n_rt, n_kc, ku_total, ku_chunk;
+  int n_rt, n_kc_max, ku_total;
   int64_t cnt_total;  // int32 row counters: [MG][NB]
-  int64_t n_sync;     // u64 sync words: status + 2 per token tile
-  int64_t t_buf, part_main, total;
+  int64_t n_sync;     // u64 handshake words: status, then (2 + n_rt) per token tile
+  int64_t t_part, t_final, part_main, total;
 };
 
 Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, int64_t n_slots,
@@ -665,20 +761,34 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   L.n_rt = (int)(r_pad / 16);
   const int KM = dtype == SSL_F32 ? 16 : 32;
   L.ku_total = (int)(m_pad / KM);
-  L.n_kc = latent_split(M, m_pad);  // 1..8
-  L.ku_chunk = (L.ku_total + L.n_kc - 1) / L.n_kc;
-  if (L.ku_chunk < 1) L.ku_chunk = 1;
-  L.n_kc = (L.ku_total + L.ku_chunk - 1) / L.ku_chunk;
-  if (L.n_kc < 1) L.n_kc = 1;
+  L.n_kc_max = latent_split_max(M, m_pad);
   L.cnt_total = (int64_t)L.MG * NB;
-  L.n_sync = 1 + 2 * (int64_t)L.MG;
+  L.n_sync = 1 + (int64_t)L.MG * (2 + L.n_rt);
+  const int64_t rows = (int64_t)L.MG * 16 * L.MT;
   int64_t off = 0;
-  L.t_buf = off;
-  off = align_up(off + 4 * (int64_t)L.n_kc * M * r_pad, 256);
+  L.t_part = off;
+  if (L.n_kc_max > 1) off = align_up(off + 4 * (int64_t)L.n_kc_max * rows * r_pad, 256);
+  L.t_final = off;
+  off = align_up(off + (int64_t)elem_bytes(dtype) * rows * r_pad, 256);
   L.part_main = off;
   off = align_up(off + 4 * (int64_t)L.MG * n_slots * (16 * L.MT * p), 256);
   L.total = off;
   return L;
+}
+
+// K chunks of this launch's latent: as many as the free compute units allow
+// (latent and row workgroups all resident at once), at most n_kc_max; then
+// evened out so no chunk is empty.
+void latent_chunks(const Layout& L, int64_t n_stream, int* n_kc, int* ku_chunk) {
+  const int64_t per_chunk = (int64_t)L.n_rt * L.MG;
+  int64_t n = per_chunk > 0 ? (device_cus() - n_stream) / per_chunk : 1;
+  if (n > L.n_kc_max) n = L.n_kc_max;
+  if (n < 1) n = 1;
+  int ku = (int)((L.ku_total + n - 1) / n);
+  if (ku < 1) ku = 1;
+  *ku_chunk = ku;
+  *n_kc = (L.ku_total + ku - 1) / ku;
+  if (*n_kc < 1) *n_kc = 1;
 }
 
 }  // namespace
@@ -748,7 +858,9 @@ int64_t ssl_slr_counter_count(int64_t M, int64_t NB) {
   return slr_layout(M, NB, 16, 0, 64, 0, SSL_BF16).cnt_total;
 }
 
-int64_t ssl_slr_sync_count(int64_t M) { return slr_layout(M, 0, 16, 0, 64, 0, SSL_BF16).n_sync; }
+int64_t ssl_slr_sync_count(int64_t M, int64_t r_pad) {
+  return slr_layout(M, 0, 16, r_pad, 64, 0, SSL_BF16).n_sync;
+}
 
 int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r_pad,
                                int64_t m_pad, int64_t n_slots, int32_t dtype) {
@@ -782,6 +894,9 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
   if ((A && !aligned(A, 16)) || (B && !aligned(B, 16)) || (values && !aligned(values, 16)))
     return fail(SSL_ERR_INVALID, "A, B and values must be 16-byte aligned");
   const Layout L = slr_layout(M, NB, block_p, r_pad, m_pad, n_slots, dtype);
+  if (L.total > 0x7fffffffLL)
+    return fail(SSL_ERR_UNSUPPORTED, "workspace of %lld bytes exceeds 2 GiB; split the call by tokens",
+                (long long)L.total);
   if (workspace_bytes < L.total || !workspace)
     return fail(SSL_ERR_WORKSPACE, "workspace of %lld bytes needed", (long long)L.total);
   if (!aligned(workspace, 256)) return fail(SSL_ERR_WORKSPACE, "workspace must be 256-byte aligned");
@@ -790,7 +905,9 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
   if (n_sync < L.n_sync || !sync)
     return fail(SSL_ERR_WORKSPACE, "%lld sync words needed", (long long)L.n_sync);
   if (!aligned(sync, 8)) return fail(SSL_ERR_WORKSPACE, "sync words must be 8-byte aligned");
-  const int64_t n_lat = (int64_t)L.n_rt * L.n_kc * L.MG;
+  int n_kc = 1, ku_chunk = 1;
+  latent_chunks(L, n_chunks * L.MG, &n_kc, &ku_chunk);
+  const int64_t n_lat = (int64_t)L.n_rt * n_kc * L.MG;
   const int64_t blocks = n_lat + n_chunks * L.MG;
   if (blocks > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
   char* ws = (char*)workspace;
@@ -801,10 +918,10 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
   a.n_chunks = (int)n_chunks; a.NB = (int)NB;
   a.A = A; a.lda = r_pad; a.bias = bias;
   a.n_slots = n_slots; a.part_main = (float*)(ws + L.part_main); a.cnt_main = counters;
-  a.B = B; a.ldb = m_pad; a.t = ws + L.t_buf; a.ldt = r_pad;
-  a.n_rt = L.n_rt; a.n_kc = L.n_kc; a.ku_total = L.ku_total; a.ku_chunk = L.ku_chunk;
+  a.B = B; a.ldb = m_pad; a.t = ws + L.t_final; a.ldt = r_pad; a.t_part = (float*)(ws + L.t_part);
+  a.MG = L.MG; a.n_rt = L.n_rt; a.n_kc = n_kc; a.ku_total = L.ku_total; a.ku_chunk = ku_chunk;
   a.n_lat_wgs = (int)n_lat;
-  a.sync = (u64*)sync; a.lr_wgs = (int)lr_wgs; a.lat_weight = kLatentUnits / L.n_kc;
+  a.sync = (u64*)sync; a.lr_wgs = (int)lr_wgs; a.lat_weight = kLatentUnits / n_kc;
   return check_hip(dispatch<MODE_FUSED>(dtype, block_p, L.MT, a, blocks, (hipStream_t)stream),
                    "slr launch");
 }

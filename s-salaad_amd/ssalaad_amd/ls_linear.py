@@ -121,7 +121,7 @@ class _KernelState:
             )
             ws = _runtime.workspace(x.device, need)
             cnt = _runtime.counters(x.device, lib.ssl_slr_counter_count(M, self.NB))
-            sync = pl.sync(lib.ssl_slr_sync_count(M))
+            sync = pl.sync(lib.ssl_slr_sync_count(M, self.r_pad))
             rc = lib.ssl_slr_forward(
                 y.data_ptr(), y.stride(0), x2.data_ptr(), x2.stride(0), self.A.data_ptr(),
                 self.B.data_ptr(), _lib.ptr(self.bias), self.col.data_ptr(),

@@ -162,11 +162,13 @@ def test_workspace_sizes_are_aligned_and_monotone():
     c = lib.ssl_slr_workspace_size(2048, 172, 64, 256, 4096, 0, _lib.SSL_BF16)
     assert a % 256 == 0 and b > a and c > a
     # counters: one per (token tile, block-row); sync words: the status word,
-    # then latent-done and consumer-ticket counters per token tile
+    # then per token tile the latent-ready and ticket words and one arrival
+    # word per 16-rank tile
     assert lib.ssl_slr_counter_count(16, 172) == 172
     assert lib.ssl_slr_counter_count(2048, 172) == 32 * 172
-    assert lib.ssl_slr_sync_count(16) == 3
-    assert lib.ssl_slr_sync_count(2048) == 1 + 2 * 32
+    assert lib.ssl_slr_sync_count(16, 256) == 1 + 2 + 16
+    assert lib.ssl_slr_sync_count(2048, 256) == 1 + 32 * (2 + 16)
+    assert lib.ssl_slr_sync_count(16, 0) == 3
     assert lib.ssl_bsr_addmm_counter_count(16, 172) == 172
     assert lib.ssl_bsr_addmm_counter_count(65, 172) == 2 * 172
     assert lib.ssl_bsr_addmm_workspace_size(16, 172, 64, 0) == 0
