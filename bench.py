@@ -126,22 +126,28 @@ def run_gpu(args):
     s = torch.cuda.Stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(s):
-        step()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=s):
         keep = step()
     torch.cuda.synchronize()
+    if args.eager:
+        # launches issued one by one (hardware counters are collected per
+        # dispatch, which graph replays do not expose)
+        run = step
+    else:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            keep = step()
+        torch.cuda.synchronize()
+        run = g.replay
 
     with torch.cuda.stream(s):
         for _ in range(args.warmup):
-            g.replay()
+            run()
         torch.cuda.synchronize()
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         ev0.record(s)
         for _ in range(args.steps):
-            g.replay()
+            run()
         ev1.record(s)
         torch.cuda.synchronize()
     ms_step = ev0.elapsed_time(ev1) / args.steps
@@ -171,6 +177,33 @@ def run_gpu(args):
         res["status"] = latent_wait_status(dev)
     res["status"] = max(res["status"], latent_wait_status(dev))
     return res
+
+
+def copy_probe(mib: int, reps: int) -> None:
+    """A plain device-to-device copy of `mib` MiB, `reps` times: the known-size
+    kernel whose FETCH_SIZE / WRITE_SIZE counters calibrate the kernel's."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    a = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": mib << 20, "reps": reps}), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, calibrated on a plain copy),
+    or None when there is none."""
+    path = ROOT / "profiles" / "slr_kernel_llama1b_decode_counters.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
 
 
 # -------------------------------------------------------------- CPU leg --
@@ -264,7 +297,14 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the step eagerly instead of replaying a HIP graph")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe(args.copy_probe, max(1, args.steps))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the SLR linear "
               "shards by output block-rows with no exchange; see the design notes).",
@@ -309,7 +349,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(g["achieved_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "slr_kernel<bf16,p32,MT1,fused>",
             "avg_launch_us": round(g["avg_launch_us"], 3),
             "algorithmic_bytes_per_launch": int(g["bytes_per_launch"]),
@@ -319,6 +359,7 @@ def main():
             "step_TFLOPs": round(g["step_tflops"], 3),
             "bytes_per_step": int(g["total_bytes_per_step"]),
             "graph_matches_eager": g["graph_matches_eager"],
+            "timing": "eager launches" if args.eager else "HIP graph replay",
             "latent_wait_status": g["status"],
         },
     }
