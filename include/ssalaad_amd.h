@@ -116,22 +116,26 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx,
  * `bias` may be NULL. y must hold M rows of n_pad columns (ldy ≥ n_pad).
  * `counters` (ssl_slr_counter_count int32) start at zero and are zero again when
  * the launch ends; they may be shared by calls ordered on one stream.
- * `sync` (ssl_slr_sync_count uint64) belongs to one plan: zero when the plan is
- * made, then advanced by every call with that plan, never reset; calls with one
- * plan must be ordered on one stream. sync[0] is set to 1 if a workgroup gave up
- * waiting (never expected; the host may check it after synchronising).
+ * `exchange` (ssl_slr_exchange_size bytes, 256-byte aligned) belongs to one plan:
+ * uint64 handshake words, zeroed when the plan is made, then advanced by every
+ * call with that plan and never reset; calls with one plan must be ordered on
+ * one stream, and the area must never be shared with another plan. Its first
+ * uint64 is set to 1 if a workgroup gave up waiting (never expected; the host
+ * may check it after synchronising). A zeroed area is always a valid state
+ * (e.g. after growing it).
  * ------------------------------------------------------------------------- */
 int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r_pad,
                                int64_t m_pad, int64_t n_slots, int32_t dtype);
 int64_t ssl_slr_counter_count(int64_t M, int64_t NB);
-int64_t ssl_slr_sync_count(int64_t M, int64_t r_pad);
+int64_t ssl_slr_exchange_size(int64_t M, int64_t r_pad, int64_t m_pad, int32_t dtype);
 int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A,
                     const void* B, const void* bias, const int32_t* col,
                     const void* values, const int32_t* plan, int64_t n_chunks,
                     int64_t n_slots, int64_t lr_wgs, int64_t M, int64_t m, int64_t m_pad,
                     int64_t NB, int64_t r_pad, int32_t block_p, int32_t block_q,
-                    int32_t dtype, int32_t* counters, int64_t n_counters, uint64_t* sync,
-                    int64_t n_sync, void* workspace, int64_t workspace_bytes, void* stream);
+                    int32_t dtype, int32_t* counters, int64_t n_counters, void* exchange,
+                    int64_t exchange_bytes, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
 /* -------------------------------------------------------------------------
  * Dense → BSR encoder (device), the rule of ssalaad/efficient/artifact.py:20-37

@@ -58,6 +58,11 @@ COMMON_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # One-lane ticket atomics stay one-lane: the wave-aggregating atomic
+    # rewrite broadcasts the result and so waits for it at once, stalling the
+    # wave's first loads behind a device round trip.
+    "-mllvm",
+    "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall",
     "-Wno-unused-function",
     "-I",

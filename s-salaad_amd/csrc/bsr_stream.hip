@@ -360,15 +360,22 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
       const int u = u0 + k * kSW;
       if (u < ue) {
         const int kcol = u * KM + KE * g;
+        if (u * KM + KM <= a.m) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int rr = mt * 16 + c;
-          const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
-          xf[k][mt] = (valid > 0)
-                          ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol, valid)
-                          : zero_frag<DT, KE>();
+          for (int mt = 0; mt < MT; ++mt)
+            xf[k][mt] = load_kfrag_full<DT, KE>(
+                a.x, (int64_t)(m0 + min(mt * 16 + c, Mrem - 1)) * a.ldx + kcol);
+        } else {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int rr = mt * 16 + c;
+            const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
+            xf[k][mt] = (valid > 0)
+                            ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol, valid)
+                            : zero_frag<DT, KE>();
+          }
         }
-        bf[k] = load_kfrag<DT, KE>(a.B, brow + kcol, KE);
+        bf[k] = load_kfrag_full<DT, KE>(a.B, brow + kcol);
       }
     }
 #pragma unroll
@@ -509,16 +516,22 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
       if (u < be) {
         const int colb = a.col[u] * Q;
         const char* vb = (const char*)a.values + (int64_t)u * (P * Q * EB);
+        const bool full = colb + Q <= a.m;
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
           const int kcol = colb + ks * KM + KE * g;
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             const int rr = mt * 16 + c;
-            const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
-            xf[k][ks][mt] = (valid > 0) ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol,
-                                                             valid)
-                                        : zero_frag<DT, KE>();
+            if (full) {
+              xf[k][ks][mt] =
+                  load_kfrag_full<DT, KE>(a.x, (int64_t)(m0 + min(rr, Mrem - 1)) * a.ldx + kcol);
+            } else {
+              const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
+              xf[k][ks][mt] = (valid > 0) ? load_kfrag<DT, KE>(
+                                                a.x, (int64_t)(m0 + rr) * a.ldx + kcol, valid)
+                                          : zero_frag<DT, KE>();
+            }
           }
           load_vstep<DT, KE, W>(raw[k][ks], vb, P, ks * KM, lane);
         }
@@ -858,8 +871,10 @@ int64_t ssl_slr_counter_count(int64_t M, int64_t NB) {
   return slr_layout(M, NB, 16, 0, 64, 0, SSL_BF16).cnt_total;
 }
 
-int64_t ssl_slr_sync_count(int64_t M, int64_t r_pad) {
-  return slr_layout(M, 0, 16, r_pad, 64, 0, SSL_BF16).n_sync;
+int64_t ssl_slr_exchange_size(int64_t M, int64_t r_pad, int64_t m_pad, int32_t dtype) {
+  (void)m_pad;
+  (void)dtype;
+  return align_up(8 * slr_layout(M, 0, 16, r_pad, 64, 0, SSL_BF16).n_sync, 256);
 }
 
 int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r_pad,
@@ -871,8 +886,8 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
                     const void* bias, const int32_t* col, const void* values, const int32_t* plan,
                     int64_t n_chunks, int64_t n_slots, int64_t lr_wgs, int64_t M, int64_t m,
                     int64_t m_pad, int64_t NB, int64_t r_pad, int32_t block_p, int32_t block_q,
-                    int32_t dtype, int32_t* counters, int64_t n_counters, uint64_t* sync,
-                    int64_t n_sync, void* workspace, int64_t workspace_bytes, void* stream) {
+                    int32_t dtype, int32_t* counters, int64_t n_counters, void* exchange,
+                    int64_t exchange_bytes, void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   if (!supported_dtype(dtype)) return fail(SSL_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
   if (!supported_block(block_p, block_q))
@@ -902,9 +917,9 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
   if (!aligned(workspace, 256)) return fail(SSL_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if (n_counters < L.cnt_total || !counters)
     return fail(SSL_ERR_WORKSPACE, "%lld zeroed counters needed", (long long)L.cnt_total);
-  if (n_sync < L.n_sync || !sync)
-    return fail(SSL_ERR_WORKSPACE, "%lld sync words needed", (long long)L.n_sync);
-  if (!aligned(sync, 8)) return fail(SSL_ERR_WORKSPACE, "sync words must be 8-byte aligned");
+  if (exchange_bytes < 8 * L.n_sync || !exchange)
+    return fail(SSL_ERR_WORKSPACE, "exchange area of %lld bytes needed", (long long)(8 * L.n_sync));
+  if (!aligned(exchange, 256)) return fail(SSL_ERR_WORKSPACE, "exchange area must be 256-byte aligned");
   int n_kc = 1, ku_chunk = 1;
   latent_chunks(L, n_chunks * L.MG, &n_kc, &ku_chunk);
   const int64_t n_lat = (int64_t)L.n_rt * n_kc * L.MG;
@@ -921,7 +936,7 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
   a.B = B; a.ldb = m_pad; a.t = ws + L.t_final; a.ldt = r_pad; a.t_part = (float*)(ws + L.t_part);
   a.MG = L.MG; a.n_rt = L.n_rt; a.n_kc = n_kc; a.ku_total = L.ku_total; a.ku_chunk = ku_chunk;
   a.n_lat_wgs = (int)n_lat;
-  a.sync = (u64*)sync; a.lr_wgs = (int)lr_wgs; a.lat_weight = kLatentUnits / n_kc;
+  a.sync = (u64*)exchange; a.lr_wgs = (int)lr_wgs; a.lat_weight = kLatentUnits / n_kc;
   return check_hip(dispatch<MODE_FUSED>(dtype, block_p, L.MT, a, blocks, (hipStream_t)stream),
                    "slr launch");
 }

@@ -180,6 +180,25 @@ __device__ __forceinline__ typename Mma<DT, KE>::Frag load_kfrag(const void* bas
   return f;
 }
 
+// Unmasked form: KE elements known to be in range (one vector access).
+template <int DT, int KE>
+__device__ __forceinline__ typename Mma<DT, KE>::Frag load_kfrag_full(const void* base,
+                                                                      int64_t off) {
+  using F = typename Mma<DT, KE>::Frag;
+  F f;
+  if constexpr (DT == DT_F32) {
+    const float4 v = *(const float4*)((const float*)base + off);
+    f.f[0] = v.x; f.f[1] = v.y; f.f[2] = v.z; f.f[3] = v.w;
+  } else if constexpr (KE == 8) {
+    const uint4 v = *(const uint4*)((const uint16_t*)base + off);
+    f.d[0] = v.x; f.d[1] = v.y; f.d[2] = v.z; f.d[3] = v.w;
+  } else {
+    const uint2 v = *(const uint2*)((const uint16_t*)base + off);
+    f.d[0] = v.x; f.d[1] = v.y;
+  }
+  return f;
+}
+
 template <int DT, int KE>
 __device__ __forceinline__ typename Mma<DT, KE>::Frag zero_frag() {
   typename Mma<DT, KE>::Frag f;

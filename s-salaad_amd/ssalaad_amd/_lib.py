@@ -48,7 +48,7 @@ _SIGNATURES = {
     ),
     "ssl_slr_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32]),
     "ssl_slr_counter_count": (_c_i64, [_c_i64, _c_i64]),
-    "ssl_slr_sync_count": (_c_i64, [_c_i64, _c_i64]),
+    "ssl_slr_exchange_size": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i32]),
     "ssl_slr_forward": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,

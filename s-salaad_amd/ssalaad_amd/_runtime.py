@@ -8,8 +8,8 @@ that stream and grown when a call needs more:
     return every counter they touch to zero, so the pool is zero at rest;
   * workspace: bytes for the low-rank latent and the partial tiles of split
     rows; no initialisation needed.
-A plan that feeds the fused kernel also owns its latent-handshake words (see
-DevicePlan.sync): those advance monotonically and are never shared.
+A plan that feeds the fused kernel also owns its exchange area (see
+DevicePlan.exchange): it advances monotonically and is never shared.
 """
 
 from __future__ import annotations
@@ -81,7 +81,7 @@ _PLANS: "weakref.WeakSet[DevicePlan]" = weakref.WeakSet()
 class DevicePlan:
     """A plan uploaded to one device."""
 
-    __slots__ = ("table", "n_chunks", "n_slots", "lr_wgs", "_sync", "__weakref__")
+    __slots__ = ("table", "n_chunks", "n_slots", "lr_wgs", "_exchange", "__weakref__")
 
     def __init__(self, table: np.ndarray, n_chunks: int, n_slots: int, device: torch.device):
         t = torch.from_numpy(table if n_chunks else np.zeros((1, _lib.PLAN_STRIDE), np.int32))
@@ -91,28 +91,30 @@ class DevicePlan:
         # workgroups that read the latent: the chunks with low-rank units
         lr = (table[:n_chunks, 4] - table[:n_chunks, 3]) if n_chunks else np.zeros(0)
         self.lr_wgs = int((lr > 0).sum())
-        self._sync: torch.Tensor | None = None
+        self._exchange: torch.Tensor | None = None
         _PLANS.add(self)
 
-    def sync(self, count: int) -> torch.Tensor:
-        """The plan's own latent-handshake words (uint64 as int64), at least `count`.
+    def exchange(self, nbytes: int) -> torch.Tensor:
+        """The plan's own exchange area (bytes), at least `nbytes`.
 
-        The kernels advance them monotonically and never reset them, so they
-        belong to this plan alone; calls with one plan are ordered on one
-        stream. Growing replaces them with zeros, which is a consistent state
-        for the next call on that stream.
+        It holds the plan's latent-handshake counters, which the kernels advance
+        monotonically and never reset, so it belongs to this plan alone and
+        calls with one plan are ordered on one stream. Growing replaces it with
+        zeros, which is a valid state for the next call.
         """
-        if self._sync is None or self._sync.numel() < count:
-            self._sync = torch.zeros(max(int(count), 8), dtype=torch.int64,
-                                     device=self.table.device)
-        return self._sync
+        if self._exchange is None or self._exchange.numel() < nbytes:
+            self._exchange = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8,
+                                         device=self.table.device)
+        return self._exchange
 
     def wait_status(self) -> int:
         """1 if a workgroup of a call with this plan gave up waiting, else 0.
 
         Synchronises the device.
         """
-        return 0 if self._sync is None else int(self._sync[0].item())
+        if self._exchange is None:
+            return 0
+        return int(self._exchange[:8].view(torch.int64)[0].item())
 
 
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}

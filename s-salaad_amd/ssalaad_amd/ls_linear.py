@@ -121,13 +121,13 @@ class _KernelState:
             )
             ws = _runtime.workspace(x.device, need)
             cnt = _runtime.counters(x.device, lib.ssl_slr_counter_count(M, self.NB))
-            sync = pl.sync(lib.ssl_slr_sync_count(M, self.r_pad))
+            xch = pl.exchange(lib.ssl_slr_exchange_size(M, self.r_pad, self.m_pad, self.dtype_code))
             rc = lib.ssl_slr_forward(
                 y.data_ptr(), y.stride(0), x2.data_ptr(), x2.stride(0), self.A.data_ptr(),
                 self.B.data_ptr(), _lib.ptr(self.bias), self.col.data_ptr(),
                 self.values.data_ptr(), pl.table.data_ptr(), pl.n_chunks, pl.n_slots,
                 pl.lr_wgs, M, m, self.m_pad, self.NB, self.r_pad, self.p, self.p,
-                self.dtype_code, cnt.data_ptr(), cnt.numel(), sync.data_ptr(), sync.numel(),
+                self.dtype_code, cnt.data_ptr(), cnt.numel(), xch.data_ptr(), xch.numel(),
                 ws.data_ptr(), ws.numel(),
                 _lib.stream_ptr(x.device),
             )

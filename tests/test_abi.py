@@ -159,16 +159,22 @@ def test_workspace_sizes_are_aligned_and_monotone():
     lib = _lib.load()
     a = lib.ssl_slr_workspace_size(16, 172, 64, 256, 4096, 0, _lib.SSL_BF16)
     b = lib.ssl_slr_workspace_size(16, 172, 64, 256, 4096, 100, _lib.SSL_BF16)
-    c = lib.ssl_slr_workspace_size(2048, 172, 64, 256, 4096, 0, _lib.SSL_BF16)
-    assert a % 256 == 0 and b > a and c > a
-    # counters: one per (token tile, block-row); sync words: the status word,
-    # then per token tile the latent-ready and ticket words and one arrival
-    # word per 16-rank tile
+    c = lib.ssl_slr_workspace_size(2048, 172, 64, 256, 4096, 10, _lib.SSL_BF16)
+    # workspace: fp32 latent partials (up to 8 K chunks at decode), the final
+    # latent (activation dtype), then the fp32 partial tiles of split rows
+    # ([MG][slots][16·MT][p]); each part 256-byte aligned
+    assert a == 8 * 16 * 256 * 4 + 16 * 256 * 2
+    assert b == a + 100 * 16 * 64 * 4
+    assert c == 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4
+    # counters: one per (token tile, block-row)
     assert lib.ssl_slr_counter_count(16, 172) == 172
     assert lib.ssl_slr_counter_count(2048, 172) == 32 * 172
-    assert lib.ssl_slr_sync_count(16, 256) == 1 + 2 + 16
-    assert lib.ssl_slr_sync_count(2048, 256) == 1 + 32 * (2 + 16)
-    assert lib.ssl_slr_sync_count(16, 0) == 3
+    # exchange: the plan's uint64 handshake words (status, then per token tile
+    # the latent-ready and ticket words and one arrival word per 16-rank
+    # tile), 256-byte aligned
+    assert lib.ssl_slr_exchange_size(16, 256, 4096, _lib.SSL_BF16) == 256
+    assert lib.ssl_slr_exchange_size(2048, 256, 4096, _lib.SSL_BF16) == 4864  # 8·(1 + 32·18)
+    assert lib.ssl_slr_exchange_size(16, 0, 4096, _lib.SSL_BF16) == 256
     assert lib.ssl_bsr_addmm_counter_count(16, 172) == 172
     assert lib.ssl_bsr_addmm_counter_count(65, 172) == 2 * 172
     assert lib.ssl_bsr_addmm_workspace_size(16, 172, 64, 0) == 0
@@ -214,7 +220,7 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     assert rc == _lib.SSL_ERR_WORKSPACE and b"counters" in lib.ssl_last_error()
     rc = lib.ssl_slr_forward(16, 64, 16, 64, 16, 16, None, 16, 16, 16, 1, 0, 1, 1, 64, 64, 1, 64,
                              64, 64, _lib.SSL_BF16, 256, 1, None, 0, 256, 1 << 20, None)
-    assert rc == _lib.SSL_ERR_WORKSPACE and b"sync" in lib.ssl_last_error()
+    assert rc == _lib.SSL_ERR_WORKSPACE and b"exchange" in lib.ssl_last_error()
     with pytest.raises(ValueError):
         _lib.check(_lib.SSL_ERR_INVALID, "x")
     with pytest.raises(TypeError):
