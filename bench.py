@@ -7,15 +7,20 @@ step = one pass of a batch through all 168 linears (y = x·Bᵀ·Aᵀ + x·Sᵀ)
 the projection work of one decode step. Weights (1.69 GB) exceed the 256 MB
 last-level cache, so every step streams them from HBM.
 
+Launches: the linears that read the same activation run as one launch of the
+fused kernel (LRSLinearGroup): q, k, v | o | gate, up | down, i.e. 4 launches
+per layer, 96 per step (--no-group: one launch per linear, 168 per step). Each
+linear is computed exactly as its own module computes it.
+
 Timing: the step is captured once in a HIP graph and replayed; W untimed
 replays, then K replays bracketed by synchronize + HIP events on the replay
 stream. value = M·K / elapsed (tokens/s).
 
-roofline: each SLR linear is one launch of the fused kernel (latent, sparse
-blocks, t·Aᵀ and epilogue), so the step's 168 launches are all that kernel; its
-average launch duration = the HIP-event time of the graph replays / 168 (gaps
-between launches included, so this slightly understates the kernel);
-achieved = algorithmic bytes per launch / that duration.
+roofline: every launch of the step is the fused kernel (latent, sparse blocks,
+t·Aᵀ and epilogue); its average launch duration = the HIP-event time of the
+graph replays / launches per step (gaps between launches included, so this
+slightly understates the kernel); achieved = algorithmic bytes per launch /
+that duration.
 
 cpu_baseline: the reference AVX2 BSR kernel (oracle/_ref, compiled from the
 reference's own source) plus torch-CPU F.linear ×2 — the reference's CPU
@@ -118,10 +123,21 @@ def run_gpu(args):
     xin = {"q": xh, "k": xh, "v": xh, "o": xo, "gate": xh, "up": xh, "down": xd}
     mods = [(name, mod) for layer in layers for name, mod in layer]
     bytes_ = [algorithmic_bytes(mod, M, e) for _, mod in mods]
-    states = [mod._kernel() for _, mod in mods]
+    # launches: the linears that read the same activation go in one launch
+    # (q, k, v | o | gate, up | down) unless --no-group
+    from ssalaad_amd import LRSLinearGroup
+
+    calls = []
+    for layer in layers:
+        d = dict(layer)
+        sets = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
+        if args.no_group:
+            sets = [[name] for name, _ in layer]
+        for names in sets:
+            calls.append((LRSLinearGroup(*[d[nm] for nm in names]), xin[names[0]]))
 
     def step():
-        return [st.forward(xin[name], mod.out_features) for (name, mod), st in zip(mods, states)]
+        return [out for grp, x in calls for out in grp(x)]
 
     s = torch.cuda.Stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))
@@ -152,19 +168,21 @@ def run_gpu(args):
         torch.cuda.synchronize()
     ms_step = ev0.elapsed_time(ev1) / args.steps
     n_lin = len(mods)
+    n_launch = len(calls)
     total_bytes = sum(b["total"] for b in bytes_)
     total_flops = sum(b["flops"] for b in bytes_)
-    avg_us = ms_step * 1e3 / n_lin
-    achieved = total_bytes / n_lin / (avg_us * 1e-6) / 1e9
+    avg_us = ms_step * 1e3 / n_launch
+    achieved = total_bytes / n_launch / (avg_us * 1e-6) / 1e9
     res = dict(
         ms_step=ms_step,
         tok_s=M / (ms_step * 1e-3),
         step_tflops=total_flops / (ms_step * 1e-3) / 1e12,
         avg_launch_us=avg_us,
         achieved_gbs=achieved,
-        bytes_per_launch=total_bytes / n_lin,
+        bytes_per_launch=total_bytes / n_launch,
         total_bytes_per_step=total_bytes,
         n_linears=n_lin,
+        n_launches=n_launch,
     )
     # a parity spot check of one linear of the timed graph against a fresh call
     name, mod = mods[-1]
@@ -299,6 +317,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step eagerly instead of replaying a HIP graph")
+    ap.add_argument("--no-group", action="store_true",
+                    help="one launch per linear instead of grouping q/k/v and gate/up")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -335,6 +355,7 @@ def main():
             "workload": "llama1b_slr_projections_decode",
             "layers": args.layers,
             "linears_per_step": g["n_linears"],
+            "launches_per_step": g["n_launches"],
             "hidden": 2048,
             "ffn": 5461,
             "rank": 256,

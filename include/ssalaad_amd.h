@@ -137,6 +137,40 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
                     int64_t exchange_bytes, void* workspace, int64_t workspace_bytes,
                     void* stream);
 
+/* One linear of a fused call (the arguments of ssl_slr_forward that differ
+ * between linears reading the same x). */
+typedef struct ssl_slr_member {
+  void* y;
+  int64_t ldy;
+  const void* A;
+  const void* B;
+  const void* bias;
+  const int32_t* col;
+  const void* values;
+  const int32_t* plan;
+  int64_t n_chunks;
+  int64_t n_slots;
+  int64_t lr_wgs;
+  int64_t NB;
+  int64_t r_pad;
+  int32_t* counters;
+  int64_t n_counters;
+  void* exchange;
+  int64_t exchange_bytes;
+  void* workspace;
+  int64_t workspace_bytes;
+} ssl_slr_member;
+
+/* Up to 4 SLR linears that read the same x (e.g. a layer's q, k and v
+ * projections, or its gate and up projections) in ONE launch: each member is
+ * computed exactly as ssl_slr_forward computes it (same rounding points), with
+ * its own plan, counters, exchange area and workspace. Replaces nothing in the
+ * reference (which calls each module on its own); it is the launch-count
+ * reduction a decode step needs. All members share dtype and block size. */
+int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int64_t m_pad,
+                          int32_t block_p, int32_t block_q, int32_t dtype,
+                          const ssl_slr_member* members, int32_t n_members, void* stream);
+
 /* -------------------------------------------------------------------------
  * Dense → BSR encoder (device), the rule of ssalaad/efficient/artifact.py:20-37
  * (dense_to_bsr) followed by the module conversion of

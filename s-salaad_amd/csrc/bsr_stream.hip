@@ -664,20 +664,41 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
 // ---------------------------------------------------------------------------
 // Kernel. Grid (1-D): [latent workgroups][stream chunks × token tiles].
 // ---------------------------------------------------------------------------
+// A launch serves up to kMaxGroup linears that read the same x (e.g. the q, k
+// and v projections): all latent workgroups first, member by member, then all
+// row workgroups, member by member. Workgroup → member lookups read the
+// descriptors in place from the kernel-argument segment (scalar loads).
+constexpr int kMaxGroup = 4;
+struct GroupArgs {
+  int n;                          // members
+  int lat_total;                  // latent workgroups of all members
+  int lat_off[kMaxGroup + 1];     // first latent workgroup of each member
+  int str_off[kMaxGroup + 1];     // first row workgroup (after lat_total) of each member
+  SlrArgs m[kMaxGroup];
+};
+
 template <int DT, int P, int MT, int MODE, int UNR>
-__global__ __launch_bounds__(kST) void slr_kernel(SlrArgs a) {
+__global__ __launch_bounds__(kST) void slr_kernel(GroupArgs g_by_value) {
+  (void)g_by_value;
+  const GroupArgs& g = *(const GroupArgs*)__builtin_amdgcn_kernarg_segment_ptr();
   constexpr int W = P / 16;
   constexpr int SLOTS = red_slots<MT, W>();
   __shared__ f32x4 red[SLOTS * MT * W * kWave];
   const int b = blockIdx.x;
   if constexpr (MODE == MODE_FUSED) {
-    if (b < a.n_lat_wgs) {
-      latent_wg<DT, MT>(a, b, red);
+    if (b < g.lat_total) {
+      int i = 0;
+      while (i + 1 < g.n && b >= g.lat_off[i + 1]) ++i;
+      latent_wg<DT, MT>(g.m[i], b - g.lat_off[i], red);
       return;
     }
   }
-  const int sb = b - (MODE == MODE_FUSED ? a.n_lat_wgs : 0);
-  const int mg = sb / a.n_chunks, chunk = sb % a.n_chunks;
+  const int sb = b - (MODE == MODE_FUSED ? g.lat_total : 0);
+  int i = 0;
+  while (i + 1 < g.n && sb >= g.str_off[i + 1]) ++i;
+  const SlrArgs& a = g.m[i];
+  const int lb = sb - g.str_off[i];
+  const int mg = lb / a.n_chunks, chunk = lb % a.n_chunks;
   stream_wg<DT, P, MT, MODE, UNR>(a, chunk, mg, red);
 }
 
@@ -697,14 +718,14 @@ constexpr int stream_unroll() {
 }
 
 template <int DT, int P, int MT, int MODE>
-hipError_t launch(const SlrArgs& a, int64_t blocks, hipStream_t s) {
+hipError_t launch(const GroupArgs& a, int64_t blocks, hipStream_t s) {
   constexpr int UNR = stream_unroll<DT, P, MT>();
   hipLaunchKernelGGL((slr_kernel<DT, P, MT, MODE, UNR>), dim3((unsigned)blocks), dim3(kST), 0, s, a);
   return hipGetLastError();
 }
 
 template <int DT, int MODE>
-hipError_t dispatch_p(int P, int MT, const SlrArgs& a, int64_t blocks, hipStream_t s) {
+hipError_t dispatch_p(int P, int MT, const GroupArgs& a, int64_t blocks, hipStream_t s) {
 #define SSL_CASE(PP, MM) \
   if (P == PP && MT == MM) return launch<DT, PP, MM, MODE>(a, blocks, s);
   SSL_CASE(16, 1) SSL_CASE(16, 2) SSL_CASE(16, 4)
@@ -715,7 +736,7 @@ hipError_t dispatch_p(int P, int MT, const SlrArgs& a, int64_t blocks, hipStream
 }
 
 template <int MODE>
-hipError_t dispatch(int dtype, int P, int MT, const SlrArgs& a, int64_t blocks, hipStream_t s) {
+hipError_t dispatch(int dtype, int P, int MT, const GroupArgs& a, int64_t blocks, hipStream_t s) {
   switch (dtype) {
     case SSL_F32: return dispatch_p<DT_F32, MODE>(P, MT, a, blocks, s);
     case SSL_BF16: return dispatch_p<DT_BF16, MODE>(P, MT, a, blocks, s);
@@ -790,10 +811,11 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
 }
 
 // K chunks of this launch's latent: as many as the free compute units allow
-// (latent and row workgroups all resident at once), at most n_kc_max; then
-// evened out so no chunk is empty.
-void latent_chunks(const Layout& L, int64_t n_stream, int* n_kc, int* ku_chunk) {
-  const int64_t per_chunk = (int64_t)L.n_rt * L.MG;
+// (latent workgroups — per_chunk of them per K chunk — and the n_stream row
+// workgroups all resident at once), at most n_kc_max; then evened out so no
+// chunk is empty.
+void latent_chunks(const Layout& L, int64_t n_stream, int64_t per_chunk, int* n_kc,
+                   int* ku_chunk) {
   int64_t n = per_chunk > 0 ? (device_cus() - n_stream) / per_chunk : 1;
   if (n > L.n_kc_max) n = L.n_kc_max;
   if (n < 1) n = 1;
@@ -858,12 +880,15 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
     return fail(SSL_ERR_WORKSPACE, "%lld zeroed counters needed",
                 (long long)ssl_bsr_addmm_counter_count(M, NB));
 
-  SlrArgs a{};
+  GroupArgs g{};
+  g.n = 1;
+  g.str_off[1] = (int)(n_chunks * MG);
+  SlrArgs& a = g.m[0];
   a.x = x; a.ldx = ldx; a.M = (int)M; a.m = (int)K;
   a.y = out; a.ldy = ldo; a.col = col; a.values = values; a.plan = plan;
   a.n_chunks = (int)n_chunks; a.NB = (int)NB;
   a.n_slots = n_slots; a.part_main = (float*)workspace; a.cnt_main = counters;
-  return check_hip(dispatch<MODE_OP>(dtype, block_p, MT, a, n_chunks * MG, (hipStream_t)stream),
+  return check_hip(dispatch<MODE_OP>(dtype, block_p, MT, g, n_chunks * MG, (hipStream_t)stream),
                    "bsr_addmm launch");
 }
 
@@ -882,63 +907,117 @@ int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r
   return slr_layout(M, NB, block_p, r_pad, m_pad, n_slots, dtype).total;
 }
 
+int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int64_t m_pad,
+                          int32_t block_p, int32_t block_q, int32_t dtype,
+                          const ssl_slr_member* members, int32_t n_members, void* stream) {
+  clear_error();
+  if (!supported_dtype(dtype)) return fail(SSL_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
+  if (!supported_block(block_p, block_q))
+    return fail(SSL_ERR_UNSUPPORTED,
+                "SLR kernel needs square 16, 32 or 64 blocks, got %dx%d", block_p, block_q);
+  if (n_members < 1 || n_members > kMaxGroup || !members)
+    return fail(SSL_ERR_INVALID, "a fused call takes 1 to %d linears, got %d", kMaxGroup, n_members);
+  if (M < 0 || m < 0) return fail(SSL_ERR_INVALID, "negative size");
+  if (m_pad % 64 || m_pad < m) return fail(SSL_ERR_INVALID, "m_pad must be a multiple of 64 and >= m");
+  const int eb = elem_bytes(dtype);
+  if (M == 0) return SSL_OK;
+  if (!x || !aligned(x, 16) || ldx < m || (ldx * eb) % 16)
+    return fail(SSL_ERR_INVALID, "x rows must be 16-byte aligned and at least m wide");
+
+  GroupArgs g{};
+  g.n = n_members;
+  Layout L[kMaxGroup];
+  int64_t n_stream = 0, rt_tiles = 0;
+  for (int i = 0; i < n_members; ++i) {
+    const ssl_slr_member& mb = members[i];
+    if (mb.NB < 0 || mb.r_pad < 0 || mb.n_chunks < 0 || mb.n_slots < 0 || mb.lr_wgs < 0)
+      return fail(SSL_ERR_INVALID, "linear %d: negative size", i);
+    if (mb.r_pad % 64) return fail(SSL_ERR_INVALID, "linear %d: r_pad must be a multiple of 64", i);
+    if (mb.NB == 0) {  // no output columns: nothing to launch for this linear
+      L[i] = slr_layout(M, 0, block_p, 0, m_pad, 0, dtype);
+      continue;
+    }
+    if (mb.n_chunks == 0)
+      return fail(SSL_ERR_INVALID, "linear %d: empty plan for a non-empty output", i);
+    if ((mb.r_pad > 0) != (mb.lr_wgs > 0) || mb.lr_wgs > mb.n_chunks)
+      return fail(SSL_ERR_INVALID, "linear %d: lr_wgs must count the plan's chunks with low-rank units", i);
+    if (!mb.y || !mb.plan || (mb.r_pad > 0 && (!mb.A || !mb.B)))
+      return fail(SSL_ERR_INVALID, "linear %d: null pointer", i);
+    if (mb.ldy < mb.NB * block_p || !aligned(mb.y, 16) || (mb.ldy * eb) % 16)
+      return fail(SSL_ERR_INVALID, "linear %d: y rows must be 16-byte aligned and NB·p wide", i);
+    if ((mb.A && !aligned(mb.A, 16)) || (mb.B && !aligned(mb.B, 16)) ||
+        (mb.values && !aligned(mb.values, 16)))
+      return fail(SSL_ERR_INVALID, "linear %d: A, B and values must be 16-byte aligned", i);
+    L[i] = slr_layout(M, mb.NB, block_p, mb.r_pad, m_pad, mb.n_slots, dtype);
+    if (L[i].total > 0x7fffffffLL)
+      return fail(SSL_ERR_UNSUPPORTED,
+                  "linear %d: workspace of %lld bytes exceeds 2 GiB; split the call by tokens", i,
+                  (long long)L[i].total);
+    if (mb.workspace_bytes < L[i].total || !mb.workspace)
+      return fail(SSL_ERR_WORKSPACE, "linear %d: workspace of %lld bytes needed", i,
+                  (long long)L[i].total);
+    if (!aligned(mb.workspace, 256))
+      return fail(SSL_ERR_WORKSPACE, "linear %d: workspace must be 256-byte aligned", i);
+    if (mb.n_counters < L[i].cnt_total || !mb.counters)
+      return fail(SSL_ERR_WORKSPACE, "linear %d: %lld zeroed counters needed", i,
+                  (long long)L[i].cnt_total);
+    if (mb.exchange_bytes < 8 * L[i].n_sync || !mb.exchange)
+      return fail(SSL_ERR_WORKSPACE, "linear %d: exchange area of %lld bytes needed", i,
+                  (long long)(8 * L[i].n_sync));
+    if (!aligned(mb.exchange, 256))
+      return fail(SSL_ERR_WORKSPACE, "linear %d: exchange area must be 256-byte aligned", i);
+    n_stream += (mb.NB > 0 ? mb.n_chunks : 0) * L[i].MG;
+    rt_tiles += (int64_t)L[i].n_rt * L[i].MG;
+  }
+  if (n_stream == 0) return SSL_OK;
+
+  // One K split for the whole launch: latent and row workgroups of every
+  // member resident at once.
+  int n_kc = 1, ku_chunk = 1;
+  latent_chunks(L[0], n_stream, rt_tiles, &n_kc, &ku_chunk);
+  int64_t lat = 0, str = 0;
+  for (int i = 0; i < n_members; ++i) {
+    const ssl_slr_member& mb = members[i];
+    g.lat_off[i] = (int)lat;
+    g.str_off[i] = (int)str;
+    lat += (int64_t)L[i].n_rt * n_kc * L[i].MG;
+    str += (mb.NB > 0 ? mb.n_chunks : 0) * L[i].MG;
+    if (lat + str > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
+    char* ws = (char*)mb.workspace;
+    SlrArgs& a = g.m[i];
+    a.x = x; a.ldx = ldx; a.M = (int)M; a.m = (int)m;
+    a.y = mb.y; a.ldy = mb.ldy; a.col = mb.col; a.values = mb.values; a.plan = mb.plan;
+    a.n_chunks = (int)mb.n_chunks; a.NB = (int)mb.NB;
+    a.A = mb.A; a.lda = mb.r_pad; a.bias = mb.bias;
+    a.n_slots = mb.n_slots; a.part_main = (float*)(ws + L[i].part_main); a.cnt_main = mb.counters;
+    a.B = mb.B; a.ldb = m_pad; a.t = ws + L[i].t_final; a.ldt = mb.r_pad;
+    a.t_part = (float*)(ws + L[i].t_part);
+    a.MG = L[i].MG; a.n_rt = L[i].n_rt; a.n_kc = n_kc; a.ku_total = L[i].ku_total;
+    a.ku_chunk = ku_chunk;
+    a.n_lat_wgs = (int)((int64_t)L[i].n_rt * n_kc * L[i].MG);
+    a.sync = (u64*)mb.exchange; a.lr_wgs = (int)mb.lr_wgs; a.lat_weight = kLatentUnits / n_kc;
+  }
+  g.lat_off[n_members] = (int)lat;
+  g.str_off[n_members] = (int)str;
+  g.lat_total = (int)lat;
+  return check_hip(
+      dispatch<MODE_FUSED>(dtype, block_p, L[0].MT, g, lat + str, (hipStream_t)stream),
+      "slr launch");
+}
+
 int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A, const void* B,
                     const void* bias, const int32_t* col, const void* values, const int32_t* plan,
                     int64_t n_chunks, int64_t n_slots, int64_t lr_wgs, int64_t M, int64_t m,
                     int64_t m_pad, int64_t NB, int64_t r_pad, int32_t block_p, int32_t block_q,
                     int32_t dtype, int32_t* counters, int64_t n_counters, void* exchange,
                     int64_t exchange_bytes, void* workspace, int64_t workspace_bytes, void* stream) {
-  clear_error();
-  if (!supported_dtype(dtype)) return fail(SSL_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
-  if (!supported_block(block_p, block_q))
-    return fail(SSL_ERR_UNSUPPORTED,
-                "SLR kernel needs square 16, 32 or 64 blocks, got %dx%d", block_p, block_q);
-  if (M < 0 || m < 0 || NB < 0 || r_pad < 0 || n_chunks < 0 || n_slots < 0 || lr_wgs < 0)
-    return fail(SSL_ERR_INVALID, "negative size");
-  if (r_pad % 64 || m_pad % 64 || m_pad < m)
-    return fail(SSL_ERR_INVALID, "r_pad and m_pad must be multiples of 64 with m_pad >= m");
-  if (M == 0 || NB == 0) return SSL_OK;
-  if (n_chunks == 0) return fail(SSL_ERR_INVALID, "empty plan for a non-empty output");
-  if ((r_pad > 0) != (lr_wgs > 0) || lr_wgs > n_chunks)
-    return fail(SSL_ERR_INVALID, "lr_wgs must count the plan's chunks with low-rank units");
-  const int eb = elem_bytes(dtype);
-  if (!y || !x || !plan || (r_pad > 0 && (!A || !B))) return fail(SSL_ERR_INVALID, "null pointer");
-  if (ldx < m || ldy < NB * block_p) return fail(SSL_ERR_INVALID, "leading dimension smaller than row");
-  if (!aligned(x, 16) || (ldx * eb) % 16) return fail(SSL_ERR_INVALID, "x rows must be 16-byte aligned");
-  if (!aligned(y, 16) || (ldy * eb) % 16) return fail(SSL_ERR_INVALID, "y rows must be 16-byte aligned");
-  if ((A && !aligned(A, 16)) || (B && !aligned(B, 16)) || (values && !aligned(values, 16)))
-    return fail(SSL_ERR_INVALID, "A, B and values must be 16-byte aligned");
-  const Layout L = slr_layout(M, NB, block_p, r_pad, m_pad, n_slots, dtype);
-  if (L.total > 0x7fffffffLL)
-    return fail(SSL_ERR_UNSUPPORTED, "workspace of %lld bytes exceeds 2 GiB; split the call by tokens",
-                (long long)L.total);
-  if (workspace_bytes < L.total || !workspace)
-    return fail(SSL_ERR_WORKSPACE, "workspace of %lld bytes needed", (long long)L.total);
-  if (!aligned(workspace, 256)) return fail(SSL_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  if (n_counters < L.cnt_total || !counters)
-    return fail(SSL_ERR_WORKSPACE, "%lld zeroed counters needed", (long long)L.cnt_total);
-  if (exchange_bytes < 8 * L.n_sync || !exchange)
-    return fail(SSL_ERR_WORKSPACE, "exchange area of %lld bytes needed", (long long)(8 * L.n_sync));
-  if (!aligned(exchange, 256)) return fail(SSL_ERR_WORKSPACE, "exchange area must be 256-byte aligned");
-  int n_kc = 1, ku_chunk = 1;
-  latent_chunks(L, n_chunks * L.MG, &n_kc, &ku_chunk);
-  const int64_t n_lat = (int64_t)L.n_rt * n_kc * L.MG;
-  const int64_t blocks = n_lat + n_chunks * L.MG;
-  if (blocks > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
-  char* ws = (char*)workspace;
-
-  SlrArgs a{};
-  a.x = x; a.ldx = ldx; a.M = (int)M; a.m = (int)m;
-  a.y = y; a.ldy = ldy; a.col = col; a.values = values; a.plan = plan;
-  a.n_chunks = (int)n_chunks; a.NB = (int)NB;
-  a.A = A; a.lda = r_pad; a.bias = bias;
-  a.n_slots = n_slots; a.part_main = (float*)(ws + L.part_main); a.cnt_main = counters;
-  a.B = B; a.ldb = m_pad; a.t = ws + L.t_final; a.ldt = r_pad; a.t_part = (float*)(ws + L.t_part);
-  a.MG = L.MG; a.n_rt = L.n_rt; a.n_kc = n_kc; a.ku_total = L.ku_total; a.ku_chunk = ku_chunk;
-  a.n_lat_wgs = (int)n_lat;
-  a.sync = (u64*)exchange; a.lr_wgs = (int)lr_wgs; a.lat_weight = kLatentUnits / n_kc;
-  return check_hip(dispatch<MODE_FUSED>(dtype, block_p, L.MT, a, blocks, (hipStream_t)stream),
-                   "slr launch");
+  ssl_slr_member mb{};
+  mb.y = y; mb.ldy = ldy; mb.A = A; mb.B = B; mb.bias = bias; mb.col = col; mb.values = values;
+  mb.plan = plan; mb.n_chunks = n_chunks; mb.n_slots = n_slots; mb.lr_wgs = lr_wgs;
+  mb.NB = NB; mb.r_pad = r_pad; mb.counters = counters; mb.n_counters = n_counters;
+  mb.exchange = exchange; mb.exchange_bytes = exchange_bytes;
+  mb.workspace = workspace; mb.workspace_bytes = workspace_bytes;
+  return ssl_slr_forward_group(x, ldx, M, m, m_pad, block_p, block_q, dtype, &mb, 1, stream);
 }
 
 }  // extern "C"

@@ -3,6 +3,7 @@
 Drop-in for the S-SALAAD hot path:
   * torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_  (ssalaad_amd.addmm_inplace)
   * LRSLinear                                              (ssalaad_amd.ls_linear)
+  * LRSLinearGroup: linears sharing an input in one launch (ssalaad_amd.ls_linear)
   * dense_to_bsr / factor_from_svd                         (ssalaad_amd.artifact)
 All compute runs in the HIP kernels of libssalaad_amd.so; there is no CPU path.
 """
@@ -12,10 +13,11 @@ from __future__ import annotations
 from . import _lib
 from .addmm_inplace import SUPPORTED_BLOCK_SIZES, bsr_addmm_inplace_, get_tuned_config
 from .artifact import dense_to_bsr, encode_for_kernels, factor_from_svd
-from .ls_linear import LRSLinear
+from .ls_linear import LRSLinear, LRSLinearGroup
 
 __all__ = [
     "LRSLinear",
+    "LRSLinearGroup",
     "SUPPORTED_BLOCK_SIZES",
     "bsr_addmm_inplace_",
     "dense_to_bsr",

@@ -65,6 +65,28 @@ _SIGNATURES = {
     ),
 }
 
+
+
+class SlrMember(ctypes.Structure):
+    """ssl_slr_member: one linear of a fused (grouped) call."""
+
+    _fields_ = [
+        ("y", _c_p), ("ldy", _c_i64), ("A", _c_p), ("B", _c_p), ("bias", _c_p),
+        ("col", _c_p), ("values", _c_p), ("plan", _c_p), ("n_chunks", _c_i64),
+        ("n_slots", _c_i64), ("lr_wgs", _c_i64), ("NB", _c_i64), ("r_pad", _c_i64),
+        ("counters", _c_p), ("n_counters", _c_i64), ("exchange", _c_p),
+        ("exchange_bytes", _c_i64), ("workspace", _c_p), ("workspace_bytes", _c_i64),
+    ]
+
+
+_SIGNATURES["ssl_slr_forward_group"] = (
+    ctypes.c_int,
+    [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, ctypes.POINTER(SlrMember),
+     _c_i32, _c_p],
+)
+
+MAX_GROUP = 4
+
 _lib = None
 
 

@@ -100,41 +100,65 @@ class _KernelState:
             self._plans[key] = pl
         return pl
 
+    def rows(self, x: torch.Tensor) -> torch.Tensor:
+        """x as [M, ·] with 16-byte aligned rows (copied into a padded buffer if not)."""
+        x2 = x.reshape(-1, x.shape[-1])
+        if x2.stride(-1) != 1 or x2.data_ptr() % 16 or (x2.stride(0) * self.elem) % 16:
+            ld = _round_up(self.m, 16 // self.elem)
+            buf = torch.zeros(x2.shape[0], ld, dtype=x2.dtype, device=x2.device)
+            buf[:, : self.m] = x2
+            x2 = buf
+        return x2
+
     def forward(self, x: torch.Tensor, out_features: int) -> torch.Tensor:
         """y = x·Bᵀ·Aᵀ + x·Sᵀ + b in one fused launch."""
-        m = self.m
-        orig = x.shape
-        x2 = x.reshape(-1, orig[-1])
-        if x2.stride(-1) != 1 or x2.data_ptr() % 16 or (x2.stride(0) * self.elem) % 16:
-            # rows must be 16-byte aligned: copy into a row-padded buffer
-            ld = _round_up(m, 16 // self.elem)
-            buf = torch.zeros(x2.shape[0], ld, dtype=x2.dtype, device=x2.device)
-            buf[:, :m] = x2
-            x2 = buf
-        M = x2.shape[0]
-        y = torch.empty(M, self.n_pad, dtype=x.dtype, device=x.device)
-        if M > 0:
-            pl = self.plan(M)
-            lib = _lib.load()
-            need = lib.ssl_slr_workspace_size(
-                M, self.NB, self.p, self.r_pad, self.m_pad, pl.n_slots, self.dtype_code
-            )
-            ws = _runtime.workspace(x.device, need)
-            cnt = _runtime.counters(x.device, lib.ssl_slr_counter_count(M, self.NB))
-            xch = pl.exchange(lib.ssl_slr_exchange_size(M, self.r_pad, self.m_pad, self.dtype_code))
-            rc = lib.ssl_slr_forward(
-                y.data_ptr(), y.stride(0), x2.data_ptr(), x2.stride(0), self.A.data_ptr(),
-                self.B.data_ptr(), _lib.ptr(self.bias), self.col.data_ptr(),
-                self.values.data_ptr(), pl.table.data_ptr(), pl.n_chunks, pl.n_slots,
-                pl.lr_wgs, M, m, self.m_pad, self.NB, self.r_pad, self.p, self.p,
-                self.dtype_code, cnt.data_ptr(), cnt.numel(), xch.data_ptr(), xch.numel(),
-                ws.data_ptr(), ws.numel(),
-                _lib.stream_ptr(x.device),
-            )
-            _lib.check(rc, "ssl_slr_forward")
-        if self.n_pad != out_features:
-            y = y[:, :out_features]
-        return y.reshape(*orig[:-1], out_features)
+        return _launch([self], x, [out_features])[0]
+
+
+def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[int]):
+    """One fused launch computing every state's linear of the same x."""
+    st0 = states[0]
+    orig = x.shape
+    x2 = st0.rows(x)
+    M = x2.shape[0]
+    ys = [torch.empty(M, st.n_pad, dtype=x.dtype, device=x.device) for st in states]
+    if M > 0:
+        lib = _lib.load()
+        plans = [st.plan(M) for st in states]
+        ws_need = [_round_up(lib.ssl_slr_workspace_size(M, st.NB, st.p, st.r_pad, st.m_pad,
+                                                        pl.n_slots, st.dtype_code), 256)
+                   for st, pl in zip(states, plans)]
+        cnt_need = [lib.ssl_slr_counter_count(M, st.NB) for st in states]
+        ws = _runtime.workspace(x.device, sum(ws_need))
+        cnt = _runtime.counters(x.device, sum(cnt_need))
+        members = (_lib.SlrMember * len(states))()
+        ws_off = cnt_off = 0
+        for i, (st, pl, y) in enumerate(zip(states, plans, ys)):
+            xch = pl.exchange(lib.ssl_slr_exchange_size(M, st.r_pad, st.m_pad, st.dtype_code))
+            mb = members[i]
+            mb.y, mb.ldy = y.data_ptr(), y.stride(0)
+            mb.A, mb.B, mb.bias = st.A.data_ptr(), st.B.data_ptr(), _lib.ptr(st.bias)
+            mb.col, mb.values = st.col.data_ptr(), st.values.data_ptr()
+            mb.plan, mb.n_chunks, mb.n_slots = pl.table.data_ptr(), pl.n_chunks, pl.n_slots
+            mb.lr_wgs, mb.NB, mb.r_pad = pl.lr_wgs, st.NB, st.r_pad
+            mb.counters = cnt.data_ptr() + 4 * cnt_off
+            mb.n_counters = cnt_need[i]
+            mb.exchange, mb.exchange_bytes = xch.data_ptr(), xch.numel()
+            mb.workspace = ws.data_ptr() + ws_off
+            mb.workspace_bytes = ws_need[i]
+            ws_off += ws_need[i]
+            cnt_off += cnt_need[i]
+        rc = lib.ssl_slr_forward_group(
+            x2.data_ptr(), x2.stride(0), M, st0.m, st0.m_pad, st0.p, st0.p, st0.dtype_code,
+            members, len(states), _lib.stream_ptr(x.device),
+        )
+        _lib.check(rc, "ssl_slr_forward_group")
+    outs = []
+    for st, y, n in zip(states, ys, out_features):
+        if st.n_pad != n:
+            y = y[:, :n]
+        outs.append(y.reshape(*orig[:-1], n))
+    return outs
 
 
 def latent_wait_status(device: torch.device) -> int:
@@ -310,3 +334,48 @@ def LRSLinear(
 
         S_sparse = dense_to_bsr(S_sparse, block_p, block_q)
     return _LRSLinearLRBlockHIP(A, B, S_sparse, block_p=block_p, block_q=block_q, **kwargs)
+
+
+class LRSLinearGroup(nn.Module):
+    """Up to four SLR linears that read the same input, computed in ONE launch.
+
+    `LRSLinearGroup(q, k, v)(x)` returns `(q(x), k(x), v(x))`, each computed as
+    its module computes it (same rounding points, same plans), in one fused
+    kernel launch instead of one per module: the latent and row workgroups of
+    every member share the device at once. The reference calls every module
+    on its own (ssalaad/efficient/model.py:41-57); grouping a layer's q/k/v
+    and gate/up projections is this library's launch-count reduction for
+    decode. Members must share in_features, dtype, device and block size.
+    """
+
+    def __init__(self, *linears: _LRSLinearBase) -> None:
+        super().__init__()
+        if not 1 <= len(linears) <= _lib.MAX_GROUP:
+            raise ValueError(f"a group takes 1 to {_lib.MAX_GROUP} linears, got {len(linears)}")
+        for mod in linears:
+            if not isinstance(mod, _LRSLinearBase):
+                raise ValueError("group members must be LRSLinear modules of this library")
+        first = linears[0]
+        for mod in linears[1:]:
+            if mod.in_features != first.in_features:
+                raise ValueError("group members must share in_features (they read the same x)")
+            if mod.A.dtype != first.A.dtype or mod.A.device != first.A.device:
+                raise ValueError("group members must share dtype and device")
+            if mod._kernel_block != first._kernel_block:
+                raise ValueError(
+                    f"group members must share the block size, got {first._kernel_block} and "
+                    f"{mod._kernel_block}"
+                )
+        self.members = nn.ModuleList(linears)
+        self.in_features = first.in_features
+
+    def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, ...]:
+        first = self.members[0]
+        if x.dtype != first.A.dtype:
+            raise TypeError(f"input dtype {x.dtype} does not match the weights' {first.A.dtype}")
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"input has {x.shape[-1]} features, expected {self.in_features}")
+        if x.device != first.A.device:
+            raise ValueError(f"input on {x.device}, weights on {first.A.device}")
+        states = [mod._kernel() for mod in self.members]
+        return tuple(_launch(states, x, [mod.out_features for mod in self.members]))

@@ -195,32 +195,41 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     rc = lib.ssl_bsr_addmm_inplace(16, 64, 16, 64, 16, 16, 16, 1, 0, 1, 64, 64, 1, 64, 64,
                                    _lib.SSL_BF16, None, 0, None, 0, None)
     assert rc == _lib.SSL_ERR_WORKSPACE
-    # bad dtype
-    rc = lib.ssl_slr_forward(1, 64, 1, 64, 1, 1, None, 1, 1, 1, 1, 0, 1, 1, 64, 64, 1, 64, 64,
-                             64, 7, None, 0, None, 0, None, 0, None)
-    assert rc == _lib.SSL_ERR_UNSUPPORTED
-    # lr_wgs inconsistent with r_pad
-    rc = lib.ssl_slr_forward(1, 64, 1, 64, 1, 1, None, 1, 1, 1, 1, 0, 0, 1, 64, 64, 1, 64, 64,
-                             64, _lib.SSL_BF16, None, 0, None, 0, None, 0, None)
-    assert rc == _lib.SSL_ERR_INVALID and b"lr_wgs" in lib.ssl_last_error()
-    # more consuming workgroups than chunks
-    rc = lib.ssl_slr_forward(1, 64, 1, 64, 1, 1, None, 1, 1, 1, 1, 0, 2, 1, 64, 64, 1, 64, 64,
-                             64, _lib.SSL_BF16, None, 0, None, 0, None, 0, None)
-    assert rc == _lib.SSL_ERR_INVALID and b"lr_wgs" in lib.ssl_last_error()
-    # r_pad not a multiple of 64
-    rc = lib.ssl_slr_forward(1, 64, 1, 64, 1, 1, None, 1, 1, 1, 1, 0, 1, 1, 64, 64, 1, 48, 64,
-                             64, _lib.SSL_BF16, None, 0, None, 0, None, 0, None)
+    # ssl_slr_forward with fake, aligned device pointers (every case below is
+    # rejected on the host before any launch)
+    P = 256
+
+    def slr(**kw):
+        a = dict(y=P, ldy=64, x=P, ldx=64, A=P, B=P, bias=None, col=P, values=P, plan=P,
+                 n_chunks=1, n_slots=0, lr_wgs=1, M=1, m=64, m_pad=64, NB=1, r_pad=64, p=64,
+                 q=64, dtype=_lib.SSL_BF16, counters=None, n_counters=0, exchange=None,
+                 exchange_bytes=0, workspace=None, workspace_bytes=0, stream=None)
+        a.update(kw)
+        return lib.ssl_slr_forward(*a.values())
+
+    assert slr(dtype=7) == _lib.SSL_ERR_UNSUPPORTED
+    assert slr(p=48, q=48) == _lib.SSL_ERR_UNSUPPORTED
+    # lr_wgs inconsistent with r_pad, or more consuming workgroups than chunks
+    assert slr(lr_wgs=0) == _lib.SSL_ERR_INVALID and b"lr_wgs" in lib.ssl_last_error()
+    assert slr(lr_wgs=2) == _lib.SSL_ERR_INVALID and b"lr_wgs" in lib.ssl_last_error()
+    # r_pad not a multiple of 64; misaligned x
+    assert slr(r_pad=48) == _lib.SSL_ERR_INVALID
+    assert slr(x=P + 2) == _lib.SSL_ERR_INVALID and b"x rows" in lib.ssl_last_error()
+    # missing workspace / counters / exchange area
+    assert slr(M=16) == _lib.SSL_ERR_WORKSPACE and b"workspace" in lib.ssl_last_error()
+    assert slr(M=16, workspace=P, workspace_bytes=1 << 20) == _lib.SSL_ERR_WORKSPACE
+    assert b"counters" in lib.ssl_last_error()
+    assert slr(M=16, workspace=P, workspace_bytes=1 << 20, counters=P,
+               n_counters=1) == _lib.SSL_ERR_WORKSPACE
+    assert b"exchange" in lib.ssl_last_error()
+    # M = 0 is a no-op
+    assert slr(M=0) == _lib.SSL_OK
+    # the group entry point: 1..4 members
+    members = (_lib.SlrMember * 5)()
+    rc = lib.ssl_slr_forward_group(P, 64, 1, 64, 64, 64, 64, _lib.SSL_BF16, members, 5, None)
+    assert rc == _lib.SSL_ERR_INVALID and b"1 to 4" in lib.ssl_last_error()
+    rc = lib.ssl_slr_forward_group(P, 64, 1, 64, 64, 64, 64, _lib.SSL_BF16, members, 0, None)
     assert rc == _lib.SSL_ERR_INVALID
-    # missing workspace / counters / sync words
-    rc = lib.ssl_slr_forward(16, 64, 16, 64, 16, 16, None, 16, 16, 16, 1, 0, 1, 1, 64, 64, 1, 64,
-                             64, 64, _lib.SSL_BF16, None, 0, None, 0, None, 0, None)
-    assert rc == _lib.SSL_ERR_WORKSPACE
-    rc = lib.ssl_slr_forward(16, 64, 16, 64, 16, 16, None, 16, 16, 16, 1, 0, 1, 1, 64, 64, 1, 64,
-                             64, 64, _lib.SSL_BF16, None, 0, None, 0, 256, 1 << 20, None)
-    assert rc == _lib.SSL_ERR_WORKSPACE and b"counters" in lib.ssl_last_error()
-    rc = lib.ssl_slr_forward(16, 64, 16, 64, 16, 16, None, 16, 16, 16, 1, 0, 1, 1, 64, 64, 1, 64,
-                             64, 64, _lib.SSL_BF16, 256, 1, None, 0, 256, 1 << 20, None)
-    assert rc == _lib.SSL_ERR_WORKSPACE and b"exchange" in lib.ssl_last_error()
     with pytest.raises(ValueError):
         _lib.check(_lib.SSL_ERR_INVALID, "x")
     with pytest.raises(TypeError):

@@ -243,6 +243,81 @@ def test_llama1b_down_proj_ragged_decode(gpu_device):
     assert err(y, oracle_y(prob, x)) <= 1e-2
 
 
+# ----------------------------------------------------- grouped launch --
+
+
+def _group_probs(dtype, specs, m, p, seed):
+    return [make_problem(n, m, r, p, d, dtype, seed=seed + i, skew=(i == 1))
+            for i, (n, r, d) in enumerate(specs)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("M", [1, 5, 16, 40, 100])
+def test_group_matches_oracle_per_member(dtype, M, gpu_device):
+    """q/k/v-like members of different widths and ranks in one launch: each
+    output equals its own oracle, and repeated calls are bit-identical."""
+    probs = _group_probs(dtype, [(256, 64, 0.5), (128, 96, 0.3), (192, 32, 0.7)], 320, 32, 40 + M)
+    mods = [_module(pr, gpu_device) for pr in probs]
+    grp = ssalaad_amd.LRSLinearGroup(*mods)
+    x = make_x(probs[0], M)
+    xt = to_dev(x, dtype, gpu_device)
+    ys = grp(xt)
+    ys2 = grp(xt)
+    torch.cuda.synchronize()
+    assert len(ys) == 3
+    for y, y2, pr in zip(ys, ys2, probs):
+        assert y.shape == (M, pr["n"])
+        assert err(y, oracle_y(pr, x)) <= TOL[dtype]
+        assert torch.equal(y, y2)
+    # members still work on their own, interleaved with the group
+    y0 = mods[0](xt)
+    torch.cuda.synchronize()
+    assert err(y0, oracle_y(probs[0], x)) <= TOL[dtype]
+    assert latent_wait_status(gpu_device) == 0
+
+
+def test_group_with_low_rank_only_and_ragged_members(gpu_device):
+    dev, dtype = gpu_device, torch.bfloat16
+    prob = make_problem(100, 200, 24, 32, 0.5, dtype, seed=3, bias=False, pad=True)
+    rng = np.random.default_rng(4)
+    A = orc.bf16_round(rng.standard_normal((72, 16)) * 0.1).astype(np.float64)
+    B = orc.bf16_round(rng.standard_normal((16, 200)) * 0.1).astype(np.float64)
+    lr = LRSLinear(to_dev(A, dtype, dev), to_dev(B, dtype, dev), torch.zeros(72, 200, device=dev),
+                   in_features=200, out_features=72)
+    sl = _module(prob, dev, bias=False)
+    x = make_x(prob, 7)
+    with pytest.raises(ValueError, match="block size"):
+        ssalaad_amd.LRSLinearGroup(sl, lr)  # 32×32 blocks vs the low-rank-only tile
+    grp = ssalaad_amd.LRSLinearGroup(sl, _module(prob, dev, bias=False))
+    y1, y2 = grp(to_dev(x, dtype, dev).reshape(1, 7, 200))
+    torch.cuda.synchronize()
+    assert y1.shape == (1, 7, 100) and torch.equal(y1, y2)
+    assert err(y1.reshape(7, 100), oracle_y(prob, x)) <= 1e-2
+    y_lr = lr(to_dev(x, dtype, dev))
+    assert err(y_lr, orc.slr_linear(x, A, B, np.zeros((72, 200)))) <= 1e-2
+
+
+def test_group_rejects_mismatched_members(gpu_device):
+    a = _module(make_problem(64, 96, 8, 32, 0.5, torch.bfloat16, seed=1), gpu_device)
+    b = _module(make_problem(64, 128, 8, 32, 0.5, torch.bfloat16, seed=2), gpu_device)
+    with pytest.raises(ValueError, match="in_features"):
+        ssalaad_amd.LRSLinearGroup(a, b)
+    with pytest.raises(ValueError, match="1 to 4"):
+        ssalaad_amd.LRSLinearGroup(a, a, a, a, a)
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_group_llama7b_attention_projections(M, gpu_device):
+    """Full-size q, k, v (4096×4096 bf16, rank 256, 64×64 blocks at 50%) in one launch."""
+    probs = _group_probs(torch.bfloat16, [(4096, 256, 0.5)] * 3, 4096, 64, 70 + M)
+    grp = ssalaad_amd.LRSLinearGroup(*[_module(pr, gpu_device) for pr in probs])
+    x = make_x(probs[0], M)
+    ys = grp(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    for y, pr in zip(ys, probs):
+        assert err(y, oracle_y(pr, x)) <= 1e-2
+
+
 # ------------------------------------------------------------ encoder --
 
 
