@@ -59,10 +59,12 @@ const char* ssl_last_error(void);
  * A plan splits the work of one BSR matrix into workgroup chunks. Each block-row
  * owns its sparse blocks (cost q each) and `lr_units` low-rank units (cost 32
  * each, 32 ranks of A per unit). A row whose cost exceeds `target_cost` is split
- * into k nearly equal chunks; chunk j takes the j-th consecutive share of the
- * row's blocks and the j-th share of its low-rank units. The k partial results
- * are summed in chunk order on the device, so long rows of skewed matrices are
- * spread across workgroups and results stay deterministic. `rows` lists the
+ * into k chunks of nearly equal cost. Without low-rank units chunk j takes the
+ * j-th consecutive share of the row's blocks; with them the row's last chunk
+ * (its finaliser, listed after every other chunk of the table) takes all the
+ * low-rank units and a smaller share of blocks. The k partial results are summed
+ * in chunk order on the device, so long rows of skewed matrices are spread
+ * across workgroups and results stay deterministic. `rows` lists the
  * block-rows that get chunks (NULL = every row 0..NB-1). target_cost <= 0 never
  * splits.
  *
@@ -77,6 +79,29 @@ int ssl_plan_build(const int32_t* crow_host, int64_t NB, const int32_t* rows_hos
                    int32_t* table_out, int64_t table_capacity, int64_t* n_chunks,
                    int64_t* n_slots);
 
+/* Prefill plan (host side, integer only): the row kernels used for calls with
+ * many token rows give one workgroup `group` block-rows at once (group · p =
+ * 256 output columns) and walk the union of their block columns, so each tile
+ * of x feeds every block of that column in the group. Groups are consecutive
+ * runs of `group` listed rows (`rows` NULL = every row 0..NB-1).
+ *   groups  (2 + group) int32 per group:  {entry_begin, entry_end, row_0 .. row_{group-1}}
+ *           (row −1: none; the last group may be short)
+ *   entries (2 + group) int32 per entry:  {col, mask, blk_0 .. blk_{group-1}}
+ *           in ascending column order; bit g of mask is set iff blk_g (the BSR
+ *           block index of slot g's row at that column) is valid (else −1).
+ * A repeated column within one row gets its own entry. Call once with NULL
+ * outputs for the counts. group ∈ [1, 16]. */
+int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB,
+                           const int32_t* rows_host, int64_t n_rows, int32_t group,
+                           int32_t* groups_out, int64_t groups_capacity, int32_t* entries_out,
+                           int64_t entries_capacity, int64_t* n_groups, int64_t* n_entries);
+/* Calls with at least this many token rows and 16-bit activations run the
+ * prefill kernels, which need a prefill plan built with this group size for
+ * the call's M and row count (n_rows: the rows the plans list; for a grouped
+ * call, all its linears' rows together). */
+int64_t ssl_prefill_min_rows(void);
+int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p);
+
 /* -------------------------------------------------------------------------
  * In-place BSR addmm:  out[:, rows of active block-rows] += x · Sᵀ
  *
@@ -89,13 +114,21 @@ int ssl_plan_build(const int32_t* crow_host, int64_t NB, const int32_t* rows_hos
  * stored back in the out dtype. Block-rows without a chunk are not touched.
  * p = q ∈ {16, 32, 64}; dtype ∈ {f32, bf16, f16} for out, x and values alike.
  * `plan` is a device copy of a table from ssl_plan_build (lr_units = 0).
+ * For M >= ssl_prefill_min_rows() with 16-bit dtypes the prefill kernel runs
+ * instead: it needs `pf_groups`/`pf_entries` (device copies from
+ * ssl_prefill_plan_build with the same rows and group = pf_group =
+ * ssl_prefill_group(M, rows, p)) and `values_pq`, the block values in
+ * (nnz, p, q) order (each block transposed); other calls may pass NULL/0 there.
  * ------------------------------------------------------------------------- */
 int64_t ssl_bsr_addmm_workspace_size(int64_t M, int64_t NB, int32_t block_p,
                                      int64_t n_slots);
 int64_t ssl_bsr_addmm_counter_count(int64_t M, int64_t NB);
 int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx,
-                          const int32_t* col, const void* values, const int32_t* plan,
-                          int64_t n_chunks, int64_t n_slots, int64_t M, int64_t N,
+                          const int32_t* col, const void* values, int64_t nnz,
+                          const int32_t* plan, int64_t n_chunks, int64_t n_slots,
+                          const void* values_pq, const int32_t* pf_groups,
+                          const int32_t* pf_entries,
+                          int64_t pf_n_groups, int32_t pf_group, int64_t M, int64_t N,
                           int64_t K, int64_t NB, int32_t block_p, int32_t block_q,
                           int32_t dtype, int32_t* counters, int64_t n_counters,
                           void* workspace, int64_t workspace_bytes, void* stream);
@@ -159,6 +192,14 @@ typedef struct ssl_slr_member {
   int64_t exchange_bytes;
   void* workspace;
   int64_t workspace_bytes;
+  /* prefill plan (ssl_prefill_plan_build with group = ssl_prefill_group(M,
+   * NB, p)): needed when M >= ssl_prefill_min_rows() and dtype is 16-bit */
+  const int32_t* pf_groups;
+  const int32_t* pf_entries;
+  int64_t pf_n_groups;
+  int32_t pf_group;
+  int64_t nnz;            /* stored blocks (length of col, first dim of values) */
+  const void* values_pq;  /* the block values in (nnz, p, q) order, for the prefill kernels */
 } ssl_slr_member;
 
 /* Up to 4 SLR linears that read the same x (e.g. a layer's q, k and v

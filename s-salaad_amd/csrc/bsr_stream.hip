@@ -41,6 +41,7 @@
 // launch it belongs to), so no launch needs an end-of-launch reset.
 
 #include "abi_internal.h"
+#include "prefill.h"
 #include "slr_common.h"
 
 namespace ssl {
@@ -160,42 +161,6 @@ __device__ __forceinline__ typename Mma<DT, KE>::Frag ld_dev_frag(__amdgpu_buffe
   static_assert(sizeof(f) == 16, "fragment image");
   __builtin_memcpy(&f, &u, 16);
   return f;
-}
-
-// ---------------------------------------------------------------------------
-// W adjacent elements in the activation dtype.
-// ---------------------------------------------------------------------------
-template <int DT, int W>
-__device__ __forceinline__ void st_w(void* base, int64_t off, const float (&v)[W]) {
-  if constexpr (DT == DT_F32) {
-    float* p = (float*)base + off;
-    if constexpr (W == 4) *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
-    else if constexpr (W == 2) *(float2*)p = make_float2(v[0], v[1]);
-    else p[0] = v[0];
-  } else {
-    uint16_t* p = (uint16_t*)base + off;
-    if constexpr (W == 1) {
-      p[0] = (uint16_t)to_bits<DT>(v[0]);
-    } else {
-      uint32_t w[W / 2];
-#pragma unroll
-      for (int i = 0; i < W / 2; ++i) w[i] = to_bits<DT>(v[2 * i]) | (to_bits<DT>(v[2 * i + 1]) << 16);
-      if constexpr (W == 4) *(uint2*)p = make_uint2(w[0], w[1]);
-      else *(uint32_t*)p = w[0];
-    }
-  }
-}
-template <int DT, int W>
-__device__ __forceinline__ void ld_w(const void* base, int64_t off, float (&v)[W]) {
-  if constexpr (DT == DT_F32) {
-    const float* p = (const float*)base + off;
-#pragma unroll
-    for (int s = 0; s < W; ++s) v[s] = p[s];
-  } else {
-    const uint16_t* p = (const uint16_t*)base + off;
-#pragma unroll
-    for (int s = 0; s < W; ++s) v[s] = (DT == DT_BF16) ? bf16_to_f32(p[s]) : f16_to_f32(p[s]);
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -801,7 +766,13 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   const int64_t rows = (int64_t)L.MG * 16 * L.MT;
   int64_t off = 0;
   L.t_part = off;
-  if (L.n_kc_max > 1) off = align_up(off + 4 * (int64_t)L.n_kc_max * rows * r_pad, 256);
+  if (M >= kPrefillMinM && dtype != SSL_F32) {
+    // prefill: the latent GEMM's K-split partials
+    const int ks = prefill_latent_split(M, r_pad, m_pad, device_cus());
+    if (ks > 1) off = align_up(off + 4 * (int64_t)ks * rows * r_pad, 256);
+  } else if (L.n_kc_max > 1) {
+    off = align_up(off + 4 * (int64_t)L.n_kc_max * rows * r_pad, 256);
+  }
   L.t_final = off;
   off = align_up(off + (int64_t)elem_bytes(dtype) * rows * r_pad, 256);
   L.part_main = off;
@@ -833,6 +804,13 @@ using namespace ssl;
 
 extern "C" {
 
+int64_t ssl_prefill_min_rows(void) { return kPrefillMinM; }
+
+int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p) {
+  if (!supported_block(block_p, block_p)) return 1;
+  return prefill_group(M, n_rows, block_p, device_cus());
+}
+
 int64_t ssl_bsr_addmm_counter_count(int64_t M, int64_t NB) {
   const int MT = tile_mt(M);
   const int64_t MG = (M + 16 * MT - 1) / (16 * MT);
@@ -847,11 +825,13 @@ int64_t ssl_bsr_addmm_workspace_size(int64_t M, int64_t NB, int32_t block_p, int
 }
 
 int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, const int32_t* col,
-                          const void* values, const int32_t* plan, int64_t n_chunks,
-                          int64_t n_slots, int64_t M, int64_t N, int64_t K, int64_t NB,
-                          int32_t block_p, int32_t block_q, int32_t dtype, int32_t* counters,
-                          int64_t n_counters, void* workspace, int64_t workspace_bytes,
-                          void* stream) {
+                          const void* values, int64_t nnz, const int32_t* plan, int64_t n_chunks,
+                          int64_t n_slots, const void* values_pq, const int32_t* pf_groups,
+                          const int32_t* pf_entries,
+                          int64_t pf_n_groups, int32_t pf_group, int64_t M, int64_t N, int64_t K,
+                          int64_t NB, int32_t block_p, int32_t block_q, int32_t dtype,
+                          int32_t* counters, int64_t n_counters, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
   clear_error();
   if (!supported_dtype(dtype)) return fail(SSL_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
   if (!supported_block(block_p, block_q))
@@ -879,6 +859,31 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
   if (n_counters < ssl_bsr_addmm_counter_count(M, NB) || !counters)
     return fail(SSL_ERR_WORKSPACE, "%lld zeroed counters needed",
                 (long long)ssl_bsr_addmm_counter_count(M, NB));
+
+  if (M >= kPrefillMinM && dtype != SSL_F32) {
+    if (!pf_groups || !pf_entries || pf_n_groups <= 0 || !values_pq)
+      return fail(SSL_ERR_INVALID, "calls with %lld token rows need a prefill plan and (p, q) "
+                  "ordered block values", (long long)M);
+    if (pf_group != prefill_group(M, n_chunks, block_p, device_cus()))
+      return fail(SSL_ERR_INVALID, "prefill plan built for group %d, this call needs %d", pf_group,
+                  prefill_group(M, n_chunks, block_p, device_cus()));
+    if (nnz < 0 || nnz * block_p * block_q * eb > 0x7fffffffLL)
+      return fail(SSL_ERR_UNSUPPORTED, "block values beyond 2 GiB");
+    PfArgs rows{};
+    rows.x = x; rows.ldx = ldx; rows.M = (int)M; rows.m = (int)K; rows.m_pad = (int)K;
+    rows.mode = PF_OP;
+    rows.n = 1;
+    PfMember& pm = rows.mb[0];
+    pm.y = out; pm.ldy = ldo; pm.values_pq = values_pq;
+    pm.values_bytes = nnz * block_p * block_q * eb;
+    pm.groups = pf_groups; pm.entries = pf_entries; pm.n_groups = (int)pf_n_groups;
+    const int64_t T = (M + prefill_row_tile(pf_group) - 1) / prefill_row_tile(pf_group);
+    if (pf_n_groups * T > 0x7fffffffLL / 8) return fail(SSL_ERR_INVALID, "grid too large");
+    rows.items = (int)(pf_n_groups * T);
+    rows.off[1] = rows.items;
+    return check_hip(prefill_launch_op(dtype, block_p, pf_group, rows, (hipStream_t)stream),
+                     "bsr_addmm prefill launch");
+  }
 
   GroupArgs g{};
   g.n = 1;
@@ -970,6 +975,71 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
     rt_tiles += (int64_t)L[i].n_rt * L[i].MG;
   }
   if (n_stream == 0) return SSL_OK;
+
+  if (M >= kPrefillMinM && dtype != SSL_F32) {
+    // Many token rows: the latent GEMM (K split, then combined), then the row
+    // GEMM over groups of block-rows.
+    const int cus = device_cus();
+    PfArgs rows{}, lat{};
+    rows.x = lat.x = x; rows.ldx = lat.ldx = ldx;
+    rows.M = lat.M = (int)M; rows.m = lat.m = (int)m; rows.m_pad = lat.m_pad = (int)m_pad;
+    rows.rows = lat.rows = (int)((M + 63) / 64 * 64);
+    rows.mode = PF_FUSED;
+    rows.n = lat.n = n_members;
+    const int64_t T64 = (M + 63) / 64;
+    // one group size for the whole call, from all members' rows together
+    int64_t total_rows = 0;
+    for (int i = 0; i < n_members; ++i)
+      if (members[i].NB > 0) total_rows += members[i].n_chunks;
+    const int G = prefill_group(M, total_rows, block_p, cus);
+    int64_t items = 0, litems = 0;
+    for (int i = 0; i < n_members; ++i) {
+      const ssl_slr_member& mb = members[i];
+      PfMember& pm = rows.mb[i];
+      rows.off[i] = (int)items;
+      lat.off[i] = (int)litems;
+      if (mb.NB == 0) continue;
+      if (!mb.pf_groups || !mb.pf_entries || mb.pf_n_groups <= 0 || mb.pf_group != G ||
+          (mb.nnz > 0 && !mb.values_pq))
+        return fail(SSL_ERR_INVALID, "linear %d: calls with %lld token rows need a prefill plan "
+                    "with group %d and (p, q) ordered block values", i, (long long)M, G);
+      const int64_t T = (M + prefill_row_tile(G) - 1) / prefill_row_tile(G);
+      if (mb.nnz < 0 || mb.nnz * block_p * block_p * eb > 0x7fffffffLL ||
+          mb.NB * block_p * mb.r_pad * eb > 0x7fffffffLL)
+        return fail(SSL_ERR_UNSUPPORTED, "linear %d: weights beyond 2 GiB", i);
+      pm.y = mb.y; pm.ldy = mb.ldy; pm.A = mb.A; pm.lda = mb.r_pad;
+      pm.A_bytes = mb.NB * block_p * mb.r_pad * eb; pm.bias = mb.bias;
+      pm.values_pq = mb.values_pq; pm.values_bytes = mb.nnz * block_p * block_p * eb;
+      pm.groups = mb.pf_groups; pm.entries = mb.pf_entries; pm.n_groups = (int)mb.pf_n_groups;
+      pm.B = mb.B; pm.ldb = m_pad;
+      pm.t = (char*)mb.workspace + L[i].t_final; pm.ldt = mb.r_pad;
+      pm.tpart = (float*)((char*)mb.workspace + L[i].t_part);
+      pm.r_pad = (int)mb.r_pad;
+      pm.ksplit = mb.r_pad > 0 ? prefill_latent_split(M, mb.r_pad, m_pad, cus) : 1;
+      lat.mb[i] = pm;
+      items += mb.pf_n_groups * T;
+      if (mb.r_pad > 0) litems += T64 * (mb.r_pad / 64) * pm.ksplit;
+      if (items > 0x7fffffffLL / 8 || litems > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
+    }
+    rows.off[n_members] = (int)items;
+    lat.off[n_members] = (int)litems;
+    rows.items = (int)items;
+    lat.items = (int)litems;
+    // combine workgroups (members with a split latent), offsets in member order
+    PfArgs comb = lat;
+    {
+      int64_t c = 0;
+      for (int i = 0; i < n_members; ++i) {
+        comb.off[i] = (int)c;
+        if (members[i].NB > 0 && members[i].r_pad > 0 && lat.mb[i].ksplit > 1)
+          c += (rows.rows * members[i].r_pad / 4 + 255) / 256;
+      }
+      comb.off[n_members] = (int)c;
+      comb.combine_items = (int)c;
+    }
+    return check_hip(prefill_launch_fused(dtype, block_p, G, rows, lat, comb, (hipStream_t)stream),
+                     "slr prefill launch");
+  }
 
   // One K split for the whole launch: latent and row workgroups of every
   // member resident at once.

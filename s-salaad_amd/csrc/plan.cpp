@@ -17,7 +17,10 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
+#include <array>
 #include <string>
+#include <vector>
 
 #include "abi_internal.h"
 
@@ -137,6 +140,79 @@ int ssl_plan_build(const int32_t* crow_host, int64_t NB, const int32_t* rows_hos
   }
   *n_chunks = chunks;
   *n_slots = slots;
+  return SSL_OK;
+}
+
+int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB,
+                           const int32_t* rows_host, int64_t n_rows, int32_t group,
+                           int32_t* groups_out, int64_t groups_capacity, int32_t* entries_out,
+                           int64_t entries_capacity, int64_t* n_groups, int64_t* n_entries) {
+  clear_error();
+  if (!crow_host || !n_groups || !n_entries || NB < 0 || group < 1 || group > 16)
+    return fail(SSL_ERR_INVALID, "invalid prefill plan arguments");
+  if (crow_host[0] != 0) return fail(SSL_ERR_INVALID, "crow[0] must be 0");
+  for (int64_t b = 0; b < NB; ++b)
+    if (crow_host[b + 1] < crow_host[b]) return fail(SSL_ERR_INVALID, "crow must be non-decreasing");
+  if (crow_host[NB] > 0 && !col_host) return fail(SSL_ERR_INVALID, "col indices needed");
+  const int64_t nr = rows_host ? n_rows : NB;
+  int64_t prev = -1;
+  for (int64_t i = 0; i < nr; ++i) {
+    const int64_t by = rows_host ? rows_host[i] : i;
+    if (by < 0 || by >= NB) return fail(SSL_ERR_INVALID, "row %lld out of range", (long long)by);
+    if (by <= prev) return fail(SSL_ERR_INVALID, "rows must be strictly ascending");
+    prev = by;
+  }
+  const int stride = 2 + group;
+  int64_t ng = 0, ne = 0;
+  std::vector<std::array<int32_t, 3>> items;  // (col, slot, block)
+  for (int64_t i0 = 0; i0 < nr; i0 += group) {
+    items.clear();
+    int32_t rows[16];
+    for (int g = 0; g < group; ++g) {
+      rows[g] = -1;
+      if (i0 + g < nr) {
+        const int32_t by = rows_host ? rows_host[i0 + g] : (int32_t)(i0 + g);
+        rows[g] = by;
+        for (int32_t k = crow_host[by]; k < crow_host[by + 1]; ++k)
+          items.push_back({col_host[k], g, k});
+      }
+    }
+    // merge by column; a slot already taken in the current entry (a repeated
+    // column within one row) starts a new entry with the same column
+    std::sort(items.begin(), items.end());
+    const int64_t e_begin = ne;
+    int32_t cur_col = -1, mask = 0;
+    int32_t* e = nullptr;
+    for (const auto& it : items) {
+      if (it[0] != cur_col || (mask >> it[1]) & 1) {
+        if (entries_out) {
+          if (ne >= entries_capacity) return fail(SSL_ERR_CAPACITY, "prefill entry capacity exceeded");
+          e = entries_out + ne * stride;
+          e[0] = it[0];
+          e[1] = 0;
+          for (int g = 0; g < group; ++g) e[2 + g] = -1;
+        }
+        ++ne;
+        cur_col = it[0];
+        mask = 0;
+      }
+      mask |= 1 << it[1];
+      if (e) {
+        e[1] = mask;
+        e[2 + it[1]] = it[2];
+      }
+    }
+    if (groups_out) {
+      if (ng >= groups_capacity) return fail(SSL_ERR_CAPACITY, "prefill group capacity exceeded");
+      int32_t* gr = groups_out + ng * stride;
+      gr[0] = (int32_t)e_begin;
+      gr[1] = (int32_t)ne;
+      for (int g = 0; g < group; ++g) gr[2 + g] = rows[g];
+    }
+    ++ng;
+  }
+  *n_groups = ng;
+  *n_entries = ne;
   return SSL_OK;
 }
 

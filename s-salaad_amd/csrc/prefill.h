@@ -1,0 +1,66 @@
+// Prefill-shaped SLR kernels (many token rows, 16-bit activations): the host
+// interface between the C-ABI entry points and csrc/prefill.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ssl {
+
+// Calls with at least this many token rows (and 16-bit activations) take the
+// LDS-tiled prefill kernels; fewer rows take the row-streaming decode kernel.
+constexpr int64_t kPrefillMinM = 128;
+
+enum : int { PF_OP = 0, PF_FUSED = 1 };
+
+struct PfMember {
+  void* y;
+  int64_t ldy;
+  const void* A;        // [NB·p][r_pad]
+  int64_t lda;
+  int64_t A_bytes;
+  const void* bias;
+  const void* values_pq;  // the block values in (nnz, p, q) order (k-contiguous per column)
+  int64_t values_bytes;
+  const int32_t* groups;   // prefill plan: (2 + G) int32 per group
+  const int32_t* entries;  // prefill plan: (2 + G) int32 per union column
+  int n_groups;
+  const void* B;        // [r_pad][m_pad]
+  int64_t ldb;
+  void* t;              // latent [rows][r_pad], activation dtype
+  int64_t ldt;
+  float* tpart;         // latent split partials [ksplit][rows][r_pad], fp32
+  int r_pad;
+  int ksplit;           // latent: K splits of this member
+};
+
+struct PfArgs {
+  const void* x;
+  int64_t ldx;
+  int M, m, m_pad;
+  int rows;             // latent rows: roundup(M, 64)
+  int mode;             // PF_OP: y += x·Sᵀ on planned rows; PF_FUSED: the SLR linear
+  int n;                // members
+  int items;            // workgroups that do work
+  int combine_items;    // latent combine: workgroups
+  int off[5];           // first item of each member
+  PfMember mb[4];
+};
+
+// Block-rows per row-kernel workgroup: 256 / p when that still gives every CU
+// a workgroup, else 1.
+int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus);
+// Token rows per row-kernel workgroup for that group size (128 or 64).
+int prefill_row_tile(int group);
+// K splits of the latent GEMM (about two workgroups per CU, ≥ 4 units each, ≤ 16).
+int prefill_latent_split(int64_t M, int64_t r_pad, int64_t m_pad, int n_cus);
+
+// The fused SLR linear: the latent GEMM (`lat`, K split over lat.ksplit), its
+// combine (`comb`, when split) and the row GEMM (`rows`), in that order on
+// `stream`. dtype: SSL_BF16 or SSL_F16; P ∈ {16, 32, 64}; G = 1 or 256/P.
+hipError_t prefill_launch_fused(int dtype, int P, int G, const PfArgs& rows, const PfArgs& lat,
+                                const PfArgs& comb, hipStream_t stream);
+// The in-place op: the row GEMM only (rows.mode = PF_OP).
+hipError_t prefill_launch_op(int dtype, int P, int G, const PfArgs& rows, hipStream_t stream);
+
+}  // namespace ssl

@@ -294,18 +294,42 @@ __device__ __forceinline__ typename Mma<DT, KE>::Frag vfrag(const VRawT<DT, KE, 
   return f;
 }
 
-// ---------------------------------------------------------------------------
-// Memory-model helpers (agent scope: visible across all XCDs of the device).
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void fence_agent() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent"); }
-
-__device__ __forceinline__ int atomic_inc_agent(int* p) {
-  return __hip_atomic_fetch_add(p, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void atomic_store_agent(int* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 __device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// ---------------------------------------------------------------------------
+// W adjacent elements in the activation dtype.
+// ---------------------------------------------------------------------------
+template <int DT, int W>
+__device__ __forceinline__ void st_w(void* base, int64_t off, const float (&v)[W]) {
+  if constexpr (DT == DT_F32) {
+    float* p = (float*)base + off;
+    if constexpr (W == 4) *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+    else if constexpr (W == 2) *(float2*)p = make_float2(v[0], v[1]);
+    else p[0] = v[0];
+  } else {
+    uint16_t* p = (uint16_t*)base + off;
+    if constexpr (W == 1) {
+      p[0] = (uint16_t)to_bits<DT>(v[0]);
+    } else {
+      uint32_t w[W / 2];
+#pragma unroll
+      for (int i = 0; i < W / 2; ++i) w[i] = to_bits<DT>(v[2 * i]) | (to_bits<DT>(v[2 * i + 1]) << 16);
+      if constexpr (W == 4) *(uint2*)p = make_uint2(w[0], w[1]);
+      else *(uint32_t*)p = w[0];
+    }
+  }
+}
+template <int DT, int W>
+__device__ __forceinline__ void ld_w(const void* base, int64_t off, float (&v)[W]) {
+  if constexpr (DT == DT_F32) {
+    const float* p = (const float*)base + off;
+#pragma unroll
+    for (int s = 0; s < W; ++s) v[s] = p[s];
+  } else {
+    const uint16_t* p = (const uint16_t*)base + off;
+#pragma unroll
+    for (int s = 0; s < W; ++s) v[s] = (DT == DT_BF16) ? bf16_to_f32(p[s]) : f16_to_f32(p[s]);
+  }
+}
 
 }  // namespace ssl

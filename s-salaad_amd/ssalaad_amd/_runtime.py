@@ -75,6 +75,45 @@ def build_plan(
     return table[: n_chunks.value], int(n_chunks.value), int(n_slots.value)
 
 
+def build_prefill_plan(
+    crow_host: np.ndarray, col_host: np.ndarray, rows_host: np.ndarray | None, group: int
+) -> tuple[np.ndarray, np.ndarray, int]:
+    """Group table [n_groups, 2 + group] and union-column entries [n_entries, 2 + group]
+    (int32) for the prefill row kernel (ssl_prefill_plan_build)."""
+    lib = _lib.load()
+    crow_host = np.ascontiguousarray(crow_host, dtype=np.int32)
+    col_host = np.ascontiguousarray(col_host, dtype=np.int32)
+    NB = crow_host.shape[0] - 1
+    rows_p, n_rows = None, 0
+    if rows_host is not None:
+        rows_host = np.ascontiguousarray(rows_host, dtype=np.int32)
+        rows_p, n_rows = rows_host.ctypes.data, rows_host.shape[0]
+    ng, ne = ctypes.c_int64(), ctypes.c_int64()
+    args = (crow_host.ctypes.data, col_host.ctypes.data if col_host.size else None, NB, rows_p,
+            n_rows, group)
+    rc = lib.ssl_prefill_plan_build(*args, None, 0, None, 0, ctypes.byref(ng), ctypes.byref(ne))
+    _lib.check(rc, "ssl_prefill_plan_build")
+    groups = np.zeros((max(ng.value, 1), 2 + group), dtype=np.int32)
+    entries = np.zeros((max(ne.value, 1), 2 + group), dtype=np.int32)
+    rc = lib.ssl_prefill_plan_build(*args, groups.ctypes.data, groups.shape[0], entries.ctypes.data,
+                                    entries.shape[0], ctypes.byref(ng), ctypes.byref(ne))
+    _lib.check(rc, "ssl_prefill_plan_build")
+    return groups, entries, int(ng.value)
+
+
+class DevicePrefillPlan:
+    """A prefill plan (group table and union-column entries) on one device."""
+
+    __slots__ = ("groups", "entries", "n_groups", "group")
+
+    def __init__(self, groups: np.ndarray, entries: np.ndarray, n_groups: int, group: int,
+                 device: torch.device):
+        self.groups = torch.from_numpy(groups).to(device)
+        self.entries = torch.from_numpy(entries).to(device)
+        self.n_groups = n_groups
+        self.group = group
+
+
 _PLANS: "weakref.WeakSet[DevicePlan]" = weakref.WeakSet()
 
 

@@ -94,7 +94,35 @@ def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_by
         table, n_chunks, n_slots = _runtime.build_plan(crow_h, act_h, block_q, 0, target)
         plan = _runtime.DevicePlan(table, n_chunks, n_slots, crow.device)
         sp.plans[target_key] = plan
-    return plan
+    pf = None
+    lib = _lib.load()
+    if M >= lib.ssl_prefill_min_rows() and elem_bytes == 2 and plan.n_chunks > 0:
+        # the prefill kernel's groups list the planned rows (active rows with blocks)
+        G = int(lib.ssl_prefill_group(M, plan.n_chunks, block_p))
+        pf = sp.plans.get(("pf", G))
+        if pf is None:
+            crow_h, _ = _validated_host_structure(crow, col, active_rows, values.shape[0], NB_K)
+            col_h = col.detach().to("cpu").numpy().astype(np.int32)
+            rows_h = plan.table.cpu().numpy()[: plan.n_chunks, 0].astype(np.int32)
+            groups, entries, ng = _runtime.build_prefill_plan(crow_h, col_h, rows_h, G)
+            pf = _runtime.DevicePrefillPlan(groups, entries, ng, G, crow.device)
+            sp.plans[("pf", G)] = pf
+    return plan, pf
+
+
+_VPQ_ATTR = "_ssl_values_pq"
+
+
+def _values_pq(values: torch.Tensor, vals: torch.Tensor) -> torch.Tensor:
+    """The blocks in (nnz, p, q) order for the prefill kernel, cached on the
+    values tensor while its data pointer and version stay the same."""
+    key = (values.data_ptr(), values._version)
+    hit = getattr(values, _VPQ_ATTR, None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    vpq = vals.transpose(1, 2).contiguous()
+    setattr(values, _VPQ_ATTR, (key, vpq))
+    return vpq
 
 
 def _aligned_rows(t: torch.Tensor) -> bool:
@@ -147,8 +175,8 @@ def bsr_addmm_inplace_(
     NB_K = K // block_q
     if M == 0 or values.shape[0] == 0 or active_rows.numel() == 0:
         return
-    plan = _plan_for(crow_indices, col_indices, active_rows, values, NB_K, block_p, block_q,
-                     M, out_inplace.element_size())
+    plan, pf = _plan_for(crow_indices, col_indices, active_rows, values, NB_K, block_p, block_q,
+                         M, out_inplace.element_size())
     if plan.n_chunks == 0:
         return
     if not _aligned_rows(x):
@@ -166,9 +194,13 @@ def bsr_addmm_inplace_(
     with torch.cuda.device(dev):
         ws = _runtime.workspace(dev, lib.ssl_bsr_addmm_workspace_size(M, NB, block_p, plan.n_slots))
         cnt = _runtime.counters(dev, lib.ssl_bsr_addmm_counter_count(M, NB))
+        vals_pq = _values_pq(values, vals) if pf else None
         rc = lib.ssl_bsr_addmm_inplace(
             target.data_ptr(), target.stride(0), x.data_ptr(), x.stride(0), col.data_ptr(),
-            vals.data_ptr(), plan.table.data_ptr(), plan.n_chunks, plan.n_slots, M, N, K, NB,
+            vals.data_ptr(), vals.shape[0], plan.table.data_ptr(), plan.n_chunks, plan.n_slots,
+            vals_pq.data_ptr() if pf else None,
+            pf.groups.data_ptr() if pf else None, pf.entries.data_ptr() if pf else None,
+            pf.n_groups if pf else 0, pf.group if pf else 0, M, N, K, NB,
             block_p, block_q, dt, cnt.data_ptr(), cnt.numel(), ws.data_ptr(), ws.numel(),
             _lib.stream_ptr(dev),
         )
@@ -177,8 +209,8 @@ def bsr_addmm_inplace_(
         out_inplace.copy_(target)
 
 
-# Same library name, op name and schema as addmm_inplace.py:130-136. A FRAGMENT
-# keeps the namespace open for the fused op registered in ops.py.
+# Same library name, op name and schema as addmm_inplace.py:130-136, in a
+# FRAGMENT of the "ssalaad" namespace.
 _lib_frag = torch.library.Library("ssalaad", "FRAGMENT")
 _lib_frag.define(
     "tilelang_bsr_addmm_inplace_dense_(Tensor(a!) out_inplace, Tensor x, "

@@ -69,16 +69,20 @@ class _KernelState:
             self.col = mod.S_col
             self.values = mod.S_values
             crow_h = mod.S_crow.detach().to("cpu").numpy().astype(np.int32)
+            self.col_h = mod.S_col.detach().to("cpu").numpy().astype(np.int32)
             self.nblk_total = int(crow_h[-1])
         else:
             self.col = torch.zeros(1, dtype=torch.int32, device=device)
             self.values = torch.zeros(16, dtype=dtype, device=device)
             crow_h = np.zeros(self.NB + 1, dtype=np.int32)
+            self.col_h = np.zeros(0, dtype=np.int32)
             self.nblk_total = 0
         self.crow_h = crow_h
         self.lr_units = self.r_pad // 32
         self.block_q = p
         self._plans: dict[int, _runtime.DevicePlan] = {}
+        self._pf_plans: dict[int, _runtime.DevicePrefillPlan] = {}
+        self._values_pq: torch.Tensor | None = None
 
     def _padded(self, t: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
         if t.shape == (rows, cols) and t.is_contiguous() and t.data_ptr() % 16 == 0:
@@ -99,6 +103,22 @@ class _KernelState:
             pl = _runtime.DevicePlan(table, n_chunks, n_slots, self.device)
             self._plans[key] = pl
         return pl
+
+    def takes_prefill(self, M: int) -> bool:
+        lib = _lib.load()
+        return M >= lib.ssl_prefill_min_rows() and self.dtype_code != _lib.SSL_F32
+
+    def prefill_plan(self, G: int) -> _runtime.DevicePrefillPlan:
+        """The prefill row kernel's plan with G block-rows per workgroup."""
+        pp = self._pf_plans.get(G)
+        if pp is None:
+            groups, entries, ng = _runtime.build_prefill_plan(self.crow_h, self.col_h, None, G)
+            pp = _runtime.DevicePrefillPlan(groups, entries, ng, G, self.device)
+            self._pf_plans[G] = pp
+        if self._values_pq is None and self.nblk_total > 0:
+            # the prefill kernels read each block k-contiguous per output column
+            self._values_pq = self.values.transpose(1, 2).contiguous()
+        return pp
 
     def rows(self, x: torch.Tensor) -> torch.Tensor:
         """x as [M, ·] with 16-byte aligned rows (copied into a padded buffer if not)."""
@@ -133,6 +153,9 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
         cnt = _runtime.counters(x.device, sum(cnt_need))
         members = (_lib.SlrMember * len(states))()
         ws_off = cnt_off = 0
+        G = 0
+        if st0.takes_prefill(M):
+            G = int(lib.ssl_prefill_group(M, sum(st.NB for st in states), st0.p))
         for i, (st, pl, y) in enumerate(zip(states, plans, ys)):
             xch = pl.exchange(lib.ssl_slr_exchange_size(M, st.r_pad, st.m_pad, st.dtype_code))
             mb = members[i]
@@ -146,6 +169,12 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
             mb.exchange, mb.exchange_bytes = xch.data_ptr(), xch.numel()
             mb.workspace = ws.data_ptr() + ws_off
             mb.workspace_bytes = ws_need[i]
+            mb.nnz = st.nblk_total
+            if G:
+                pp = st.prefill_plan(G)
+                mb.pf_groups, mb.pf_entries = pp.groups.data_ptr(), pp.entries.data_ptr()
+                mb.pf_n_groups, mb.pf_group = pp.n_groups, pp.group
+                mb.values_pq = _lib.ptr(st._values_pq)
             ws_off += ws_need[i]
             cnt_off += cnt_need[i]
         rc = lib.ssl_slr_forward_group(

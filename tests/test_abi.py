@@ -145,6 +145,49 @@ def test_plan_rejects_bad_structures():
         _plan([0, 1, 2], rows=[2])
 
 
+def _pf_plan(crow, col, rows=None, group=4):
+    return _runtime.build_prefill_plan(np.asarray(crow, np.int32), np.asarray(col, np.int32),
+                                       None if rows is None else np.asarray(rows, np.int32), group)
+
+
+def test_prefill_plan_merges_each_groups_columns():
+    """Every block of every listed row appears exactly once, in its row's slot,
+    entries of a group ascend by column, and masks match the slots present."""
+    rng = np.random.default_rng(1)
+    NB, NBK = 23, 17
+    counts = rng.integers(0, NBK + 1, NB)
+    crow = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    col = np.concatenate([np.sort(rng.choice(NBK, c, replace=False)) for c in counts]).astype(np.int32)
+    for rows in (None, [0, 2, 3, 7, 11, 12, 20, 22]):
+        for G in (1, 4, 8, 16):
+            groups, entries, ng = _pf_plan(crow, col, rows, G)
+            listed = list(range(NB)) if rows is None else rows
+            assert ng == -(-len(listed) // G)
+            seen = []
+            for gi in range(ng):
+                e0, e1 = groups[gi, 0], groups[gi, 1]
+                grows = groups[gi, 2:]
+                assert list(grows[grows >= 0]) == listed[gi * G:(gi + 1) * G]
+                cols = entries[e0:e1, 0]
+                assert np.all(np.diff(cols) > 0)
+                for c, mask, *blks in entries[e0:e1]:
+                    for g in range(G):
+                        b = blks[g]
+                        assert ((mask >> g) & 1) == (b >= 0)
+                        if b >= 0:
+                            assert crow[grows[g]] <= b < crow[grows[g] + 1] and col[b] == c
+                            seen.append(b)
+            want = [b for r in listed for b in range(crow[r], crow[r + 1])]
+            assert sorted(seen) == sorted(want)
+
+
+def test_prefill_plan_repeated_column_gets_its_own_entry():
+    crow, col = [0, 3], [5, 5, 2]
+    groups, entries, ng = _pf_plan(crow, col, None, 1)
+    assert ng == 1 and [tuple(e[:3]) for e in entries[groups[0, 0]:groups[0, 1]]] == \
+        [(2, 1, 2), (5, 1, 0), (5, 1, 1)]
+
+
 def test_plan_target_cost_policy():
     assert _runtime.plan_target_cost(10**6, 64, 2, M=65) == 0  # several token tiles: no split
     # rows are split beyond 512 KiB of weights: 4096 cost units of a 64-row bf16 block
@@ -165,7 +208,9 @@ def test_workspace_sizes_are_aligned_and_monotone():
     # ([MG][slots][16·MT][p]); each part 256-byte aligned
     assert a == 8 * 16 * 256 * 4 + 16 * 256 * 2
     assert b == a + 100 * 16 * 64 * 4
-    assert c == 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4
+    # 2048 rows take the prefill kernels: the latent GEMM's K-split fp32
+    # partials (4 splits on a 256-CU device, the count assumed without a GPU)
+    assert c == 4 * 2048 * 256 * 4 + 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4
     # counters: one per (token tile, block-row)
     assert lib.ssl_slr_counter_count(16, 172) == 172
     assert lib.ssl_slr_counter_count(2048, 172) == 32 * 172
@@ -183,18 +228,28 @@ def test_workspace_sizes_are_aligned_and_monotone():
 
 def test_entry_points_reject_bad_arguments_before_any_launch():
     lib = _lib.load()
+    P = 256
+
+    def op(**kw):
+        a = dict(out=P, ldo=64, x=P, ldx=64, col=P, values=P, nnz=1, plan=P, n_chunks=1, n_slots=0,
+                 values_pq=None, pf_groups=None, pf_entries=None, pf_n_groups=0, pf_group=0, M=1, N=64, K=64, NB=1,
+                 p=64, q=64, dtype=_lib.SSL_BF16, counters=None, n_counters=0, workspace=None,
+                 workspace_bytes=0, stream=None)
+        a.update(kw)
+        return lib.ssl_bsr_addmm_inplace(*a.values())
+
     # unsupported block shape
-    rc = lib.ssl_bsr_addmm_inplace(1, 64, 1, 64, 1, 1, 1, 1, 0, 1, 64, 64, 1, 8, 8,
-                                   _lib.SSL_BF16, None, 0, None, 0, None)
-    assert rc == _lib.SSL_ERR_UNSUPPORTED and b"square" in lib.ssl_last_error()
+    assert op(p=8, q=8, N=8, K=8) == _lib.SSL_ERR_UNSUPPORTED and b"square" in lib.ssl_last_error()
     # N inconsistent with NB·p
-    rc = lib.ssl_bsr_addmm_inplace(1, 64, 1, 64, 1, 1, 1, 1, 0, 1, 60, 64, 1, 64, 64,
-                                   _lib.SSL_BF16, None, 0, None, 0, None)
-    assert rc == _lib.SSL_ERR_INVALID
+    assert op(N=60) == _lib.SSL_ERR_INVALID
     # missing counters
-    rc = lib.ssl_bsr_addmm_inplace(16, 64, 16, 64, 16, 16, 16, 1, 0, 1, 64, 64, 1, 64, 64,
-                                   _lib.SSL_BF16, None, 0, None, 0, None)
-    assert rc == _lib.SSL_ERR_WORKSPACE
+    assert op(M=16) == _lib.SSL_ERR_WORKSPACE
+    # prefill-sized call without a prefill plan
+    big = dict(M=4096, counters=P, n_counters=1 << 20)
+    assert op(**big) == _lib.SSL_ERR_INVALID and b"prefill plan" in lib.ssl_last_error()
+    assert lib.ssl_prefill_min_rows() == 128
+    assert lib.ssl_prefill_group(4096, 172, 64) in (1, 4)
+
     # ssl_slr_forward with fake, aligned device pointers (every case below is
     # rejected on the host before any launch)
     P = 256

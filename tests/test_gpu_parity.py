@@ -243,6 +243,69 @@ def test_llama1b_down_proj_ragged_decode(gpu_device):
     assert err(y, oracle_y(prob, x)) <= 1e-2
 
 
+# ------------------------------------------------------ prefill path --
+# Calls with ≥ 128 token rows and 16-bit activations take the LDS-tiled
+# latent GEMM + row GEMM kernels.
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("p", [16, 32, 64])
+@pytest.mark.parametrize("M", [128, 300, 1100])
+def test_prefill_module_matches_oracle(dtype, p, M, gpu_device):
+    prob = make_problem(4 * 64, 6 * 64, 128, p, 0.5, dtype, seed=p + M, skew=(p == 32))
+    mod = _module(prob, gpu_device)
+    x = make_x(prob, M)
+    y = mod(to_dev(x, dtype, gpu_device))
+    y2 = mod(to_dev(x, dtype, gpu_device))
+    torch.cuda.synchronize()
+    assert y.shape == (M, prob["n"])
+    assert err(y, oracle_y(prob, x)) <= TOL[dtype]
+    assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("M", [128, 257])
+def test_prefill_ragged_features_no_bias(M, gpu_device):
+    prob = make_problem(100, 200, 24, 32, 0.5, torch.bfloat16, seed=M, bias=False, pad=True)
+    mod = _module(prob, gpu_device, bias=False)
+    x = make_x(prob, M)
+    y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    assert y.shape == (M, 100)
+    assert err(y, oracle_y(prob, x)) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("p", [16, 64])
+@pytest.mark.parametrize("M", [128, 600])
+def test_prefill_op_matches_oracle_and_keeps_inactive_rows(dtype, p, M, gpu_device):
+    out, want, out0, act, prob = _op_case(dtype, p, M, True, 7 * p + M, gpu_device)
+    assert err(out, want) <= TOL[dtype]
+    got = out.double().cpu().numpy()
+    for by in sorted(set(range(prob["NB"])) - set(act.tolist())):
+        assert np.array_equal(got[:, by * p:(by + 1) * p], out0[:, by * p:(by + 1) * p])
+
+
+def test_prefill_group(gpu_device):
+    probs = _group_probs(torch.bfloat16, [(256, 64, 0.5), (128, 96, 0.3), (192, 128, 0.7)], 320, 32, 9)
+    grp = ssalaad_amd.LRSLinearGroup(*[_module(pr, gpu_device) for pr in probs])
+    x = make_x(probs[0], 333)
+    ys = grp(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    for y, pr in zip(ys, probs):
+        assert err(y, oracle_y(pr, x)) <= 1e-2
+
+
+def test_prefill_llama7b_ffn_2048_tokens(gpu_device):
+    """Full-size 11008×4096 bf16 at 2048 tokens; the oracle checks a spread of rows."""
+    prob = make_problem(11008, 4096, 256, 64, 0.5, torch.bfloat16, seed=11)
+    mod = _module(prob, gpu_device)
+    x = make_x(prob, 2048)
+    y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    rows = np.r_[0:40, 1000:1030, 2000:2048]
+    assert err(y[rows], oracle_y(prob, x[rows])) <= 1e-2
+
+
 # ----------------------------------------------------- grouped launch --
 
 
