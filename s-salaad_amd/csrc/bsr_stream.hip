@@ -475,11 +475,15 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   for (int u0 = bb + wid; u0 < be; u0 += kSW * UNR) {
     Raw raw[UNR][NKS];
     Frag xf[UNR][NKS][MT];
+    // the batch's column indices first, as scalar loads issued together
+    int colk[UNR];
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) colk[k] = ld_uniform(a.col, min(u0 + k * kSW, be - 1)) * Q;
 #pragma unroll
     for (int k = 0; k < UNR; ++k) {
       const int u = u0 + k * kSW;
       if (u < be) {
-        const int colb = a.col[u] * Q;
+        const int colb = colk[k];
         const char* vb = (const char*)a.values + (int64_t)u * (P * Q * EB);
         const bool full = colb + Q <= a.m;
 #pragma unroll

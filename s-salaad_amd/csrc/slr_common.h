@@ -296,6 +296,15 @@ __device__ __forceinline__ typename Mma<DT, KE>::Frag vfrag(const VRawT<DT, KE, 
 
 __device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Wave-uniform read of a structure array that no kernel writes (column indices,
+// plan entries). Through the constant address space it becomes a scalar load,
+// counted by lgkmcnt: waiting for it does not also wait for the vector loads
+// already in flight, as a vector load's vmcnt wait would (that counter retires
+// in order).
+__device__ __forceinline__ int ld_uniform(const int32_t* p, int64_t i) {
+  return ((const __attribute__((address_space(4))) int32_t*)p)[i];
+}
+
 // ---------------------------------------------------------------------------
 // W adjacent elements in the activation dtype.
 // ---------------------------------------------------------------------------
