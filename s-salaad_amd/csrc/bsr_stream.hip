@@ -301,7 +301,7 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
   using MM = Mma<DT, KE>;
   using Frag = typename MM::Frag;
   constexpr int KM = MM::KM;
-  constexpr int UNR = MT == 1 ? 16 : (MT == 2 ? 8 : 4);
+  constexpr int UNR = MT == 1 ? 8 : (MT == 2 ? 4 : 2);
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = wave_uniform(threadIdx.x >> 6);
@@ -647,7 +647,8 @@ struct GroupArgs {
 };
 
 template <int DT, int P, int MT, int MODE, int UNR>
-__global__ __launch_bounds__(kST) void slr_kernel(GroupArgs g_by_value) {
+__global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_kernel(
+    GroupArgs g_by_value) {
   (void)g_by_value;
   const GroupArgs& g = *(const GroupArgs*)__builtin_amdgcn_kernarg_segment_ptr();
   constexpr int W = P / 16;
@@ -678,10 +679,11 @@ namespace {
 
 template <int DT, int P, int MT>
 constexpr int stream_unroll() {
-  // Units per wave per batch: about 32 KiB of weights per wave for one token
-  // tile (a 32-block row in one batch of the 8 waves), fewer for wide tiles.
+  // Units per wave per batch: a 32-block row in one batch of the 8 waves for
+  // 32×32 and 64×64 blocks, fewer units for wide tiles. 16-bit 32×32 kernels stay
+  // within 128 VGPRs, so two workgroups share a compute unit.
   constexpr int bytes = P * P * Elem<DT>::bytes;
-  constexpr int u = bytes >= 16384 ? 2 : (bytes >= 8192 ? 4 : (bytes >= 2048 ? 8 : 16));
+  constexpr int u = bytes >= 16384 ? 2 : (bytes >= 2048 ? 4 : 16);
   constexpr int d = MT >= 4 ? 4 : MT;
   return u / d > 0 ? u / d : 1;
 }
