@@ -26,6 +26,17 @@ cpu_baseline: the reference AVX2 BSR kernel (oracle/_ref, compiled from the
 reference's own source) plus torch-CPU F.linear ×2 — the reference's CPU
 forward, fp32 — timed on this host on a sample (one layer's 7 linears, repeated
 for ~10 s) and scaled to the 24-layer step.
+
+Other workloads (--workload, one JSON line each; the default above is the
+headline):
+  llama7b_ffn_decode   one 11008×4096 SLR linear (64×64 blocks at 50%, r 256,
+                       bf16), --batch tokens (default 1), 8 weight copies
+                       cycled in a HIP graph: GB/s of algorithmic bytes
+  llama7b_ffn_prefill  the same linear at 2048 tokens (latent GEMM, its
+                       combine, the row GEMM): TFLOP/s
+  block_topk           the compression loop's block projection (project_S) of
+                       an 11008×4096 fp32 matrix, 64×64 blocks, half kept:
+                       GB/s of compulsory traffic
 """
 
 from __future__ import annotations
@@ -197,6 +208,107 @@ def run_gpu(args):
     return res
 
 
+def _time_graph(fns, reps):
+    """Mean µs per call of `fns` (called in turn) replayed in a HIP graph."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in fns:
+            f()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for f in fns:
+                f()
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            g.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps / len(fns)
+
+
+def _time_eager(fn, reps):
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def run_workload(args) -> dict:
+    """The non-default workloads (see the module docstring)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(args.seed)
+    n, m, r, p = 11008, 4096, 256, 64
+    base = {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "data": "synthetic", "cpu_baseline": None}
+    if args.workload == "llama7b_ffn_decode":
+        M = args.batch if args.batch_set else 1
+        mods = [make_linear(n, m, r, p, 0.5, gen, dev, torch.bfloat16) for _ in range(8)]
+        x = torch.randn(M, m, generator=gen).to(torch.bfloat16).to(dev)
+        sts = [md._kernel() for md in mods]
+        us = _time_graph([lambda st=st: st.forward(x, n) for st in sts], args.steps)
+        b = algorithmic_bytes(mods[0], M, 2)["total"]
+        gbs = b / us / 1e3
+        return dict(base, metric="SLR-linear decode GB/s (LLaMA-7B FFN projection)",
+                    value=round(gbs, 1), unit="GB/s", ms_per_step=round(us / 1e3, 5), dtype="bf16",
+                    config={"workload": "llama7b_ffn_decode", "n": n, "m": m, "rank": r,
+                            "block": p, "block_density": 0.5, "batch_tokens": M,
+                            "weight_copies": 8, "parallelism": "single_gpu"},
+                    roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                              "traffic": None, "algorithmic_bytes_per_launch": int(b),
+                              "avg_launch_us": round(us, 3)})
+    if args.workload == "llama7b_ffn_prefill":
+        M = args.batch if args.batch_set else 2048
+        mod = make_linear(n, m, r, p, 0.5, gen, dev, torch.bfloat16)
+        x = torch.randn(M, m, generator=gen).to(torch.bfloat16).to(dev)
+        us = _time_eager(lambda: mod(x), args.steps)
+        fl = algorithmic_bytes(mod, M, 2)["flops"]
+        tf = fl / us / 1e6
+        return dict(base, metric="SLR-linear prefill TFLOP/s (LLaMA-7B FFN projection)",
+                    value=round(tf, 1), unit="TFLOP/s", ms_per_step=round(us / 1e3, 5),
+                    dtype="bf16",
+                    config={"workload": "llama7b_ffn_prefill", "n": n, "m": m, "rank": r,
+                            "block": p, "block_density": 0.5, "batch_tokens": M,
+                            "parallelism": "single_gpu"},
+                    roofline={"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
+                              "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4), "traffic": None,
+                              "flops_per_call": int(fl), "low_rank_flops": 2 * M * r * (m + n)})
+    if args.workload == "block_topk":
+        import ssalaad_amd
+
+        Mt = torch.randn(n, m, generator=gen).to(dev)
+        keep = (n // p) * (m // p) // 2
+        us = _time_eager(lambda: ssalaad_amd.block_topk(Mt, keep, p, p), args.steps)
+        b = n * m * 4 * 3 + (n // p) * (m // p) * 5  # read twice, write fp32 once; norms + flags
+        gbs = b / us / 1e3
+        return dict(base, metric="block projection GB/s (project_S, 11008x4096 fp32)",
+                    value=round(gbs, 1), unit="GB/s", ms_per_step=round(us / 1e3, 5), dtype="f32",
+                    config={"workload": "block_topk", "n": n, "m": m, "block": p,
+                            "blocks_kept": keep, "parallelism": "single_gpu"},
+                    roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                              "traffic": None, "bytes_per_call": int(b)})
+    raise SystemExit(f"unknown workload {args.workload}")
+
+
 def copy_probe(mib: int, reps: int) -> None:
     """A plain device-to-device copy of `mib` MiB, `reps` times: the known-size
     kernel whose FETCH_SIZE / WRITE_SIZE counters calibrate the kernel's."""
@@ -310,7 +422,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--layers", type=int, default=24)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -321,7 +433,13 @@ def main():
                     help="one launch per linear instead of grouping q/k/v and gate/up")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (counter calibration)")
+    ap.add_argument("--workload", default="llama1b_decode",
+                    choices=["llama1b_decode", "llama7b_ffn_decode", "llama7b_ffn_prefill",
+                             "block_topk"])
     args = ap.parse_args()
+    args.batch_set = args.batch is not None
+    if args.batch is None:
+        args.batch = 16
     if args.copy_probe:
         copy_probe(args.copy_probe, max(1, args.steps))
         return
@@ -330,6 +448,11 @@ def main():
               "shards by output block-rows with no exchange; see the design notes).",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload != "llama1b_decode":
+        line = run_workload(args)
+        line["warmup"] = args.warmup
+        print(json.dumps(line), flush=True)
+        return
     _log("[bench] GPU leg")
     g = run_gpu(args)
     _log(f"[bench] GPU: {g['ms_step']:.3f} ms/step, {g['tok_s']:.0f} tok/s")

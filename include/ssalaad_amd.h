@@ -213,6 +213,24 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
                           const ssl_slr_member* members, int32_t n_members, void* stream);
 
 /* -------------------------------------------------------------------------
+ * Block projection (device): keep the n_keep blocks of largest Frobenius norm.
+ * Replaces ssalaad/inference/egar.py:296-317 (_project_S), the sparse step of
+ * the compression loop (called at egar.py:464):
+ *   norms[b] = Σ_block v² with v the input as fp32   (M.float(), pow(2).sum)
+ *   keep[b]  = 1 for the n_keep largest norms         (topk(n_keep, largest=True))
+ *   out      = the input as fp32 where its block is kept, else 0
+ * S is [NB·p, lds] in `dtype`; blocks are numbered row-major (b = by·NBK + bc).
+ * n_keep is clamped to [0, NB·NBK] as the reference does. A NaN norm counts as
+ * the largest (as in torch.topk). Equal norms are taken in ascending block
+ * order: deterministic, where torch.topk leaves the order unspecified.
+ * `norms` (NB·NBK fp32) and `keep` (NB·NBK bytes) are device arrays the call
+ * fills; `out` ([NB·p, ldo] fp32) may be NULL to get the mask only.
+ * ------------------------------------------------------------------------- */
+int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t block_p,
+                   int32_t block_q, int32_t dtype, int64_t n_keep, float* norms, uint8_t* keep,
+                   float* out, int64_t ldo, void* stream);
+
+/* -------------------------------------------------------------------------
  * Dense → BSR encoder (device), the rule of ssalaad/efficient/artifact.py:20-37
  * (dense_to_bsr) followed by the module conversion of
  * ssalaad/efficient/ls_linear.py:89-97:

@@ -15,6 +15,9 @@ It restates, in NumPy (float64 unless stated), what the reference computes:
                         (F.linear outputs in bf16, fp32 accumulation of the
                         sparse term from the bf16 output, bias add in bf16)
   factor_from_svd       ssalaad/efficient/artifact.py:7-17
+  project_blocks        ssalaad/inference/egar.py:296-317 (_project_S): keep the
+                        n_keep blocks of largest Frobenius norm (fp32 input,
+                        equal norms taken in ascending row-major block order)
 
 How each function is pinned (tests/test_oracle.py):
   * dense_to_bsr        vs torch.Tensor.to_sparse_bsr (the library routine the
@@ -31,6 +34,13 @@ How each function is pinned (tests/test_oracle.py):
                         equal on inputs whose every intermediate is representable;
   * factor_from_svd     A @ B reconstructs a rank-r matrix; rank 0 gives empty
                         factors (tests/test_ssalaad.py:276-283).
+  * project_blocks      the reference's own case (tests/test_ssalaad.py:215-221),
+                        the selection torch.topk makes on tie-free inputs (the
+                        routine _project_S calls), brute force over every subset
+                        on tiny inputs, and the clamping of n_keep (egar.py:304-306).
+                        Which of several EQUAL norms survive is parity unpinned:
+                        torch.topk does not specify it; the oracle and the GPU
+                        take the lowest block index.
 """
 
 from __future__ import annotations
@@ -184,6 +194,32 @@ def factor_from_svd(U, sigma, Vh, rank: int):
 
 
 # ---------------------------------------------------------------- metrics --
+
+
+def project_blocks(M, n_keep: int, block_p: int, block_q: int):
+    """(kept fp32 matrix, keep mask [rb, cb]) of egar.py:296-317.
+
+    The block norms are sums of squares of the fp32 values, accumulated in
+    float64 here (the reference sums in fp32; the selections agree unless two
+    norms at the threshold are closer than fp32 rounding). NaN norms count as
+    the largest. Equal norms: ascending row-major block order.
+    """
+    Mf = np.asarray(M, dtype=np.float32)
+    n, m = Mf.shape
+    rb, cb = n // block_p, m // block_q
+    n_keep = min(max(int(n_keep), 0), rb * cb)
+    keep = np.zeros(rb * cb, dtype=bool)
+    if n_keep > 0:
+        blk = Mf.astype(np.float64).reshape(rb, block_p, cb, block_q)
+        norms = (blk * blk).sum(axis=(1, 3)).reshape(-1)
+        key = np.where(np.isnan(norms), np.inf, norms)
+        nan_first = np.isnan(norms)
+        # sort by (NaN first, then larger norm first, then lower index first)
+        order = np.lexsort((np.arange(rb * cb), -key, ~nan_first))
+        keep[order[:n_keep]] = True
+    keep = keep.reshape(rb, cb)
+    mask = np.repeat(np.repeat(keep, block_p, axis=0), block_q, axis=1)
+    return np.where(mask, Mf, np.float32(0)).astype(np.float32), keep
 
 
 def max_abs_normalised_error(y, y_ref) -> float:

@@ -1,0 +1,271 @@
+// Block projection on the device: keep the n_keep blocks of largest Frobenius
+// norm, the sparse step of the reference's compression loop
+// (ssalaad/inference/egar.py:296-317, _project_S):
+//
+//   norms[b]  = Σ over block b of v², v = the input as fp32   (M.float(), .pow(2).sum)
+//   keep      = the n_keep largest norms                       (topk(n_keep, largest=True))
+//   out       = the input as fp32 where its block is kept, 0 elsewhere
+//
+// The selection is a most-significant-digit radix select over the norms' fp32
+// bit patterns, which order like the values themselves because every norm is
+// ≥ +0 or NaN (all NaNs are folded into one pattern above +inf, so NaN blocks
+// count as the largest, as in torch.topk). Blocks whose norms are equal are
+// taken in ascending block order (row-major), which makes the result
+// deterministic; torch.topk leaves that order unspecified.
+#include "abi_internal.h"
+#include "slr_common.h"
+
+namespace ssl {
+namespace {
+
+constexpr int kSelThreads = 1024;
+constexpr uint32_t kNanKey = 0x7fc00000u;
+
+template <int DT>
+__device__ __forceinline__ float elem_f32(const void* base, int64_t i) {
+  if constexpr (DT == DT_F32) return ((const float*)base)[i];
+  else if constexpr (DT == DT_BF16) return bf16_to_f32(((const uint16_t*)base)[i]);
+  else return f16_to_f32(((const uint16_t*)base)[i]);
+}
+
+// One wave per block: the fp32 sum of squares (lane-strided partial sums, then a
+// fixed butterfly, so repeated runs give identical bits).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void block_sumsq_kernel(const void* S, int64_t lds, int NB,
+                                                               int NBK, int p, int q, bool vec,
+                                                               float* norms) {
+  const int lane = threadIdx.x & 63;
+  const int64_t blk = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (blk >= (int64_t)NB * NBK) return;
+  const int by = (int)(blk / NBK), bc = (int)(blk % NBK);
+  const int64_t base = (int64_t)by * p * lds + (int64_t)bc * q;
+  constexpr int EB = Elem<DT>::bytes, VE = 16 / EB;  // elements per 16-byte piece
+  float acc = 0.f;
+  if (vec) {
+    // pieces of VE elements: cpr per block row, all rows
+    const int cpr = q / VE, pieces = p * cpr;
+    for (int idx0 = lane; idx0 < pieces; idx0 += 4 * kWave) {
+      uint4 v4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int idx = idx0 + u * kWave;
+        const int i = idx / cpr, j = (idx % cpr) * VE;
+        v4[u] = idx < pieces ? *(const uint4*)((const char*)S + (base + (int64_t)i * lds + j) * EB)
+                             : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t w[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          if constexpr (DT == DT_F32) {
+            const float v = __uint_as_float(w[h]);
+            acc = fmaf(v, v, acc);
+          } else {
+            const float lo = DT == DT_BF16 ? bf16_to_f32(w[h] & 0xffffu) : f16_to_f32(w[h] & 0xffffu);
+            const float hi = DT == DT_BF16 ? bf16_to_f32(w[h] >> 16) : f16_to_f32(w[h] >> 16);
+            acc = fmaf(lo, lo, acc);
+            acc = fmaf(hi, hi, acc);
+          }
+        }
+      }
+    }
+  } else {
+    for (int idx = lane; idx < p * q; idx += kWave) {
+      const int i = idx / q, j = idx % q;
+      const float v = elem_f32<DT>(S, base + (int64_t)i * lds + j);
+      acc = fmaf(v, v, acc);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+  if (lane == 0) norms[blk] = acc;
+}
+
+__device__ __forceinline__ uint32_t norm_key(float v) {
+  const uint32_t b = __float_as_uint(v);
+  return (b & 0x7fffffffu) > 0x7f800000u ? kNanKey : b;
+}
+
+// Single workgroup: keep[b] = 1 for the n_keep largest keys (ties: lowest b first).
+// STAGED: the keys are copied into LDS once (n ≤ kLdsKeys) and every pass reads them there.
+constexpr int kLdsKeys = 15360;  // 60 KiB of keys: within 64 KiB of LDS with the rest
+
+template <bool STAGED>
+__global__ __launch_bounds__(kSelThreads) void block_topk_kernel(const float* norms, int n,
+                                                                 int n_keep, uint8_t* keep) {
+  extern __shared__ uint32_t s_keys[];
+  auto key_at = [&](int i) { return STAGED ? s_keys[i] : norm_key(norms[i]); };
+  __shared__ int hist[256];
+  __shared__ uint32_t s_prefix, s_mask;
+  __shared__ int s_need, s_eq;
+  __shared__ int s_wave[kSelThreads / kWave];
+  const int t = threadIdx.x;
+  if (n_keep <= 0 || n_keep >= n) {
+    for (int i = t; i < n; i += kSelThreads) keep[i] = n_keep > 0 ? 1 : 0;
+    return;
+  }
+  if (t == 0) {
+    s_prefix = 0u;
+    s_mask = 0u;
+    s_need = n_keep;
+  }
+  if constexpr (STAGED)
+    for (int i = t; i < n; i += kSelThreads) s_keys[i] = norm_key(norms[i]);
+  __syncthreads();
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int d = t; d < 256; d += kSelThreads) hist[d] = 0;
+    __syncthreads();
+    const uint32_t prefix = s_prefix, mask = s_mask;
+    for (int i = t; i < n; i += kSelThreads) {
+      const uint32_t k = key_at(i);
+      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1);
+    }
+    __syncthreads();
+    if (t < kWave) {
+      // The digit of the need-th largest key among those matching the prefix.
+      // Lane l holds bins 4l .. 4l + 3; a suffix sum over the lanes gives the
+      // count above each lane's bins, and exactly one lane's bins contain it.
+      const int need0 = s_need;
+      int h[4], sum4 = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        h[b] = hist[4 * t + b];
+        sum4 += h[b];
+      }
+      int incl = sum4;  // Σ of lanes t .. 63
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const int v = __shfl_down(incl, off, kWave);
+        if (t + off < kWave) incl += v;
+      }
+      const int above = incl - sum4;
+      if (above < need0 && need0 <= incl) {
+        int cum = above, d = 4 * t;
+#pragma unroll
+        for (int b = 3; b >= 0; --b) {
+          if (cum + h[b] >= need0) {
+            d = 4 * t + b;
+            break;
+          }
+          cum += h[b];
+        }
+        s_need = need0 - cum;
+        s_eq = hist[d];  // keys matching the prefix so far (after the last digit: equal to T)
+        s_prefix = prefix | ((uint32_t)d << shift);
+        s_mask = mask | (255u << shift);
+      }
+    }
+    __syncthreads();
+  }
+  // Threshold key T: keep every key above it and the first s_need keys equal
+  // to it in block order.
+  const uint32_t T = s_prefix;
+  const int need = s_need;
+  if (need == s_eq) {
+    // every key equal to T is kept: no order among them to respect
+    for (int i = t; i < n; i += kSelThreads) keep[i] = key_at(i) >= T ? 1 : 0;
+    return;
+  }
+  const int lane = t & 63, w = t >> 6;
+  int taken = 0;  // equal keys already kept in earlier chunks (same in every thread)
+  for (int c0 = 0; c0 < n; c0 += kSelThreads) {
+    const int i = c0 + t;
+    uint32_t k = 0;
+    if (i < n) k = key_at(i);
+    const bool eq = i < n && k == T;
+    const unsigned long long bal = __ballot(eq);
+    const int before = __popcll(bal & ((1ull << lane) - 1ull));
+    if (lane == 0) s_wave[w] = __popcll(bal);
+    __syncthreads();
+    int wave_off = 0, chunk_total = 0;
+    for (int v = 0; v < kSelThreads / kWave; ++v) {
+      const int c = s_wave[v];
+      if (v < w) wave_off += c;
+      chunk_total += c;
+    }
+    if (i < n) keep[i] = (k > T || (eq && taken + wave_off + before < need)) ? 1 : 0;
+    taken += chunk_total;
+    __syncthreads();
+  }
+}
+
+// out[i, j] = input as fp32 where block (i / p, j / q) is kept, else 0.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void block_mask_kernel(const void* S, int64_t lds, int n,
+                                                              int m, int p, int q, int NBK,
+                                                              const uint8_t* keep, float* out,
+                                                              int64_t ldo, bool vec) {
+  for (int i = blockIdx.y; i < n; i += gridDim.y) {
+    const uint8_t* krow = keep + (int64_t)(i / p) * NBK;
+    for (int j0 = 4 * (blockIdx.x * kThreads + threadIdx.x); j0 < m; j0 += 4 * gridDim.x * kThreads) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = j0 + u;
+        v[u] = (j < m && krow[j / q]) ? elem_f32<DT>(S, (int64_t)i * lds + j) : 0.f;
+      }
+      if (vec && j0 + 4 <= m) {
+        *(float4*)(out + (int64_t)i * ldo + j0) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (j0 + u < m) out[(int64_t)i * ldo + j0 + u] = v[u];
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace ssl
+
+using namespace ssl;
+
+extern "C" {
+
+int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t block_p,
+                   int32_t block_q, int32_t dtype, int64_t n_keep, float* norms, uint8_t* keep,
+                   float* out, int64_t ldo, void* stream) {
+  clear_error();
+  if (block_p <= 0 || block_q <= 0 || NB < 0 || NBK < 0) return fail(SSL_ERR_INVALID, "bad sizes");
+  if (dtype != SSL_F32 && dtype != SSL_BF16 && dtype != SSL_F16)
+    return fail(SSL_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
+  const int64_t nblocks = NB * NBK;
+  if (nblocks == 0) return SSL_OK;
+  if (nblocks > 0x7fffffffLL || NB * block_p > 0x7fffffffLL || NBK * block_q > 0x7fffffffLL)
+    return fail(SSL_ERR_INVALID, "too many blocks");
+  if (lds < NBK * block_q) return fail(SSL_ERR_INVALID, "lds smaller than the row");
+  if (!S || !norms || !keep) return fail(SSL_ERR_INVALID, "null pointer");
+  if (out && ldo < NBK * block_q) return fail(SSL_ERR_INVALID, "ldo smaller than the row");
+  hipStream_t s = (hipStream_t)stream;
+  const unsigned grid = (unsigned)((nblocks + kWaves - 1) / kWaves);
+  const int n = (int)(NB * block_p), m = (int)(NBK * block_q);
+  const int mcols = (m + 4 * kThreads - 1) / (4 * kThreads);
+  const dim3 mgrid((unsigned)(mcols < 64 ? mcols : 64), (unsigned)(n < 65535 ? n : 65535));
+  const int eb = elem_bytes(dtype);
+  const int keep_n = (int)(n_keep < 0 ? 0 : (n_keep > nblocks ? nblocks : n_keep));
+  // 16-byte pieces of the input: aligned base, row stride and block rows
+  const bool vec_in = ((uintptr_t)S % 16 == 0) && (lds * eb) % 16 == 0 && (block_q * eb) % 16 == 0;
+  const bool vec_out = out && ((uintptr_t)out % 16 == 0) && ldo % 4 == 0;
+#define SSL_PROJECT(DTC)                                                                       \
+  hipLaunchKernelGGL(block_sumsq_kernel<DTC>, dim3(grid), dim3(kThreads), 0, s, S, lds, (int)NB, \
+                     (int)NBK, block_p, block_q, vec_in, norms);                                \
+  if (nblocks <= kLdsKeys)                                                                       \
+    hipLaunchKernelGGL(block_topk_kernel<true>, dim3(1), dim3(kSelThreads),                      \
+                       (unsigned)(4 * nblocks), s, norms, (int)nblocks, keep_n, keep);           \
+  else                                                                                          \
+    hipLaunchKernelGGL(block_topk_kernel<false>, dim3(1), dim3(kSelThreads), 0, s, norms,        \
+                       (int)nblocks, keep_n, keep);                                             \
+  if (out)                                                                                      \
+    hipLaunchKernelGGL(block_mask_kernel<DTC>, mgrid, dim3(kThreads), 0, s, S, lds, n, m,        \
+                       block_p, block_q, (int)NBK, keep, out, ldo, vec_out);
+  switch (dtype) {
+    case SSL_F32: SSL_PROJECT(DT_F32) break;
+    case SSL_BF16: SSL_PROJECT(DT_BF16) break;
+    case SSL_F16: SSL_PROJECT(DT_F16) break;
+  }
+#undef SSL_PROJECT
+  return check_hip(hipGetLastError(), "block projection launch");
+}
+
+}  // extern "C"

@@ -5,6 +5,7 @@ Drop-in for the S-SALAAD hot path:
   * LRSLinear                                              (ssalaad_amd.ls_linear)
   * LRSLinearGroup: linears sharing an input in one launch (ssalaad_amd.ls_linear)
   * dense_to_bsr / factor_from_svd                         (ssalaad_amd.artifact)
+  * project_S: the compression loop's block top-k           (ssalaad_amd.project)
 All compute runs in the HIP kernels of libssalaad_amd.so; there is no CPU path.
 """
 
@@ -14,17 +15,20 @@ from . import _lib
 from .addmm_inplace import SUPPORTED_BLOCK_SIZES, bsr_addmm_inplace_, get_tuned_config
 from .artifact import dense_to_bsr, encode_for_kernels, factor_from_svd
 from .ls_linear import LRSLinear, LRSLinearGroup
+from .project import block_topk, project_S
 
 __all__ = [
     "LRSLinear",
     "LRSLinearGroup",
     "SUPPORTED_BLOCK_SIZES",
+    "block_topk",
     "bsr_addmm_inplace_",
     "dense_to_bsr",
     "encode_for_kernels",
     "factor_from_svd",
     "get_tuned_config",
     "library_path",
+    "project_S",
 ]
 
 

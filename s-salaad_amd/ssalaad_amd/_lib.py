@@ -62,6 +62,11 @@ _SIGNATURES = {
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64,
          _c_p, _c_i64, _c_p, _c_i64, _c_p],
     ),
+    "ssl_block_topk": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_p, _c_p, _c_p, _c_i64,
+         _c_p],
+    ),
     "ssl_bsr_encode_count": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p],

@@ -299,3 +299,15 @@ def test_encoder_rejects_bad_arguments():
     assert rc == _lib.SSL_ERR_INVALID  # lds < NBK·q
     rc = lib.ssl_bsr_encode_count(None, 32, 0, 2, 16, 16, 9, None, 1, None, 1, None)
     assert rc == _lib.SSL_ERR_UNSUPPORTED
+
+
+def test_block_topk_rejects_bad_arguments_before_any_launch():
+    lib = _lib.load()
+    fake = 256  # never dereferenced: every call below fails its argument checks first
+    assert lib.ssl_block_topk(fake, 64, 2, 2, 0, 32, _lib.SSL_F32, 1, fake, fake, None, 0, None) == 1
+    assert lib.ssl_block_topk(fake, 32, 2, 2, 32, 32, _lib.SSL_F32, 1, fake, fake, None, 0, None) == 1
+    assert lib.ssl_block_topk(fake, 64, 2, 2, 32, 32, 7, 1, fake, fake, None, 0, None) == 2
+    assert lib.ssl_block_topk(None, 64, 2, 2, 32, 32, _lib.SSL_BF16, 1, fake, fake, None, 0, None) == 1
+    assert lib.ssl_block_topk(fake, 64, 2, 2, 32, 32, _lib.SSL_BF16, 1, fake, fake, fake, 16, None) == 1
+    assert b"ldo" in lib.ssl_last_error()
+    assert lib.ssl_block_topk(fake, 64, 0, 2, 32, 32, _lib.SSL_BF16, 1, None, None, None, 0, None) == 0

@@ -381,6 +381,95 @@ def test_group_llama7b_attention_projections(M, gpu_device):
         assert err(y, oracle_y(pr, x)) <= 1e-2
 
 
+# --------------------------------------------- block projection (_project_S) --
+
+
+def _separated(n, m, p, q, seed):
+    """Random blocks whose Frobenius norms differ by ≥ 0.1% (no near ties)."""
+    rng = np.random.default_rng(seed)
+    rb, cb = n // p, m // q
+    M = rng.standard_normal((n, m)).astype(np.float32)
+    blk = M.reshape(rb, p, cb, q)
+    norms = np.sqrt((blk.astype(np.float64) ** 2).sum(axis=(1, 3)))
+    target = 1.0 + 1e-3 * rng.permutation(rb * cb).reshape(rb, cb)
+    blk *= (target / norms)[:, None, :, None].astype(np.float32)
+    return blk.reshape(n, m)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("shape", [(64, 96, 16, 16), (128, 128, 32, 32), (256, 512, 64, 64),
+                                   (48, 40, 8, 4), (12, 20, 1, 1)])
+def test_project_S_matches_oracle(dtype, shape, gpu_device):
+    """Keep mask and kept values exact (the values are the input as fp32)."""
+    n, m, p, q = shape
+    M = _separated(n, m, p, q, seed=n * 7 + m)
+    Md = torch.from_numpy(M).to(dtype)
+    Mq = Md.float().numpy()                      # the input as the kernel sees it
+    total = (n // p) * (m // q)
+    for n_keep in (-3, 0, 1, total // 2, total - 1, total, total + 5):
+        out, keep, _ = ssalaad_amd.block_topk(Md.to(gpu_device), n_keep, p, q)
+        torch.cuda.synchronize()
+        want, want_keep = orc.project_blocks(Mq, n_keep, p, q)
+        assert np.array_equal(keep.cpu().numpy(), want_keep), n_keep
+        assert np.array_equal(out.cpu().numpy(), want), n_keep
+
+
+def test_project_S_ties_nan_and_inf(gpu_device):
+    M = np.ones((8, 12), np.float32)             # twelve equal 2×4 blocks (4 × 3)
+    out = ssalaad_amd.project_S(torch.from_numpy(M).to(gpu_device), 5, 2, 4)
+    keep = (out.cpu().numpy().reshape(4, 2, 3, 4) != 0).any(axis=(1, 3)).reshape(-1)
+    assert np.flatnonzero(keep).tolist() == [0, 1, 2, 3, 4]   # lowest block index first
+    M = _separated(16, 16, 4, 4, seed=11)
+    M[5, 6] = np.nan
+    M[13, 1] = np.inf
+    for n_keep in (1, 2, 7):
+        out, keep, _ = ssalaad_amd.block_topk(torch.from_numpy(M).to(gpu_device), n_keep, 4, 4)
+        want, want_keep = orc.project_blocks(M, n_keep, 4, 4)
+        assert np.array_equal(keep.cpu().numpy(), want_keep)
+        got = out.cpu().numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert np.array_equal(np.nan_to_num(got, nan=7.0), np.nan_to_num(want, nan=7.0))
+
+
+def test_project_S_rejects_bad_arguments(gpu_device):
+    M = torch.ones(8, 8, device=gpu_device)
+    with pytest.raises(RuntimeError, match="invalid for input"):
+        ssalaad_amd.project_S(M, 1, 3, 4)
+    with pytest.raises(ValueError, match="GPU"):
+        ssalaad_amd.project_S(M.cpu(), 1, 4, 4)
+
+
+def test_project_then_encode_gives_the_reference_structure(gpu_device):
+    """The compression loop's path: project (fp32) → cast to bf16 → dense_to_bsr
+    (egar.py:464, :552-553; artifact.py:20-37), structure and values bit-exact."""
+    n, m, p = 512, 768, 32
+    M = _separated(n, m, p, p, seed=21)
+    M[32:64, 64:96] = 1e-41                      # fp32 subnormals: zero once cast to bf16
+    total = (n // p) * (m // p)
+    for n_keep in (total // 2, total):
+        out = ssalaad_amd.project_S(torch.from_numpy(M).to(gpu_device), n_keep, p, p)
+        S = ssalaad_amd.dense_to_bsr(out.to(torch.bfloat16), p, p)
+        torch.cuda.synchronize()
+        want_proj, _ = orc.project_blocks(M, n_keep, p, p)
+        crow, col, vals = orc.dense_to_bsr(orc.bf16_round(want_proj), p, p)
+        assert np.array_equal(S.crow_indices().cpu().numpy(), crow)
+        assert np.array_equal(S.col_indices().cpu().numpy(), col)
+        assert np.array_equal(S.values().float().cpu().numpy(), vals)
+    assert crow[-1] == total - 1                 # the kept subnormal block is dropped
+
+
+def test_project_S_llama7b_ffn_shape(gpu_device):
+    """11008×4096 fp32, 64×64 blocks, half of them kept."""
+    n, m, p = 11008, 4096, 64
+    M = _separated(n, m, p, p, seed=23)
+    total = (n // p) * (m // p)
+    out, keep, _ = ssalaad_amd.block_topk(torch.from_numpy(M).to(gpu_device), total // 2, p, p)
+    torch.cuda.synchronize()
+    want, want_keep = orc.project_blocks(M, total // 2, p, p)
+    assert np.array_equal(keep.cpu().numpy(), want_keep)
+    assert torch.equal(out.cpu(), torch.from_numpy(want))
+
+
 # ------------------------------------------------------------ encoder --
 
 

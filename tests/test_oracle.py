@@ -343,3 +343,87 @@ def test_planted_mistakes_are_caught_by_the_golden_vectors():
     col_shift = np.minimum(c["col"] + 1, 4).astype(np.int32)
     assert not close(orc.bsr_addmm_inplace(c["out"], c["x"], c["crow"], col_shift, c["values_t"],
                                            c["active"]))
+
+
+# ------------------------------------------------- block projection (_project_S) --
+
+
+def _torch_project(M, n_keep, p, q):
+    """The reference's selection (egar.py:296-317), written with the routines it calls."""
+    M_f = torch.from_numpy(np.asarray(M, np.float32))
+    n, m = M_f.shape
+    rb, cb = n // p, m // q
+    n_keep = min(max(n_keep, 0), rb * cb)
+    keep = torch.zeros(rb * cb, dtype=torch.bool)
+    if n_keep:
+        blk = M_f.reshape(rb, p, cb, q).permute(0, 2, 1, 3)
+        _, order = blk.pow(2).sum(dim=(2, 3)).flatten().topk(n_keep, largest=True)
+        keep[order] = True
+    return keep.reshape(rb, cb).numpy()
+
+
+def _separated_blocks(n, m, p, q, seed):
+    """Random blocks whose Frobenius norms differ by ≥ 0.1% (no near ties)."""
+    rng = np.random.default_rng(seed)
+    rb, cb = n // p, m // q
+    M = rng.standard_normal((n, m)).astype(np.float32)
+    blk = M.reshape(rb, p, cb, q)
+    norms = np.sqrt((blk.astype(np.float64) ** 2).sum(axis=(1, 3)))
+    target = 1.0 + 1e-3 * rng.permutation(rb * cb).reshape(rb, cb)
+    blk *= (target / norms)[:, None, :, None].astype(np.float32)
+    return blk.reshape(n, m)
+
+
+def test_project_blocks_reference_case():
+    """tests/test_ssalaad.py:215-221: the larger of two 4×4 blocks survives."""
+    M = np.zeros((8, 8), np.float32)
+    M[0:4, 0:4] = 3.0
+    M[4:8, 4:8] = 1.0
+    kept, keep = orc.project_blocks(M, 1, 4, 4)
+    assert np.array_equal(kept[0:4, 0:4], M[0:4, 0:4])
+    assert float(np.abs(kept[4:8, 4:8]).max()) == 0.0
+    assert keep.tolist() == [[True, False], [False, False]]
+
+
+@pytest.mark.parametrize("shape", [(64, 96, 16, 16), (128, 64, 32, 32), (24, 40, 4, 8), (6, 10, 1, 1)])
+def test_project_blocks_matches_torch_topk_without_ties(shape):
+    n, m, p, q = shape
+    M = _separated_blocks(n, m, p, q, seed=n + m)
+    total = (n // p) * (m // q)
+    for n_keep in (1, total // 3, total // 2, total - 1):
+        kept, keep = orc.project_blocks(M, n_keep, p, q)
+        assert np.array_equal(keep, _torch_project(M, n_keep, p, q))
+        mask = np.repeat(np.repeat(keep, p, 0), q, 1)
+        assert np.array_equal(kept, np.where(mask, M, 0).astype(np.float32))
+
+
+def test_project_blocks_maximises_the_kept_energy_by_brute_force():
+    from itertools import combinations
+
+    M = _separated_blocks(6, 6, 2, 3, seed=3)   # 3 × 2 = 6 blocks
+    blk = M.astype(np.float64).reshape(3, 2, 2, 3)
+    norms = (blk ** 2).sum(axis=(1, 3)).reshape(-1)
+    for n_keep in range(7):
+        best = max(combinations(range(6), n_keep), key=lambda s: sum(norms[list(s)]))
+        _, keep = orc.project_blocks(M, n_keep, 2, 3)
+        assert sorted(np.flatnonzero(keep.reshape(-1)).tolist()) == sorted(best)
+
+
+def test_project_blocks_clamps_n_keep_and_breaks_ties_by_block_order():
+    M = np.ones((4, 6), np.float32)                # six equal 2×2 blocks
+    for n_keep, want in ((-2, 0), (0, 0), (3, 3), (6, 6), (9, 6)):
+        kept, keep = orc.project_blocks(M, n_keep, 2, 2)
+        assert int(keep.sum()) == want
+        assert np.flatnonzero(keep.reshape(-1)).tolist() == list(range(want))  # lowest first
+        assert kept.dtype == np.float32 and float(kept.sum()) == 4.0 * want
+
+
+def test_project_blocks_counts_nan_and_inf_blocks_as_largest_like_torch():
+    M = _separated_blocks(8, 8, 2, 2, seed=5)
+    M[2, 3] = np.nan                               # block (1, 1)
+    M[6, 0] = np.inf                               # block (3, 0)
+    for n_keep in (1, 2, 3):
+        _, keep = orc.project_blocks(M, n_keep, 2, 2)
+        assert np.array_equal(keep, _torch_project(M, n_keep, 2, 2))
+    _, keep = orc.project_blocks(M, 2, 2, 2)
+    assert keep[1, 1] and keep[3, 0]
