@@ -37,6 +37,10 @@ headline):
   block_topk           the compression loop's block projection (project_S) of
                        an 11008×4096 fp32 matrix, 64×64 blocks, half kept:
                        GB/s of compulsory traffic
+  llama60m_forward     the LLaMA-60M-shaped decoder (8 layers, hidden 512, 8
+                       heads, FFN 1376, vocab 32000) with every q/k/v/o/gate/
+                       up/down an SLR linear (rank dim/4, 32×32 blocks at 50%,
+                       N(0, 0.02)), fp32 forward of 8 × 256 tokens: tok/s
 """
 
 from __future__ import annotations
@@ -306,6 +310,51 @@ def run_workload(args) -> dict:
                     roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                               "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                               "traffic": None, "bytes_per_call": int(b)})
+    if args.workload == "llama60m_forward":
+        from ssalaad_amd import LRSLinear
+        from ssalaad_amd.bundle import build_model_from_config
+
+        cfg = {"model_type": "llama", "hidden_size": 512, "intermediate_size": 1376,
+               "num_hidden_layers": 8, "num_attention_heads": 8, "num_key_value_heads": 8,
+               "vocab_size": 32000, "max_position_embeddings": 256, "rms_norm_eps": 1e-6,
+               "hidden_act": "silu", "bos_token_id": 1, "eos_token_id": 2, "pad_token_id": 0,
+               "tie_word_embeddings": False}
+        torch.manual_seed(args.seed)
+        model = build_model_from_config(cfg, attn_implementation="sdpa").eval()
+        projs = ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                 "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"]
+        total_bytes = 0
+        for li in range(cfg["num_hidden_layers"]):
+            for proj in projs:
+                parent = model.get_submodule(f"model.layers.{li}.{proj.split('.')[0]}")
+                old = getattr(parent, proj.split(".")[1])
+                nn_, mm = old.out_features, old.in_features
+                rr, pp = min(nn_, mm) // 4, 32
+                NB, NBK = nn_ // pp, mm // pp
+                k = NB * NBK // 2
+                slots = torch.randperm(NB * NBK, generator=gen)[:k].sort().values
+                crow = torch.zeros(NB + 1, dtype=torch.int64)
+                crow[1:] = torch.bincount(slots // NBK, minlength=NB).cumsum(0)
+                vals = torch.randn(k, pp, pp, generator=gen) * 0.02
+                S = torch.sparse_bsr_tensor(crow.to(dev), (slots % NBK).to(dev), vals.to(dev),
+                                            size=(nn_, mm))
+                A = (torch.randn(nn_, rr, generator=gen) * 0.02).to(dev)
+                B = (torch.randn(rr, mm, generator=gen) * 0.02).to(dev)
+                mod = LRSLinear(A, B, S, in_features=mm, out_features=nn_, block_p=pp, block_q=pp)
+                total_bytes += 4 * (rr * (nn_ + mm) + k * pp * pp)
+                setattr(parent, proj.split(".")[1], mod)
+        model = model.to(dev)
+        ids = torch.randint(3, cfg["vocab_size"], (8, 256), generator=gen).to(dev)
+        with torch.no_grad():
+            us = _time_eager(lambda: model(input_ids=ids), max(3, args.steps // 5))
+        tok_s = 8 * 256 / (us * 1e-6)
+        return dict(base, metric="LLaMA-60M SLR forward tok/s (fp32, 8 x 256 tokens)",
+                    value=round(tok_s, 1), unit="tok/s", ms_per_step=round(us / 1e3, 4), dtype="f32",
+                    config={"workload": "llama60m_forward", "layers": 8, "hidden": 512, "ffn": 1376,
+                            "heads": 8, "vocab": 32000, "rank": "dim/4", "block": 32,
+                            "block_density": 0.5, "batch": 8, "seq_len": 256,
+                            "slr_weight_bytes": total_bytes, "parallelism": "single_gpu"},
+                    roofline=None)
     raise SystemExit(f"unknown workload {args.workload}")
 
 
@@ -435,7 +484,7 @@ def main():
                     help="only run a plain device copy of MIB MiB (counter calibration)")
     ap.add_argument("--workload", default="llama1b_decode",
                     choices=["llama1b_decode", "llama7b_ffn_decode", "llama7b_ffn_prefill",
-                             "block_topk"])
+                             "block_topk", "llama60m_forward"])
     args = ap.parse_args()
     args.batch_set = args.batch is not None
     if args.batch is None:

@@ -6,6 +6,7 @@ Drop-in for the S-SALAAD hot path:
   * LRSLinearGroup: linears sharing an input in one launch (ssalaad_amd.ls_linear)
   * dense_to_bsr / factor_from_svd                         (ssalaad_amd.artifact)
   * project_S: the compression loop's block top-k           (ssalaad_amd.project)
+  * save_artifact / load_artifact / build_efficient_model: bundles (ssalaad_amd.bundle)
 All compute runs in the HIP kernels of libssalaad_amd.so; there is no CPU path.
 """
 
@@ -14,6 +15,7 @@ from __future__ import annotations
 from . import _lib
 from .addmm_inplace import SUPPORTED_BLOCK_SIZES, bsr_addmm_inplace_, get_tuned_config
 from .artifact import dense_to_bsr, encode_for_kernels, factor_from_svd
+from .bundle import build_efficient_model, load_artifact, save_artifact
 from .ls_linear import LRSLinear, LRSLinearGroup
 from .project import block_topk, project_S
 
@@ -22,13 +24,16 @@ __all__ = [
     "LRSLinearGroup",
     "SUPPORTED_BLOCK_SIZES",
     "block_topk",
+    "build_efficient_model",
     "bsr_addmm_inplace_",
     "dense_to_bsr",
     "encode_for_kernels",
     "factor_from_svd",
     "get_tuned_config",
     "library_path",
+    "load_artifact",
     "project_S",
+    "save_artifact",
 ]
 
 
