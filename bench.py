@@ -37,6 +37,10 @@ headline):
   block_topk           the compression loop's block projection (project_S) of
                        an 11008×4096 fp32 matrix, 64×64 blocks, half kept:
                        GB/s of compulsory traffic
+  llama7b_ffn_decode_nm24  the same projection with 2:4 S (two of every four
+                       input features kept, N(0, 0.02)) instead of blocks:
+                       GB/s of algorithmic bytes (values plus 4-bit
+                       positions per group)
   llama60m_forward     the LLaMA-60M-shaped decoder (8 layers, hidden 512, 8
                        heads, FFN 1376, vocab 32000) with every q/k/v/o/gate/
                        up/down an SLR linear (rank dim/4, 32×32 blocks at 50%,
@@ -279,6 +283,32 @@ def run_workload(args) -> dict:
                               "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                               "traffic": None, "algorithmic_bytes_per_launch": int(b),
                               "avg_launch_us": round(us, 3)})
+    if args.workload == "llama7b_ffn_decode_nm24":
+        from ssalaad_amd import LRSLinear
+
+        M = args.batch if args.batch_set else 1
+        mods = []
+        for _ in range(8):
+            grp = torch.rand(n, m // 4, 4, generator=gen).argsort(dim=-1).argsort(dim=-1) < 2
+            S = (torch.randn(n, m, generator=gen) * 0.02 * grp.reshape(n, m)).to(torch.bfloat16)
+            A = (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
+            B = (torch.randn(r, m, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
+            mods.append(LRSLinear(A, B, S.to(dev), in_features=m, out_features=n, nm_n=2, nm_m=4))
+        x = torch.randn(M, m, generator=gen).to(torch.bfloat16).to(dev)
+        sts = [md._kernel() for md in mods]
+        us = _time_graph([lambda st=st: st.forward(x, n) for st in sts], args.steps)
+        b = 2 * M * (m + n) + 2 * r * (n + m) + 2 * (n * m // 2) + n * m // 8
+        gbs = b / us / 1e3
+        return dict(base, metric="SLR-linear decode GB/s (LLaMA-7B FFN projection, 2:4 S)",
+                    value=round(gbs, 1), unit="GB/s", ms_per_step=round(us / 1e3, 5), dtype="bf16",
+                    config={"workload": "llama7b_ffn_decode_nm24", "n": n, "m": m, "rank": r,
+                            "sparsity": "2:4", "batch_tokens": M, "weight_copies": 8,
+                            "parallelism": "single_gpu"},
+                    roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                              "traffic": None, "algorithmic_bytes_per_launch": int(b),
+                              "stored_bytes_per_launch": int(2 * r * (n + m) + (n // 32) * (m // 32) * 1280),
+                              "avg_launch_us": round(us, 3)})
     if args.workload == "llama7b_ffn_prefill":
         M = args.batch if args.batch_set else 2048
         mod = make_linear(n, m, r, p, 0.5, gen, dev, torch.bfloat16)
@@ -484,7 +514,7 @@ def main():
                     help="only run a plain device copy of MIB MiB (counter calibration)")
     ap.add_argument("--workload", default="llama1b_decode",
                     choices=["llama1b_decode", "llama7b_ffn_decode", "llama7b_ffn_prefill",
-                             "block_topk", "llama60m_forward"])
+                             "llama7b_ffn_decode_nm24", "block_topk", "llama60m_forward"])
     args = ap.parse_args()
     args.batch_set = args.batch is not None
     if args.batch is None:

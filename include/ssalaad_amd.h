@@ -200,7 +200,22 @@ typedef struct ssl_slr_member {
   int32_t pf_group;
   int64_t nnz;            /* stored blocks (length of col, first dim of values) */
   const void* values_pq;  /* the block values in (nnz, p, q) order, for the prefill kernels */
+  /* storage of `values`: SSL_S_BSR, (nnz, q, p) blocks (the reference module's
+   * layout), or SSL_S_NM24, 2:4-sparse 32×32 blocks in the layout below
+   * (replaces the semi-structured S of ssalaad/efficient/ls_linear.py:167-219) */
+  int32_t s_format;
 } ssl_slr_member;
+
+typedef enum { SSL_S_BSR = 0, SSL_S_NM24 = 1 } ssl_s_format;
+
+/* Bytes of one packed 2:4 block (32 input features × 32 output features):
+ *   values [16][16][2] of the activation dtype: [c][i][s] = the i-th kept value,
+ *          in increasing input feature order, of output column 2c + s (two kept
+ *          values per group of four input features: group i / 2, slot i % 2);
+ *   index  [16][8][2] bytes: [c][grp][s] = i0 | i1 << 2, the positions (0..3,
+ *          i0 < i1) of the two kept values of group grp in output column 2c + s.
+ * A group with fewer than two non-zeros keeps zeros at unused positions. */
+int64_t ssl_nm24_block_bytes(void);
 
 /* Up to 4 SLR linears that read the same x (e.g. a layer's q, k and v
  * projections, or its gate and up projections) in ONE launch: each member is

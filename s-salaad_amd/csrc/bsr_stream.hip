@@ -47,6 +47,7 @@
 namespace ssl {
 
 enum : int { MODE_OP = 0, MODE_FUSED = 1 };
+enum : int { SF_BSR = 0, SF_NM24 = 1 };  // sparse block storage
 
 constexpr int kSW = 8;            // waves per streaming workgroup
 constexpr int kST = kSW * kWave;  // threads per streaming workgroup
@@ -416,7 +417,8 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
 // ---------------------------------------------------------------------------
 // Streaming workgroup: one plan chunk for one token tile.
 // ---------------------------------------------------------------------------
-template <int DT, int P, int MT, int MODE, int UNR>
+// SF: storage of the sparse blocks, SF_BSR (q, p) blocks or SF_NM24 packed 2:4 blocks.
+template <int DT, int P, int MT, int MODE, int UNR, int SF>
 __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f32x4* red) {
   constexpr int Q = P;
   constexpr int W = P / 16;
@@ -425,7 +427,9 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   using Frag = typename MM::Frag;
   constexpr int KM = MM::KM;
   constexpr int NKS = Q / KM;
-  using Raw = VRawT<DT, KE, W>;
+  static_assert(SF == SF_BSR || (P == kNmBlock && DT != DT_F32), "2:4 blocks are 32×32, 16-bit");
+  using Raw = typename std::conditional<SF == SF_NM24, NmRaw, VRawT<DT, KE, W>>::type;
+  constexpr int BLK_BYTES = SF == SF_NM24 ? kNmBlockBytes : P * Q * Elem<DT>::bytes;
   constexpr int KEL = (DT == DT_F32) ? 4 : 8;  // low-rank part: widest fragment
   using ML = Mma<DT, KEL>;
   using FragL = typename ML::Frag;
@@ -484,7 +488,7 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
       const int u = u0 + k * kSW;
       if (u < be) {
         const int colb = colk[k];
-        const char* vb = (const char*)a.values + (int64_t)u * (P * Q * EB);
+        const char* vb = (const char*)a.values + (int64_t)u * BLK_BYTES;
         const bool full = colb + Q <= a.m;
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
@@ -502,7 +506,8 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
                                           : zero_frag<DT, KE>();
             }
           }
-          load_vstep<DT, KE, W>(raw[k][ks], vb, P, ks * KM, lane);
+          if constexpr (SF == SF_NM24) load_nm(raw[k][ks], vb, lane);
+          else load_vstep<DT, KE, W>(raw[k][ks], vb, P, ks * KM, lane);
         }
       }
     }
@@ -513,7 +518,9 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
         for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
           for (int s = 0; s < W; ++s) {
-            const Frag vf = vfrag<DT, KE, W>(raw[k][ks], s);
+            Frag vf;
+            if constexpr (SF == SF_NM24) vf = nm_frag<DT>(raw[k][ks], s);
+            else vf = vfrag<DT, KE, W>(raw[k][ks], s);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][s], xf[k][ks][mt], vf);
           }
@@ -646,7 +653,7 @@ struct GroupArgs {
   SlrArgs m[kMaxGroup];
 };
 
-template <int DT, int P, int MT, int MODE, int UNR>
+template <int DT, int P, int MT, int MODE, int UNR, int SF>
 __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_kernel(
     GroupArgs g_by_value) {
   (void)g_by_value;
@@ -669,7 +676,7 @@ __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_ke
   const SlrArgs& a = g.m[i];
   const int lb = sb - g.str_off[i];
   const int mg = lb / a.n_chunks, chunk = lb % a.n_chunks;
-  stream_wg<DT, P, MT, MODE, UNR>(a, chunk, mg, red);
+  stream_wg<DT, P, MT, MODE, UNR, SF>(a, chunk, mg, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -677,7 +684,7 @@ __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_ke
 // ---------------------------------------------------------------------------
 namespace {
 
-template <int DT, int P, int MT>
+template <int DT, int P, int MT, int SF = SF_BSR>
 constexpr int stream_unroll() {
   // Units per wave per batch: a 32-block row in one batch of the 8 waves for
   // 32×32 and 64×64 blocks, fewer units for wide tiles. 16-bit 32×32 kernels stay
@@ -688,11 +695,23 @@ constexpr int stream_unroll() {
   return u / d > 0 ? u / d : 1;
 }
 
-template <int DT, int P, int MT, int MODE>
+template <int DT, int P, int MT, int MODE, int SF = SF_BSR>
 hipError_t launch(const GroupArgs& a, int64_t blocks, hipStream_t s) {
-  constexpr int UNR = stream_unroll<DT, P, MT>();
-  hipLaunchKernelGGL((slr_kernel<DT, P, MT, MODE, UNR>), dim3((unsigned)blocks), dim3(kST), 0, s, a);
+  constexpr int UNR = stream_unroll<DT, P, MT, SF>();
+  hipLaunchKernelGGL((slr_kernel<DT, P, MT, MODE, UNR, SF>), dim3((unsigned)blocks), dim3(kST), 0, s,
+                     a);
   return hipGetLastError();
+}
+
+// The fused linear on 2:4 blocks: 32×32, 16-bit only.
+template <int DT>
+hipError_t dispatch_nm(int MT, const GroupArgs& a, int64_t blocks, hipStream_t s) {
+  switch (MT) {
+    case 1: return launch<DT, kNmBlock, 1, MODE_FUSED, SF_NM24>(a, blocks, s);
+    case 2: return launch<DT, kNmBlock, 2, MODE_FUSED, SF_NM24>(a, blocks, s);
+    case 4: return launch<DT, kNmBlock, 4, MODE_FUSED, SF_NM24>(a, blocks, s);
+  }
+  return hipErrorInvalidValue;
 }
 
 template <int DT, int MODE>
@@ -811,6 +830,8 @@ using namespace ssl;
 extern "C" {
 
 int64_t ssl_prefill_min_rows(void) { return kPrefillMinM; }
+
+int64_t ssl_nm24_block_bytes(void) { return kNmBlockBytes; }
 
 int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p) {
   if (!supported_block(block_p, block_p)) return 1;
@@ -939,10 +960,17 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
   g.n = n_members;
   Layout L[kMaxGroup];
   int64_t n_stream = 0, rt_tiles = 0;
+  const int s_format = members[0].s_format;
+  if (s_format != SSL_S_BSR && s_format != SSL_S_NM24)
+    return fail(SSL_ERR_INVALID, "unknown sparse storage format %d", s_format);
+  if (s_format == SSL_S_NM24 && (block_p != kNmBlock || block_q != kNmBlock || dtype == SSL_F32))
+    return fail(SSL_ERR_UNSUPPORTED, "2:4 blocks are 32x32 with 16-bit activations");
   for (int i = 0; i < n_members; ++i) {
     const ssl_slr_member& mb = members[i];
     if (mb.NB < 0 || mb.r_pad < 0 || mb.n_chunks < 0 || mb.n_slots < 0 || mb.lr_wgs < 0)
       return fail(SSL_ERR_INVALID, "linear %d: negative size", i);
+    if (mb.s_format != s_format)
+      return fail(SSL_ERR_INVALID, "linear %d: all linears of a call share the sparse storage", i);
     if (mb.r_pad % 64) return fail(SSL_ERR_INVALID, "linear %d: r_pad must be a multiple of 64", i);
     if (mb.NB == 0) {  // no output columns: nothing to launch for this linear
       L[i] = slr_layout(M, 0, block_p, 0, m_pad, 0, dtype);
@@ -982,9 +1010,10 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
   }
   if (n_stream == 0) return SSL_OK;
 
-  if (M >= kPrefillMinM && dtype != SSL_F32) {
+  if (M >= kPrefillMinM && dtype != SSL_F32 && s_format == SSL_S_BSR) {
     // Many token rows: the latent GEMM (K split, then combined), then the row
-    // GEMM over groups of block-rows.
+    // GEMM over groups of block-rows. (2:4 blocks stay on the row-streaming
+    // kernel at every M.)
     const int cus = device_cus();
     PfArgs rows{}, lat{};
     rows.x = lat.x = x; rows.ldx = lat.ldx = ldx;
@@ -1076,6 +1105,11 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
   g.lat_off[n_members] = (int)lat;
   g.str_off[n_members] = (int)str;
   g.lat_total = (int)lat;
+  if (s_format == SSL_S_NM24)
+    return check_hip(dtype == SSL_BF16
+                         ? dispatch_nm<DT_BF16>(L[0].MT, g, lat + str, (hipStream_t)stream)
+                         : dispatch_nm<DT_F16>(L[0].MT, g, lat + str, (hipStream_t)stream),
+                     "slr launch (2:4)");
   return check_hip(
       dispatch<MODE_FUSED>(dtype, block_p, L[0].MT, g, lat + str, (hipStream_t)stream),
       "slr launch");

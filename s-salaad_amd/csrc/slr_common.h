@@ -294,6 +294,53 @@ __device__ __forceinline__ typename Mma<DT, KE>::Frag vfrag(const VRawT<DT, KE, 
   return f;
 }
 
+// ---------------------------------------------------------------------------
+// 2:4 blocks (N:M sparse S, two kept values in every group of four consecutive
+// input features). A stored 32×32 block (32 input features k × 32 output
+// columns j, the orientation of the (q, p) blocks) is kNmBlockBytes bytes:
+//   values [16][16][2] 16-bit: [c][i][s] = the i-th kept value (k ascending)
+//          of output column 2c + s, i.e. group i / 2, slot i % 2
+//   index  [16][8][2] bytes:   [c][grp][s] = i0 | i1 << 2, the positions
+//          (0..3, i0 < i1) of the group's two kept values in column 2c + s
+// Lane (c, g) of a wave covers columns 2c, 2c + 1 and k ∈ [8g, 8g + 8): one
+// 16-byte piece of values at 64c + 16g and four index bytes at 1024 + 16c + 4g,
+// so one load instruction reads 1 KiB contiguous.
+// ---------------------------------------------------------------------------
+constexpr int kNmBlock = 32;
+constexpr int kNmBlockBytes = 1280;
+
+struct NmRaw {
+  uint4 v;
+  uint32_t idx;
+};
+
+__device__ __forceinline__ void load_nm(NmRaw& r, const char* blk, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+  r.v = *(const uint4*)(blk + 64 * c + 16 * g);
+  r.idx = *(const uint32_t*)(blk + 1024 + 16 * c + 4 * g);
+}
+
+// The dense MFMA B fragment (8 consecutive k of output column 2c + s) of a lane's piece.
+template <int DT>
+__device__ __forceinline__ typename Mma<DT, 8>::Frag nm_frag(const NmRaw& r, int s) {
+  typename Mma<DT, 8>::Frag f;
+  const uint32_t w[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // kept values of column s, group h: packed i = 2h, 2h + 1 → word i, half s
+    const uint32_t v0 = (w[2 * h] >> (16 * s)) & 0xffffu;
+    const uint32_t v1 = (w[2 * h + 1] >> (16 * s)) & 0xffffu;
+    const uint32_t ix = (r.idx >> (8 * (2 * h + s))) & 0xffu;
+    const uint32_t i0 = ix & 3u, i1 = (ix >> 2) & 3u;
+    uint32_t e[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) e[t] = (i0 == (uint32_t)t) ? v0 : ((i1 == (uint32_t)t) ? v1 : 0u);
+    f.d[2 * h] = e[0] | (e[1] << 16);
+    f.d[2 * h + 1] = e[2] | (e[3] << 16);
+  }
+  return f;
+}
+
 __device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // Wave-uniform read of a structure array that no kernel writes (column indices,

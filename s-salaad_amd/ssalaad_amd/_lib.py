@@ -52,6 +52,7 @@ _SIGNATURES = {
         [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p],
     ),
     "ssl_prefill_min_rows": (_c_i64, []),
+    "ssl_nm24_block_bytes": (_c_i64, []),
     "ssl_prefill_group": (_c_i32, [_c_i64, _c_i64, _c_i32]),
     "ssl_slr_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32]),
     "ssl_slr_counter_count": (_c_i64, [_c_i64, _c_i64]),
@@ -89,7 +90,7 @@ class SlrMember(ctypes.Structure):
         ("counters", _c_p), ("n_counters", _c_i64), ("exchange", _c_p),
         ("exchange_bytes", _c_i64), ("workspace", _c_p), ("workspace_bytes", _c_i64),
         ("pf_groups", _c_p), ("pf_entries", _c_p), ("pf_n_groups", _c_i64), ("pf_group", _c_i32),
-        ("nnz", _c_i64), ("values_pq", _c_p),
+        ("nnz", _c_i64), ("values_pq", _c_p), ("s_format", _c_i32),
     ]
 
 

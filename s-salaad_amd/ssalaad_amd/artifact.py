@@ -72,3 +72,60 @@ def encode_for_kernels(S: torch.Tensor, block_p: int, block_q: int):
     """Dense (n, m) -> (crow int32, col int32, values (nnz, q, p), active_rows int32)."""
     crow, col, _, vt, active = _encode(S, block_p, block_q, False, True)
     return crow, col, vt, active
+
+
+NM_BLOCK = 32  # 2:4 blocks: 32 input × 32 output features
+
+
+def nm24_pack(S: torch.Tensor) -> dict:
+    """2:4-sparse dense S [n, m] (16-bit, on the GPU) → the kernels' packed blocks.
+
+    At most two of every four consecutive entries of a row (input features
+    4g .. 4g + 3) may be non-zero (the pattern ssalaad/inference/egar.py:285-293
+    produces). The matrix is cut into 32×32 blocks (zero padded at the edges);
+    blocks with a non-zero are stored row-major in the layout `ssl_nm24_block_bytes`
+    documents: the two kept values of every group and their positions. Groups
+    with fewer than two non-zeros keep zeros at unused positions.
+    Returns {crow, col, active_rows (int32), blocks (uint8 [nnz, 1280]), NB, NBK}.
+    """
+    if S.dim() != 2:
+        raise ValueError("S must be 2-D")
+    if S.device.type != "cuda":
+        raise ValueError("the 2:4 packer runs on a ROCm GPU device; move S there first")
+    if S.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("2:4 S needs 16-bit values (bf16 or fp16)")
+    return _nm24_pack(S)
+
+
+def _nm24_pack(S: torch.Tensor) -> dict:
+    n, m = S.shape
+    if m % 4:
+        raise ValueError(f"in_features {m} is not a multiple of 4 (2:4 groups)")
+    P = NM_BLOCK
+    NB, NBK = -(-n // P), -(-m // P)
+    Sp = torch.zeros(NB * P, NBK * P, dtype=S.dtype, device=S.device)
+    Sp[:n, :m] = S
+    G = NBK * P // 4
+    Sg = Sp.view(NB * P, G, 4)
+    nz = Sg != 0
+    if bool((nz.sum(-1) > 2).any()):
+        raise ValueError("S is not 2:4: a group of four input features holds more than two non-zeros")
+    # the (up to) two non-zero positions of each group, lowest first; empty
+    # slots take other positions, whose values are zero
+    key = nz.to(torch.int32) * (8 - torch.arange(4, device=S.device, dtype=torch.int32)) + (
+        3 - torch.arange(4, device=S.device, dtype=torch.int32))
+    idx = key.topk(2, dim=-1).indices.sort(dim=-1).values           # [rows, G, 2], i0 < i1
+    vals = torch.gather(Sg, -1, idx)                                 # [rows, G, 2]
+    ib = (idx[..., 0] | (idx[..., 1] << 2)).to(torch.uint8)          # [rows, G]
+    # blocks: [by][bc] → values [c][i = 2·grp + slot][s], index [c][grp][s]
+    v = vals.view(NB, 16, 2, NBK, 8, 2).permute(0, 3, 1, 4, 5, 2).reshape(NB, NBK, 512)
+    x = ib.view(NB, 16, 2, NBK, 8).permute(0, 3, 1, 4, 2).reshape(NB, NBK, 256)
+    blocks = torch.cat([v.contiguous().view(torch.uint8).view(NB, NBK, 1024), x], dim=-1)
+    keep = nz.view(NB, P, NBK, 8, 4).any(dim=4).any(dim=3).any(dim=1)  # [NB, NBK]
+    counts = keep.sum(dim=1)
+    crow = torch.zeros(NB + 1, dtype=torch.int32, device=S.device)
+    crow[1:] = counts.cumsum(0).to(torch.int32)
+    col = keep.nonzero(as_tuple=False)[:, 1].to(torch.int32)
+    active = (counts > 0).nonzero(as_tuple=False).squeeze(-1).to(torch.int32)
+    return dict(crow=crow, col=col, active_rows=active, blocks=blocks[keep].contiguous(), NB=NB,
+                NBK=NBK)

@@ -19,7 +19,9 @@ Differences from the reference, all extensions:
     the padding must be zero, and y is returned at the true width;
   * no CPU path: the library is the GPU kernels, so CPU tensors are rejected
     (the reference's AVX2 CPU class, :140-164, is the oracle's baseline instead);
-  * N:M (2:4) S is rejected (out of this library's scope).
+  * N:M (2:4) S (nm_n=2, nm_m=4, :167-224) runs on the same fused kernel with
+    S packed into 32×32 blocks of kept values and positions (16-bit only)
+    instead of the semi-structured tensor of cuSPARSELt.
 """
 
 from __future__ import annotations
@@ -65,7 +67,14 @@ class _KernelState:
         if mod.bias is not None:
             b = mod.bias.to(dtype)
             self.bias = b if (self.n_pad == n and b.is_contiguous()) else F.pad(b, (0, self.n_pad - n)).contiguous()
-        if mod.S_nnz > 0:
+        self.s_format = 1 if getattr(mod, "kind", "") == "nm" else 0
+        if self.s_format == 1:
+            self.col = mod._nm_col
+            self.values = mod._nm_blocks
+            crow_h = mod._nm_crow.detach().to("cpu").numpy().astype(np.int32)
+            self.col_h = mod._nm_col.detach().to("cpu").numpy().astype(np.int32)
+            self.nblk_total = int(crow_h[-1])
+        elif mod.S_nnz > 0:
             self.col = mod.S_col
             self.values = mod.S_values
             crow_h = mod.S_crow.detach().to("cpu").numpy().astype(np.int32)
@@ -106,7 +115,8 @@ class _KernelState:
 
     def takes_prefill(self, M: int) -> bool:
         lib = _lib.load()
-        return M >= lib.ssl_prefill_min_rows() and self.dtype_code != _lib.SSL_F32
+        return (M >= lib.ssl_prefill_min_rows() and self.dtype_code != _lib.SSL_F32
+                and self.s_format == 0)
 
     def prefill_plan(self, G: int) -> _runtime.DevicePrefillPlan:
         """The prefill row kernel's plan with G block-rows per workgroup."""
@@ -170,6 +180,7 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
             mb.workspace = ws.data_ptr() + ws_off
             mb.workspace_bytes = ws_need[i]
             mb.nnz = st.nblk_total
+            mb.s_format = st.s_format
             if G:
                 pp = st.prefill_plan(G)
                 mb.pf_groups, mb.pf_entries = pp.groups.data_ptr(), pp.entries.data_ptr()
@@ -321,6 +332,51 @@ class _LRSLinearLRBlockHIP(_LRSLinearLRBlockBase):
             raise ValueError("The HIP block kernel requires fp16, bf16 or fp32.")
 
 
+class _LRSLinearLRNMHIP(_LRSLinearBase):
+    """2:4 (N:M) S on the gfx950 streaming kernel (replaces ls_linear.py:167-219).
+
+    S is packed once into 32×32 blocks holding the two kept values of every
+    group of four input features and their positions (artifact.nm24_pack); the
+    kernel expands each block into MFMA fragments in registers, so a decode
+    call streams about 5/8 of the dense block bytes. The fused launch adds
+    t·Aᵀ and the bias as for block-sparse S. As in the reference's N:M class,
+    the packed S is not part of the state dict (non-persistent buffers).
+    """
+
+    kind = "nm"
+
+    def __init__(self, A, B, S_dense, *, in_features, out_features, bias) -> None:
+        super().__init__(A, B, in_features=in_features, out_features=out_features, bias=bias)
+        if tuple(S_dense.shape) != (out_features, in_features):
+            raise ValueError(
+                f"S shape {tuple(S_dense.shape)} must equal "
+                f"(out_features, in_features)=({out_features},{in_features})"
+            )
+        from .artifact import NM_BLOCK, nm24_pack
+
+        packed = nm24_pack(S_dense.to(A.dtype))
+        self._kernel_block = NM_BLOCK
+        self.block_p = self.block_q = None
+        self.S_nnz = int(packed["blocks"].shape[0]) * NM_BLOCK * NM_BLOCK // 2
+        self.register_buffer("_nm_crow", packed["crow"], persistent=False)
+        self.register_buffer("_nm_col", packed["col"], persistent=False)
+        self.register_buffer("_nm_blocks", packed["blocks"], persistent=False)
+        self._nm_dtype = A.dtype  # the dtype the packed values are stored in
+
+    def _kernel(self) -> _KernelState:
+        if self.A.dtype != self._nm_dtype:
+            raise TypeError(
+                f"the 2:4 blocks were packed as {self._nm_dtype}; rebuild the module to run in "
+                f"{self.A.dtype}"
+            )
+        return super()._kernel()
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"rank={self.r}, S_nnz={self.S_nnz}, N:M 2:4 (32×32 packed blocks), "
+                f"bias={self.bias is not None}")
+
+
 def LRSLinear(
     A,
     B,
@@ -348,7 +404,12 @@ def LRSLinear(
     if nnz == 0:
         return _LRSLinearLR(A, B, **kwargs)
     if nm_n is not None:
-        raise ValueError("N:M (2:4) S is not supported by the HIP kernels.")
+        if (nm_n, nm_m) != (2, 4) or not A.is_cuda:
+            raise ValueError("N:M inference requires CUDA and a 2:4 mask.")
+        if A.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("The HIP 2:4 kernel requires fp16 or bf16.")
+        dense = S_sparse if S_sparse.layout == torch.strided else S_sparse.to_dense()
+        return _LRSLinearLRNMHIP(A, B, dense.to(A.device), **kwargs)
     if block_p is None or block_q is None:
         raise ValueError("Sparse S needs a recorded block shape to pick a kernel.")
     if block_p != block_q or block_p not in SUPPORTED_BLOCK_SIZES:
@@ -390,6 +451,8 @@ class LRSLinearGroup(nn.Module):
                 raise ValueError("group members must share in_features (they read the same x)")
             if mod.A.dtype != first.A.dtype or mod.A.device != first.A.device:
                 raise ValueError("group members must share dtype and device")
+            if (getattr(mod, "kind", "") == "nm") != (getattr(first, "kind", "") == "nm"):
+                raise ValueError("group members must share the sparse storage (2:4 or blocks)")
             if mod._kernel_block != first._kernel_block:
                 raise ValueError(
                     f"group members must share the block size, got {first._kernel_block} and "

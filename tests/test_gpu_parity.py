@@ -548,3 +548,106 @@ def test_no_workgroup_gave_up_waiting_for_the_latent(gpu_device):
         mod(to_dev(make_x(prob, M), torch.bfloat16, gpu_device))
     torch.cuda.synchronize()
     assert latent_wait_status(gpu_device) == 0
+
+
+# ------------------------------------------------------------ 2:4 (N:M) S --
+
+
+def _nm24(n, m, seed, dtype):
+    """Random 2:4 S (0, 1 or 2 non-zeros in every group of four input features)."""
+    rng = np.random.default_rng(seed)
+    count = rng.choice(3, size=(n, m // 4), p=[0.15, 0.25, 0.6])        # kept per group
+    rank = np.argsort(rng.random((n, m // 4, 4)), axis=-1).argsort(axis=-1)  # random order
+    keep = rank < count[..., None]
+    S = (rng.standard_normal((n, m // 4, 4)) * 0.05 * keep).reshape(n, m)
+    return torch.from_numpy(S).to(dtype).double().numpy()
+
+
+def _nm_module(n, m, r, dtype, dev, seed, bias=True):
+    rng = np.random.default_rng(seed + 1)
+    A = rng.standard_normal((n, r)) * 0.05
+    B = rng.standard_normal((r, m)) * 0.05
+    b = rng.standard_normal(n) * 0.1 if bias else None
+    A, B = (torch.from_numpy(t).to(dtype).double().numpy() for t in (A, B))
+    if b is not None:
+        b = torch.from_numpy(b).to(dtype).double().numpy()
+    S = _nm24(n, m, seed, dtype)
+    mod = LRSLinear(to_dev(A, dtype, dev), to_dev(B, dtype, dev), to_dev(S, dtype, dev),
+                    in_features=m, out_features=n,
+                    bias=None if b is None else to_dev(b, dtype, dev), nm_n=2, nm_m=4)
+    return mod, (A, B, S, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("shape", [(256, 192, 64), (100, 200, 24), (64, 4096, 256)])
+@pytest.mark.parametrize("M", [1, 16, 33, 130])
+def test_nm24_module_matches_oracle(dtype, shape, M, gpu_device):
+    n, m, r = shape
+    mod, (A, B, S, b) = _nm_module(n, m, r, dtype, gpu_device, seed=n + m + M)
+    assert mod.kind == "nm" and "S_nm" not in dict(mod.named_buffers())
+    x = np.random.default_rng(M).standard_normal((M, m))
+    x = torch.from_numpy(x).to(dtype).double().numpy()
+    xt = to_dev(x, dtype, gpu_device)
+    y1, y2 = mod(xt), mod(xt)
+    torch.cuda.synchronize()
+    want = orc.slr_linear(x, A, B, S, b)
+    assert y1.shape == (M, n)
+    assert err(y1, want) <= TOL[dtype]
+    assert torch.equal(y1, y2)
+    assert latent_wait_status(gpu_device) == 0
+
+
+def test_nm24_pack_round_trip_and_rules(gpu_device):
+    from ssalaad_amd.artifact import nm24_pack
+
+    S = _nm24(70, 100, 5, torch.bfloat16)
+    S[32:64, 32:64] = 0                                        # an empty block is not stored
+    pk = nm24_pack(to_dev(S, torch.bfloat16, gpu_device))
+    crow, col = pk["crow"].cpu().numpy(), pk["col"].cpu().numpy()
+    blocks = pk["blocks"].cpu()
+    D = np.zeros((pk["NB"] * 32, pk["NBK"] * 32))
+    for by in range(pk["NB"]):
+        for k in range(crow[by], crow[by + 1]):
+            vals = blocks[k, :1024].view(torch.bfloat16).float().numpy().reshape(16, 16, 2)
+            ix = blocks[k, 1024:].numpy().reshape(16, 8, 2)
+            for c in range(16):
+                for s_ in range(2):
+                    for grp in range(8):
+                        i0, i1 = ix[c, grp, s_] & 3, ix[c, grp, s_] >> 2
+                        assert i0 < i1
+                        D[by * 32 + 2 * c + s_, col[k] * 32 + 4 * grp + i0] = vals[c, 2 * grp, s_]
+                        D[by * 32 + 2 * c + s_, col[k] * 32 + 4 * grp + i1] = vals[c, 2 * grp + 1, s_]
+    assert np.array_equal(D[:70, :100], S)
+    assert crow[-1] == pk["NB"] * pk["NBK"] - 1
+    bad = S.copy()
+    bad[3, 0:3] = 1.0                                          # three non-zeros in one group
+    with pytest.raises(ValueError, match="not 2:4"):
+        nm24_pack(to_dev(bad, torch.bfloat16, gpu_device))
+    A, B = torch.zeros(64, 8, device=gpu_device), torch.zeros(8, 64, device=gpu_device)
+    with pytest.raises(ValueError, match="fp16 or bf16"):
+        LRSLinear(A, B, torch.ones(64, 64, device=gpu_device), in_features=64, out_features=64,
+                  nm_n=2, nm_m=4)
+
+
+def test_nm24_group_and_mixing_rules(gpu_device):
+    dtype = torch.bfloat16
+    mods = [_nm_module(n, 160, r, dtype, gpu_device, seed=7 + n)[0] for n, r in ((96, 32), (64, 16))]
+    grp = ssalaad_amd.LRSLinearGroup(*mods)
+    x = to_dev(np.random.default_rng(9).standard_normal((5, 160)), dtype, gpu_device)
+    ys = grp(x)
+    torch.cuda.synchronize()
+    for y, mod in zip(ys, mods):
+        assert torch.equal(y, mod(x))
+    blk = _module(make_problem(96, 160, 8, 32, 0.5, dtype, seed=3), gpu_device)
+    with pytest.raises(ValueError, match="sparse storage"):
+        ssalaad_amd.LRSLinearGroup(mods[0], blk)
+
+
+def test_nm24_llama7b_ffn_shape_decode(gpu_device):
+    """11008×4096 bf16, rank 256, 2:4 S: one fused launch per call."""
+    mod, (A, B, S, b) = _nm_module(11008, 4096, 256, torch.bfloat16, gpu_device, seed=31, bias=False)
+    x = np.random.default_rng(2).standard_normal((4, 4096))
+    x = torch.from_numpy(x).to(torch.bfloat16).double().numpy()
+    y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, orc.slr_linear(x, A, B, S, b)) <= 1e-2

@@ -53,11 +53,14 @@ def test_cpu_tensors_have_no_fallback():
                   block_p=16, block_q=16)
 
 
-def test_nm_is_rejected():
+def test_nm_needs_a_gpu_and_a_2_4_mask():
+    """ls_linear.py:254-256: N:M runs on the GPU with a 2:4 mask only."""
     A, B = torch.randn(32, 4), torch.randn(4, 32)
     S = _block_sparse(32, 32, 16, [(0, 0)])
-    with pytest.raises(ValueError, match="N:M"):
+    with pytest.raises(ValueError, match="N:M inference requires CUDA and a 2:4 mask"):
         LRSLinear(A, B, S, in_features=32, out_features=32, nm_n=2, nm_m=4)
+    with pytest.raises(ValueError, match="N:M inference requires CUDA and a 2:4 mask"):
+        LRSLinear(A, B, S, in_features=32, out_features=32, nm_n=1, nm_m=4)
 
 
 def test_zero_s_gives_the_low_rank_module():
