@@ -45,6 +45,13 @@ headline):
                        heads, FFN 1376, vocab 32000) with every q/k/v/o/gate/
                        up/down an SLR linear (rank dim/4, 32×32 blocks at 50%,
                        N(0, 0.02)), fp32 forward of 8 × 256 tokens: tok/s
+  llama1b_decode_step  the whole KV-cached decode step of the LLaMA-1B-shaped
+                       model (the projection stack above, plus RMSNorm, rotary
+                       embedding, attention over a 1024-token context of
+                       synthetic keys/values, SiLU, residuals and a 32000-word
+                       LM head), --batch sequences (default 16), one HIP graph
+                       per step: tok/s, and GB/s of the step's compulsory
+                       bytes (weights plus the keys and values read)
 """
 
 from __future__ import annotations
@@ -385,7 +392,92 @@ def run_workload(args) -> dict:
                             "block_density": 0.5, "batch": 8, "seq_len": 256,
                             "slr_weight_bytes": total_bytes, "parallelism": "single_gpu"},
                     roofline=None)
+    if args.workload == "llama1b_decode_step":
+        return run_decode_step(args, base, gen, dev)
     raise SystemExit(f"unknown workload {args.workload}")
+
+
+def run_decode_step(args, base: dict, gen, dev) -> dict:
+    """The LLaMA-1B-shaped decode step through DecodeEngine at a 1024-token context."""
+    import torch
+    from torch import nn
+
+    from ssalaad_amd import DecodeEngine
+    from ssalaad_amd.bundle import build_model_from_config
+
+    B = args.batch if args.batch_set else 16
+    ctx, vocab, h, f, layers = 1024, 32000, 2048, 5461, args.layers
+    dtype = torch.bfloat16
+    cfg = {"model_type": "llama", "hidden_size": h, "intermediate_size": f,
+           "num_hidden_layers": layers, "num_attention_heads": 16, "num_key_value_heads": 16,
+           "head_dim": 128, "vocab_size": vocab, "max_position_embeddings": ctx,
+           "rms_norm_eps": 1e-5, "rope_theta": 500000.0, "hidden_act": "silu",
+           "tie_word_embeddings": False}
+    t0 = time.time()
+    with torch.device("meta"):
+        model = build_model_from_config(cfg, attn_implementation="sdpa")
+    model = model.to_empty(device=dev).to(dtype)
+    with torch.no_grad():
+        model.model.embed_tokens.weight.copy_(torch.randn(vocab, h, generator=gen).to(dtype))
+        model.lm_head.weight.copy_((torch.randn(vocab, h, generator=gen) * 0.02).to(dtype))
+        for name, prm in model.named_parameters():
+            if "norm" in name:
+                prm.fill_(1.0)
+    model.model.rotary_emb = type(model.model.rotary_emb)(config=model.config, device=dev)
+    slr_bytes = 0
+    for li in range(layers):
+        lay = model.model.layers[li]
+        for part, proj, (nm, n, m) in zip(
+                ["self_attn"] * 4 + ["mlp"] * 3,
+                ["q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"],
+                llama1b_shapes()):
+            mod = make_linear(n, m, 256, 32, 0.5, gen, dev, dtype)
+            slr_bytes += algorithmic_bytes(mod, 0, 2)["total"]
+            setattr(getattr(lay, part), proj, mod)
+    model.eval()
+    torch.cuda.synchronize()
+    _log(f"[bench] built the {layers}-layer decode model in {time.time() - t0:.1f}s")
+    eng = DecodeEngine(model, max_batch=B, max_context=ctx)
+    with torch.no_grad():  # a full synthetic context: keys and values ~N(0, 1)
+        for li in range(layers):
+            eng.k_cache[li].copy_(torch.randn(eng.k_cache[li].shape, generator=gen).to(dtype))
+            eng.v_cache[li].copy_(torch.randn(eng.v_cache[li].shape, generator=gen).to(dtype))
+    tokens = torch.randint(0, vocab, (B,), generator=gen)
+    positions = [ctx - 1] * B
+    logits = eng.step(tokens, positions)  # eager run, then capture
+    logits = eng.step(tokens, positions)
+    torch.cuda.synchronize()
+    finite = bool(torch.isfinite(logits).all())
+    g, _ = eng._graphs[B]
+    s = eng._stream
+    with torch.cuda.stream(s):
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(args.steps):
+            g.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    kv_bytes = layers * B * 2 * 16 * ctx * 128 * 2
+    head_bytes = vocab * h * 2 + B * vocab * 2
+    norm_bytes = (2 * layers + 1) * h * 2
+    total = slr_bytes + kv_bytes + head_bytes + norm_bytes + B * h * 2
+    gbs = total / (ms * 1e-3) / 1e9
+    return dict(base, metric="LLaMA-1B decode step tok/s (KV cache, 1024-token context)",
+                value=round(B / (ms * 1e-3), 1), unit="tok/s", ms_per_step=round(ms, 4),
+                dtype="bf16",
+                config={"workload": "llama1b_decode_step", "layers": layers, "hidden": h,
+                        "ffn": f, "heads": 16, "kv_heads": 16, "head_dim": 128,
+                        "vocab": vocab, "context": ctx, "batch_sequences": B, "rank": 256,
+                        "block": 32, "block_density": 0.5, "parallelism": "single_gpu"},
+                roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                          "step_bytes": int(total), "slr_weight_bytes": int(slr_bytes),
+                          "kv_bytes": int(kv_bytes), "lm_head_bytes": int(head_bytes)},
+                logits_finite=finite)
 
 
 def copy_probe(mib: int, reps: int) -> None:
@@ -514,7 +606,8 @@ def main():
                     help="only run a plain device copy of MIB MiB (counter calibration)")
     ap.add_argument("--workload", default="llama1b_decode",
                     choices=["llama1b_decode", "llama7b_ffn_decode", "llama7b_ffn_prefill",
-                             "llama7b_ffn_decode_nm24", "block_topk", "llama60m_forward"])
+                             "llama7b_ffn_decode_nm24", "block_topk", "llama60m_forward",
+                             "llama1b_decode_step"])
     args = ap.parse_args()
     args.batch_set = args.batch is not None
     if args.batch is None:

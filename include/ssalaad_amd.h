@@ -268,6 +268,67 @@ int ssl_bsr_encode_fill(const void* S, int64_t lds, int64_t NB, int64_t NBK,
                         const uint8_t* flags, const int32_t* crow, int32_t* col,
                         void* values_bsr, void* values_t, void* stream);
 
+/* -------------------------------------------------------------------------
+ * KV-cached decode step: the pieces of a LLaMA / Qwen3 decoder layer around
+ * its SLR linears, for one new token per sequence. The reference has no
+ * cached decode: its greedy generation recomputes the whole prefix with the
+ * Hugging Face forward every step (ssalaad/inference/generate.py:1-26). These
+ * calls reproduce that forward's per-token arithmetic (transformers'
+ * LlamaDecoderLayer / Qwen3DecoderLayer) from a cache. Batch row b is
+ * sequence slot b; `pos` (device int32 [rows]) is each row's position, which
+ * must lie in [0, max_ctx). Caches are [slots, kv_heads, max_ctx, head_dim] in
+ * the model dtype, 16-byte aligned.
+ * ------------------------------------------------------------------------- */
+
+/* h += delta (skipped when delta is NULL), rounded to the dtype; then
+ * out = weight · (h · rsqrt(mean(h²) + eps)) with LlamaRMSNorm's rounding
+ * points. h [rows, ldh] is updated in place (the residual stream). */
+int ssl_add_rmsnorm(void* h, int64_t ldh, const void* delta, int64_t ldd, const void* weight,
+                    void* out, int64_t ldo, int64_t rows, int64_t hidden, float eps,
+                    int32_t dtype, void* stream);
+
+/* The layer-0 input: h[row] = embed[tokens[row]] (embed [vocab, lde]; a token
+ * outside [0, vocab) gives a zero row), then out = weight · norm(h) as above.
+ * hidden at most 8192 for both calls. */
+int ssl_embed_rmsnorm(const void* embed, int64_t lde, int64_t vocab, const int64_t* tokens,
+                      void* h, int64_t ldh, const void* weight, void* out, int64_t ldo,
+                      int64_t rows, int64_t hidden, float eps, int32_t dtype, void* stream);
+
+/* Rotary embedding of q [rows, ldq] (heads·head_dim used) into q_out
+ * [rows, heads, head_dim] and of k into k_cache at (row, head, pos[row]); v
+ * is copied into v_cache at the same place. cos/sin tables are
+ * [max_ctx, head_dim] in the dtype (the model's rotary embedding evaluated at
+ * every position). q_norm / k_norm ([head_dim], may be NULL) apply Qwen3's
+ * per-head RMSNorm first. head_dim even and at most 256. */
+int ssl_rope_kv_append(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                       int64_t ldv, const void* cos_table, const void* sin_table,
+                       const void* q_norm, const void* k_norm, float eps, const int32_t* pos,
+                       void* q_out, void* k_cache, void* v_cache, int64_t rows, int32_t heads,
+                       int32_t kv_heads, int32_t head_dim, int64_t max_ctx, int32_t dtype,
+                       void* stream);
+
+/* out[row, h·head_dim + d] = softmax_j(q·k_j · scale) · v_j over positions
+ * j ≤ pos[row] of the row's cache, with query head h reading key/value head
+ * h / (heads / kv_heads). fp32 accumulation, one rounding at the store.
+ * The context is cut into n_split slices whose partials are merged by a
+ * second kernel; ssl_decode_attention_splits proposes n_split for a batch,
+ * the workspace (ssl_decode_attention_workspace_size bytes, 16-byte aligned)
+ * holds the partials. head_dim 64, 128 or 256; q [rows, heads, head_dim]. */
+int32_t ssl_decode_attention_splits(int64_t rows, int32_t heads, int32_t kv_heads,
+                                    int64_t max_ctx);
+int64_t ssl_decode_attention_workspace_size(int64_t rows, int32_t heads, int32_t head_dim,
+                                            int32_t n_split);
+int ssl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                         const int32_t* pos, void* out, int64_t ldo, int64_t rows, int32_t heads,
+                         int32_t kv_heads, int32_t head_dim, int64_t max_ctx, float scale,
+                         int32_t n_split, void* workspace, int64_t workspace_bytes,
+                         int32_t dtype, void* stream);
+
+/* out = silu(gate) · up (LlamaMLP's act_fn(gate_proj(x)) * up_proj(x)), silu
+ * rounded to the dtype before the product. */
+int ssl_silu_mul(const void* gate, int64_t ldg, const void* up, int64_t ldu, void* out,
+                 int64_t ldo, int64_t rows, int64_t n, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,625 @@
+// Decode-step kernels around the SLR linears of a LLaMA / Qwen3 decoder layer:
+// one new token per sequence, keys and values kept in a per-layer cache.
+//
+//   add_rmsnorm   h += delta (rounded to the model dtype), out = w · norm(h);
+//                 or h = embed[token] first (the layer-0 input)
+//   rope_kv       q/k rotary embedding (after Qwen3's per-head RMSNorm), k and v
+//                 written into the cache at the sequence's position
+//   attn_split    softmax(q·Kᵀ·scale)·V over one slice of a sequence's context,
+//                 per wave an online softmax, the slice's partial (max, sum, o)
+//   attn_combine  the slices' partials merged into the head's output
+//   silu_mul      silu(gate) · up
+//
+// Rounding points follow transformers' LlamaRMSNorm / apply_rotary_pos_emb /
+// LlamaMLP (transformers 5.15.0, models/llama/modeling_llama.py): every torch
+// operation on a 16-bit tensor rounds its fp32 result to the tensor's dtype.
+// The attention itself accumulates in fp32 and rounds once at the output.
+//
+// Caches are [slots, kv_heads, max_ctx, head_dim] per layer; batch row b uses
+// slot b. All loads of keys and values are 16-byte vectors, one row of a head
+// spread over head_dim·elem/16 lanes, so a wave reads whole rows contiguously.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "abi_internal.h"
+#include "slr_common.h"
+
+namespace ssl {
+namespace {
+
+template <int DT>
+__device__ __forceinline__ float rnd(float f) {
+  if constexpr (DT == DT_F32) return f;
+  else if constexpr (DT == DT_BF16) return bf16_to_f32(f32_to_bf16(f));
+  else return f16_to_f32(f32_to_f16(f));
+}
+
+template <int DT>
+__device__ __forceinline__ void store_scalar(void* p, int64_t i, float f) {
+  if constexpr (DT == DT_F32) ((float*)p)[i] = f;
+  else ((uint16_t*)p)[i] = (uint16_t)to_bits<DT>(f);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// add_rmsnorm: one workgroup per row, K elements per thread (hidden <= 256·K)
+// held in registers, so every load of the row is issued before the first use.
+// With `tokens` the row is first gathered from the embedding table (h =
+// embed[token]; a token outside [0, vocab) gives a zero row).
+// ---------------------------------------------------------------------------
+template <int DT, int K>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(
+    void* __restrict__ h, int64_t ldh, const void* __restrict__ delta, int64_t ldd,
+    const void* __restrict__ w, void* __restrict__ out, int64_t ldo, int hidden, float eps,
+    const void* __restrict__ embed, int64_t lde, const int64_t* __restrict__ tokens,
+    int64_t vocab) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const void* src = h;
+  int64_t srow = row * ldh;
+  bool valid = true;
+  if (tokens) {
+    const int64_t t = tokens[row];
+    valid = t >= 0 && t < vocab;
+    src = embed;
+    srow = valid ? t * lde : 0;
+  }
+  float v[K], d[K], wv[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int i = tid + 256 * k;
+    v[k] = (i < hidden && valid) ? load_scalar<DT>(src, srow + i) : 0.f;
+    d[k] = (i < hidden && delta) ? load_scalar<DT>(delta, row * ldd + i) : 0.f;
+    wv[k] = i < hidden ? load_scalar<DT>(w, i) : 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    if (delta) v[k] = rnd<DT>(v[k] + d[k]);
+    ss += v[k] * v[k];
+  }
+  if (delta || tokens) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int i = tid + 256 * k;
+      if (i < hidden) store_scalar<DT>(h, row * ldh + i, v[k]);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float rs = rsqrtf(tot / (float)hidden + eps);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int i = tid + 256 * k;
+    if (i < hidden) store_scalar<DT>(out, row * ldo + i, wv[k] * rnd<DT>(v[k] * rs));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// rope_kv: one wave per (row, head slot); slots [0, heads) are query heads,
+// [heads, heads + kv_heads) key heads (whose value head is copied alongside).
+// head_dim <= 256: a lane holds at most two rotary pairs (j, j + head_dim/2).
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(64) void rope_kv_kernel(
+    const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+    const void* cos_t, const void* sin_t, const void* q_norm, const void* k_norm, float eps,
+    const int32_t* pos, void* q_out, void* k_cache, void* v_cache, int heads, int kv_heads, int hd,
+    int64_t max_ctx) {
+  // torch rounds q·cos and rotate_half(q)·sin separately before the sum
+#pragma clang fp contract(off)
+  const int slot = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int64_t p = pos[b];
+  if (p < 0 || p >= max_ctx) return;  // the host rejects such positions before launching
+  const bool is_q = slot < heads;
+  const int kh = slot - heads;
+  const void* src = is_q ? q : k;
+  const int64_t soff = is_q ? b * ldq + (int64_t)slot * hd : b * ldk + (int64_t)kh * hd;
+  void* dst = is_q ? q_out : k_cache;
+  const int64_t doff = is_q ? (b * heads + slot) * hd : ((b * kv_heads + kh) * max_ctx + p) * hd;
+  const void* nw = is_q ? q_norm : k_norm;
+  const int half = hd >> 1;
+
+  float x1[2], x2[2];
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int j = lane + 64 * u;
+    x1[u] = x2[u] = 0.f;
+    if (j < half) {
+      x1[u] = load_scalar<DT>(src, soff + j);
+      x2[u] = load_scalar<DT>(src, soff + j + half);
+      ss += x1[u] * x1[u] + x2[u] * x2[u];
+    }
+  }
+  if (nw) {  // Qwen3: RMSNorm over the head's features before the rotation
+    const float rs = rsqrtf(wave_sum(ss) / (float)hd + eps);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = lane + 64 * u;
+      if (j < half) {
+        x1[u] = rnd<DT>(load_scalar<DT>(nw, j) * rnd<DT>(x1[u] * rs));
+        x2[u] = rnd<DT>(load_scalar<DT>(nw, j + half) * rnd<DT>(x2[u] * rs));
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int j = lane + 64 * u;
+    if (j < half) {
+      const float c1 = load_scalar<DT>(cos_t, p * hd + j), s1 = load_scalar<DT>(sin_t, p * hd + j);
+      const float c2 = load_scalar<DT>(cos_t, p * hd + j + half);
+      const float s2 = load_scalar<DT>(sin_t, p * hd + j + half);
+      // rotate_half(x) = (-x2, x1)
+      store_scalar<DT>(dst, doff + j, rnd<DT>(x1[u] * c1) - rnd<DT>(x2[u] * s1));
+      store_scalar<DT>(dst, doff + j + half, rnd<DT>(x2[u] * c2) + rnd<DT>(x1[u] * s2));
+    }
+  }
+  if (!is_q) {
+    const int64_t vs = b * ldv + (int64_t)kh * hd;
+    for (int j = lane; j < hd; j += 64)
+      store_scalar<DT>(v_cache, doff + j, load_scalar<DT>(v, vs + j));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// attn_split: workgroup (split, head block, row). A lane reads 16 bytes (VE
+// elements) of a key/value row; LPR lanes cover a row and a wave instruction
+// reads RPI whole rows. Each wave takes 4·RPI positions per step and keeps its
+// own online softmax (max m, sum l, o) for the GB query heads that share one
+// key/value head; the four waves are merged through LDS at the end.
+// Scores are kept in base 2: s = q·k · scale · log2(e).
+// ---------------------------------------------------------------------------
+template <int DT>
+struct Vec16 {
+  static constexpr int VE = DT == DT_F32 ? 4 : 8;
+  __device__ __forceinline__ static void load(float* f, const void* base, int64_t off) {
+    const uint4 raw = *(const uint4*)((const char*)base + off * Elem<DT>::bytes);
+    if constexpr (DT == DT_F32) {
+      f[0] = __uint_as_float(raw.x);
+      f[1] = __uint_as_float(raw.y);
+      f[2] = __uint_as_float(raw.z);
+      f[3] = __uint_as_float(raw.w);
+    } else {
+      const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (DT == DT_BF16) {
+          f[2 * i] = bf16_to_f32(w[i] & 0xffffu);
+          f[2 * i + 1] = bf16_to_f32(w[i] >> 16);
+        } else {
+          f[2 * i] = f16_to_f32(w[i] & 0xffffu);
+          f[2 * i + 1] = f16_to_f32(w[i] >> 16);
+        }
+      }
+    }
+  }
+};
+
+constexpr int kAttnJ = 4;  // wave instructions (row groups) per step
+
+template <int DT, int HD, int GB>
+__global__ __launch_bounds__(256) void attn_split_kernel(
+    const void* q, const void* kc, const void* vc, const int32_t* pos, int64_t max_ctx, int heads,
+    int kv_heads, int n_split, float scale_log2, float* part_o, float* part_ml) {
+  constexpr int VE = Vec16<DT>::VE;
+  constexpr int LPR = HD / VE;
+  constexpr int RPI = 64 / LPR;
+  constexpr int WSTEP = kAttnJ * RPI;  // positions per wave per step
+  constexpr int STEP = 4 * WSTEP;      // positions per workgroup per step
+  static_assert(LPR <= 64 && (LPR & (LPR - 1)) == 0, "head_dim must give a power-of-two lane count");
+  __shared__ float sh_o[4][GB][HD];
+  __shared__ float sh_m[4][GB];
+  __shared__ float sh_l[4][GB];
+
+  const int split = blockIdx.x;
+  const int G = heads / kv_heads;
+  const int n_hb = (G + GB - 1) / GB;
+  const int kh = blockIdx.y / n_hb;
+  const int g0 = (blockIdx.y % n_hb) * GB;
+  const int ng = min(GB, G - g0);
+  const int64_t b = blockIdx.z;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rr = lane / LPR, vv = lane % LPR;
+
+  const int64_t L = min((int64_t)pos[b] + 1, max_ctx);
+  int64_t per = (L + n_split - 1) / n_split;
+  per = (per + STEP - 1) / STEP * STEP;
+  const int64_t lo = (int64_t)split * per;
+  const int64_t hi = min(lo + per, L);
+
+  float qf[GB][VE];
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    if (g < ng) {
+      Vec16<DT>::load(qf[g], q, (b * heads + (int64_t)kh * G + g0 + g) * HD + vv * VE);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VE; ++e) qf[g][e] = 0.f;
+    }
+  }
+  float m[GB], l[GB], o[GB][VE];
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) o[g][e] = 0.f;
+  }
+  const int64_t head_off = (b * kv_heads + kh) * max_ctx * HD;
+
+  for (int64_t p0 = lo; p0 < hi; p0 += STEP) {
+    float kf[kAttnJ][VE], vf[kAttnJ][VE];
+    bool ok[kAttnJ];
+#pragma unroll
+    for (int j = 0; j < kAttnJ; ++j) {
+      const int64_t p = p0 + wave * WSTEP + j * RPI + rr;
+      ok[j] = p < hi;
+      if (ok[j]) Vec16<DT>::load(kf[j], kc, head_off + p * HD + vv * VE);
+    }
+#pragma unroll
+    for (int j = 0; j < kAttnJ; ++j) {
+      const int64_t p = p0 + wave * WSTEP + j * RPI + rr;
+      if (ok[j]) Vec16<DT>::load(vf[j], vc, head_off + p * HD + vv * VE);
+    }
+    float s[GB][kAttnJ];
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+#pragma unroll
+      for (int j = 0; j < kAttnJ; ++j) {
+        float d = 0.f;
+        if (ok[j]) {
+#pragma unroll
+          for (int e = 0; e < VE; ++e) d += qf[g][e] * kf[j][e];
+        }
+#pragma unroll
+        for (int off = 1; off < LPR; off <<= 1) d += __shfl_xor(d, off);
+        s[g][j] = ok[j] ? d * scale_log2 : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      float mx = s[g][0];
+#pragma unroll
+      for (int j = 1; j < kAttnJ; ++j) mx = fmaxf(mx, s[g][j]);
+#pragma unroll
+      for (int off = LPR; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      const float mn = fmaxf(m[g], mx);
+      if (mn == -INFINITY) continue;  // no valid position for this wave yet
+      const float alpha = exp2f(m[g] - mn);
+      float ps = 0.f;
+      float pj[kAttnJ];
+#pragma unroll
+      for (int j = 0; j < kAttnJ; ++j) {
+        pj[j] = ok[j] ? exp2f(s[g][j] - mn) : 0.f;
+        ps += pj[j];
+      }
+#pragma unroll
+      for (int off = LPR; off < 64; off <<= 1) ps += __shfl_xor(ps, off);
+      l[g] = l[g] * alpha + ps;
+      m[g] = mn;
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        float acc = o[g][e] * alpha;
+#pragma unroll
+        for (int j = 0; j < kAttnJ; ++j)
+          if (ok[j]) acc += pj[j] * vf[j][e];
+        o[g][e] = acc;
+      }
+    }
+  }
+  // sum o over the wave's row groups, then merge the four waves
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+      float acc = o[g][e];
+#pragma unroll
+      for (int off = LPR; off < 64; off <<= 1) acc += __shfl_xor(acc, off);
+      o[g][e] = acc;
+    }
+    if (rr == 0) {
+#pragma unroll
+      for (int e = 0; e < VE; ++e) sh_o[wave][g][vv * VE + e] = o[g][e];
+    }
+    if (lane == 0) {
+      sh_m[wave][g] = m[g];
+      sh_l[wave][g] = l[g];
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < GB * HD; i += 256) {
+    const int g = i / HD, d = i % HD;
+    if (g >= ng) continue;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sh_m[w][g]);
+    float lsum = 0.f, acc = 0.f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float sc = exp2f(sh_m[w][g] - mx);  // 0 for a wave with no position
+        lsum += sh_l[w][g] * sc;
+        acc += sh_o[w][g][d] * sc;
+      }
+    }
+    const int64_t hrow = (b * heads + (int64_t)kh * G + g0 + g) * n_split + split;
+    part_o[hrow * HD + d] = acc;
+    if (d == 0) {
+      part_ml[2 * hrow] = mx;
+      part_ml[2 * hrow + 1] = lsum;
+    }
+  }
+}
+
+// attn_combine: workgroup (head, row); thread d < head_dim.
+template <int DT>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* part_o, const float* part_ml,
+                                                           void* out, int64_t ldo, int heads, int hd,
+                                                           int n_split) {
+  const int h = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int64_t base = (b * heads + h) * n_split;
+  float mx = -INFINITY;
+  for (int s = 0; s < n_split; ++s)
+    if (part_ml[2 * (base + s) + 1] > 0.f) mx = fmaxf(mx, part_ml[2 * (base + s)]);
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    float lsum = 0.f, acc = 0.f;
+    for (int s = 0; s < n_split; ++s) {
+      const float ls = part_ml[2 * (base + s) + 1];
+      if (!(ls > 0.f)) continue;
+      const float sc = exp2f(part_ml[2 * (base + s)] - mx);
+      lsum += ls * sc;
+      acc += part_o[(base + s) * hd + d] * sc;
+    }
+    store_scalar<DT>(out, b * ldo + (int64_t)h * hd + d, lsum > 0.f ? acc / lsum : 0.f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// silu_mul: out = silu(gate) · up, silu rounded to the dtype first (LlamaMLP).
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const void* g, int64_t ldg, const void* u,
+                                                       int64_t ldu, void* out, int64_t ldo,
+                                                       int64_t rows, int64_t n) {
+  const int64_t total = rows * n;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / n, c = i % n;
+    const float gv = load_scalar<DT>(g, r * ldg + c);
+    const float a = rnd<DT>(gv / (1.f + expf(-gv)));
+    store_scalar<DT>(out, r * ldo + c, a * load_scalar<DT>(u, r * ldu + c));
+  }
+}
+
+template <template <int> class K, typename... Args>
+void launch_dt(int dtype, dim3 grid, dim3 block, hipStream_t st, Args... args) {
+  if (dtype == SSL_F32) hipLaunchKernelGGL(K<DT_F32>::fn, grid, block, 0, st, args...);
+  else if (dtype == SSL_BF16) hipLaunchKernelGGL(K<DT_BF16>::fn, grid, block, 0, st, args...);
+  else hipLaunchKernelGGL(K<DT_F16>::fn, grid, block, 0, st, args...);
+}
+
+template <int DT>
+void launch_norm(int hidden, unsigned rows, hipStream_t st, void* h, int64_t ldh,
+                 const void* delta, int64_t ldd, const void* w, void* out, int64_t ldo, float eps,
+                 const void* embed, int64_t lde, const int64_t* tokens, int64_t vocab) {
+  const int k = (hidden + 255) / 256;
+#define SSL_NORM(KK)                                                                           \
+  hipLaunchKernelGGL((add_rmsnorm_kernel<DT, KK>), dim3(rows), dim3(256), 0, st, h, ldh, delta, \
+                     ldd, w, out, ldo, hidden, eps, embed, lde, tokens, vocab)
+  if (k <= 1) SSL_NORM(1);
+  else if (k <= 2) SSL_NORM(2);
+  else if (k <= 4) SSL_NORM(4);
+  else if (k <= 8) SSL_NORM(8);
+  else if (k <= 16) SSL_NORM(16);
+  else SSL_NORM(32);
+#undef SSL_NORM
+}
+
+int norm_launch(int32_t dtype, int hidden, unsigned rows, hipStream_t st, void* h, int64_t ldh,
+                const void* delta, int64_t ldd, const void* w, void* out, int64_t ldo, float eps,
+                const void* embed, int64_t lde, const int64_t* tokens, int64_t vocab) {
+  if (dtype == SSL_F32)
+    launch_norm<DT_F32>(hidden, rows, st, h, ldh, delta, ldd, w, out, ldo, eps, embed, lde, tokens, vocab);
+  else if (dtype == SSL_BF16)
+    launch_norm<DT_BF16>(hidden, rows, st, h, ldh, delta, ldd, w, out, ldo, eps, embed, lde, tokens, vocab);
+  else
+    launch_norm<DT_F16>(hidden, rows, st, h, ldh, delta, ldd, w, out, ldo, eps, embed, lde, tokens, vocab);
+  return check_hip(hipGetLastError(), "rmsnorm launch");
+}
+template <int DT>
+struct Rope { static constexpr auto fn = rope_kv_kernel<DT>; };
+template <int DT>
+struct Combine { static constexpr auto fn = attn_combine_kernel<DT>; };
+template <int DT>
+struct SiluMul { static constexpr auto fn = silu_mul_kernel<DT>; };
+
+template <int DT, int HD>
+int launch_attn_hd(int GB, dim3 grid, hipStream_t st, const void* q, const void* kc,
+                   const void* vc, const int32_t* pos, int64_t max_ctx, int heads, int kv_heads,
+                   int n_split, float sl2, float* po, float* pml) {
+  switch (GB) {
+    case 1: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 1>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 2>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 4>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml); break;
+    default: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 8>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml); break;
+  }
+  return 0;
+}
+
+template <int DT>
+void launch_attn(int hd, int GB, dim3 grid, hipStream_t st, const void* q, const void* kc,
+                 const void* vc, const int32_t* pos, int64_t max_ctx, int heads, int kv_heads,
+                 int n_split, float sl2, float* po, float* pml) {
+  if (hd == 64) launch_attn_hd<DT, 64>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml);
+  else if (hd == 128) launch_attn_hd<DT, 128>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml);
+  else launch_attn_hd<DT, 256>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml);
+}
+
+int head_block(int G) { return G >= 5 ? 8 : (G >= 3 ? 4 : G); }
+
+int check_dtype(int32_t dtype) {
+  if (dtype != SSL_F32 && dtype != SSL_BF16 && dtype != SSL_F16)
+    return fail(SSL_ERR_INVALID, "unknown dtype code %d", dtype);
+  return SSL_OK;
+}
+
+}  // namespace
+}  // namespace ssl
+
+using namespace ssl;
+
+extern "C" int ssl_add_rmsnorm(void* h, int64_t ldh, const void* delta, int64_t ldd,
+                               const void* weight, void* out, int64_t ldo, int64_t rows,
+                               int64_t hidden, float eps, int32_t dtype, void* stream) {
+  clear_error();
+  if (int rc = check_dtype(dtype)) return rc;
+  if (rows < 0 || rows > 65535 * 1024LL || hidden <= 0)
+    return fail(SSL_ERR_INVALID, "add_rmsnorm: rows %lld, hidden %lld", (long long)rows,
+                (long long)hidden);
+  if (hidden > 8192) return fail(SSL_ERR_UNSUPPORTED, "add_rmsnorm: hidden %lld above 8192",
+                                 (long long)hidden);
+  if (rows == 0) return SSL_OK;
+  if (!h || !weight || !out || ldh < hidden || ldo < hidden || (delta && ldd < hidden))
+    return fail(SSL_ERR_INVALID, "add_rmsnorm: null pointer or leading dimension below hidden");
+  return norm_launch(dtype, (int)hidden, (unsigned)rows, (hipStream_t)stream, h, ldh, delta, ldd,
+                     weight, out, ldo, eps, nullptr, 0, nullptr, 0);
+}
+
+extern "C" int ssl_embed_rmsnorm(const void* embed, int64_t lde, int64_t vocab,
+                                 const int64_t* tokens, void* h, int64_t ldh, const void* weight,
+                                 void* out, int64_t ldo, int64_t rows, int64_t hidden, float eps,
+                                 int32_t dtype, void* stream) {
+  clear_error();
+  if (int rc = check_dtype(dtype)) return rc;
+  if (rows < 0 || rows > 65535 * 1024LL || hidden <= 0 || vocab <= 0)
+    return fail(SSL_ERR_INVALID, "embed_rmsnorm: rows %lld, hidden %lld, vocab %lld",
+                (long long)rows, (long long)hidden, (long long)vocab);
+  if (hidden > 8192) return fail(SSL_ERR_UNSUPPORTED, "embed_rmsnorm: hidden %lld above 8192",
+                                 (long long)hidden);
+  if (rows == 0) return SSL_OK;
+  if (!embed || !tokens || !h || !weight || !out || lde < hidden || ldh < hidden || ldo < hidden)
+    return fail(SSL_ERR_INVALID, "embed_rmsnorm: null pointer or leading dimension below hidden");
+  return norm_launch(dtype, (int)hidden, (unsigned)rows, (hipStream_t)stream, h, ldh, nullptr, 0,
+                     weight, out, ldo, eps, embed, lde, tokens, vocab);
+}
+
+extern "C" int ssl_rope_kv_append(const void* q, int64_t ldq, const void* k, int64_t ldk,
+                                  const void* v, int64_t ldv, const void* cos_table,
+                                  const void* sin_table, const void* q_norm, const void* k_norm,
+                                  float eps, const int32_t* pos, void* q_out, void* k_cache,
+                                  void* v_cache, int64_t rows, int32_t heads, int32_t kv_heads,
+                                  int32_t head_dim, int64_t max_ctx, int32_t dtype, void* stream) {
+  clear_error();
+  if (int rc = check_dtype(dtype)) return rc;
+  if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
+    return fail(SSL_ERR_INVALID, "rope_kv: %d heads over %d key/value heads", heads, kv_heads);
+  if (head_dim <= 0 || head_dim > 256 || head_dim % 2)
+    return fail(SSL_ERR_UNSUPPORTED, "rope_kv: head_dim %d (even, at most 256)", head_dim);
+  if (rows < 0 || rows > 65535 || max_ctx <= 0)
+    return fail(SSL_ERR_INVALID, "rope_kv: rows %lld, max_ctx %lld", (long long)rows,
+                (long long)max_ctx);
+  if (rows == 0) return SSL_OK;
+  if (!q || !k || !v || !cos_table || !sin_table || !pos || !q_out || !k_cache || !v_cache)
+    return fail(SSL_ERR_INVALID, "rope_kv: null pointer");
+  if (ldq < (int64_t)heads * head_dim || ldk < (int64_t)kv_heads * head_dim ||
+      ldv < (int64_t)kv_heads * head_dim)
+    return fail(SSL_ERR_INVALID, "rope_kv: leading dimension below the projection width");
+  launch_dt<Rope>(dtype, dim3(heads + kv_heads, (unsigned)rows), dim3(64), (hipStream_t)stream, q,
+                  ldq, k, ldk, v, ldv, cos_table, sin_table, q_norm, k_norm, eps, pos, q_out,
+                  k_cache, v_cache, (int)heads, (int)kv_heads, (int)head_dim, max_ctx);
+  return check_hip(hipGetLastError(), "rope_kv launch");
+}
+
+extern "C" int32_t ssl_decode_attention_splits(int64_t rows, int32_t heads, int32_t kv_heads,
+                                               int64_t max_ctx) {
+  if (rows <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || max_ctx <= 0) return 1;
+  const int G = heads / kv_heads;
+  const int64_t blocks = rows * kv_heads * ((G + head_block(G) - 1) / head_block(G));
+  // about 1024 workgroups, each with at least 64 positions of the full context
+  int64_t s = (1024 + blocks - 1) / blocks;
+  s = std::min<int64_t>(s, (max_ctx + 63) / 64);
+  return (int32_t)std::max<int64_t>(1, std::min<int64_t>(s, 64));
+}
+
+extern "C" int64_t ssl_decode_attention_workspace_size(int64_t rows, int32_t heads,
+                                                       int32_t head_dim, int32_t n_split) {
+  if (rows <= 0 || heads <= 0 || head_dim <= 0 || n_split <= 0) return 0;
+  return rows * heads * n_split * ((int64_t)head_dim + 2) * 4;
+}
+
+extern "C" int ssl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                                    const int32_t* pos, void* out, int64_t ldo, int64_t rows,
+                                    int32_t heads, int32_t kv_heads, int32_t head_dim,
+                                    int64_t max_ctx, float scale, int32_t n_split,
+                                    void* workspace, int64_t workspace_bytes, int32_t dtype,
+                                    void* stream) {
+  clear_error();
+  if (int rc = check_dtype(dtype)) return rc;
+  if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
+    return fail(SSL_ERR_INVALID, "attention: %d heads over %d key/value heads", heads, kv_heads);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(SSL_ERR_UNSUPPORTED, "attention: head_dim %d (64, 128 or 256)", head_dim);
+  if (rows < 0 || rows > 65535 || max_ctx <= 0 || n_split <= 0 || n_split > 256)
+    return fail(SSL_ERR_INVALID, "attention: rows %lld, max_ctx %lld, splits %d",
+                (long long)rows, (long long)max_ctx, n_split);
+  if (rows == 0) return SSL_OK;
+  if (!q || !k_cache || !v_cache || !pos || !out || ldo < (int64_t)heads * head_dim)
+    return fail(SSL_ERR_INVALID, "attention: null pointer or output leading dimension too small");
+  if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+    return fail(SSL_ERR_INVALID, "attention: q and the caches must be 16-byte aligned");
+  const int64_t need = ssl_decode_attention_workspace_size(rows, heads, head_dim, n_split);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
+    return fail(SSL_ERR_WORKSPACE, "attention: workspace of %lld bytes needed",
+                (long long)need);
+  const int G = heads / kv_heads;
+  const int GB = head_block(G);
+  const int n_hb = (G + GB - 1) / GB;
+  float* po = (float*)workspace;
+  float* pml = po + rows * heads * n_split * head_dim;
+  const float sl2 = scale * 1.4426950408889634f;
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid((unsigned)n_split, (unsigned)(kv_heads * n_hb), (unsigned)rows);
+  if (dtype == SSL_F32)
+    launch_attn<DT_F32>(head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
+                        kv_heads, n_split, sl2, po, pml);
+  else if (dtype == SSL_BF16)
+    launch_attn<DT_BF16>(head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
+                         kv_heads, n_split, sl2, po, pml);
+  else
+    launch_attn<DT_F16>(head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
+                        kv_heads, n_split, sl2, po, pml);
+  if (int rc = check_hip(hipGetLastError(), "attention launch")) return rc;
+  launch_dt<Combine>(dtype, dim3(heads, (unsigned)rows), dim3(std::min(256, (int)head_dim)), st,
+                     (const float*)po, (const float*)pml, out, ldo, (int)heads, (int)head_dim,
+                     (int)n_split);
+  return check_hip(hipGetLastError(), "attention combine launch");
+}
+
+extern "C" int ssl_silu_mul(const void* gate, int64_t ldg, const void* up, int64_t ldu, void* out,
+                            int64_t ldo, int64_t rows, int64_t n, int32_t dtype, void* stream) {
+  clear_error();
+  if (int rc = check_dtype(dtype)) return rc;
+  if (rows < 0 || n < 0) return fail(SSL_ERR_INVALID, "silu_mul: negative size");
+  if (rows == 0 || n == 0) return SSL_OK;
+  if (!gate || !up || !out || ldg < n || ldu < n || ldo < n)
+    return fail(SSL_ERR_INVALID, "silu_mul: null pointer or leading dimension below n");
+  const int64_t total = rows * n;
+  const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
+  launch_dt<SiluMul>(dtype, dim3(blocks), dim3(256), (hipStream_t)stream, gate, ldg, up, ldu, out,
+                     ldo, rows, n);
+  return check_hip(hipGetLastError(), "silu_mul launch");
+}

@@ -7,6 +7,7 @@ Drop-in for the S-SALAAD hot path:
   * dense_to_bsr / factor_from_svd                         (ssalaad_amd.artifact)
   * project_S: the compression loop's block top-k           (ssalaad_amd.project)
   * save_artifact / load_artifact / build_efficient_model: bundles (ssalaad_amd.bundle)
+  * DecodeEngine / generate: KV-cached greedy decode of a loaded model (ssalaad_amd.decode)
 All compute runs in the HIP kernels of libssalaad_amd.so; there is no CPU path.
 """
 
@@ -16,10 +17,12 @@ from . import _lib
 from .addmm_inplace import SUPPORTED_BLOCK_SIZES, bsr_addmm_inplace_, get_tuned_config
 from .artifact import dense_to_bsr, encode_for_kernels, factor_from_svd
 from .bundle import build_efficient_model, load_artifact, save_artifact
+from .decode import DecodeEngine, generate
 from .ls_linear import LRSLinear, LRSLinearGroup
 from .project import block_topk, project_S
 
 __all__ = [
+    "DecodeEngine",
     "LRSLinear",
     "LRSLinearGroup",
     "SUPPORTED_BLOCK_SIZES",
@@ -29,6 +32,7 @@ __all__ = [
     "dense_to_bsr",
     "encode_for_kernels",
     "factor_from_svd",
+    "generate",
     "get_tuned_config",
     "library_path",
     "load_artifact",

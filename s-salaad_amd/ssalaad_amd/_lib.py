@@ -76,6 +76,32 @@ _SIGNATURES = {
         ctypes.c_int,
         [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p],
     ),
+    "ssl_add_rmsnorm": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_i32,
+         _c_p],
+    ),
+    "ssl_embed_rmsnorm": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
+         ctypes.c_float, _c_i32, _c_p],
+    ),
+    "ssl_rope_kv_append": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, ctypes.c_float, _c_p,
+         _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_p],
+    ),
+    "ssl_decode_attention_splits": (_c_i32, [_c_i64, _c_i32, _c_i32, _c_i64]),
+    "ssl_decode_attention_workspace_size": (_c_i64, [_c_i64, _c_i32, _c_i32, _c_i32]),
+    "ssl_decode_attention": (
+        ctypes.c_int,
+        [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i64,
+         ctypes.c_float, _c_i32, _c_p, _c_i64, _c_i32, _c_p],
+    ),
+    "ssl_silu_mul": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p],
+    ),
 }
 
 

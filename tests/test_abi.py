@@ -311,3 +311,46 @@ def test_block_topk_rejects_bad_arguments_before_any_launch():
     assert lib.ssl_block_topk(fake, 64, 2, 2, 32, 32, _lib.SSL_BF16, 1, fake, fake, fake, 16, None) == 1
     assert b"ldo" in lib.ssl_last_error()
     assert lib.ssl_block_topk(fake, 64, 0, 2, 32, 32, _lib.SSL_BF16, 1, None, None, None, 0, None) == 0
+
+
+def test_decode_entry_points_reject_bad_arguments_before_any_launch():
+    lib = _lib.load()
+    fake = 256  # never dereferenced: every call below fails its argument checks first
+    bf = _lib.SSL_BF16
+    # add_rmsnorm: unknown dtype, leading dimension below hidden, null weight
+    assert lib.ssl_add_rmsnorm(fake, 64, None, 0, fake, fake, 64, 2, 64, 1e-6, 9, None) == 1
+    assert lib.ssl_add_rmsnorm(fake, 32, None, 0, fake, fake, 64, 2, 64, 1e-6, bf, None) == 1
+    assert lib.ssl_add_rmsnorm(fake, 64, None, 0, None, fake, 64, 2, 64, 1e-6, bf, None) == 1
+    assert lib.ssl_add_rmsnorm(None, 64, None, 0, None, None, 64, 0, 64, 1e-6, bf, None) == 0
+    assert lib.ssl_add_rmsnorm(fake, 9000, None, 0, fake, fake, 9000, 2, 9000, 1e-6, bf, None) == 2
+    # embed_rmsnorm: no vocabulary, narrow table, null tokens
+    assert lib.ssl_embed_rmsnorm(fake, 64, 0, fake, fake, 64, fake, fake, 64, 2, 64, 1e-6, bf, None) == 1
+    assert lib.ssl_embed_rmsnorm(fake, 32, 9, fake, fake, 64, fake, fake, 64, 2, 64, 1e-6, bf, None) == 1
+    assert lib.ssl_embed_rmsnorm(fake, 64, 9, None, fake, 64, fake, fake, 64, 2, 64, 1e-6, bf, None) == 1
+    # rope: heads not a multiple of kv_heads, odd or too wide heads, narrow rows
+    args = [fake, 512, fake, 128, fake, 128, fake, fake, None, None, 1e-6, fake, fake, fake, fake, 2]
+    assert lib.ssl_rope_kv_append(*args, 4, 3, 128, 16, bf, None) == 1
+    assert lib.ssl_rope_kv_append(*args, 4, 1, 127, 16, bf, None) == 2
+    assert lib.ssl_rope_kv_append(*args, 4, 1, 512, 16, bf, None) == 2
+    assert lib.ssl_rope_kv_append(*args, 8, 1, 128, 16, bf, None) == 1
+    # attention: head_dim without a kernel, too many splits, small workspace, misalignment
+    a = [fake, fake, fake, fake, fake, 512, 2, 4, 4]
+    assert lib.ssl_decode_attention(*a, 96, 16, 0.1, 1, fake, 1 << 20, bf, None) == 2
+    assert lib.ssl_decode_attention(*a, 128, 16, 0.1, 300, fake, 1 << 20, bf, None) == 1
+    need = lib.ssl_decode_attention_workspace_size(2, 4, 128, 3)
+    assert need == 2 * 4 * 3 * 130 * 4
+    assert lib.ssl_decode_attention(*a, 128, 16, 0.1, 3, fake, need - 1, bf, None) == 3
+    assert lib.ssl_decode_attention(fake + 2, *a[1:], 128, 16, 0.1, 3, fake, need, bf, None) == 1
+    # silu_mul: leading dimension below n
+    assert lib.ssl_silu_mul(fake, 8, fake, 16, fake, 16, 2, 16, bf, None) == 1
+    assert lib.ssl_silu_mul(None, 8, None, 16, None, 16, 0, 16, bf, None) == 0
+
+
+def test_decode_attention_split_policy():
+    lib = _lib.load()
+    # about 1024 workgroups, slices of at least 64 positions, at most 64 slices
+    assert lib.ssl_decode_attention_splits(1, 16, 16, 1024) == 16
+    assert lib.ssl_decode_attention_splits(16, 16, 16, 1024) == 4
+    assert lib.ssl_decode_attention_splits(1, 32, 8, 100000) == 64
+    assert lib.ssl_decode_attention_splits(64, 32, 32, 4096) == 1
+    assert lib.ssl_decode_attention_splits(1, 4, 4, 10) == 1

@@ -130,3 +130,34 @@ def test_factor_from_svd_mirror():
 def test_encoder_front_end_checks_shape_first():
     with pytest.raises(ValueError, match="not divisible"):
         ssalaad_amd.dense_to_bsr(torch.zeros(10, 16), 4, 4)
+
+
+def _tiny_llama():
+    from ssalaad_amd.bundle import build_model_from_config
+
+    return build_model_from_config({
+        "model_type": "llama", "hidden_size": 64, "intermediate_size": 96, "num_hidden_layers": 1,
+        "num_attention_heads": 4, "num_key_value_heads": 4, "vocab_size": 50,
+        "max_position_embeddings": 16, "hidden_act": "silu"})
+
+
+def test_generate_checks_arguments_like_the_reference():
+    """generate.py:14-19: the same errors before any work."""
+    from ssalaad_amd import generate
+
+    model = _tiny_llama()
+    with pytest.raises(ValueError, match="nonempty"):
+        generate(model, torch.zeros(2, 0, dtype=torch.long), 1)
+    with pytest.raises(ValueError, match="nonempty"):
+        generate(model, torch.zeros(3, dtype=torch.long), 1)
+    with pytest.raises(ValueError, match="nonnegative"):
+        generate(model, torch.zeros(1, 4, dtype=torch.long), -1)
+    with pytest.raises(ValueError, match="context length"):
+        generate(model, torch.zeros(1, 10, dtype=torch.long), 7)
+
+
+def test_decode_engine_has_no_cpu_path():
+    from ssalaad_amd import DecodeEngine
+
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        DecodeEngine(_tiny_llama(), max_batch=1, max_context=4)
