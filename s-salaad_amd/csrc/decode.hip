@@ -72,18 +72,26 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     src = embed;
     srow = valid ? t * lde : 0;
   }
+  // Loads are unconditional (indices clamped into the row) and masked
+  // afterwards: a load under a per-lane condition becomes a branch that waits
+  // for it, which would serialise the row.
   float v[K], d[K], wv[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const int i = tid + 256 * k;
-    v[k] = (i < hidden && valid) ? load_scalar<DT>(src, srow + i) : 0.f;
-    d[k] = (i < hidden && delta) ? load_scalar<DT>(delta, row * ldd + i) : 0.f;
-    wv[k] = i < hidden ? load_scalar<DT>(w, i) : 0.f;
+    const int i = min(tid + 256 * k, hidden - 1);
+    v[k] = load_scalar<DT>(src, srow + i);
+    wv[k] = load_scalar<DT>(w, i);
+  }
+  if (delta) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) d[k] = load_scalar<DT>(delta, row * ldd + min(tid + 256 * k, hidden - 1));
   }
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
+    const bool in = tid + 256 * k < hidden;
     if (delta) v[k] = rnd<DT>(v[k] + d[k]);
+    v[k] = (in && valid) ? v[k] : 0.f;
     ss += v[k] * v[k];
   }
   if (delta || tokens) {
@@ -132,39 +140,36 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(
   const void* nw = is_q ? q_norm : k_norm;
   const int half = hd >> 1;
 
-  float x1[2], x2[2];
+  float x1[2], x2[2], c1[2], s1[2], c2[2], s2[2];
   float ss = 0.f;
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int j = lane + 64 * u;
-    x1[u] = x2[u] = 0.f;
-    if (j < half) {
-      x1[u] = load_scalar<DT>(src, soff + j);
-      x2[u] = load_scalar<DT>(src, soff + j + half);
-      ss += x1[u] * x1[u] + x2[u] * x2[u];
-    }
+  for (int u = 0; u < 2; ++u) {  // clamped, unconditional loads (see add_rmsnorm)
+    const int j = min(lane + 64 * u, half - 1);
+    x1[u] = load_scalar<DT>(src, soff + j);
+    x2[u] = load_scalar<DT>(src, soff + j + half);
+    c1[u] = load_scalar<DT>(cos_t, p * hd + j);
+    s1[u] = load_scalar<DT>(sin_t, p * hd + j);
+    c2[u] = load_scalar<DT>(cos_t, p * hd + j + half);
+    s2[u] = load_scalar<DT>(sin_t, p * hd + j + half);
   }
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    if (lane + 64 * u < half) ss += x1[u] * x1[u] + x2[u] * x2[u];
   if (nw) {  // Qwen3: RMSNorm over the head's features before the rotation
     const float rs = rsqrtf(wave_sum(ss) / (float)hd + eps);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int j = lane + 64 * u;
-      if (j < half) {
-        x1[u] = rnd<DT>(load_scalar<DT>(nw, j) * rnd<DT>(x1[u] * rs));
-        x2[u] = rnd<DT>(load_scalar<DT>(nw, j + half) * rnd<DT>(x2[u] * rs));
-      }
+      const int j = min(lane + 64 * u, half - 1);
+      x1[u] = rnd<DT>(load_scalar<DT>(nw, j) * rnd<DT>(x1[u] * rs));
+      x2[u] = rnd<DT>(load_scalar<DT>(nw, j + half) * rnd<DT>(x2[u] * rs));
     }
   }
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const int j = lane + 64 * u;
-    if (j < half) {
-      const float c1 = load_scalar<DT>(cos_t, p * hd + j), s1 = load_scalar<DT>(sin_t, p * hd + j);
-      const float c2 = load_scalar<DT>(cos_t, p * hd + j + half);
-      const float s2 = load_scalar<DT>(sin_t, p * hd + j + half);
-      // rotate_half(x) = (-x2, x1)
-      store_scalar<DT>(dst, doff + j, rnd<DT>(x1[u] * c1) - rnd<DT>(x2[u] * s1));
-      store_scalar<DT>(dst, doff + j + half, rnd<DT>(x2[u] * c2) + rnd<DT>(x1[u] * s2));
+    if (j < half) {  // rotate_half(x) = (-x2, x1)
+      store_scalar<DT>(dst, doff + j, rnd<DT>(x1[u] * c1[u]) - rnd<DT>(x2[u] * s1[u]));
+      store_scalar<DT>(dst, doff + j + half, rnd<DT>(x2[u] * c2[u]) + rnd<DT>(x1[u] * s2[u]));
     }
   }
   if (!is_q) {
@@ -185,8 +190,13 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(
 template <int DT>
 struct Vec16 {
   static constexpr int VE = DT == DT_F32 ? 4 : 8;
+  __device__ __forceinline__ static uint4 raw(const void* base, int64_t off) {
+    return *(const uint4*)((const char*)base + off * Elem<DT>::bytes);
+  }
   __device__ __forceinline__ static void load(float* f, const void* base, int64_t off) {
-    const uint4 raw = *(const uint4*)((const char*)base + off * Elem<DT>::bytes);
+    unpack(f, raw(base, off));
+  }
+  __device__ __forceinline__ static void unpack(float* f, const uint4 raw) {
     if constexpr (DT == DT_F32) {
       f[0] = __uint_as_float(raw.x);
       f[1] = __uint_as_float(raw.y);
@@ -261,34 +271,41 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
   const int64_t head_off = (b * kv_heads + kh) * max_ctx * HD;
 
   for (int64_t p0 = lo; p0 < hi; p0 += STEP) {
-    float kf[kAttnJ][VE], vf[kAttnJ][VE];
+    // positions past the slice are clamped to its last one (loads stay
+    // unconditional, see add_rmsnorm) and masked out of the softmax
+    uint4 kr[kAttnJ], vr[kAttnJ];
     bool ok[kAttnJ];
 #pragma unroll
     for (int j = 0; j < kAttnJ; ++j) {
       const int64_t p = p0 + wave * WSTEP + j * RPI + rr;
       ok[j] = p < hi;
-      if (ok[j]) Vec16<DT>::load(kf[j], kc, head_off + p * HD + vv * VE);
+      kr[j] = Vec16<DT>::raw(kc, head_off + (ok[j] ? p : hi - 1) * HD + vv * VE);
     }
 #pragma unroll
     for (int j = 0; j < kAttnJ; ++j) {
       const int64_t p = p0 + wave * WSTEP + j * RPI + rr;
-      if (ok[j]) Vec16<DT>::load(vf[j], vc, head_off + p * HD + vv * VE);
+      vr[j] = Vec16<DT>::raw(vc, head_off + (ok[j] ? p : hi - 1) * HD + vv * VE);
     }
+    // every key and value load of the step is issued before the first use
+    __builtin_amdgcn_sched_barrier(0);
+    float kf[kAttnJ][VE], vf[kAttnJ][VE];
+#pragma unroll
+    for (int j = 0; j < kAttnJ; ++j) Vec16<DT>::unpack(kf[j], kr[j]);
     float s[GB][kAttnJ];
 #pragma unroll
     for (int g = 0; g < GB; ++g) {
 #pragma unroll
       for (int j = 0; j < kAttnJ; ++j) {
         float d = 0.f;
-        if (ok[j]) {
 #pragma unroll
-          for (int e = 0; e < VE; ++e) d += qf[g][e] * kf[j][e];
-        }
+        for (int e = 0; e < VE; ++e) d += qf[g][e] * kf[j][e];
 #pragma unroll
         for (int off = 1; off < LPR; off <<= 1) d += __shfl_xor(d, off);
         s[g][j] = ok[j] ? d * scale_log2 : -INFINITY;
       }
     }
+#pragma unroll
+    for (int j = 0; j < kAttnJ; ++j) Vec16<DT>::unpack(vf[j], vr[j]);
 #pragma unroll
     for (int g = 0; g < GB; ++g) {
       float mx = s[g][0];
@@ -314,8 +331,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
       for (int e = 0; e < VE; ++e) {
         float acc = o[g][e] * alpha;
 #pragma unroll
-        for (int j = 0; j < kAttnJ; ++j)
-          if (ok[j]) acc += pj[j] * vf[j][e];
+        for (int j = 0; j < kAttnJ; ++j) acc += pj[j] * vf[j][e];  // pj = 0 when masked
         o[g][e] = acc;
       }
     }
@@ -364,24 +380,31 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
   }
 }
 
-// attn_combine: workgroup (head, row); thread d < head_dim.
+// attn_combine: workgroup (head, row); the slices' (max, sum) pairs go to LDS,
+// then thread d < head_dim sums the weighted partial outputs (every slice has
+// written its partial, zero for an empty one).
 template <int DT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* part_o, const float* part_ml,
                                                            void* out, int64_t ldo, int heads, int hd,
                                                            int n_split) {
+  __shared__ float sm[256], sl[256];
   const int h = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int64_t base = (b * heads + h) * n_split;
+  for (int s = threadIdx.x; s < n_split; s += blockDim.x) {
+    sm[s] = part_ml[2 * (base + s)];
+    sl[s] = part_ml[2 * (base + s) + 1];
+  }
+  __syncthreads();
   float mx = -INFINITY;
   for (int s = 0; s < n_split; ++s)
-    if (part_ml[2 * (base + s) + 1] > 0.f) mx = fmaxf(mx, part_ml[2 * (base + s)]);
+    if (sl[s] > 0.f) mx = fmaxf(mx, sm[s]);
   for (int d = threadIdx.x; d < hd; d += blockDim.x) {
     float lsum = 0.f, acc = 0.f;
+#pragma unroll 8
     for (int s = 0; s < n_split; ++s) {
-      const float ls = part_ml[2 * (base + s) + 1];
-      if (!(ls > 0.f)) continue;
-      const float sc = exp2f(part_ml[2 * (base + s)] - mx);
-      lsum += ls * sc;
+      const float sc = sl[s] > 0.f ? exp2f(sm[s] - mx) : 0.f;
+      lsum += sl[s] * sc;
       acc += part_o[(base + s) * hd + d] * sc;
     }
     store_scalar<DT>(out, b * ldo + (int64_t)h * hd + d, lsum > 0.f ? acc / lsum : 0.f);
