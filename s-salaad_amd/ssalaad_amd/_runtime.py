@@ -42,6 +42,38 @@ def plan_target_cost(total_cost: int, block_p: int, elem_bytes: int, M: int) -> 
     return max(1, _CHUNK_BYTES // (block_p * elem_bytes))
 
 
+# Row balancing for decode-shaped calls whose rows are long enough that the
+# longest one sets the launch time (see balanced_target). _BALANCE_LATENT_MIN
+# is the number of latent K chunks the balancing leaves room for.
+_BALANCE_MIN_ROW_BYTES = 128 * 1024
+_BALANCE_LATENT_MIN = 4
+
+
+def balanced_target(costs: np.ndarray, cost_bytes: int, slots: int, lat_tiles: int) -> int:
+    """A chunk cost target that splits only the longest rows, into the
+    workgroup slots the other rows and a minimal latent leave free (0 = none).
+
+    costs: per-row cost; cost_bytes: weight bytes per cost unit; slots: row and
+    latent workgroups resident at once; lat_tiles: latent workgroups per K chunk.
+    """
+    costs = costs[costs > 0]
+    if costs.size == 0 or _BALANCE_LATENT_MIN <= 0:
+        return 0
+    if costs.mean() * cost_bytes < _BALANCE_MIN_ROW_BYTES:
+        return 0
+    budget = slots - _BALANCE_LATENT_MIN * lat_tiles
+    if budget <= costs.size:
+        return 0
+    lo, hi = int(costs.mean() // 2), int(costs.max())  # hi: no split
+    while lo < hi:  # smallest target whose chunk count fits the budget
+        mid = (lo + hi) // 2
+        if int(np.ceil(costs / mid).sum()) <= budget:
+            hi = mid
+        else:
+            lo = mid + 1
+    return 0 if lo >= costs.max() else lo
+
+
 def build_plan(
     crow_host: np.ndarray,
     rows_host: np.ndarray | None,

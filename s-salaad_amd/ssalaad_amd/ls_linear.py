@@ -106,6 +106,13 @@ class _KernelState:
         if pl is None:
             total = self.nblk_total * self.block_q + self.NB * self.lr_units * 32
             target = _runtime.plan_target_cost(total, self.p, self.elem, M)
+            if key == 1 and self.s_format == 0 and self.p == 64:
+                # one workgroup per compute unit at p = 64: split the longest rows
+                costs = np.diff(self.crow_h).astype(np.int64) * self.block_q + self.lr_units * 32
+                n_cu = torch.cuda.get_device_properties(self.device).multi_processor_count
+                bal = _runtime.balanced_target(costs, self.p * self.elem, n_cu, self.r_pad // 16)
+                if bal:
+                    target = min(target, bal) if target else bal
             table, n_chunks, n_slots = _runtime.build_plan(
                 self.crow_h, None, self.block_q, self.lr_units, target
             )

@@ -354,3 +354,31 @@ def test_decode_attention_split_policy():
     assert lib.ssl_decode_attention_splits(1, 32, 8, 100000) == 64
     assert lib.ssl_decode_attention_splits(64, 32, 32, 4096) == 1
     assert lib.ssl_decode_attention_splits(1, 4, 4, 10) == 1
+
+
+def test_balanced_target_splits_only_the_longest_rows():
+    """The decode balancing target (p = 64 rows, one workgroup per compute unit):
+    the chunk count fits the slots a minimal latent leaves free, only rows above
+    the target split, and short rows or a full device get no target."""
+    rng = np.random.default_rng(0)
+    blocks = rng.binomial(64, 0.5, size=172)
+    costs = blocks.astype(np.int64) * 64 + 8 * 32
+    lat_min = _runtime._BALANCE_LATENT_MIN
+    t = _runtime.balanced_target(costs, 128, 256, 16)
+    assert 0 < t < costs.max()
+    chunks = np.ceil(costs / t).sum()
+    assert costs.size < chunks <= 256 - lat_min * 16
+    assert np.ceil(costs / (t - 1)).sum() > 256 - lat_min * 16  # the smallest such target
+    assert _runtime.balanced_target(costs, 16, 256, 16) == 0  # rows under 128 KiB
+    assert _runtime.balanced_target(np.full(400, 2304), 128, 256, 16) == 0  # no free slots
+    # the plan built with it covers every unit once
+    crow = np.concatenate([[0], np.cumsum(blocks)]).astype(np.int32)
+    table, n_chunks, _ = _runtime.build_plan(crow, None, 64, 8, t)
+    assert n_chunks == chunks
+    for row in range(172):
+        mine = table[table[:, 0] == row]
+        spans = sorted((int(b), int(e)) for b, e in mine[:, 1:3])
+        assert spans[0][0] == crow[row] and spans[-1][1] == crow[row + 1]
+        assert all(spans[i][1] == spans[i + 1][0] for i in range(len(spans) - 1))
+        assert (len(mine) > 1) == (costs[row] > t)
+        assert sum(int(e - b) for b, e in mine[:, 3:5]) == 8
