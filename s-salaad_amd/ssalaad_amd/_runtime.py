@@ -47,6 +47,9 @@ def plan_target_cost(total_cost: int, block_p: int, elem_bytes: int, M: int) -> 
 # is the number of latent K chunks the balancing leaves room for.
 _BALANCE_MIN_ROW_BYTES = 128 * 1024
 _BALANCE_LATENT_MIN = 4
+# Block sizes it applies to: at p = 32 (two workgroups per compute unit,
+# shorter rows) the split rows' exchange costs more than the straggler.
+_BALANCE_P = (64,)
 
 
 def balanced_target(costs: np.ndarray, cost_bytes: int, slots: int, lat_tiles: int) -> int:

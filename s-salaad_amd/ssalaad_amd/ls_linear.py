@@ -106,7 +106,7 @@ class _KernelState:
         if pl is None:
             total = self.nblk_total * self.block_q + self.NB * self.lr_units * 32
             target = _runtime.plan_target_cost(total, self.p, self.elem, M)
-            if key == 1 and self.s_format == 0 and self.p == 64:
+            if key == 1 and self.s_format == 0 and self.p in _runtime._BALANCE_P:
                 # one workgroup per compute unit at p = 64: split the longest rows
                 costs = np.diff(self.crow_h).astype(np.int64) * self.block_q + self.lr_units * 32
                 n_cu = torch.cuda.get_device_properties(self.device).multi_processor_count
