@@ -310,19 +310,24 @@ int ssl_rope_kv_append(const void* q, int64_t ldq, const void* k, int64_t ldk, c
 /* out[row, h·head_dim + d] = softmax_j(q·k_j · scale) · v_j over positions
  * j ≤ pos[row] of the row's cache, with query head h reading key/value head
  * h / (heads / kv_heads). fp32 accumulation, one rounding at the store.
- * The context is cut into n_split slices whose partials are merged by a
- * second kernel; ssl_decode_attention_splits proposes n_split for a batch,
- * the workspace (ssl_decode_attention_workspace_size bytes, 16-byte aligned)
- * holds the partials. head_dim 64, 128 or 256; q [rows, heads, head_dim]. */
+ * The context is cut into n_split slices (at most 256); the slice that
+ * finishes last merges every slice's partial in the same launch.
+ * ssl_decode_attention_splits proposes n_split for a batch; the workspace
+ * (ssl_decode_attention_workspace_size bytes, 16-byte aligned) holds the
+ * partials; `counters` (ssl_decode_attention_counter_count int32) must be zero
+ * before the first call and every completed call leaves them zero. Calls that
+ * share counters must be ordered. head_dim 64, 128 or 256; q [rows, heads,
+ * head_dim]. */
 int32_t ssl_decode_attention_splits(int64_t rows, int32_t heads, int32_t kv_heads,
                                     int64_t max_ctx);
 int64_t ssl_decode_attention_workspace_size(int64_t rows, int32_t heads, int32_t head_dim,
                                             int32_t n_split);
+int64_t ssl_decode_attention_counter_count(int64_t rows, int32_t heads, int32_t kv_heads);
 int ssl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                          const int32_t* pos, void* out, int64_t ldo, int64_t rows, int32_t heads,
                          int32_t kv_heads, int32_t head_dim, int64_t max_ctx, float scale,
                          int32_t n_split, void* workspace, int64_t workspace_bytes,
-                         int32_t dtype, void* stream);
+                         int32_t* counters, int64_t n_counters, int32_t dtype, void* stream);
 
 /* out = silu(gate) · up (LlamaMLP's act_fn(gate_proj(x)) * up_proj(x)), silu
  * rounded to the dtype before the product. */

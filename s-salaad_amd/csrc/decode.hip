@@ -6,8 +6,8 @@
 //   rope_kv       q/k rotary embedding (after Qwen3's per-head RMSNorm), k and v
 //                 written into the cache at the sequence's position
 //   attn_split    softmax(q·Kᵀ·scale)·V over one slice of a sequence's context,
-//                 per wave an online softmax, the slice's partial (max, sum, o)
-//   attn_combine  the slices' partials merged into the head's output
+//                 per wave an online softmax, the slice's partial (max, sum, o);
+//                 the last slice to finish merges all of them into the output
 //   silu_mul      silu(gate) · up
 //
 // Rounding points follow transformers' LlamaRMSNorm / apply_rotary_pos_emb /
@@ -42,6 +42,22 @@ __device__ __forceinline__ void store_scalar(void* p, int64_t i, float f) {
   if constexpr (DT == DT_F32) ((float*)p)[i] = f;
   else ((uint16_t*)p)[i] = (uint16_t)to_bits<DT>(f);
 }
+
+// Device-coherent (agent scope) accesses for the attention slices' partials.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The same device-coherent read as a plain buffer load (cache policy sc1), so
+// that many of them can be in flight at once; `r` spans the partials.
+constexpr int kSc1Policy = 16;
+__device__ __forceinline__ float ld_sc1(__amdgpu_buffer_rsrc_t r, int64_t idx) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)(idx * 4), 0, kSc1Policy));
+}
+
+constexpr int kMaxSplits = 256;
 
 __device__ __forceinline__ float wave_sum(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
@@ -223,7 +239,8 @@ constexpr int kAttnJ = 4;  // wave instructions (row groups) per step
 template <int DT, int HD, int GB>
 __global__ __launch_bounds__(256) void attn_split_kernel(
     const void* q, const void* kc, const void* vc, const int32_t* pos, int64_t max_ctx, int heads,
-    int kv_heads, int n_split, float scale_log2, float* part_o, float* part_ml) {
+    int kv_heads, int n_split, float scale_log2, float* part_o, float* part_ml, int* counters,
+    void* out, int64_t ldo) {
   constexpr int VE = Vec16<DT>::VE;
   constexpr int LPR = HD / VE;
   constexpr int RPI = 64 / LPR;
@@ -372,42 +389,52 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
       }
     }
     const int64_t hrow = (b * heads + (int64_t)kh * G + g0 + g) * n_split + split;
-    part_o[hrow * HD + d] = acc;
+    st_agent(part_o + hrow * HD + d, acc);
     if (d == 0) {
-      part_ml[2 * hrow] = mx;
-      part_ml[2 * hrow + 1] = lsum;
+      st_agent(part_ml + 2 * hrow, mx);
+      st_agent(part_ml + 2 * hrow + 1, lsum);
     }
   }
-}
 
-// attn_combine: workgroup (head, row); the slices' (max, sum) pairs go to LDS,
-// then thread d < head_dim sums the weighted partial outputs (every slice has
-// written its partial, zero for an empty one).
-template <int DT>
-__global__ __launch_bounds__(256) void attn_combine_kernel(const float* part_o, const float* part_ml,
-                                                           void* out, int64_t ldo, int heads, int hd,
-                                                           int n_split) {
-  __shared__ float sm[256], sl[256];
-  const int h = blockIdx.x;
-  const int64_t b = blockIdx.y;
-  const int64_t base = (b * heads + h) * n_split;
-  for (int s = threadIdx.x; s < n_split; s += blockDim.x) {
-    sm[s] = part_ml[2 * (base + s)];
-    sl[s] = part_ml[2 * (base + s) + 1];
+  // The slice that finishes last merges every slice of its heads: partials are
+  // stored device-coherently and acknowledged before the arrival count, which
+  // the last arriver returns to zero (the counters are zero at rest).
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ int last;
+  int* cnt = counters + (b * kv_heads + kh) * n_hb + (blockIdx.y % n_hb);
+  if (threadIdx.x == 0) {
+    last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_split - 1;
+    if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  float mx = -INFINITY;
-  for (int s = 0; s < n_split; ++s)
-    if (sl[s] > 0.f) mx = fmaxf(mx, sm[s]);
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+  if (!last) return;
+  __shared__ float cm[GB][kMaxSplits], cl[GB][kMaxSplits];
+  for (int i = threadIdx.x; i < ng * n_split; i += 256) {
+    const int g = i / n_split, sp = i % n_split;
+    const int64_t hrow = (b * heads + (int64_t)kh * G + g0 + g) * n_split + sp;
+    cm[g][sp] = ld_agent(part_ml + 2 * hrow);
+    cl[g][sp] = ld_agent(part_ml + 2 * hrow + 1);
+  }
+  __syncthreads();
+  // partials span rows·heads·n_split·HD floats (below 2 GiB: the host checks)
+  const auto pr = __builtin_amdgcn_make_buffer_rsrc(part_o, (short)0, 0x7fffffff, 0x00020000);
+  for (int i = threadIdx.x; i < GB * HD; i += 256) {
+    const int g = i / HD, d = i % HD;
+    if (g >= ng) continue;
+    const int h = kh * G + g0 + g;
+    const int64_t base = (b * heads + h) * n_split;
+    float mx = -INFINITY;
+    for (int sp = 0; sp < n_split; ++sp)
+      if (cl[g][sp] > 0.f) mx = fmaxf(mx, cm[g][sp]);
     float lsum = 0.f, acc = 0.f;
 #pragma unroll 8
-    for (int s = 0; s < n_split; ++s) {
-      const float sc = sl[s] > 0.f ? exp2f(sm[s] - mx) : 0.f;
-      lsum += sl[s] * sc;
-      acc += part_o[(base + s) * hd + d] * sc;
+    for (int sp = 0; sp < n_split; ++sp) {  // every slice stored its partial (zero if empty)
+      const float sc = cl[g][sp] > 0.f ? exp2f(cm[g][sp] - mx) : 0.f;
+      lsum += cl[g][sp] * sc;
+      acc += ld_sc1(pr, (base + sp) * HD + d) * sc;
     }
-    store_scalar<DT>(out, b * ldo + (int64_t)h * hd + d, lsum > 0.f ? acc / lsum : 0.f);
+    store_scalar<DT>(out, b * ldo + (int64_t)h * HD + d, lsum > 0.f ? acc / lsum : 0.f);
   }
 }
 
@@ -466,19 +493,18 @@ int norm_launch(int32_t dtype, int hidden, unsigned rows, hipStream_t st, void* 
 template <int DT>
 struct Rope { static constexpr auto fn = rope_kv_kernel<DT>; };
 template <int DT>
-struct Combine { static constexpr auto fn = attn_combine_kernel<DT>; };
-template <int DT>
 struct SiluMul { static constexpr auto fn = silu_mul_kernel<DT>; };
 
 template <int DT, int HD>
 int launch_attn_hd(int GB, dim3 grid, hipStream_t st, const void* q, const void* kc,
                    const void* vc, const int32_t* pos, int64_t max_ctx, int heads, int kv_heads,
-                   int n_split, float sl2, float* po, float* pml) {
+                   int n_split, float sl2, float* po, float* pml, int* cnt, void* out,
+                   int64_t ldo) {
   switch (GB) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 1>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 2>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 4>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml); break;
-    default: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 8>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml); break;
+    case 1: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 1>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 2>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 4>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo); break;
+    default: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 8>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo); break;
   }
   return 0;
 }
@@ -486,10 +512,10 @@ int launch_attn_hd(int GB, dim3 grid, hipStream_t st, const void* q, const void*
 template <int DT>
 void launch_attn(int hd, int GB, dim3 grid, hipStream_t st, const void* q, const void* kc,
                  const void* vc, const int32_t* pos, int64_t max_ctx, int heads, int kv_heads,
-                 int n_split, float sl2, float* po, float* pml) {
-  if (hd == 64) launch_attn_hd<DT, 64>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml);
-  else if (hd == 128) launch_attn_hd<DT, 128>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml);
-  else launch_attn_hd<DT, 256>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml);
+                 int n_split, float sl2, float* po, float* pml, int* cnt, void* out, int64_t ldo) {
+  if (hd == 64) launch_attn_hd<DT, 64>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo);
+  else if (hd == 128) launch_attn_hd<DT, 128>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo);
+  else launch_attn_hd<DT, 256>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo);
 }
 
 int head_block(int G) { return G >= 5 ? 8 : (G >= 3 ? 4 : G); }
@@ -572,9 +598,10 @@ extern "C" int32_t ssl_decode_attention_splits(int64_t rows, int32_t heads, int3
   if (rows <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || max_ctx <= 0) return 1;
   const int G = heads / kv_heads;
   const int64_t blocks = rows * kv_heads * ((G + head_block(G) - 1) / head_block(G));
-  // about 1024 workgroups, each with at least 64 positions of the full context
+  // about 1024 workgroups, each with at least 128 positions of the full context
+  // (the last slice to finish merges them all, so fewer slices end sooner)
   int64_t s = (1024 + blocks - 1) / blocks;
-  s = std::min<int64_t>(s, (max_ctx + 63) / 64);
+  s = std::min<int64_t>(s, (max_ctx + 127) / 128);
   return (int32_t)std::max<int64_t>(1, std::min<int64_t>(s, 64));
 }
 
@@ -584,19 +611,26 @@ extern "C" int64_t ssl_decode_attention_workspace_size(int64_t rows, int32_t hea
   return rows * heads * n_split * ((int64_t)head_dim + 2) * 4;
 }
 
+extern "C" int64_t ssl_decode_attention_counter_count(int64_t rows, int32_t heads,
+                                                      int32_t kv_heads) {
+  if (rows <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads) return 0;
+  const int G = heads / kv_heads;
+  return rows * kv_heads * ((G + head_block(G) - 1) / head_block(G));
+}
+
 extern "C" int ssl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                                     const int32_t* pos, void* out, int64_t ldo, int64_t rows,
                                     int32_t heads, int32_t kv_heads, int32_t head_dim,
                                     int64_t max_ctx, float scale, int32_t n_split,
-                                    void* workspace, int64_t workspace_bytes, int32_t dtype,
-                                    void* stream) {
+                                    void* workspace, int64_t workspace_bytes, int32_t* counters,
+                                    int64_t n_counters, int32_t dtype, void* stream) {
   clear_error();
   if (int rc = check_dtype(dtype)) return rc;
   if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
     return fail(SSL_ERR_INVALID, "attention: %d heads over %d key/value heads", heads, kv_heads);
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(SSL_ERR_UNSUPPORTED, "attention: head_dim %d (64, 128 or 256)", head_dim);
-  if (rows < 0 || rows > 65535 || max_ctx <= 0 || n_split <= 0 || n_split > 256)
+  if (rows < 0 || rows > 65535 || max_ctx <= 0 || n_split <= 0 || n_split > kMaxSplits)
     return fail(SSL_ERR_INVALID, "attention: rows %lld, max_ctx %lld, splits %d",
                 (long long)rows, (long long)max_ctx, n_split);
   if (rows == 0) return SSL_OK;
@@ -605,9 +639,15 @@ extern "C" int ssl_decode_attention(const void* q, const void* k_cache, const vo
   if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
     return fail(SSL_ERR_INVALID, "attention: q and the caches must be 16-byte aligned");
   const int64_t need = ssl_decode_attention_workspace_size(rows, heads, head_dim, n_split);
+  if (need > 0x7fffffffLL)
+    return fail(SSL_ERR_UNSUPPORTED, "attention: partials of %lld bytes (at most 2 GiB)",
+                (long long)need);
   if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
     return fail(SSL_ERR_WORKSPACE, "attention: workspace of %lld bytes needed",
                 (long long)need);
+  if (!counters || n_counters < ssl_decode_attention_counter_count(rows, heads, kv_heads))
+    return fail(SSL_ERR_WORKSPACE, "attention: %lld counters needed",
+                (long long)ssl_decode_attention_counter_count(rows, heads, kv_heads));
   const int G = heads / kv_heads;
   const int GB = head_block(G);
   const int n_hb = (G + GB - 1) / GB;
@@ -618,18 +658,14 @@ extern "C" int ssl_decode_attention(const void* q, const void* k_cache, const vo
   dim3 grid((unsigned)n_split, (unsigned)(kv_heads * n_hb), (unsigned)rows);
   if (dtype == SSL_F32)
     launch_attn<DT_F32>(head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
-                        kv_heads, n_split, sl2, po, pml);
+                        kv_heads, n_split, sl2, po, pml, counters, out, ldo);
   else if (dtype == SSL_BF16)
     launch_attn<DT_BF16>(head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
-                         kv_heads, n_split, sl2, po, pml);
+                         kv_heads, n_split, sl2, po, pml, counters, out, ldo);
   else
     launch_attn<DT_F16>(head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
-                        kv_heads, n_split, sl2, po, pml);
-  if (int rc = check_hip(hipGetLastError(), "attention launch")) return rc;
-  launch_dt<Combine>(dtype, dim3(heads, (unsigned)rows), dim3(std::min(256, (int)head_dim)), st,
-                     (const float*)po, (const float*)pml, out, ldo, (int)heads, (int)head_dim,
-                     (int)n_split);
-  return check_hip(hipGetLastError(), "attention combine launch");
+                        kv_heads, n_split, sl2, po, pml, counters, out, ldo);
+  return check_hip(hipGetLastError(), "attention launch");
 }
 
 extern "C" int ssl_silu_mul(const void* gate, int64_t ldg, const void* up, int64_t ldu, void* out,

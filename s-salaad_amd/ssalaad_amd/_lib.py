@@ -93,10 +93,11 @@ _SIGNATURES = {
     ),
     "ssl_decode_attention_splits": (_c_i32, [_c_i64, _c_i32, _c_i32, _c_i64]),
     "ssl_decode_attention_workspace_size": (_c_i64, [_c_i64, _c_i32, _c_i32, _c_i32]),
+    "ssl_decode_attention_counter_count": (_c_i64, [_c_i64, _c_i32, _c_i32]),
     "ssl_decode_attention": (
         ctypes.c_int,
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i64,
-         ctypes.c_float, _c_i32, _c_p, _c_i64, _c_i32, _c_p],
+         ctypes.c_float, _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_p],
     ),
     "ssl_silu_mul": (
         ctypes.c_int,

@@ -8,7 +8,8 @@ Hugging Face forward of the model `build_efficient_model` returns:
 
   per layer   add_rmsnorm (residual add fused; the embedding gather at layer 0)
               -> q,k,v in one fused SLR launch
-              -> rope + cache append -> split-context attention -> o_proj
+              -> rope + cache append -> split-context attention (its slices merged
+              by the last one to finish) -> o_proj
               -> add_rmsnorm -> gate,up in one fused SLR launch -> silu·up
               -> down_proj
   then        the final add_rmsnorm and the LM head (a plain library GEMM).
@@ -125,6 +126,9 @@ class DecodeEngine:
         self.pos = torch.zeros(max_batch, dtype=torch.int32, device=dev)
         ws = self.lib.ssl_decode_attention_workspace_size(max_batch, self.heads, hd, 64)
         self.attn_ws = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
+        # arrival counters of the attention slices: zero at rest, reset by the kernel
+        nc = self.lib.ssl_decode_attention_counter_count(max_batch, self.heads, self.kv_heads)
+        self.attn_cnt = torch.zeros(max(nc, 1), dtype=torch.int32, device=dev)
         self.use_graphs = use_graphs
         self._stream = torch.cuda.Stream(dev)
         self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
@@ -167,7 +171,8 @@ class DecodeEngine:
             rc = lib.ssl_decode_attention(
                 self.q.data_ptr(), self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(),
                 self.pos.data_ptr(), self.att.data_ptr(), self.att.stride(0), B, H, KH, hd, ctx,
-                self.scale, n_split, self.attn_ws.data_ptr(), self.attn_ws.numel(), self.dt, st)
+                self.scale, n_split, self.attn_ws.data_ptr(), self.attn_ws.numel(),
+                self.attn_cnt.data_ptr(), self.attn_cnt.numel(), self.dt, st)
             self._check(rc, "ssl_decode_attention")
             o = L.o(self.att[:B])
             self._add_rmsnorm(B, o, L.post_norm)

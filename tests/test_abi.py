@@ -335,12 +335,16 @@ def test_decode_entry_points_reject_bad_arguments_before_any_launch():
     assert lib.ssl_rope_kv_append(*args, 8, 1, 128, 16, bf, None) == 1
     # attention: head_dim without a kernel, too many splits, small workspace, misalignment
     a = [fake, fake, fake, fake, fake, 512, 2, 4, 4]
-    assert lib.ssl_decode_attention(*a, 96, 16, 0.1, 1, fake, 1 << 20, bf, None) == 2
-    assert lib.ssl_decode_attention(*a, 128, 16, 0.1, 300, fake, 1 << 20, bf, None) == 1
+    cn = lib.ssl_decode_attention_counter_count(2, 4, 4)
+    assert cn == 2 * 4 and lib.ssl_decode_attention_counter_count(2, 16, 1) == 2 * 2
+    assert lib.ssl_decode_attention(*a, 96, 16, 0.1, 1, fake, 1 << 20, fake, cn, bf, None) == 2
+    assert lib.ssl_decode_attention(*a, 128, 16, 0.1, 300, fake, 1 << 20, fake, cn, bf, None) == 1
     need = lib.ssl_decode_attention_workspace_size(2, 4, 128, 3)
     assert need == 2 * 4 * 3 * 130 * 4
-    assert lib.ssl_decode_attention(*a, 128, 16, 0.1, 3, fake, need - 1, bf, None) == 3
-    assert lib.ssl_decode_attention(fake + 2, *a[1:], 128, 16, 0.1, 3, fake, need, bf, None) == 1
+    assert lib.ssl_decode_attention(*a, 128, 16, 0.1, 3, fake, need - 1, fake, cn, bf, None) == 3
+    assert lib.ssl_decode_attention(*a, 128, 16, 0.1, 3, fake, need, fake, cn - 1, bf, None) == 3
+    assert lib.ssl_decode_attention(fake + 2, *a[1:], 128, 16, 0.1, 3, fake, need, fake, cn, bf,
+                                    None) == 1
     # silu_mul: leading dimension below n
     assert lib.ssl_silu_mul(fake, 8, fake, 16, fake, 16, 2, 16, bf, None) == 1
     assert lib.ssl_silu_mul(None, 8, None, 16, None, 16, 0, 16, bf, None) == 0
@@ -348,8 +352,8 @@ def test_decode_entry_points_reject_bad_arguments_before_any_launch():
 
 def test_decode_attention_split_policy():
     lib = _lib.load()
-    # about 1024 workgroups, slices of at least 64 positions, at most 64 slices
-    assert lib.ssl_decode_attention_splits(1, 16, 16, 1024) == 16
+    # about 1024 workgroups, slices of at least 128 positions, at most 64 slices
+    assert lib.ssl_decode_attention_splits(1, 16, 16, 1024) == 8
     assert lib.ssl_decode_attention_splits(16, 16, 16, 1024) == 4
     assert lib.ssl_decode_attention_splits(1, 32, 8, 100000) == 64
     assert lib.ssl_decode_attention_splits(64, 32, 32, 4096) == 1

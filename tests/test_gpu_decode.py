@@ -52,12 +52,16 @@ def _attention(q, kc, vc, pos, heads, kvh, hd, ctx, n_split=None):
     ns = n_split or lib.ssl_decode_attention_splits(B, heads, kvh, ctx)
     ws = torch.empty(lib.ssl_decode_attention_workspace_size(B, heads, hd, ns), dtype=torch.uint8,
                      device=q.device)
+    cnt = torch.zeros(lib.ssl_decode_attention_counter_count(B, heads, kvh), dtype=torch.int32,
+                      device=q.device)
     out = torch.full((B, heads * hd), float("nan"), dtype=q.dtype, device=q.device)
     rc = lib.ssl_decode_attention(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(),
                                   out.data_ptr(), out.stride(0), B, heads, kvh, hd, ctx,
-                                  hd ** -0.5, ns, ws.data_ptr(), ws.numel(),
-                                  L.dtype_code(q.dtype), L.stream_ptr(q.device))
+                                  hd ** -0.5, ns, ws.data_ptr(), ws.numel(), cnt.data_ptr(),
+                                  cnt.numel(), L.dtype_code(q.dtype), L.stream_ptr(q.device))
     L.check(rc, "ssl_decode_attention")
+    torch.cuda.synchronize()
+    assert (cnt == 0).all()  # every arrival counter is back at zero
     return out
 
 
