@@ -101,7 +101,9 @@ def test_bundle_reproduces_the_dense_model(tmp_path, layout, gpu_device):
                  "S": _bsr_cpu(S.to(torch.bfloat16), 16), "block_p": 16, "block_q": 16}
     path = tmp_path / "model.pt"
     bundle.save_artifact(path, {name: layer}, {"mode": "egar"}, model=model, model_config=TINY)
-    restored, _, meta = bundle.build_efficient_model(path, device=gpu_device)
+    # the bundle holds bf16 factors, as the reference's does; the restored model
+    # runs in fp32 so that no bf16 attention product runs on the GPU
+    restored, _, meta = bundle.build_efficient_model(path, device=gpu_device, dtype=torch.float32)
     assert meta == {"mode": "egar"}
     got = restored(input_ids=ids.to(gpu_device)).logits.float().cpu()
     torch.testing.assert_close(got, expected, atol=0.1, rtol=0.1)
@@ -147,3 +149,54 @@ def test_llama60m_every_projection_slr_matches_dense_weights(tmp_path, gpu_devic
     assert type(model.get_submodule("model.layers.3.mlp.down_proj")).__name__.startswith("_LRSLinear")
     err = float((got - want).abs().max() / want.abs().max())
     assert err <= 1e-4, err
+
+
+@pytest.mark.gpu
+def test_bundle_then_generate_matches_the_recompute_loop(tmp_path, gpu_device):
+    """A bundle loaded by build_efficient_model (fp32) generates, with the cached
+    decode step, the tokens the reference's loop picks by recomputing the prefix
+    with the same model (generate.py:12-26). Two layers; q/k/v/gate/up/down are
+    SLR linears (32x32 blocks at 50%), o_proj of layer 0 a plain dense layer."""
+    from ssalaad_amd import generate
+
+    cfg = dict(TINY, hidden_size=256, intermediate_size=352, num_hidden_layers=2,
+               num_attention_heads=4, num_key_value_heads=2, vocab_size=300)
+    torch.manual_seed(1)
+    gen = torch.Generator().manual_seed(1)
+    dense = bundle.build_model_from_config(cfg).eval()
+    with torch.no_grad():
+        for name, prm in dense.named_parameters():
+            if "norm" not in name:
+                prm.copy_(torch.randn(prm.shape, generator=gen) * (1.0 if "embed" in name else 0.08))
+    layers = {}
+    for li in range(2):
+        for proj in PROJ:
+            name = f"model.layers.{li}.{proj}"
+            lin = dense.get_submodule(name)
+            if li == 0 and proj == "self_attn.o_proj":
+                layers[name] = {"W": lin.weight.detach().clone()}
+                continue
+            n, m = lin.out_features, lin.in_features
+            r, p = 32, 32
+            A = torch.randn(n, r, generator=gen) * 0.1
+            B = torch.randn(r, m, generator=gen) * 0.1
+            NB, NBK = n // p, m // p
+            keep = torch.randperm(NB * NBK, generator=gen)[: NB * NBK // 2]
+            mask = torch.zeros(NB * NBK)
+            mask[keep] = 1
+            S = torch.randn(n, m, generator=gen) * 0.05 * mask.view(NB, 1, NBK, 1).expand(
+                NB, p, NBK, p).reshape(n, m)
+            with torch.no_grad():
+                lin.weight.copy_(A @ B + S)
+            layers[name] = {"A": A, "B": B, "S": _bsr_cpu(S, p), "block_p": p, "block_q": p}
+    path = tmp_path / "gen.pt"
+    bundle.save_artifact(path, layers, {"mode": "egar"}, model=dense, model_config=cfg)
+    model, _, _ = bundle.build_efficient_model(path, device=gpu_device, dtype=torch.float32)
+    prompt = torch.randint(3, 300, (2, 6), generator=gen)
+    out = generate(model, prompt, 10)
+    seq = prompt.to(gpu_device)
+    with torch.no_grad():
+        for _ in range(10):
+            logits = model(input_ids=seq, use_cache=False).logits[:, -1]
+            seq = torch.cat((seq, logits.argmax(-1, keepdim=True)), dim=1)
+    assert torch.equal(out, seq.cpu())
