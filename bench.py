@@ -616,8 +616,9 @@ def main():
         copy_probe(args.copy_probe, max(1, args.steps))
         return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the SLR linear "
-              "shards by output block-rows with no exchange; see the design notes).",
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported. The SLR linear "
+              "shards by output block-rows with no exchange inside a layer, so one GPU's "
+              "share at its real shape is what this benchmark measures.",
               file=sys.stderr)
         sys.exit(2)
     if args.workload != "llama1b_decode":
