@@ -45,6 +45,11 @@ headline):
                        heads, FFN 1376, vocab 32000) with every q/k/v/o/gate/
                        up/down an SLR linear (rank dim/4, 32×32 blocks at 50%,
                        N(0, 0.02)), fp32 forward of 8 × 256 tokens: tok/s
+  sweep                the LLaMA-7B layer set (11008x4096, 4096x11008, 4096x4096;
+                       64x64 blocks at 30/50/70%; r 256; 1, 16, 256, 2048 tokens)
+                       and the skew sweep (4096x11008, r 128, Zipf(1.2) rows at
+                       10/50/90% mean density, blocks 16/32/64, 1 and 2048
+                       tokens): one JSON line with every point in "points"
   llama1b_decode_step  the whole KV-cached decode step of the LLaMA-1B-shaped
                        model (the projection stack above, plus RMSNorm, rotary
                        embedding, attention over a 1024-token context of
@@ -85,16 +90,53 @@ def llama1b_shapes():
             ("down", h, f)]
 
 
-def make_linear(n, m, r, p, density, gen, dev, dtype):
-    """Random SLR linear with exactly round(d·NB·NBK) uniformly placed blocks."""
+def zipf_row_counts(NB: int, NBK: int, density: float, gen, s: float = 1.2):
+    """Blocks per row ∝ rank^-s over a seeded permutation of the rows, water-filled
+    to round(d·NB·NBK) blocks in all under the cap of NBK per row."""
+    import torch
+
+    target = int(round(density * NB * NBK))
+    w = torch.arange(1, NB + 1, dtype=torch.float64) ** (-s)
+    w = w[torch.randperm(NB, generator=gen)]
+    counts = torch.zeros(NB, dtype=torch.int64)
+    remaining = target
+    while remaining > 0:
+        free = counts < NBK
+        if not bool(free.any()):
+            break
+        share = w * free
+        add = torch.minimum((share / share.sum() * remaining).floor().long(), NBK - counts)
+        if int(add.sum()) == 0:  # the remainder one at a time, largest weight first
+            for i in torch.argsort(-share).tolist():
+                if remaining == 0:
+                    break
+                if counts[i] < NBK:
+                    counts[i] += 1
+                    remaining -= 1
+            break
+        counts += add
+        remaining -= int(add.sum())
+    return counts
+
+
+def make_linear(n, m, r, p, density, gen, dev, dtype, skew=False):
+    """Random SLR linear with exactly round(d·NB·NBK) blocks: uniformly placed,
+    or with Zipf(1.2) row counts (skew) and uniform columns within each row."""
     import torch
 
     from ssalaad_amd import LRSLinear
 
     NB, NBK = -(-n // p), -(-m // p)
-    k = int(round(density * NB * NBK))
-    slots = torch.randperm(NB * NBK, generator=gen, device="cpu")[:k].sort().values
-    rows, cols = slots // NBK, slots % NBK
+    if skew:
+        counts = zipf_row_counts(NB, NBK, density, gen)
+        rows = torch.repeat_interleave(torch.arange(NB), counts)
+        cols = torch.cat([torch.randperm(NBK, generator=gen)[: int(c)].sort().values
+                          for c in counts])
+        k = int(counts.sum())
+    else:
+        k = int(round(density * NB * NBK))
+        slots = torch.randperm(NB * NBK, generator=gen, device="cpu")[:k].sort().values
+        rows, cols = slots // NBK, slots % NBK
     crow = torch.zeros(NB + 1, dtype=torch.int64)
     crow[1:] = torch.bincount(rows, minlength=NB).cumsum(0)
     vals = (torch.randn(k, p, p, generator=gen, device="cpu") * 0.02).to(dtype)
@@ -394,7 +436,67 @@ def run_workload(args) -> dict:
                     roofline=None)
     if args.workload == "llama1b_decode_step":
         return run_decode_step(args, base, gen, dev)
+    if args.workload == "sweep":
+        return run_sweep(args, base, gen, dev)
     raise SystemExit(f"unknown workload {args.workload}")
+
+
+def run_sweep(args, base: dict, gen, dev) -> dict:
+    """The LLaMA-7B layer-set and skew sweeps: one point per (shape, density,
+    block, structure, tokens). Up to 256 tokens (HBM-bound) the weights are cycled
+    over enough copies to exceed 600 MB in a HIP graph; 2048 tokens run eagerly
+    on one copy (MFMA-bound). value = the 11008x4096, d 0.5, 1-token point."""
+    import math
+
+    import torch
+
+    pts = []
+    for (n, m) in ((11008, 4096), (4096, 11008), (4096, 4096)):
+        for d in (0.3, 0.5, 0.7):
+            for M in (1, 16, 256, 2048):
+                pts.append(dict(set="llama7b", n=n, m=m, r=256, p=64, d=d, skew=False, M=M))
+    for p in (16, 32, 64):
+        for d in (0.1, 0.5, 0.9):
+            for M in (1, 2048):
+                pts.append(dict(set="skew", n=4096, m=11008, r=128, p=p, d=d, skew=True, M=M))
+    out = []
+    head = None
+    for pt in pts:
+        n, m, r, p, d, M = pt["n"], pt["m"], pt["r"], pt["p"], pt["d"], pt["M"]
+        first = make_linear(n, m, r, p, d, gen, dev, torch.bfloat16, skew=pt["skew"])
+        b = algorithmic_bytes(first, M, 2)
+        wbytes = algorithmic_bytes(first, 0, 2)["total"]
+        x = torch.randn(M, m, generator=gen).to(torch.bfloat16).to(dev)
+        if M <= 256:
+            copies = max(4, math.ceil(600e6 / wbytes))
+            mods = [first] + [make_linear(n, m, r, p, d, gen, dev, torch.bfloat16, skew=pt["skew"])
+                              for _ in range(copies - 1)]
+            sts = [md._kernel() for md in mods]
+            us = _time_graph([lambda st=st: st.forward(x, n) for st in sts],
+                             max(20, args.steps // 2))
+            del mods, sts
+        else:
+            copies = 1
+            us = _time_eager(lambda: first(x), max(5, args.steps // 10))
+        gbs = b["total"] / us / 1e3
+        tf = b["flops"] / us / 1e6
+        bound = "hbm" if M <= 256 else "mfma"
+        frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tf / 2500.0
+        rec = dict(pt, us=round(us, 3), gbs=round(gbs, 1), tflops=round(tf, 1), bound=bound,
+                   frac=round(frac, 4), copies=copies, nnz=first.S_nnz)
+        out.append(rec)
+        if (pt["set"], n, m, d, M) == ("llama7b", 11008, 4096, 0.5, 1):
+            head = rec
+        _log(f"[sweep] {json.dumps(rec)}")
+        del first, x
+        torch.cuda.empty_cache()
+    return dict(base, metric="SLR-linear sweep GB/s (LLaMA-7B set and skewed structures)",
+                value=head["gbs"], unit="GB/s", ms_per_step=round(head["us"] / 1e3, 5),
+                dtype="bf16",
+                config={"workload": "sweep", "points": len(out), "parallelism": "single_gpu"},
+                roofline={"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": head["frac"], "traffic": None},
+                points=out)
 
 
 def run_decode_step(args, base: dict, gen, dev) -> dict:
@@ -607,7 +709,7 @@ def main():
     ap.add_argument("--workload", default="llama1b_decode",
                     choices=["llama1b_decode", "llama7b_ffn_decode", "llama7b_ffn_prefill",
                              "llama7b_ffn_decode_nm24", "block_topk", "llama60m_forward",
-                             "llama1b_decode_step"])
+                             "llama1b_decode_step", "sweep"])
     args = ap.parse_args()
     args.batch_set = args.batch is not None
     if args.batch is None:
