@@ -50,6 +50,11 @@ _BALANCE_LATENT_MIN = 4
 # Block sizes it applies to: at p = 32 (two workgroups per compute unit,
 # shorter rows) the split rows' exchange costs more than the straggler.
 _BALANCE_P = (64,)
+# Any block size: structures whose longest row exceeds this multiple of the mean
+# and that the default target leaves whole (Zipf rows of 16×16 blocks at decode:
+# 51 → 26 µs; rows the default already splits got slower when split further,
+# the latent losing its K chunks to the extra row workgroups).
+_BALANCE_SKEW = 1.5
 
 
 def balanced_target(costs: np.ndarray, cost_bytes: int, slots: int, lat_tiles: int) -> int:
@@ -62,7 +67,7 @@ def balanced_target(costs: np.ndarray, cost_bytes: int, slots: int, lat_tiles: i
     costs = costs[costs > 0]
     if costs.size == 0 or _BALANCE_LATENT_MIN <= 0:
         return 0
-    if costs.mean() * cost_bytes < _BALANCE_MIN_ROW_BYTES:
+    if costs.max() * cost_bytes < _BALANCE_MIN_ROW_BYTES:
         return 0
     budget = slots - _BALANCE_LATENT_MIN * lat_tiles
     if budget <= costs.size:

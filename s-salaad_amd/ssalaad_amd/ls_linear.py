@@ -106,11 +106,16 @@ class _KernelState:
         if pl is None:
             total = self.nblk_total * self.block_q + self.NB * self.lr_units * 32
             target = _runtime.plan_target_cost(total, self.p, self.elem, M)
-            if key == 1 and self.s_format == 0 and self.p in _runtime._BALANCE_P:
-                # one workgroup per compute unit at p = 64: split the longest rows
-                costs = np.diff(self.crow_h).astype(np.int64) * self.block_q + self.lr_units * 32
+            costs = np.diff(self.crow_h).astype(np.int64) * self.block_q + self.lr_units * 32
+            # a skewed structure whose longest row the default target leaves whole
+            skewed = (costs.size > 0 and costs.max() > _runtime._BALANCE_SKEW * costs.mean()
+                      and (target == 0 or costs.max() <= target))
+            if key == 1 and self.s_format == 0 and (self.p in _runtime._BALANCE_P or skewed):
+                # split the longest rows into the workgroup slots left free
                 n_cu = torch.cuda.get_device_properties(self.device).multi_processor_count
-                bal = _runtime.balanced_target(costs, self.p * self.elem, n_cu, self.r_pad // 16)
+                per_cu = 2 if (self.p <= 32 and self.elem == 2) else 1
+                bal = _runtime.balanced_target(costs, self.p * self.elem, n_cu * per_cu,
+                                               self.r_pad // 16)
                 if bal:
                     target = min(target, bal) if target else bal
             table, n_chunks, n_slots = _runtime.build_plan(
