@@ -233,6 +233,21 @@ def test_llama7b_ffn_shape_decode(M, gpu_device):
     assert err(y, oracle_y(prob, x)) <= 1e-2
 
 
+@pytest.mark.parametrize("M", [1, 16])
+def test_zipf_16x16_rows_split_for_decode(M, gpu_device):
+    """4096×11008 bf16, rank 128, Zipf(1.2) rows of 16×16 blocks at 10% mean density:
+    the full rows (688 blocks, 352 KB) are split across workgroups by the decode
+    balancing, and the result matches the oracle."""
+    prob = make_problem(4096, 11008, 128, 16, 0.1, torch.bfloat16, seed=11, skew=True)
+    mod = _module(prob, gpu_device)
+    st = mod._kernel()
+    assert st.plan(M).n_chunks > st.NB  # some rows were split
+    x = make_x(prob, M)
+    y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= 1e-2
+
+
 def test_llama1b_down_proj_ragged_decode(gpu_device):
     """2048×5461 bf16 (in_features not a block multiple), 32×32 blocks, rank 256."""
     prob = make_problem(2048, 5461, 256, 32, 0.5, torch.bfloat16, seed=8, pad=True)
