@@ -291,6 +291,15 @@ def _time_graph(fns, reps):
     return e0.elapsed_time(e1) * 1e3 / reps / len(fns)
 
 
+def _time_calls(fns, reps, eager: bool):
+    """µs per call of `fns` called in turn: replayed in a HIP graph, or with
+    --eager issued one by one (hardware counters are collected per dispatch)."""
+    if not eager:
+        return _time_graph(fns, reps)
+    n = len(fns)
+    return _time_eager(lambda: [f() for f in fns], max(1, reps // n)) / n
+
+
 def _time_eager(fn, reps):
     import torch
 
@@ -320,7 +329,7 @@ def run_workload(args) -> dict:
         mods = [make_linear(n, m, r, p, 0.5, gen, dev, torch.bfloat16) for _ in range(8)]
         x = torch.randn(M, m, generator=gen).to(torch.bfloat16).to(dev)
         sts = [md._kernel() for md in mods]
-        us = _time_graph([lambda st=st: st.forward(x, n) for st in sts], args.steps)
+        us = _time_calls([lambda st=st: st.forward(x, n) for st in sts], args.steps, args.eager)
         b = algorithmic_bytes(mods[0], M, 2)["total"]
         gbs = b / us / 1e3
         return dict(base, metric="SLR-linear decode GB/s (LLaMA-7B FFN projection)",
@@ -345,7 +354,7 @@ def run_workload(args) -> dict:
             mods.append(LRSLinear(A, B, S.to(dev), in_features=m, out_features=n, nm_n=2, nm_m=4))
         x = torch.randn(M, m, generator=gen).to(torch.bfloat16).to(dev)
         sts = [md._kernel() for md in mods]
-        us = _time_graph([lambda st=st: st.forward(x, n) for st in sts], args.steps)
+        us = _time_calls([lambda st=st: st.forward(x, n) for st in sts], args.steps, args.eager)
         b = 2 * M * (m + n) + 2 * r * (n + m) + 2 * (n * m // 2) + n * m // 8
         gbs = b / us / 1e3
         return dict(base, metric="SLR-linear decode GB/s (LLaMA-7B FFN projection, 2:4 S)",
@@ -701,7 +710,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
-                    help="launch the step eagerly instead of replaying a HIP graph")
+                    help="launch eagerly instead of replaying a HIP graph (default workload, "
+                         "llama7b_ffn_decode and llama7b_ffn_decode_nm24)")
     ap.add_argument("--no-group", action="store_true",
                     help="one launch per linear instead of grouping q/k/v and gate/up")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
