@@ -50,6 +50,8 @@ headline):
                        and the skew sweep (4096x11008, r 128, Zipf(1.2) rows at
                        10/50/90% mean density, blocks 16/32/64, 1 and 2048
                        tokens): one JSON line with every point in "points"
+  llama1b_prefill      the default workload's 24-layer projection stack at 2048
+                       tokens (one HIP graph of the 96 grouped launches): TFLOP/s
   llama1b_decode_step  the whole KV-cached decode step of the LLaMA-1B-shaped
                        model (the projection stack above, plus RMSNorm, rotary
                        embedding, attention over a 1024-token context of
@@ -447,6 +449,22 @@ def run_workload(args) -> dict:
         return run_decode_step(args, base, gen, dev)
     if args.workload == "sweep":
         return run_sweep(args, base, gen, dev)
+    if args.workload == "llama1b_prefill":
+        M = args.batch if args.batch_set else 2048
+        args.batch = M
+        g = run_gpu(args)
+        tf = g["step_tflops"]
+        return dict(base, metric="LLaMA-1B projection stack prefill TFLOP/s (2048 tokens)",
+                    value=round(tf, 1), unit="TFLOP/s", ms_per_step=round(g["ms_step"], 4),
+                    dtype="bf16",
+                    config={"workload": "llama1b_prefill", "layers": args.layers, "hidden": 2048,
+                            "ffn": 5461, "rank": 256, "block": 32, "block_density": 0.5,
+                            "batch_tokens": M, "launches_per_step": g["n_launches"],
+                            "parallelism": "single_gpu"},
+                    roofline={"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
+                              "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4), "traffic": None,
+                              "tok_s": round(g["tok_s"], 1)},
+                    graph_matches_eager=g["graph_matches_eager"])
     raise SystemExit(f"unknown workload {args.workload}")
 
 
@@ -719,7 +737,7 @@ def main():
     ap.add_argument("--workload", default="llama1b_decode",
                     choices=["llama1b_decode", "llama7b_ffn_decode", "llama7b_ffn_prefill",
                              "llama7b_ffn_decode_nm24", "block_topk", "llama60m_forward",
-                             "llama1b_decode_step", "sweep"])
+                             "llama1b_decode_step", "sweep", "llama1b_prefill"])
     args = ap.parse_args()
     args.batch_set = args.batch is not None
     if args.batch is None:
