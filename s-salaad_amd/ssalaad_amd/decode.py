@@ -72,14 +72,17 @@ class DecodeEngine:
             raise ValueError(f"unsupported activation {cfg.hidden_act}; the decode step uses silu")
         if any(t != "full_attention" for t in (getattr(cfg, "layer_types", None) or [])):
             raise NotImplementedError("sliding-window layers are not supported by the decode step")
-        embed = model.model.embed_tokens.weight
-        if not embed.is_cuda:
-            raise ValueError("the decode engine runs on a ROCm GPU; move the model to 'cuda' first")
+        hd = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        if hd not in (64, 128, 256):
+            raise NotImplementedError(f"head_dim {hd}: the decode attention runs 64, 128 or 256")
         rot = model.model.rotary_emb
         if getattr(rot, "rope_type", "default") == "dynamic":
             raise NotImplementedError("dynamic rotary scaling is not supported by the decode step")
         if max_batch < 1 or max_context < 1:
             raise ValueError("max_batch and max_context must be positive")
+        embed = model.model.embed_tokens.weight
+        if not embed.is_cuda:
+            raise ValueError("the decode engine runs on a ROCm GPU; move the model to 'cuda' first")
         self.lib = _lib.load()
         self.device = embed.device
         self.dtype = embed.dtype
