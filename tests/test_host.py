@@ -158,9 +158,14 @@ def test_generate_checks_arguments_like_the_reference():
 
 def test_decode_engine_has_no_cpu_path():
     from ssalaad_amd import DecodeEngine
+    from ssalaad_amd.bundle import build_model_from_config
 
+    model = build_model_from_config({
+        "model_type": "llama", "hidden_size": 128, "intermediate_size": 64, "num_hidden_layers": 1,
+        "num_attention_heads": 2, "num_key_value_heads": 2, "vocab_size": 50,
+        "max_position_embeddings": 16, "hidden_act": "silu"})
     with pytest.raises(ValueError, match="ROCm GPU"):
-        DecodeEngine(_tiny_llama(), max_batch=1, max_context=4)
+        DecodeEngine(model, max_batch=1, max_context=4)
 
 
 def test_decode_engine_rejects_head_widths_without_a_kernel():
