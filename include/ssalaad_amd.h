@@ -329,6 +329,24 @@ int ssl_decode_attention(const void* q, const void* k_cache, const void* v_cache
                          int32_t n_split, void* workspace, int64_t workspace_bytes,
                          int32_t* counters, int64_t n_counters, int32_t dtype, void* stream);
 
+/* ssl_rope_kv_append followed by ssl_decode_attention in one launch, with the
+ * same results: q, k, v are the projections of the new token ([rows, ld*],
+ * 16-byte aligned rows), the new key is rotated and, with the value, written
+ * into the caches at pos[row], and the attention reads that position from
+ * registers. The roped q is not stored. Workspace, counters and splits as for
+ * ssl_decode_attention; head_dim 64, 128 or 256. Replaces, for one decode
+ * step, the rotary embedding, the cache update and sdpa of LlamaAttention
+ * (transformers modeling_llama.py), as called by the reference's generation
+ * loop (ssalaad/inference/generate.py:1-26). */
+int ssl_decode_rope_attention(const void* q, int64_t ldq, const void* k, int64_t ldk,
+                              const void* v, int64_t ldv, const void* cos_table,
+                              const void* sin_table, const void* q_norm, const void* k_norm,
+                              float eps, const int32_t* pos, void* k_cache, void* v_cache,
+                              void* out, int64_t ldo, int64_t rows, int32_t heads,
+                              int32_t kv_heads, int32_t head_dim, int64_t max_ctx, float scale,
+                              int32_t n_split, void* workspace, int64_t workspace_bytes,
+                              int32_t* counters, int64_t n_counters, int32_t dtype, void* stream);
+
 /* out = silu(gate) · up (LlamaMLP's act_fn(gate_proj(x)) * up_proj(x)), silu
  * rounded to the dtype before the product. */
 int ssl_silu_mul(const void* gate, int64_t ldg, const void* up, int64_t ldu, void* out,

@@ -232,15 +232,96 @@ struct Vec16 {
       }
     }
   }
+  // f holds values already rounded to DT
+  __device__ __forceinline__ static uint4 pack(const float* f) {
+    if constexpr (DT == DT_F32) {
+      return uint4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                   __float_as_uint(f[3])};
+    } else {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = to_bits<DT>(f[2 * i]) | (to_bits<DT>(f[2 * i + 1]) << 16);
+      return uint4{w[0], w[1], w[2], w[3]};
+    }
+  }
 };
+
+// (a & mask) | (b & ~mask), dword by dword
+__device__ __forceinline__ uint4 merge(uint32_t mask, const uint4 a, const uint4 b) {
+  return uint4{(a.x & mask) | (b.x & ~mask), (a.y & mask) | (b.y & ~mask),
+               (a.z & mask) | (b.z & ~mask), (a.w & mask) | (b.w & ~mask)};
+}
+
+// The q/k/v projections of the new token, for the attention launch that also
+// applies the rotary embedding and appends the key and value to the cache.
+struct RopeIn {
+  const void* q;
+  int64_t ldq;
+  const void* k;
+  int64_t ldk;
+  const void* v;
+  int64_t ldv;
+  const void* cos_t;   // [max_ctx, head_dim]
+  const void* sin_t;
+  const void* q_norm;  // Qwen3's per-head RMSNorm weights, or null
+  const void* k_norm;
+  float eps;
+  void* k_cache;       // the caches the launch reads, written at the new position
+  void* v_cache;
+};
+
+// One head's rotary embedding in the attention layout (lane vv of a row group
+// holds features vv·VE … vv·VE + VE − 1), with rope_kv_kernel's rounding
+// points. The partner features (± head_dim / 2) are read from memory rather
+// than exchanged between lanes (x: own, xp: partner; c, s: the tables at the
+// own features; w, wp: the per-head RMSNorm weights when `norm`). Under the
+// norm the sum of squares is reduced over the row group's LPR lanes. All
+// operands are raw vectors, loaded by the caller before the first use.
+template <int DT, int HD>
+__device__ __forceinline__ void rope_apply(float* out, const uint4 xr, const uint4 xpr,
+                                          const uint4 cr, const uint4 sr, bool norm,
+                                          const uint4 wr, const uint4 wpr, float eps, int vv) {
+#pragma clang fp contract(off)
+  constexpr int VE = Vec16<DT>::VE;
+  constexpr int LPR = HD / VE;
+  const bool low = vv * VE < HD / 2;
+  float x[VE], xp[VE], c[VE], s[VE];
+  Vec16<DT>::unpack(x, xr);
+  Vec16<DT>::unpack(xp, xpr);
+  Vec16<DT>::unpack(c, cr);
+  Vec16<DT>::unpack(s, sr);
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) ss += x[e] * x[e];
+#pragma unroll
+    for (int off = 1; off < LPR; off <<= 1) ss += __shfl_xor(ss, off);
+    const float rs = rsqrtf(ss / (float)HD + eps);
+    float w[VE], wp[VE];
+    Vec16<DT>::unpack(w, wr);
+    Vec16<DT>::unpack(wp, wpr);
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+      x[e] = rnd<DT>(w[e] * rnd<DT>(x[e] * rs));
+      xp[e] = rnd<DT>(wp[e] * rnd<DT>(xp[e] * rs));
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < VE; ++e) {  // rotate_half(x) = (-x2, x1)
+    const float a = rnd<DT>(x[e] * c[e]), bb = rnd<DT>(xp[e] * s[e]);
+    out[e] = rnd<DT>(low ? a - bb : a + bb);
+  }
+}
 
 constexpr int kAttnJ = 4;  // wave instructions (row groups) per step
 
-template <int DT, int HD, int GB>
-__global__ __launch_bounds__(256) void attn_split_kernel(
+// ROPE: 0 q read as given; 1 rotary embedding and cache append in the launch;
+// 2 the same after Qwen3's per-head RMSNorm.
+template <int DT, int HD, int GB, int ROPE>
+__global__ __launch_bounds__(256, ROPE == 1 && GB == 1 ? 4 : 1) void attn_split_kernel(
     const void* q, const void* kc, const void* vc, const int32_t* pos, int64_t max_ctx, int heads,
     int kv_heads, int n_split, float scale_log2, float* part_o, float* part_ml, int* counters,
-    void* out, int64_t ldo) {
+    void* out, int64_t ldo, RopeIn R) {
   constexpr int VE = Vec16<DT>::VE;
   constexpr int LPR = HD / VE;
   constexpr int RPI = 64 / LPR;
@@ -261,20 +342,97 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int rr = lane / LPR, vv = lane % LPR;
 
-  const int64_t L = min((int64_t)pos[b] + 1, max_ctx);
+  const int64_t pcur = pos[b];
+  const int64_t L = min(pcur + 1, max_ctx);
   int64_t per = (L + n_split - 1) / n_split;
   per = (per + STEP - 1) / STEP * STEP;
   const int64_t lo = (int64_t)split * per;
   const int64_t hi = min(lo + per, L);
+  const int64_t head_off = (b * kv_heads + kh) * max_ctx * HD;
 
   float qf[GB][VE];
+  uint4 kn = {0, 0, 0, 0}, vn = {0, 0, 0, 0};  // the new token's key (rotated) and value
+  // Rotary embedding of the query heads and the new key. It runs in the first
+  // step of the loop, after that step's key and value loads are issued, so the
+  // projections' loads share their round trip.
+  auto rope_prep = [&]() {
+    // the host rejects positions outside [0, max_ctx); the clamp keeps table reads in bounds
+    const int64_t pt = min(max(pcur, (int64_t)0), max_ctx - 1);
+    const int e0 = vv * VE;
+    const int ep = e0 < HD / 2 ? e0 + HD / 2 : e0 - HD / 2;
+    // Buffer loads: each row base is uniform (a scalar resource) and lanes add
+    // one of two 32-bit byte offsets, so these loads, whose addresses do not
+    // change over the loop, hold no 64-bit address registers through it.
+    const int o0 = e0 * Elem<DT>::bytes, op = ep * Elem<DT>::bytes;
+    auto at = [](const void* base, int64_t elems, int off) {
+      const auto r = __builtin_amdgcn_make_buffer_rsrc(
+          (char*)const_cast<void*>(base) + elems * Elem<DT>::bytes, (short)0, 0x7fffffff,
+          0x00020000);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+      return uint4{v[0], v[1], v[2], v[3]};
+    };
+    // every load first (a use between them would wait for all earlier loads,
+    // the key/value loads of the step included)
+    uint4 qx[GB], qxp[GB];
 #pragma unroll
-  for (int g = 0; g < GB; ++g) {
-    if (g < ng) {
-      Vec16<DT>::load(qf[g], q, (b * heads + (int64_t)kh * G + g0 + g) * HD + vv * VE);
-    } else {
+    for (int g = 0; g < GB; ++g) {
+      const int64_t row = b * R.ldq + ((int64_t)kh * G + g0 + (g < ng ? g : 0)) * HD;
+      qx[g] = at(R.q, row, o0);
+      qxp[g] = at(R.q, row, op);
+    }
+    const int64_t krow = b * R.ldk + (int64_t)kh * HD;
+    const uint4 kx = at(R.k, krow, o0), kxp = at(R.k, krow, op);
+    const uint4 cr = at(R.cos_t, pt * HD, o0), sr = at(R.sin_t, pt * HD, o0);
+    vn = at(R.v, b * R.ldv + (int64_t)kh * HD, o0);
+    uint4 qw0{}, qw1{}, kw0{}, kw1{};
+    if constexpr (ROPE == 2) {
+      // a missing weight vector (one of the two norms only) reads a table row, unused
+      const void* qw = R.q_norm ? R.q_norm : R.cos_t;
+      const void* kw = R.k_norm ? R.k_norm : R.cos_t;
+      qw0 = at(qw, 0, o0);
+      qw1 = at(qw, 0, op);
+      kw0 = at(kw, 0, o0);
+      kw1 = at(kw, 0, op);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      if (g < ng) {
+        rope_apply<DT, HD>(qf[g], qx[g], qxp[g], cr, sr, ROPE == 2 && R.q_norm != nullptr, qw0,
+                           qw1, R.eps, vv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VE; ++e) qf[g][e] = 0.f;
+      }
+    }
+    float kf[VE];
+    rope_apply<DT, HD>(kf, kx, kxp, cr, sr, ROPE == 2 && R.k_norm != nullptr, kw0, kw1, R.eps,
+                       vv);
+    kn = Vec16<DT>::pack(kf);
+    // The slice that holds the new position reads its key and value from
+    // registers; the first head block of that slice also writes them into the
+    // cache for later steps. No other workgroup of the launch reads that
+    // position, so the write needs no ordering within the launch.
+    if (pcur >= lo && pcur < hi && blockIdx.y % n_hb == 0 && wave == 0 && rr == 0) {
+      *(uint4*)((char*)R.k_cache + (head_off + pcur * HD + e0) * Elem<DT>::bytes) = kn;
+      *(uint4*)((char*)R.v_cache + (head_off + pcur * HD + e0) * Elem<DT>::bytes) = vn;
+    }
+  };
+  if constexpr (ROPE) {
+    // an empty slice never runs the loop: its partial is empty whatever q is
+#pragma unroll
+    for (int g = 0; g < GB; ++g)
 #pragma unroll
       for (int e = 0; e < VE; ++e) qf[g][e] = 0.f;
+  } else {
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      if (g < ng) {
+        Vec16<DT>::load(qf[g], q, (b * heads + (int64_t)kh * G + g0 + g) * HD + vv * VE);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VE; ++e) qf[g][e] = 0.f;
+      }
     }
   }
   float m[GB], l[GB], o[GB][VE];
@@ -285,7 +443,6 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
 #pragma unroll
     for (int e = 0; e < VE; ++e) o[g][e] = 0.f;
   }
-  const int64_t head_off = (b * kv_heads + kh) * max_ctx * HD;
 
   for (int64_t p0 = lo; p0 < hi; p0 += STEP) {
     // positions past the slice are clamped to its last one (loads stay
@@ -305,6 +462,17 @@ __global__ __launch_bounds__(256) void attn_split_kernel(
     }
     // every key and value load of the step is issued before the first use
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (ROPE) {
+      if (p0 == lo) rope_prep();
+#pragma unroll
+      for (int j = 0; j < kAttnJ; ++j) {
+        // a bitwise merge of values: `c ? kn : kr[j]` on two vector lvalues
+        // selects between their addresses, which keeps both in scratch memory
+        const uint32_t c = 0u - (uint32_t)(p0 + wave * WSTEP + j * RPI + rr == pcur);
+        kr[j] = merge(c, kn, kr[j]);
+        vr[j] = merge(c, vn, vr[j]);
+      }
+    }
     float kf[kAttnJ][VE], vf[kAttnJ][VE];
 #pragma unroll
     for (int j = 0; j < kAttnJ; ++j) Vec16<DT>::unpack(kf[j], kr[j]);
@@ -495,27 +663,38 @@ struct Rope { static constexpr auto fn = rope_kv_kernel<DT>; };
 template <int DT>
 struct SiluMul { static constexpr auto fn = silu_mul_kernel<DT>; };
 
-template <int DT, int HD>
+template <int DT, int HD, int ROPE>
 int launch_attn_hd(int GB, dim3 grid, hipStream_t st, const void* q, const void* kc,
                    const void* vc, const int32_t* pos, int64_t max_ctx, int heads, int kv_heads,
                    int n_split, float sl2, float* po, float* pml, int* cnt, void* out,
-                   int64_t ldo) {
+                   int64_t ldo, const RopeIn& R) {
   switch (GB) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 1>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 2>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 4>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo); break;
-    default: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 8>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo); break;
+    case 1: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 1, ROPE>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo, R); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 2, ROPE>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo, R); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 4, ROPE>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo, R); break;
+    default: hipLaunchKernelGGL((attn_split_kernel<DT, HD, 8, ROPE>), grid, dim3(256), 0, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo, R); break;
   }
   return 0;
 }
 
+template <int DT, int ROPE>
+void launch_attn_rope(int hd, int GB, dim3 grid, hipStream_t st, const void* q, const void* kc,
+                      const void* vc, const int32_t* pos, int64_t max_ctx, int heads, int kv_heads,
+                      int n_split, float sl2, float* po, float* pml, int* cnt, void* out,
+                      int64_t ldo, const RopeIn& R) {
+  if (hd == 64) launch_attn_hd<DT, 64, ROPE>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo, R);
+  else if (hd == 128) launch_attn_hd<DT, 128, ROPE>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo, R);
+  else launch_attn_hd<DT, 256, ROPE>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo, R);
+}
+
 template <int DT>
-void launch_attn(int hd, int GB, dim3 grid, hipStream_t st, const void* q, const void* kc,
-                 const void* vc, const int32_t* pos, int64_t max_ctx, int heads, int kv_heads,
-                 int n_split, float sl2, float* po, float* pml, int* cnt, void* out, int64_t ldo) {
-  if (hd == 64) launch_attn_hd<DT, 64>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo);
-  else if (hd == 128) launch_attn_hd<DT, 128>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo);
-  else launch_attn_hd<DT, 256>(GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo);
+void launch_attn(int rope, int hd, int GB, dim3 grid, hipStream_t st, const void* q,
+                 const void* kc, const void* vc, const int32_t* pos, int64_t max_ctx, int heads,
+                 int kv_heads, int n_split, float sl2, float* po, float* pml, int* cnt, void* out,
+                 int64_t ldo, const RopeIn& R) {
+  if (rope == 2) launch_attn_rope<DT, 2>(hd, GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo, R);
+  else if (rope == 1) launch_attn_rope<DT, 1>(hd, GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo, R);
+  else launch_attn_rope<DT, 0>(hd, GB, grid, st, q, kc, vc, pos, max_ctx, heads, kv_heads, n_split, sl2, po, pml, cnt, out, ldo, R);
 }
 
 int head_block(int G) { return G >= 5 ? 8 : (G >= 3 ? 4 : G); }
@@ -618,35 +797,37 @@ extern "C" int64_t ssl_decode_attention_counter_count(int64_t rows, int32_t head
   return rows * kv_heads * ((G + head_block(G) - 1) / head_block(G));
 }
 
-extern "C" int ssl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
-                                    const int32_t* pos, void* out, int64_t ldo, int64_t rows,
-                                    int32_t heads, int32_t kv_heads, int32_t head_dim,
-                                    int64_t max_ctx, float scale, int32_t n_split,
-                                    void* workspace, int64_t workspace_bytes, int32_t* counters,
-                                    int64_t n_counters, int32_t dtype, void* stream) {
-  clear_error();
+namespace ssl {
+namespace {
+
+// Checks and launch shared by the attention entry points; R.q is set only for
+// the launch that also applies the rotary embedding and appends to the cache.
+int attention_launch(const char* what, const void* q, const void* k_cache, const void* v_cache,
+                     const int32_t* pos, void* out, int64_t ldo, int64_t rows, int32_t heads,
+                     int32_t kv_heads, int32_t head_dim, int64_t max_ctx, float scale,
+                     int32_t n_split, void* workspace, int64_t workspace_bytes, int32_t* counters,
+                     int64_t n_counters, int32_t dtype, void* stream, const RopeIn& R) {
   if (int rc = check_dtype(dtype)) return rc;
   if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
-    return fail(SSL_ERR_INVALID, "attention: %d heads over %d key/value heads", heads, kv_heads);
+    return fail(SSL_ERR_INVALID, "%s: %d heads over %d key/value heads", what, heads, kv_heads);
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail(SSL_ERR_UNSUPPORTED, "attention: head_dim %d (64, 128 or 256)", head_dim);
+    return fail(SSL_ERR_UNSUPPORTED, "%s: head_dim %d (64, 128 or 256)", what, head_dim);
   if (rows < 0 || rows > 65535 || max_ctx <= 0 || n_split <= 0 || n_split > kMaxSplits)
-    return fail(SSL_ERR_INVALID, "attention: rows %lld, max_ctx %lld, splits %d",
+    return fail(SSL_ERR_INVALID, "%s: rows %lld, max_ctx %lld, splits %d", what,
                 (long long)rows, (long long)max_ctx, n_split);
   if (rows == 0) return SSL_OK;
-  if (!q || !k_cache || !v_cache || !pos || !out || ldo < (int64_t)heads * head_dim)
-    return fail(SSL_ERR_INVALID, "attention: null pointer or output leading dimension too small");
-  if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
-    return fail(SSL_ERR_INVALID, "attention: q and the caches must be 16-byte aligned");
+  if ((!R.q && !q) || !k_cache || !v_cache || !pos || !out || ldo < (int64_t)heads * head_dim)
+    return fail(SSL_ERR_INVALID, "%s: null pointer or output leading dimension too small", what);
+  if ((!R.q && !aligned(q, 16)) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+    return fail(SSL_ERR_INVALID, "%s: q and the caches must be 16-byte aligned", what);
   const int64_t need = ssl_decode_attention_workspace_size(rows, heads, head_dim, n_split);
   if (need > 0x7fffffffLL)
-    return fail(SSL_ERR_UNSUPPORTED, "attention: partials of %lld bytes (at most 2 GiB)",
+    return fail(SSL_ERR_UNSUPPORTED, "%s: partials of %lld bytes (at most 2 GiB)", what,
                 (long long)need);
   if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
-    return fail(SSL_ERR_WORKSPACE, "attention: workspace of %lld bytes needed",
-                (long long)need);
+    return fail(SSL_ERR_WORKSPACE, "%s: workspace of %lld bytes needed", what, (long long)need);
   if (!counters || n_counters < ssl_decode_attention_counter_count(rows, heads, kv_heads))
-    return fail(SSL_ERR_WORKSPACE, "attention: %lld counters needed",
+    return fail(SSL_ERR_WORKSPACE, "%s: %lld counters needed", what,
                 (long long)ssl_decode_attention_counter_count(rows, heads, kv_heads));
   const int G = heads / kv_heads;
   const int GB = head_block(G);
@@ -655,17 +836,62 @@ extern "C" int ssl_decode_attention(const void* q, const void* k_cache, const vo
   float* pml = po + rows * heads * n_split * head_dim;
   const float sl2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
+  const int rope = !R.q ? 0 : (R.q_norm || R.k_norm) ? 2 : 1;
   dim3 grid((unsigned)n_split, (unsigned)(kv_heads * n_hb), (unsigned)rows);
   if (dtype == SSL_F32)
-    launch_attn<DT_F32>(head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
-                        kv_heads, n_split, sl2, po, pml, counters, out, ldo);
+    launch_attn<DT_F32>(rope, head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
+                        kv_heads, n_split, sl2, po, pml, counters, out, ldo, R);
   else if (dtype == SSL_BF16)
-    launch_attn<DT_BF16>(head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
-                         kv_heads, n_split, sl2, po, pml, counters, out, ldo);
+    launch_attn<DT_BF16>(rope, head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
+                         kv_heads, n_split, sl2, po, pml, counters, out, ldo, R);
   else
-    launch_attn<DT_F16>(head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
-                        kv_heads, n_split, sl2, po, pml, counters, out, ldo);
+    launch_attn<DT_F16>(rope, head_dim, GB, grid, st, q, k_cache, v_cache, pos, max_ctx, heads,
+                        kv_heads, n_split, sl2, po, pml, counters, out, ldo, R);
   return check_hip(hipGetLastError(), "attention launch");
+}
+
+}  // namespace
+}  // namespace ssl
+
+extern "C" int ssl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                                    const int32_t* pos, void* out, int64_t ldo, int64_t rows,
+                                    int32_t heads, int32_t kv_heads, int32_t head_dim,
+                                    int64_t max_ctx, float scale, int32_t n_split,
+                                    void* workspace, int64_t workspace_bytes, int32_t* counters,
+                                    int64_t n_counters, int32_t dtype, void* stream) {
+  clear_error();
+  return attention_launch("attention", q, k_cache, v_cache, pos, out, ldo, rows, heads, kv_heads,
+                          head_dim, max_ctx, scale, n_split, workspace, workspace_bytes,
+                          counters, n_counters, dtype, stream, RopeIn{});
+}
+
+extern "C" int ssl_decode_rope_attention(
+    const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+    const void* cos_table, const void* sin_table, const void* q_norm, const void* k_norm, float eps,
+    const int32_t* pos, void* k_cache, void* v_cache, void* out, int64_t ldo, int64_t rows,
+    int32_t heads, int32_t kv_heads, int32_t head_dim, int64_t max_ctx, float scale,
+    int32_t n_split, void* workspace, int64_t workspace_bytes, int32_t* counters,
+    int64_t n_counters, int32_t dtype, void* stream) {
+  clear_error();
+  if (rows > 0) {
+    if (!q || !k || !v || !cos_table || !sin_table)
+      return fail(SSL_ERR_INVALID, "rope_attention: null pointer");
+    if (heads <= 0 || kv_heads <= 0 || ldq < (int64_t)heads * head_dim ||
+        ldk < (int64_t)kv_heads * head_dim || ldv < (int64_t)kv_heads * head_dim)
+      return fail(SSL_ERR_INVALID, "rope_attention: leading dimension below the projection width");
+    const int64_t eb = dtype == SSL_F32 ? 4 : 2;
+    // every access is a 16-byte vector of one head's features
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(cos_table, 16) ||
+        !aligned(sin_table, 16) || (q_norm && !aligned(q_norm, 16)) ||
+        (k_norm && !aligned(k_norm, 16)) || (ldq * eb) % 16 || (ldk * eb) % 16 || (ldv * eb) % 16)
+      return fail(SSL_ERR_INVALID,
+                  "rope_attention: q, k, v, the tables and the norm weights must be 16-byte "
+                  "aligned, and so must their rows");
+  }
+  RopeIn R{q, ldq, k, ldk, v, ldv, cos_table, sin_table, q_norm, k_norm, eps, k_cache, v_cache};
+  return attention_launch("rope_attention", nullptr, k_cache, v_cache, pos, out, ldo, rows, heads,
+                          kv_heads, head_dim, max_ctx, scale, n_split, workspace, workspace_bytes,
+                          counters, n_counters, dtype, stream, R);
 }
 
 extern "C" int ssl_silu_mul(const void* gate, int64_t ldg, const void* up, int64_t ldu, void* out,

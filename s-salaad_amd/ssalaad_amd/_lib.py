@@ -99,6 +99,12 @@ _SIGNATURES = {
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i64,
          ctypes.c_float, _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_p],
     ),
+    "ssl_decode_rope_attention": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, ctypes.c_float, _c_p,
+         _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, ctypes.c_float,
+         _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_p],
+    ),
     "ssl_silu_mul": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p],

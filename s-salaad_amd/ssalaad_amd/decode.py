@@ -8,8 +8,8 @@ Hugging Face forward of the model `build_efficient_model` returns:
 
   per layer   add_rmsnorm (residual add fused; the embedding gather at layer 0)
               -> q,k,v in one fused SLR launch
-              -> rope + cache append -> split-context attention (its slices merged
-              by the last one to finish) -> o_proj
+              -> one launch: rope, cache append and split-context attention (its
+              slices merged by the last one to finish) -> o_proj
               -> add_rmsnorm -> gate,up in one fused SLR launch -> silu·up
               -> down_proj
   then        the final add_rmsnorm and the LM head (a plain library GEMM).
@@ -122,7 +122,6 @@ class DecodeEngine:
         self.sin = sin[0].to(dt).contiguous()
         self.h = torch.zeros(max_batch, self.hidden, dtype=dt, device=dev)
         self.xn = torch.zeros_like(self.h)
-        self.q = torch.zeros(max_batch, self.heads, hd, dtype=dt, device=dev)
         self.att = torch.zeros(max_batch, self.heads * hd, dtype=dt, device=dev)
         self.act = torch.zeros(max_batch, _round_up(self.ffn, 8), dtype=dt, device=dev)
         self.tokens = torch.zeros(max_batch, dtype=torch.int64, device=dev)
@@ -165,18 +164,15 @@ class DecodeEngine:
                 self._add_rmsnorm(B, delta, L.in_norm)
             x = self.xn[:B]
             q, k, v = L.qkv(x)
-            rc = lib.ssl_rope_kv_append(
+            # rotary embedding, cache append and attention in one launch
+            rc = lib.ssl_decode_rope_attention(
                 q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
                 self.cos.data_ptr(), self.sin.data_ptr(), _lib.ptr(L.q_norm), _lib.ptr(L.k_norm),
-                self.eps, self.pos.data_ptr(), self.q.data_ptr(), self.k_cache[li].data_ptr(),
-                self.v_cache[li].data_ptr(), B, H, KH, hd, ctx, self.dt, st)
-            self._check(rc, "ssl_rope_kv_append")
-            rc = lib.ssl_decode_attention(
-                self.q.data_ptr(), self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(),
-                self.pos.data_ptr(), self.att.data_ptr(), self.att.stride(0), B, H, KH, hd, ctx,
-                self.scale, n_split, self.attn_ws.data_ptr(), self.attn_ws.numel(),
+                self.eps, self.pos.data_ptr(), self.k_cache[li].data_ptr(),
+                self.v_cache[li].data_ptr(), self.att.data_ptr(), self.att.stride(0), B, H, KH, hd,
+                ctx, self.scale, n_split, self.attn_ws.data_ptr(), self.attn_ws.numel(),
                 self.attn_cnt.data_ptr(), self.attn_cnt.numel(), self.dt, st)
-            self._check(rc, "ssl_decode_attention")
+            self._check(rc, "ssl_decode_rope_attention")
             o = L.o(self.att[:B])
             self._add_rmsnorm(B, o, L.post_norm)
             g, u = L.gu(x)

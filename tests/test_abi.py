@@ -345,6 +345,19 @@ def test_decode_entry_points_reject_bad_arguments_before_any_launch():
     assert lib.ssl_decode_attention(*a, 128, 16, 0.1, 3, fake, need, fake, cn - 1, bf, None) == 3
     assert lib.ssl_decode_attention(fake + 2, *a[1:], 128, 16, 0.1, 3, fake, need, fake, cn, bf,
                                     None) == 1
+    # rope + attention in one launch: the attention checks, plus the projections'
+    # widths and 16-byte rows
+    r = [fake, 512, fake, 512, fake, 512, fake, fake, None, None, 1e-6, fake, fake, fake, fake,
+         512, 2, 4, 4]
+    tail = [16, 0.1, 3, fake, need, fake, cn, bf, None]
+    assert lib.ssl_decode_rope_attention(*r, 96, *tail) == 2
+    assert lib.ssl_decode_rope_attention(*r, 128, 16, 0.1, 3, fake, need - 1, fake, cn, bf,
+                                         None) == 3
+    assert lib.ssl_decode_rope_attention(*r[:1], 256, *r[2:], 128, *tail) == 1  # ldq < 4·128
+    assert lib.ssl_decode_rope_attention(*r[:1], 516, *r[2:], 128, *tail) == 1  # 1032-byte rows
+    assert lib.ssl_decode_rope_attention(*r[:2], fake + 2, *r[3:], 128, *tail) == 1  # k misaligned
+    assert lib.ssl_decode_rope_attention(*r[:6], None, *r[7:], 128, *tail) == 1  # no cos table
+    assert lib.ssl_decode_rope_attention(*r[:16], 0, *r[17:], 128, *tail) == 0  # no rows
     # silu_mul: leading dimension below n
     assert lib.ssl_silu_mul(fake, 8, fake, 16, fake, 16, 2, 16, bf, None) == 1
     assert lib.ssl_silu_mul(None, 8, None, 16, None, 16, 0, 16, bf, None) == 0

@@ -220,6 +220,71 @@ def test_rope_kv_append_matches_transformers(model_type, dtype, gpu_device):
         assert _err(got_k.float().cpu(), want_k.float().cpu()) <= tol
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("hd", [64, 128, 256])
+@pytest.mark.parametrize("heads,kvh", [(4, 4), (8, 2), (6, 2), (16, 1)])
+@pytest.mark.parametrize("model_type,n_split", [("llama", None), ("llama", 7), ("qwen3", None)])
+def test_rope_attention_equals_rope_then_attention(dt, hd, heads, kvh, model_type, n_split,
+                                                   gpu_device):
+    """The fused launch against ssl_rope_kv_append + ssl_decode_attention on the
+    same inputs: bit-identical output and caches (Qwen3's per-head norm sums
+    its squares in another order: within one rounding)."""
+    L, lib = _lib()
+    dtype = DTYPES[dt]
+    g = torch.Generator().manual_seed(hd * 7 + heads + kvh + (n_split or 0))
+    B, ctx = 4, 300
+    positions = [0, 63, 299, 128] if n_split is None else [64, 1, 150, 299]
+    dev = gpu_device
+    q = torch.randn(B, heads * hd + 64, generator=g).to(dtype).to(dev)[:, : heads * hd]
+    k = torch.randn(B, kvh * hd, generator=g).to(dtype).to(dev)
+    v = torch.randn(B, kvh * hd, generator=g).to(dtype).to(dev)
+    cos = (torch.rand(ctx, hd, generator=g) * 2 - 1).to(dtype).to(dev)
+    sin = (torch.rand(ctx, hd, generator=g) * 2 - 1).to(dtype).to(dev)
+    qn = kn = None
+    if model_type == "qwen3":
+        qn = (1 + 0.3 * torch.randn(hd, generator=g)).to(dtype).to(dev)
+        kn = (1 + 0.3 * torch.randn(hd, generator=g)).to(dtype).to(dev)
+    kc0 = torch.randn(B, kvh, ctx, hd, generator=g).to(dtype).to(dev)
+    vc0 = torch.randn(B, kvh, ctx, hd, generator=g).to(dtype).to(dev)
+    pos = torch.tensor(positions, dtype=torch.int32, device=dev)
+    code, st = L.dtype_code(dtype), L.stream_ptr(dev)
+
+    kcA, vcA = kc0.clone(), vc0.clone()
+    q_out = torch.empty(B, heads, hd, dtype=dtype, device=dev)
+    rc = lib.ssl_rope_kv_append(q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(),
+                                v.stride(0), cos.data_ptr(), sin.data_ptr(), L.ptr(qn), L.ptr(kn),
+                                1e-6, pos.data_ptr(), q_out.data_ptr(), kcA.data_ptr(),
+                                vcA.data_ptr(), B, heads, kvh, hd, ctx, code, st)
+    L.check(rc, "ssl_rope_kv_append")
+    outA = _attention(q_out, kcA, vcA, pos, heads, kvh, hd, ctx, n_split)
+
+    kcB, vcB = kc0.clone(), vc0.clone()
+    ns = n_split or lib.ssl_decode_attention_splits(B, heads, kvh, ctx)
+    ws = torch.empty(lib.ssl_decode_attention_workspace_size(B, heads, hd, ns), dtype=torch.uint8,
+                     device=dev)
+    cnt = torch.zeros(lib.ssl_decode_attention_counter_count(B, heads, kvh), dtype=torch.int32,
+                      device=dev)
+    outB = torch.full((B, heads * hd), float("nan"), dtype=dtype, device=dev)
+    rc = lib.ssl_decode_rope_attention(
+        q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
+        cos.data_ptr(), sin.data_ptr(), L.ptr(qn), L.ptr(kn), 1e-6, pos.data_ptr(),
+        kcB.data_ptr(), vcB.data_ptr(), outB.data_ptr(), outB.stride(0), B, heads, kvh, hd, ctx,
+        hd ** -0.5, ns, ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel(), code, st)
+    L.check(rc, "ssl_decode_rope_attention")
+    torch.cuda.synchronize()
+    assert (cnt == 0).all()
+    assert torch.equal(vcB, vcA)
+    if model_type == "llama":
+        assert torch.equal(kcB, kcA)
+        assert torch.equal(outB, outA)
+    else:
+        tol = {"f32": 1e-6, "bf16": 1e-2, "f16": 2e-3}[dt]
+        changed = (kcB != kc0).any(-1)
+        assert torch.equal(changed, (kcA != kc0).any(-1))  # only the new positions
+        assert _err(kcB.float().cpu(), kcA.float().cpu()) <= tol
+        assert _err(outB.float().cpu(), outA.float().cpu()) <= 2 * tol
+
+
 def test_silu_mul_matches_torch(gpu_device):
     L, lib = _lib()
     for dtype in (torch.float32, torch.bfloat16):
