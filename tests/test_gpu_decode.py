@@ -91,7 +91,7 @@ def test_attention_matches_float64_softmax(dt, hd, heads, kvh, n_split, gpu_devi
 
 def test_attention_long_context_and_every_split_count(gpu_device):
     """A 4096-position context, bf16, MHA with 128-wide heads; every split count
-    from 1 to 64 gives the same answer to fp32 rounding."""
+    from 1 to 128 gives the same answer to fp32 rounding."""
     g = torch.Generator().manual_seed(5)
     B, H, hd, ctx = 2, 4, 128, 4096
     q = torch.randn(B, H, hd, generator=g).to(torch.bfloat16)
@@ -104,7 +104,7 @@ def test_attention_long_context_and_every_split_count(gpu_device):
         L = int(pos[b]) + 1
         want[b] = dor.attention(q[b].double().numpy(), kc[b, :, :L].double().numpy(),
                                 vc[b, :, :L].double().numpy(), hd ** -0.5).reshape(-1)
-    for ns in (1, 2, 5, 16, 33, 64):
+    for ns in (1, 2, 5, 16, 33, 64, 128):
         out = _attention(qd, kd, vd, pd, H, H, hd, ctx, ns).float().cpu()
         assert _err(out, want) <= 1e-2, ns
 
@@ -223,7 +223,8 @@ def test_rope_kv_append_matches_transformers(model_type, dtype, gpu_device):
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("hd", [64, 128, 256])
 @pytest.mark.parametrize("heads,kvh", [(4, 4), (8, 2), (6, 2), (16, 1)])
-@pytest.mark.parametrize("model_type,n_split", [("llama", None), ("llama", 7), ("qwen3", None)])
+@pytest.mark.parametrize("model_type,n_split",
+                         [("llama", None), ("llama", 7), ("llama", 200), ("qwen3", None)])
 def test_rope_attention_equals_rope_then_attention(dt, hd, heads, kvh, model_type, n_split,
                                                    gpu_device):
     """The fused launch against ssl_rope_kv_append + ssl_decode_attention on the
