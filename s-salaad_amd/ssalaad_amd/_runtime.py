@@ -48,8 +48,10 @@ def plan_target_cost(total_cost: int, block_p: int, elem_bytes: int, M: int) -> 
 _BALANCE_MIN_ROW_BYTES = 128 * 1024
 _BALANCE_LATENT_MIN = 4
 # Block sizes it applies to: at p = 32 (two workgroups per compute unit,
-# shorter rows) the split rows' exchange costs more than the straggler.
-_BALANCE_P = (64,)
+# shorter rows) the split rows' exchange costs more than the straggler. At
+# p = 16 a row of small blocks streams slowly on one workgroup (a 4096-row
+# call has 256 block-rows for 512 slots), so splitting pays even unskewed.
+_BALANCE_P = (16, 64)
 # Any block size: structures whose longest row exceeds this multiple of the mean
 # and that the default target leaves whole (Zipf rows of 16×16 blocks at decode:
 # 51 → 26 µs; rows the default already splits got slower when split further,

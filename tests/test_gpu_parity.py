@@ -234,11 +234,13 @@ def test_llama7b_ffn_shape_decode(M, gpu_device):
 
 
 @pytest.mark.parametrize("M", [1, 16])
-def test_zipf_16x16_rows_split_for_decode(M, gpu_device):
-    """4096×11008 bf16, rank 128, Zipf(1.2) rows of 16×16 blocks at 10% mean density:
-    the full rows (688 blocks, 352 KB) are split across workgroups by the decode
-    balancing, and the result matches the oracle."""
-    prob = make_problem(4096, 11008, 128, 16, 0.1, torch.bfloat16, seed=11, skew=True)
+@pytest.mark.parametrize("density,skew", [(0.1, True), (0.9, False)], ids=["zipf10", "uniform90"])
+def test_zipf_16x16_rows_split_for_decode(M, density, skew, gpu_device):
+    """4096×11008 bf16, rank 128, rows of 16×16 blocks: Zipf(1.2) at 10% mean
+    density (the full rows, 688 blocks, 352 KB) or uniform at 90% (every row
+    about 620 blocks). The decode balancing splits rows across workgroups, and
+    the result matches the oracle."""
+    prob = make_problem(4096, 11008, 128, 16, density, torch.bfloat16, seed=11, skew=skew)
     mod = _module(prob, gpu_device)
     st = mod._kernel()
     assert st.plan(M).n_chunks > st.NB  # some rows were split
