@@ -250,6 +250,41 @@ def test_zipf_16x16_rows_split_for_decode(M, density, skew, gpu_device):
     assert err(y, oracle_y(prob, x)) <= 1e-2
 
 
+def test_repeated_calls_and_graph_replays_are_bit_identical(gpu_device):
+    """The handshake words are monotonic and the counters return to zero, so
+    call k + 1 must see exactly what call k saw: 100 eager calls and 100 graph
+    replays of a q/k/v-like group and of a split-row 1B down projection all
+    equal the first output bit for bit, and no wait gave up."""
+    dtype = torch.bfloat16
+    probs = _group_probs(dtype, [(256, 64, 0.5), (128, 96, 0.3), (192, 32, 0.7)], 320, 32, 77)
+    grp = ssalaad_amd.LRSLinearGroup(*[_module(pr, gpu_device) for pr in probs])
+    down = _module(make_problem(2048, 5461, 256, 32, 0.5, dtype, seed=5, pad=True), gpu_device)
+    xg = to_dev(make_x(probs[0], 16), dtype, gpu_device)
+    xd = to_dev(np.random.default_rng(3).standard_normal((16, 5461)), dtype, gpu_device)
+
+    def step():
+        return list(grp(xg)) + [down(xd)]
+
+    first = [t.clone() for t in step()]
+    for _ in range(100):
+        outs = step()
+        assert all(torch.equal(a, b) for a, b in zip(outs, first))
+    s = torch.cuda.Stream(gpu_device)
+    s.wait_stream(torch.cuda.current_stream(gpu_device))
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        outs = step()
+    for _ in range(100):
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()  # eager work between replays
+        assert all(torch.equal(a, b) for a, b in zip(outs, first))
+    assert latent_wait_status(gpu_device) == 0
+
+
 def test_llama1b_down_proj_ragged_decode(gpu_device):
     """2048×5461 bf16 (in_features not a block multiple), 32×32 blocks, rank 256."""
     prob = make_problem(2048, 5461, 256, 32, 0.5, torch.bfloat16, seed=8, pad=True)
