@@ -1,4 +1,5 @@
-"""Seeded random sweep of the fused SLR linear against the oracle.
+"""Seeded random sweeps against the oracle: the fused SLR linear, the device
+encoder (dense -> BSR, bit-exact structure and values) and the block projection.
 
 Each case draws its shape (feature counts that need not be block multiples),
 rank, block size, density, row structure (uniform or Zipf), dtype, bias and
@@ -8,6 +9,8 @@ linears that read the same x, runs them as a group and one by one, and checks:
   * the grouped outputs equal the single-linear outputs bit for bit;
   * no latent wait gave up.
 A failure names its seed; the case can be rebuilt alone with `_case(seed)`.
+The encoder and projection sweeps draw block shapes from 1 to 64 (not square
+too) and compare structure, values and keep masks exactly.
 """
 
 from __future__ import annotations
@@ -23,6 +26,7 @@ sys.path.insert(0, str(Path(__file__).resolve().parent))
 from slr_cases import TOL, err, make_problem, make_x, oracle_y, sparse_bsr_tensor, to_dev  # noqa: E402
 
 import ssalaad_amd  # noqa: E402
+from oracle import slr_oracle as orc  # noqa: E402
 from ssalaad_amd import LRSLinear  # noqa: E402
 from ssalaad_amd.ls_linear import latent_wait_status  # noqa: E402
 
@@ -76,3 +80,85 @@ def test_random_slr_linears_match_the_oracle(seed, gpu_device):
         assert err(y, oracle_y(pr, x)) <= TOL[c["dtype"]], c
         assert torch.equal(y, yg), c
     assert latent_wait_status(gpu_device) == 0, c
+
+
+# ------------------------------------------------ encoder and projection --
+
+_BITS = {torch.float32: torch.int32, torch.bfloat16: torch.int16, torch.float16: torch.int16}
+_SIZES = (1, 2, 4, 8, 16, 32, 64)
+
+
+def _random_dense(rng, rb, cb, p, q, dtype) -> torch.Tensor:
+    """Blocks drawn as zero, dense, one non-zero, -0.0, NaN, inf or subnormal."""
+    S = np.zeros((rb * p, cb * q), np.float32)
+    kinds = rng.choice(7, size=(rb, cb), p=[0.35, 0.3, 0.1, 0.05, 0.07, 0.06, 0.07])
+    tiny = {torch.float32: 1e-40, torch.bfloat16: 1e-40, torch.float16: 1e-7}[dtype]
+    for r in range(rb):
+        for c in range(cb):
+            blk = S[r * p:(r + 1) * p, c * q:(c + 1) * q]
+            i, j = rng.integers(p), rng.integers(q)
+            k = kinds[r, c]
+            if k == 1:
+                blk[:] = rng.standard_normal((p, q))
+            elif k == 2:
+                blk[i, j] = rng.standard_normal()
+            elif k == 3:
+                blk[:] = -0.0
+            elif k == 4:
+                blk[i, j] = np.nan
+            elif k == 5:
+                blk[i, j] = np.inf * rng.choice([-1, 1])
+            elif k == 6:
+                blk[i, j] = tiny
+    return torch.from_numpy(S).to(dtype)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_encoder_structure_is_bit_exact(seed, gpu_device):
+    rng = np.random.default_rng(5000 + seed)
+    p, q = int(rng.choice(_SIZES)), int(rng.choice(_SIZES))
+    rb, cb = int(rng.integers(1, 13)), int(rng.integers(1, 13))
+    dtype = DTYPES[int(rng.integers(3))]
+    S = _random_dense(rng, rb, cb, p, q, dtype)
+    crow, col, vals = orc.dense_to_bsr(S.float().numpy(), p, q)
+    crow32, col32, _, act = orc.module_buffers(crow, col, vals)
+    k_crow, k_col, k_vt, k_act = ssalaad_amd.encode_for_kernels(S.to(gpu_device), p, q)
+    bsr = ssalaad_amd.dense_to_bsr(S.to(gpu_device), p, q)
+    torch.cuda.synchronize()
+    case = (seed, p, q, rb, cb, dtype)
+    assert np.array_equal(k_crow.cpu().numpy(), crow32), case
+    assert np.array_equal(k_col.cpu().numpy(), col32), case
+    assert np.array_equal(k_act.cpu().numpy(), act), case
+    assert np.array_equal(bsr.crow_indices().cpu().numpy(), crow), case
+    assert np.array_equal(bsr.col_indices().cpu().numpy(), col), case
+    bits = _BITS[dtype]
+    S_bits = S.view(bits).numpy()
+    rows = np.repeat(np.arange(rb), np.diff(crow))
+    want = (np.stack([S_bits[r * p:(r + 1) * p, c * q:(c + 1) * q] for r, c in zip(rows, col)])
+            if len(col) else np.zeros((0, p, q), S_bits.dtype))
+    assert np.array_equal(bsr.values().cpu().view(bits).numpy(), want), case
+    assert np.array_equal(k_vt.cpu().view(bits).numpy(), want.transpose(0, 2, 1)), case
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_block_projection_matches_the_oracle(seed, gpu_device):
+    """Block norms separated by construction (each block scaled by a distinct
+    power of 1.05), so the top-k selection is the same in fp32 and float64."""
+    rng = np.random.default_rng(7000 + seed)
+    p, q = int(rng.choice(_SIZES)), int(rng.choice(_SIZES))
+    rb, cb = int(rng.integers(1, 17)), int(rng.integers(1, 17))
+    dtype = (torch.float32, torch.bfloat16)[int(rng.integers(2))]
+    M = rng.standard_normal((rb * p, cb * q))
+    M /= np.sqrt((M.reshape(rb, p, cb, q) ** 2).sum(axis=(1, 3)))[:, None, :, None].repeat(
+        p, 1).repeat(q, 3).reshape(rb * p, cb * q)
+    scale = 1.05 ** rng.permutation(rb * cb).reshape(rb, cb)
+    M *= np.repeat(np.repeat(scale, p, axis=0), q, axis=1)
+    Md = torch.from_numpy(M.astype(np.float32)).to(dtype)
+    total = rb * cb
+    n_keep = int(rng.integers(-2, total + 3))
+    out, keep, _ = ssalaad_amd.block_topk(Md.to(gpu_device), n_keep, p, q)
+    torch.cuda.synchronize()
+    want, want_keep = orc.project_blocks(Md.float().numpy(), n_keep, p, q)
+    case = (seed, p, q, rb, cb, dtype, n_keep)
+    assert np.array_equal(keep.cpu().numpy(), want_keep), case
+    assert np.array_equal(out.cpu().numpy(), want), case
