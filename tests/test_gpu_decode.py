@@ -386,6 +386,34 @@ def test_engine_steps_match_the_oracle(model_type, kv_heads, head_dim, heads, dt
     assert worst <= TOL_MODEL[dtype]
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_engine_configs_match_the_oracle(seed, gpu_device):
+    """Random decoder shapes through DecodeEngine, every step against the oracle:
+    LLaMA or Qwen3, 2–16 query heads (the configs need hidden 256 to be a
+    multiple) over any divisor as key/value heads, head_dim 64/128/256, fp32 or
+    bf16, 1–4 sequences, 4–20 steps."""
+    from ssalaad_amd import DecodeEngine
+
+    rng = np.random.default_rng(900 + seed)
+    model_type = ("llama", "qwen3")[int(rng.integers(2))]
+    heads = int(rng.choice([2, 4, 8, 16]))
+    kvh = int(rng.choice([d for d in range(1, heads + 1) if heads % d == 0]))
+    hd = int(rng.choice([64, 128, 256]))
+    dtype = (torch.float32, torch.bfloat16)[int(rng.integers(2))]
+    B, T = int(rng.integers(1, 5)), int(rng.integers(4, 21))
+    model, dense = _slr_pair(model_type, dtype, kvh, gpu_device, seed=seed, head_dim=hd,
+                             heads=heads)
+    P = dor.params_from_hf(dense)
+    ids = torch.randint(0, 384, (B, T), generator=torch.Generator().manual_seed(seed))
+    eng = DecodeEngine(model, max_batch=B, max_context=T)
+    cache = dor.KVCache.empty(len(P.layers), B, P.kv_heads, T, P.head_dim)
+    case = (seed, model_type, heads, kvh, hd, dtype, B, T)
+    for t in range(T):
+        got = eng.step(ids[:, t], [t] * B).float().cpu().numpy()
+        want = dor.decode_step(P, cache, ids[:, t].numpy(), [t] * B)
+        assert _err(got, want) <= TOL_MODEL[dtype], (case, t)
+
+
 def test_engine_ragged_positions_and_batch_sizes(gpu_device):
     """Sequences at different positions in one step, and steps of 1 to 3 rows
     sharing the same cache slots (one graph per batch size)."""
