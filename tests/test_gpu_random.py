@@ -10,7 +10,8 @@ linears that read the same x, runs them as a group and one by one, and checks:
   * no latent wait gave up.
 A failure names its seed; the case can be rebuilt alone with `_case(seed)`.
 The encoder and projection sweeps draw block shapes from 1 to 64 (not square
-too) and compare structure, values and keep masks exactly.
+too) and compare structure, values and keep masks exactly; the in-place op
+sweep checks active block-rows against the oracle and every other row's bits.
 """
 
 from __future__ import annotations
@@ -162,3 +163,42 @@ def test_random_block_projection_matches_the_oracle(seed, gpu_device):
     case = (seed, p, q, rb, cb, dtype, n_keep)
     assert np.array_equal(keep.cpu().numpy(), want_keep), case
     assert np.array_equal(out.cpu().numpy(), want), case
+
+
+# ------------------------------------------------------- in-place op --
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_inplace_op_matches_the_oracle(seed, gpu_device):
+    """torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_ on random shapes,
+    block sizes, dtypes and token counts (decode and prefill kernels), with
+    `active_rows` a random subset of the block-rows that hold blocks: active
+    rows match the oracle, every other row keeps its bits."""
+    import ssalaad_amd.addmm_inplace  # noqa: F401  (registers the op)
+
+    rng = np.random.default_rng(9000 + seed)
+    p = int(rng.choice([16, 32, 64]))
+    dtype = DTYPES[int(rng.integers(3))]
+    NB, NBK = int(rng.integers(1, 13)), int(rng.integers(1, 13))
+    M = int(rng.choice([1, 5, 16, 64, 65, 130, 300]))
+    prob = make_problem(NB * p, NBK * p, 4, p, float(rng.choice([0.2, 0.5, 0.9])), dtype,
+                        seed=seed, skew=bool(rng.integers(2)))
+    crow32, col32, vt, act_all = orc.module_buffers(prob["crow"], prob["col"], prob["vals"])
+    act = np.sort(rng.permutation(act_all)[: int(rng.integers(0, len(act_all) + 1))]).astype(np.int32)
+    x = make_x(prob, M, seed=seed)
+    out0 = torch.from_numpy(rng.standard_normal((M, NB * p))).to(dtype).double().numpy()
+    want = orc.bsr_addmm_inplace(out0, x, crow32, col32, vt, act)
+    dev = gpu_device
+    out = to_dev(out0, dtype, dev)
+    torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_(
+        out, to_dev(x, dtype, dev), torch.from_numpy(crow32).to(dev),
+        torch.from_numpy(col32).to(dev), to_dev(vt, dtype, dev), torch.from_numpy(act).to(dev))
+    torch.cuda.synchronize()
+    case = (seed, p, dtype, NB, NBK, M, len(act))
+    got = out.double().cpu().numpy()
+    cols = np.zeros(NB * p, bool)
+    for by in act:
+        cols[by * p:(by + 1) * p] = True
+    if cols.any():
+        assert err(out[:, torch.from_numpy(cols).to(dev)], want[:, cols]) <= TOL[dtype], case
+    assert np.array_equal(got[:, ~cols], out0[:, ~cols]), case
