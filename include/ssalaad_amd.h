@@ -101,6 +101,14 @@ int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, in
  * call, all its linears' rows together). */
 int64_t ssl_prefill_min_rows(void);
 int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p);
+/* 1 if a fused SLR call (ssl_slr_forward, ssl_slr_forward_group) with block
+ * storage, M token rows and n_rows block-rows over all its linears takes the
+ * prefill kernels (and so needs their plans), 0 if it streams. At least
+ * ssl_prefill_min_rows() rows and 16-bit activations, except 32×32 or smaller
+ * blocks up to 512 rows and calls of fewer than 100 block-rows at the minimum
+ * row count. The in-place op (ssl_bsr_addmm_inplace) keeps the plain
+ * threshold. */
+int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_t dtype);
 
 /* -------------------------------------------------------------------------
  * In-place BSR addmm:  out[:, rows of active block-rows] += x · Sᵀ

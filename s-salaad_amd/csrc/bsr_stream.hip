@@ -831,6 +831,20 @@ extern "C" {
 
 int64_t ssl_prefill_min_rows(void) { return kPrefillMinM; }
 
+// Which kernels a fused call with block storage takes. The prefill kernels
+// from kPrefillMinM token rows with 16-bit activations, except where the
+// streaming kernel (one weight pass per 64-row token tile, the re-reads served
+// by the caches) measured faster on MI355X: blocks of 32×32 or less up to 512
+// rows (LLaMA-1B gate 5461×2048 at 128 / 256 / 512 rows: 34.2 / 41.8 / 65.5 µs
+// prefill, 24.5 / 35.6 / 55.1 streaming), and calls of fewer than 100
+// block-rows up to 128 rows (4096×4096 with 64×64 blocks: 40.7 -> 31.9 µs).
+int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_t dtype) {
+  if (dtype == SSL_F32 || M < kPrefillMinM) return 0;
+  if (block_p <= 32 && M <= 512) return 0;
+  if (M <= kPrefillMinM && n_rows < 100) return 0;
+  return 1;
+}
+
 int64_t ssl_nm24_block_bytes(void) { return kNmBlockBytes; }
 
 int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p) {
@@ -1010,7 +1024,9 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
   }
   if (n_stream == 0) return SSL_OK;
 
-  if (M >= kPrefillMinM && dtype != SSL_F32 && s_format == SSL_S_BSR) {
+  int64_t call_rows = 0;
+  for (int i = 0; i < n_members; ++i) call_rows += members[i].NB;
+  if (s_format == SSL_S_BSR && ssl_slr_takes_prefill(M, call_rows, block_p, dtype)) {
     // Many token rows: the latent GEMM (K split, then combined), then the row
     // GEMM over groups of block-rows. (2:4 blocks stay on the row-streaming
     // kernel at every M.)

@@ -125,10 +125,14 @@ class _KernelState:
             self._plans[key] = pl
         return pl
 
-    def takes_prefill(self, M: int) -> bool:
-        lib = _lib.load()
-        return (M >= lib.ssl_prefill_min_rows() and self.dtype_code != _lib.SSL_F32
-                and self.s_format == 0)
+    def takes_prefill(self, M: int, n_rows: int | None = None) -> bool:
+        """Whether a fused call of M token rows over `n_rows` block-rows (this
+        linear's alone by default) runs the prefill kernels; the library decides
+        (ssl_slr_takes_prefill), so host and device agree."""
+        if self.s_format != 0:
+            return False
+        rows = self.NB if n_rows is None else n_rows
+        return bool(_lib.load().ssl_slr_takes_prefill(M, rows, self.p, self.dtype_code))
 
     def prefill_plan(self, G: int) -> _runtime.DevicePrefillPlan:
         """The prefill row kernel's plan with G block-rows per workgroup."""
@@ -176,7 +180,7 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
         members = (_lib.SlrMember * len(states))()
         ws_off = cnt_off = 0
         G = 0
-        if st0.takes_prefill(M):
+        if st0.takes_prefill(M, sum(st.NB for st in states)):
             G = int(lib.ssl_prefill_group(M, sum(st.NB for st in states), st0.p))
         for i, (st, pl, y) in enumerate(zip(states, plans, ys)):
             xch = pl.exchange(lib.ssl_slr_exchange_size(M, st.r_pad, st.m_pad, st.dtype_code))

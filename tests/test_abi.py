@@ -248,6 +248,12 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     big = dict(M=4096, counters=P, n_counters=1 << 20)
     assert op(**big) == _lib.SSL_ERR_INVALID and b"prefill plan" in lib.ssl_last_error()
     assert lib.ssl_prefill_min_rows() == 128
+    # fused calls: streaming for small blocks up to 512 rows and for calls of
+    # fewer than 100 block-rows at 128 rows; fp32 always streams
+    tp = lambda M, rows, p, dt=_lib.SSL_BF16: lib.ssl_slr_takes_prefill(M, rows, p, dt)
+    assert tp(127, 500, 64) == 0 and tp(128, 172, 64) == 1 and tp(128, 64, 64) == 0
+    assert tp(129, 64, 64) == 1 and tp(512, 500, 32) == 0 and tp(513, 500, 32) == 1
+    assert tp(300, 500, 16) == 0 and tp(2048, 64, 32) == 1 and tp(4096, 500, 64, _lib.SSL_F32) == 0
     assert lib.ssl_prefill_group(4096, 172, 64) in (1, 4)
 
     # ssl_slr_forward with fake, aligned device pointers (every case below is

@@ -302,7 +302,7 @@ def test_llama1b_down_proj_ragged_decode(gpu_device):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("p", [16, 32, 64])
-@pytest.mark.parametrize("M", [128, 300, 1100])
+@pytest.mark.parametrize("M", [128, 300, 600, 1100])
 def test_prefill_module_matches_oracle(dtype, p, M, gpu_device):
     prob = make_problem(4 * 64, 6 * 64, 128, p, 0.5, dtype, seed=p + M, skew=(p == 32))
     mod = _module(prob, gpu_device)
@@ -315,7 +315,7 @@ def test_prefill_module_matches_oracle(dtype, p, M, gpu_device):
     assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("M", [128, 257])
+@pytest.mark.parametrize("M", [128, 257, 600])
 def test_prefill_ragged_features_no_bias(M, gpu_device):
     prob = make_problem(100, 200, 24, 32, 0.5, torch.bfloat16, seed=M, bias=False, pad=True)
     mod = _module(prob, gpu_device, bias=False)
@@ -340,7 +340,7 @@ def test_prefill_op_matches_oracle_and_keeps_inactive_rows(dtype, p, M, gpu_devi
 def test_prefill_group(gpu_device):
     probs = _group_probs(torch.bfloat16, [(256, 64, 0.5), (128, 96, 0.3), (192, 128, 0.7)], 320, 32, 9)
     grp = ssalaad_amd.LRSLinearGroup(*[_module(pr, gpu_device) for pr in probs])
-    x = make_x(probs[0], 333)
+    x = make_x(probs[0], 700)  # above 512 rows: 32×32 blocks take the prefill kernels
     ys = grp(to_dev(x, torch.bfloat16, gpu_device))
     torch.cuda.synchronize()
     for y, pr in zip(ys, probs):
