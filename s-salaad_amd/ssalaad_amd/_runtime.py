@@ -84,6 +84,25 @@ def balanced_target(costs: np.ndarray, cost_bytes: int, slots: int, lat_tiles: i
     return 0 if lo >= costs.max() else lo
 
 
+def partial_split_plan(crow_host: np.ndarray, block_q: int, lr_units: int,
+                       n_split: int) -> tuple[np.ndarray, int, int]:
+    """A plan whose last `n_split` block-rows are split in two and the others
+    kept whole, for structures of equal rows (2:4 storage) where the free
+    workgroup slots fit only some extra chunks. Each split row's finaliser
+    still follows its other chunk, as the kernel requires."""
+    crow_host = np.ascontiguousarray(crow_host, dtype=np.int32)
+    NB = crow_host.shape[0] - 1
+    costs = np.diff(crow_host).astype(np.int64) * block_q + lr_units * 32
+    half = int(costs.max()) // 2 + 1
+    ta, na, sa = build_plan(crow_host, np.arange(0, NB - n_split, dtype=np.int32), block_q,
+                            lr_units, 0)
+    tb, nb, sb = build_plan(crow_host, np.arange(NB - n_split, NB, dtype=np.int32), block_q,
+                            lr_units, half)
+    if sa:
+        raise RuntimeError("an unsplit plan holds partial-sum slots")
+    return np.concatenate([ta[:na], tb[:nb]]).astype(np.int32), na + nb, sb
+
+
 def build_plan(
     crow_host: np.ndarray,
     rows_host: np.ndarray | None,

@@ -128,6 +128,29 @@ def test_plan_finaliser_takes_the_low_rank_units():
     assert n1 == 3 and s1 == 0 and all(int(r[6]) == 1 for r in table1)
 
 
+def test_partial_split_plan_covers_every_unit_once():
+    """Equal rows (2:4 storage), the last 4 of 10 split in two: every block and
+    low-rank unit once, each split row's finaliser after its other chunk, two
+    partial slots per split row."""
+    crow = np.arange(0, 11 * 12, 12, dtype=np.int32)
+    table, n, slots = _runtime.partial_split_plan(crow, 32, 8, 4)
+    assert n == 6 + 8 and slots == 8
+    seen_blocks, per_row = [], {}
+    for idx, (row, bb, be, lb, le, seq, nseq, slot) in enumerate(table[:n]):
+        seen_blocks += list(range(bb, be))
+        per_row.setdefault(int(row), []).append((seq, nseq, lb, le, slot, idx))
+    assert sorted(seen_blocks) == list(range(crow[-1]))
+    for row, parts in per_row.items():
+        parts.sort()
+        assert len(parts) == (2 if row >= 6 else 1)
+        assert sum(le - lb for _, _, lb, le, _, _ in parts) == 8    # every unit once
+        fin = parts[-1]
+        assert (fin[2], fin[3]) == (0, 8) and fin[5] == max(p[5] for p in parts)
+    # a row's chunks share a slot base; chunk `seq` uses base + seq
+    split_slots = sorted(p[4] + p[0] for r, ps in per_row.items() if r >= 6 for p in ps)
+    assert split_slots == list(range(8))
+
+
 def test_plan_with_row_list_skips_unlisted_and_empty_rows():
     crow = [0, 3, 3, 7, 9]
     table, n, _ = _plan(crow, rows=[0, 1, 3], q=16)

@@ -696,10 +696,16 @@ def test_nm24_group_and_mixing_rules(gpu_device):
 
 
 def test_nm24_llama7b_ffn_shape_decode(gpu_device):
-    """11008×4096 bf16, rank 256, 2:4 S: one fused launch per call."""
+    """11008×4096 bf16, rank 256, 2:4 S: one fused launch per call, with some of
+    the 344 equal rows split in two to fill the free workgroup slots."""
     mod, (A, B, S, b) = _nm_module(11008, 4096, 256, torch.bfloat16, gpu_device, seed=31, bias=False)
+    st = mod._kernel()
+    assert st.NB < st.plan(4).n_chunks < 2 * st.NB  # a partial split
     x = np.random.default_rng(2).standard_normal((4, 4096))
     x = torch.from_numpy(x).to(torch.bfloat16).double().numpy()
     y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    y2 = mod(to_dev(x, torch.bfloat16, gpu_device))
     torch.cuda.synchronize()
     assert err(y, orc.slr_linear(x, A, B, S, b)) <= 1e-2
+    assert torch.equal(y, y2)
+    assert latent_wait_status(gpu_device) == 0
