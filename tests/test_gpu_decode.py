@@ -308,9 +308,10 @@ def test_silu_mul_matches_torch(gpu_device):
 # ---------------------------------------------------------------- engine --
 
 
-def _slr_pair(model_type, dtype, kv_heads, dev, seed=0, head_dim=64, heads=4, layers=2):
+def _slr_pair(model_type, dtype, kv_heads, dev, seed=0, head_dim=64, heads=4, layers=2, nm=False):
     """An SLR-compressed model on the GPU and its dense float64 twin on the CPU
-    (every projection W = A·B + S from the same dtype-valued factors)."""
+    (every projection W = A·B + S from the same dtype-valued factors). With
+    `nm`, S is 2:4-sparse along the input features (two of every four kept)."""
     from ssalaad_amd import LRSLinear
     from ssalaad_amd.bundle import build_model_from_config
 
@@ -350,6 +351,15 @@ def _slr_pair(model_type, dtype, kv_heads, dev, seed=0, head_dim=64, heads=4, la
             A = (0.1 * torch.randn(n, r, generator=g)).to(dtype)
             B = (0.1 * torch.randn(r, m, generator=g)).to(dtype)
             S = torch.sparse_bsr_tensor(crow, slots % NBK, vals, size=(n, m))
+            if nm:
+                keep = torch.rand(n, m // 4, 4, generator=g).argsort(-1).argsort(-1) < 2
+                Sd = ((0.05 * torch.randn(n, m, generator=g)) * keep.reshape(n, m)).to(dtype)
+                with torch.no_grad():
+                    dense.get_submodule(f"model.layers.{li}.{part}.{proj}").weight.copy_(
+                        A.double() @ B.double() + Sd.double())
+                setattr(parent, proj, LRSLinear(A.to(dev), B.to(dev), Sd.to(dev), in_features=m,
+                                                out_features=n, nm_n=2, nm_m=4))
+                continue
             with torch.no_grad():
                 dense.get_submodule(f"model.layers.{li}.{part}.{proj}").weight.copy_(
                     A.double() @ B.double() + S.to_dense().double())
@@ -412,6 +422,26 @@ def test_random_engine_configs_match_the_oracle(seed, gpu_device):
         got = eng.step(ids[:, t], [t] * B).float().cpu().numpy()
         want = dor.decode_step(P, cache, ids[:, t].numpy(), [t] * B)
         assert _err(got, want) <= TOL_MODEL[dtype], (case, t)
+
+
+@pytest.mark.parametrize("model_type,kv_heads", [("llama", 2), ("qwen3", 4)])
+def test_engine_with_2to4_projections_matches_the_oracle(model_type, kv_heads, gpu_device):
+    """Every projection with 2:4 S (bf16): the grouped q/k/v and gate/up launches
+    and the decode step on packed 2:4 blocks, against the oracle at every step."""
+    from ssalaad_amd import DecodeEngine
+
+    model, dense = _slr_pair(model_type, torch.bfloat16, kv_heads, gpu_device, seed=11, nm=True)
+    assert all(getattr(m, "kind", "") == "nm" for n_, m in model.named_modules()
+               if n_.endswith(("q_proj", "down_proj")))
+    P = dor.params_from_hf(dense)
+    B, T = 2, 10
+    ids = torch.randint(0, 384, (B, T), generator=torch.Generator().manual_seed(12))
+    eng = DecodeEngine(model, max_batch=B, max_context=T)
+    cache = dor.KVCache.empty(len(P.layers), B, P.kv_heads, T, P.head_dim)
+    for t in range(T):
+        got = eng.step(ids[:, t], [t] * B).float().cpu().numpy()
+        want = dor.decode_step(P, cache, ids[:, t].numpy(), [t] * B)
+        assert _err(got, want) <= TOL_MODEL[torch.bfloat16], t
 
 
 def test_engine_ragged_positions_and_batch_sizes(gpu_device):
