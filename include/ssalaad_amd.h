@@ -53,6 +53,25 @@ typedef enum { SSL_F32 = 0, SSL_BF16 = 1, SSL_F16 = 2 } ssl_dtype;
 int ssl_version(void);
 const char* ssl_last_error(void);
 
+/* Test hooks (host-side process-wide settings read at each launch; no
+ * reference counterpart). They exist so that tests can reach paths that a
+ * healthy device never takes, with every kernel still ending normally:
+ *   SSL_DEBUG_PREFILL_TILE      0: the library picks the prefill row tile;
+ *                               1: always the narrow tile; 2: always the wide
+ *                               tile (ssl_prefill_group follows it).
+ *   SSL_DEBUG_WAIT_POLLS        polls before a bounded wait gives up (0: the
+ *                               default of several seconds).
+ *   SSL_DEBUG_WAIT_UNREACHABLE  nonzero: every wait of the fused kernel targets
+ *                               a count no launch reaches, so each gives up
+ *                               after its polls and reports it.
+ * Not for concurrent use with calls on other threads. */
+typedef enum {
+  SSL_DEBUG_PREFILL_TILE = 0,
+  SSL_DEBUG_WAIT_POLLS = 1,
+  SSL_DEBUG_WAIT_UNREACHABLE = 2
+} ssl_debug_knob;
+int ssl_debug_set(int32_t knob, int64_t value);
+
 /* -------------------------------------------------------------------------
  * Work plans (host side, integer only).
  *
@@ -72,12 +91,17 @@ const char* ssl_last_error(void);
  *   {row, blk_begin, blk_end, lr_begin, lr_end, seq, nseq, slot}
  * (blk_* index the BSR block arrays; lr_* count 32-rank units of the row).
  * Returns the chunk count in *n_chunks and the partial-sum slot count in *n_slots.
+ * The structure is checked first (SSL_ERR_INVALID otherwise): crow starts at 0
+ * and never decreases, each of the crow[NB] blocks has col in [0, NBK) (col may
+ * be NULL only without blocks), and `rows` is strictly ascending in [0, NB).
+ * The kernels index with these numbers unchecked, so callers build a plan from
+ * the same crow/col they pass to the device.
  * ------------------------------------------------------------------------- */
 #define SSL_PLAN_STRIDE 8
-int ssl_plan_build(const int32_t* crow_host, int64_t NB, const int32_t* rows_host,
-                   int64_t n_rows, int32_t block_q, int32_t lr_units, int64_t target_cost,
-                   int32_t* table_out, int64_t table_capacity, int64_t* n_chunks,
-                   int64_t* n_slots);
+int ssl_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB, int64_t NBK,
+                   const int32_t* rows_host, int64_t n_rows, int32_t block_q, int32_t lr_units,
+                   int64_t target_cost, int32_t* table_out, int64_t table_capacity,
+                   int64_t* n_chunks, int64_t* n_slots);
 
 /* Prefill plan (host side, integer only): the row kernels used for calls with
  * many token rows give one workgroup `group` block-rows at once (group · p =
@@ -90,9 +114,10 @@ int ssl_plan_build(const int32_t* crow_host, int64_t NB, const int32_t* rows_hos
  *           in ascending column order; bit g of mask is set iff blk_g (the BSR
  *           block index of slot g's row at that column) is valid (else −1).
  * A repeated column within one row gets its own entry. Call once with NULL
- * outputs for the counts. group ∈ [1, 16]. */
+ * outputs for the counts. group ∈ [1, 16]. The structure is checked as for
+ * ssl_plan_build. */
 int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB,
-                           const int32_t* rows_host, int64_t n_rows, int32_t group,
+                           int64_t NBK, const int32_t* rows_host, int64_t n_rows, int32_t group,
                            int32_t* groups_out, int64_t groups_capacity, int32_t* entries_out,
                            int64_t entries_capacity, int64_t* n_groups, int64_t* n_entries);
 /* Calls with at least this many token rows and 16-bit activations run the
@@ -212,6 +237,11 @@ typedef struct ssl_slr_member {
    * layout), or SSL_S_NM24, 2:4-sparse 32×32 blocks in the layout below
    * (replaces the semi-structured S of ssalaad/efficient/ls_linear.py:167-219) */
   int32_t s_format;
+  /* where a workgroup that gave up waiting records it (uint64, set to 1;
+   * device memory, never cleared by the library). NULL: the first uint64 of
+   * `exchange`. Sharing one word between every call lets a host check all of
+   * them at once. */
+  uint64_t* status;
 } ssl_slr_member;
 
 typedef enum { SSL_S_BSR = 0, SSL_S_NM24 = 1 } ssl_s_format;

@@ -53,7 +53,8 @@ constexpr int kSW = 8;            // waves per streaming workgroup
 constexpr int kST = kSW * kWave;  // threads per streaming workgroup
 
 // Polls of a counter before a wait gives up and flags an error in the status
-// word (seconds; a healthy launch waits microseconds).
+// word (seconds; a healthy launch waits microseconds). ssl_debug_set can lower
+// it for tests of the give-up path.
 constexpr int kSpinLimit = 1 << 22;
 
 // ---------------------------------------------------------------------------
@@ -138,14 +139,17 @@ __device__ __forceinline__ void st_u64(u64* p, u64 v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Spin (one lane) until *flag >= target; bounded, sets *status on timeout.
+// Spin (one lane) until *flag >= target; bounded (`polls`), sets *status on
+// timeout. The caller goes on either way, so every workgroup of the launch
+// still ends; a wait that gave up leaves its tile unreliable, which the status
+// word reports.
 template <typename T>
-__device__ __forceinline__ void wait_at_least(const T* flag, T target, u64* status) {
+__device__ __forceinline__ void wait_at_least(const T* flag, T target, u64* status, int polls) {
   int n = 0;
   while (__hip_atomic_load(const_cast<T*>(flag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
          target) {
     __builtin_amdgcn_s_sleep(2);
-    if (++n > kSpinLimit) {
+    if (++n > polls) {
       st_u64(status, 1);
       break;
     }
@@ -287,6 +291,12 @@ struct SlrArgs {
   u64* sync;
   int lr_wgs;       // workgroups that consume the latent (per token tile)
   int lat_weight;   // kLatentUnits / n_kc
+  // Bounded waits: where a timeout is reported (the caller's status word, or
+  // sync[0]), polls before giving up, and an offset added to every wait's
+  // target (nonzero only when a test forces the give-up path).
+  u64* status;
+  int wait_polls;
+  int wait_bias;
 };
 
 __device__ __forceinline__ u64* tile_sync(const SlrArgs& a, int mg) {
@@ -535,7 +545,7 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
     if (used_t) {
       if (threadIdx.x == 0) {
         const u64 target = (ticket / (u64)a.lr_wgs + 1) * (u64)a.n_rt;
-        wait_at_least<u64>(tile_sync(a, mg), target, a.sync);
+        wait_at_least<u64>(tile_sync(a, mg), target + (u64)a.wait_bias, a.status, a.wait_polls);
       }
       __syncthreads();
       const auto tr = dev_rsrc(a.t);
@@ -576,7 +586,7 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
     const bool finaliser_mode = (MODE == MODE_FUSED) && a.n_rt > 0;
     if (finaliser_mode && used_t) {
       // the row's finaliser: wait for the other nseq - 1 chunks
-      if (lane == 0) wait_at_least<int>(counter, nseq - 1, a.sync);
+      if (lane == 0) wait_at_least<int>(counter, nseq - 1 + a.wait_bias, a.status, a.wait_polls);
     } else {
       store_partial<MT, W>(acc, part_base + (int64_t)seq * TSZ, Mrem, lane);
       wait_mem();
@@ -585,6 +595,7 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
       old = __builtin_amdgcn_readfirstlane(old);
       if (finaliser_mode || old != nseq - 1) return;
     }
+    // This chunk combines the row (the finaliser, or the op's last arrival).
     // sum the partials in chunk order, this chunk's tile at its own position
     f32x4 tot[MT][W];
 #pragma unroll
@@ -605,7 +616,11 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int s = 0; s < W; ++s) acc[mt][s] = tot[mt][s];
-    if (lane == 0) st_int(counter, 0);
+    // Return the row counter to zero by subtracting the arrivals this launch
+    // makes (nseq - 1 other chunks for the finaliser; all nseq in the op)
+    // rather than storing 0: if a finaliser's wait gave up, the chunks still to
+    // arrive bring the counter back to exactly zero by the launch's end.
+    if (lane == 0) rmw_add(counter, finaliser_mode ? -(nseq - 1) : -nseq);
   }
 
   // epilogue: lane (c, g) owns W adjacent output columns of rows 16·mt + 4g + e
@@ -746,20 +761,6 @@ int latent_split_max(int64_t M, int64_t m_pad) {
   if (n > by_tokens) n = by_tokens;
   if (n > 8) n = 8;
   return n < 1 ? 1 : (int)n;
-}
-
-// Compute units of the current device (cached per device).
-int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-      v = 256;
-    cache[dev] = v;
-  }
-  return cache[dev];
 }
 
 bool supported_block(int p, int q) { return p == q && (p == 16 || p == 32 || p == 64); }
@@ -1092,6 +1093,7 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
                      "slr prefill launch");
   }
 
+  const DebugKnobs& knobs = debug_knobs();
   // One K split for the whole launch: latent and row workgroups of every
   // member resident at once.
   int n_kc = 1, ku_chunk = 1;
@@ -1117,6 +1119,10 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
     a.ku_chunk = ku_chunk;
     a.n_lat_wgs = (int)((int64_t)L[i].n_rt * n_kc * L[i].MG);
     a.sync = (u64*)mb.exchange; a.lr_wgs = (int)mb.lr_wgs; a.lat_weight = kLatentUnits / n_kc;
+    a.status = mb.status ? (u64*)mb.status : (u64*)mb.exchange;
+    a.wait_polls = knobs.wait_polls > 0 ? (int)knobs.wait_polls : kSpinLimit;
+    // out of reach of any launch: tickets and counters advance far less per launch
+    a.wait_bias = knobs.wait_unreachable ? (1 << 30) : 0;
   }
   g.lat_off[n_members] = (int)lat;
   g.str_off[n_members] = (int)str;

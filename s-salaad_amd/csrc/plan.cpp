@@ -22,11 +22,14 @@
 #include <string>
 #include <vector>
 
-#include "abi_internal.h"
+#include "abi_common.h"
 
 namespace ssl {
 
 static thread_local std::string g_last_error;
+static DebugKnobs g_knobs{};
+
+DebugKnobs& debug_knobs() { return g_knobs; }
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -38,12 +41,35 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-int check_hip(hipError_t e, const char* what) {
-  if (e == hipSuccess) return SSL_OK;
-  return fail(SSL_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
-}
-
 void clear_error() { g_last_error.clear(); }
+
+// The structure checks every planner makes before it reads an index: crow
+// starts at 0 and never decreases, every block's column lies in [0, NBK), and
+// the listed rows are strictly ascending block-rows. The kernels index x, the
+// block values and the plan with these numbers, so nothing the host has not
+// checked reaches the device.
+static int check_structure(const int32_t* crow, const int32_t* col, int64_t NB, int64_t NBK,
+                           const int32_t* rows, int64_t n_rows) {
+  if (crow[0] != 0) return fail(SSL_ERR_INVALID, "crow[0] must be 0");
+  for (int64_t b = 0; b < NB; ++b)
+    if (crow[b + 1] < crow[b]) return fail(SSL_ERR_INVALID, "crow must be non-decreasing");
+  const int64_t nnz = crow[NB];
+  if (nnz > 0 && !col) return fail(SSL_ERR_INVALID, "col indices needed for %lld blocks", (long long)nnz);
+  if (nnz > 0 && NBK <= 0) return fail(SSL_ERR_INVALID, "NBK must be positive when blocks exist");
+  for (int64_t k = 0; k < nnz; ++k)
+    if (col[k] < 0 || col[k] >= NBK)
+      return fail(SSL_ERR_INVALID, "col[%lld] = %d outside [0, %lld)", (long long)k, col[k],
+                  (long long)NBK);
+  const int64_t nr = rows ? n_rows : NB;
+  int64_t prev = -1;
+  for (int64_t i = 0; i < nr; ++i) {
+    const int64_t by = rows ? rows[i] : i;
+    if (by < 0 || by >= NB) return fail(SSL_ERR_INVALID, "row %lld out of range", (long long)by);
+    if (by <= prev) return fail(SSL_ERR_INVALID, "rows must be strictly ascending");
+    prev = by;
+  }
+  return SSL_OK;
+}
 
 }  // namespace ssl
 
@@ -55,23 +81,35 @@ int ssl_version(void) { return 3; }
 
 const char* ssl_last_error(void) { return g_last_error.c_str(); }
 
-int ssl_plan_build(const int32_t* crow_host, int64_t NB, const int32_t* rows_host, int64_t n_rows,
-                   int32_t block_q, int32_t lr_units, int64_t target_cost, int32_t* table_out,
-                   int64_t table_capacity, int64_t* n_chunks, int64_t* n_slots) {
+int ssl_debug_set(int32_t knob, int64_t value) {
   clear_error();
-  if (!crow_host || !n_chunks || !n_slots || NB < 0 || block_q <= 0 || lr_units < 0)
-    return fail(SSL_ERR_INVALID, "invalid plan arguments");
-  if (crow_host[0] != 0) return fail(SSL_ERR_INVALID, "crow[0] must be 0");
-  for (int64_t b = 0; b < NB; ++b)
-    if (crow_host[b + 1] < crow_host[b]) return fail(SSL_ERR_INVALID, "crow must be non-decreasing");
-  const int64_t nr = rows_host ? n_rows : NB;
-  int64_t prev = -1;
-  for (int64_t i = 0; i < nr; ++i) {
-    const int64_t by = rows_host ? rows_host[i] : i;
-    if (by < 0 || by >= NB) return fail(SSL_ERR_INVALID, "row %lld out of range", (long long)by);
-    if (by <= prev) return fail(SSL_ERR_INVALID, "rows must be strictly ascending");
-    prev = by;
+  DebugKnobs& k = debug_knobs();
+  switch (knob) {
+    case SSL_DEBUG_PREFILL_TILE:
+      if (value < 0 || value > 2) return fail(SSL_ERR_INVALID, "prefill tile override must be 0, 1 or 2");
+      k.prefill_group = value;
+      return SSL_OK;
+    case SSL_DEBUG_WAIT_POLLS:
+      if (value < 0 || value > (1LL << 30)) return fail(SSL_ERR_INVALID, "wait polls out of range");
+      k.wait_polls = value;
+      return SSL_OK;
+    case SSL_DEBUG_WAIT_UNREACHABLE:
+      k.wait_unreachable = value != 0;
+      return SSL_OK;
   }
+  return fail(SSL_ERR_INVALID, "unknown debug knob %d", knob);
+}
+
+int ssl_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB, int64_t NBK,
+                   const int32_t* rows_host, int64_t n_rows, int32_t block_q, int32_t lr_units,
+                   int64_t target_cost, int32_t* table_out, int64_t table_capacity,
+                   int64_t* n_chunks, int64_t* n_slots) {
+  clear_error();
+  if (!crow_host || !n_chunks || !n_slots || NB < 0 || block_q <= 0 || lr_units < 0 ||
+      (rows_host && n_rows < 0) || (table_out && table_capacity < 0))
+    return fail(SSL_ERR_INVALID, "invalid plan arguments");
+  if (int rc = check_structure(crow_host, col_host, NB, NBK, rows_host, n_rows)) return rc;
+  const int64_t nr = rows_host ? n_rows : NB;
   // Two passes: non-finaliser chunks first, then finalisers (pass 1 only when
   // rows have low-rank units).
   int64_t chunks = 0, slots = 0;
@@ -144,24 +182,16 @@ int ssl_plan_build(const int32_t* crow_host, int64_t NB, const int32_t* rows_hos
 }
 
 int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB,
-                           const int32_t* rows_host, int64_t n_rows, int32_t group,
+                           int64_t NBK, const int32_t* rows_host, int64_t n_rows, int32_t group,
                            int32_t* groups_out, int64_t groups_capacity, int32_t* entries_out,
                            int64_t entries_capacity, int64_t* n_groups, int64_t* n_entries) {
   clear_error();
-  if (!crow_host || !n_groups || !n_entries || NB < 0 || group < 1 || group > 16)
+  if (!crow_host || !n_groups || !n_entries || NB < 0 || group < 1 || group > 16 ||
+      (rows_host && n_rows < 0) || (groups_out && groups_capacity < 0) ||
+      (entries_out && entries_capacity < 0))
     return fail(SSL_ERR_INVALID, "invalid prefill plan arguments");
-  if (crow_host[0] != 0) return fail(SSL_ERR_INVALID, "crow[0] must be 0");
-  for (int64_t b = 0; b < NB; ++b)
-    if (crow_host[b + 1] < crow_host[b]) return fail(SSL_ERR_INVALID, "crow must be non-decreasing");
-  if (crow_host[NB] > 0 && !col_host) return fail(SSL_ERR_INVALID, "col indices needed");
+  if (int rc = check_structure(crow_host, col_host, NB, NBK, rows_host, n_rows)) return rc;
   const int64_t nr = rows_host ? n_rows : NB;
-  int64_t prev = -1;
-  for (int64_t i = 0; i < nr; ++i) {
-    const int64_t by = rows_host ? rows_host[i] : i;
-    if (by < 0 || by >= NB) return fail(SSL_ERR_INVALID, "row %lld out of range", (long long)by);
-    if (by <= prev) return fail(SSL_ERR_INVALID, "rows must be strictly ascending");
-    prev = by;
-  }
   const int stride = 2 + group;
   int64_t ng = 0, ne = 0;
   std::vector<std::array<int32_t, 3>> items;  // (col, slot, block)

@@ -482,6 +482,9 @@ int prefill_row_tile(int group) { return group > 1 ? 128 : 64; }
 int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus) {
   // the wide configuration when it still gives every CU a workgroup
   const int gmax = 256 / block_p;
+  const int64_t forced = debug_knobs().prefill_group;  // test hook
+  if (forced == 1) return 1;
+  if (forced == 2) return gmax;
   const int64_t items = ((M + 127) / 128) * ((n_rows + gmax - 1) / gmax);
   return items >= n_cus ? gmax : 1;
 }

@@ -25,6 +25,11 @@ SSL_ERR_CAPACITY = 5
 SSL_F32, SSL_BF16, SSL_F16 = 0, 1, 2
 PLAN_STRIDE = 8
 
+# ssl_debug_set knobs (test hooks)
+DEBUG_PREFILL_TILE = 0
+DEBUG_WAIT_POLLS = 1
+DEBUG_WAIT_UNREACHABLE = 2
+
 _DTYPE_CODE = {torch.float32: SSL_F32, torch.bfloat16: SSL_BF16, torch.float16: SSL_F16}
 
 _c_i64 = ctypes.c_int64
@@ -35,9 +40,11 @@ _c_p = ctypes.c_void_p
 _SIGNATURES = {
     "ssl_version": (ctypes.c_int, []),
     "ssl_last_error": (ctypes.c_char_p, []),
+    "ssl_debug_set": (ctypes.c_int, [_c_i32, _c_i64]),
     "ssl_plan_build": (
         ctypes.c_int,
-        [_c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_i64, _c_p, _c_i64, _c_p, _c_p],
+        [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_i64, _c_p, _c_i64, _c_p,
+         _c_p],
     ),
     "ssl_bsr_addmm_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i32, _c_i64]),
     "ssl_bsr_addmm_counter_count": (_c_i64, [_c_i64, _c_i64]),
@@ -49,7 +56,8 @@ _SIGNATURES = {
     ),
     "ssl_prefill_plan_build": (
         ctypes.c_int,
-        [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p],
+        [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_p,
+         _c_p],
     ),
     "ssl_prefill_min_rows": (_c_i64, []),
     "ssl_nm24_block_bytes": (_c_i64, []),
@@ -124,7 +132,7 @@ class SlrMember(ctypes.Structure):
         ("counters", _c_p), ("n_counters", _c_i64), ("exchange", _c_p),
         ("exchange_bytes", _c_i64), ("workspace", _c_p), ("workspace_bytes", _c_i64),
         ("pf_groups", _c_p), ("pf_entries", _c_p), ("pf_n_groups", _c_i64), ("pf_group", _c_i32),
-        ("nnz", _c_i64), ("values_pq", _c_p), ("s_format", _c_i32),
+        ("nnz", _c_i64), ("values_pq", _c_p), ("s_format", _c_i32), ("status", _c_p),
     ]
 
 

@@ -10,6 +10,15 @@ that stream and grown when a call needs more:
     rows; no initialisation needed.
 A plan that feeds the fused kernel also owns its exchange area (see
 DevicePlan.exchange): it advances monotonically and is never shared.
+
+A buffer that is outgrown is retired, never freed: a HIP graph captured
+earlier holds its raw address and replays into it, so every retired pool
+buffer and exchange area lives as long as the process (the pools grow
+geometrically, so the retired ones total less than the live one).
+
+Every fused call reports a bounded wait that gave up in one status word per
+device (`status_word`), which the host reads when it chooses to (a read
+synchronises; the decode engine mirrors it into host memory once per step).
 """
 
 from __future__ import annotations
@@ -84,8 +93,8 @@ def balanced_target(costs: np.ndarray, cost_bytes: int, slots: int, lat_tiles: i
     return 0 if lo >= costs.max() else lo
 
 
-def partial_split_plan(crow_host: np.ndarray, block_q: int, lr_units: int,
-                       n_split: int) -> tuple[np.ndarray, int, int]:
+def partial_split_plan(crow_host: np.ndarray, col_host: np.ndarray, NBK: int, block_q: int,
+                       lr_units: int, n_split: int) -> tuple[np.ndarray, int, int]:
     """A plan whose last `n_split` block-rows are split in two and the others
     kept whole, for structures of equal rows (2:4 storage) where the free
     workgroup slots fit only some extra chunks. Each split row's finaliser
@@ -94,10 +103,10 @@ def partial_split_plan(crow_host: np.ndarray, block_q: int, lr_units: int,
     NB = crow_host.shape[0] - 1
     costs = np.diff(crow_host).astype(np.int64) * block_q + lr_units * 32
     half = int(costs.max()) // 2 + 1
-    ta, na, sa = build_plan(crow_host, np.arange(0, NB - n_split, dtype=np.int32), block_q,
-                            lr_units, 0)
-    tb, nb, sb = build_plan(crow_host, np.arange(NB - n_split, NB, dtype=np.int32), block_q,
-                            lr_units, half)
+    ta, na, sa = build_plan(crow_host, col_host, NBK, np.arange(0, NB - n_split, dtype=np.int32),
+                            block_q, lr_units, 0)
+    tb, nb, sb = build_plan(crow_host, col_host, NBK, np.arange(NB - n_split, NB, dtype=np.int32),
+                            block_q, lr_units, half)
     if sa:
         raise RuntimeError("an unsplit plan holds partial-sum slots")
     return np.concatenate([ta[:na], tb[:nb]]).astype(np.int32), na + nb, sb
@@ -105,14 +114,19 @@ def partial_split_plan(crow_host: np.ndarray, block_q: int, lr_units: int,
 
 def build_plan(
     crow_host: np.ndarray,
+    col_host: np.ndarray,
+    NBK: int,
     rows_host: np.ndarray | None,
     block_q: int,
     lr_units: int,
     target_cost: int,
 ) -> tuple[np.ndarray, int, int]:
-    """Return (table [n_chunks, 8] int32, n_chunks, n_slots) for a BSR structure."""
+    """Return (table [n_chunks, 8] int32, n_chunks, n_slots) for a BSR structure
+    with NBK block-columns; the library checks crow, col and rows first."""
     lib = _lib.load()
     crow_host = np.ascontiguousarray(crow_host, dtype=np.int32)
+    col_host = np.ascontiguousarray(col_host, dtype=np.int32)
+    col_p = col_host.ctypes.data if col_host.size else None
     NB = crow_host.shape[0] - 1
     rows_p = None
     n_rows = 0
@@ -123,13 +137,13 @@ def build_plan(
     n_chunks = ctypes.c_int64()
     n_slots = ctypes.c_int64()
     rc = lib.ssl_plan_build(
-        crow_host.ctypes.data, NB, rows_p, n_rows, block_q, lr_units, target_cost,
+        crow_host.ctypes.data, col_p, NB, NBK, rows_p, n_rows, block_q, lr_units, target_cost,
         None, 0, ctypes.byref(n_chunks), ctypes.byref(n_slots),
     )
     _lib.check(rc, "ssl_plan_build")
     table = np.zeros((max(n_chunks.value, 1), _lib.PLAN_STRIDE), dtype=np.int32)
     rc = lib.ssl_plan_build(
-        crow_host.ctypes.data, NB, rows_p, n_rows, block_q, lr_units, target_cost,
+        crow_host.ctypes.data, col_p, NB, NBK, rows_p, n_rows, block_q, lr_units, target_cost,
         table.ctypes.data, table.shape[0], ctypes.byref(n_chunks), ctypes.byref(n_slots),
     )
     _lib.check(rc, "ssl_plan_build")
@@ -137,7 +151,8 @@ def build_plan(
 
 
 def build_prefill_plan(
-    crow_host: np.ndarray, col_host: np.ndarray, rows_host: np.ndarray | None, group: int
+    crow_host: np.ndarray, col_host: np.ndarray, NBK: int, rows_host: np.ndarray | None,
+    group: int
 ) -> tuple[np.ndarray, np.ndarray, int]:
     """Group table [n_groups, 2 + group] and union-column entries [n_entries, 2 + group]
     (int32) for the prefill row kernel (ssl_prefill_plan_build)."""
@@ -150,8 +165,8 @@ def build_prefill_plan(
         rows_host = np.ascontiguousarray(rows_host, dtype=np.int32)
         rows_p, n_rows = rows_host.ctypes.data, rows_host.shape[0]
     ng, ne = ctypes.c_int64(), ctypes.c_int64()
-    args = (crow_host.ctypes.data, col_host.ctypes.data if col_host.size else None, NB, rows_p,
-            n_rows, group)
+    args = (crow_host.ctypes.data, col_host.ctypes.data if col_host.size else None, NB, NBK,
+            rows_p, n_rows, group)
     rc = lib.ssl_prefill_plan_build(*args, None, 0, None, 0, ctypes.byref(ng), ctypes.byref(ne))
     _lib.check(rc, "ssl_prefill_plan_build")
     groups = np.zeros((max(ng.value, 1), 2 + group), dtype=np.int32)
@@ -181,7 +196,8 @@ _PLANS: "weakref.WeakSet[DevicePlan]" = weakref.WeakSet()
 class DevicePlan:
     """A plan uploaded to one device."""
 
-    __slots__ = ("table", "n_chunks", "n_slots", "lr_wgs", "_exchange", "__weakref__")
+    __slots__ = ("table", "n_chunks", "n_slots", "lr_wgs", "_exchange", "_retired",
+                 "__weakref__")
 
     def __init__(self, table: np.ndarray, n_chunks: int, n_slots: int, device: torch.device):
         t = torch.from_numpy(table if n_chunks else np.zeros((1, _lib.PLAN_STRIDE), np.int32))
@@ -192,6 +208,7 @@ class DevicePlan:
         lr = (table[:n_chunks, 4] - table[:n_chunks, 3]) if n_chunks else np.zeros(0)
         self.lr_wgs = int((lr > 0).sum())
         self._exchange: torch.Tensor | None = None
+        self._retired: list[torch.Tensor] = []
         _PLANS.add(self)
 
     def exchange(self, nbytes: int) -> torch.Tensor:
@@ -200,9 +217,12 @@ class DevicePlan:
         It holds the plan's latent-handshake counters, which the kernels advance
         monotonically and never reset, so it belongs to this plan alone and
         calls with one plan are ordered on one stream. Growing replaces it with
-        zeros, which is a valid state for the next call.
+        zeros, which is a valid state for the next call; the outgrown area is
+        kept alive with the plan, since a graph captured earlier replays into it.
         """
         if self._exchange is None or self._exchange.numel() < nbytes:
+            if self._exchange is not None:
+                self._retired.append(self._exchange)
             self._exchange = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8,
                                          device=self.table.device)
         return self._exchange
@@ -219,6 +239,9 @@ class DevicePlan:
 
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 _COUNTERS: dict[tuple[int, int], torch.Tensor] = {}
+# Outgrown pool buffers: kept for the life of the process (see the module doc).
+_RETIRED: list[torch.Tensor] = []
+_STATUS: dict[int, torch.Tensor] = {}
 
 
 def _key(device: torch.device) -> tuple[int, int]:
@@ -232,6 +255,7 @@ def _grown(pool, key, n, dtype, device, minimum):
         size = max(int(n), minimum)
         if buf is not None:
             size = max(size, 2 * buf.numel())
+            _RETIRED.append(buf)
         buf = torch.zeros(size, dtype=dtype, device=device)
         pool[key] = buf
     return buf
@@ -245,3 +269,24 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 def counters(device: torch.device, count: int) -> torch.Tensor:
     """int32 counters (zero at rest) of at least `count` for the current stream."""
     return _grown(_COUNTERS, _key(device), count, torch.int32, device, 1 << 14)
+
+
+def status_word(device: torch.device) -> torch.Tensor:
+    """The device's wait-status word (int64 on the device): every fused call on
+    it sets the word to 1 when one of its workgroups gave up waiting (its output
+    is then unreliable). Zero until then; only `reset_status` clears it."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    w = _STATUS.get(idx)
+    if w is None:
+        w = torch.zeros(1, dtype=torch.int64, device=torch.device("cuda", idx))
+        _STATUS[idx] = w
+    return w
+
+
+def read_status(device: torch.device) -> int:
+    """The device's wait status (synchronises with the device)."""
+    return int(status_word(device).item())
+
+
+def reset_status(device: torch.device) -> None:
+    status_word(device).zero_()

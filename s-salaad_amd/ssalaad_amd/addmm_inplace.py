@@ -91,7 +91,9 @@ def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_by
         crow_h, act_h = _validated_host_structure(crow, col, active_rows, values.shape[0], NB_K)
         total = int(crow_h[-1]) * block_q
         target = _runtime.plan_target_cost(total, block_p, elem_bytes, M)
-        table, n_chunks, n_slots = _runtime.build_plan(crow_h, act_h, block_q, 0, target)
+        col_h = col.detach().to("cpu").numpy().astype(np.int32)
+        table, n_chunks, n_slots = _runtime.build_plan(crow_h, col_h, NB_K, act_h, block_q, 0,
+                                                       target)
         plan = _runtime.DevicePlan(table, n_chunks, n_slots, crow.device)
         sp.plans[target_key] = plan
     pf = None
@@ -104,7 +106,7 @@ def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_by
             crow_h, _ = _validated_host_structure(crow, col, active_rows, values.shape[0], NB_K)
             col_h = col.detach().to("cpu").numpy().astype(np.int32)
             rows_h = plan.table.cpu().numpy()[: plan.n_chunks, 0].astype(np.int32)
-            groups, entries, ng = _runtime.build_prefill_plan(crow_h, col_h, rows_h, G)
+            groups, entries, ng = _runtime.build_prefill_plan(crow_h, col_h, NB_K, rows_h, G)
             pf = _runtime.DevicePrefillPlan(groups, entries, ng, G, crow.device)
             sp.plans[("pf", G)] = pf
     return plan, pf

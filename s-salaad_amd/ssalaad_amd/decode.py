@@ -30,7 +30,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from . import _lib
+from . import _lib, _runtime
 from .ls_linear import LRSLinearGroup, _LRSLinearBase
 
 
@@ -132,6 +132,12 @@ class DecodeEngine:
         nc = self.lib.ssl_decode_attention_counter_count(max_batch, self.heads, self.kv_heads)
         self.attn_cnt = torch.zeros(max(nc, 1), dtype=torch.int32, device=dev)
         self.use_graphs = use_graphs
+        # Host mirror of the device's wait-status word, refreshed (one 8-byte
+        # copy, no synchronisation) after every step and checked before the
+        # next, so a fused launch whose wait gave up is reported one step late
+        # at no per-step cost.
+        self._status_dev = _runtime.status_word(dev)
+        self._status_host = torch.zeros(1, dtype=torch.int64, pin_memory=True)
         self._stream = torch.cuda.Stream(dev)
         self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
 
@@ -198,6 +204,11 @@ class DecodeEngine:
         pos_h = positions.to("cpu")
         if int(pos_h.min()) < 0 or int(pos_h.max()) >= self.max_context:
             raise ValueError(f"positions must lie in [0, {self.max_context})")
+        if int(self._status_host[0]) != 0:
+            raise RuntimeError(
+                "a fused SLR launch of an earlier step gave up waiting for another "
+                "workgroup (bounded wait); its logits are unreliable. Clear the device's "
+                "status word (ssalaad_amd._runtime.reset_status) before stepping again.")
         cur = torch.cuda.current_stream(self.device)
         s = self._stream
         s.wait_stream(cur)
@@ -215,6 +226,7 @@ class DecodeEngine:
                 with torch.cuda.graph(g, stream=s):
                     gout = self._body(B)
                 self._graphs[B] = (g, gout)
+            self._status_host.copy_(self._status_dev, non_blocking=True)
         cur.wait_stream(s)
         return out
 

@@ -46,10 +46,14 @@ class _KernelState:
 
     Buffers the kernels can read as they are (aligned, padded dims already
     multiples) are used in place; otherwise a zero-padded copy is made once.
+    The state records which buffers (and which in-place version of each) it was
+    built from; the module rebuilds it when any of them changes, e.g. after
+    load_state_dict or an in-place copy into A.
     """
 
     def __init__(self, mod: "_LRSLinearBase", device: torch.device):
         dtype = mod.A.dtype
+        self.key = mod._weights_key()
         self.device = device
         self.dtype_code = _lib.dtype_code(dtype)
         self.elem = torch.empty((), dtype=dtype).element_size()
@@ -89,6 +93,7 @@ class _KernelState:
         self.crow_h = crow_h
         self.lr_units = self.r_pad // 32
         self.block_q = p
+        self.NBK = -(-m // p)
         self._plans: dict[int, _runtime.DevicePlan] = {}
         self._pf_plans: dict[int, _runtime.DevicePrefillPlan] = {}
         self._values_pq: torch.Tensor | None = None
@@ -130,10 +135,10 @@ class _KernelState:
                     n_split = free
             if n_split:
                 table, n_chunks, n_slots = _runtime.partial_split_plan(
-                    self.crow_h, self.block_q, self.lr_units, n_split)
+                    self.crow_h, self.col_h, self.NBK, self.block_q, self.lr_units, n_split)
             else:
                 table, n_chunks, n_slots = _runtime.build_plan(
-                    self.crow_h, None, self.block_q, self.lr_units, target
+                    self.crow_h, self.col_h, self.NBK, None, self.block_q, self.lr_units, target
                 )
             pl = _runtime.DevicePlan(table, n_chunks, n_slots, self.device)
             self._plans[key] = pl
@@ -152,7 +157,8 @@ class _KernelState:
         """The prefill row kernel's plan with G block-rows per workgroup."""
         pp = self._pf_plans.get(G)
         if pp is None:
-            groups, entries, ng = _runtime.build_prefill_plan(self.crow_h, self.col_h, None, G)
+            groups, entries, ng = _runtime.build_prefill_plan(self.crow_h, self.col_h, self.NBK,
+                                                              None, G)
             pp = _runtime.DevicePrefillPlan(groups, entries, ng, G, self.device)
             self._pf_plans[G] = pp
         if self._values_pq is None and self.nblk_total > 0:
@@ -191,6 +197,7 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
         cnt_need = [lib.ssl_slr_counter_count(M, st.NB) for st in states]
         ws = _runtime.workspace(x.device, sum(ws_need))
         cnt = _runtime.counters(x.device, sum(cnt_need))
+        status = _runtime.status_word(x.device).data_ptr()
         members = (_lib.SlrMember * len(states))()
         ws_off = cnt_off = 0
         G = 0
@@ -211,6 +218,7 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
             mb.workspace_bytes = ws_need[i]
             mb.nnz = st.nblk_total
             mb.s_format = st.s_format
+            mb.status = status
             if G:
                 pp = st.prefill_plan(G)
                 mb.pf_groups, mb.pf_entries = pp.groups.data_ptr(), pp.entries.data_ptr()
@@ -232,12 +240,14 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
 
 
 def latent_wait_status(device: torch.device) -> int:
-    """1 if a fused call of any live plan on `device` had a workgroup give up
-    waiting (its output tile is then unreliable), else 0. Synchronises.
+    """1 if a fused call on `device` had a workgroup give up waiting (its output
+    tile is then unreliable), else 0: the device's status word, which every call
+    of this package reports into, and the plans' own words (used by callers of
+    the C ABI that pass no status word). Synchronises.
     """
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    return max([pl.wait_status() for pl in list(_runtime._PLANS)
-                if pl.table.device.index == idx] + [0])
+    words = [pl.wait_status() for pl in list(_runtime._PLANS) if pl.table.device.index == idx]
+    return max(words + [_runtime.read_status(torch.device("cuda", idx))])
 
 
 class _LRSLinearBase(nn.Module):
@@ -271,9 +281,16 @@ class _LRSLinearBase(nn.Module):
         self._state = None  # weights moved or cast: rebuild the kernel view lazily
         return super()._apply(fn, recurse=recurse)
 
+    def _weights_key(self) -> tuple:
+        """Identity and in-place version of every buffer the kernel view is
+        built from (the reference module reads its buffers on every forward;
+        this lets an update after the first forward take effect too)."""
+        return tuple((name, t.data_ptr(), t._version) for name, t in self._buffers.items()
+                     if t is not None)
+
     def _kernel(self) -> _KernelState:
         st = self._state
-        if st is None or st.device != self.A.device:
+        if st is None or st.device != self.A.device or st.key != self._weights_key():
             if self.A.device.type != "cuda":
                 raise ValueError("The HIP SLR kernels need the module on a ROCm GPU device.")
             st = _KernelState(self, self.A.device)

@@ -74,3 +74,17 @@ def to_dev(a, dtype, device):
 
 def err(y_gpu: torch.Tensor, y_ref: np.ndarray) -> float:
     return orc.max_abs_normalised_error(y_gpu.double().cpu().numpy(), y_ref)
+
+
+def make_module(prob, dev, bias=True):
+    """The package's LRSLinear for a problem (BSR S on the device)."""
+    from ssalaad_amd import LRSLinear
+
+    dt = prob["dtype"]
+    S = sparse_bsr_tensor(prob, dev)
+    return LRSLinear(
+        to_dev(prob["A"], dt, dev), to_dev(prob["B"], dt, dev), S,
+        in_features=prob["m"], out_features=prob["n"],
+        bias=to_dev(prob["bias"], dt, dev) if (bias and prob["bias"] is not None) else None,
+        block_p=prob["p"], block_q=prob["p"],
+    )

@@ -52,8 +52,14 @@ def test_version():
 # ------------------------------------------------------------------ plans --
 
 
-def _plan(crow, rows=None, q=64, lr=0, target=0):
-    table, n, s = _runtime.build_plan(np.asarray(crow, np.int32),
+def _cols(crow):
+    """Valid column indices for a structure whose columns do not matter."""
+    return np.zeros(max(int(np.asarray(crow)[-1]), 0), np.int32)
+
+
+def _plan(crow, rows=None, q=64, lr=0, target=0, col=None, NBK=1):
+    col = _cols(crow) if col is None else np.asarray(col, np.int32)
+    table, n, s = _runtime.build_plan(np.asarray(crow, np.int32), col, NBK,
                                       None if rows is None else np.asarray(rows, np.int32),
                                       q, lr, target)
     return table, n, s
@@ -133,7 +139,7 @@ def test_partial_split_plan_covers_every_unit_once():
     low-rank unit once, each split row's finaliser after its other chunk, two
     partial slots per split row."""
     crow = np.arange(0, 11 * 12, 12, dtype=np.int32)
-    table, n, slots = _runtime.partial_split_plan(crow, 32, 8, 4)
+    table, n, slots = _runtime.partial_split_plan(crow, _cols(crow), 1, 32, 8, 4)
     assert n == 6 + 8 and slots == 8
     seen_blocks, per_row = [], {}
     for idx, (row, bb, be, lb, le, seq, nseq, slot) in enumerate(table[:n]):
@@ -168,8 +174,26 @@ def test_plan_rejects_bad_structures():
         _plan([0, 1, 2], rows=[2])
 
 
-def _pf_plan(crow, col, rows=None, group=4):
-    return _runtime.build_prefill_plan(np.asarray(crow, np.int32), np.asarray(col, np.int32),
+@pytest.mark.parametrize("bad", [-1, 4, 1 << 30])
+def test_plans_reject_column_indices_out_of_range(bad):
+    """The library checks every block's column before any kernel can index x
+    or the values with it (both planners)."""
+    crow = [0, 2, 3]
+    with pytest.raises(ValueError, match="col"):
+        _plan(crow, col=[0, bad, 1], NBK=4)
+    with pytest.raises(ValueError, match="col"):
+        _pf_plan(crow, [0, bad, 1], NBK=4)
+    _plan(crow, col=[0, 3, 1], NBK=4)        # in range: accepted
+    _pf_plan(crow, [0, 3, 1], NBK=4)
+    with pytest.raises(ValueError, match="col"):
+        _runtime.build_plan(np.asarray(crow, np.int32), np.zeros(0, np.int32), 4, None, 16, 0, 0)
+
+
+def _pf_plan(crow, col, rows=None, group=4, NBK=None):
+    col = np.asarray(col, np.int32)
+    if NBK is None:
+        NBK = int(col.max()) + 1 if col.size else 1
+    return _runtime.build_prefill_plan(np.asarray(crow, np.int32), col, NBK,
                                        None if rows is None else np.asarray(rows, np.int32), group)
 
 
@@ -419,7 +443,7 @@ def test_balanced_target_splits_only_the_longest_rows():
     assert _runtime.balanced_target(np.full(400, 2304), 128, 256, 16) == 0  # no free slots
     # the plan built with it covers every unit once
     crow = np.concatenate([[0], np.cumsum(blocks)]).astype(np.int32)
-    table, n_chunks, _ = _runtime.build_plan(crow, None, 64, 8, t)
+    table, n_chunks, _ = _runtime.build_plan(crow, _cols(crow), 1, None, 64, 8, t)
     assert n_chunks == chunks
     for row in range(172):
         mine = table[table[:, 0] == row]

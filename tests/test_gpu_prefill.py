@@ -1,0 +1,148 @@
+"""The prefill row kernels (calls with many token rows, 16-bit activations),
+every tile configuration checked against the oracle on every output row.
+
+The library picks one of two row tiles per call (ssl_prefill_group): "wide"
+(128 token rows × 256/p block-rows per workgroup) when that still gives every
+compute unit a workgroup, else "narrow" (64 × 1). Small shapes pick narrow, so
+the wide tiles run only at full size; the test hook SSL_DEBUG_PREFILL_TILE
+forces either tile on any shape, for the fused linear (PF_FUSED), the grouped
+launch and the in-place op (PF_OP). The full-size cases at the end are the
+shapes where the library picks the wide tile by itself, checked on all rows.
+The forward these compute is ssalaad/efficient/ls_linear.py:124-137 (the op:
+ssalaad/tilelang_sparse/addmm_inplace.py:41-82).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import slr_oracle as orc
+from slr_cases import TOL, err, make_module, make_problem, make_x, oracle_y, to_dev
+
+import ssalaad_amd
+from ssalaad_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+WIDE, NARROW = 2, 1
+DT16 = [torch.bfloat16, torch.float16]
+
+
+@pytest.fixture
+def tile():
+    """Force a prefill row tile for the test's calls; restores the default."""
+    lib = _lib.load()
+
+    def force(mode):
+        _lib.check(lib.ssl_debug_set(_lib.DEBUG_PREFILL_TILE, mode), "ssl_debug_set")
+
+    yield force
+    force(0)
+
+
+def _group_of(M, rows, p):
+    return int(_lib.load().ssl_prefill_group(M, rows, p))
+
+
+@pytest.mark.parametrize("dtype", DT16, ids=["bf16", "f16"])
+@pytest.mark.parametrize("p", [16, 32, 64])
+@pytest.mark.parametrize("mode", [WIDE, NARROW], ids=["wide", "narrow"])
+@pytest.mark.parametrize("M", [600, 1030])
+def test_forced_tiles_fused_linear(dtype, p, mode, M, tile, gpu_device):
+    """Ragged block-row count (not a multiple of the wide group), skewed rows,
+    ragged token count: every row of every tile against the oracle."""
+    tile(mode)
+    prob = make_problem(13 * p + 64, 9 * 64, 128, p, 0.5, dtype, seed=p + M + mode, skew=True)
+    rows = prob["NB"]
+    assert _group_of(M, rows, p) == (256 // p if mode == WIDE else 1)
+    mod = make_module(prob, gpu_device)
+    x = make_x(prob, M)
+    y = mod(to_dev(x, dtype, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", DT16, ids=["bf16", "f16"])
+@pytest.mark.parametrize("p", [16, 32, 64])
+@pytest.mark.parametrize("mode", [WIDE, NARROW], ids=["wide", "narrow"])
+def test_forced_tiles_grouped_launch(dtype, p, mode, tile, gpu_device):
+    tile(mode)
+    specs = [(5 * p, 64, 0.5), (3 * p, 96, 0.3), (7 * p, 128, 0.7)]
+    probs = [make_problem(n, 8 * p, r, p, d, dtype, seed=31 + i, skew=(i == 1))
+             for i, (n, r, d) in enumerate(specs)]
+    grp = ssalaad_amd.LRSLinearGroup(*[make_module(pr, gpu_device) for pr in probs])
+    x = make_x(probs[0], 700)
+    ys = grp(to_dev(x, dtype, gpu_device))
+    torch.cuda.synchronize()
+    for y, pr in zip(ys, probs):
+        assert err(y, oracle_y(pr, x)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", DT16, ids=["bf16", "f16"])
+@pytest.mark.parametrize("p", [16, 32, 64])
+@pytest.mark.parametrize("mode", [WIDE, NARROW], ids=["wide", "narrow"])
+def test_forced_tiles_inplace_op(dtype, p, mode, tile, gpu_device):
+    """PF_OP: out += x·Sᵀ on the active rows only; every other row keeps its bits."""
+    tile(mode)
+    M = 300
+    prob = make_problem(13 * p, 10 * p, 4, p, 0.3, dtype, seed=5 * p + mode, skew=True)
+    crow32, col32, vt, act = orc.module_buffers(prob["crow"], prob["col"], prob["vals"])
+    x = make_x(prob, M, seed=3)
+    rng = np.random.default_rng(p)
+    out0 = torch.from_numpy(rng.standard_normal((M, prob["n"]))).to(dtype).double().numpy()
+    want = orc.bsr_addmm_inplace(out0, x, crow32, col32, vt, act)
+    dev = gpu_device
+    out = to_dev(out0, dtype, dev)
+    torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_(
+        out, to_dev(x, dtype, dev), torch.from_numpy(crow32).to(dev),
+        torch.from_numpy(col32).to(dev), to_dev(vt, dtype, dev), torch.from_numpy(act).to(dev))
+    torch.cuda.synchronize()
+    assert err(out, want) <= TOL[dtype]
+    got = out.double().cpu().numpy()
+    for by in sorted(set(range(prob["NB"])) - set(act.tolist())):
+        assert np.array_equal(got[:, by * p:(by + 1) * p], out0[:, by * p:(by + 1) * p])
+
+
+# -------------------------------------------- full size, library's choice --
+
+
+def test_skewed_16x16_at_2048_tokens_every_row(gpu_device):
+    """4096×11008 bf16, rank 128, 16×16 blocks with Zipf(1.2) rows at 50% mean
+    density, 2048 tokens: the wide p = 16 tile (16 block-rows per workgroup)."""
+    prob = make_problem(4096, 11008, 128, 16, 0.5, torch.bfloat16, seed=21, skew=True)
+    assert _group_of(2048, prob["NB"], 16) == 16
+    mod = make_module(prob, gpu_device)
+    x = make_x(prob, 2048)
+    y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= 1e-2
+
+
+def test_llama1b_gate_up_group_at_2048_tokens_every_row(gpu_device):
+    """LLaMA-1B gate and up (5461×2048, 32×32 blocks at 50%, rank 256, FFN padded
+    to 5472) in one grouped launch at 2048 tokens: the wide p = 32 tile (8
+    block-rows per workgroup)."""
+    probs = [make_problem(5461, 2048, 256, 32, 0.5, torch.bfloat16, seed=40 + i, pad=True)
+             for i in range(2)]
+    assert _group_of(2048, 2 * probs[0]["NB"], 32) == 8
+    grp = ssalaad_amd.LRSLinearGroup(*[make_module(pr, gpu_device) for pr in probs])
+    x = make_x(probs[0], 2048)
+    ys = grp(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    for y, pr in zip(ys, probs):
+        assert y.shape == (2048, 5461)
+        assert err(y, oracle_y(pr, x)) <= 1e-2
+
+
+def test_llama7b_ffn_at_2048_tokens_every_row(gpu_device):
+    """11008×4096 bf16, 64×64 blocks at 50%, rank 256, 2048 tokens: the wide
+    p = 64 tile (4 block-rows per workgroup), every row against the oracle."""
+    prob = make_problem(11008, 4096, 256, 64, 0.5, torch.bfloat16, seed=11)
+    assert _group_of(2048, prob["NB"], 64) == 4
+    mod = make_module(prob, gpu_device)
+    x = make_x(prob, 2048)
+    y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= 1e-2
