@@ -191,6 +191,12 @@ class DecodeEngine:
         return self.lm_head(self.xn[:B])
 
     # ---------------------------------------------------------------- public
+    def clear_status(self) -> None:
+        """Reset the device's wait-status word and this engine's host mirror of it."""
+        self._stream.synchronize()
+        _runtime.reset_status(self.device)
+        self._status_host.zero_()
+
     @torch.no_grad()
     def step(self, tokens, positions) -> torch.Tensor:
         tokens = torch.as_tensor(tokens, dtype=torch.int64).reshape(-1)
@@ -207,8 +213,8 @@ class DecodeEngine:
         if int(self._status_host[0]) != 0:
             raise RuntimeError(
                 "a fused SLR launch of an earlier step gave up waiting for another "
-                "workgroup (bounded wait); its logits are unreliable. Clear the device's "
-                "status word (ssalaad_amd._runtime.reset_status) before stepping again.")
+                "workgroup (bounded wait); its logits are unreliable. Call clear_status() "
+                "before stepping again.")
         cur = torch.cuda.current_stream(self.device)
         s = self._stream
         s.wait_stream(cur)

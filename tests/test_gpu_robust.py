@@ -93,8 +93,8 @@ def test_decode_engine_raises_after_a_wait_gave_up(knobs, gpu_device):
     torch.cuda.synchronize()
     with pytest.raises(RuntimeError, match="gave up waiting"):
         eng.step([5, 6], [2, 2])
-    _runtime.reset_status(gpu_device)
-    eng.step([5, 6], [2, 2])       # mirror refreshed after the reset
+    eng.clear_status()
+    eng.step([5, 6], [2, 2])
     eng.step([7, 8], [3, 3])
 
 
