@@ -203,6 +203,30 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
                     int64_t exchange_bytes, void* workspace, int64_t workspace_bytes,
                     void* stream);
 
+/* ssl_slr_forward with no caller scratch and no allocation. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, hosts that forbid hipMalloc).
+ * The counters, handshake words and workspace come from a file-scope device
+ * array of ssl_slr_noalloc_scratch_bytes() (16 MiB) that each GPU the library
+ * runs on holds until the process ends: at most 256 KiB of row counters, 256
+ * KiB of handshake words and 15.5 MiB of workspace, as the *_counter_count,
+ * *_exchange_size and *_workspace_size queries compute them for the call;
+ * beyond that the call returns SSL_ERR_CAPACITY before any launch. Each call
+ * first clears the counters and handshake words it uses (a fill kernel on
+ * `stream`, then the fused launch), so calls with different plans may follow
+ * one another; calls that overlap on one GPU (other streams or threads) race on
+ * the shared array. A wait that gave up is recorded in the first handshake word
+ * (cleared by the next call). Same arguments, limits and results as
+ * ssl_slr_forward otherwise (16-bit calls of ssl_prefill_min_rows() rows or
+ * more need the prefill plans, which this entry point does not take). */
+int64_t ssl_slr_noalloc_scratch_bytes(void);
+int ssl_slr_forward_noalloc(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A,
+                            const void* B, const void* bias, const int32_t* col,
+                            const void* values, const int32_t* plan, int64_t n_chunks,
+                            int64_t n_slots, int64_t lr_wgs, int64_t M, int64_t m, int64_t m_pad,
+                            int64_t NB, int64_t r_pad, int32_t block_p, int32_t block_q,
+                            int32_t dtype, void* stream);
+
 /* One linear of a fused call (the arguments of ssl_slr_forward that differ
  * between linears reading the same x). */
 typedef struct ssl_slr_member {

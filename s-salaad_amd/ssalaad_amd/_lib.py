@@ -72,6 +72,12 @@ _SIGNATURES = {
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64,
          _c_p, _c_i64, _c_p, _c_i64, _c_p],
     ),
+    "ssl_slr_noalloc_scratch_bytes": (_c_i64, []),
+    "ssl_slr_forward_noalloc": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
+    ),
     "ssl_block_topk": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_p, _c_p, _c_p, _c_i64,
