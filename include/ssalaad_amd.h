@@ -125,7 +125,7 @@ int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, in
  * the call's M and row count (n_rows: the rows the plans list; for a grouped
  * call, all its linears' rows together). */
 int64_t ssl_prefill_min_rows(void);
-int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p);
+int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q);
 /* 1 if a fused SLR call (ssl_slr_forward, ssl_slr_forward_group) with block
  * storage, M token rows and n_rows block-rows over all its linears takes the
  * prefill kernels (and so needs their plans), 0 if it streams. At least
@@ -133,7 +133,8 @@ int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p);
  * blocks up to 512 rows and calls of fewer than 100 block-rows at the minimum
  * row count. The in-place op (ssl_bsr_addmm_inplace) keeps the plain
  * threshold. */
-int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_t dtype);
+int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q,
+                              int32_t dtype);
 
 /* -------------------------------------------------------------------------
  * In-place BSR addmm:  out[:, rows of active block-rows] += x · Sᵀ
@@ -145,14 +146,18 @@ int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_
  * computes: for each planned block-row `by`, acc = out[:, by·p : by·p+p] in fp32,
  * plus Σ_blocks x[:, col·q : col·q+q] · values[blk]  (values blocks are (q, p)),
  * stored back in the out dtype. Block-rows without a chunk are not touched.
- * p = q ∈ {16, 32, 64}; dtype ∈ {f32, bf16, f16} for out, x and values alike.
- * `plan` is a device copy of a table from ssl_plan_build (lr_units = 0).
- * For M >= ssl_prefill_min_rows() with 16-bit dtypes the prefill kernel runs
- * instead: it needs `pf_groups`/`pf_entries` (device copies from
- * ssl_prefill_plan_build with the same rows and group = pf_group =
- * ssl_prefill_group(M, rows, p)) and `values_pq`, the block values in
- * (nnz, p, q) order (each block transposed); other calls may pass NULL/0 there.
+ * Blocks: p ∈ {16, 32, 48, 64} output features, q any multiple of 16 up to
+ * 256 input features (square or not); dtype ∈ {f32, bf16, f16} for out, x and
+ * values alike. `plan` is a device copy of a table from ssl_plan_build
+ * (lr_units = 0). Calls for which ssl_bsr_addmm_takes_prefill(M, p, q, dtype)
+ * is 1 run the prefill kernel instead: they need `pf_groups`/`pf_entries`
+ * (device copies from ssl_prefill_plan_build with the same rows and group =
+ * pf_group = ssl_prefill_group(M, rows, p, q)) and `values_pq`, the block
+ * values in (nnz, p, q) order (each block transposed); other calls may pass
+ * NULL/0 there.
  * ------------------------------------------------------------------------- */
+int32_t ssl_bsr_addmm_takes_prefill(int64_t M, int32_t block_p, int32_t block_q,
+                                    int32_t dtype);
 int64_t ssl_bsr_addmm_workspace_size(int64_t M, int64_t NB, int32_t block_p,
                                      int64_t n_slots);
 int64_t ssl_bsr_addmm_counter_count(int64_t M, int64_t NB);

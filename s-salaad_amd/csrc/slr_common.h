@@ -222,7 +222,9 @@ struct VRaw;  // raw registers of one macro step
 
 template <int KE, int W>
 struct VRaw16 {
-  // W = 4: two dwords per row; W = 2: one dword; W = 1: one 16-bit value.
+  // W = 4: two dwords per row; W = 3: columns 0, 1 in the first dword and
+  // column 2 in the low half of the second; W = 2: one dword; W = 1: one
+  // 16-bit value.
   uint32_t r[KE][(W + 1) / 2];
 };
 template <int W>
@@ -245,6 +247,8 @@ __device__ __forceinline__ void load_vstep(VRawT<DT, KE, W>& raw, const void* bl
       if constexpr (W == 4) {
         float4 v = *(const float4*)q;
         raw.r[e][0] = v.x; raw.r[e][1] = v.y; raw.r[e][2] = v.z; raw.r[e][3] = v.w;
+      } else if constexpr (W == 3) {  // 12-byte pieces: 4-byte aligned only
+        raw.r[e][0] = q[0]; raw.r[e][1] = q[1]; raw.r[e][2] = q[2];
       } else if constexpr (W == 2) {
         float2 v = *(const float2*)q;
         raw.r[e][0] = v.x; raw.r[e][1] = v.y;
@@ -260,6 +264,9 @@ __device__ __forceinline__ void load_vstep(VRawT<DT, KE, W>& raw, const void* bl
       if constexpr (W == 4) {
         uint2 v = *(const uint2*)q;
         raw.r[e][0] = v.x; raw.r[e][1] = v.y;
+      } else if constexpr (W == 3) {  // 6-byte pieces: 2-byte aligned only
+        raw.r[e][0] = (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+        raw.r[e][1] = (uint32_t)q[2];
       } else if constexpr (W == 2) {
         raw.r[e][0] = *(const uint32_t*)q;
       } else {
@@ -361,11 +368,15 @@ __device__ __forceinline__ void st_w(void* base, int64_t off, const float (&v)[W
     float* p = (float*)base + off;
     if constexpr (W == 4) *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
     else if constexpr (W == 2) *(float2*)p = make_float2(v[0], v[1]);
-    else p[0] = v[0];
+    else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) p[i] = v[i];
+    }
   } else {
     uint16_t* p = (uint16_t*)base + off;
-    if constexpr (W == 1) {
-      p[0] = (uint16_t)to_bits<DT>(v[0]);
+    if constexpr (W == 1 || W == 3) {
+#pragma unroll
+      for (int i = 0; i < W; ++i) p[i] = (uint16_t)to_bits<DT>(v[i]);
     } else {
       uint32_t w[W / 2];
 #pragma unroll

@@ -1,0 +1,14 @@
+// Instantiations of the streaming SLR / BSR kernel (stream_kernel.h) for
+// f16 activations: every block width P, fragment depth KE and token-tile
+// height MT, in both modes. One file per dtype keeps the build parallel.
+#include "stream_kernel.h"
+
+namespace ssl {
+
+template <>
+hipError_t stream_launch<DT_F16>(int mode, int sf, int P, int KE, int MT, const GroupArgs& a,
+                               int64_t blocks, hipStream_t s) {
+  return stream_dispatch<DT_F16>(mode, sf, P, KE, MT, a, blocks, s);
+}
+
+}  // namespace ssl

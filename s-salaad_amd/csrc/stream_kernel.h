@@ -1,0 +1,796 @@
+#pragma once
+// Device code of the streaming SLR / BSR kernels (slr_kernel), shared by the
+// per-dtype instantiation files stream_{bf16,f16,f32}.hip; the host side is
+// bsr_stream.hip.
+//
+// Decode-shaped calls (up to 64 token rows per tile) are HBM-bound: every
+// weight byte is read once per token tile and feeds a handful of MFMAs. The
+// kernels are therefore organised around keeping as many weight bytes in
+// flight as possible and around the few cross-workgroup exchanges that the
+// computation needs, because on a loaded device each exchange (a device-coherent
+// store, its acknowledgement and a counter update) costs microseconds.
+//
+// Row-resident workgroups. A plan (plan.cpp) gives one workgroup (8 waves) a
+// whole block-row — its sparse (q, p) blocks and, for the fused linear, the
+// 32-rank slices of A — unless the row is long, in which case it is split into
+// a few chunks. The 8 waves take the units round-robin and issue all of their
+// loads before the first MFMA (about 32 blocks of 64×64 in one batch), so a
+// typical row costs one memory round trip. Weights go from HBM straight into
+// registers (no LDS staging: each byte is used once per token tile); the sparse
+// blocks, stored (q, p) as in the reference module, are transposed into MFMA
+// fragments with register byte permutes.
+//
+// Reduction. The 8 wave tiles are summed in LDS in a fixed tree order; wave 0
+// then runs the epilogue (bias, or the in-place add of the op) and stores the
+// row tile once.
+//
+// Split rows. A chunk of a split row stores its fp32 tile with device-coherent
+// (sc1) stores, waits for the acknowledgement and bumps the row's counter. In
+// the fused linear the row's finaliser chunk (the one with the low-rank units,
+// launched after all other chunks) waits for the others and sums the partials in
+// chunk order; in the in-place op the chunk that arrives last does. Results are
+// deterministic either way. Only exchanged data is accessed device-coherently;
+// no workgroup writes back or invalidates a whole L2.
+//
+// The latent. The fused launch starts with one workgroup per 16-rank tile of
+// t = x·Bᵀ and chunk of in_features (one batch of loads each); each stores its
+// fp32 partial device-coherently and bumps the token tile's ready counter. The
+// consumers sum the partials in chunk order and round once. Low-rank units
+// load their A slices first and wait for that counter (bounded spin) only then.
+// Only one thread per workgroup polls. Workgroups of one XCD are dispatched in
+// index order, so every workgroup a chunk may wait for (latent tiles, earlier
+// chunks of its row) is resident or done before it, and every wait ends. The
+// latent counters are monotonic per plan (a consumer's ticket tells it which
+// launch it belongs to), so no launch needs an end-of-launch reset.
+
+#include "abi_internal.h"
+#include "slr_common.h"
+
+namespace ssl {
+
+enum : int { MODE_OP = 0, MODE_FUSED = 1 };
+enum : int { SF_BSR = 0, SF_NM24 = 1 };  // sparse block storage
+
+constexpr int kSW = 8;            // waves per streaming workgroup
+constexpr int kST = kSW * kWave;  // threads per streaming workgroup
+
+// Polls of a counter before a wait gives up and flags an error in the status
+// word (seconds; a healthy launch waits microseconds). ssl_debug_set can lower
+// it for tests of the give-up path.
+constexpr int kSpinLimit = 1 << 22;
+
+// ---------------------------------------------------------------------------
+// Device-coherent (agent scope) 32-bit accesses for data exchanged between
+// workgroups of one launch: sc1 loads/stores, no cache-wide maintenance.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev_u32(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int rmw_add(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_int(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_int(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Vector forms of the same device-coherent accesses: buffer loads/stores with
+// the sc1 cache policy (what the relaxed agent-scope atomics above compile to),
+// N = 1, 2, 3 or 4 floats at a wave-uniform base plus a per-lane byte offset below
+// 2 GiB (the host checks the workspace size).
+constexpr int kSc1 = 16;  // cache-policy bit: sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                           0x00020000);
+}
+template <int N>
+__device__ __forceinline__ void ld_dev_vec(__amdgpu_buffer_rsrc_t r, int byte_off, float* v) {
+  if constexpr (N == 4) {
+    const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kSc1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(u[i]);
+  } else if constexpr (N == 2) {
+    const auto u = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, kSc1);
+    v[0] = __uint_as_float(u[0]);
+    v[1] = __uint_as_float(u[1]);
+  } else if constexpr (N == 3) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      v[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off + 4 * i, 0, kSc1));
+  } else {
+    static_assert(N == 1, "1, 2, 3 or 4 floats");
+    v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, kSc1));
+  }
+}
+template <int N>
+__device__ __forceinline__ void st_dev_vec(__amdgpu_buffer_rsrc_t r, int byte_off, const float* v) {
+  if constexpr (N == 4) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 u = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                     __float_as_uint(v[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(u, r, byte_off, 0, kSc1);
+  } else if constexpr (N == 2) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 u = {__float_as_uint(v[0]), __float_as_uint(v[1])};
+    __builtin_amdgcn_raw_buffer_store_b64(u, r, byte_off, 0, kSc1);
+  } else if constexpr (N == 3) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[i]), r, byte_off + 4 * i, 0, kSc1);
+  } else {
+    static_assert(N == 1, "1, 2, 3 or 4 floats");
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, byte_off, 0, kSc1);
+  }
+}
+
+// All of this thread's earlier memory operations have completed (stores are
+// acknowledged by the device-coherent level).
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
+typedef unsigned long long u64;
+constexpr int kLatentUnits = 840;  // divisible by every latent split 1..8
+__device__ __forceinline__ u64 rmw_add64(u64* p, u64 v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 ld_u64(const u64* p) {
+  return __hip_atomic_load(const_cast<u64*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_u64(u64* p, u64 v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Spin (one lane) until *flag >= target; bounded (`polls`), sets *status on
+// timeout. The caller goes on either way, so every workgroup of the launch
+// still ends; a wait that gave up leaves its tile unreliable, which the status
+// word reports.
+template <typename T>
+__device__ __forceinline__ void wait_at_least(const T* flag, T target, u64* status, int polls) {
+  int n = 0;
+  while (__hip_atomic_load(const_cast<T*>(flag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+         target) {
+    __builtin_amdgcn_s_sleep(2);
+    if (++n > polls) {
+      st_u64(status, 1);
+      break;
+    }
+  }
+}
+
+// One KE-element fragment (16 bytes) of the final latent, read device-coherently.
+template <int DT, int KE>
+__device__ __forceinline__ typename Mma<DT, KE>::Frag ld_dev_frag(__amdgpu_buffer_rsrc_t r,
+                                                                  int byte_off) {
+  static_assert(KE * Elem<DT>::bytes == 16, "16-byte fragments");
+  const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kSc1);
+  typename Mma<DT, KE>::Frag f;
+  static_assert(sizeof(f) == 16, "fragment image");
+  __builtin_memcpy(&f, &u, 16);
+  return f;
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic tree reduction of the kSW wave tiles into wave 0's registers:
+// rounds of halving; in each round wave i (< half) adds wave i + half's tile,
+// passed through LDS in groups of SLOTS tiles.
+// ---------------------------------------------------------------------------
+template <int MT, int W>
+constexpr int red_slots() {
+  return MT * W <= 8 ? 4 : 2;  // LDS: SLOTS × MT·W KiB
+}
+
+template <int MT, int W>
+__device__ __forceinline__ void tree_reduce(f32x4 (&acc)[MT][W], f32x4* red, int wid, int lane) {
+  constexpr int SLOTS = red_slots<MT, W>();
+#pragma unroll
+  for (int half = kSW / 2; half >= 1; half /= 2) {
+#pragma unroll
+    for (int g0 = 0; g0 < half; g0 += SLOTS) {
+      const int g1 = g0 + SLOTS < half ? g0 + SLOTS : half;
+      if (wid >= half + g0 && wid < half + g1) {
+        f32x4* slot = red + (wid - half - g0) * (MT * W * kWave);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int s = 0; s < W; ++s) slot[(mt * W + s) * kWave + lane] = acc[mt][s];
+      }
+      __syncthreads();
+      if (wid >= g0 && wid < g1) {
+        const f32x4* slot = red + (wid - g0) * (MT * W * kWave);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int s = 0; s < W; ++s) acc[mt][s] += slot[(mt * W + s) * kWave + lane];
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Wave-level exchange of a row tile held in registers (lane-native layout:
+// lane (c, g), element e of column tile s -> row 16·mt + 4g + e, column W·c + s).
+// Partial tiles live in memory row-major [16·MT][16·W] fp32.
+template <int MT, int W>
+__device__ __forceinline__ void store_partial(const f32x4 (&acc)[MT][W], float* part, int Mrem,
+                                              int lane) {
+  constexpr int TP = 16 * W;
+  const int c = lane & 15, g = lane >> 4;
+  const auto r = dev_rsrc(part);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rr = mt * 16 + 4 * g + e;
+      if (rr < Mrem) {
+        float v[W];
+#pragma unroll
+        for (int s = 0; s < W; ++s) v[s] = acc[mt][s][e];
+        st_dev_vec<W>(r, (rr * TP + W * c) * 4, v);
+      }
+    }
+}
+template <int MT, int W>
+__device__ __forceinline__ void add_partial(f32x4 (&tot)[MT][W], const float* part, int Mrem,
+                                            int lane) {
+  constexpr int TP = 16 * W;
+  const int c = lane & 15, g = lane >> 4;
+  const auto r = dev_rsrc(part);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rr = mt * 16 + 4 * g + e;
+      if (rr < Mrem) {
+        float v[W];
+        ld_dev_vec<W>(r, (rr * TP + W * c) * 4, v);
+#pragma unroll
+        for (int s = 0; s < W; ++s) tot[mt][s][e] += v[s];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel arguments (one struct for every mode).
+// ---------------------------------------------------------------------------
+struct SlrArgs {
+  // activations
+  const void* x;
+  int64_t ldx;
+  int M, m;
+  // output and the streamed part
+  void* y;
+  int64_t ldy;
+  const int32_t* col;
+  const void* values;
+  const int32_t* plan;
+  int n_chunks;
+  int NB;
+  // Sparse blocks are walked in K slabs of KM rows (the MFMA's k extent):
+  // block b's slab ks is KM·p contiguous values at b·blk_bytes + ks·slab_bytes.
+  int q;                // block_q: input features per block
+  int nks;              // slabs per block (q / KM; 1 for 2:4 storage)
+  uint32_t nks_magic;   // ceil(2^32 / nks) when nks > 1: slab → block by a high multiply
+  int blk_bytes;        // bytes per stored block
+  int slab_bytes;       // bytes per slab
+  const void* A;
+  int64_t lda;
+  const void* bias;
+  int64_t n_slots;
+  float* part_main;
+  int* cnt_main;  // [MG][NB]
+  // latent
+  const void* B;
+  int64_t ldb;
+  void* t;          // final latent [MG·16·MT][ldt], activation dtype
+  int64_t ldt;
+  float* t_part;    // fp32 partials [n_kc][MG][n_rt][MT·256] (lane-native tiles)
+  int MG;           // token tiles
+  int n_rt;         // 16-rank tiles
+  int n_kc;         // in_features chunks of the latent
+  int ku_total;     // in_features in KM-column units
+  int ku_chunk;     // KM-column units per latent chunk
+  int n_lat_wgs;    // latent workgroups at the start of the grid (n_rt·n_kc·MG)
+  // Handshake words, all monotonic (never reset): sync[0] is the status (1 =
+  // a wait gave up); token tile mg owns sync[1 + mg·(2 + n_rt) ...]:
+  //   [0] final latent tiles written (+1 per rank tile and launch)
+  //   [1] consumer tickets (+1 per consuming workgroup and launch)
+  //   [2 + rt] arrivals of rank tile rt's K chunks (+kLatentUnits/n_kc each,
+  //       so every launch adds exactly kLatentUnits whatever its split)
+  u64* sync;
+  int lr_wgs;       // workgroups that consume the latent (per token tile)
+  int lat_weight;   // kLatentUnits / n_kc
+  // Bounded waits: where a timeout is reported (the caller's status word, or
+  // sync[0]), polls before giving up, and an offset added to every wait's
+  // target (nonzero only when a test forces the give-up path).
+  u64* status;
+  int wait_polls;
+  int wait_bias;
+};
+
+__device__ __forceinline__ u64* tile_sync(const SlrArgs& a, int mg) {
+  return a.sync + 1 + (int64_t)mg * (2 + a.n_rt);
+}
+
+// ---------------------------------------------------------------------------
+// Latent workgroup: t[token tile, 16-rank tile rt] over all of in_features.
+// ---------------------------------------------------------------------------
+template <int DT, int MT>
+__device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) {
+  constexpr int KE = (DT == DT_F32) ? 4 : 8;
+  using MM = Mma<DT, KE>;
+  using Frag = typename MM::Frag;
+  constexpr int KM = MM::KM;
+  constexpr int UNR = MT == 1 ? 8 : (MT == 2 ? 4 : 2);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = wave_uniform(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int per_mg = a.n_rt * a.n_kc;
+  const int mg = wg / per_mg, rt = (wg % per_mg) / a.n_kc, kc = wg % a.n_kc;
+  const int m0 = mg * MT * 16;
+  const int Mrem = min(a.M - m0, MT * 16);
+  const int64_t brow = (int64_t)(rt * 16 + c) * a.ldb;
+  const int ub = kc * a.ku_chunk, ue = min(ub + a.ku_chunk, a.ku_total);
+
+  f32x4 acc[MT][1];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int u0 = ub + wid; u0 < ue; u0 += kSW * UNR) {
+    Frag xf[UNR][MT];
+    Frag bf[UNR];
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int u = u0 + k * kSW;
+      if (u < ue) {
+        const int kcol = u * KM + KE * g;
+        if (u * KM + KM <= a.m) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            xf[k][mt] = load_kfrag_full<DT, KE>(
+                a.x, (int64_t)(m0 + min(mt * 16 + c, Mrem - 1)) * a.ldx + kcol);
+        } else {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int rr = mt * 16 + c;
+            const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
+            xf[k][mt] = (valid > 0)
+                            ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol, valid)
+                            : zero_frag<DT, KE>();
+          }
+        }
+        bf[k] = load_kfrag_full<DT, KE>(a.B, brow + kcol);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      if (u0 + k * kSW < ue) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][0], xf[k][mt], bf[k]);
+      }
+    }
+  }
+
+  tree_reduce<MT, 1>(acc, red, wid, lane);
+  if (wid != 0) return;
+  // wave 0: lane (c, g) holds rows 16·mt + 4g + e of rank rt·16 + c.
+  u64* sy = tile_sync(a, mg);
+  if (a.n_kc > 1) {
+    // Publish this K chunk's fp32 partial; the last chunk of the rank tile to
+    // arrive sums all of them in chunk order (deterministic) and goes on.
+    const auto pr = dev_rsrc(a.t_part);
+    const int64_t slab = (int64_t)a.MG * a.n_rt * (MT * 256);  // floats per K chunk
+    const int64_t tile = ((int64_t)mg * a.n_rt + rt) * (MT * 256);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float v[4] = {acc[mt][0][0], acc[mt][0][1], acc[mt][0][2], acc[mt][0][3]};
+      st_dev_vec<4>(pr, (int)((kc * slab + tile + (mt * 64 + lane) * 4) * 4), v);
+    }
+    wait_mem();
+    int last = 0;
+    if (lane == 0) {
+      const u64 old = rmw_add64(sy + 2 + rt, (u64)a.lat_weight);
+      last = (old + (u64)a.lat_weight) % kLatentUnits == 0;
+    }
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
+    f32x4 tot[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) tot[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < a.n_kc; ++k) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (k == kc) {
+          tot[mt] += acc[mt][0];
+        } else {
+          float v[4];
+          ld_dev_vec<4>(pr, (int)((k * slab + tile + (mt * 64 + lane) * 4) * 4), v);
+          tot[mt] += f32x4{v[0], v[1], v[2], v[3]};
+        }
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt][0] = tot[mt];
+  }
+  // Final latent tile, rounded once to the activation dtype as F.linear's
+  // output is. Rows past M hold zeros (their x rows were read as zero).
+  const auto tr = dev_rsrc(a.t);
+  constexpr int EB = Elem<DT>::bytes;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int off = (int)(((int64_t)(m0 + mt * 16 + 4 * g + e) * a.ldt + rt * 16 + c) * EB);
+      if constexpr (DT == DT_F32) {
+        float v = acc[mt][0][e];
+        st_dev_vec<1>(tr, off, &v);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)to_bits<DT>(acc[mt][0][e]), tr, off,
+                                              0, kSc1);
+      }
+    }
+  wait_mem();
+  if (lane == 0) rmw_add64(sy, 1);
+}
+
+// ---------------------------------------------------------------------------
+// Streaming workgroup: one plan chunk for one token tile.
+// ---------------------------------------------------------------------------
+// SF: storage of the sparse blocks, SF_BSR (q, p) blocks or SF_NM24 packed 2:4 blocks.
+// P: output features per block-row (the tile width; W = P / 16 MFMA column tiles).
+// KE: k elements per lane of the sparse MFMA fragments (8 when q is a multiple
+// of 32 for 16-bit activations, else 4), so one K slab is KM = 4·KE block rows
+// and q (any multiple of KM) is a runtime value.
+template <int DT, int P, int KE, int MT, int MODE, int UNR, int SF>
+__device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f32x4* red) {
+  constexpr int W = P / 16;
+  using MM = Mma<DT, KE>;
+  using Frag = typename MM::Frag;
+  constexpr int KM = MM::KM;
+  static_assert(DT != DT_F32 || KE == 4, "fp32 fragments hold 4 k");
+  static_assert(SF == SF_BSR || (P == kNmBlock && DT != DT_F32 && KE == 8),
+                "2:4 blocks are 32×32, 16-bit");
+  using Raw = typename std::conditional<SF == SF_NM24, NmRaw, VRawT<DT, KE, W>>::type;
+  constexpr int KEL = (DT == DT_F32) ? 4 : 8;  // low-rank part: widest fragment
+  using ML = Mma<DT, KEL>;
+  using FragL = typename ML::Frag;
+  constexpr int NLS = 32 / ML::KM;  // macro steps per 32-rank unit
+  constexpr int EB = Elem<DT>::bytes;
+  constexpr int TSZ = MT * 16 * P;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = wave_uniform(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int32_t* d = a.plan + (int64_t)chunk * SSL_PLAN_STRIDE;
+  const int row = d[0], bb = d[1], be = d[2], lb = d[3], le = d[4], seq = d[5], nseq = d[6];
+  const int slot = d[7];
+  const int m0 = mg * MT * 16;
+  const int Mrem = min(a.M - m0, MT * 16);
+
+  f32x4 acc[MT][W];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int s = 0; s < W; ++s) acc[mt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const bool used_t = (MODE == MODE_FUSED) && lb < le;
+  // A consumer of the latent takes a ticket at once (its latency hides behind
+  // the row's loads). Launch k's consumers hold tickets k·lr_wgs ... and wait
+  // for (k + 1)·(latent workgroups) completions, so no counter is ever reset.
+  u64 ticket = 0;
+  if (used_t && threadIdx.x == 0) ticket = rmw_add64(tile_sync(a, mg) + 1, 1);
+
+  // The wave's first low-rank unit of A does not depend on the latent: its
+  // loads go out ahead of the sparse blocks.
+  FragL af0[NLS][W];
+  if constexpr (MODE == MODE_FUSED) {
+    if (used_t && lb + wid < le) {
+#pragma unroll
+      for (int ls = 0; ls < NLS; ++ls)
+#pragma unroll
+        for (int s = 0; s < W; ++s)
+          af0[ls][s] = load_kfrag<DT, KEL>(
+              a.A, (int64_t)(row * P + W * c + s) * a.lda + (lb + wid) * 32 + ls * ML::KM + KEL * g,
+              KEL);
+    }
+  }
+
+  // ---- sparse blocks, as K slabs: the chunk's slabs [bb·nks, be·nks) go to
+  // the waves round-robin; a batch issues all its loads (x, then the slab)
+  // slab by slab before the first MFMA, so each slab waits only for its own data.
+  const int nks = a.nks;
+  const int vb = bb * nks, ve = be * nks;
+  for (int v0 = vb + wid; v0 < ve; v0 += kSW * UNR) {
+    Raw raw[UNR];
+    Frag xf[UNR][MT];
+    // the batch's column indices first, as scalar loads issued together
+    int colk[UNR];
+    int64_t voff[UNR];
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int v = min(v0 + k * kSW, ve - 1);
+      const int blk = nks == 1 ? v : (int)__umulhi((uint32_t)v, a.nks_magic);
+      const int ks = v - blk * nks;
+      colk[k] = ld_uniform(a.col, blk) * a.q + ks * KM;
+      voff[k] = (int64_t)blk * a.blk_bytes + ks * a.slab_bytes;
+    }
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      if (v0 + k * kSW < ve) {
+        const char* vb_ = (const char*)a.values + voff[k];
+        const int kcol = colk[k] + KE * g;
+        const bool full = colk[k] + KM <= a.m;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int rr = mt * 16 + c;
+          if (full) {
+            xf[k][mt] =
+                load_kfrag_full<DT, KE>(a.x, (int64_t)(m0 + min(rr, Mrem - 1)) * a.ldx + kcol);
+          } else {
+            const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
+            xf[k][mt] = (valid > 0) ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol,
+                                                         valid)
+                                    : zero_frag<DT, KE>();
+          }
+        }
+        if constexpr (SF == SF_NM24) load_nm(raw[k], vb_, lane);
+        else load_vstep<DT, KE, W>(raw[k], vb_, P, 0, lane);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      if (v0 + k * kSW < ve) {
+#pragma unroll
+        for (int s = 0; s < W; ++s) {
+          Frag vf;
+          if constexpr (SF == SF_NM24) vf = nm_frag<DT>(raw[k], s);
+          else vf = vfrag<DT, KE, W>(raw[k], s);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][s], xf[k][mt], vf);
+        }
+      }
+    }
+  }
+
+  // ---- low-rank units: 32 ranks of A per unit, t·Aᵀ. One thread of the
+  // workgroup waits for this launch's final latent; the barrier releases the
+  // other waves, which then read it device-coherently.
+  if constexpr (MODE == MODE_FUSED) {
+    if (used_t) {
+      if (threadIdx.x == 0) {
+        const u64 target = (ticket / (u64)a.lr_wgs + 1) * (u64)a.n_rt;
+        wait_at_least<u64>(tile_sync(a, mg), target + (u64)a.wait_bias, a.status, a.wait_polls);
+      }
+      __syncthreads();
+      const auto tr = dev_rsrc(a.t);
+      for (int u = lb + wid; u < le; u += kSW) {
+        FragL af[NLS][W];
+        FragL tf[NLS][MT];
+#pragma unroll
+        for (int ls = 0; ls < NLS; ++ls) {
+          const int kr = u * 32 + ls * ML::KM + KEL * g;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            tf[ls][mt] = ld_dev_frag<DT, KEL>(
+                tr, (int)(((int64_t)(m0 + mt * 16 + c) * a.ldt + kr) * EB));
+#pragma unroll
+          for (int s = 0; s < W; ++s)
+            af[ls][s] = (u == lb + wid)
+                            ? af0[ls][s]
+                            : load_kfrag<DT, KEL>(a.A, (int64_t)(row * P + W * c + s) * a.lda + kr,
+                                                  KEL);
+        }
+#pragma unroll
+        for (int ls = 0; ls < NLS; ++ls)
+#pragma unroll
+          for (int s = 0; s < W; ++s)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) ML::run(acc[mt][s], tf[ls][mt], af[ls][s]);
+      }
+    }
+  }
+
+  tree_reduce<MT, W>(acc, red, wid, lane);
+  if (wid != 0) return;
+
+  // ---- wave 0: combine (split rows) and epilogue ---------------------------
+  if (nseq > 1) {
+    float* part_base = a.part_main + ((int64_t)mg * a.n_slots + slot) * TSZ;
+    int* counter = a.cnt_main + (int64_t)mg * a.NB + row;
+    const bool finaliser_mode = (MODE == MODE_FUSED) && a.n_rt > 0;
+    if (finaliser_mode && used_t) {
+      // the row's finaliser: wait for the other nseq - 1 chunks
+      if (lane == 0) wait_at_least<int>(counter, nseq - 1 + a.wait_bias, a.status, a.wait_polls);
+    } else {
+      store_partial<MT, W>(acc, part_base + (int64_t)seq * TSZ, Mrem, lane);
+      wait_mem();
+      int old = 0;
+      if (lane == 0) old = rmw_add(counter, 1);
+      old = __builtin_amdgcn_readfirstlane(old);
+      if (finaliser_mode || old != nseq - 1) return;
+    }
+    // This chunk combines the row (the finaliser, or the op's last arrival).
+    // sum the partials in chunk order, this chunk's tile at its own position
+    f32x4 tot[MT][W];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int s = 0; s < W; ++s) tot[mt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < nseq; ++k) {
+      if (k == seq) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int s = 0; s < W; ++s) tot[mt][s] += acc[mt][s];
+      } else {
+        add_partial<MT, W>(tot, part_base + (int64_t)k * TSZ, Mrem, lane);
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int s = 0; s < W; ++s) acc[mt][s] = tot[mt][s];
+    // Return the row counter to zero by subtracting the arrivals this launch
+    // makes (nseq - 1 other chunks for the finaliser; all nseq in the op)
+    // rather than storing 0: if a finaliser's wait gave up, the chunks still to
+    // arrive bring the counter back to exactly zero by the launch's end.
+    if (lane == 0) rmw_add(counter, finaliser_mode ? -(nseq - 1) : -nseq);
+  }
+
+  // epilogue: lane (c, g) owns W adjacent output columns of rows 16·mt + 4g + e
+  const int j0 = row * P + W * c;
+  float bv[W];
+#pragma unroll
+  for (int s = 0; s < W; ++s) bv[s] = 0.f;
+  if constexpr (MODE == MODE_FUSED) {
+    if (a.bias != nullptr) ld_w<DT, W>(a.bias, j0, bv);
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rr = mt * 16 + 4 * g + e;
+      if (rr < Mrem) {
+        const int64_t off = (int64_t)(m0 + rr) * a.ldy + j0;
+        float o[W];
+        if constexpr (MODE == MODE_FUSED) {
+#pragma unroll
+          for (int s = 0; s < W; ++s) o[s] = acc[mt][s][e] + bv[s];
+        } else {
+          ld_w<DT, W>(a.y, off, o);
+#pragma unroll
+          for (int s = 0; s < W; ++s) o[s] += acc[mt][s][e];
+        }
+        st_w<DT, W>(a.y, off, o);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel. Grid (1-D): [latent workgroups][stream chunks × token tiles].
+// ---------------------------------------------------------------------------
+// A launch serves up to kMaxGroup linears that read the same x (e.g. the q, k
+// and v projections): all latent workgroups first, member by member, then all
+// row workgroups, member by member. Workgroup → member lookups read the
+// descriptors in place from the kernel-argument segment (scalar loads).
+constexpr int kMaxGroup = 4;
+struct GroupArgs {
+  int n;                          // members
+  int lat_total;                  // latent workgroups of all members
+  int lat_off[kMaxGroup + 1];     // first latent workgroup of each member
+  int str_off[kMaxGroup + 1];     // first row workgroup (after lat_total) of each member
+  SlrArgs m[kMaxGroup];
+};
+
+template <int DT, int P, int KE, int MT, int MODE, int UNR, int SF>
+__global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_kernel(
+    GroupArgs g_by_value) {
+  (void)g_by_value;
+  const GroupArgs& g = *(const GroupArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  constexpr int W = P / 16;
+  constexpr int SLOTS = red_slots<MT, W>();
+  __shared__ f32x4 red[SLOTS * MT * W * kWave];
+  const int b = blockIdx.x;
+  if constexpr (MODE == MODE_FUSED) {
+    if (b < g.lat_total) {
+      int i = 0;
+      while (i + 1 < g.n && b >= g.lat_off[i + 1]) ++i;
+      latent_wg<DT, MT>(g.m[i], b - g.lat_off[i], red);
+      return;
+    }
+  }
+  const int sb = b - (MODE == MODE_FUSED ? g.lat_total : 0);
+  int i = 0;
+  while (i + 1 < g.n && sb >= g.str_off[i + 1]) ++i;
+  const SlrArgs& a = g.m[i];
+  const int lb = sb - g.str_off[i];
+  const int mg = lb / a.n_chunks, chunk = lb % a.n_chunks;
+  stream_wg<DT, P, KE, MT, MODE, UNR, SF>(a, chunk, mg, red);
+}
+
+// Slabs per wave per batch. The byte budget of the square-block kernels
+// (a 32-block row in one batch of the 8 waves for 32×32 and 64×64 blocks,
+// fewer units for wide tiles; 16-bit kernels with P ≤ 32 stay within 128 VGPRs,
+// so two workgroups share a compute unit), expressed in slabs of KM = 4·KE rows.
+template <int DT, int P, int KE, int MT>
+constexpr int stream_unroll() {
+  constexpr int KM = 4 * KE;
+  constexpr int bytes = P * P * Elem<DT>::bytes;
+  constexpr int u = bytes >= 16384 ? 2 : (bytes >= 2048 ? 4 : 16);
+  constexpr int d = MT >= 4 ? 4 : MT;
+  constexpr int blocks = u / d > 0 ? u / d : 1;
+  constexpr int slabs = blocks * P / KM;
+  return slabs > 0 ? slabs : 1;
+}
+
+// One launch of slr_kernel (grid: `blocks` workgroups of kST threads) for a
+// dtype; defined in stream_{bf16,f16,f32}.hip. P ∈ {16, 32, 48, 64}; KE 4 or
+// 8 (4 for fp32); MT ∈ {1, 2, 4}; SF_NM24 only with P = 32, KE = 8, MODE_FUSED.
+template <int DT>
+hipError_t stream_launch(int mode, int sf, int P, int KE, int MT, const GroupArgs& a,
+                         int64_t blocks, hipStream_t s);
+
+template <int DT, int P, int KE, int MT, int MODE, int SF>
+hipError_t stream_launch_one(const GroupArgs& a, int64_t blocks, hipStream_t s) {
+  constexpr int UNR = stream_unroll<DT, P, KE, MT>();
+  hipLaunchKernelGGL((slr_kernel<DT, P, KE, MT, MODE, UNR, SF>), dim3((unsigned)blocks), dim3(kST),
+                     0, s, a);
+  return hipGetLastError();
+}
+
+// The instantiation table of one dtype (expanded in its own file).
+template <int DT>
+hipError_t stream_dispatch(int mode, int sf, int P, int KE, int MT, const GroupArgs& a,
+                           int64_t blocks, hipStream_t s) {
+  if constexpr (DT != DT_F32) {
+    if (sf == SF_NM24) {
+      if (P != kNmBlock || KE != 8 || mode != MODE_FUSED) return hipErrorInvalidValue;
+      switch (MT) {
+        case 1: return stream_launch_one<DT, kNmBlock, 8, 1, MODE_FUSED, SF_NM24>(a, blocks, s);
+        case 2: return stream_launch_one<DT, kNmBlock, 8, 2, MODE_FUSED, SF_NM24>(a, blocks, s);
+        case 4: return stream_launch_one<DT, kNmBlock, 8, 4, MODE_FUSED, SF_NM24>(a, blocks, s);
+      }
+      return hipErrorInvalidValue;
+    }
+  }
+  if (sf != SF_BSR) return hipErrorInvalidValue;
+#define SSL_MT(PP, KK, MD)                                                     \
+  switch (MT) {                                                                \
+    case 1: return stream_launch_one<DT, PP, KK, 1, MD, SF_BSR>(a, blocks, s); \
+    case 2: return stream_launch_one<DT, PP, KK, 2, MD, SF_BSR>(a, blocks, s); \
+    case 4: return stream_launch_one<DT, PP, KK, 4, MD, SF_BSR>(a, blocks, s); \
+  }                                                                            \
+  return hipErrorInvalidValue;
+#define SSL_KE(PP, MD)                           \
+  if (KE == 4) { SSL_MT(PP, 4, MD) }             \
+  if constexpr (DT != DT_F32) {                  \
+    if (KE == 8) { SSL_MT(PP, 8, MD) }           \
+  }                                              \
+  return hipErrorInvalidValue;
+#define SSL_P(MD)                        \
+  switch (P) {                           \
+    case 16: { SSL_KE(16, MD) }          \
+    case 32: { SSL_KE(32, MD) }          \
+    case 48: { SSL_KE(48, MD) }          \
+    case 64: { SSL_KE(64, MD) }          \
+  }                                      \
+  return hipErrorInvalidValue;
+  if (mode == MODE_FUSED) {
+    SSL_P(MODE_FUSED)
+  }
+  SSL_P(MODE_OP)
+#undef SSL_P
+#undef SSL_KE
+#undef SSL_MT
+}
+
+}  // namespace ssl
+

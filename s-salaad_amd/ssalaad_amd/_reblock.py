@@ -1,0 +1,62 @@
+"""Block shapes the kernels run, and the exact re-blocking into them.
+
+The streaming kernel's tile is P ∈ {16, 32, 48, 64} output features wide and
+walks a block's Q input features as K slabs, Q any multiple of 16 up to 256.
+The reference GPU module accepts any block whose sides are multiples of 16
+(ssalaad/efficient/ls_linear.py:114-117). A (q, p)-stored block with p > 64 or
+q > 256 is therefore cut into (Q, P) sub-blocks: block-row `by` becomes the
+p / P kernel rows by·(p/P) + h, each holding, for every block of the row, its
+q / Q sub-blocks in column order (column col·(q/Q) + j). The sub-blocks tile
+the block exactly, so the product is the same sum with the same terms; only
+the order in which fp32 partial sums are added changes. Output columns are
+unchanged (kernel row r covers columns r·P … r·P + P − 1 = by·p + h·P …).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+KERNEL_P = (64, 48, 32, 16)   # tile widths, widest first
+MAX_Q = 256
+
+
+def kernel_block_shape(p: int, q: int) -> tuple[int, int]:
+    """(P, Q) the kernels run a (p, q) block as: the widest tile dividing p,
+    and q itself up to MAX_Q, else its largest multiple-of-16 divisor ≤ MAX_Q."""
+    P = next(w for w in KERNEL_P if p % w == 0)
+    Q = q if q <= MAX_Q else max(d for d in range(16, MAX_Q + 1, 16) if q % d == 0)
+    return P, Q
+
+
+def reblock(crow_h: np.ndarray, col_h: np.ndarray, values: torch.Tensor, p: int, q: int,
+            P: int, Q: int):
+    """Return (crow', col', values') of the same matrix in (Q, P) blocks:
+    crow'/col' int32 NumPy arrays, values' (nnz', Q, P) on values' device."""
+    fp, fq = p // P, q // Q
+    NB = crow_h.shape[0] - 1
+    counts = np.diff(crow_h.astype(np.int64))
+    # new rows (by, h): every block of row by, in order, for each h
+    order_k = []
+    order_h = []
+    for by in range(NB):
+        ks = np.arange(crow_h[by], crow_h[by + 1])
+        for h in range(fp):
+            order_k.append(ks)
+            order_h.append(np.full(ks.shape, h))
+    k_idx = np.concatenate(order_k) if order_k else np.zeros(0, np.int64)
+    h_idx = np.concatenate(order_h) if order_h else np.zeros(0, np.int64)
+    new_counts = np.repeat(counts, fp) * fq
+    crow2 = np.concatenate([[0], np.cumsum(new_counts)]).astype(np.int32)
+    col2 = ((col_h.astype(np.int64)[k_idx] * fq)[:, None] + np.arange(fq)[None]).reshape(-1)
+    nnz = values.shape[0]
+    v5 = values.reshape(nnz, fq, Q, fp, P).permute(0, 3, 1, 2, 4)   # (k, h, j, Q, P)
+    dev = values.device
+    vals2 = v5[torch.from_numpy(k_idx).to(dev), torch.from_numpy(h_idx).to(dev)]
+    return crow2, col2.astype(np.int32), vals2.reshape(-1, Q, P).contiguous()
+
+
+def reblock_rows(rows: np.ndarray, fp: int) -> np.ndarray:
+    """Kernel rows of the listed block-rows (each becomes fp consecutive rows)."""
+    rows = np.asarray(rows, dtype=np.int64)
+    return (rows[:, None] * fp + np.arange(fp)[None]).reshape(-1).astype(np.int32)

@@ -7,9 +7,12 @@ TileLang/CUDA JIT kernel:
 
     out_inplace[:, by·p:(by+1)·p] += Σ_blocks x[:, col·q:(col+1)·q] · values[blk]
 
-for each block-row `by` listed in `active_rows`; values are (nnz, q, p). The
-accumulator starts from out in fp32 and is stored once in out's dtype. Unlike the
-TileLang kernel, M needs no padding to a tile multiple.
+for each block-row `by` listed in `active_rows`; values are (nnz, q, p), p and q
+any multiples of 16 (square or not), as the TileLang kernel takes them
+(:59-63, :96-97). The accumulator starts from out in fp32 and is stored once in
+out's dtype. Unlike the TileLang kernel, M needs no padding to a tile multiple.
+Blocks wider than the kernels' tiles (p > 64, or q > 256) are cut exactly into
+sub-blocks once per structure (_reblock.py).
 
 The per-structure work plan (which workgroup sums which blocks) is built on the
 host the first time a given crow/col/active_rows triple is seen and cached on the
@@ -25,9 +28,12 @@ import weakref
 import numpy as np
 import torch
 
-from . import _lib, _runtime
+from . import _lib, _reblock, _runtime
 
-SUPPORTED_BLOCK_SIZES = (16, 32, 64)
+# Block sides the kernels take: multiples of 16 (tiles of 16, 32, 48 or 64
+# output features natively, wider blocks cut into those).
+BLOCK_MULTIPLE = 16
+SUPPORTED_BLOCK_SIZES = (16, 32, 48, 64)
 
 _TORCH_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
@@ -98,9 +104,10 @@ def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_by
         sp.plans[target_key] = plan
     pf = None
     lib = _lib.load()
-    if M >= lib.ssl_prefill_min_rows() and elem_bytes == 2 and plan.n_chunks > 0:
+    dt = _lib.SSL_BF16 if elem_bytes == 2 else _lib.SSL_F32
+    if lib.ssl_bsr_addmm_takes_prefill(M, block_p, block_q, dt) and plan.n_chunks > 0:
         # the prefill kernel's groups list the planned rows (active rows with blocks)
-        G = int(lib.ssl_prefill_group(M, plan.n_chunks, block_p))
+        G = int(lib.ssl_prefill_group(M, plan.n_chunks, block_p, block_q))
         pf = sp.plans.get(("pf", G))
         if pf is None:
             crow_h, _ = _validated_host_structure(crow, col, active_rows, values.shape[0], NB_K)
@@ -110,6 +117,27 @@ def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_by
             pf = _runtime.DevicePrefillPlan(groups, entries, ng, G, crow.device)
             sp.plans[("pf", G)] = pf
     return plan, pf
+
+
+_VIEW_ATTR = "_ssl_kernel_view"
+
+
+def _kernel_view(crow, col, values, active_rows, p, q, P, Q, NB_K):
+    """(crow, col, values, active_rows) of the same matrix in the (Q, P) blocks
+    the kernels run, cached on the values tensor while every input keeps its
+    identity and version. The structure is validated before it is cut."""
+    key = tuple((t.data_ptr(), t._version) for t in (crow, col, values, active_rows))
+    hit = getattr(values, _VIEW_ATTR, None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    crow_h, act_h = _validated_host_structure(crow, col, active_rows, values.shape[0], NB_K)
+    col_h = col.detach().to("cpu").numpy().astype(np.int32)
+    crow2, col2, vals2 = _reblock.reblock(crow_h, col_h, values.contiguous(), p, q, P, Q)
+    dev = values.device
+    view = (torch.from_numpy(crow2).to(dev), torch.from_numpy(col2).to(dev), vals2,
+            torch.from_numpy(_reblock.reblock_rows(act_h, p // P)).to(dev))
+    setattr(values, _VIEW_ATTR, (key, view))
+    return view
 
 
 _VPQ_ATTR = "_ssl_values_pq"
@@ -160,9 +188,9 @@ def bsr_addmm_inplace_(
         raise ValueError("all tensors must be on one ROCm GPU device")
     block_q = int(values.shape[1])
     block_p = int(values.shape[2])
-    if block_p != block_q or block_p not in SUPPORTED_BLOCK_SIZES:
+    if block_p % BLOCK_MULTIPLE or block_q % BLOCK_MULTIPLE or block_p == 0 or block_q == 0:
         raise ValueError(
-            f"The HIP BSR kernel needs square {SUPPORTED_BLOCK_SIZES} blocks, "
+            f"The HIP BSR kernel requires block dimensions divisible by {BLOCK_MULTIPLE}, "
             f"got {block_p}x{block_q}."
         )
     M, N = out_inplace.shape
@@ -177,6 +205,11 @@ def bsr_addmm_inplace_(
     NB_K = K // block_q
     if M == 0 or values.shape[0] == 0 or active_rows.numel() == 0:
         return
+    P, Q = _reblock.kernel_block_shape(block_p, block_q)
+    if (P, Q) != (block_p, block_q):
+        view = _kernel_view(crow_indices, col_indices, values, active_rows, block_p, block_q, P,
+                            Q, NB_K)
+        return bsr_addmm_inplace_(out_inplace, x, *view)
     plan, pf = _plan_for(crow_indices, col_indices, active_rows, values, NB_K, block_p, block_q,
                          M, out_inplace.element_size())
     if plan.n_chunks == 0:

@@ -12,6 +12,11 @@ is one call of `ssl_slr_forward` — one kernel launch that computes the latent
 t = x·Bᵀ and streams t·Aᵀ, the sparse term and the bias into one epilogue —
 instead of the reference's F.linear ×2 + BSR op + bias add (:124-137).
 
+Block shapes: any block whose sides are multiples of 16, square or not, as
+the reference's GPU class takes (:114-117). The kernels run p ∈ {16, 32, 48,
+64} output features by up to 256 input features natively; wider blocks are cut
+exactly into such sub-blocks once, in the module's kernel view (_reblock.py).
+
 Differences from the reference, all extensions:
   * fp32 runs on the GPU too (the TileLang class requires fp16/bf16, :118-119);
   * out/in features that are not multiples of the block (e.g. FFN 5461) are
@@ -31,9 +36,11 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import _lib, _runtime
+from . import _lib, _reblock, _runtime
 
-SUPPORTED_BLOCK_SIZES = (16, 32, 64)
+# The reference's CPU (AVX2) class takes these square blocks; CPU tensors with
+# any other block get its message (there is no CPU path here at all).
+CPU_BLOCK_SIZES = (8, 16, 32, 64)
 _LR_ONLY_BLOCK = 64  # output tile width when S is all zero
 
 
@@ -58,9 +65,11 @@ class _KernelState:
         self.dtype_code = _lib.dtype_code(dtype)
         self.elem = torch.empty((), dtype=dtype).element_size()
         n, m, r = mod.out_features, mod.in_features, mod.r
-        p = mod._kernel_block
-        self.p = p
-        self.NB = -(-n // p)
+        p, q = mod._kernel_block
+        self.p, self.q = p, q
+        # kernel block-rows: a stored block-row of bp features is bp / p kernel rows
+        bp = getattr(mod, "block_p", None) or p
+        self.NB = -(-n // bp) * (bp // p)
         self.n_pad = self.NB * p
         self.r_pad = _round_up(max(r, 1), 64)
         self.m_pad = _round_up(max(m, 1), 64)
@@ -83,6 +92,11 @@ class _KernelState:
             self.values = mod.S_values
             crow_h = mod.S_crow.detach().to("cpu").numpy().astype(np.int32)
             self.col_h = mod.S_col.detach().to("cpu").numpy().astype(np.int32)
+            bp, bq = mod.block_p, mod.block_q
+            if (bp, bq) != (p, q):  # cut into the (q, p) sub-blocks the kernels run
+                crow_h, self.col_h, self.values = _reblock.reblock(
+                    crow_h, self.col_h, mod.S_values, bp, bq, p, q)
+                self.col = torch.from_numpy(self.col_h).to(device)
             self.nblk_total = int(crow_h[-1])
         else:
             self.col = torch.zeros(1, dtype=torch.int32, device=device)
@@ -92,8 +106,10 @@ class _KernelState:
             self.nblk_total = 0
         self.crow_h = crow_h
         self.lr_units = self.r_pad // 32
-        self.block_q = p
-        self.NBK = -(-m // p)
+        self.block_q = q
+        # kernel block-columns: a stored block-column of bq features is bq / q of them
+        bq = getattr(mod, "block_q", None) or q
+        self.NBK = -(-m // bq) * (bq // q)
         self._plans: dict[int, _runtime.DevicePlan] = {}
         self._pf_plans: dict[int, _runtime.DevicePrefillPlan] = {}
         self._values_pq: torch.Tensor | None = None
@@ -151,7 +167,7 @@ class _KernelState:
         if self.s_format != 0:
             return False
         rows = self.NB if n_rows is None else n_rows
-        return bool(_lib.load().ssl_slr_takes_prefill(M, rows, self.p, self.dtype_code))
+        return bool(_lib.load().ssl_slr_takes_prefill(M, rows, self.p, self.q, self.dtype_code))
 
     def prefill_plan(self, G: int) -> _runtime.DevicePrefillPlan:
         """The prefill row kernel's plan with G block-rows per workgroup."""
@@ -202,7 +218,7 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
         ws_off = cnt_off = 0
         G = 0
         if st0.takes_prefill(M, sum(st.NB for st in states)):
-            G = int(lib.ssl_prefill_group(M, sum(st.NB for st in states), st0.p))
+            G = int(lib.ssl_prefill_group(M, sum(st.NB for st in states), st0.p, st0.q))
         for i, (st, pl, y) in enumerate(zip(states, plans, ys)):
             xch = pl.exchange(lib.ssl_slr_exchange_size(M, st.r_pad, st.m_pad, st.dtype_code))
             mb = members[i]
@@ -227,7 +243,7 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
             ws_off += ws_need[i]
             cnt_off += cnt_need[i]
         rc = lib.ssl_slr_forward_group(
-            x2.data_ptr(), x2.stride(0), M, st0.m, st0.m_pad, st0.p, st0.p, st0.dtype_code,
+            x2.data_ptr(), x2.stride(0), M, st0.m, st0.m_pad, st0.p, st0.q, st0.dtype_code,
             members, len(states), _lib.stream_ptr(x.device),
         )
         _lib.check(rc, "ssl_slr_forward_group")
@@ -254,7 +270,7 @@ class _LRSLinearBase(nn.Module):
     """Buffers and validation of ls_linear.py:7-44."""
 
     kind: str = ""
-    _kernel_block: int = _LR_ONLY_BLOCK
+    _kernel_block: tuple[int, int] = (_LR_ONLY_BLOCK, _LR_ONLY_BLOCK)  # (P, Q) the kernels run
 
     def __init__(self, A, B, *, in_features, out_features, bias=None) -> None:
         super().__init__()
@@ -333,7 +349,7 @@ class _LRSLinearLRBlockBase(_LRSLinearBase):
             )
         self.block_p = p
         self.block_q = q
-        self._kernel_block = p
+        self._kernel_block = _reblock.kernel_block_shape(p, q) if p % 16 == 0 and q % 16 == 0 else (p, q)
         self.S_nnz = int(S_sparse._nnz())
         crow = S_sparse.crow_indices()
         self.register_buffer("S_crow", crow.to(torch.int32).clone())
@@ -370,11 +386,8 @@ class _LRSLinearLRBlockHIP(_LRSLinearLRBlockBase):
         super().__init__(*args, **kwargs)
         if self.S_values.device.type != "cuda":
             raise ValueError("The HIP block kernel requires a ROCm GPU device.")
-        if self.block_p != self.block_q or self.block_p not in SUPPORTED_BLOCK_SIZES:
-            raise ValueError(
-                f"The HIP block kernel needs square blocks of size "
-                f"{SUPPORTED_BLOCK_SIZES}, got {self.block_p}x{self.block_q}."
-            )
+        if self.block_p % 16 or self.block_q % 16:
+            raise ValueError("The HIP block kernel requires block dimensions divisible by 16.")
         if self.S_values.dtype not in (torch.float16, torch.bfloat16, torch.float32):
             raise ValueError("The HIP block kernel requires fp16, bf16 or fp32.")
 
@@ -402,7 +415,7 @@ class _LRSLinearLRNMHIP(_LRSLinearBase):
         from .artifact import NM_BLOCK, nm24_pack
 
         packed = nm24_pack(S_dense.to(A.dtype))
-        self._kernel_block = NM_BLOCK
+        self._kernel_block = (NM_BLOCK, NM_BLOCK)
         self.block_p = self.block_q = None
         self.S_nnz = int(packed["blocks"].shape[0]) * NM_BLOCK * NM_BLOCK // 2
         self.register_buffer("_nm_crow", packed["crow"], persistent=False)
@@ -459,12 +472,14 @@ def LRSLinear(
         return _LRSLinearLRNMHIP(A, B, dense.to(A.device), **kwargs)
     if block_p is None or block_q is None:
         raise ValueError("Sparse S needs a recorded block shape to pick a kernel.")
-    if block_p != block_q or block_p not in SUPPORTED_BLOCK_SIZES:
-        raise ValueError(
-            f"The HIP kernel supports square {SUPPORTED_BLOCK_SIZES} blocks, "
-            f"got ({block_p}, {block_q})."
-        )
     if not A.is_cuda:
+        # The reference sends CPU tensors to its AVX2 class (square 8/16/32/64
+        # blocks, :265-273); this package has no CPU path at all.
+        if block_p != block_q or block_p not in CPU_BLOCK_SIZES:
+            raise ValueError(
+                f"The AVX2 kernel supports square {CPU_BLOCK_SIZES} blocks, "
+                f"got ({block_p}, {block_q}); this package runs none of them on the CPU."
+            )
         raise ValueError("The HIP kernels need A, B and S on a ROCm GPU device.")
     if S_sparse.layout == torch.strided:
         from .artifact import dense_to_bsr
@@ -502,8 +517,8 @@ class LRSLinearGroup(nn.Module):
                 raise ValueError("group members must share the sparse storage (2:4 or blocks)")
             if mod._kernel_block != first._kernel_block:
                 raise ValueError(
-                    f"group members must share the block size, got {first._kernel_block} and "
-                    f"{mod._kernel_block}"
+                    f"group members must share the kernel block shape, got {first._kernel_block} "
+                    f"and {mod._kernel_block}"
                 )
         self.members = nn.ModuleList(linears)
         self.in_features = first.in_features

@@ -16,36 +16,38 @@ def round_to(a: np.ndarray, dtype: torch.dtype) -> np.ndarray:
     return torch.from_numpy(np.asarray(a, dtype=np.float32)).to(dtype).double().numpy()
 
 
-def make_problem(n, m, r, p, density, dtype, seed=0, skew=False, bias=True, pad=False):
-    """A random SLR linear. With pad=True, n and m need not be multiples of p:
-    S is stored at the padded shape (ceil(n/p)·p, ceil(m/p)·p) with zero padding."""
+def make_problem(n, m, r, p, density, dtype, seed=0, skew=False, bias=True, pad=False, q=None):
+    """A random SLR linear with (p, q) blocks (q = p by default). With pad=True,
+    n and m need not be multiples of the block: S is stored at the padded shape
+    (ceil(n/p)·p, ceil(m/q)·q) with zero padding."""
+    q = p if q is None else q
     rng = np.random.default_rng(seed)
-    NB, NBK = -(-n // p), -(-m // p)
+    NB, NBK = -(-n // p), -(-m // q)
     if not pad:
-        assert n % p == 0 and m % p == 0
+        assert n % p == 0 and m % q == 0
     if skew:
         rows, cols = orc.zipf_block_structure(NB, NBK, density, rng)
     else:
         rows, cols = orc.random_block_structure(NB, NBK, density, rng)
-    vals = rng.standard_normal((len(rows), p, p)) * 0.02
+    vals = rng.standard_normal((len(rows), p, q)) * 0.02
     # zero the padded rows/columns of edge blocks
     for k, (br, bc) in enumerate(zip(rows, cols)):
         if (br + 1) * p > n:
             vals[k, n - br * p:, :] = 0
-        if (bc + 1) * p > m:
-            vals[k, :, m - bc * p:] = 0
+        if (bc + 1) * q > m:
+            vals[k, :, m - bc * q:] = 0
     vals = round_to(vals, dtype)
     crow, col, vals = orc.structure_to_bsr(rows, cols, NB, vals)
     A = round_to(rng.standard_normal((n, r)) * 0.02, dtype)
     B = round_to(rng.standard_normal((r, m)) * 0.02, dtype)
     b = round_to(rng.standard_normal(n) * 0.1, dtype) if bias else None
-    return dict(n=n, m=m, r=r, p=p, NB=NB, NBK=NBK, crow=crow, col=col, vals=vals, A=A, B=B,
-                bias=b, dtype=dtype, rng=rng)
+    return dict(n=n, m=m, r=r, p=p, q=q, NB=NB, NBK=NBK, crow=crow, col=col, vals=vals, A=A,
+                B=B, bias=b, dtype=dtype, rng=rng)
 
 
 def s_dense(prob) -> np.ndarray:
     full = orc.bsr_to_dense(prob["crow"], prob["col"], prob["vals"], prob["NB"] * prob["p"],
-                            prob["NBK"] * prob["p"])
+                            prob["NBK"] * prob["q"])
     return full[: prob["n"], : prob["m"]]
 
 
@@ -55,7 +57,7 @@ def sparse_bsr_tensor(prob, device) -> torch.Tensor:
         torch.from_numpy(prob["crow"]).to(device),
         torch.from_numpy(prob["col"]).to(device),
         torch.from_numpy(prob["vals"]).to(device=device, dtype=prob["dtype"]),
-        size=(prob["NB"] * p, prob["NBK"] * p),
+        size=(prob["NB"] * p, prob["NBK"] * prob["q"]),
     )
 
 
@@ -86,5 +88,5 @@ def make_module(prob, dev, bias=True):
         to_dev(prob["A"], dt, dev), to_dev(prob["B"], dt, dev), S,
         in_features=prob["m"], out_features=prob["n"],
         bias=to_dev(prob["bias"], dt, dev) if (bias and prob["bias"] is not None) else None,
-        block_p=prob["p"], block_q=prob["p"],
+        block_p=prob["p"], block_q=prob["q"],
     )

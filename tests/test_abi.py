@@ -285,8 +285,15 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
         a.update(kw)
         return lib.ssl_bsr_addmm_inplace(*a.values())
 
-    # unsupported block shape
-    assert op(p=8, q=8, N=8, K=8) == _lib.SSL_ERR_UNSUPPORTED and b"square" in lib.ssl_last_error()
+    # unsupported block shapes: sides not multiples of 16, tiles wider than 64,
+    # blocks deeper than 256 (the Python layer cuts those into sub-blocks first)
+    for p, q in ((8, 8), (16, 8), (80, 16), (128, 64), (64, 272), (64, 0)):
+        assert op(p=p, q=q, N=p, K=max(q, 16)) == _lib.SSL_ERR_UNSUPPORTED, (p, q)
+        assert b"output features" in lib.ssl_last_error()
+    # every supported shape gets past the shape check (then stops at N ≠ NB·p)
+    for p in (16, 32, 48, 64):
+        for q in (16, 32, 48, 64, 96, 256):
+            assert op(p=p, q=q, N=p + 1, K=q) == _lib.SSL_ERR_INVALID, (p, q)
     # N inconsistent with NB·p
     assert op(N=60) == _lib.SSL_ERR_INVALID
     # missing counters
@@ -297,11 +304,17 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     assert lib.ssl_prefill_min_rows() == 128
     # fused calls: streaming for small blocks up to 512 rows and for calls of
     # fewer than 100 block-rows at 128 rows; fp32 always streams
-    tp = lambda M, rows, p, dt=_lib.SSL_BF16: lib.ssl_slr_takes_prefill(M, rows, p, dt)
+    tp = lambda M, rows, p, dt=_lib.SSL_BF16, q=None: lib.ssl_slr_takes_prefill(
+        M, rows, p, p if q is None else q, dt)
     assert tp(127, 500, 64) == 0 and tp(128, 172, 64) == 1 and tp(128, 64, 64) == 0
     assert tp(129, 64, 64) == 1 and tp(512, 500, 32) == 0 and tp(513, 500, 32) == 1
     assert tp(300, 500, 16) == 0 and tp(2048, 64, 32) == 1 and tp(4096, 500, 64, _lib.SSL_F32) == 0
-    assert lib.ssl_prefill_group(4096, 172, 64) in (1, 4)
+    assert lib.ssl_prefill_group(4096, 172, 64, 64) in (1, 4)
+    # the prefill kernels take square 16/32/64 blocks; other shapes stream
+    assert tp(2048, 500, 32, q=64) == 0 and tp(2048, 500, 48) == 0
+    ap = lambda M, p, q, dt=_lib.SSL_BF16: lib.ssl_bsr_addmm_takes_prefill(M, p, q, dt)
+    assert ap(128, 64, 64) == 1 and ap(127, 64, 64) == 0 and ap(4096, 32, 64) == 0
+    assert ap(4096, 64, 64, _lib.SSL_F32) == 0
 
     # ssl_slr_forward with fake, aligned device pointers (every case below is
     # rejected on the host before any launch)
@@ -316,7 +329,7 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
         return lib.ssl_slr_forward(*a.values())
 
     assert slr(dtype=7) == _lib.SSL_ERR_UNSUPPORTED
-    assert slr(p=48, q=48) == _lib.SSL_ERR_UNSUPPORTED
+    assert slr(p=80, q=48) == _lib.SSL_ERR_UNSUPPORTED
     # lr_wgs inconsistent with r_pad, or more consuming workgroups than chunks
     assert slr(lr_wgs=0) == _lib.SSL_ERR_INVALID and b"lr_wgs" in lib.ssl_last_error()
     assert slr(lr_wgs=2) == _lib.SSL_ERR_INVALID and b"lr_wgs" in lib.ssl_last_error()

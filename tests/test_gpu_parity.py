@@ -56,10 +56,11 @@ def test_op_matches_reference_kernel_golden_outputs(name, gpu_device):
 
 
 def test_op_rejects_block_8(gpu_device):
+    """Block sides must be multiples of 16, as for the TileLang kernel."""
     c = make_case("reftest_b8")
     out = torch.from_numpy(c["out"].copy()).to(gpu_device)
     args = [torch.from_numpy(c[k]).to(gpu_device) for k in ("x", "crow", "col", "values_t", "active")]
-    with pytest.raises(ValueError, match="square"):
+    with pytest.raises(ValueError, match="divisible by 16"):
         _op(out, *args)
 
 
@@ -401,7 +402,7 @@ def test_group_with_low_rank_only_and_ragged_members(gpu_device):
                    in_features=200, out_features=72)
     sl = _module(prob, dev, bias=False)
     x = make_x(prob, 7)
-    with pytest.raises(ValueError, match="block size"):
+    with pytest.raises(ValueError, match="block shape"):
         ssalaad_amd.LRSLinearGroup(sl, lr)  # 32×32 blocks vs the low-rank-only tile
     grp = ssalaad_amd.LRSLinearGroup(sl, _module(prob, dev, bias=False))
     y1, y2 = grp(to_dev(x, dtype, dev).reshape(1, 7, 200))

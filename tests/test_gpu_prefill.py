@@ -43,7 +43,7 @@ def tile():
 
 
 def _group_of(M, rows, p):
-    return int(_lib.load().ssl_prefill_group(M, rows, p))
+    return int(_lib.load().ssl_prefill_group(M, rows, p, p))
 
 
 @pytest.mark.parametrize("dtype", DT16, ids=["bf16", "f16"])

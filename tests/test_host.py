@@ -29,11 +29,13 @@ def test_block_kernel_rejects_unsupported_block_shape():
                   block_p=8, block_q=16)
 
 
-@pytest.mark.parametrize("block", [8, 48])
-def test_block_sizes_without_a_kernel_are_rejected(block):
+@pytest.mark.parametrize("block,message", [(8, "GPU"), (48, "square"), (16, "GPU")])
+def test_cpu_tensors_get_the_reference_cpu_message_or_no_fallback(block, message):
+    """CPU tensors: blocks the reference's AVX2 class refuses get its "square"
+    message (ls_linear.py:265-273); the others find no CPU path here."""
     A, B = torch.randn(96, 4), torch.randn(4, 96)
     S = _block_sparse(96, 96, block, [(0, 0)])
-    with pytest.raises(ValueError, match="square"):
+    with pytest.raises(ValueError, match=message):
         LRSLinear(A, B, S.to_sparse_bsr(blocksize=(block, block)), in_features=96,
                   out_features=96, block_p=block, block_q=block)
 

@@ -101,19 +101,23 @@ def test_c_port_matches_live_reference_build_when_present():
 # -------------------------------------------- reference tests restated --
 
 
-@pytest.mark.parametrize("block", [8, 16, 32, 64])
-def test_oracle_bsr_addmm_matches_a_dense_matmul(block):
-    """tests/test_ssalaad.py:320-327, with torch's to_sparse_bsr building the buffers."""
+@pytest.mark.parametrize("p,q", [(8, 8), (16, 16), (32, 32), (64, 64), (16, 32), (32, 16),
+                                 (48, 48), (48, 16), (64, 48), (128, 32), (16, 512)])
+def test_oracle_bsr_addmm_matches_a_dense_matmul(p, q):
+    """tests/test_ssalaad.py:320-327, with torch's to_sparse_bsr building the
+    buffers: square blocks as the reference test has them, and the non-square
+    (p, q) blocks the reference's GPU op takes (addmm_inplace.py:59-63, 96-97:
+    values (nnz, q, p), p and q read separately). A transposed block, swapped
+    p/q or a wrong column stride fails the closed form x·Sᵀ."""
     g = torch.Generator().manual_seed(0)
-    S = torch.zeros(block * 4, block * 6)
+    S = torch.zeros(p * 4, q * 6)
     for br, bc in [(0, 1), (1, 0), (1, 3), (2, 5), (3, 2)]:
-        S[br * block:(br + 1) * block, bc * block:(bc + 1) * block] = torch.randn(
-            block, block, generator=g)
-    x = torch.randn(5, block * 6, generator=g)
-    bsr = S.to_sparse_bsr(blocksize=(block, block))
+        S[br * p:(br + 1) * p, bc * q:(bc + 1) * q] = torch.randn(p, q, generator=g)
+    x = torch.randn(5, q * 6, generator=g)
+    bsr = S.to_sparse_bsr(blocksize=(p, q))
     crow = bsr.crow_indices().to(torch.int32)
     got = orc.bsr_addmm_inplace(
-        np.zeros((5, block * 4)), x.numpy(), crow.numpy(), bsr.col_indices().to(torch.int32).numpy(),
+        np.zeros((5, p * 4)), x.numpy(), crow.numpy(), bsr.col_indices().to(torch.int32).numpy(),
         bsr.values().transpose(1, 2).contiguous().numpy(),
         (crow[1:] - crow[:-1]).nonzero().squeeze(-1).to(torch.int32).numpy())
     np.testing.assert_allclose(got, (x @ S.T).numpy(), rtol=0, atol=1e-4)
