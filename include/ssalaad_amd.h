@@ -57,8 +57,9 @@ const char* ssl_last_error(void);
  * reference counterpart). They exist so that tests can reach paths that a
  * healthy device never takes, with every kernel still ending normally:
  *   SSL_DEBUG_PREFILL_TILE      0: the library picks the prefill row tile;
- *                               1: always the narrow tile; 2: always the wide
- *                               tile (ssl_prefill_group follows it).
+ *                               1: always the narrow tile (128 token rows ×
+ *                               64 output features); 2: always the tall one
+ *                               (256 × 64).
  *   SSL_DEBUG_WAIT_POLLS        polls before a bounded wait gives up (0: the
  *                               default of several seconds).
  *   SSL_DEBUG_WAIT_UNREACHABLE  nonzero: every wait of the fused kernel targets
@@ -105,21 +106,31 @@ int ssl_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB
 
 /* Prefill plan (host side, integer only): the row kernels used for calls with
  * many token rows give one workgroup `group` block-rows at once (group · p =
- * 256 output columns) and walk the union of their block columns, so each tile
- * of x feeds every block of that column in the group. Groups are consecutive
- * runs of `group` listed rows (`rows` NULL = every row 0..NB-1).
- *   groups  (2 + group) int32 per group:  {entry_begin, entry_end, row_0 .. row_{group-1}}
+ * 128 or 64 output features) and walk the union of their block columns in
+ * steps of 64 columns, E = 64 / p union entries per step, so each tile of x
+ * feeds every block of that column in the group. Groups are consecutive runs of
+ * `group` listed rows (`rows` NULL = every row 0..NB-1).
+ *   groups  (2 + group) int32 per group:  {step_begin, step_end, row_0 .. row_{group-1}}
  *           (row −1: none; the last group may be short)
- *   entries (2 + group) int32 per entry:  {col, mask, blk_0 .. blk_{group-1}}
- *           in ascending column order; bit g of mask is set iff blk_g (the BSR
- *           block index of slot g's row at that column) is valid (else −1).
- * A repeated column within one row gets its own entry. Call once with NULL
- * outputs for the counts. group ∈ [1, 16]. The structure is checked as for
- * ssl_plan_build. */
+ *   steps   ssl_prefill_step_ints(p, group) int32 per step:
+ *           {mask, col_0 .. col_{E-1}, W[4][IB][E]}
+ *           col_e: first x column of entry e (−1 past the last entry);
+ *           W[w][i][e] = blk[e][(8·(w + 4i)) / p]: the BSR block index of that
+ *           slot's row at entry e's column, or −1 (IB = group·p / 32: the row
+ *           kernel's 4 waves each load IB runs of 8 weight rows per step, and
+ *           each finds its block indices in one place);
+ *           mask bit (h·group + g): slot g holds a block in the step's 32-column
+ *           half h (h = 0, 1). Entries ascend by column; a column repeated within
+ *           one row starts another entry. Padding words are −1.
+ * Call once with NULL outputs for the counts. p ∈ {16, 32, 64} and group · p =
+ * 64 (the row kernel's tiles; ssl_prefill_step_ints is 0 otherwise).
+ * The structure is checked as for ssl_plan_build. */
+int32_t ssl_prefill_step_ints(int32_t block_p, int32_t group);
 int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB,
-                           int64_t NBK, const int32_t* rows_host, int64_t n_rows, int32_t group,
-                           int32_t* groups_out, int64_t groups_capacity, int32_t* entries_out,
-                           int64_t entries_capacity, int64_t* n_groups, int64_t* n_entries);
+                           int64_t NBK, const int32_t* rows_host, int64_t n_rows, int32_t block_p,
+                           int32_t group, int32_t* groups_out, int64_t groups_capacity,
+                           int32_t* steps_out, int64_t steps_capacity, int64_t* n_groups,
+                           int64_t* n_steps);
 /* Calls with at least this many token rows and 16-bit activations run the
  * prefill kernels, which need a prefill plan built with this group size for
  * the call's M and row count (n_rows: the rows the plans list; for a grouped
@@ -150,7 +161,7 @@ int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_
  * 256 input features (square or not); dtype ∈ {f32, bf16, f16} for out, x and
  * values alike. `plan` is a device copy of a table from ssl_plan_build
  * (lr_units = 0). Calls for which ssl_bsr_addmm_takes_prefill(M, p, q, dtype)
- * is 1 run the prefill kernel instead: they need `pf_groups`/`pf_entries`
+ * is 1 run the prefill kernel instead: they need `pf_groups`/`pf_steps`
  * (device copies from ssl_prefill_plan_build with the same rows and group =
  * pf_group = ssl_prefill_group(M, rows, p, q)) and `values_pq`, the block
  * values in (nnz, p, q) order (each block transposed); other calls may pass
@@ -165,7 +176,7 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx,
                           const int32_t* col, const void* values, int64_t nnz,
                           const int32_t* plan, int64_t n_chunks, int64_t n_slots,
                           const void* values_pq, const int32_t* pf_groups,
-                          const int32_t* pf_entries,
+                          const int32_t* pf_steps,
                           int64_t pf_n_groups, int32_t pf_group, int64_t M, int64_t N,
                           int64_t K, int64_t NB, int32_t block_p, int32_t block_q,
                           int32_t dtype, int32_t* counters, int64_t n_counters,
@@ -255,9 +266,10 @@ typedef struct ssl_slr_member {
   void* workspace;
   int64_t workspace_bytes;
   /* prefill plan (ssl_prefill_plan_build with group = ssl_prefill_group(M,
-   * NB, p)): needed when M >= ssl_prefill_min_rows() and dtype is 16-bit */
+   * rows of every linear of the call, p, q)): needed when
+   * ssl_slr_takes_prefill is 1 for the call */
   const int32_t* pf_groups;
-  const int32_t* pf_entries;
+  const int32_t* pf_steps;
   int64_t pf_n_groups;
   int32_t pf_group;
   int64_t nnz;            /* stored blocks (length of col, first dim of values) */

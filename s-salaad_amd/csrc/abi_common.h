@@ -21,7 +21,7 @@ inline int tile_mt(int64_t M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
 
 // Test hooks set through ssl_debug_set (host-side values read at launch time).
 struct DebugKnobs {
-  int64_t prefill_group;  // 0: the library's choice; 1: narrow tiles; 2: wide tiles
+  int64_t prefill_group;  // 0: the library's choice; 1: narrow, 2: tall row tiles
   int64_t wait_polls;     // polls before a bounded wait gives up (0: the default)
   int64_t wait_unreachable;  // nonzero: every wait's target is out of reach
 };

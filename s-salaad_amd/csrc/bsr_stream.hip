@@ -181,7 +181,7 @@ int64_t ssl_bsr_addmm_workspace_size(int64_t M, int64_t NB, int32_t block_p, int
 int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, const int32_t* col,
                           const void* values, int64_t nnz, const int32_t* plan, int64_t n_chunks,
                           int64_t n_slots, const void* values_pq, const int32_t* pf_groups,
-                          const int32_t* pf_entries,
+                          const int32_t* pf_steps,
                           int64_t pf_n_groups, int32_t pf_group, int64_t M, int64_t N, int64_t K,
                           int64_t NB, int32_t block_p, int32_t block_q, int32_t dtype,
                           int32_t* counters, int64_t n_counters, void* workspace,
@@ -218,7 +218,7 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
   if (nnz < 0 || !slab_count_ok(nnz, block_q / (4 * stream_ke(dtype, block_q))))
     return fail(SSL_ERR_UNSUPPORTED, "too many blocks (%lld) for one call", (long long)nnz);
   if (ssl_bsr_addmm_takes_prefill(M, block_p, block_q, dtype)) {
-    if (!pf_groups || !pf_entries || pf_n_groups <= 0 || !values_pq)
+    if (!pf_groups || !pf_steps || pf_n_groups <= 0 || !values_pq)
       return fail(SSL_ERR_INVALID, "calls with %lld token rows need a prefill plan and (p, q) "
                   "ordered block values", (long long)M);
     if (pf_group != prefill_group(M, n_chunks, block_p, device_cus()))
@@ -226,6 +226,8 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
                   prefill_group(M, n_chunks, block_p, device_cus()));
     if (nnz < 0 || nnz * block_p * block_q * eb > 0x7fffffffLL)
       return fail(SSL_ERR_UNSUPPORTED, "block values beyond 2 GiB");
+    if (M * ldx * eb > 0x7fffffffLL || M * ldo * eb > 0x7fffffffLL)
+      return fail(SSL_ERR_UNSUPPORTED, "x or out beyond 2 GiB; split the call by tokens");
     PfArgs rows{};
     rows.x = x; rows.ldx = ldx; rows.M = (int)M; rows.m = (int)K; rows.m_pad = (int)K;
     rows.mode = PF_OP;
@@ -233,8 +235,9 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
     PfMember& pm = rows.mb[0];
     pm.y = out; pm.ldy = ldo; pm.values_pq = values_pq;
     pm.values_bytes = nnz * block_p * block_q * eb;
-    pm.groups = pf_groups; pm.entries = pf_entries; pm.n_groups = (int)pf_n_groups;
-    const int64_t T = (M + prefill_row_tile(pf_group) - 1) / prefill_row_tile(pf_group);
+    pm.groups = pf_groups; pm.steps = pf_steps; pm.n_groups = (int)pf_n_groups;
+    rows.bm = prefill_row_tile(M, n_chunks, pf_group, block_p, device_cus());
+    const int64_t T = (M + rows.bm - 1) / rows.bm;
     if (pf_n_groups * T > 0x7fffffffLL / 8) return fail(SSL_ERR_INVALID, "grid too large");
     rows.items = (int)(pf_n_groups * T);
     rows.off[1] = rows.items;
@@ -354,17 +357,19 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
     // kernel at every M.)
     const int cus = device_cus();
     PfArgs rows{}, lat{};
+    if (M * ldx * eb > 0x7fffffffLL)
+      return fail(SSL_ERR_UNSUPPORTED, "x beyond 2 GiB; split the call by tokens");
     rows.x = lat.x = x; rows.ldx = lat.ldx = ldx;
     rows.M = lat.M = (int)M; rows.m = lat.m = (int)m; rows.m_pad = lat.m_pad = (int)m_pad;
-    rows.rows = lat.rows = (int)((M + 63) / 64 * 64);
     rows.mode = PF_FUSED;
     rows.n = lat.n = n_members;
-    const int64_t T64 = (M + 63) / 64;
+    const int64_t T128 = (M + 127) / 128;  // latent token tiles
     // one group size for the whole call, from all members' rows together
     int64_t total_rows = 0;
     for (int i = 0; i < n_members; ++i)
       if (members[i].NB > 0) total_rows += members[i].n_chunks;
     const int G = prefill_group(M, total_rows, block_p, cus);
+    rows.bm = prefill_row_tile(M, total_rows, G, block_p, cus);
     int64_t items = 0, litems = 0;
     for (int i = 0; i < n_members; ++i) {
       const ssl_slr_member& mb = members[i];
@@ -372,18 +377,19 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       rows.off[i] = (int)items;
       lat.off[i] = (int)litems;
       if (mb.NB == 0) continue;
-      if (!mb.pf_groups || !mb.pf_entries || mb.pf_n_groups <= 0 || mb.pf_group != G ||
+      if (!mb.pf_groups || !mb.pf_steps || mb.pf_n_groups <= 0 || mb.pf_group != G ||
           (mb.nnz > 0 && !mb.values_pq))
         return fail(SSL_ERR_INVALID, "linear %d: calls with %lld token rows need a prefill plan "
                     "with group %d and (p, q) ordered block values", i, (long long)M, G);
-      const int64_t T = (M + prefill_row_tile(G) - 1) / prefill_row_tile(G);
+      const int64_t T = (M + rows.bm - 1) / rows.bm;
       if (mb.nnz < 0 || mb.nnz * block_p * block_p * eb > 0x7fffffffLL ||
-          mb.NB * block_p * mb.r_pad * eb > 0x7fffffffLL)
-        return fail(SSL_ERR_UNSUPPORTED, "linear %d: weights beyond 2 GiB", i);
+          mb.NB * block_p * mb.r_pad * eb > 0x7fffffffLL || M * mb.ldy * eb > 0x7fffffffLL ||
+          (int64_t)mb.r_pad * m_pad * eb > 0x7fffffffLL)
+        return fail(SSL_ERR_UNSUPPORTED, "linear %d: weights or output beyond 2 GiB", i);
       pm.y = mb.y; pm.ldy = mb.ldy; pm.A = mb.A; pm.lda = mb.r_pad;
       pm.A_bytes = mb.NB * block_p * mb.r_pad * eb; pm.bias = mb.bias;
       pm.values_pq = mb.values_pq; pm.values_bytes = mb.nnz * block_p * block_p * eb;
-      pm.groups = mb.pf_groups; pm.entries = mb.pf_entries; pm.n_groups = (int)mb.pf_n_groups;
+      pm.groups = mb.pf_groups; pm.steps = mb.pf_steps; pm.n_groups = (int)mb.pf_n_groups;
       pm.B = mb.B; pm.ldb = m_pad;
       pm.t = (char*)mb.workspace + L[i].t_final; pm.ldt = mb.r_pad;
       pm.tpart = (float*)((char*)mb.workspace + L[i].t_part);
@@ -391,7 +397,7 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       pm.ksplit = mb.r_pad > 0 ? prefill_latent_split(M, mb.r_pad, m_pad, cus) : 1;
       lat.mb[i] = pm;
       items += mb.pf_n_groups * T;
-      if (mb.r_pad > 0) litems += T64 * (mb.r_pad / 64) * pm.ksplit;
+      if (mb.r_pad > 0) litems += T128 * (mb.r_pad / 64) * pm.ksplit;
       if (items > 0x7fffffffLL / 8 || litems > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
     }
     rows.off[n_members] = (int)items;
@@ -405,7 +411,7 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       for (int i = 0; i < n_members; ++i) {
         comb.off[i] = (int)c;
         if (members[i].NB > 0 && members[i].r_pad > 0 && lat.mb[i].ksplit > 1)
-          c += (rows.rows * members[i].r_pad / 4 + 255) / 256;
+          c += (M * members[i].r_pad / 4 + 255) / 256;
       }
       comb.off[n_members] = (int)c;
       comb.combine_items = (int)c;

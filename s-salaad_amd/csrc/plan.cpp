@@ -181,22 +181,42 @@ int ssl_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB
   return SSL_OK;
 }
 
+// Step record layout (the prefill row kernel's load mapping): 4 waves, each
+// issuing IB = group·p / 32 loads of 8 weight rows per step; load i of wave w
+// covers features 8·(w + 4i) .. +7, i.e. slot (8·(w + 4i)) / p.
+static int32_t prefill_ib(int32_t block_p, int32_t group) {
+  return block_p * group == 64 ? 2 : 0;  // the row kernel's tiles are 64 features wide
+}
+
+int32_t ssl_prefill_step_ints(int32_t block_p, int32_t group) {
+  if (block_p <= 0 || 64 % block_p || group < 1 || group > 16) return 0;
+  const int32_t ib = prefill_ib(block_p, group);
+  if (ib == 0) return 0;
+  const int32_t E = 64 / block_p;
+  return (1 + E + 4 * ib * E + 3) / 4 * 4;
+}
+
 int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB,
-                           int64_t NBK, const int32_t* rows_host, int64_t n_rows, int32_t group,
-                           int32_t* groups_out, int64_t groups_capacity, int32_t* entries_out,
-                           int64_t entries_capacity, int64_t* n_groups, int64_t* n_entries) {
+                           int64_t NBK, const int32_t* rows_host, int64_t n_rows, int32_t block_p,
+                           int32_t group, int32_t* groups_out, int64_t groups_capacity,
+                           int32_t* steps_out, int64_t steps_capacity, int64_t* n_groups,
+                           int64_t* n_steps) {
   clear_error();
-  if (!crow_host || !n_groups || !n_entries || NB < 0 || group < 1 || group > 16 ||
+  const int32_t stride = ssl_prefill_step_ints(block_p, group);
+  if (!crow_host || !n_groups || !n_steps || NB < 0 || stride == 0 ||
       (rows_host && n_rows < 0) || (groups_out && groups_capacity < 0) ||
-      (entries_out && entries_capacity < 0))
+      (steps_out && steps_capacity < 0))
     return fail(SSL_ERR_INVALID, "invalid prefill plan arguments");
   if (int rc = check_structure(crow_host, col_host, NB, NBK, rows_host, n_rows)) return rc;
   const int64_t nr = rows_host ? n_rows : NB;
-  const int stride = 2 + group;
-  int64_t ng = 0, ne = 0;
+  const int E = 64 / block_p;  // union entries per 64-column step
+  const int gstride = 2 + group;
+  int64_t ng = 0, ns = 0;
   std::vector<std::array<int32_t, 3>> items;  // (col, slot, block)
+  std::vector<int32_t> ent;                   // entries of one group: (1 + group) each
   for (int64_t i0 = 0; i0 < nr; i0 += group) {
     items.clear();
+    ent.clear();
     int32_t rows[16];
     for (int g = 0; g < group; ++g) {
       rows[g] = -1;
@@ -207,42 +227,60 @@ int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, in
           items.push_back({col_host[k], g, k});
       }
     }
-    // merge by column; a slot already taken in the current entry (a repeated
-    // column within one row) starts a new entry with the same column
+    // union entries by column; a slot already taken in the current entry (a
+    // repeated column within one row) starts a new entry with the same column
     std::sort(items.begin(), items.end());
-    const int64_t e_begin = ne;
-    int32_t cur_col = -1, mask = 0;
-    int32_t* e = nullptr;
+    int32_t cur_col = -1, taken = 0;
     for (const auto& it : items) {
-      if (it[0] != cur_col || (mask >> it[1]) & 1) {
-        if (entries_out) {
-          if (ne >= entries_capacity) return fail(SSL_ERR_CAPACITY, "prefill entry capacity exceeded");
-          e = entries_out + ne * stride;
-          e[0] = it[0];
-          e[1] = 0;
-          for (int g = 0; g < group; ++g) e[2 + g] = -1;
-        }
-        ++ne;
+      if (it[0] != cur_col || (taken >> it[1]) & 1) {
+        ent.push_back(it[0]);
+        for (int g = 0; g < group; ++g) ent.push_back(-1);
         cur_col = it[0];
-        mask = 0;
+        taken = 0;
       }
-      mask |= 1 << it[1];
-      if (e) {
-        e[1] = mask;
-        e[2 + it[1]] = it[2];
+      taken |= 1 << it[1];
+      ent[ent.size() - group + it[1]] = it[2];
+    }
+    const int64_t n_ent = (int64_t)ent.size() / (1 + group);
+    const int64_t steps = (n_ent + E - 1) / E;
+    if (steps_out) {
+      if (ns + steps > steps_capacity) return fail(SSL_ERR_CAPACITY, "prefill step capacity exceeded");
+      for (int64_t st = 0; st < steps; ++st) {
+        int32_t* r = steps_out + (ns + st) * stride;
+        for (int32_t w = 0; w < stride; ++w) r[w] = -1;
+        int32_t mask = 0;
+        const int ib = prefill_ib(block_p, group);
+        for (int e = 0; e < E; ++e) {
+          const int64_t k = st * E + e;
+          if (k >= n_ent) continue;
+          const int32_t* en = &ent[(size_t)(k * (1 + group))];
+          r[1 + e] = en[0] * block_p;  // first x column of the entry
+          for (int g = 0; g < group; ++g) {
+            if (en[1 + g] < 0) continue;
+            // 32-column halves of the step this entry covers
+            const int h0 = (e * block_p) / 32, h1 = (e * block_p + block_p - 1) / 32;
+            for (int h = h0; h <= h1; ++h) mask |= 1 << (h * group + g);
+          }
+          // each wave's loads: blk[e][slot(w, i)] at 1 + E + (w·ib + i)·E + e
+          for (int w = 0; w < 4; ++w)
+            for (int i = 0; i < ib; ++i)
+              r[1 + E + (w * ib + i) * E + e] = en[1 + (8 * (w + 4 * i)) / block_p];
+        }
+        r[0] = mask;
       }
     }
     if (groups_out) {
       if (ng >= groups_capacity) return fail(SSL_ERR_CAPACITY, "prefill group capacity exceeded");
-      int32_t* gr = groups_out + ng * stride;
-      gr[0] = (int32_t)e_begin;
-      gr[1] = (int32_t)ne;
+      int32_t* gr = groups_out + ng * gstride;
+      gr[0] = (int32_t)ns;
+      gr[1] = (int32_t)(ns + steps);
       for (int g = 0; g < group; ++g) gr[2 + g] = rows[g];
     }
+    ns += steps;
     ++ng;
   }
   *n_groups = ng;
-  *n_entries = ne;
+  *n_steps = ns;
   return SSL_OK;
 }
 

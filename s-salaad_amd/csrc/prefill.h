@@ -22,14 +22,14 @@ struct PfMember {
   const void* bias;
   const void* values_pq;  // the block values in (nnz, p, q) order (k-contiguous per column)
   int64_t values_bytes;
-  const int32_t* groups;   // prefill plan: (2 + G) int32 per group
-  const int32_t* entries;  // prefill plan: (2 + G) int32 per union column
+  const int32_t* groups;  // prefill plan: (2 + G) int32 per group
+  const int32_t* steps;   // prefill plan: ssl_prefill_step_ints(p, G) int32 per step
   int n_groups;
   const void* B;        // [r_pad][m_pad]
   int64_t ldb;
-  void* t;              // latent [rows][r_pad], activation dtype
+  void* t;              // latent [M][r_pad], activation dtype
   int64_t ldt;
-  float* tpart;         // latent split partials [ksplit][rows][r_pad], fp32
+  float* tpart;         // latent split partials [ksplit][M][r_pad], fp32
   int r_pad;
   int ksplit;           // latent: K splits of this member
 };
@@ -38,26 +38,27 @@ struct PfArgs {
   const void* x;
   int64_t ldx;
   int M, m, m_pad;
-  int rows;             // latent rows: roundup(M, 64)
   int mode;             // PF_OP: y += x·Sᵀ on planned rows; PF_FUSED: the SLR linear
   int n;                // members
   int items;            // workgroups that do work
+  int bm;               // rows kernels: token rows per tile (prefill_row_tile)
   int combine_items;    // latent combine: workgroups
   int off[5];           // first item of each member
   PfMember mb[4];
 };
 
-// Block-rows per row-kernel workgroup: 256 / p when that still gives every CU
-// a workgroup, else 1.
+// Row-kernel tiles (token rows × output features): narrow 128 × 64, tall
+// 256 × 64 and wide 256 × 128; a workgroup owns BN / p block-rows.
+// Block-rows per row-kernel workgroup (64/p or 128/p).
 int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus);
-// Token rows per row-kernel workgroup for that group size (128 or 64).
-int prefill_row_tile(int group);
-// K splits of the latent GEMM (about two workgroups per CU, ≥ 4 units each, ≤ 16).
+// Token rows per row-kernel workgroup (128 or 256) for that group size.
+int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus);
+// K splits of the latent GEMM (about one workgroup per CU, ≥ 4 steps each, ≤ 16).
 int prefill_latent_split(int64_t M, int64_t r_pad, int64_t m_pad, int n_cus);
 
 // The fused SLR linear: the latent GEMM (`lat`, K split over lat.ksplit), its
 // combine (`comb`, when split) and the row GEMM (`rows`), in that order on
-// `stream`. dtype: SSL_BF16 or SSL_F16; P ∈ {16, 32, 64}; G = 1 or 256/P.
+// `stream`. dtype: SSL_BF16 or SSL_F16; P ∈ {16, 32, 64}; G = 128/P or 64/P.
 hipError_t prefill_launch_fused(int dtype, int P, int G, const PfArgs& rows, const PfArgs& lat,
                                 const PfArgs& comb, hipStream_t stream);
 // The in-place op: the row GEMM only (rows.mode = PF_OP).

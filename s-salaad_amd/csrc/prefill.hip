@@ -1,26 +1,42 @@
 // Prefill-shaped SLR linear on gfx950: many token rows (M ≥ kPrefillMinM), 16-bit
-// activations. Two LDS-tiled MFMA kernels instead of the row-streaming decode
+// activations. Two LDS-tiled MFMA GEMM kernels replace the row-streaming decode
 // kernel (which re-reads each weight row once per 64-token tile):
 //
-//   latent  t[M, r_pad] = x · Bᵀ                   dense GEMM, rounded once to
-//                                                    the activation dtype (as F.linear)
+//   latent  t[M, r_pad] = x · Bᵀ                  dense GEMM (K split, fp32
+//                                                   partials summed in split order),
+//                                                   rounded once to the activation
+//                                                   dtype, as F.linear's output is
 //   rows    y[:, row] = Σ_blocks x[:, col·p:+p] · V_blockᵀ + t · A[row·p:+p, :]ᵀ
 //                       (+ bias, or + the old out for the in-place op)
 //
-// Both run one engine: a workgroup of 4 waves owns a BM × BN output tile (BM =
-// 64·MTW token rows, wave w the rows [16·MTW·w, +16·MTW)) and walks a list of
-// K units of width KU. Each unit stages an A tile (BM × KU, from x or t) and a
-// B tile (BN × KU, k-contiguous per output column) in LDS, double buffered:
-// the next units' global loads are in flight while the current one feeds the
-// MFMAs. Every B tile is copied as k-contiguous rows: sparse blocks come from a
-// (p, q)-ordered copy of the block values (made once per weight), low-rank and
-// latent units from the rows of A or B.
+// One engine runs both. A workgroup (4 waves) owns a BM × BN output tile and
+// walks a list of steps, each 64 columns of k. A step stages an A tile (BM × 64
+// of x or t) and a B tile (BN × 64 of weights, k-contiguous per output feature)
+// in LDS; wave (wm, wn) multiplies its TM × TN share with v_mfma_f32_16x16x32.
+// Tiles go from global memory straight into LDS (buffer loads with the lds
+// flag) through a ring of S stages: the loads of the next S − 1 steps are in
+// flight while one step computes, with one barrier per step.
 //
-// Token rows past M read row M − 1 (their outputs are never stored), so the
-// only masked loads are x columns past in_features in a ragged last unit.
-// Row workgroups are ordered XCD-major, token tile by token tile: the
-// workgroups one XCD runs at a time share a token tile, so its x panel stays in
-// that XCD's L2 while the block-rows stream past it.
+// Sparse steps. The row kernel gives a workgroup G = BN / p block-rows ("slots")
+// and walks the union of their block columns, 64 / p union entries per step (the
+// plan: ssl_prefill_plan_build). A step record holds a presence mask, the first
+// x column of each entry and, per entry and slot, the BSR block index (−1 when
+// the slot's row has no block there), laid out so that each wave's words are
+// contiguous. Each wave loads its view of a record (one word per lane) into LDS
+// S steps ahead of the tile loads that use it; a lane then reads the column and
+// block indices of its own chunks with ordinary LDS loads. An absent block or
+// entry loads from a buffer offset past the resource, which returns zeros with
+// no memory traffic, and the MFMAs of a slot absent from a 32-column half of
+// the step are skipped (a wave-uniform branch on the mask). The low-rank units
+// follow the sparse steps: t's 64-rank slices against the slots' rows of A.
+//
+// Rows of x past M read row M − 1 (their outputs are never stored). Columns of x
+// past in_features (a ragged last block column) are zeroed in LDS once the
+// stage has landed. Workgroups are ordered XCD-major, token tile by token tile:
+// the workgroups one XCD runs at a time share a token tile, so its x panel stays
+// in that XCD's L2 while the weights stream past it (each weight block is read
+// by every XCD at about the same time, so the 256 MB MALL serves all but the
+// first read).
 
 #include "abi_internal.h"
 #include "prefill.h"
@@ -32,378 +48,463 @@ namespace {
 
 constexpr int kPfThreads = 256;  // 4 waves
 constexpr int kXcds = 8;
-
-template <int DT>
-__device__ __forceinline__ typename Mma<DT, 8>::Frag lds_frag8(const uint16_t* p) {
-  const uint4 v = *(const uint4*)p;
-  typename Mma<DT, 8>::Frag f;
-  f.d[0] = v.x; f.d[1] = v.y; f.d[2] = v.z; f.d[3] = v.w;
-  return f;
-}
-template <int DT>
-__device__ __forceinline__ typename Mma<DT, 4>::Frag lds_frag4(const uint16_t* p) {
-  const uint2 v = *(const uint2*)p;
-  typename Mma<DT, 4>::Frag f;
-  f.d[0] = v.x; f.d[1] = v.y;
-  return f;
-}
-
-// Buffer-resource loads: an offset at or past the resource's size reads as
-// zero with no memory access, so absent blocks need no branch and no traffic.
+constexpr int kK = 64;           // k per step
 constexpr uint32_t kOob = 0x80000000u;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t mk_rsrc(const void* base, int64_t bytes) {
-  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (int)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
-__device__ __forceinline__ uint4 ld16_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-  return make_uint4(u[0], u[1], u[2], u[3]);
-}
 
-template <int DT, int KE>
-__device__ __forceinline__ typename Mma<DT, KE>::Frag zero_past(typename Mma<DT, KE>::Frag f,
-                                                                 int k0, int kmax) {
-  // elements k0 + e (e < KE) at or past kmax read as zero
+enum : int { K_ROWS_OP = 0, K_ROWS_FUSED = 1, K_LATENT = 2 };
+
+// 16-byte chunk with its 16-bit elements at and past `valid` set to zero.
+__device__ __forceinline__ uint4 keep_first(uint4 v, int valid) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int d = 0; d < KE / 2; ++d) {
-    const uint32_t lo = (k0 + 2 * d < kmax) ? (f.d[d] & 0xffffu) : 0u;
-    const uint32_t hi = (k0 + 2 * d + 1 < kmax) ? (f.d[d] & 0xffff0000u) : 0u;
-    f.d[d] = lo | hi;
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t lo = (2 * d < valid) ? (w[d] & 0xffffu) : 0u;
+    const uint32_t hi = (2 * d + 1 < valid) ? (w[d] & 0xffff0000u) : 0u;
+    w[d] = lo | hi;
   }
-  return f;
+  return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// Tile geometry. A workgroup owns BM = 64·MTW token rows (wave w: the rows
-// [16·MTW·w, +16·MTW)) and G block-rows of p columns ("slots"). A unit is one
-// K step of width p: the A tile (x or t columns, each wave its own rows, straight
-// into registers) and the B tiles of the G slots (p × p each, through LDS, shared
-// by the 4 waves).
-template <int DT, int P, int G, int MTW>
-struct Geo {
-  static constexpr int KU = P, W = P / 16, KP = P + 8;
-  static constexpr int KE = P >= 32 ? 8 : 4;
-  static constexpr int KM = Mma<DT, KE>::KM;
-  static constexpr int NKS = P / KM;
-  static constexpr int CHUNKS = G * P * P / 8;  // 16-byte pieces of the G B tiles
-  static constexpr int NLD = (CHUNKS + kPfThreads - 1) / kPfThreads;
+template <int BM, int BN, int WM, int WN>
+struct Tile {
+  static_assert(WM * WN == 4, "four waves");
+  static constexpr int TM = BM / WM, TN = BN / WN;
+  static constexpr int MTI = TM / 16, NTI = TN / 16;
+  static constexpr int IA = BM / 32;  // A loads per wave per step (8 rows × 128 B each)
+  static constexpr int IB = BN / 32;  // B loads per wave per step
+  static constexpr int LDS = (BM + BN) * kK;  // elements per LDS stage (rows of 128 bytes)
 };
 
-template <int DT, int P, int G, int MTW>
-struct Stage {
-  using Gm = Geo<DT, P, G, MTW>;
-  typename Mma<DT, Gm::KE>::Frag a[MTW][Gm::NKS];
-  uint4 b[Gm::NLD];
-  int mask;
-};
-
-// Where one unit's tiles come from (all wave-uniform).
-template <int G>
-struct Unit {
-  const uint16_t* a;  // A source: row-major, row stride lda, unit columns [ka, ka + p)
-  int64_t lda;
-  int ka;
-  int kmax;           // A columns at and past kmax read as zero (in_features for x)
-  int kread;          // last column a full fragment may start at (row length − KE)
-  __amdgpu_buffer_rsrc_t br;  // B source
-  uint32_t base[G];   // per slot: byte offset of its p × p tile in br, kOob if absent
-  uint32_t bld;       // bytes between the k-contiguous rows [col][k] of a tile
-  int mask;           // slots present
-};
-
-// LDS row of B-tile column j: column W·c + s at row 16·s + c, so the 16 lanes
-// reading one column tile hit 16 consecutive rows (no bank conflict) while a
-// lane still owns W adjacent output columns in the epilogue.
-template <int P>
-__device__ __forceinline__ int brow(int j) {
-  constexpr int W = P / 16;
-  return 16 * (j % W) + j / W;
+__device__ __forceinline__ int ld_word(const int32_t* p, int i) {
+  return __builtin_amdgcn_readfirstlane(ld_uniform(p, i));
 }
 
-template <int G>
-__device__ __forceinline__ uint32_t slot_base(const Unit<G>& u, int g) {
-  uint32_t v = kOob;
+// word base + k·stride_k of `rec` for k = sel (0 ≤ sel < N, per lane): scalar
+// loads and a chain of selects (no local array, which a per-lane index would
+// place in scratch memory)
+template <int N>
+__device__ __forceinline__ int pick_word(const int32_t* rec, int base, int stride_k, int sel) {
+  int x = ld_word(rec, base);
 #pragma unroll
-  for (int q = 0; q < G; ++q) v = (g == q) ? u.base[q] : v;
-  return v;
-}
-
-template <int DT, int P, int G, int MTW>
-__device__ __forceinline__ void load_unit(const Unit<G>& u, int m0, int M, int wid, int lane,
-                                          Stage<DT, P, G, MTW>& st) {
-  using Gm = Geo<DT, P, G, MTW>;
-  constexpr int KE = Gm::KE;
-  const int c = lane & 15, gq = lane >> 4;
-#pragma unroll
-  for (int mt = 0; mt < MTW; ++mt) {
-    const int row = min(m0 + wid * 16 * MTW + mt * 16 + c, M - 1);
-    const uint16_t* rp = u.a + (int64_t)row * u.lda;
-#pragma unroll
-    for (int ks = 0; ks < Gm::NKS; ++ks) {
-      const int k = u.ka + ks * Gm::KM + KE * gq;
-      const auto f = load_kfrag_full<DT, KE>(rp, min(k, u.kread));
-      st.a[mt][ks] = (k + KE <= u.kmax) ? f : zero_past<DT, KE>(f, k, u.kmax);
-    }
+  for (int k = 1; k < N; ++k) {
+    const int v = ld_word(rec, base + k * stride_k);
+    x = (sel == k) ? v : x;
   }
-  const int tid = threadIdx.x;
-  constexpr int PER = P * P / 8;   // pieces per tile
-  constexpr int CPR = P / 8;       // pieces per tile row
-#pragma unroll
-  for (int i = 0; i < Gm::NLD; ++i) {
-    const int q = tid + kPfThreads * i;
-    const int g = q / PER, r = q % PER;
-    const int j = r / CPR, kc = (r % CPR) * 8;
-    const uint32_t off =
-        (q < Gm::CHUNKS ? slot_base(u, g) : kOob) + (uint32_t)j * u.bld + (uint32_t)(kc * 2);
-    st.b[i] = ld16_buf(u.br, off);
-  }
-  st.mask = u.mask;
+  return x;
 }
 
-template <int DT, int P, int G, int MTW>
-__device__ __forceinline__ void store_b(const Stage<DT, P, G, MTW>& st, uint16_t* sb) {
-  using Gm = Geo<DT, P, G, MTW>;
-  constexpr int KP = Gm::KP;
-  constexpr int PER = P * P / 8, CPR = P / 8;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < Gm::NLD; ++i) {
-    const int q = tid + kPfThreads * i;
-    if (Gm::CHUNKS % kPfThreads == 0 || q < Gm::CHUNKS) {
-      const int g = q / PER, r = q % PER;
-      const int j = r / CPR, kc = (r % CPR) * 8;
-      *(uint4*)(sb + (g * P + brow<P>(j)) * KP + kc) = st.b[i];
-    }
-  }
+// A buffer resource as four SGPRs (base, no stride, size in bytes; loads at
+// offsets past the size read zeros), for the direct-to-LDS loads below.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, int64_t bytes) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint32_t n = bytes > 0x7fffffffLL ? 0x7fffffffu : (uint32_t)bytes;
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32) & 0xffffu);
+  r[2] = __builtin_amdgcn_readfirstlane(n);
+  r[3] = 0x00020000u;
+  return r;
 }
 
-// MFMAs of one unit for the slots present: A fragments from the stage
-// registers, B from LDS; acc[g][mt][s] (column tile s, lane column c → column W·c + s).
-template <int DT, int P, int G, int MTW>
-__device__ __forceinline__ void compute_unit(const Stage<DT, P, G, MTW>& st, const uint16_t* sb,
-                                             int lane, f32x4 (&acc)[G][MTW][P / 16]) {
-  using Gm = Geo<DT, P, G, MTW>;
-  constexpr int KE = Gm::KE, W = Gm::W, KP = Gm::KP;
-  using MM = Mma<DT, KE>;
-  const int c = lane & 15, gq = lane >> 4;
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if ((st.mask >> g) & 1) {
-#pragma unroll
-      for (int ks = 0; ks < Gm::NKS; ++ks) {
-        const int k = ks * Gm::KM + KE * gq;
-        typename MM::Frag bf[W];
-#pragma unroll
-        for (int s = 0; s < W; ++s) {
-          const uint16_t* p = sb + (g * P + 16 * s + c) * KP + k;
-          if constexpr (KE == 8) bf[s] = lds_frag8<DT>(p);
-          else bf[s] = lds_frag4<DT>(p);
-        }
-#pragma unroll
-        for (int mt = 0; mt < MTW; ++mt)
-#pragma unroll
-          for (int s = 0; s < W; ++s) MM::run(acc[g][mt][s], st.a[mt][ks], bf[s]);
-      }
-    }
-  }
+// Global memory straight into LDS, 16 bytes per lane: lane l of the wave
+// writes LDS byte address lds + 16·l, so one instruction fills 1 KiB. The byte
+// offset is voff (per lane) + soff
+// (uniform); every use keeps soff inside the buffer, so the zero-fill of a
+// lane rests on voff alone (an absent block or chunk: voff ≥ 2^31). Issued as
+// inline assembly so that the compiler neither tracks these LDS writes nor
+// inserts its own waits for them: the engine waits with explicit vmcnt counts
+// (every load of the loop is unconditional, so the counts are exact) and
+// orders LDS access with explicit barriers. No memory clobber: the waits and
+// barriers that order LDS access around these loads are compiler barriers
+// themselves.
+__device__ __forceinline__ void dma16(const u32x4& r, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p);
 }
 
-// The unit pipeline: D units in flight in registers (a ring whose slot k
-// always holds a unit ≡ k mod D, a constant once the loop is unrolled); the B
-// tiles of the unit being computed sit in one LDS buffer while the next unit's
-// are written to the other. A unit's loads are issued D units before its MFMAs.
-// Units past the end load the last unit again (never computed), so every load
-// is unconditional and each wait covers exactly the loads it needs.
-template <int DT, int P, int G, int MTW, int D, typename UnitFn>
-__device__ __forceinline__ void run_units(const UnitFn& unit, int U, int m0, int M, uint16_t* sb0,
-                                          uint16_t* sb1, int wid, int lane,
-                                          f32x4 (&acc)[G][MTW][P / 16]) {
-  if (U <= 0) return;
-  Stage<DT, P, G, MTW> st[D];
-#pragma unroll
-  for (int k = 0; k < D; ++k) load_unit<DT, P, G, MTW>(unit(min(k, U - 1)), m0, M, wid, lane, st[k]);
-  store_b<DT, P, G, MTW>(st[0], sb0);
-  __syncthreads();
-  for (int u0 = 0; u0 < U; u0 += D) {
-#pragma unroll
-    for (int k = 0; k < D; ++k) {
-      const int u = u0 + k;
-      const int s = (k + 1) % D;  // holds unit u + 1
-      if (u < U) {
-        compute_unit<DT, P, G, MTW>(st[k], (u & 1) ? sb1 : sb0, lane, acc);
-        if (u + 1 < U) store_b<DT, P, G, MTW>(st[s], (u & 1) ? sb0 : sb1);
-      }
-      load_unit<DT, P, G, MTW>(unit(min(u + D, U - 1)), m0, M, wid, lane, st[k]);
-      __syncthreads();
-    }
-  }
+// s_waitcnt vmcnt(n) / lgkmcnt(0), also compiler barriers for memory accesses
+// (LDS reads of data a direct-to-LDS load wrote must stay after the wait).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Workgroup barrier that is also a compiler barrier for memory accesses. It
+// first waits for this wave's LDS reads (the stage the next loads overwrite
+// was read by the previous step's fragment loads); loads are waited for
+// explicitly.
+__device__ __forceinline__ void barrier_only() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// XCD-major work order: blocks b, b + 8, b + 16, ... run on one XCD, so the
-// items one XCD holds at a time are consecutive (one token tile: its x panel
-// stays in that XCD's L2 while the block-rows stream past).
-__device__ __forceinline__ int xcd_item(int items) {
-  const int b = blockIdx.x;
-  const int per_xcd = (items + kXcds - 1) / kXcds;
-  return (b % kXcds) * per_xcd + b / kXcds;
+// LDS layout of a stage: rows of 64 elements (128 bytes), A rows first, then
+// B rows. The 16-byte chunk kc of row R sits at position kc ^ (R % 8) of the
+// row, so the 8 rows one load instruction fills and the 16 rows one fragment
+// read covers spread over all banks without padding (which the 1 KiB
+// contiguous direct-to-LDS writes cannot skip).
+__device__ __forceinline__ int lds_chunk(int R, int kc) { return R * kK + ((kc ^ (R & 7)) << 3); }
+
+// Workgroups per compute unit that the stages' LDS allows (160 KiB per CU).
+constexpr int pf_occupancy(int BM, int BN, int S) {
+  return (160 * 1024) / ((BM + BN) * kK * 2 * S) > 4 ? 4 : (160 * 1024) / ((BM + BN) * kK * 2 * S);
 }
 
 // ---------------------------------------------------------------------------
-// Row kernel: one workgroup per (token tile, group of G block-rows).
+// The engine. KIND: K_ROWS_OP / K_ROWS_FUSED (rows of the block-sparse linear)
+// or K_LATENT (t = x·Bᵀ). P: block size (rows kernels). S: LDS stages (loads
+// of S − 1 steps in flight while one step computes).
+//
+// Every kernel argument the step loop uses is read into a register before the
+// loop: the loop's waits and barriers are compiler barriers for memory, which
+// would otherwise reload them from the argument segment every step.
 // ---------------------------------------------------------------------------
-template <int DT, int P, int G, int MTW, int D>
-__global__ __launch_bounds__(kPfThreads, 2) void pf_rows_kernel(PfArgs by_value) {
+template <int DT, int KIND, int P, int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
+    PfArgs by_value) {
   (void)by_value;
   const PfArgs& a = *(const PfArgs*)__builtin_amdgcn_kernarg_segment_ptr();
-  using Gm = Geo<DT, P, G, MTW>;
-  constexpr int BM = 64 * MTW, W = Gm::W, KP = Gm::KP, EB = 2;
-  __shared__ __align__(16) uint16_t sb[2][G * P * KP];
+  using T = Tile<BM, BN, WM, WN>;
+  constexpr int IA = T::IA, IB = T::IB, MTI = T::MTI, NTI = T::NTI;
+  constexpr bool ROWS = KIND != K_LATENT;
+  constexpr int G = ROWS ? BN / P : 1;
+  constexpr int E = ROWS ? 64 / P : 1;
+  constexpr int EB = 2;
+  constexpr int kRecInts = (1 + E + 4 * IB * E + 3) / 4 * 4;  // ssl_prefill_step_ints(P, G)
+  constexpr int LOADS = IA + IB;    // tile load instructions per wave per step
+  // loads issued after a step's tile loads by the time that step is waited
+  // on: the tile loads of the S − 2 later steps
+  constexpr int kWait = (S - 2) * LOADS;
+  // the rows kernels' record loads rely on every load being waited for at
+  // each step
+  static_assert(!ROWS || S == 2, "rows kernels run two stages");
+  constexpr int NRV = 1 + E + IB * E;  // words of a wave's record view
+  static_assert(NRV <= 64, "a record view is one word per lane");
+  using MM = Mma<DT, 8>;
+  using Frag = typename MM::Frag;
+  __shared__ __align__(1024) uint16_t lds[S][T::LDS];
 
-  const int item = xcd_item(a.items);
-  if (item >= a.items) return;
-  int i = 0;
-  while (i + 1 < a.n && item >= a.off[i + 1]) ++i;
-  const PfMember& mb = a.mb[i];
-  const int local = item - a.off[i];
-  const int tt = local / mb.n_groups, grp = local % mb.n_groups;
-  const int m0 = tt * BM;
-  const int32_t* gr = mb.groups + (int64_t)grp * (2 + G);
-  const int e0 = gr[0], e1 = gr[1];
-  int rowmask = 0;
-#pragma unroll
-  for (int g = 0; g < G; ++g) rowmask |= (gr[2 + g] >= 0) << g;
-  const int nsp = e1 - e0;
-  const int nlr = (a.mode == PF_FUSED) ? mb.r_pad / P : 0;
-  const int U = nsp + nlr;
-  const auto vr = mk_rsrc(mb.values_pq, mb.values_bytes);
-  const auto ar = mk_rsrc(mb.A, mb.A_bytes);
+  // ---- which tile
+  const int items = (KIND == K_LATENT) ? (int)gridDim.x : a.items;
+  int item;
+  if constexpr (KIND == K_LATENT) {
+    item = blockIdx.x;
+  } else {  // XCD-major order
+    const int b = blockIdx.x;
+    const int per_xcd = (items + kXcds - 1) / kXcds;
+    item = (b % kXcds) * per_xcd + b / kXcds;
+    if (item >= items) return;
+  }
+  int mi = 0;
+  while (mi + 1 < a.n && item >= a.off[mi + 1]) ++mi;
+  const PfMember& mb = a.mb[mi];
+  const int local = item - a.off[mi];
+  const int M = a.M, m = a.m;
 
-  auto unit = [&](int u) {
-    Unit<G> s;
-    if (u < nsp) {
-      const int32_t* e = mb.entries + (int64_t)(e0 + u) * (2 + G);
-      s.a = (const uint16_t*)a.x; s.lda = a.ldx; s.ka = e[0] * P; s.kmax = a.m;
-      s.kread = (int)a.ldx - Gm::KE;
-      s.br = vr; s.bld = P * EB; s.mask = e[1];
+  int m0, s_begin, s_end;            // token tile; step range
+  int n_sp = 0;                      // sparse steps (rows kernels)
+  const int32_t* gr = nullptr;       // group record: {step_begin, step_end, rows[G]}
+  int rt = 0, kspl = 0;              // latent: rank tile, K split
+  if constexpr (KIND == K_LATENT) {
+    const int n_rt = mb.r_pad / BN;
+    kspl = local % mb.ksplit;
+    const int tile = local / mb.ksplit;
+    rt = tile % n_rt;
+    m0 = (tile / n_rt) * BM;
+    const int units = a.m_pad / kK;
+    const int ku = (units + mb.ksplit - 1) / mb.ksplit;
+    s_begin = kspl * ku;
+    s_end = min(s_begin + ku, units);
+  } else {
+    const int tt = local / mb.n_groups, grp = local % mb.n_groups;
+    m0 = tt * BM;
+    gr = mb.groups + (int64_t)grp * (2 + G);
+    s_begin = ld_word(gr, 0);
+    n_sp = ld_word(gr, 1) - s_begin;
+    const int n_lr = (KIND == K_ROWS_FUSED) ? mb.r_pad / kK : 0;
+    s_end = s_begin + n_sp + n_lr;
+  }
+  const int U = s_end - s_begin;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wid / WN, wn = wid % WN;
+  // This lane loads, in every tile load instruction, row (8·instr_row + lane / 8)
+  // and the column chunk that lands at position lane % 8 of that row.
+  const int lrow = lane >> 3;
+  const int kc = (lane & 7) ^ lrow;
+  const int e_t = (ROWS && E > 1) ? (kc * 8) / P : 0;  // rows kernels: this lane's entry of a step
+  const int kin = ROWS ? (kc * 8) % P : kc * 8;  // and its column within the entry
+
+  // ---- LDS byte addresses: stage 0's A rows 8·wid and B rows 8·wid
+  const uint32_t la0 = lds_addr(&lds[0][8 * wid * kK]);
+  const uint32_t lb0 = lds_addr(&lds[0][(BM + 8 * wid) * kK]);
+  constexpr uint32_t kStageBytes = T::LDS * 2, kRowBytes32 = 32 * kK * 2;
+
+  // ---- constant parts of this lane's addresses
+  const u32x4 xr = rsrc_words(a.x, (int64_t)M * a.ldx * EB);
+  uint32_t ax[IA];               // x offsets of its A loads at entry column 0
 #pragma unroll
-      for (int g = 0; g < G; ++g)
-        s.base[g] = e[2 + g] >= 0 ? (uint32_t)e[2 + g] * (uint32_t)(P * P * EB) : kOob;
-    } else {
-      const int k0 = (u - nsp) * P;
-      s.a = (const uint16_t*)mb.t; s.lda = mb.ldt; s.ka = k0; s.kmax = 1 << 30;
-      s.kread = (int)mb.ldt - Gm::KE;
-      s.br = ar; s.bld = (uint32_t)(mb.lda * EB); s.mask = rowmask;
+  for (int i = 0; i < IA; ++i)
+    ax[i] = (uint32_t)(min(m0 + 8 * (wid + 4 * i) + lrow, M - 1) * a.ldx * EB + kin * EB);
+  u32x4 tr = xr, br = xr, ar = xr;
+  uint32_t at_[IA];              // t offsets of its A loads (low-rank steps)
+  uint32_t bconst[IB];           // B offsets that do not change per step
+  uint32_t lroff[IB];            // A-matrix offsets of its B loads (low-rank steps)
+  const int32_t* steps = nullptr;  // this group's first step record
+  int rword = 0;                   // this lane's word of a record
+  int lr_mask = 0;
+  if constexpr (KIND == K_LATENT) {
+    br = rsrc_words(mb.B, (int64_t)mb.r_pad * mb.ldb * EB);
 #pragma unroll
-      for (int g = 0; g < G; ++g)
-        s.base[g] = gr[2 + g] >= 0
-                        ? (uint32_t)(((int64_t)gr[2 + g] * P * mb.lda + k0) * EB)
-                        : kOob;
+    for (int i = 0; i < IB; ++i)
+      bconst[i] = (uint32_t)(((int64_t)(rt * BN + 8 * (wid + 4 * i) + lrow) * mb.ldb + kc * 8) * EB);
+#pragma unroll
+    for (int i = 0; i < IA; ++i) at_[i] = 0;
+#pragma unroll
+    for (int i = 0; i < IB; ++i) lroff[i] = 0;
+  } else {
+    br = rsrc_words(mb.values_pq, mb.values_bytes);
+#pragma unroll
+    for (int i = 0; i < IB; ++i) {
+      const int f = 8 * (wid + 4 * i) + lrow, j = f % P;
+      bconst[i] = (uint32_t)((j * P + kin) * EB);
     }
-    return s;
+    if constexpr (KIND == K_ROWS_FUSED) {
+      tr = rsrc_words(mb.t, (int64_t)M * mb.ldt * EB);
+      ar = rsrc_words(mb.A, mb.A_bytes);
+#pragma unroll
+      for (int i = 0; i < IA; ++i)
+        at_[i] = (uint32_t)((min(m0 + 8 * (wid + 4 * i) + lrow, M - 1) * mb.ldt + kc * 8) * EB);
+#pragma unroll
+      for (int i = 0; i < IB; ++i) {
+        const int f = 8 * (wid + 4 * i) + lrow;
+        const int row = ld_word(gr, 2 + (8 * (wid + 4 * i)) / P);
+        lroff[i] = row < 0 ? kOob : (uint32_t)(((int64_t)(row * P + f % P) * mb.lda + kc * 8) * EB);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) lr_mask |= (ld_word(gr, 2 + g) >= 0) ? (1 << g) | (1 << (G + g)) : 0;
+    } else {
+#pragma unroll
+      for (int i = 0; i < IA; ++i) at_[i] = 0;
+#pragma unroll
+      for (int i = 0; i < IB; ++i) lroff[i] = 0;
+    }
+    steps = mb.steps + (int64_t)s_begin * kRecInts;
+    // lane j of the wave holds word j of its view {mask, col[E], W[wave][IB][E]}
+    const int j = lane < NRV ? lane : 0;
+    rword = j < 1 + E ? j : 1 + E + wid * IB * E + (j - 1 - E);
+  }
+
+  // ---- the wave's view of sparse step v's record, one word per lane (an
+  // ordinary vector load, issued one step before the tile loads that use it;
+  // with two stages every load of the previous step has been waited for when
+  // it is used, so the compiler's own wait for it costs nothing)
+  auto read_record = [&](int v) -> int {
+    if constexpr (ROWS) {
+      if (n_sp > 0) return steps[(int64_t)min(v, n_sp - 1) * kRecInts + rword];
+    }
+    return -1;
+  };
+  // word w of the view as seen by this lane: lane w's value (uniform) or, for
+  // the per-entry words, the word of this lane's entry (w + e_t)
+  auto view_word = [&](int rv, int w) -> int { return __builtin_amdgcn_readlane(rv, w); };
+  auto view_entry = [&](int rv, int w) -> int {
+    if constexpr (E == 1) return __builtin_amdgcn_readlane(rv, w);
+    else return __builtin_amdgcn_ds_bpermute((w + e_t) * 4, rv);
   };
 
-  const int lane = threadIdx.x & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  f32x4 acc[G][MTW][W];
+  // ---- issue the tile loads of step u (clamped past the end) into stage `k`
+  // (rv: the step's record view); returns the step's mask (uniform).
+  // `ragged` is set when an x chunk of the step is cut by in_features (those
+  // chunks are fixed up once they landed); `xcol` is then this lane's first x
+  // column in the step.
+  auto fetch = [&](int u, int k, int rv, int& ragged, int& xcol) -> int {
+    u = min(u, U - 1);
+    int mask;
+    const uint32_t la = la0 + (uint32_t)k * kStageBytes, lb = lb0 + (uint32_t)k * kStageBytes;
+    if constexpr (KIND == K_LATENT) {
+      const int k0 = (s_begin + u) * kK;
+      const int col = k0 + kc * 8;
+      ragged = k0 + kK > m;
+      xcol = col;
+      const uint32_t xcb = col < m ? (uint32_t)(k0 * EB) : kOob;
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+      for (int i = 0; i < IA; ++i) dma16(xr, ax[i] + xcb, 0, la + i * kRowBytes32);
 #pragma unroll
-    for (int mt = 0; mt < MTW; ++mt)
+      for (int i = 0; i < IB; ++i) dma16(br, bconst[i], (uint32_t)(k0 * EB), lb + i * kRowBytes32);
+      mask = 3;
+    } else {
+      if (u < n_sp) {
+        mask = view_word(rv, 0);
+        const int c = view_entry(rv, 1);  // first x column of this lane's entry, or −1
+        const uint32_t xcb = c >= 0 ? (uint32_t)(c * EB) : kOob;
 #pragma unroll
-      for (int s = 0; s < W; ++s) acc[g][mt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < IA; ++i) dma16(xr, ax[i] + xcb, 0, la + i * kRowBytes32);
+#pragma unroll
+        for (int i = 0; i < IB; ++i) {
+          const int blk = view_entry(rv, 1 + E + i * E);
+          dma16(br, blk < 0 ? kOob : (uint32_t)blk * (uint32_t)(P * P * EB) + bconst[i], 0,
+                lb + i * kRowBytes32);
+        }
+        if (m % P != 0) {  // only a ragged last block column cuts chunks
+          xcol = c >= 0 ? c + kin : 0x3fffffff;
+          ragged = __builtin_amdgcn_ballot_w64(xcol + 8 > m) != 0;
+        } else {
+          xcol = 0;
+          ragged = 0;
+        }
+      } else {
+        const uint32_t k0b = (uint32_t)((u - n_sp) * kK * EB);  // ranks (K_ROWS_FUSED only)
+#pragma unroll
+        for (int i = 0; i < IA; ++i) dma16(tr, at_[i], k0b, la + i * kRowBytes32);
+#pragma unroll
+        for (int i = 0; i < IB; ++i) dma16(ar, lroff[i], k0b, lb + i * kRowBytes32);
+        mask = lr_mask;
+        ragged = 0;
+        xcol = 0;
+      }
+    }
+    return mask;
+  };
 
-  run_units<DT, P, G, MTW, D>(unit, U, m0, a.M, sb[0], sb[1], wid, lane, acc);
+  // ---- zero the x elements at and past in_features in a landed ragged stage
+  auto fix_ragged = [&](int k, int xcol) {
+    const int valid = m - xcol;
+    if (valid < 8) {
+#pragma unroll
+      for (int i = 0; i < IA; ++i) {
+        uint16_t* q = &lds[k][lds_chunk(8 * (wid + 4 * i) + lrow, kc)];
+        *(uint4*)q = valid <= 0 ? make_uint4(0, 0, 0, 0) : keep_first(*(const uint4*)q, valid);
+      }
+    }
+  };
 
-  // epilogue: lane (c, gq) owns W adjacent columns of rows 16·mt + 4gq + e
+  f32x4 acc[MTI][NTI];
+#pragma unroll
+  for (int mt = 0; mt < MTI; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NTI; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
   const int c = lane & 15, gq = lane >> 4;
+  // ---- the MFMAs of one step from an LDS stage
+  auto compute = [&](const uint16_t* buf, int mask_in) {
+    const int mask = __builtin_amdgcn_readfirstlane(mask_in);
+    Frag af[2][MTI], bf[2][NTI];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const int row = gr[2 + g];
-    if (row < 0) continue;
-    const int j0 = row * P + W * c;
-    float bv[W];
+    for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-    for (int s = 0; s < W; ++s) bv[s] = 0.f;
-    if (a.mode == PF_FUSED && mb.bias != nullptr) ld_w<DT, W>(mb.bias, j0, bv);
+      for (int mt = 0; mt < MTI; ++mt) {
+        const uint4 v = *(const uint4*)(buf + lds_chunk(wm * T::TM + 16 * mt + c, ks * 4 + gq));
+        af[ks][mt].d[0] = v.x; af[ks][mt].d[1] = v.y; af[ks][mt].d[2] = v.z; af[ks][mt].d[3] = v.w;
+      }
 #pragma unroll
-    for (int mt = 0; mt < MTW; ++mt)
+      for (int nt = 0; nt < NTI; ++nt) {
+        const uint4 v =
+            *(const uint4*)(buf + lds_chunk(BM + wn * T::TN + 16 * nt + c, ks * 4 + gq));
+        bf[ks][nt].d[0] = v.x; bf[ks][nt].d[1] = v.y; bf[ks][nt].d[2] = v.z; bf[ks][nt].d[3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int nt = 0; nt < NTI; ++nt) {
+        const int slot = (KIND == K_LATENT) ? 0 : (wn * T::TN + 16 * nt) / P;
+        if ((mask >> (ks * G + slot)) & 1) {
+#pragma unroll
+          for (int mt = 0; mt < MTI; ++mt) MM::run(acc[mt][nt], af[ks][mt], bf[ks][nt]);
+        }
+      }
+    }
+  };
+
+  if (U > 0) {
+    // stage (u % S) holds step u's tiles and (rows kernels) its record view;
+    // the tile loads of S − 1 steps are in flight, and the record loads of the
+    // S steps after those
+    int masks[S], rag[S], xcol[S];
+#pragma unroll
+    for (int k = 0; k < S - 1; ++k) masks[k] = fetch(k, k, read_record(k), rag[k], xcol[k]);
+    int next = read_record(S - 1);  // the record of the step the loop fetches first
+    for (int u0 = 0; u0 < U; u0 += S) {
+#pragma unroll
+      for (int k = 0; k < S; ++k) {
+        const int u = u0 + k;
+        if (u < U) {
+          wait_vmcnt<kWait>();                    // this wave's loads of step u landed
+          if (__builtin_amdgcn_readfirstlane(rag[k])) {
+            fix_ragged(k, xcol[k]);
+            wait_lgkm0();
+          }
+          barrier_only();                         // every wave's; step u − 1 computed
+          const int nk = (k + S - 1) % S;         // stage of step u + S − 1 (= step u − 1's)
+          masks[nk] = fetch(u + S - 1, nk, next, rag[nk], xcol[nk]);
+          next = read_record(u + S);
+          compute(lds[k], masks[k]);
+        }
+      }
+    }
+  }
+  wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
+
+  // ---- epilogue: lane (c, gq) holds rows 16·mt + 4gq + e of column 16·nt + c.
+  // The output pointers and strides are read into registers first: the
+  // stores below could otherwise alias the argument segment and force a
+  // reload per store.
+  if constexpr (KIND == K_LATENT) {
+    uint16_t* const t_out = (uint16_t*)mb.t;
+    float* const t_part = mb.tpart;
+    const int64_t ldt = mb.ldt;
+    const bool whole = mb.ksplit == 1;
+#pragma unroll
+    for (int mt = 0; mt < MTI; ++mt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int r = m0 + wid * 16 * MTW + mt * 16 + 4 * gq + e;
-        if (r < a.M) {
-          const int64_t off = (int64_t)r * mb.ldy + j0;
-          float o[W];
-          if (a.mode == PF_FUSED) {
+        const int r = m0 + wm * T::TM + 16 * mt + 4 * gq + e;
+        if (r >= M) continue;
 #pragma unroll
-            for (int s = 0; s < W; ++s) o[s] = acc[g][mt][s][e] + bv[s];
+        for (int nt = 0; nt < NTI; ++nt) {
+          const int col = rt * BN + wn * T::TN + 16 * nt + c;
+          const float v = acc[mt][nt][e];
+          if (whole) {
+            t_out[(int64_t)r * ldt + col] = (uint16_t)to_bits<DT>(v);
           } else {
-            ld_w<DT, W>(mb.y, off, o);
-#pragma unroll
-            for (int s = 0; s < W; ++s) o[s] += acc[g][mt][s][e];
+            t_part[((int64_t)kspl * M + r) * ldt + col] = v;
           }
-          st_w<DT, W>(mb.y, off, o);
         }
       }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Latent kernel: one workgroup per (64-row token tile, 64-rank tile, K split).
-// Writes the rounded latent when there is one split, else fp32 partials that
-// pf_latent_combine sums in split order. Rows past M come from row M − 1.
-// ---------------------------------------------------------------------------
-template <int DT, int D>
-__global__ __launch_bounds__(kPfThreads) void pf_latent_kernel(PfArgs by_value) {
-  (void)by_value;
-  const PfArgs& a = *(const PfArgs*)__builtin_amdgcn_kernarg_segment_ptr();
-  constexpr int P = 64, G = 1, MTW = 1, BM = 64, EB = 2;
-  using Gm = Geo<DT, P, G, MTW>;
-  constexpr int W = Gm::W, KP = Gm::KP;
-  __shared__ __align__(16) uint16_t sb[2][G * P * KP];
-
-  const int b = blockIdx.x;
-  int i = 0;
-  while (i + 1 < a.n && b >= a.off[i + 1]) ++i;
-  const PfMember& mb = a.mb[i];
-  const int n_rt = mb.r_pad / P;
-  const int local = b - a.off[i];
-  const int ks = local % mb.ksplit, tile = local / mb.ksplit;
-  const int tt = tile / n_rt, rt = tile % n_rt;
-  const int m0 = tt * BM;
-  const int units = a.m_pad / P;
-  const int ku = (units + mb.ksplit - 1) / mb.ksplit;
-  const int ub = ks * ku, ue = min(ub + ku, units);
-  const auto br = mk_rsrc(mb.B, (int64_t)mb.r_pad * mb.ldb * EB);
-
-  auto unit = [&](int u) {
-    Unit<G> s;
-    const int k0 = (ub + u) * P;
-    s.a = (const uint16_t*)a.x; s.lda = a.ldx; s.ka = k0; s.kmax = a.m;
-    s.kread = (int)a.ldx - Gm::KE;
-    s.br = br; s.bld = (uint32_t)(mb.ldb * EB); s.mask = 1;
-    s.base[0] = (uint32_t)(((int64_t)rt * P * mb.ldb + k0) * EB);
-    return s;
-  };
-  const int lane = threadIdx.x & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  f32x4 acc[G][MTW][W];
+  } else {
+    uint16_t* const y_out = (uint16_t*)mb.y;
+    const int64_t ldy = mb.ldy;
+    const void* const bias = mb.bias;
 #pragma unroll
-  for (int s = 0; s < W; ++s) acc[0][0][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-  run_units<DT, P, G, MTW, D>(unit, ue - ub, m0, a.M, sb[0], sb[1], wid, lane, acc);
-
-  // rows m0 + 16·wid + 4gq + e, ranks rt·64 + W·c + s
-  const int c = lane & 15, gq = lane >> 4;
+    for (int nt = 0; nt < NTI; ++nt) {
+      const int f = wn * T::TN + 16 * nt + c;
+      const int row = ld_word(gr, 2 + (wn * T::TN + 16 * nt) / P);
+      if (row < 0) continue;
+      const int col = row * P + f % P;
+      float bv = 0.f;
+      if (KIND == K_ROWS_FUSED && bias != nullptr) bv = load_scalar<DT>(bias, col);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int r = m0 + wid * 16 + 4 * gq + e;
-    float o[W];
+      for (int mt = 0; mt < MTI; ++mt)
 #pragma unroll
-    for (int s = 0; s < W; ++s) o[s] = acc[0][0][s][e];
-    const int64_t idx = (int64_t)r * mb.ldt + rt * P + W * c;
-    if (mb.ksplit == 1) {
-      st_w<DT, W>(mb.t, idx, o);
-    } else {
-      float* pp = mb.tpart + (int64_t)ks * a.rows * mb.ldt + idx;
-      *(float4*)pp = make_float4(o[0], o[1], o[2], o[3]);
+        for (int e = 0; e < 4; ++e) {
+          const int r = m0 + wm * T::TM + 16 * mt + 4 * gq + e;
+          if (r >= M) continue;
+          uint16_t* yp = y_out + (int64_t)r * ldy + col;
+          float o = acc[mt][nt][e];
+          if constexpr (KIND == K_ROWS_FUSED) o += bv;
+          else o += load_scalar<DT>(yp, 0);
+          *yp = (uint16_t)to_bits<DT>(o);
+        }
     }
   }
 }
@@ -418,9 +519,9 @@ __global__ __launch_bounds__(kPfThreads) void pf_latent_combine(PfArgs by_value)
   while (i + 1 < a.n && b >= a.off[i + 1]) ++i;
   const PfMember& mb = a.mb[i];
   const int64_t q = (int64_t)(b - a.off[i]) * kPfThreads + threadIdx.x;  // 4-element piece
-  const int64_t n = (int64_t)a.rows * mb.ldt / 4;
+  const int64_t n = (int64_t)a.M * mb.ldt / 4;
   if (q >= n) return;
-  const int64_t slab = (int64_t)a.rows * mb.ldt;
+  const int64_t slab = (int64_t)a.M * mb.ldt;
   float4 v = *(const float4*)(mb.tpart + 4 * q);
   for (int k = 1; k < mb.ksplit; ++k) {
     const float4 w = *(const float4*)(mb.tpart + k * slab + 4 * q);
@@ -430,29 +531,32 @@ __global__ __launch_bounds__(kPfThreads) void pf_latent_combine(PfArgs by_value)
   st_w<DT, 4>(mb.t, 4 * q, o);
 }
 
-// Two configurations per block size, both two waves per SIMD (≤ 256 registers):
-//   wide:   128 token rows × G = 256/p block-rows (x tiles shared by G rows)
-//   narrow: 64 token rows × 1 block-row (more workgroups for smaller calls)
-template <int DT, int P>
-hipError_t launch_rows(const PfArgs& a, int G, int bm, hipStream_t s) {
-  constexpr int GM = 256 / P;
+// Row-kernel tiles: tall 256 × 64 (waves 4 × 1, 64 × 64 each; 80 KiB of LDS,
+// two workgroups per compute unit) and narrow 128 × 64 (waves 2 × 2, 64 × 32
+// each; 48 KiB, three per compute unit), both with two stages. The latent uses
+// the narrow tile with three stages.
+constexpr int kLatentStages = 3;
+
+template <int DT, int KIND, int P>
+hipError_t launch_rows(const PfArgs& a, int G, hipStream_t s) {
   const int per_xcd = (a.items + kXcds - 1) / kXcds;
   const dim3 grid((unsigned)(per_xcd * kXcds)), blk(kPfThreads);
-  constexpr int D = P == 64 ? 2 : 3;
-  if (G == GM && bm == 128) hipLaunchKernelGGL((pf_rows_kernel<DT, P, GM, 2, D>), grid, blk, 0, s, a);
-  else if (G == 1 && bm == 64) hipLaunchKernelGGL((pf_rows_kernel<DT, P, 1, 1, 8>), grid, blk, 0, s, a);
-  else return hipErrorInvalidValue;
+  if (G * P == 64 && a.bm == 256)
+    hipLaunchKernelGGL((pf_gemm<DT, KIND, P, 256, 64, 4, 1, 2>), grid, blk, 0, s, a);
+  else if (G * P == 64 && a.bm == 128)
+    hipLaunchKernelGGL((pf_gemm<DT, KIND, P, 128, 64, 2, 2, 2>), grid, blk, 0, s, a);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
-template <int DT>
+template <int DT, int KIND>
 hipError_t launch_rows_p(const PfArgs& rows, int P, int G, hipStream_t s) {
   if (rows.items == 0) return hipSuccess;
-  const int bm = prefill_row_tile(G);
   switch (P) {
-    case 16: return launch_rows<DT, 16>(rows, G, bm, s);
-    case 32: return launch_rows<DT, 32>(rows, G, bm, s);
-    case 64: return launch_rows<DT, 64>(rows, G, bm, s);
+    case 16: return launch_rows<DT, KIND, 16>(rows, G, s);
+    case 32: return launch_rows<DT, KIND, 32>(rows, G, s);
+    case 64: return launch_rows<DT, KIND, 64>(rows, G, s);
   }
   return hipErrorInvalidValue;
 }
@@ -461,8 +565,8 @@ template <int DT>
 hipError_t launch_fused(const PfArgs& rows, const PfArgs& lat, const PfArgs& comb, int P, int G,
                         hipStream_t s) {
   if (lat.items > 0) {
-    hipLaunchKernelGGL((pf_latent_kernel<DT, 4>), dim3((unsigned)lat.items), dim3(kPfThreads), 0, s,
-                       lat);
+    hipLaunchKernelGGL((pf_gemm<DT, K_LATENT, 64, 128, 64, 2, 2, kLatentStages>),
+                       dim3((unsigned)lat.items), dim3(kPfThreads), 0, s, lat);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (comb.combine_items > 0) {
@@ -472,27 +576,35 @@ hipError_t launch_fused(const PfArgs& rows, const PfArgs& lat, const PfArgs& com
       if (e != hipSuccess) return e;
     }
   }
-  return launch_rows_p<DT>(rows, P, G, s);
+  return launch_rows_p<DT, K_ROWS_FUSED>(rows, P, G, s);
 }
 
 }  // namespace
 
-int prefill_row_tile(int group) { return group > 1 ? 128 : 64; }
-
 int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus) {
-  // the wide configuration when it still gives every CU a workgroup
-  const int gmax = 256 / block_p;
+  (void)M; (void)n_rows; (void)n_cus;
+  return 64 / block_p;
+}
+
+int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus) {
+  (void)block_p;
   const int64_t forced = debug_knobs().prefill_group;  // test hook
-  if (forced == 1) return 1;
-  if (forced == 2) return gmax;
-  const int64_t items = ((M + 127) / 128) * ((n_rows + gmax - 1) / gmax);
-  return items >= n_cus ? gmax : 1;
+  if (forced == 1) return 128;
+  if (forced == 2) return 256;
+  // the tall tile (fewer re-reads of x and of the weights, more MFMA work per
+  // LDS byte) unless it would leave compute units idle that the narrow one
+  // fills: it runs two workgroups per compute unit
+  const int64_t groups = (n_rows + group - 1) / group;
+  const int64_t tall = ((M + 255) / 256) * groups, narrow = ((M + 127) / 128) * groups;
+  return (tall >= 2 * n_cus || tall >= narrow) ? 256 : 128;
 }
 
 int prefill_latent_split(int64_t M, int64_t r_pad, int64_t m_pad, int n_cus) {
-  const int64_t tiles = ((M + 63) / 64) * (r_pad / 64);
+  // latent tiles are 128 tokens × 64 ranks; split K until about one workgroup
+  // per compute unit, keeping at least 4 steps (256 columns) per split
+  const int64_t tiles = ((M + 127) / 128) * (r_pad / 64);
   if (tiles <= 0) return 1;
-  int64_t ks = (2 * n_cus) / tiles;
+  int64_t ks = n_cus / tiles;
   const int64_t units = m_pad / 64;
   if (ks > units / 4) ks = units / 4;
   if (ks > 16) ks = 16;
@@ -510,8 +622,8 @@ hipError_t prefill_launch_fused(int dtype, int P, int G, const PfArgs& rows, con
 
 hipError_t prefill_launch_op(int dtype, int P, int G, const PfArgs& rows, hipStream_t stream) {
   switch (dtype) {
-    case SSL_BF16: return launch_rows_p<DT_BF16>(rows, P, G, stream);
-    case SSL_F16: return launch_rows_p<DT_F16>(rows, P, G, stream);
+    case SSL_BF16: return launch_rows_p<DT_BF16, K_ROWS_OP>(rows, P, G, stream);
+    case SSL_F16: return launch_rows_p<DT_F16, K_ROWS_OP>(rows, P, G, stream);
   }
   return hipErrorInvalidValue;
 }

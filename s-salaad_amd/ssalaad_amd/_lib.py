@@ -54,10 +54,11 @@ _SIGNATURES = {
          _c_i64, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p,
          _c_i64, _c_p],
     ),
+    "ssl_prefill_step_ints": (_c_i32, [_c_i32, _c_i32]),
     "ssl_prefill_plan_build": (
         ctypes.c_int,
-        [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_p,
-         _c_p],
+        [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_p, _c_i64,
+         _c_p, _c_p],
     ),
     "ssl_prefill_min_rows": (_c_i64, []),
     "ssl_nm24_block_bytes": (_c_i64, []),
@@ -138,7 +139,7 @@ class SlrMember(ctypes.Structure):
         ("n_slots", _c_i64), ("lr_wgs", _c_i64), ("NB", _c_i64), ("r_pad", _c_i64),
         ("counters", _c_p), ("n_counters", _c_i64), ("exchange", _c_p),
         ("exchange_bytes", _c_i64), ("workspace", _c_p), ("workspace_bytes", _c_i64),
-        ("pf_groups", _c_p), ("pf_entries", _c_p), ("pf_n_groups", _c_i64), ("pf_group", _c_i32),
+        ("pf_groups", _c_p), ("pf_steps", _c_p), ("pf_n_groups", _c_i64), ("pf_group", _c_i32),
         ("nnz", _c_i64), ("values_pq", _c_p), ("s_format", _c_i32), ("status", _c_p),
     ]
 

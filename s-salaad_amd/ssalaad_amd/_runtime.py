@@ -152,10 +152,11 @@ def build_plan(
 
 def build_prefill_plan(
     crow_host: np.ndarray, col_host: np.ndarray, NBK: int, rows_host: np.ndarray | None,
-    group: int
+    block_p: int, group: int
 ) -> tuple[np.ndarray, np.ndarray, int]:
-    """Group table [n_groups, 2 + group] and union-column entries [n_entries, 2 + group]
-    (int32) for the prefill row kernel (ssl_prefill_plan_build)."""
+    """Group table [n_groups, 2 + group] and 64-column step records
+    [n_steps, ssl_prefill_step_ints(p, group)] (int32) for the prefill row
+    kernels (ssl_prefill_plan_build)."""
     lib = _lib.load()
     crow_host = np.ascontiguousarray(crow_host, dtype=np.int32)
     col_host = np.ascontiguousarray(col_host, dtype=np.int32)
@@ -164,28 +165,31 @@ def build_prefill_plan(
     if rows_host is not None:
         rows_host = np.ascontiguousarray(rows_host, dtype=np.int32)
         rows_p, n_rows = rows_host.ctypes.data, rows_host.shape[0]
-    ng, ne = ctypes.c_int64(), ctypes.c_int64()
+    stride = int(lib.ssl_prefill_step_ints(block_p, group))
+    if stride <= 0:
+        raise ValueError(f"no prefill plan for block {block_p} and group {group}")
+    ng, ns = ctypes.c_int64(), ctypes.c_int64()
     args = (crow_host.ctypes.data, col_host.ctypes.data if col_host.size else None, NB, NBK,
-            rows_p, n_rows, group)
-    rc = lib.ssl_prefill_plan_build(*args, None, 0, None, 0, ctypes.byref(ng), ctypes.byref(ne))
+            rows_p, n_rows, block_p, group)
+    rc = lib.ssl_prefill_plan_build(*args, None, 0, None, 0, ctypes.byref(ng), ctypes.byref(ns))
     _lib.check(rc, "ssl_prefill_plan_build")
     groups = np.zeros((max(ng.value, 1), 2 + group), dtype=np.int32)
-    entries = np.zeros((max(ne.value, 1), 2 + group), dtype=np.int32)
-    rc = lib.ssl_prefill_plan_build(*args, groups.ctypes.data, groups.shape[0], entries.ctypes.data,
-                                    entries.shape[0], ctypes.byref(ng), ctypes.byref(ne))
+    steps = np.zeros((max(ns.value, 1), stride), dtype=np.int32)
+    rc = lib.ssl_prefill_plan_build(*args, groups.ctypes.data, groups.shape[0], steps.ctypes.data,
+                                    steps.shape[0], ctypes.byref(ng), ctypes.byref(ns))
     _lib.check(rc, "ssl_prefill_plan_build")
-    return groups, entries, int(ng.value)
+    return groups, steps, int(ng.value)
 
 
 class DevicePrefillPlan:
-    """A prefill plan (group table and union-column entries) on one device."""
+    """A prefill plan (group table and step records) on one device."""
 
-    __slots__ = ("groups", "entries", "n_groups", "group")
+    __slots__ = ("groups", "steps", "n_groups", "group")
 
-    def __init__(self, groups: np.ndarray, entries: np.ndarray, n_groups: int, group: int,
+    def __init__(self, groups: np.ndarray, steps: np.ndarray, n_groups: int, group: int,
                  device: torch.device):
         self.groups = torch.from_numpy(groups).to(device)
-        self.entries = torch.from_numpy(entries).to(device)
+        self.steps = torch.from_numpy(steps).to(device)
         self.n_groups = n_groups
         self.group = group
 

@@ -113,8 +113,8 @@ def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_by
             crow_h, _ = _validated_host_structure(crow, col, active_rows, values.shape[0], NB_K)
             col_h = col.detach().to("cpu").numpy().astype(np.int32)
             rows_h = plan.table.cpu().numpy()[: plan.n_chunks, 0].astype(np.int32)
-            groups, entries, ng = _runtime.build_prefill_plan(crow_h, col_h, NB_K, rows_h, G)
-            pf = _runtime.DevicePrefillPlan(groups, entries, ng, G, crow.device)
+            groups, steps, ng = _runtime.build_prefill_plan(crow_h, col_h, NB_K, rows_h, block_p, G)
+            pf = _runtime.DevicePrefillPlan(groups, steps, ng, G, crow.device)
             sp.plans[("pf", G)] = pf
     return plan, pf
 
@@ -234,7 +234,7 @@ def bsr_addmm_inplace_(
             target.data_ptr(), target.stride(0), x.data_ptr(), x.stride(0), col.data_ptr(),
             vals.data_ptr(), vals.shape[0], plan.table.data_ptr(), plan.n_chunks, plan.n_slots,
             vals_pq.data_ptr() if pf else None,
-            pf.groups.data_ptr() if pf else None, pf.entries.data_ptr() if pf else None,
+            pf.groups.data_ptr() if pf else None, pf.steps.data_ptr() if pf else None,
             pf.n_groups if pf else 0, pf.group if pf else 0, M, N, K, NB,
             block_p, block_q, dt, cnt.data_ptr(), cnt.numel(), ws.data_ptr(), ws.numel(),
             _lib.stream_ptr(dev),

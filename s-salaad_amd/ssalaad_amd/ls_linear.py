@@ -173,9 +173,9 @@ class _KernelState:
         """The prefill row kernel's plan with G block-rows per workgroup."""
         pp = self._pf_plans.get(G)
         if pp is None:
-            groups, entries, ng = _runtime.build_prefill_plan(self.crow_h, self.col_h, self.NBK,
-                                                              None, G)
-            pp = _runtime.DevicePrefillPlan(groups, entries, ng, G, self.device)
+            groups, steps, ng = _runtime.build_prefill_plan(self.crow_h, self.col_h, self.NBK,
+                                                            None, self.p, G)
+            pp = _runtime.DevicePrefillPlan(groups, steps, ng, G, self.device)
             self._pf_plans[G] = pp
         if self._values_pq is None and self.nblk_total > 0:
             # the prefill kernels read each block k-contiguous per output column
@@ -237,7 +237,7 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
             mb.status = status
             if G:
                 pp = st.prefill_plan(G)
-                mb.pf_groups, mb.pf_entries = pp.groups.data_ptr(), pp.entries.data_ptr()
+                mb.pf_groups, mb.pf_steps = pp.groups.data_ptr(), pp.steps.data_ptr()
                 mb.pf_n_groups, mb.pf_group = pp.n_groups, pp.group
                 mb.values_pq = _lib.ptr(st._values_pq)
             ws_off += ws_need[i]

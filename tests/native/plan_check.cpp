@@ -92,40 +92,55 @@ static void check_plan(const Structure& s, bool use_rows, int32_t q, int32_t lr,
   }
 }
 
-static void check_prefill(const Structure& s, bool use_rows, int32_t group) {
+static void check_prefill(const Structure& s, bool use_rows, int32_t p, int32_t group) {
   const int32_t* rows = row_list(s, use_rows);
   const int64_t nr = use_rows ? (int64_t)s.rows.size() : s.NB;
   int64_t ng = -1, ne = -1;
-  int rc = ssl_prefill_plan_build(s.crow.data(), s.col.data(), s.NB, s.NBK, rows, nr, group,
+  int rc = ssl_prefill_plan_build(s.crow.data(), s.col.data(), s.NB, s.NBK, rows, nr, p, group,
                                   nullptr, 0, nullptr, 0, &ng, &ne);
   CHECK(rc == SSL_OK);
   if (rc != SSL_OK) return;
-  const int stride = 2 + group;
+  const int gstride = 2 + group;
+  const int stride = ssl_prefill_step_ints(p, group);
+  const int E = 64 / p, IB = group * p / 32;
+  CHECK(stride >= 1 + E + 4 * IB * E);
   if (ng > 0) {
-    std::vector<int32_t> g((size_t)((ng - 1) * stride + 1)), e((size_t)(ne * stride + 1));
+    std::vector<int32_t> g((size_t)((ng - 1) * gstride + 1)), e((size_t)(ne * stride + 1));
     int64_t a, b;
-    CHECK(ssl_prefill_plan_build(s.crow.data(), s.col.data(), s.NB, s.NBK, rows, nr, group,
+    CHECK(ssl_prefill_plan_build(s.crow.data(), s.col.data(), s.NB, s.NBK, rows, nr, p, group,
                                  g.data(), ng - 1, e.data(), ne, &a, &b) == SSL_ERR_CAPACITY);
   }
-  std::vector<int32_t> g((size_t)(ng * stride)), e((size_t)(ne * stride));
+  std::vector<int32_t> g((size_t)(ng * gstride)), e((size_t)(ne * stride));
   int64_t ng2, ne2;
-  CHECK(ssl_prefill_plan_build(s.crow.data(), s.col.data(), s.NB, s.NBK, rows, nr, group,
+  CHECK(ssl_prefill_plan_build(s.crow.data(), s.col.data(), s.NB, s.NBK, rows, nr, p, group,
                                g.data(), ng, e.data(), ne, &ng2, &ne2) == SSL_OK);
   CHECK(ng2 == ng && ne2 == ne);
   std::vector<int> seen(s.col.size(), 0);
   for (int64_t i = 0; i < ng; ++i) {
-    const int32_t* gr = &g[(size_t)(i * stride)];
+    const int32_t* gr = &g[(size_t)(i * gstride)];
     CHECK(gr[0] >= 0 && gr[0] <= gr[1] && gr[1] <= ne);
     for (int32_t k = gr[0]; k < gr[1] && k >= 0 && k < ne; ++k) {
-      const int32_t* en = &e[(size_t)(k * stride)];
-      CHECK(en[0] >= 0 && en[0] < s.NBK);
-      for (int sl = 0; sl < group; ++sl) {
-        const bool on = (en[1] >> sl) & 1;
-        CHECK(on == (en[2 + sl] >= 0));
-        if (!on) continue;
-        const int32_t row = gr[2 + sl], blk = en[2 + sl];
-        CHECK(row >= 0 && blk >= s.crow[row] && blk < s.crow[row + 1] && s.col[blk] == en[0]);
-        if (blk >= 0 && blk < (int32_t)s.col.size()) ++seen[blk];
+      const int32_t* rec = &e[(size_t)(k * stride)];
+      for (int en = 0; en < E; ++en) {
+        const int32_t c = rec[1 + en];
+        CHECK(c == -1 || (c >= 0 && c % p == 0 && c / p < s.NBK));
+        // the words of wave w, load i hold slot 8·(w + 4i) / p; all copies agree
+        for (int w = 0; w < 4; ++w)
+          for (int i = 0; i < IB; ++i) {
+            const int sl = 8 * (w + 4 * i) / p;
+            CHECK(rec[1 + E + (w * IB + i) * E + en] == rec[1 + E + ((sl * p / 8) % 4 * IB + (sl * p / 8) / 4) * E + en]);
+          }
+        for (int sl = 0; sl < group; ++sl) {
+          const int fw = sl * p / 8;  // first 8-feature run of the slot: wave fw % 4, load fw / 4
+          const int32_t blk = rec[1 + E + ((fw % 4) * IB + fw / 4) * E + en];
+          if (blk < 0) continue;
+          CHECK(c >= 0);
+          const int h0 = en * p / 32, h1 = (en * p + p - 1) / 32;
+          CHECK(((rec[0] >> (h0 * group + sl)) & 1) && ((rec[0] >> (h1 * group + sl)) & 1));
+          const int32_t row = gr[2 + sl];
+          CHECK(row >= 0 && blk >= s.crow[row] && blk < s.crow[row + 1] && s.col[blk] * p == c);
+          if (blk >= 0 && blk < (int32_t)s.col.size()) ++seen[blk];
+        }
       }
     }
   }
@@ -144,9 +159,10 @@ int main() {
     const int64_t target = (rng() % 3 == 0) ? 0 : 1 + rng() % 200;
     check_plan(s, false, q, lr, target);
     check_plan(s, true, q, lr, target);
-    const int32_t group = 1 + rng() % 16;
-    check_prefill(s, false, group);
-    check_prefill(s, true, group);
+    const int32_t pp = 16 << (rng() % 3);
+    const int32_t group = 64 / pp;
+    check_prefill(s, false, pp, group);
+    check_prefill(s, true, pp, group);
     // corrupted copies are refused
     if (!s.col.empty()) {
       Structure bad = s;
@@ -155,7 +171,7 @@ int main() {
       CHECK(ssl_plan_build(bad.crow.data(), bad.col.data(), bad.NB, bad.NBK, nullptr, 0, q, lr,
                            target, nullptr, 0, &a, &b) == SSL_ERR_INVALID);
       CHECK(ssl_prefill_plan_build(bad.crow.data(), bad.col.data(), bad.NB, bad.NBK, nullptr, 0,
-                                   group, nullptr, 0, nullptr, 0, &a, &b) == SSL_ERR_INVALID);
+                                   pp, group, nullptr, 0, nullptr, 0, &a, &b) == SSL_ERR_INVALID);
     }
     if (s.NB > 1 && s.crow[s.NB] > 0) {
       Structure bad = s;

@@ -189,50 +189,99 @@ def test_plans_reject_column_indices_out_of_range(bad):
         _runtime.build_plan(np.asarray(crow, np.int32), np.zeros(0, np.int32), 4, None, 16, 0, 0)
 
 
-def _pf_plan(crow, col, rows=None, group=4, NBK=None):
+def _pf_plan(crow, col, rows=None, group=1, NBK=None, p=64):
     col = np.asarray(col, np.int32)
     if NBK is None:
         NBK = int(col.max()) + 1 if col.size else 1
     return _runtime.build_prefill_plan(np.asarray(crow, np.int32), col, NBK,
-                                       None if rows is None else np.asarray(rows, np.int32), group)
+                                       None if rows is None else np.asarray(rows, np.int32), p,
+                                       group)
 
 
-def test_prefill_plan_merges_each_groups_columns():
+def _steps_to_entries(steps, s0, s1, p, G):
+    """The union entries (col_block, {slot: blk}) a group's step records hold,
+    in order, checking each step's mask against its blocks on the way. A record
+    holds, per wave w of the row kernel and load i, the block indices of slot
+    8·(w + 4i) / p: every copy of a slot's index must agree."""
+    E, IB = 64 // p, G * p // 32
+    out = []
+    for rec in steps[s0:s1]:
+        mask, cols = rec[0], rec[1:1 + E]
+        W = rec[1 + E:1 + E + 4 * IB * E].reshape(4, IB, E)
+        blks = np.full((E, G), -2, np.int64)
+        for w in range(4):
+            for i in range(IB):
+                g = 8 * (w + 4 * i) // p
+                assert (blks[:, g] == -2).all() or (blks[:, g] == W[w, i]).all()
+                blks[:, g] = W[w, i]
+        assert (blks != -2).all()  # every slot has its words
+        want = 0
+        for e in range(E):
+            if cols[e] < 0:
+                assert (blks[e] < 0).all()
+                continue
+            assert cols[e] % p == 0
+            out.append((cols[e] // p, {g: int(blks[e, g]) for g in range(G) if blks[e, g] >= 0}))
+            for g in range(G):
+                if blks[e, g] >= 0:
+                    for h in range(2):  # 32-column halves the entry covers
+                        if e * p < 32 * (h + 1) and (e + 1) * p > 32 * h:
+                            want |= 1 << (h * G + g)
+        assert int(mask) & 0xffffffff == want
+        assert (rec[1 + E + 4 * IB * E:] == -1).all()  # padding
+    return out
+
+
+@pytest.mark.parametrize("p", [16, 32, 64])
+def test_prefill_plan_merges_each_groups_columns(p):
     """Every block of every listed row appears exactly once, in its row's slot,
-    entries of a group ascend by column, and masks match the slots present."""
+    entries of a group ascend by column, E = 64/p entries per step, and the
+    masks match the slots present in each 32-column half."""
     rng = np.random.default_rng(1)
     NB, NBK = 23, 17
     counts = rng.integers(0, NBK + 1, NB)
     crow = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     col = np.concatenate([np.sort(rng.choice(NBK, c, replace=False)) for c in counts]).astype(np.int32)
+    lib = _lib.load()
     for rows in (None, [0, 2, 3, 7, 11, 12, 20, 22]):
-        for G in (1, 4, 8, 16):
-            groups, entries, ng = _pf_plan(crow, col, rows, G)
+        for G in (64 // p,):  # the row kernel's tiles are 64 features wide
+            groups, steps, ng = _pf_plan(crow, col, rows, G, p=p)
+            assert steps.shape[1] == lib.ssl_prefill_step_ints(p, G) and steps.shape[1] % 4 == 0
             listed = list(range(NB)) if rows is None else rows
             assert ng == -(-len(listed) // G)
             seen = []
             for gi in range(ng):
-                e0, e1 = groups[gi, 0], groups[gi, 1]
+                s0, s1 = groups[gi, 0], groups[gi, 1]
                 grows = groups[gi, 2:]
                 assert list(grows[grows >= 0]) == listed[gi * G:(gi + 1) * G]
-                cols = entries[e0:e1, 0]
+                ents = _steps_to_entries(steps, s0, s1, p, G)
+                assert s1 - s0 == -(-len(ents) // (64 // p))
+                cols = [c for c, _ in ents]
                 assert np.all(np.diff(cols) > 0)
-                for c, mask, *blks in entries[e0:e1]:
-                    for g in range(G):
-                        b = blks[g]
-                        assert ((mask >> g) & 1) == (b >= 0)
-                        if b >= 0:
-                            assert crow[grows[g]] <= b < crow[grows[g] + 1] and col[b] == c
-                            seen.append(b)
+                for c, blks in ents:
+                    for g, b in blks.items():
+                        assert crow[grows[g]] <= b < crow[grows[g] + 1] and col[b] == c
+                        seen.append(b)
             want = [b for r in listed for b in range(crow[r], crow[r + 1])]
             assert sorted(seen) == sorted(want)
 
 
 def test_prefill_plan_repeated_column_gets_its_own_entry():
     crow, col = [0, 3], [5, 5, 2]
-    groups, entries, ng = _pf_plan(crow, col, None, 1)
-    assert ng == 1 and [tuple(e[:3]) for e in entries[groups[0, 0]:groups[0, 1]]] == \
-        [(2, 1, 2), (5, 1, 0), (5, 1, 1)]
+    groups, steps, ng = _pf_plan(crow, col, None, 1, p=64)
+    ents = _steps_to_entries(steps, groups[0, 0], groups[0, 1], 64, 1)
+    assert ng == 1 and ents == [(2, {0: 2}), (5, {0: 0}), (5, {0: 1})]
+
+
+def test_prefill_step_ints():
+    lib = _lib.load()
+    # 1 + E + 4·IB·E words rounded up to 4 (E = 64/p entries, IB = 2 loads of 8
+    # weight rows per wave)
+    assert lib.ssl_prefill_step_ints(64, 1) == 12 and lib.ssl_prefill_step_ints(32, 2) == 20
+    assert lib.ssl_prefill_step_ints(16, 4) == 40
+    # only the row kernel's tiles (group·p = 64) have records
+    assert lib.ssl_prefill_step_ints(48, 2) == 0 and lib.ssl_prefill_step_ints(16, 17) == 0
+    assert lib.ssl_prefill_step_ints(64, 2) == 0 and lib.ssl_prefill_step_ints(16, 8) == 0
 
 
 def test_plan_target_cost_policy():
@@ -309,7 +358,7 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     assert tp(127, 500, 64) == 0 and tp(128, 172, 64) == 1 and tp(128, 64, 64) == 0
     assert tp(129, 64, 64) == 1 and tp(512, 500, 32) == 0 and tp(513, 500, 32) == 1
     assert tp(300, 500, 16) == 0 and tp(2048, 64, 32) == 1 and tp(4096, 500, 64, _lib.SSL_F32) == 0
-    assert lib.ssl_prefill_group(4096, 172, 64, 64) in (1, 4)
+    assert lib.ssl_prefill_group(4096, 172, 64, 64) == 1  # 64 output features per row tile
     # the prefill kernels take square 16/32/64 blocks; other shapes stream
     assert tp(2048, 500, 32, q=64) == 0 and tp(2048, 500, 48) == 0
     ap = lambda M, p, q, dt=_lib.SSL_BF16: lib.ssl_bsr_addmm_takes_prefill(M, p, q, dt)

@@ -1,13 +1,12 @@
 """The prefill row kernels (calls with many token rows, 16-bit activations),
 every tile configuration checked against the oracle on every output row.
 
-The library picks one of two row tiles per call (ssl_prefill_group): "wide"
-(128 token rows × 256/p block-rows per workgroup) when that still gives every
-compute unit a workgroup, else "narrow" (64 × 1). Small shapes pick narrow, so
-the wide tiles run only at full size; the test hook SSL_DEBUG_PREFILL_TILE
-forces either tile on any shape, for the fused linear (PF_FUSED), the grouped
-launch and the in-place op (PF_OP). The full-size cases at the end are the
-shapes where the library picks the wide tile by itself, checked on all rows.
+The row kernel has two tiles (token rows × output features, 64/p block-rows
+per workgroup): "narrow" (128 × 64) and "tall" (256 × 64); the library picks
+one per call. The test hook SSL_DEBUG_PREFILL_TILE
+forces each tile on any shape, for the fused linear (PF_FUSED), the grouped
+launch and the in-place op (PF_OP). The full-size cases at the end run every
+tile at the benchmark shapes, checked on all rows.
 The forward these compute is ssalaad/efficient/ls_linear.py:124-137 (the op:
 ssalaad/tilelang_sparse/addmm_inplace.py:41-82).
 """
@@ -26,7 +25,9 @@ from ssalaad_amd import _lib
 
 pytestmark = pytest.mark.gpu
 
-WIDE, NARROW = 2, 1
+NARROW, TALL = 1, 2
+MODES = [NARROW, TALL]
+MODE_IDS = ["narrow", "tall"]
 DT16 = [torch.bfloat16, torch.float16]
 
 
@@ -48,15 +49,15 @@ def _group_of(M, rows, p):
 
 @pytest.mark.parametrize("dtype", DT16, ids=["bf16", "f16"])
 @pytest.mark.parametrize("p", [16, 32, 64])
-@pytest.mark.parametrize("mode", [WIDE, NARROW], ids=["wide", "narrow"])
+@pytest.mark.parametrize("mode", MODES, ids=MODE_IDS)
 @pytest.mark.parametrize("M", [600, 1030])
 def test_forced_tiles_fused_linear(dtype, p, mode, M, tile, gpu_device):
-    """Ragged block-row count (not a multiple of the wide group), skewed rows,
+    """Ragged block-row count, skewed rows,
     ragged token count: every row of every tile against the oracle."""
     tile(mode)
     prob = make_problem(13 * p + 64, 9 * 64, 128, p, 0.5, dtype, seed=p + M + mode, skew=True)
     rows = prob["NB"]
-    assert _group_of(M, rows, p) == (256 // p if mode == WIDE else 1)
+    assert _group_of(M, rows, p) == 64 // p
     mod = make_module(prob, gpu_device)
     x = make_x(prob, M)
     y = mod(to_dev(x, dtype, gpu_device))
@@ -66,7 +67,7 @@ def test_forced_tiles_fused_linear(dtype, p, mode, M, tile, gpu_device):
 
 @pytest.mark.parametrize("dtype", DT16, ids=["bf16", "f16"])
 @pytest.mark.parametrize("p", [16, 32, 64])
-@pytest.mark.parametrize("mode", [WIDE, NARROW], ids=["wide", "narrow"])
+@pytest.mark.parametrize("mode", MODES, ids=MODE_IDS)
 def test_forced_tiles_grouped_launch(dtype, p, mode, tile, gpu_device):
     tile(mode)
     specs = [(5 * p, 64, 0.5), (3 * p, 96, 0.3), (7 * p, 128, 0.7)]
@@ -82,7 +83,7 @@ def test_forced_tiles_grouped_launch(dtype, p, mode, tile, gpu_device):
 
 @pytest.mark.parametrize("dtype", DT16, ids=["bf16", "f16"])
 @pytest.mark.parametrize("p", [16, 32, 64])
-@pytest.mark.parametrize("mode", [WIDE, NARROW], ids=["wide", "narrow"])
+@pytest.mark.parametrize("mode", MODES, ids=MODE_IDS)
 def test_forced_tiles_inplace_op(dtype, p, mode, tile, gpu_device):
     """PF_OP: out += x·Sᵀ on the active rows only; every other row keeps its bits."""
     tile(mode)
@@ -108,11 +109,13 @@ def test_forced_tiles_inplace_op(dtype, p, mode, tile, gpu_device):
 # -------------------------------------------- full size, library's choice --
 
 
-def test_skewed_16x16_at_2048_tokens_every_row(gpu_device):
+@pytest.mark.parametrize("mode", [0] + MODES, ids=["auto"] + MODE_IDS)
+def test_skewed_16x16_at_2048_tokens_every_row(mode, tile, gpu_device):
     """4096×11008 bf16, rank 128, 16×16 blocks with Zipf(1.2) rows at 50% mean
-    density, 2048 tokens: the wide p = 16 tile (16 block-rows per workgroup)."""
+    density, 2048 tokens."""
+    tile(mode)
     prob = make_problem(4096, 11008, 128, 16, 0.5, torch.bfloat16, seed=21, skew=True)
-    assert _group_of(2048, prob["NB"], 16) == 16
+    assert _group_of(2048, prob["NB"], 16) == 4
     mod = make_module(prob, gpu_device)
     x = make_x(prob, 2048)
     y = mod(to_dev(x, torch.bfloat16, gpu_device))
@@ -120,13 +123,14 @@ def test_skewed_16x16_at_2048_tokens_every_row(gpu_device):
     assert err(y, oracle_y(prob, x)) <= 1e-2
 
 
-def test_llama1b_gate_up_group_at_2048_tokens_every_row(gpu_device):
+@pytest.mark.parametrize("mode", [0] + MODES, ids=["auto"] + MODE_IDS)
+def test_llama1b_gate_up_group_at_2048_tokens_every_row(mode, tile, gpu_device):
     """LLaMA-1B gate and up (5461×2048, 32×32 blocks at 50%, rank 256, FFN padded
-    to 5472) in one grouped launch at 2048 tokens: the wide p = 32 tile (8
-    block-rows per workgroup)."""
+    to 5472) in one grouped launch at 2048 tokens."""
+    tile(mode)
     probs = [make_problem(5461, 2048, 256, 32, 0.5, torch.bfloat16, seed=40 + i, pad=True)
              for i in range(2)]
-    assert _group_of(2048, 2 * probs[0]["NB"], 32) == 8
+    assert _group_of(2048, 2 * probs[0]["NB"], 32) == 2
     grp = ssalaad_amd.LRSLinearGroup(*[make_module(pr, gpu_device) for pr in probs])
     x = make_x(probs[0], 2048)
     ys = grp(to_dev(x, torch.bfloat16, gpu_device))
@@ -136,11 +140,13 @@ def test_llama1b_gate_up_group_at_2048_tokens_every_row(gpu_device):
         assert err(y, oracle_y(pr, x)) <= 1e-2
 
 
-def test_llama7b_ffn_at_2048_tokens_every_row(gpu_device):
-    """11008×4096 bf16, 64×64 blocks at 50%, rank 256, 2048 tokens: the wide
-    p = 64 tile (4 block-rows per workgroup), every row against the oracle."""
+@pytest.mark.parametrize("mode", [0] + MODES, ids=["auto"] + MODE_IDS)
+def test_llama7b_ffn_at_2048_tokens_every_row(mode, tile, gpu_device):
+    """11008×4096 bf16, 64×64 blocks at 50%, rank 256, 2048 tokens, every row
+    against the oracle."""
+    tile(mode)
     prob = make_problem(11008, 4096, 256, 64, 0.5, torch.bfloat16, seed=11)
-    assert _group_of(2048, prob["NB"], 64) == 4
+    assert _group_of(2048, prob["NB"], 64) == 1
     mod = make_module(prob, gpu_device)
     x = make_x(prob, 2048)
     y = mod(to_dev(x, torch.bfloat16, gpu_device))
