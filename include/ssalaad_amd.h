@@ -325,6 +325,23 @@ int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t 
                    float* out, int64_t ldo, void* stream);
 
 /* -------------------------------------------------------------------------
+ * ssl_project_nm — N:M projection of a dense matrix.
+ * Replaces ssalaad/inference/egar.py:284-292 (_project_S_nm), the sparse step
+ * of the compression loop for N:M structure:
+ *   in each run of nm_m consecutive entries of a row, keep the nm_n of
+ *   largest magnitude (|R|.topk(nm_n)); out = R.float() · mask.
+ * R is [n, ldr] in `dtype`; out is [n, ldo] fp32; keep (optional, [n, ldk]
+ * bytes) receives the mask. A NaN magnitude counts as the largest (as in
+ * torch.topk); equal magnitudes go to the lower index (torch.topk leaves
+ * that order unspecified). Dropped entries are R·0 as the reference's
+ * multiply leaves them (−0 for negative values, NaN for ±inf and NaN).
+ * nm_m ∈ [1, 32], nm_n ∈ [0, nm_m], m a multiple of nm_m.
+ * ------------------------------------------------------------------------- */
+int ssl_project_nm(const void* R, int64_t ldr, int64_t n, int64_t m, int32_t nm_n, int32_t nm_m,
+                   int32_t dtype, float* out, int64_t ldo, uint8_t* keep, int64_t ldk,
+                   void* stream);
+
+/* -------------------------------------------------------------------------
  * Dense → BSR encoder (device), the rule of ssalaad/efficient/artifact.py:20-37
  * (dense_to_bsr) followed by the module conversion of
  * ssalaad/efficient/ls_linear.py:89-97:

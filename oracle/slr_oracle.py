@@ -18,6 +18,9 @@ It restates, in NumPy (float64 unless stated), what the reference computes:
   project_blocks        ssalaad/inference/egar.py:296-317 (_project_S): keep the
                         n_keep blocks of largest Frobenius norm (fp32 input,
                         equal norms taken in ascending row-major block order)
+  project_nm            ssalaad/inference/egar.py:284-292 (_project_S_nm): in
+                        each run of nm_m consecutive entries of a row keep the
+                        nm_n of largest magnitude; out = R.float() · mask
 
 How each function is pinned (tests/test_oracle.py):
   * dense_to_bsr        vs torch.Tensor.to_sparse_bsr (the library routine the
@@ -41,6 +44,15 @@ How each function is pinned (tests/test_oracle.py):
                         Which of several EQUAL norms survive is parity unpinned:
                         torch.topk does not specify it; the oracle and the GPU
                         take the lowest block index.
+  * project_nm          vs the routine _project_S_nm calls (torch.topk over
+                        |R| in groups, then scatter and multiply) on tie-free
+                        inputs, brute force over every subset of tiny groups,
+                        the closed forms nm_n = nm_m (R·1) and nm_n = 0 (R·0,
+                        so −0 and NaN survive as the multiply leaves them), and
+                        the reference's 2:4 case. Which of EQUAL magnitudes
+                        survive is parity unpinned (torch.topk leaves it
+                        unspecified); the oracle and the GPU take the lower
+                        index. A NaN counts as the largest magnitude.
 """
 
 from __future__ import annotations
@@ -220,6 +232,37 @@ def project_blocks(M, n_keep: int, block_p: int, block_q: int):
     keep = keep.reshape(rb, cb)
     mask = np.repeat(np.repeat(keep, block_p, axis=0), block_q, axis=1)
     return np.where(mask, Mf, np.float32(0)).astype(np.float32), keep
+
+
+def project_nm(R, nm_n: int, nm_m: int):
+    """(R.float()·mask, mask) of egar.py:284-292: in each run of nm_m
+    consecutive entries along a row, the nm_n of largest |R| are kept (mask 1).
+    NaN magnitudes count as the largest; equal magnitudes: lower index first.
+    Dropped entries are R·0 as the reference's multiply leaves them (−0 for
+    negative values, NaN for NaN and ±inf)."""
+    Rf = np.asarray(R, dtype=np.float32)
+    n, m = Rf.shape
+    if nm_m <= 0 or m % nm_m:
+        raise ValueError("m must be a multiple of nm_m")
+    if not 0 <= nm_n <= nm_m:
+        raise ValueError("nm_n must lie in [0, nm_m]")
+    R3 = Rf.reshape(n, m // nm_m, nm_m)
+    mag = np.abs(R3)
+    key = np.where(np.isnan(mag), np.inf, mag).astype(np.float64)
+    nan = np.isnan(mag)
+    # rank of each entry in its group: entries that come before it in the
+    # order (NaN first, then larger magnitude, then lower index)
+    idx = np.arange(nm_m)
+    before = (
+        (nan[..., :, None] & ~nan[..., None, :])
+        | ((nan[..., :, None] == nan[..., None, :])
+           & ((key[..., :, None] > key[..., None, :])
+              | ((key[..., :, None] == key[..., None, :]) & (idx[:, None] < idx[None, :]))))
+    )  # before[..., k, j]: entry k precedes entry j
+    rank = before.sum(axis=-2)
+    mask = rank < nm_n
+    out = (R3 * mask.astype(np.float32)).astype(np.float32)
+    return out.reshape(n, m), mask.reshape(n, m)
 
 
 def max_abs_normalised_error(y, y_ref) -> float:

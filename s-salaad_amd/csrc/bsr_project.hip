@@ -216,6 +216,48 @@ __global__ __launch_bounds__(kThreads) void block_mask_kernel(const void* S, int
   }
 }
 
+// ---------------------------------------------------------------------------
+// N:M projection (ssalaad/inference/egar.py:284-292, _project_S_nm): in each
+// run of nm_m consecutive entries of a row keep the nm_n of largest
+// magnitude; out = value · (kept ? 1 : 0) in fp32. The reference multiplies by
+// the mask, so a dropped negative value gives −0 and a dropped ±inf or NaN
+// gives NaN; the same multiply here gives the same. An entry's order key is
+// its magnitude's bit pattern (non-negative floats order like their bits),
+// every NaN folded above +inf; equal keys go to the lower index. One thread
+// per group; NMM ≥ nm_m bounds the unrolled group.
+// ---------------------------------------------------------------------------
+template <int DT, int NMM>
+__global__ __launch_bounds__(kThreads) void nm_project_kernel(const void* R, int64_t ldr, int n,
+                                                              int groups_per_row, int nm_n,
+                                                              int nm_m, float* out, int64_t ldo,
+                                                              uint8_t* keep, int64_t ldk) {
+  const int64_t total = (int64_t)n * groups_per_row;
+  for (int64_t g = (int64_t)blockIdx.x * kThreads + threadIdx.x; g < total;
+       g += (int64_t)gridDim.x * kThreads) {
+    const int64_t row = g / groups_per_row;
+    const int64_t c0 = (g % groups_per_row) * nm_m;
+    float v[NMM];
+    uint32_t key[NMM];
+#pragma unroll
+    for (int j = 0; j < NMM; ++j) {
+      v[j] = j < nm_m ? elem_f32<DT>(R, row * ldr + c0 + j) : 0.f;
+      const uint32_t b = __float_as_uint(v[j]) & 0x7fffffffu;
+      key[j] = j < nm_m ? (b > 0x7f800000u ? kNanKey : b) : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < NMM; ++j) {
+      if (j >= nm_m) break;
+      int rank = 0;
+#pragma unroll
+      for (int k = 0; k < NMM; ++k)
+        rank += (k < nm_m && (key[k] > key[j] || (key[k] == key[j] && k < j))) ? 1 : 0;
+      const bool kept = rank < nm_n;
+      out[row * ldo + c0 + j] = v[j] * (kept ? 1.f : 0.f);
+      if (keep) keep[row * ldk + c0 + j] = kept ? 1 : 0;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace ssl
 
@@ -266,6 +308,45 @@ int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t 
   }
 #undef SSL_PROJECT
   return check_hip(hipGetLastError(), "block projection launch");
+}
+
+int ssl_project_nm(const void* R, int64_t ldr, int64_t n, int64_t m, int32_t nm_n, int32_t nm_m,
+                   int32_t dtype, float* out, int64_t ldo, uint8_t* keep, int64_t ldk,
+                   void* stream) {
+  clear_error();
+  if (n < 0 || m < 0) return fail(SSL_ERR_INVALID, "negative size");
+  if (nm_m < 1 || nm_m > 32)
+    return fail(SSL_ERR_UNSUPPORTED, "group size nm_m=%d outside [1, 32]", nm_m);
+  if (nm_n < 0 || nm_n > nm_m)
+    return fail(SSL_ERR_INVALID, "nm_n=%d outside [0, nm_m=%d]", nm_n, nm_m);
+  if (m % nm_m) return fail(SSL_ERR_INVALID, "m=%lld is not a multiple of nm_m=%d", (long long)m, nm_m);
+  if (dtype != SSL_F32 && dtype != SSL_BF16 && dtype != SSL_F16)
+    return fail(SSL_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
+  if (n == 0 || m == 0) return SSL_OK;
+  if (!R || !out) return fail(SSL_ERR_INVALID, "null pointer");
+  if (ldr < m || ldo < m || (keep && ldk < m)) return fail(SSL_ERR_INVALID, "row stride smaller than the row");
+  if (n > 0x7fffffffLL || m / nm_m > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "too large");
+  const int64_t total = n * (m / nm_m);
+  const int64_t want = (total + kThreads - 1) / kThreads;
+  const unsigned grid = (unsigned)(want < 8192 ? want : 8192);
+  hipStream_t s = (hipStream_t)stream;
+  const int gpr = (int)(m / nm_m);
+#define SSL_NM(DTC, NMM)                                                                     \
+  hipLaunchKernelGGL((nm_project_kernel<DTC, NMM>), dim3(grid), dim3(kThreads), 0, s, R, ldr, \
+                     (int)n, gpr, nm_n, nm_m, out, ldo, keep, ldk)
+#define SSL_NM_DT(DTC)                   \
+  if (nm_m <= 4) SSL_NM(DTC, 4);         \
+  else if (nm_m <= 8) SSL_NM(DTC, 8);    \
+  else if (nm_m <= 16) SSL_NM(DTC, 16);  \
+  else SSL_NM(DTC, 32);
+  switch (dtype) {
+    case SSL_F32: SSL_NM_DT(DT_F32) break;
+    case SSL_BF16: SSL_NM_DT(DT_BF16) break;
+    case SSL_F16: SSL_NM_DT(DT_F16) break;
+  }
+#undef SSL_NM_DT
+#undef SSL_NM
+  return check_hip(hipGetLastError(), "N:M projection launch");
 }
 
 }  // extern "C"

@@ -5,7 +5,7 @@ Drop-in for the S-SALAAD hot path:
   * LRSLinear                                              (ssalaad_amd.ls_linear)
   * LRSLinearGroup: linears sharing an input in one launch (ssalaad_amd.ls_linear)
   * dense_to_bsr / factor_from_svd                         (ssalaad_amd.artifact)
-  * project_S: the compression loop's block top-k           (ssalaad_amd.project)
+  * project_S / project_S_nm: the compression loop's sparse steps (ssalaad_amd.project)
   * save_artifact / load_artifact / build_efficient_model: bundles (ssalaad_amd.bundle)
   * DecodeEngine / generate: KV-cached greedy decode of a loaded model (ssalaad_amd.decode)
 All compute runs in the HIP kernels of libssalaad_amd.so; there is no CPU path.
@@ -19,7 +19,7 @@ from .artifact import dense_to_bsr, encode_for_kernels, factor_from_svd
 from .bundle import build_efficient_model, load_artifact, save_artifact
 from .decode import DecodeEngine, generate
 from .ls_linear import LRSLinear, LRSLinearGroup
-from .project import block_topk, project_S
+from .project import block_topk, project_S, project_S_nm, project_nm
 
 __all__ = [
     "DecodeEngine",
@@ -37,6 +37,8 @@ __all__ = [
     "library_path",
     "load_artifact",
     "project_S",
+    "project_S_nm",
+    "project_nm",
     "save_artifact",
 ]
 

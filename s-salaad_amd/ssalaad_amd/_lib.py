@@ -85,6 +85,10 @@ _SIGNATURES = {
         [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_p, _c_p, _c_p, _c_i64,
          _c_p],
     ),
+    "ssl_project_nm": (
+        ctypes.c_int,
+        [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_p],
+    ),
     "ssl_bsr_encode_count": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p],

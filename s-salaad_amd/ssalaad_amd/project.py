@@ -1,10 +1,15 @@
-"""Sparse projection of the compression loop on the GPU.
+"""Sparse projections of the compression loop on the GPU.
 
 `project_S(M, n_keep, block_p, block_q)` replaces ssalaad/inference/egar.py:296-317
 (`_project_S`): keep the `n_keep` blocks of largest Frobenius norm of M, as fp32,
 zeros elsewhere. It runs `ssl_block_topk` (block sums of squares, a radix select
 of the n_keep largest, the masked copy). Equal norms are taken in ascending
 row-major block order (torch.topk leaves that order unspecified).
+
+`project_S_nm(R, nm_n, nm_m)` replaces egar.py:284-292 (`_project_S_nm`): in
+each run of nm_m consecutive entries of a row keep the nm_n of largest
+magnitude, R.float() · mask. It runs `ssl_project_nm` (one thread per group).
+Equal magnitudes go to the lower index.
 """
 
 from __future__ import annotations
@@ -49,3 +54,36 @@ def block_topk(M: torch.Tensor, n_keep: int, block_p: int, block_q: int):
 def project_S(M: torch.Tensor, n_keep: int, block_p: int, block_q: int) -> torch.Tensor:
     """Keep the ``n_keep`` blocks of largest Frobenius norm (egar.py:296-317)."""
     return block_topk(M, n_keep, block_p, block_q)[0]
+
+
+def project_nm(R: torch.Tensor, nm_n: int, nm_m: int):
+    """(R.float() · mask, keep mask [n, m] bool) of egar.py:284-292."""
+    if R.dim() != 2:
+        raise ValueError("R must be 2-D")
+    if R.device.type != "cuda":
+        raise ValueError("the N:M projection runs on a ROCm GPU device; move R there first")
+    n, m = R.shape
+    if nm_m <= 0 or m % nm_m:
+        # the reference's R.float().view(n, m // nm_m, nm_m)
+        raise RuntimeError(
+            f"shape '[{n}, {m // max(nm_m, 1)}, {nm_m}]' is invalid for input of size {n * m}"
+        )
+    if not 0 <= nm_n <= nm_m:
+        raise RuntimeError("selected index k out of range")  # topk(nm_n) over nm_m entries
+    if R.stride(-1) != 1:
+        R = R.contiguous()
+    out = torch.empty(n, m, dtype=torch.float32, device=R.device)
+    keep = torch.empty(n, m, dtype=torch.uint8, device=R.device)
+    if n * m:
+        lib = _lib.load()
+        with torch.cuda.device(R.device):
+            rc = lib.ssl_project_nm(R.data_ptr(), R.stride(0), n, m, int(nm_n), int(nm_m),
+                                    _lib.dtype_code(R.dtype), out.data_ptr(), out.stride(0),
+                                    keep.data_ptr(), keep.stride(0), _lib.stream_ptr(R.device))
+        _lib.check(rc, "ssl_project_nm")
+    return out, keep.bool()
+
+
+def project_S_nm(R: torch.Tensor, nm_n: int, nm_m: int) -> torch.Tensor:
+    """Keep the nm_n largest entries in each consecutive group of nm_m (egar.py:284-292)."""
+    return project_nm(R, nm_n, nm_m)[0]

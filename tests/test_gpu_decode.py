@@ -13,9 +13,14 @@ Tolerances (max-abs normalised error):
   16-bit kernels: bit-exact where torch rounds the same values at the same
         points (rotary embedding, residual add), else one rounding of the
         output (bf16 1e-2, fp16 2e-3);
-  bf16 model logits 3e-2: the Hugging Face forward rounds to bf16 about ten
-        times per layer (every projection, norm, rotation, residual add and
-        the activation), each worth up to 2^-9 relative; measured 1.3e-2.
+  bf16 model logits: at most twice the error of the reference's own bf16
+        forward on the same weights, measured in the same test. That forward
+        (the Hugging Face model on the CPU in bf16 with each projection
+        computed as the reference GPU module does, _ReferenceSLR) is itself
+        1.2e-2 to 1.4e-2 from the float64 oracle on these models: it rounds to
+        bf16 about ten times per layer, each worth up to 2^-9 relative. No
+        bf16 implementation meets a 1e-2 bar on them, so the bar is set
+        relative to the reference's own rounding, with 3e-2 as a ceiling.
 """
 
 from __future__ import annotations
@@ -308,10 +313,46 @@ def test_silu_mul_matches_torch(gpu_device):
 # ---------------------------------------------------------------- engine --
 
 
-def _slr_pair(model_type, dtype, kv_heads, dev, seed=0, head_dim=64, heads=4, layers=2, nm=False):
-    """An SLR-compressed model on the GPU and its dense float64 twin on the CPU
-    (every projection W = A·B + S from the same dtype-valued factors). With
-    `nm`, S is 2:4-sparse along the input features (two of every four kept)."""
+class _ReferenceSLR(torch.nn.Module):
+    """The reference GPU modules' arithmetic on the CPU, in the model's dtype.
+    Block S (ssalaad/efficient/ls_linear.py:124-137): F.linear(F.linear(x, B),
+    A) rounded as torch rounds it, then x·Sᵀ accumulated in fp32 onto that
+    output and rounded once, as the in-place op does (addmm_inplace.py:41-82).
+    2:4 S (ls_linear.py:211-219): y = F.linear(x, S), then y += latent·Aᵀ
+    with one rounding (addmm_), latent = F.linear(x, B)."""
+
+    def __init__(self, A, B, S_dense, nm=False):
+        super().__init__()
+        self.A, self.B, self.S, self.nm = A, B, S_dense, nm
+
+    def forward(self, x):
+        F = torch.nn.functional
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        if self.nm:
+            latent = F.linear(x2, self.B)
+            y = F.linear(x2, self.S)
+            y = (y.float() + latent.float() @ self.A.float().t()).to(x.dtype)
+        else:
+            y = F.linear(F.linear(x2, self.B), self.A)
+            y = (y.float() + x2.float() @ self.S.float().t()).to(x.dtype)
+        return y.reshape(*shape[:-1], y.shape[-1])
+
+
+def _slr_pair(*args, **kwargs):
+    model, dense, _ = _slr_triple(*args, **kwargs)
+    return model, dense
+
+
+def _slr_triple(model_type, dtype, kv_heads, dev, seed=0, head_dim=64, heads=4, layers=2,
+                nm=False):
+    """An SLR-compressed model on the GPU, its dense float64 twin on the CPU
+    (every projection W = A·B + S from the same dtype-valued factors) and, for
+    16-bit dtypes, the same model on the CPU with the reference module's
+    arithmetic in that dtype (None for fp32). With `nm`, S is 2:4-sparse along
+    the input features (two of every four kept). dev=None builds no GPU model."""
+    import copy
+
     from ssalaad_amd import LRSLinear
     from ssalaad_amd.bundle import build_model_from_config
 
@@ -332,6 +373,7 @@ def _slr_pair(model_type, dtype, kv_heads, dev, seed=0, head_dim=64, heads=4, la
             else:
                 prm.copy_(0.1 * torch.randn(prm.shape, generator=g))
     model = model.to(dtype)
+    mirror = copy.deepcopy(model).eval() if dtype != torch.float32 else None
     dense = build_model_from_config(cfg, attn_implementation="eager").double()
     dense.load_state_dict({k: t.double() for k, t in model.state_dict().items()})
     p, r = 32, 32
@@ -357,20 +399,44 @@ def _slr_pair(model_type, dtype, kv_heads, dev, seed=0, head_dim=64, heads=4, la
                 with torch.no_grad():
                     dense.get_submodule(f"model.layers.{li}.{part}.{proj}").weight.copy_(
                         A.double() @ B.double() + Sd.double())
-                setattr(parent, proj, LRSLinear(A.to(dev), B.to(dev), Sd.to(dev), in_features=m,
-                                                out_features=n, nm_n=2, nm_m=4))
+                if mirror is not None:
+                    setattr(mirror.get_submodule(f"model.layers.{li}.{part}"), proj,
+                            _ReferenceSLR(A, B, Sd, nm=True))
+                if dev is not None:
+                    setattr(parent, proj, LRSLinear(A.to(dev), B.to(dev), Sd.to(dev),
+                                                    in_features=m, out_features=n, nm_n=2, nm_m=4))
                 continue
             with torch.no_grad():
                 dense.get_submodule(f"model.layers.{li}.{part}.{proj}").weight.copy_(
                     A.double() @ B.double() + S.to_dense().double())
+            if mirror is not None:
+                setattr(mirror.get_submodule(f"model.layers.{li}.{part}"), proj,
+                        _ReferenceSLR(A, B, S.to_dense()))
+            if dev is None:
+                continue
             setattr(parent, proj, LRSLinear(
                 A.to(dev), B.to(dev), torch.sparse_bsr_tensor(crow.to(dev), (slots % NBK).to(dev),
                                                               vals.to(dev), size=(n, m)),
                 in_features=m, out_features=n, block_p=p, block_q=p))
-    return model.to(dev).eval(), dense.eval()
+    return (model.to(dev).eval() if dev is not None else None), dense.eval(), mirror
 
 
-TOL_MODEL = {torch.float32: 1e-5, torch.bfloat16: 3e-2}
+TOL_MODEL = {torch.float32: 1e-5, torch.bfloat16: 3e-2}  # bf16: the ceiling of the relative bar
+BF16_VS_REFERENCE = 2.0
+
+
+def _mirror_logits(mirror, ids):
+    """Full-sequence logits of the reference-arithmetic CPU model (float32 copy)."""
+    with torch.no_grad():
+        return mirror(input_ids=ids, use_cache=False).logits.float().numpy()
+
+
+def _bar(dtype, ref_err):
+    """The logits bar: 1e-5 for fp32; for 16-bit, twice the reference's own
+    error (ref_err) up to the ceiling."""
+    if dtype == torch.float32:
+        return TOL_MODEL[dtype]
+    return min(TOL_MODEL[dtype], BF16_VS_REFERENCE * ref_err)
 
 
 @pytest.mark.parametrize("model_type,kv_heads,head_dim,heads", [
@@ -380,20 +446,24 @@ TOL_MODEL = {torch.float32: 1e-5, torch.bfloat16: 3e-2}
 def test_engine_steps_match_the_oracle(model_type, kv_heads, head_dim, heads, dtype, gpu_device):
     from ssalaad_amd import DecodeEngine
 
-    model, dense = _slr_pair(model_type, dtype, kv_heads, gpu_device, head_dim=head_dim,
-                             heads=heads)
+    model, dense, mirror = _slr_triple(model_type, dtype, kv_heads, gpu_device, head_dim=head_dim,
+                                       heads=heads)
     P = dor.params_from_hf(dense)
     B, T = 3, 12
     ids = torch.randint(0, 384, (B, T), generator=torch.Generator().manual_seed(7))
+    ref = _mirror_logits(mirror, ids) if mirror is not None else None
     eng = DecodeEngine(model, max_batch=4, max_context=T)
     cache = dor.KVCache.empty(len(P.layers), B, P.kv_heads, T, P.head_dim)
-    worst = 0.0
+    worst = ref_worst = 0.0
     for t in range(T):
         got = eng.step(ids[:, t], [t] * B).float().cpu().numpy()
         want = dor.decode_step(P, cache, ids[:, t].numpy(), [t] * B)
         worst = max(worst, _err(got, want))
-    print(f"[decode] {model_type} kv{kv_heads} hd{head_dim} {dtype}: worst logits error {worst:.2e}")
-    assert worst <= TOL_MODEL[dtype]
+        if ref is not None:
+            ref_worst = max(ref_worst, _err(ref[:, t], want))
+    print(f"[decode] {model_type} kv{kv_heads} hd{head_dim} {dtype}: worst logits error "
+          f"{worst:.2e} (reference arithmetic: {ref_worst:.2e})")
+    assert worst <= _bar(dtype, ref_worst)
 
 
 @pytest.mark.parametrize("seed", range(12))
@@ -411,17 +481,23 @@ def test_random_engine_configs_match_the_oracle(seed, gpu_device):
     hd = int(rng.choice([64, 128, 256]))
     dtype = (torch.float32, torch.bfloat16)[int(rng.integers(2))]
     B, T = int(rng.integers(1, 5)), int(rng.integers(4, 21))
-    model, dense = _slr_pair(model_type, dtype, kvh, gpu_device, seed=seed, head_dim=hd,
-                             heads=heads)
+    model, dense, mirror = _slr_triple(model_type, dtype, kvh, gpu_device, seed=seed, head_dim=hd,
+                                       heads=heads)
     P = dor.params_from_hf(dense)
     ids = torch.randint(0, 384, (B, T), generator=torch.Generator().manual_seed(seed))
+    ref = _mirror_logits(mirror, ids) if mirror is not None else None
     eng = DecodeEngine(model, max_batch=B, max_context=T)
     cache = dor.KVCache.empty(len(P.layers), B, P.kv_heads, T, P.head_dim)
     case = (seed, model_type, heads, kvh, hd, dtype, B, T)
+    errs, ref_errs = [], []
     for t in range(T):
         got = eng.step(ids[:, t], [t] * B).float().cpu().numpy()
         want = dor.decode_step(P, cache, ids[:, t].numpy(), [t] * B)
-        assert _err(got, want) <= TOL_MODEL[dtype], (case, t)
+        errs.append(_err(got, want))
+        if ref is not None:
+            ref_errs.append(_err(ref[:, t], want))
+    worst, ref_worst = max(errs), max(ref_errs, default=0.0)
+    assert worst <= _bar(dtype, ref_worst), (case, worst, ref_worst)
 
 
 @pytest.mark.parametrize("model_type,kv_heads", [("llama", 2), ("qwen3", 4)])
@@ -430,18 +506,23 @@ def test_engine_with_2to4_projections_matches_the_oracle(model_type, kv_heads, g
     and the decode step on packed 2:4 blocks, against the oracle at every step."""
     from ssalaad_amd import DecodeEngine
 
-    model, dense = _slr_pair(model_type, torch.bfloat16, kv_heads, gpu_device, seed=11, nm=True)
+    model, dense, mirror = _slr_triple(model_type, torch.bfloat16, kv_heads, gpu_device, seed=11,
+                                       nm=True)
     assert all(getattr(m, "kind", "") == "nm" for n_, m in model.named_modules()
                if n_.endswith(("q_proj", "down_proj")))
     P = dor.params_from_hf(dense)
     B, T = 2, 10
     ids = torch.randint(0, 384, (B, T), generator=torch.Generator().manual_seed(12))
+    ref = _mirror_logits(mirror, ids)
     eng = DecodeEngine(model, max_batch=B, max_context=T)
     cache = dor.KVCache.empty(len(P.layers), B, P.kv_heads, T, P.head_dim)
+    errs, ref_errs = [], []
     for t in range(T):
         got = eng.step(ids[:, t], [t] * B).float().cpu().numpy()
         want = dor.decode_step(P, cache, ids[:, t].numpy(), [t] * B)
-        assert _err(got, want) <= TOL_MODEL[torch.bfloat16], t
+        errs.append(_err(got, want))
+        ref_errs.append(_err(ref[:, t], want))
+    assert max(errs) <= _bar(torch.bfloat16, max(ref_errs)), (max(errs), max(ref_errs))
 
 
 def test_engine_ragged_positions_and_batch_sizes(gpu_device):

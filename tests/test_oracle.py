@@ -431,3 +431,70 @@ def test_project_blocks_counts_nan_and_inf_blocks_as_largest_like_torch():
         assert np.array_equal(keep, _torch_project(M, n_keep, 2, 2))
     _, keep = orc.project_blocks(M, 2, 2, 2)
     assert keep[1, 1] and keep[3, 0]
+
+
+# ------------------------------------------------------- N:M projection --
+
+
+def _torch_project_nm(R, nm_n, nm_m):
+    """The routine egar.py:284-292 calls: |R| top-k per group, scatter, multiply."""
+    R3 = torch.from_numpy(np.asarray(R, np.float32)).view(R.shape[0], -1, nm_m)
+    _, top = R3.abs().topk(nm_n, dim=-1)
+    mask = torch.zeros_like(R3, dtype=torch.bool)
+    mask.scatter_(-1, top, True)
+    return (R3 * mask.float()).view(R.shape).numpy(), mask.view(R.shape).numpy()
+
+
+def _tie_free(n, m, seed):
+    """Entries with distinct magnitudes (a permutation of spaced values, random signs)."""
+    rng = np.random.default_rng(seed)
+    mag = (1.0 + rng.permutation(n * m) * 1e-3).astype(np.float32)
+    return (mag * rng.choice([-1.0, 1.0], n * m)).astype(np.float32).reshape(n, m)
+
+
+def test_project_nm_reference_case():
+    """tests/test_ssalaad.py:222-223."""
+    R = np.array([[4.0, 1.0, 3.0, 2.0, 0.5, 9.0, 0.1, 7.0]], np.float32)
+    out, mask = orc.project_nm(R, 2, 4)
+    assert out[0].tolist() == [4, 0, 3, 0, 0, 9, 0, 7]
+    assert mask[0].tolist() == [True, False, True, False, False, True, False, True]
+
+
+@pytest.mark.parametrize("nm_n,nm_m", [(2, 4), (1, 4), (3, 4), (4, 8), (1, 2), (8, 16), (5, 7)])
+def test_project_nm_matches_torch_topk_without_ties(nm_n, nm_m):
+    R = _tie_free(6, 4 * nm_m, seed=nm_m)
+    out, mask = orc.project_nm(R, nm_n, nm_m)
+    want, wmask = _torch_project_nm(R, nm_n, nm_m)
+    assert np.array_equal(mask, wmask)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))  # bits, −0 included
+
+
+def test_project_nm_keeps_the_largest_subset_by_brute_force():
+    from itertools import combinations
+
+    R = _tie_free(3, 10, seed=4)
+    for nm_n in range(6):
+        _, mask = orc.project_nm(R, nm_n, 5)
+        for row in range(3):
+            for g in range(2):
+                vals = np.abs(R[row, 5 * g:5 * g + 5].astype(np.float64))
+                best = max(combinations(range(5), nm_n), key=lambda s: sum(vals[list(s)]))
+                assert sorted(np.flatnonzero(mask[row, 5 * g:5 * g + 5]).tolist()) == sorted(best)
+
+
+def test_project_nm_closed_forms_and_special_values():
+    R = np.array([[-1.0, 2.0, -0.0, np.inf, np.nan, -3.0, 0.5, 0.25]], np.float32)
+    out, mask = orc.project_nm(R, 4, 4)           # keep all: R·1
+    assert mask.all() and np.array_equal(out.view(np.uint32), (R * np.float32(1)).view(np.uint32))
+    out, mask = orc.project_nm(R, 0, 4)           # keep none: R·0 (−0, NaN for inf and NaN)
+    assert not mask.any()
+    assert np.array_equal(np.isnan(out), np.isnan(R * np.float32(0)))
+    assert np.signbit(out[0, 0]) and not np.signbit(out[0, 1])
+    out, mask = orc.project_nm(R, 1, 4)           # NaN counts as the largest magnitude
+    assert mask[0].tolist() == [False, False, False, True, True, False, False, False]
+    ties = np.array([[1.0, -1.0, 1.0, 1.0]], np.float32)
+    assert orc.project_nm(ties, 2, 4)[1][0].tolist() == [True, True, False, False]  # lower index
+    with pytest.raises(ValueError):
+        orc.project_nm(R, 2, 3)                   # m not a multiple of nm_m
+    with pytest.raises(ValueError):
+        orc.project_nm(R, 5, 4)
