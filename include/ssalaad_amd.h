@@ -59,7 +59,9 @@ const char* ssl_last_error(void);
  *   SSL_DEBUG_PREFILL_TILE      0: the library picks the prefill row tile;
  *                               1: always the narrow tile (128 token rows ×
  *                               64 output features); 2: always the tall one
- *                               (256 × 64).
+ *                               (256 × 64). Either also sends fp32 calls of
+ *                               ssl_prefill_min_rows() rows or more to the
+ *                               prefill kernels whatever their size.
  *   SSL_DEBUG_WAIT_POLLS        polls before a bounded wait gives up (0: the
  *                               default of several seconds).
  *   SSL_DEBUG_WAIT_UNREACHABLE  nonzero: every wait of the fused kernel targets
@@ -106,44 +108,48 @@ int ssl_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB
 
 /* Prefill plan (host side, integer only): the row kernels used for calls with
  * many token rows give one workgroup `group` block-rows at once (group · p =
- * 128 or 64 output features) and walk the union of their block columns in
- * steps of 64 columns, E = 64 / p union entries per step, so each tile of x
- * feeds every block of that column in the group. Groups are consecutive runs of
- * `group` listed rows (`rows` NULL = every row 0..NB-1).
+ * 64 output features) and walk the union of their block columns in steps of
+ * step_cols columns (64 for 16-bit activations, 32 for fp32: 128 bytes of a
+ * row either way), E = step_cols / p union entries per step, so each tile of
+ * x feeds every block of that column in the group. Groups are consecutive runs
+ * of `group` listed rows (`rows` NULL = every row 0..NB-1).
  *   groups  (2 + group) int32 per group:  {step_begin, step_end, row_0 .. row_{group-1}}
  *           (row −1: none; the last group may be short)
- *   steps   ssl_prefill_step_ints(p, group) int32 per step:
+ *   steps   ssl_prefill_step_ints(p, group, step_cols) int32 per step:
  *           {mask, col_0 .. col_{E-1}, W[4][IB][E]}
  *           col_e: first x column of entry e (−1 past the last entry);
  *           W[w][i][e] = blk[e][(8·(w + 4i)) / p]: the BSR block index of that
  *           slot's row at entry e's column, or −1 (IB = group·p / 32: the row
  *           kernel's 4 waves each load IB runs of 8 weight rows per step, and
  *           each finds its block indices in one place);
- *           mask bit (h·group + g): slot g holds a block in the step's 32-column
- *           half h (h = 0, 1). Entries ascend by column; a column repeated within
- *           one row starts another entry. Padding words are −1.
- * Call once with NULL outputs for the counts. p ∈ {16, 32, 64} and group · p =
- * 64 (the row kernel's tiles; ssl_prefill_step_ints is 0 otherwise).
- * The structure is checked as for ssl_plan_build. */
-int32_t ssl_prefill_step_ints(int32_t block_p, int32_t group);
+ *           mask bit (h·group + g): slot g holds a block in half h (h = 0, 1)
+ *           of the step's columns. Entries ascend by column; a column repeated
+ *           within one row starts another entry. Padding words are −1.
+ * Call once with NULL outputs for the counts. step_cols ∈ {32, 64}, p divides
+ * step_cols and group · p = 64 (the row kernel's tiles;
+ * ssl_prefill_step_ints is 0 otherwise). The structure is checked as for
+ * ssl_plan_build. */
+int32_t ssl_prefill_step_ints(int32_t block_p, int32_t group, int32_t step_cols);
 int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB,
                            int64_t NBK, const int32_t* rows_host, int64_t n_rows, int32_t block_p,
-                           int32_t group, int32_t* groups_out, int64_t groups_capacity,
-                           int32_t* steps_out, int64_t steps_capacity, int64_t* n_groups,
-                           int64_t* n_steps);
-/* Calls with at least this many token rows and 16-bit activations run the
- * prefill kernels, which need a prefill plan built with this group size for
- * the call's M and row count (n_rows: the rows the plans list; for a grouped
- * call, all its linears' rows together). */
+                           int32_t group, int32_t step_cols, int32_t* groups_out,
+                           int64_t groups_capacity, int32_t* steps_out, int64_t steps_capacity,
+                           int64_t* n_groups, int64_t* n_steps);
+/* Calls with at least this many token rows run the prefill kernels (16-bit
+ * activations with 16/32/64 square blocks, fp32 with 16/32), which need a
+ * prefill plan built with this group size for the call's M and row count
+ * (n_rows: the rows the plans list; for a grouped call, all its linears' rows
+ * together). ssl_prefill_step_cols gives the plan's step width for a dtype. */
+int32_t ssl_prefill_step_cols(int32_t dtype);
 int64_t ssl_prefill_min_rows(void);
 int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q);
 /* 1 if a fused SLR call (ssl_slr_forward, ssl_slr_forward_group) with block
  * storage, M token rows and n_rows block-rows over all its linears takes the
  * prefill kernels (and so needs their plans), 0 if it streams. At least
- * ssl_prefill_min_rows() rows and 16-bit activations, except 32×32 or smaller
- * blocks up to 512 rows and calls of fewer than 100 block-rows at the minimum
- * row count. The in-place op (ssl_bsr_addmm_inplace) keeps the plain
- * threshold. */
+ * ssl_prefill_min_rows() rows, except 32×32 or smaller 16-bit blocks up to
+ * 512 rows and calls of fewer than 100 block-rows at the minimum row count;
+ * fp32 calls only when the row kernel's grid fills the device. The in-place
+ * op (ssl_bsr_addmm_inplace) keeps the plain threshold (fp32: streams). */
 int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q,
                               int32_t dtype);
 

@@ -17,6 +17,8 @@ per step, from a key/value cache:
   rotate          modeling_llama.py:130-160 (rotate_half, apply_rotary_pos_emb)
   attention       modeling_llama.py:191-214 (eager_attention_forward; causal,
                   so a decode query sees every cached position up to its own)
+  forward         the same forward over whole sequences at once (every position's
+                  logits, causal attention), for prefill-sized model checks
   decode_step     modeling_llama.py:217-325 (LlamaAttention, LlamaDecoderLayer),
                   :163-177 (LlamaMLP with silu), :347-418 (LlamaModel.forward),
                   :421-493 (LlamaForCausalLM: logits = lm_head(norm(h)));
@@ -29,8 +31,10 @@ decode_step, run token by token from an empty cache, reproduces the logits of
 transformers' LlamaForCausalLM / Qwen3ForCausalLM full-sequence forward in
 a float64 model at every position, for MHA and grouped-query attention, with
 and without projection biases. The bound is 2e-6 (normalised): transformers
-evaluates RMSNorm and the rotary tables in fp32 even in a float64 model. rms_norm and rotate are also checked against
-their closed forms (unit RMS, norm preservation of the rotation).
+evaluates RMSNorm and the rotary tables in fp32 even in a float64 model.
+forward is pinned the same way and against decode_step at every position.
+rms_norm and rotate are also checked against their closed forms (unit RMS,
+norm preservation of the rotation).
 """
 
 from __future__ import annotations
@@ -168,6 +172,44 @@ def decode_step(P: DecoderParams, cache: KVCache, tokens, positions) -> np.ndarr
             h = h + _linear(d, "down", g / (1.0 + np.exp(-g)) * u)
         out.append(P.lm_head @ rms_norm(h, P.norm, P.eps))
     return np.stack(out)
+
+
+def forward(P: DecoderParams, ids) -> np.ndarray:
+    """Logits [batch, T, vocab] of whole sequences ids [batch, T] (positions
+    0 .. T−1, causal attention): decode_step's arithmetic on every position at once."""
+    ids = np.asarray(ids)
+    Bn, T = ids.shape
+    hd, H, KH = P.head_dim, P.heads, P.kv_heads
+    cos, sin = rope_tables(P.inv_freq, range(T), P.attention_scaling)  # [T, hd]
+    causal = np.triu(np.full((T, T), -np.inf), 1)
+
+    def lin(d, name, x):
+        y = x @ d[name].T
+        if d.get(name + "_bias") is not None:
+            y = y + d[name + "_bias"]
+        return y
+
+    h = P.embed[ids].astype(np.float64)                                # [B, T, hidden]
+    for d in P.layers:
+        x = rms_norm(h, d["in_norm"], P.eps)
+        q = lin(d, "q", x).reshape(Bn, T, H, hd).transpose(0, 2, 1, 3)   # [B, H, T, hd]
+        k = lin(d, "k", x).reshape(Bn, T, KH, hd).transpose(0, 2, 1, 3)
+        v = lin(d, "v", x).reshape(Bn, T, KH, hd).transpose(0, 2, 1, 3)
+        if P.qk_norm:
+            q = rms_norm(q, d["q_norm"], P.eps)
+            k = rms_norm(k, d["k_norm"], P.eps)
+        q, k = rotate(q, cos, sin), rotate(k, cos, sin)
+        rep = H // KH
+        k = np.repeat(k, rep, axis=1)
+        v = np.repeat(v, rep, axis=1)
+        s = q @ k.transpose(0, 1, 3, 2) * hd ** -0.5 + causal             # [B, H, T, T]
+        pr = np.exp(s - s.max(axis=-1, keepdims=True))
+        a = (pr / pr.sum(axis=-1, keepdims=True)) @ v                     # [B, H, T, hd]
+        h = h + lin(d, "o", a.transpose(0, 2, 1, 3).reshape(Bn, T, H * hd))
+        x = rms_norm(h, d["post_norm"], P.eps)
+        g = lin(d, "gate", x)
+        h = h + lin(d, "down", g / (1.0 + np.exp(-g)) * lin(d, "up", x))
+    return rms_norm(h, P.norm, P.eps) @ P.lm_head.T
 
 
 def greedy(P: DecoderParams, prompt: np.ndarray, max_new_tokens: int) -> np.ndarray:

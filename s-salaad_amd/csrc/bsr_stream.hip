@@ -42,8 +42,11 @@ int latent_split_max(int64_t M, int64_t m_pad) {
 bool supported_block(int p, int q) {
   return (p == 16 || p == 32 || p == 48 || p == 64) && q >= 16 && q <= 256 && q % 16 == 0;
 }
-// Block shapes the prefill kernels take (square 16, 32 or 64).
-bool prefill_block(int p, int q) { return p == q && (p == 16 || p == 32 || p == 64); }
+// Block shapes the prefill kernels take: square 16, 32 or 64 (fp32: 16 or 32,
+// which divide its 32-column steps).
+bool prefill_block(int p, int q, int dtype) {
+  return p == q && (p == 16 || p == 32 || (p == 64 && dtype != SSL_F32));
+}
 
 // k elements per lane of the sparse MFMA fragments for q-deep blocks.
 int stream_ke(int dtype, int q) { return (dtype != SSL_F32 && q % 32 == 0) ? 8 : 4; }
@@ -99,9 +102,11 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   const int64_t rows = (int64_t)L.MG * 16 * L.MT;
   int64_t off = 0;
   L.t_part = off;
-  if (M >= kPrefillMinM && dtype != SSL_F32) {
-    // prefill: the latent GEMM's K-split partials
-    const int ks = prefill_latent_split(M, r_pad, m_pad, device_cus());
+  if (M >= kPrefillMinM) {
+    // the prefill latent GEMM's K-split partials, or the streaming kernel's
+    // (calls of this size may take either kernel)
+    int ks = prefill_latent_split(M, r_pad, m_pad, device_cus());
+    if (ks < L.n_kc_max) ks = L.n_kc_max;
     if (ks > 1) off = align_up(off + 4 * (int64_t)ks * rows * r_pad, 256);
   } else if (L.n_kc_max > 1) {
     off = align_up(off + 4 * (int64_t)L.n_kc_max * rows * r_pad, 256);
@@ -140,15 +145,24 @@ extern "C" {
 int64_t ssl_prefill_min_rows(void) { return kPrefillMinM; }
 
 // Which kernels a fused call with block storage takes. The prefill kernels
-// from kPrefillMinM token rows with 16-bit activations, except where the
-// streaming kernel (one weight pass per 64-row token tile, the re-reads served
+// from kPrefillMinM token rows (fp32: when their grid fills the device),
+// except where the 16-bit streaming kernel (one weight pass per 64-row token tile, the re-reads served
 // by the caches) measured faster on MI355X: blocks of 32×32 or less up to 512
 // rows (LLaMA-1B gate 5461×2048 at 128 / 256 / 512 rows: 34.2 / 41.8 / 65.5 µs
 // prefill, 24.5 / 35.6 / 55.1 streaming), and calls of fewer than 100
 // block-rows up to 128 rows (4096×4096 with 64×64 blocks: 40.7 -> 31.9 µs).
 int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q,
                               int32_t dtype) {
-  if (dtype == SSL_F32 || M < kPrefillMinM || !prefill_block(block_p, block_q)) return 0;
+  if (M < kPrefillMinM || !prefill_block(block_p, block_q, dtype)) return 0;
+  if (dtype == SSL_F32) {
+    // fp32 runs 16 times fewer MFMA flops per cycle: the tiled kernels win once
+    // their grid fills the device; smaller calls keep the streaming kernel's
+    // finer split (LLaMA-60M shapes at 2048 rows: 512-wide outputs stream).
+    // A forced row tile (test hook) sends every such call to the tiled kernels.
+    if (debug_knobs().prefill_group != 0) return 1;
+    const int64_t items = ((M + 127) / 128) * ((n_rows + 64 / block_p - 1) / (64 / block_p));
+    return items >= device_cus() ? 1 : 0;
+  }
   if (block_p <= 32 && M <= 512) return 0;
   if (M <= kPrefillMinM && n_rows < 100) return 0;
   return 1;
@@ -156,13 +170,18 @@ int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_
 
 int64_t ssl_nm24_block_bytes(void) { return kNmBlockBytes; }
 
+int32_t ssl_prefill_step_cols(int32_t dtype) { return dtype == SSL_F32 ? 32 : 64; }
+
 int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q) {
-  if (!prefill_block(block_p, block_q)) return 1;
+  if (!(block_p == block_q && (block_p == 16 || block_p == 32 || block_p == 64))) return 1;
   return prefill_group(M, n_rows, block_p, device_cus());
 }
 
 int32_t ssl_bsr_addmm_takes_prefill(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype) {
-  return M >= kPrefillMinM && dtype != SSL_F32 && prefill_block(block_p, block_q);
+  // fp32: only under a forced row tile (test hook); the streaming kernel's
+  // finer split is the default for the op
+  return M >= kPrefillMinM && prefill_block(block_p, block_q, dtype) &&
+         (dtype != SSL_F32 || debug_knobs().prefill_group != 0);
 }
 
 int64_t ssl_bsr_addmm_counter_count(int64_t M, int64_t NB) {

@@ -188,28 +188,30 @@ static int32_t prefill_ib(int32_t block_p, int32_t group) {
   return block_p * group == 64 ? 2 : 0;  // the row kernel's tiles are 64 features wide
 }
 
-int32_t ssl_prefill_step_ints(int32_t block_p, int32_t group) {
-  if (block_p <= 0 || 64 % block_p || group < 1 || group > 16) return 0;
+int32_t ssl_prefill_step_ints(int32_t block_p, int32_t group, int32_t step_cols) {
+  if (step_cols != 32 && step_cols != 64) return 0;
+  if (block_p <= 0 || step_cols % block_p || group < 1 || group > 16) return 0;
   const int32_t ib = prefill_ib(block_p, group);
   if (ib == 0) return 0;
-  const int32_t E = 64 / block_p;
+  const int32_t E = step_cols / block_p;
   return (1 + E + 4 * ib * E + 3) / 4 * 4;
 }
 
 int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB,
                            int64_t NBK, const int32_t* rows_host, int64_t n_rows, int32_t block_p,
-                           int32_t group, int32_t* groups_out, int64_t groups_capacity,
-                           int32_t* steps_out, int64_t steps_capacity, int64_t* n_groups,
-                           int64_t* n_steps) {
+                           int32_t group, int32_t step_cols, int32_t* groups_out,
+                           int64_t groups_capacity, int32_t* steps_out, int64_t steps_capacity,
+                           int64_t* n_groups, int64_t* n_steps) {
   clear_error();
-  const int32_t stride = ssl_prefill_step_ints(block_p, group);
+  const int32_t stride = ssl_prefill_step_ints(block_p, group, step_cols);
   if (!crow_host || !n_groups || !n_steps || NB < 0 || stride == 0 ||
       (rows_host && n_rows < 0) || (groups_out && groups_capacity < 0) ||
       (steps_out && steps_capacity < 0))
     return fail(SSL_ERR_INVALID, "invalid prefill plan arguments");
   if (int rc = check_structure(crow_host, col_host, NB, NBK, rows_host, n_rows)) return rc;
   const int64_t nr = rows_host ? n_rows : NB;
-  const int E = 64 / block_p;  // union entries per 64-column step
+  const int E = step_cols / block_p;  // union entries per step
+  const int half = step_cols / 2;     // columns per mask half
   const int gstride = 2 + group;
   int64_t ng = 0, ns = 0;
   std::vector<std::array<int32_t, 3>> items;  // (col, slot, block)
@@ -257,8 +259,8 @@ int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, in
           r[1 + e] = en[0] * block_p;  // first x column of the entry
           for (int g = 0; g < group; ++g) {
             if (en[1 + g] < 0) continue;
-            // 32-column halves of the step this entry covers
-            const int h0 = (e * block_p) / 32, h1 = (e * block_p + block_p - 1) / 32;
+            // halves of the step this entry covers
+            const int h0 = (e * block_p) / half, h1 = (e * block_p + block_p - 1) / half;
             for (int h = h0; h <= h1; ++h) mask |= 1 << (h * group + g);
           }
           // each wave's loads: blk[e][slot(w, i)] at 1 + E + (w·ib + i)·E + e

@@ -1,6 +1,6 @@
 // Prefill-shaped SLR linear on gfx950: many token rows (M ≥ kPrefillMinM), 16-bit
-// activations. Two LDS-tiled MFMA GEMM kernels replace the row-streaming decode
-// kernel (which re-reads each weight row once per 64-token tile):
+// or fp32 activations. Two LDS-tiled MFMA GEMM kernels replace the row-streaming
+// decode kernel (which re-reads each weight row once per 64-token tile):
 //
 //   latent  t[M, r_pad] = x · Bᵀ                  dense GEMM (K split, fp32
 //                                                   partials summed in split order),
@@ -10,9 +10,10 @@
 //                       (+ bias, or + the old out for the in-place op)
 //
 // One engine runs both. A workgroup (4 waves) owns a BM × BN output tile and
-// walks a list of steps, each 64 columns of k. A step stages an A tile (BM × 64
-// of x or t) and a B tile (BN × 64 of weights, k-contiguous per output feature)
-// in LDS; wave (wm, wn) multiplies its TM × TN share with v_mfma_f32_16x16x32.
+// walks a list of steps, each 128 bytes of k (64 columns of 16-bit data, 32 of
+// fp32). A step stages an A tile (BM rows of x or t) and a B tile (BN rows of
+// weights, k-contiguous per output feature) in LDS; wave (wm, wn) multiplies
+// its TM × TN share with v_mfma_f32_16x16x32 (fp32: v_mfma_f32_16x16x4f32).
 // Tiles go from global memory straight into LDS (buffer loads with the lds
 // flag) through a ring of S stages: the loads of the next S − 1 steps are in
 // flight while one step computes, with one barrier per step.
@@ -48,21 +49,33 @@ namespace {
 
 constexpr int kPfThreads = 256;  // 4 waves
 constexpr int kXcds = 8;
-constexpr int kK = 64;           // k per step
+constexpr int kK = 64;           // 16-bit units per LDS row (128 bytes)
 constexpr uint32_t kOob = 0x80000000u;
 
 enum : int { K_ROWS_OP = 0, K_ROWS_FUSED = 1, K_LATENT = 2 };
 
-// 16-byte chunk with its 16-bit elements at and past `valid` set to zero.
+// 16-byte chunk with its elements (EB bytes each) at and past `valid` set to zero.
+template <int EB>
 __device__ __forceinline__ uint4 keep_first(uint4 v, int valid) {
   uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    const uint32_t lo = (2 * d < valid) ? (w[d] & 0xffffu) : 0u;
-    const uint32_t hi = (2 * d + 1 < valid) ? (w[d] & 0xffff0000u) : 0u;
-    w[d] = lo | hi;
+    if constexpr (EB == 4) {
+      w[d] = d < valid ? w[d] : 0u;
+    } else {
+      const uint32_t lo = (2 * d < valid) ? (w[d] & 0xffffu) : 0u;
+      const uint32_t hi = (2 * d + 1 < valid) ? (w[d] & 0xffff0000u) : 0u;
+      w[d] = lo | hi;
+    }
   }
   return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Element i of an activation-dtype array as fp32 bits stored back.
+template <int DT>
+__device__ __forceinline__ void store_elem(void* base, int64_t i, float v) {
+  if constexpr (DT == DT_F32) ((float*)base)[i] = v;
+  else ((uint16_t*)base)[i] = (uint16_t)to_bits<DT>(v);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -160,7 +173,10 @@ constexpr int pf_occupancy(int BM, int BN, int S) {
 // ---------------------------------------------------------------------------
 // The engine. KIND: K_ROWS_OP / K_ROWS_FUSED (rows of the block-sparse linear)
 // or K_LATENT (t = x·Bᵀ). P: block size (rows kernels). S: LDS stages (loads
-// of S − 1 steps in flight while one step computes).
+// of S − 1 steps in flight while one step computes). A step is 128 bytes of
+// every tile row: 64 k columns of 16-bit data (one v_mfma_f32_16x16x32 per
+// 32 k) or 32 of fp32 (four v_mfma_f32_16x16x4f32 per 16 k, element e of a
+// lane's 16-byte chunk in the e-th).
 //
 // Every kernel argument the step loop uses is read into a register before the
 // loop: the loop's waits and barriers are compiler barriers for memory, which
@@ -175,8 +191,11 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   constexpr int IA = T::IA, IB = T::IB, MTI = T::MTI, NTI = T::NTI;
   constexpr bool ROWS = KIND != K_LATENT;
   constexpr int G = ROWS ? BN / P : 1;
-  constexpr int E = ROWS ? 64 / P : 1;
-  constexpr int EB = 2;
+  constexpr int EB = Elem<DT>::bytes;
+  constexpr int CE = 16 / EB;       // elements per 16-byte chunk
+  constexpr int KS = 8 * CE;        // k columns per step
+  static_assert(!ROWS || KS % P == 0, "a step holds whole blocks");
+  constexpr int E = ROWS ? KS / P : 1;
   constexpr int kRecInts = (1 + E + 4 * IB * E + 3) / 4 * 4;  // ssl_prefill_step_ints(P, G)
   constexpr int LOADS = IA + IB;    // tile load instructions per wave per step
   // loads issued after a step's tile loads by the time that step is waited
@@ -187,7 +206,7 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   static_assert(!ROWS || S == 2, "rows kernels run two stages");
   constexpr int NRV = 1 + E + IB * E;  // words of a wave's record view
   static_assert(NRV <= 64, "a record view is one word per lane");
-  using MM = Mma<DT, 8>;
+  using MM = Mma<DT, DT == DT_F32 ? 4 : 8>;
   using Frag = typename MM::Frag;
   __shared__ __align__(1024) uint16_t lds[S][T::LDS];
 
@@ -218,7 +237,7 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
     const int tile = local / mb.ksplit;
     rt = tile % n_rt;
     m0 = (tile / n_rt) * BM;
-    const int units = a.m_pad / kK;
+    const int units = a.m_pad / KS;
     const int ku = (units + mb.ksplit - 1) / mb.ksplit;
     s_begin = kspl * ku;
     s_end = min(s_begin + ku, units);
@@ -228,7 +247,7 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
     gr = mb.groups + (int64_t)grp * (2 + G);
     s_begin = ld_word(gr, 0);
     n_sp = ld_word(gr, 1) - s_begin;
-    const int n_lr = (KIND == K_ROWS_FUSED) ? mb.r_pad / kK : 0;
+    const int n_lr = (KIND == K_ROWS_FUSED) ? mb.r_pad / KS : 0;
     s_end = s_begin + n_sp + n_lr;
   }
   const int U = s_end - s_begin;
@@ -241,8 +260,8 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   // and the column chunk that lands at position lane % 8 of that row.
   const int lrow = lane >> 3;
   const int kc = (lane & 7) ^ lrow;
-  const int e_t = (ROWS && E > 1) ? (kc * 8) / P : 0;  // rows kernels: this lane's entry of a step
-  const int kin = ROWS ? (kc * 8) % P : kc * 8;  // and its column within the entry
+  const int e_t = (ROWS && E > 1) ? (kc * CE) / P : 0;  // rows kernels: this lane's entry of a step
+  const int kin = ROWS ? (kc * CE) % P : kc * CE;  // and its column within the entry
 
   // ---- LDS byte addresses: stage 0's A rows 8·wid and B rows 8·wid
   const uint32_t la0 = lds_addr(&lds[0][8 * wid * kK]);
@@ -266,7 +285,7 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
     br = rsrc_words(mb.B, (int64_t)mb.r_pad * mb.ldb * EB);
 #pragma unroll
     for (int i = 0; i < IB; ++i)
-      bconst[i] = (uint32_t)(((int64_t)(rt * BN + 8 * (wid + 4 * i) + lrow) * mb.ldb + kc * 8) * EB);
+      bconst[i] = (uint32_t)(((int64_t)(rt * BN + 8 * (wid + 4 * i) + lrow) * mb.ldb + kc * CE) * EB);
 #pragma unroll
     for (int i = 0; i < IA; ++i) at_[i] = 0;
 #pragma unroll
@@ -283,12 +302,12 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
       ar = rsrc_words(mb.A, mb.A_bytes);
 #pragma unroll
       for (int i = 0; i < IA; ++i)
-        at_[i] = (uint32_t)((min(m0 + 8 * (wid + 4 * i) + lrow, M - 1) * mb.ldt + kc * 8) * EB);
+        at_[i] = (uint32_t)((min(m0 + 8 * (wid + 4 * i) + lrow, M - 1) * mb.ldt + kc * CE) * EB);
 #pragma unroll
       for (int i = 0; i < IB; ++i) {
         const int f = 8 * (wid + 4 * i) + lrow;
         const int row = ld_word(gr, 2 + (8 * (wid + 4 * i)) / P);
-        lroff[i] = row < 0 ? kOob : (uint32_t)(((int64_t)(row * P + f % P) * mb.lda + kc * 8) * EB);
+        lroff[i] = row < 0 ? kOob : (uint32_t)(((int64_t)(row * P + f % P) * mb.lda + kc * CE) * EB);
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) lr_mask |= (ld_word(gr, 2 + g) >= 0) ? (1 << g) | (1 << (G + g)) : 0;
@@ -332,9 +351,9 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
     int mask;
     const uint32_t la = la0 + (uint32_t)k * kStageBytes, lb = lb0 + (uint32_t)k * kStageBytes;
     if constexpr (KIND == K_LATENT) {
-      const int k0 = (s_begin + u) * kK;
-      const int col = k0 + kc * 8;
-      ragged = k0 + kK > m;
+      const int k0 = (s_begin + u) * KS;
+      const int col = k0 + kc * CE;
+      ragged = k0 + KS > m;
       xcol = col;
       const uint32_t xcb = col < m ? (uint32_t)(k0 * EB) : kOob;
 #pragma unroll
@@ -357,13 +376,13 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
         }
         if (m % P != 0) {  // only a ragged last block column cuts chunks
           xcol = c >= 0 ? c + kin : 0x3fffffff;
-          ragged = __builtin_amdgcn_ballot_w64(xcol + 8 > m) != 0;
+          ragged = __builtin_amdgcn_ballot_w64(xcol + CE > m) != 0;
         } else {
           xcol = 0;
           ragged = 0;
         }
       } else {
-        const uint32_t k0b = (uint32_t)((u - n_sp) * kK * EB);  // ranks (K_ROWS_FUSED only)
+        const uint32_t k0b = (uint32_t)((u - n_sp) * KS * EB);  // ranks (K_ROWS_FUSED only)
 #pragma unroll
         for (int i = 0; i < IA; ++i) dma16(tr, at_[i], k0b, la + i * kRowBytes32);
 #pragma unroll
@@ -379,11 +398,11 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   // ---- zero the x elements at and past in_features in a landed ragged stage
   auto fix_ragged = [&](int k, int xcol) {
     const int valid = m - xcol;
-    if (valid < 8) {
+    if (valid < CE) {
 #pragma unroll
       for (int i = 0; i < IA; ++i) {
         uint16_t* q = &lds[k][lds_chunk(8 * (wid + 4 * i) + lrow, kc)];
-        *(uint4*)q = valid <= 0 ? make_uint4(0, 0, 0, 0) : keep_first(*(const uint4*)q, valid);
+        *(uint4*)q = valid <= 0 ? make_uint4(0, 0, 0, 0) : keep_first<EB>(*(const uint4*)q, valid);
       }
     }
   };
@@ -404,13 +423,13 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
 #pragma unroll
       for (int mt = 0; mt < MTI; ++mt) {
         const uint4 v = *(const uint4*)(buf + lds_chunk(wm * T::TM + 16 * mt + c, ks * 4 + gq));
-        af[ks][mt].d[0] = v.x; af[ks][mt].d[1] = v.y; af[ks][mt].d[2] = v.z; af[ks][mt].d[3] = v.w;
+        af[ks][mt] = __builtin_bit_cast(Frag, v);
       }
 #pragma unroll
       for (int nt = 0; nt < NTI; ++nt) {
         const uint4 v =
             *(const uint4*)(buf + lds_chunk(BM + wn * T::TN + 16 * nt + c, ks * 4 + gq));
-        bf[ks][nt].d[0] = v.x; bf[ks][nt].d[1] = v.y; bf[ks][nt].d[2] = v.z; bf[ks][nt].d[3] = v.w;
+        bf[ks][nt] = __builtin_bit_cast(Frag, v);
       }
     }
 #pragma unroll
@@ -460,7 +479,7 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   // stores below could otherwise alias the argument segment and force a
   // reload per store.
   if constexpr (KIND == K_LATENT) {
-    uint16_t* const t_out = (uint16_t*)mb.t;
+    void* const t_out = mb.t;
     float* const t_part = mb.tpart;
     const int64_t ldt = mb.ldt;
     const bool whole = mb.ksplit == 1;
@@ -475,14 +494,14 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
           const int col = rt * BN + wn * T::TN + 16 * nt + c;
           const float v = acc[mt][nt][e];
           if (whole) {
-            t_out[(int64_t)r * ldt + col] = (uint16_t)to_bits<DT>(v);
+            store_elem<DT>(t_out, (int64_t)r * ldt + col, v);
           } else {
             t_part[((int64_t)kspl * M + r) * ldt + col] = v;
           }
         }
       }
   } else {
-    uint16_t* const y_out = (uint16_t*)mb.y;
+    void* const y_out = mb.y;
     const int64_t ldy = mb.ldy;
     const void* const bias = mb.bias;
 #pragma unroll
@@ -499,11 +518,11 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
         for (int e = 0; e < 4; ++e) {
           const int r = m0 + wm * T::TM + 16 * mt + 4 * gq + e;
           if (r >= M) continue;
-          uint16_t* yp = y_out + (int64_t)r * ldy + col;
+          const int64_t yi = (int64_t)r * ldy + col;
           float o = acc[mt][nt][e];
           if constexpr (KIND == K_ROWS_FUSED) o += bv;
-          else o += load_scalar<DT>(yp, 0);
-          *yp = (uint16_t)to_bits<DT>(o);
+          else o += load_scalar<DT>(y_out, yi);
+          store_elem<DT>(y_out, yi, o);
         }
     }
   }
@@ -556,7 +575,9 @@ hipError_t launch_rows_p(const PfArgs& rows, int P, int G, hipStream_t s) {
   switch (P) {
     case 16: return launch_rows<DT, KIND, 16>(rows, G, s);
     case 32: return launch_rows<DT, KIND, 32>(rows, G, s);
-    case 64: return launch_rows<DT, KIND, 64>(rows, G, s);
+    case 64:
+      if constexpr (DT != DT_F32) return launch_rows<DT, KIND, 64>(rows, G, s);
+      break;  // fp32 steps are 32 columns: 64-wide blocks stream
   }
   return hipErrorInvalidValue;
 }
@@ -616,6 +637,7 @@ hipError_t prefill_launch_fused(int dtype, int P, int G, const PfArgs& rows, con
   switch (dtype) {
     case SSL_BF16: return launch_fused<DT_BF16>(rows, lat, comb, P, G, stream);
     case SSL_F16: return launch_fused<DT_F16>(rows, lat, comb, P, G, stream);
+    case SSL_F32: return launch_fused<DT_F32>(rows, lat, comb, P, G, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -624,6 +646,7 @@ hipError_t prefill_launch_op(int dtype, int P, int G, const PfArgs& rows, hipStr
   switch (dtype) {
     case SSL_BF16: return launch_rows_p<DT_BF16, K_ROWS_OP>(rows, P, G, stream);
     case SSL_F16: return launch_rows_p<DT_F16, K_ROWS_OP>(rows, P, G, stream);
+    case SSL_F32: return launch_rows_p<DT_F32, K_ROWS_OP>(rows, P, G, stream);
   }
   return hipErrorInvalidValue;
 }

@@ -54,11 +54,12 @@ _SIGNATURES = {
          _c_i64, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p,
          _c_i64, _c_p],
     ),
-    "ssl_prefill_step_ints": (_c_i32, [_c_i32, _c_i32]),
+    "ssl_prefill_step_ints": (_c_i32, [_c_i32, _c_i32, _c_i32]),
+    "ssl_prefill_step_cols": (_c_i32, [_c_i32]),
     "ssl_prefill_plan_build": (
         ctypes.c_int,
-        [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_p, _c_i64, _c_p, _c_i64,
-         _c_p, _c_p],
+        [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p,
+         _c_i64, _c_p, _c_p],
     ),
     "ssl_prefill_min_rows": (_c_i64, []),
     "ssl_nm24_block_bytes": (_c_i64, []),

@@ -152,11 +152,12 @@ def build_plan(
 
 def build_prefill_plan(
     crow_host: np.ndarray, col_host: np.ndarray, NBK: int, rows_host: np.ndarray | None,
-    block_p: int, group: int
+    block_p: int, group: int, step_cols: int = 64
 ) -> tuple[np.ndarray, np.ndarray, int]:
-    """Group table [n_groups, 2 + group] and 64-column step records
-    [n_steps, ssl_prefill_step_ints(p, group)] (int32) for the prefill row
-    kernels (ssl_prefill_plan_build)."""
+    """Group table [n_groups, 2 + group] and step records of `step_cols`
+    columns (64 for 16-bit activations, 32 for fp32: ssl_prefill_step_cols)
+    [n_steps, ssl_prefill_step_ints(p, group, step_cols)] (int32) for the
+    prefill row kernels (ssl_prefill_plan_build)."""
     lib = _lib.load()
     crow_host = np.ascontiguousarray(crow_host, dtype=np.int32)
     col_host = np.ascontiguousarray(col_host, dtype=np.int32)
@@ -165,12 +166,13 @@ def build_prefill_plan(
     if rows_host is not None:
         rows_host = np.ascontiguousarray(rows_host, dtype=np.int32)
         rows_p, n_rows = rows_host.ctypes.data, rows_host.shape[0]
-    stride = int(lib.ssl_prefill_step_ints(block_p, group))
+    stride = int(lib.ssl_prefill_step_ints(block_p, group, step_cols))
     if stride <= 0:
-        raise ValueError(f"no prefill plan for block {block_p} and group {group}")
+        raise ValueError(f"no prefill plan for block {block_p}, group {group} and "
+                         f"{step_cols}-column steps")
     ng, ns = ctypes.c_int64(), ctypes.c_int64()
     args = (crow_host.ctypes.data, col_host.ctypes.data if col_host.size else None, NB, NBK,
-            rows_p, n_rows, block_p, group)
+            rows_p, n_rows, block_p, group, step_cols)
     rc = lib.ssl_prefill_plan_build(*args, None, 0, None, 0, ctypes.byref(ng), ctypes.byref(ns))
     _lib.check(rc, "ssl_prefill_plan_build")
     groups = np.zeros((max(ng.value, 1), 2 + group), dtype=np.int32)

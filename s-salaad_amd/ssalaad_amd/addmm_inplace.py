@@ -108,14 +108,16 @@ def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_by
     if lib.ssl_bsr_addmm_takes_prefill(M, block_p, block_q, dt) and plan.n_chunks > 0:
         # the prefill kernel's groups list the planned rows (active rows with blocks)
         G = int(lib.ssl_prefill_group(M, plan.n_chunks, block_p, block_q))
-        pf = sp.plans.get(("pf", G))
+        step_cols = int(lib.ssl_prefill_step_cols(dt))
+        pf = sp.plans.get(("pf", G, step_cols))
         if pf is None:
             crow_h, _ = _validated_host_structure(crow, col, active_rows, values.shape[0], NB_K)
             col_h = col.detach().to("cpu").numpy().astype(np.int32)
             rows_h = plan.table.cpu().numpy()[: plan.n_chunks, 0].astype(np.int32)
-            groups, steps, ng = _runtime.build_prefill_plan(crow_h, col_h, NB_K, rows_h, block_p, G)
+            groups, steps, ng = _runtime.build_prefill_plan(crow_h, col_h, NB_K, rows_h, block_p, G,
+                                                            step_cols)
             pf = _runtime.DevicePrefillPlan(groups, steps, ng, G, crow.device)
-            sp.plans[("pf", G)] = pf
+            sp.plans[("pf", G, step_cols)] = pf
     return plan, pf
 
 

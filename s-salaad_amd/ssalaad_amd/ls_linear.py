@@ -173,8 +173,9 @@ class _KernelState:
         """The prefill row kernel's plan with G block-rows per workgroup."""
         pp = self._pf_plans.get(G)
         if pp is None:
+            step_cols = int(_lib.load().ssl_prefill_step_cols(self.dtype_code))
             groups, steps, ng = _runtime.build_prefill_plan(self.crow_h, self.col_h, self.NBK,
-                                                            None, self.p, G)
+                                                            None, self.p, G, step_cols)
             pp = _runtime.DevicePrefillPlan(groups, steps, ng, G, self.device)
             self._pf_plans[G] = pp
         if self._values_pq is None and self.nblk_total > 0:

@@ -92,28 +92,29 @@ static void check_plan(const Structure& s, bool use_rows, int32_t q, int32_t lr,
   }
 }
 
-static void check_prefill(const Structure& s, bool use_rows, int32_t p, int32_t group) {
+static void check_prefill(const Structure& s, bool use_rows, int32_t p, int32_t group,
+                          int32_t sc) {
   const int32_t* rows = row_list(s, use_rows);
   const int64_t nr = use_rows ? (int64_t)s.rows.size() : s.NB;
   int64_t ng = -1, ne = -1;
   int rc = ssl_prefill_plan_build(s.crow.data(), s.col.data(), s.NB, s.NBK, rows, nr, p, group,
-                                  nullptr, 0, nullptr, 0, &ng, &ne);
+                                  sc, nullptr, 0, nullptr, 0, &ng, &ne);
   CHECK(rc == SSL_OK);
   if (rc != SSL_OK) return;
   const int gstride = 2 + group;
-  const int stride = ssl_prefill_step_ints(p, group);
-  const int E = 64 / p, IB = group * p / 32;
+  const int stride = ssl_prefill_step_ints(p, group, sc);
+  const int E = sc / p, IB = group * p / 32, half = sc / 2;
   CHECK(stride >= 1 + E + 4 * IB * E);
   if (ng > 0) {
     std::vector<int32_t> g((size_t)((ng - 1) * gstride + 1)), e((size_t)(ne * stride + 1));
     int64_t a, b;
     CHECK(ssl_prefill_plan_build(s.crow.data(), s.col.data(), s.NB, s.NBK, rows, nr, p, group,
-                                 g.data(), ng - 1, e.data(), ne, &a, &b) == SSL_ERR_CAPACITY);
+                                 sc, g.data(), ng - 1, e.data(), ne, &a, &b) == SSL_ERR_CAPACITY);
   }
   std::vector<int32_t> g((size_t)(ng * gstride)), e((size_t)(ne * stride));
   int64_t ng2, ne2;
   CHECK(ssl_prefill_plan_build(s.crow.data(), s.col.data(), s.NB, s.NBK, rows, nr, p, group,
-                               g.data(), ng, e.data(), ne, &ng2, &ne2) == SSL_OK);
+                               sc, g.data(), ng, e.data(), ne, &ng2, &ne2) == SSL_OK);
   CHECK(ng2 == ng && ne2 == ne);
   std::vector<int> seen(s.col.size(), 0);
   for (int64_t i = 0; i < ng; ++i) {
@@ -135,7 +136,7 @@ static void check_prefill(const Structure& s, bool use_rows, int32_t p, int32_t 
           const int32_t blk = rec[1 + E + ((fw % 4) * IB + fw / 4) * E + en];
           if (blk < 0) continue;
           CHECK(c >= 0);
-          const int h0 = en * p / 32, h1 = (en * p + p - 1) / 32;
+          const int h0 = en * p / half, h1 = (en * p + p - 1) / half;
           CHECK(((rec[0] >> (h0 * group + sl)) & 1) && ((rec[0] >> (h1 * group + sl)) & 1));
           const int32_t row = gr[2 + sl];
           CHECK(row >= 0 && blk >= s.crow[row] && blk < s.crow[row + 1] && s.col[blk] * p == c);
@@ -161,8 +162,9 @@ int main() {
     check_plan(s, true, q, lr, target);
     const int32_t pp = 16 << (rng() % 3);
     const int32_t group = 64 / pp;
-    check_prefill(s, false, pp, group);
-    check_prefill(s, true, pp, group);
+    const int32_t sc = (pp <= 32 && rng() % 2) ? 32 : 64;
+    check_prefill(s, false, pp, group, sc);
+    check_prefill(s, true, pp, group, sc);
     // corrupted copies are refused
     if (!s.col.empty()) {
       Structure bad = s;
@@ -171,7 +173,7 @@ int main() {
       CHECK(ssl_plan_build(bad.crow.data(), bad.col.data(), bad.NB, bad.NBK, nullptr, 0, q, lr,
                            target, nullptr, 0, &a, &b) == SSL_ERR_INVALID);
       CHECK(ssl_prefill_plan_build(bad.crow.data(), bad.col.data(), bad.NB, bad.NBK, nullptr, 0,
-                                   pp, group, nullptr, 0, nullptr, 0, &a, &b) == SSL_ERR_INVALID);
+                                   pp, group, sc, nullptr, 0, nullptr, 0, &a, &b) == SSL_ERR_INVALID);
     }
     if (s.NB > 1 && s.crow[s.NB] > 0) {
       Structure bad = s;

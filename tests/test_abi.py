@@ -189,21 +189,21 @@ def test_plans_reject_column_indices_out_of_range(bad):
         _runtime.build_plan(np.asarray(crow, np.int32), np.zeros(0, np.int32), 4, None, 16, 0, 0)
 
 
-def _pf_plan(crow, col, rows=None, group=1, NBK=None, p=64):
+def _pf_plan(crow, col, rows=None, group=1, NBK=None, p=64, step_cols=64):
     col = np.asarray(col, np.int32)
     if NBK is None:
         NBK = int(col.max()) + 1 if col.size else 1
     return _runtime.build_prefill_plan(np.asarray(crow, np.int32), col, NBK,
                                        None if rows is None else np.asarray(rows, np.int32), p,
-                                       group)
+                                       group, step_cols)
 
 
-def _steps_to_entries(steps, s0, s1, p, G):
+def _steps_to_entries(steps, s0, s1, p, G, step_cols=64):
     """The union entries (col_block, {slot: blk}) a group's step records hold,
     in order, checking each step's mask against its blocks on the way. A record
     holds, per wave w of the row kernel and load i, the block indices of slot
     8·(w + 4i) / p: every copy of a slot's index must agree."""
-    E, IB = 64 // p, G * p // 32
+    E, IB, half = step_cols // p, G * p // 32, step_cols // 2
     out = []
     for rec in steps[s0:s1]:
         mask, cols = rec[0], rec[1:1 + E]
@@ -224,19 +224,19 @@ def _steps_to_entries(steps, s0, s1, p, G):
             out.append((cols[e] // p, {g: int(blks[e, g]) for g in range(G) if blks[e, g] >= 0}))
             for g in range(G):
                 if blks[e, g] >= 0:
-                    for h in range(2):  # 32-column halves the entry covers
-                        if e * p < 32 * (h + 1) and (e + 1) * p > 32 * h:
+                    for h in range(2):  # halves of the step the entry covers
+                        if e * p < half * (h + 1) and (e + 1) * p > half * h:
                             want |= 1 << (h * G + g)
         assert int(mask) & 0xffffffff == want
         assert (rec[1 + E + 4 * IB * E:] == -1).all()  # padding
     return out
 
 
-@pytest.mark.parametrize("p", [16, 32, 64])
-def test_prefill_plan_merges_each_groups_columns(p):
+@pytest.mark.parametrize("p,step_cols", [(16, 64), (32, 64), (64, 64), (16, 32), (32, 32)])
+def test_prefill_plan_merges_each_groups_columns(p, step_cols):
     """Every block of every listed row appears exactly once, in its row's slot,
-    entries of a group ascend by column, E = 64/p entries per step, and the
-    masks match the slots present in each 32-column half."""
+    entries of a group ascend by column, E = step_cols/p entries per step, and
+    the masks match the slots present in each half of a step."""
     rng = np.random.default_rng(1)
     NB, NBK = 23, 17
     counts = rng.integers(0, NBK + 1, NB)
@@ -245,8 +245,9 @@ def test_prefill_plan_merges_each_groups_columns(p):
     lib = _lib.load()
     for rows in (None, [0, 2, 3, 7, 11, 12, 20, 22]):
         for G in (64 // p,):  # the row kernel's tiles are 64 features wide
-            groups, steps, ng = _pf_plan(crow, col, rows, G, p=p)
-            assert steps.shape[1] == lib.ssl_prefill_step_ints(p, G) and steps.shape[1] % 4 == 0
+            groups, steps, ng = _pf_plan(crow, col, rows, G, p=p, step_cols=step_cols)
+            assert steps.shape[1] == lib.ssl_prefill_step_ints(p, G, step_cols)
+            assert steps.shape[1] % 4 == 0
             listed = list(range(NB)) if rows is None else rows
             assert ng == -(-len(listed) // G)
             seen = []
@@ -254,8 +255,8 @@ def test_prefill_plan_merges_each_groups_columns(p):
                 s0, s1 = groups[gi, 0], groups[gi, 1]
                 grows = groups[gi, 2:]
                 assert list(grows[grows >= 0]) == listed[gi * G:(gi + 1) * G]
-                ents = _steps_to_entries(steps, s0, s1, p, G)
-                assert s1 - s0 == -(-len(ents) // (64 // p))
+                ents = _steps_to_entries(steps, s0, s1, p, G, step_cols)
+                assert s1 - s0 == -(-len(ents) // (step_cols // p))
                 cols = [c for c, _ in ents]
                 assert np.all(np.diff(cols) > 0)
                 for c, blks in ents:
@@ -275,13 +276,17 @@ def test_prefill_plan_repeated_column_gets_its_own_entry():
 
 def test_prefill_step_ints():
     lib = _lib.load()
-    # 1 + E + 4·IB·E words rounded up to 4 (E = 64/p entries, IB = 2 loads of 8
-    # weight rows per wave)
-    assert lib.ssl_prefill_step_ints(64, 1) == 12 and lib.ssl_prefill_step_ints(32, 2) == 20
-    assert lib.ssl_prefill_step_ints(16, 4) == 40
-    # only the row kernel's tiles (group·p = 64) have records
-    assert lib.ssl_prefill_step_ints(48, 2) == 0 and lib.ssl_prefill_step_ints(16, 17) == 0
-    assert lib.ssl_prefill_step_ints(64, 2) == 0 and lib.ssl_prefill_step_ints(16, 8) == 0
+    sc = lib.ssl_prefill_step_ints
+    # 1 + E + 4·IB·E words rounded up to 4 (E = step_cols/p entries, IB = 2
+    # loads of 8 weight rows per wave)
+    assert sc(64, 1, 64) == 12 and sc(32, 2, 64) == 20 and sc(16, 4, 64) == 40
+    assert sc(32, 2, 32) == 12 and sc(16, 4, 32) == 20  # fp32: 32-column steps
+    # only the row kernel's tiles (group·p = 64) and whole blocks per step
+    assert sc(48, 2, 64) == 0 and sc(16, 17, 64) == 0
+    assert sc(64, 2, 64) == 0 and sc(16, 8, 64) == 0
+    assert sc(64, 1, 32) == 0 and sc(32, 2, 48) == 0
+    assert lib.ssl_prefill_step_cols(_lib.SSL_F32) == 32
+    assert lib.ssl_prefill_step_cols(_lib.SSL_BF16) == 64
 
 
 def test_plan_target_cost_policy():

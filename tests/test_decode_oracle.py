@@ -57,6 +57,24 @@ def test_decode_steps_reproduce_the_full_sequence_forward(model_type, kv_heads, 
         assert err < TOL, (t, err)
 
 
+@pytest.mark.parametrize("model_type,kv_heads,bias", [
+    ("llama", 4, False), ("llama", 2, True), ("qwen3", 2, False),
+])
+def test_whole_sequence_forward_matches_transformers_and_decode_steps(model_type, kv_heads, bias):
+    model = tiny_model(model_type, kv_heads, bias, seed=3)
+    P = dor.params_from_hf(model)
+    B, T = 2, 9
+    ids = torch.randint(0, 97, (B, T), generator=torch.Generator().manual_seed(4))
+    with torch.no_grad():
+        want = model(input_ids=ids, use_cache=False).logits.numpy()
+    got = dor.forward(P, ids.numpy())
+    assert np.abs(got - want).max() / np.abs(want).max() < TOL
+    cache = dor.KVCache.empty(len(P.layers), B, P.kv_heads, T, P.head_dim)
+    for t in range(T):
+        step = dor.decode_step(P, cache, ids[:, t].numpy(), [t] * B)
+        assert np.abs(got[:, t] - step).max() / np.abs(step).max() < 1e-12
+
+
 def test_ragged_positions_match_per_sequence_runs():
     """Sequences at different positions in one step give their own logits."""
     model = tiny_model("llama", 2)

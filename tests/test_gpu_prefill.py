@@ -152,3 +152,80 @@ def test_llama7b_ffn_at_2048_tokens_every_row(mode, tile, gpu_device):
     y = mod(to_dev(x, torch.bfloat16, gpu_device))
     torch.cuda.synchronize()
     assert err(y, oracle_y(prob, x)) <= 1e-2
+
+
+# ------------------------------------------------------------------- fp32 --
+# fp32 calls run the same kernels with 32-column steps (128 bytes per tile
+# row, v_mfma_f32_16x16x4f32); 16×16 and 32×32 blocks (64-wide blocks stream).
+# The library sends them there when the grid fills the device; a forced tile
+# sends any call of 128 rows or more.
+
+
+@pytest.mark.parametrize("p", [16, 32])
+@pytest.mark.parametrize("mode", MODES, ids=MODE_IDS)
+@pytest.mark.parametrize("M", [600, 1030])
+def test_fp32_forced_tiles_fused_linear(p, mode, M, tile, gpu_device):
+    tile(mode)
+    dt = torch.float32
+    prob = make_problem(13 * p + 64, 9 * 64 + 3 * p, 128, p, 0.5, dt, seed=p + M + mode, skew=True)
+    assert _lib.load().ssl_slr_takes_prefill(M, prob["NB"], p, p, _lib.SSL_F32) == 1
+    mod = make_module(prob, gpu_device)
+    x = make_x(prob, M)
+    y = mod(to_dev(x, dt, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= TOL[dt]
+
+
+@pytest.mark.parametrize("p", [16, 32])
+@pytest.mark.parametrize("mode", MODES, ids=MODE_IDS)
+def test_fp32_ragged_features_and_grouped_launch(p, mode, tile, gpu_device):
+    """n and m not multiples of the block (a ragged last block column is cut by
+    in_features), three linears in one launch, 300 token rows."""
+    tile(mode)
+    dt = torch.float32
+    specs = [(5 * p + 3, 96, 0.5), (3 * p, 64, 0.3), (7 * p - 5, 128, 0.7)]
+    m = 8 * p - 7
+    probs = [make_problem(n, m, r, p, d, dt, seed=71 + i, skew=(i == 1), pad=True)
+             for i, (n, r, d) in enumerate(specs)]
+    grp = ssalaad_amd.LRSLinearGroup(*[make_module(pr, gpu_device) for pr in probs])
+    x = make_x(probs[0], 300)
+    ys = grp(to_dev(x, dt, gpu_device))
+    torch.cuda.synchronize()
+    for y, pr in zip(ys, probs):
+        assert err(y, oracle_y(pr, x)) <= TOL[dt]
+
+
+@pytest.mark.parametrize("p", [16, 32])
+@pytest.mark.parametrize("mode", MODES, ids=MODE_IDS)
+def test_fp32_inplace_op(p, mode, tile, gpu_device):
+    tile(mode)
+    dt = torch.float32
+    M = 300
+    prob = make_problem(13 * p, 10 * p, 4, p, 0.3, dt, seed=7 * p + mode, skew=True)
+    crow32, col32, vt, act = orc.module_buffers(prob["crow"], prob["col"], prob["vals"])
+    x = make_x(prob, M, seed=3)
+    rng = np.random.default_rng(p)
+    out0 = rng.standard_normal((M, prob["n"])).astype(np.float32).astype(np.float64)
+    want = orc.bsr_addmm_inplace(out0, x, crow32, col32, vt, act)
+    dev = gpu_device
+    out = to_dev(out0, dt, dev)
+    torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_(
+        out, to_dev(x, dt, dev), torch.from_numpy(crow32).to(dev),
+        torch.from_numpy(col32).to(dev), to_dev(vt, dt, dev), torch.from_numpy(act).to(dev))
+    torch.cuda.synchronize()
+    assert err(out, want) <= TOL[dt]
+    got = out.double().cpu().numpy()
+    for by in sorted(set(range(prob["NB"])) - set(act.tolist())):
+        assert np.array_equal(got[:, by * p:(by + 1) * p], out0[:, by * p:(by + 1) * p])
+
+
+def test_fp32_llama60m_gate_at_2048_tokens_every_row(gpu_device):
+    """LLaMA-60M gate (1376×512, 32×32 blocks at 50%, rank 128), fp32, 2048
+    tokens: the shape of config 2's projections."""
+    dt = torch.float32
+    prob = make_problem(1376, 512, 128, 32, 0.5, dt, seed=60)
+    mod = make_module(prob, gpu_device)
+    x = make_x(prob, 2048)
+    y = mod(to_dev(x, dt, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= TOL[dt]
