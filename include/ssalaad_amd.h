@@ -279,7 +279,9 @@ typedef struct ssl_slr_member {
   int64_t pf_n_groups;
   int32_t pf_group;
   int64_t nnz;            /* stored blocks (length of col, first dim of values) */
-  const void* values_pq;  /* the block values in (nnz, p, q) order, for the prefill kernels */
+  const void* values_pq;  /* for the prefill kernels: the block values in (nnz, p, q) order;
+                           * 2:4 storage: the blocks in the prefill layout
+                           * (ssl_nm24_prefill_block_bytes) */
   /* storage of `values`: SSL_S_BSR, (nnz, q, p) blocks (the reference module's
    * layout), or SSL_S_NM24, 2:4-sparse 32×32 blocks in the layout below
    * (replaces the semi-structured S of ssalaad/efficient/ls_linear.py:167-219) */
@@ -301,6 +303,19 @@ typedef enum { SSL_S_BSR = 0, SSL_S_NM24 = 1 } ssl_s_format;
  *          i0 < i1) of the two kept values of group grp in output column 2c + s.
  * A group with fewer than two non-zeros keeps zeros at unused positions. */
 int64_t ssl_nm24_block_bytes(void);
+
+/* Bytes of one 2:4 block in the layout the prefill row kernel reads (the
+ * operands of v_smfmac_f32_16x16x64), the same blocks in the same order:
+ *   values [32][2][8] of the activation dtype: [j][h][t] = kept value 8h + t
+ *          of output column j (input features 16h .. 16h + 15: four groups,
+ *          two kept values each, group by group);
+ *   index  [32] uint32: bits 16h + 4q .. 16h + 4q + 3 = i0 | i1 << 2 of
+ *          group 4h + q of output column j.
+ * Calls with ssl_nm24_takes_prefill(M, n_rows, dtype) = 1 pass these as the
+ * member's values_pq, with a prefill plan (group 2, 64-column steps) over the
+ * 2:4 block structure. */
+int64_t ssl_nm24_prefill_block_bytes(void);
+int32_t ssl_nm24_takes_prefill(int64_t M, int64_t n_rows, int32_t dtype);
 
 /* Up to 4 SLR linears that read the same x (e.g. a layer's q, k and v
  * projections, or its gate and up projections) in ONE launch: each member is

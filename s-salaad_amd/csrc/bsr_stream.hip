@@ -170,6 +170,14 @@ int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_
 
 int64_t ssl_nm24_block_bytes(void) { return kNmBlockBytes; }
 
+int64_t ssl_nm24_prefill_block_bytes(void) { return kNmPrefillBlockBytes; }
+
+// 2:4 calls take the prefill kernels (v_smfmac) from kPrefillMinM token rows.
+int32_t ssl_nm24_takes_prefill(int64_t M, int64_t n_rows, int32_t dtype) {
+  (void)n_rows;
+  return (M >= kPrefillMinM && dtype != SSL_F32) ? 1 : 0;
+}
+
 int32_t ssl_prefill_step_cols(int32_t dtype) { return dtype == SSL_F32 ? 32 : 64; }
 
 int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q) {
@@ -370,10 +378,12 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
 
   int64_t call_rows = 0;
   for (int i = 0; i < n_members; ++i) call_rows += members[i].NB;
-  if (s_format == SSL_S_BSR && ssl_slr_takes_prefill(M, call_rows, block_p, block_q, dtype)) {
+  const bool nm = s_format == SSL_S_NM24;
+  if (nm ? ssl_nm24_takes_prefill(M, call_rows, dtype)
+         : ssl_slr_takes_prefill(M, call_rows, block_p, block_q, dtype)) {
     // Many token rows: the latent GEMM (K split, then combined), then the row
-    // GEMM over groups of block-rows. (2:4 blocks stay on the row-streaming
-    // kernel at every M.)
+    // GEMM over groups of block-rows (2:4: on the structured-sparse MFMA).
+    const int64_t blk_bytes = nm ? kNmPrefillBlockBytes : (int64_t)block_p * block_p * eb;
     const int cus = device_cus();
     PfArgs rows{}, lat{};
     if (M * ldx * eb > 0x7fffffffLL)
@@ -399,15 +409,16 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       if (!mb.pf_groups || !mb.pf_steps || mb.pf_n_groups <= 0 || mb.pf_group != G ||
           (mb.nnz > 0 && !mb.values_pq))
         return fail(SSL_ERR_INVALID, "linear %d: calls with %lld token rows need a prefill plan "
-                    "with group %d and (p, q) ordered block values", i, (long long)M, G);
+                    "with group %d and %s", i, (long long)M, G,
+                    nm ? "2:4 blocks in the prefill layout" : "(p, q) ordered block values");
       const int64_t T = (M + rows.bm - 1) / rows.bm;
-      if (mb.nnz < 0 || mb.nnz * block_p * block_p * eb > 0x7fffffffLL ||
+      if (mb.nnz < 0 || mb.nnz * blk_bytes > 0x7fffffffLL ||
           mb.NB * block_p * mb.r_pad * eb > 0x7fffffffLL || M * mb.ldy * eb > 0x7fffffffLL ||
           (int64_t)mb.r_pad * m_pad * eb > 0x7fffffffLL)
         return fail(SSL_ERR_UNSUPPORTED, "linear %d: weights or output beyond 2 GiB", i);
       pm.y = mb.y; pm.ldy = mb.ldy; pm.A = mb.A; pm.lda = mb.r_pad;
       pm.A_bytes = mb.NB * block_p * mb.r_pad * eb; pm.bias = mb.bias;
-      pm.values_pq = mb.values_pq; pm.values_bytes = mb.nnz * block_p * block_p * eb;
+      pm.values_pq = mb.values_pq; pm.values_bytes = mb.nnz * blk_bytes;
       pm.groups = mb.pf_groups; pm.steps = mb.pf_steps; pm.n_groups = (int)mb.pf_n_groups;
       pm.B = mb.B; pm.ldb = m_pad;
       pm.t = (char*)mb.workspace + L[i].t_final; pm.ldt = mb.r_pad;
@@ -435,6 +446,9 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       comb.off[n_members] = (int)c;
       comb.combine_items = (int)c;
     }
+    if (nm)
+      return check_hip(prefill_launch_fused_nm24(dtype, rows, lat, comb, (hipStream_t)stream),
+                       "slr prefill launch (2:4)");
     return check_hip(prefill_launch_fused(dtype, block_p, G, rows, lat, comb, (hipStream_t)stream),
                      "slr prefill launch");
   }

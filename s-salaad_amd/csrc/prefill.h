@@ -61,6 +61,12 @@ int prefill_latent_split(int64_t M, int64_t r_pad, int64_t m_pad, int n_cus);
 // `stream`. dtype: SSL_BF16 or SSL_F16; P ∈ {16, 32, 64}; G = 128/P or 64/P.
 hipError_t prefill_launch_fused(int dtype, int P, int G, const PfArgs& rows, const PfArgs& lat,
                                 const PfArgs& comb, hipStream_t stream);
+// The fused SLR linear with 2:4 S (32×32 blocks in the row kernel's layout,
+// kNmPrefillBlockBytes each): latent, combine, then the row GEMM on
+// v_smfmac_f32_16x16x64. dtype: SSL_BF16 or SSL_F16; G = 2.
+hipError_t prefill_launch_fused_nm24(int dtype, const PfArgs& rows, const PfArgs& lat,
+                                     const PfArgs& comb, hipStream_t stream);
+constexpr int kNmPrefillBlockBytes = 32 * 2 * 16 + 32 * 4;
 // The in-place op: the row GEMM only (rows.mode = PF_OP).
 hipError_t prefill_launch_op(int dtype, int P, int G, const PfArgs& rows, hipStream_t stream);
 

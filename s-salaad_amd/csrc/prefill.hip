@@ -52,7 +52,16 @@ constexpr int kXcds = 8;
 constexpr int kK = 64;           // 16-bit units per LDS row (128 bytes)
 constexpr uint32_t kOob = 0x80000000u;
 
-enum : int { K_ROWS_OP = 0, K_ROWS_FUSED = 1, K_LATENT = 2 };
+enum : int { K_ROWS_OP = 0, K_ROWS_FUSED = 1, K_LATENT = 2, K_ROWS_NM = 3 };
+
+// 2:4 blocks as the row kernel reads them (32 input × 32 output features per
+// block, kNmPfBytes each): values [j][h][8] 16-bit — output feature j, half h
+// of the block's 32 input features, the 8 kept values of its 4 groups in
+// order (group, slot) — then index [j] uint32: for half h (bits 16h..16h+15)
+// one nibble per group, i0 | i1 << 2, the kept values' positions in the group.
+// Lane (i, g) of v_smfmac_f32_16x16x64 reads one 16-byte values piece (its
+// feature, 16 input features) and 16 index bits: exactly these.
+constexpr int kNmPfBytes = kNmPrefillBlockBytes;
 
 // 16-byte chunk with its elements (EB bytes each) at and past `valid` set to zero.
 template <int EB>
@@ -76,6 +85,22 @@ template <int DT>
 __device__ __forceinline__ void store_elem(void* base, int64_t i, float v) {
   if constexpr (DT == DT_F32) ((float*)base)[i] = v;
   else ((uint16_t*)base)[i] = (uint16_t)to_bits<DT>(v);
+}
+
+// D (16 × 16) += A · B with A 16 × 64 2:4-sparse (8 kept 16-bit values per
+// lane, `idx` their positions) and B 64 × 16 dense (16 values per lane: k in
+// [8g, 8g + 8) then [32 + 8g, 32 + 8g + 8) for lane group g).
+template <int DT>
+__device__ __forceinline__ void smfmac64(f32x4& acc, uint4 a, uint4 b0, uint4 b1, int idx) {
+  typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+  const u32x8 b = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+  if constexpr (DT == DT_BF16) {
+    acc = __builtin_amdgcn_smfmac_f32_16x16x64_bf16(__builtin_bit_cast(bf16x8, a),
+                                                     __builtin_bit_cast(bf16x16, b), acc, idx, 0, 0);
+  } else {
+    acc = __builtin_amdgcn_smfmac_f32_16x16x64_f16(__builtin_bit_cast(f16x8, a),
+                                                    __builtin_bit_cast(f16x16, b), acc, idx, 0, 0);
+  }
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -137,6 +162,14 @@ __device__ __forceinline__ void dma16(const u32x4& r, uint32_t voff, uint32_t so
                : "s"(lds), "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff))
                : "m0");
 }
+// 4 bytes a lane: lane l writes LDS byte address lds + 4·l (active lanes only).
+__device__ __forceinline__ void dma4(const u32x4& r, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(r)
+               : "m0");
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p);
@@ -171,8 +204,10 @@ constexpr int pf_occupancy(int BM, int BN, int S) {
 }
 
 // ---------------------------------------------------------------------------
-// The engine. KIND: K_ROWS_OP / K_ROWS_FUSED (rows of the block-sparse linear)
-// or K_LATENT (t = x·Bᵀ). P: block size (rows kernels). S: LDS stages (loads
+// The engine. KIND: K_ROWS_OP / K_ROWS_FUSED (rows of the block-sparse linear),
+// K_ROWS_NM (the fused linear with 2:4 S on v_smfmac_f32_16x16x64: its tiles
+// are computed transposed, output features × tokens, because the sparse
+// operand of the structured-sparse MFMA is its A) or K_LATENT (t = x·Bᵀ). P: block size (rows kernels). S: LDS stages (loads
 // of S − 1 steps in flight while one step computes). A step is 128 bytes of
 // every tile row: 64 k columns of 16-bit data (one v_mfma_f32_16x16x32 per
 // 32 k) or 32 of fp32 (four v_mfma_f32_16x16x4f32 per 16 k, element e of a
@@ -190,6 +225,9 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   using T = Tile<BM, BN, WM, WN>;
   constexpr int IA = T::IA, IB = T::IB, MTI = T::MTI, NTI = T::NTI;
   constexpr bool ROWS = KIND != K_LATENT;
+  constexpr bool NM = KIND == K_ROWS_NM;
+  constexpr bool LR = KIND == K_ROWS_FUSED || NM;  // rows kernels with low-rank steps
+  static_assert(!NM || (P == 32 && BN == 64 && DT != DT_F32), "2:4 tiles: 32-wide blocks, 16-bit");
   constexpr int G = ROWS ? BN / P : 1;
   constexpr int EB = Elem<DT>::bytes;
   constexpr int CE = 16 / EB;       // elements per 16-byte chunk
@@ -247,7 +285,7 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
     gr = mb.groups + (int64_t)grp * (2 + G);
     s_begin = ld_word(gr, 0);
     n_sp = ld_word(gr, 1) - s_begin;
-    const int n_lr = (KIND == K_ROWS_FUSED) ? mb.r_pad / KS : 0;
+    const int n_lr = LR ? mb.r_pad / KS : 0;
     s_end = s_begin + n_sp + n_lr;
   }
   const int U = s_end - s_begin;
@@ -263,9 +301,13 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   const int e_t = (ROWS && E > 1) ? (kc * CE) / P : 0;  // rows kernels: this lane's entry of a step
   const int kin = ROWS ? (kc * CE) % P : kc * CE;  // and its column within the entry
 
-  // ---- LDS byte addresses: stage 0's A rows 8·wid and B rows 8·wid
+  // ---- LDS byte addresses: stage 0's A rows 8·wid and B rows 8·wid; 2:4
+  // steps: this wave's 16 rows of the values region (64 bytes a row) and its
+  // 16 rows of the index region (8 bytes a row, after 4 KiB of values)
   const uint32_t la0 = lds_addr(&lds[0][8 * wid * kK]);
   const uint32_t lb0 = lds_addr(&lds[0][(BM + 8 * wid) * kK]);
+  const uint32_t lnv0 = lds_addr(&lds[0][BM * kK]) + 1024u * wid;
+  const uint32_t lni0 = lds_addr(&lds[0][BM * kK]) + 4096u + 128u * wid;
   constexpr uint32_t kStageBytes = T::LDS * 2, kRowBytes32 = 32 * kK * 2;
 
   // ---- constant parts of this lane's addresses
@@ -297,7 +339,7 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
       const int f = 8 * (wid + 4 * i) + lrow, j = f % P;
       bconst[i] = (uint32_t)((j * P + kin) * EB);
     }
-    if constexpr (KIND == K_ROWS_FUSED) {
+    if constexpr (LR) {
       tr = rsrc_words(mb.t, (int64_t)M * mb.ldt * EB);
       ar = rsrc_words(mb.A, mb.A_bytes);
 #pragma unroll
@@ -311,6 +353,7 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) lr_mask |= (ld_word(gr, 2 + g) >= 0) ? (1 << g) | (1 << (G + g)) : 0;
+      if constexpr (NM) lr_mask |= 1 << 30;  // a low-rank step: dense MFMAs
     } else {
 #pragma unroll
       for (int i = 0; i < IA; ++i) at_[i] = 0;
@@ -368,11 +411,29 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
         const uint32_t xcb = c >= 0 ? (uint32_t)(c * EB) : kOob;
 #pragma unroll
         for (int i = 0; i < IA; ++i) dma16(xr, ax[i] + xcb, 0, la + i * kRowBytes32);
+        if constexpr (NM) {
+          // this wave's 16 feature rows (slot wid / 2): lane l takes row l / 4,
+          // entry (l % 4) / 2, half l % 2 of the values; lanes < 32 the
+          // index word of row l / 2, entry l % 2
+          const int b0 = view_word(rv, 1 + E + (wid >> 1) * E);
+          const int b1 = view_word(rv, 1 + E + (wid >> 1) * E + 1);
+          const uint32_t kst = (uint32_t)k * kStageBytes;
+          const int bv = (lane & 2) ? b1 : b0;
+          const uint32_t jv = 16 * (wid & 1) + (lane >> 2);
+          dma16(br, bv < 0 ? kOob : (uint32_t)bv * kNmPfBytes + jv * 32 + (lane & 1) * 16, 0,
+                lnv0 + kst);
+          if (lane < 32) {
+            const int bi = (lane & 1) ? b1 : b0;
+            const uint32_t ji = 16 * (wid & 1) + (lane >> 1);
+            dma4(br, bi < 0 ? kOob : (uint32_t)bi * kNmPfBytes + 1024 + ji * 4, lni0 + kst);
+          }
+        } else {
 #pragma unroll
-        for (int i = 0; i < IB; ++i) {
-          const int blk = view_entry(rv, 1 + E + i * E);
-          dma16(br, blk < 0 ? kOob : (uint32_t)blk * (uint32_t)(P * P * EB) + bconst[i], 0,
-                lb + i * kRowBytes32);
+          for (int i = 0; i < IB; ++i) {
+            const int blk = view_entry(rv, 1 + E + i * E);
+            dma16(br, blk < 0 ? kOob : (uint32_t)blk * (uint32_t)(P * P * EB) + bconst[i], 0,
+                  lb + i * kRowBytes32);
+          }
         }
         if (m % P != 0) {  // only a ragged last block column cuts chunks
           xcol = c >= 0 ? c + kin : 0x3fffffff;
@@ -417,6 +478,37 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   // ---- the MFMAs of one step from an LDS stage
   auto compute = [&](const uint16_t* buf, int mask_in) {
     const int mask = __builtin_amdgcn_readfirstlane(mask_in);
+    if constexpr (NM) {
+      if (!((mask >> 30) & 1)) {
+        // 2:4 step: A = the weights' kept values (features × 64 k), B = the x
+        // chunks gq and 4 + gq of each token row; tiles are features × tokens
+        uint4 xa[MTI][2], sv[NTI];
+        int ix[NTI];
+        const uint16_t* vb = buf + BM * kK;  // values region (64 bytes a feature row)
+#pragma unroll
+        for (int mt = 0; mt < MTI; ++mt) {
+          const int row = wm * T::TM + 16 * mt + c;
+          xa[mt][0] = *(const uint4*)(buf + lds_chunk(row, gq));
+          xa[mt][1] = *(const uint4*)(buf + lds_chunk(row, 4 + gq));
+        }
+#pragma unroll
+        for (int nt = 0; nt < NTI; ++nt) {
+          const int f = wn * T::TN + 16 * nt + c;
+          sv[nt] = *(const uint4*)(vb + f * 32 + gq * 8);
+          ix[nt] = vb[2048 + f * 4 + (gq >> 1) * 2 + (gq & 1)];
+        }
+#pragma unroll
+        for (int nt = 0; nt < NTI; ++nt) {
+          const int slot = (wn * T::TN + 16 * nt) / P;
+          if (((mask >> slot) | (mask >> (G + slot))) & 1) {
+#pragma unroll
+            for (int mt = 0; mt < MTI; ++mt)
+              smfmac64<DT>(acc[mt][nt], sv[nt], xa[mt][0], xa[mt][1], ix[nt]);
+          }
+        }
+        return;
+      }
+    }
     Frag af[2][MTI], bf[2][NTI];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -439,7 +531,10 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
         const int slot = (KIND == K_LATENT) ? 0 : (wn * T::TN + 16 * nt) / P;
         if ((mask >> (ks * G + slot)) & 1) {
 #pragma unroll
-          for (int mt = 0; mt < MTI; ++mt) MM::run(acc[mt][nt], af[ks][mt], bf[ks][nt]);
+          for (int mt = 0; mt < MTI; ++mt) {
+            if constexpr (NM) MM::run(acc[mt][nt], bf[ks][nt], af[ks][mt]);  // features × tokens
+            else MM::run(acc[mt][nt], af[ks][mt], bf[ks][nt]);
+          }
         }
       }
     }
@@ -500,6 +595,31 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
           }
         }
       }
+  } else if constexpr (NM) {
+    // lane (c, gq) holds features 4gq + e of feature tile nt for token 16·mt + c
+    void* const y_out = mb.y;
+    const int64_t ldy = mb.ldy;
+    const void* const bias = mb.bias;
+#pragma unroll
+    for (int nt = 0; nt < NTI; ++nt) {
+      const int fl = wn * T::TN + 16 * nt + 4 * gq;
+      const int row = ld_word(gr, 2 + (wn * T::TN + 16 * nt) / P);
+      if (row < 0) continue;
+      const int col = row * P + fl % P;
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias != nullptr) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = load_scalar<DT>(bias, col + e);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MTI; ++mt) {
+        const int r = m0 + wm * T::TM + 16 * mt + c;
+        if (r >= M) continue;
+        const float o[4] = {acc[mt][nt][0] + bv[0], acc[mt][nt][1] + bv[1], acc[mt][nt][2] + bv[2],
+                            acc[mt][nt][3] + bv[3]};
+        st_w<DT, 4>(y_out, (int64_t)r * ldy + col, o);
+      }
+    }
   } else {
     void* const y_out = mb.y;
     const int64_t ldy = mb.ldy;
@@ -583,8 +703,7 @@ hipError_t launch_rows_p(const PfArgs& rows, int P, int G, hipStream_t s) {
 }
 
 template <int DT>
-hipError_t launch_fused(const PfArgs& rows, const PfArgs& lat, const PfArgs& comb, int P, int G,
-                        hipStream_t s) {
+hipError_t launch_latent(const PfArgs& lat, const PfArgs& comb, hipStream_t s) {
   if (lat.items > 0) {
     hipLaunchKernelGGL((pf_gemm<DT, K_LATENT, 64, 128, 64, 2, 2, kLatentStages>),
                        dim3((unsigned)lat.items), dim3(kPfThreads), 0, s, lat);
@@ -597,7 +716,31 @@ hipError_t launch_fused(const PfArgs& rows, const PfArgs& lat, const PfArgs& com
       if (e != hipSuccess) return e;
     }
   }
+  return hipSuccess;
+}
+
+template <int DT>
+hipError_t launch_fused(const PfArgs& rows, const PfArgs& lat, const PfArgs& comb, int P, int G,
+                        hipStream_t s) {
+  const hipError_t e = launch_latent<DT>(lat, comb, s);
+  if (e != hipSuccess) return e;
   return launch_rows_p<DT, K_ROWS_FUSED>(rows, P, G, s);
+}
+
+template <int DT>
+hipError_t launch_fused_nm24(const PfArgs& rows, const PfArgs& lat, const PfArgs& comb,
+                             hipStream_t s) {
+  hipError_t e = launch_latent<DT>(lat, comb, s);
+  if (e != hipSuccess || rows.items == 0) return e;
+  const int per_xcd = (rows.items + kXcds - 1) / kXcds;
+  const dim3 grid((unsigned)(per_xcd * kXcds)), blk(kPfThreads);
+  if (rows.bm == 256)
+    hipLaunchKernelGGL((pf_gemm<DT, K_ROWS_NM, 32, 256, 64, 4, 1, 2>), grid, blk, 0, s, rows);
+  else if (rows.bm == 128)
+    hipLaunchKernelGGL((pf_gemm<DT, K_ROWS_NM, 32, 128, 64, 2, 2, 2>), grid, blk, 0, s, rows);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -638,6 +781,15 @@ hipError_t prefill_launch_fused(int dtype, int P, int G, const PfArgs& rows, con
     case SSL_BF16: return launch_fused<DT_BF16>(rows, lat, comb, P, G, stream);
     case SSL_F16: return launch_fused<DT_F16>(rows, lat, comb, P, G, stream);
     case SSL_F32: return launch_fused<DT_F32>(rows, lat, comb, P, G, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t prefill_launch_fused_nm24(int dtype, const PfArgs& rows, const PfArgs& lat,
+                                     const PfArgs& comb, hipStream_t stream) {
+  switch (dtype) {
+    case SSL_BF16: return launch_fused_nm24<DT_BF16>(rows, lat, comb, stream);
+    case SSL_F16: return launch_fused_nm24<DT_F16>(rows, lat, comb, stream);
   }
   return hipErrorInvalidValue;
 }

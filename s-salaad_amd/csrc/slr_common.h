@@ -26,6 +26,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x16 __attribute__((ext_vector_type(16)));
 
 enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 

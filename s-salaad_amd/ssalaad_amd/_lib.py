@@ -63,6 +63,8 @@ _SIGNATURES = {
     ),
     "ssl_prefill_min_rows": (_c_i64, []),
     "ssl_nm24_block_bytes": (_c_i64, []),
+    "ssl_nm24_prefill_block_bytes": (_c_i64, []),
+    "ssl_nm24_takes_prefill": (_c_i32, [_c_i64, _c_i64, _c_i32]),
     "ssl_prefill_group": (_c_i32, [_c_i64, _c_i64, _c_i32, _c_i32]),
     "ssl_slr_takes_prefill": (_c_i32, [_c_i64, _c_i64, _c_i32, _c_i32, _c_i32]),
     "ssl_bsr_addmm_takes_prefill": (_c_i32, [_c_i64, _c_i32, _c_i32, _c_i32]),

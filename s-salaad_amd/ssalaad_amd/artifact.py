@@ -97,6 +97,24 @@ def nm24_pack(S: torch.Tensor) -> dict:
     return _nm24_pack(S)
 
 
+def nm24_prefill_layout(blocks: torch.Tensor) -> torch.Tensor:
+    """Packed 2:4 blocks (uint8 [nnz, ssl_nm24_block_bytes()]) → the same blocks
+    in the layout the prefill row kernel reads (uint8 [nnz,
+    ssl_nm24_prefill_block_bytes()], include/ssalaad_amd.h): per output column
+    j, its 16 kept values in order, then one uint32 of position nibbles per
+    column (i0 | i1 << 2 for each group, group 4h + q at bit 16h + 4q)."""
+    nnz = blocks.shape[0]
+    vals = blocks[:, :1024].contiguous().view(torch.int16).view(nnz, 16, 16, 2)   # [c][i][s]
+    v = vals.permute(0, 1, 3, 2).reshape(nnz, 32, 16)                             # [j = 2c + s][i]
+    ib = blocks[:, 1024:1280].view(nnz, 16, 8, 2).permute(0, 1, 3, 2).reshape(nnz, 32, 2, 4)
+    shifts = torch.tensor([0, 4, 8, 12], dtype=torch.int32, device=blocks.device)
+    idx16 = (ib.to(torch.int32) << shifts).sum(dim=-1)                            # [j][h]
+    idx = torch.stack([idx16[..., 0] & 0xFF, idx16[..., 0] >> 8,
+                       idx16[..., 1] & 0xFF, idx16[..., 1] >> 8], dim=-1)         # little-endian
+    return torch.cat([v.contiguous().view(torch.uint8).view(nnz, 1024),
+                      idx.to(torch.uint8).view(nnz, 128)], dim=1).contiguous()
+
+
 def _nm24_pack(S: torch.Tensor) -> dict:
     n, m = S.shape
     if m % 4:

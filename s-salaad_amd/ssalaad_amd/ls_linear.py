@@ -164,9 +164,9 @@ class _KernelState:
         """Whether a fused call of M token rows over `n_rows` block-rows (this
         linear's alone by default) runs the prefill kernels; the library decides
         (ssl_slr_takes_prefill), so host and device agree."""
-        if self.s_format != 0:
-            return False
         rows = self.NB if n_rows is None else n_rows
+        if self.s_format == 1:  # 2:4: the row kernel on v_smfmac
+            return bool(_lib.load().ssl_nm24_takes_prefill(M, rows, self.dtype_code))
         return bool(_lib.load().ssl_slr_takes_prefill(M, rows, self.p, self.q, self.dtype_code))
 
     def prefill_plan(self, G: int) -> _runtime.DevicePrefillPlan:
@@ -179,8 +179,14 @@ class _KernelState:
             pp = _runtime.DevicePrefillPlan(groups, steps, ng, G, self.device)
             self._pf_plans[G] = pp
         if self._values_pq is None and self.nblk_total > 0:
-            # the prefill kernels read each block k-contiguous per output column
-            self._values_pq = self.values.transpose(1, 2).contiguous()
+            if self.s_format == 1:
+                # 2:4 blocks as the structured-sparse MFMA reads them
+                from .artifact import nm24_prefill_layout
+
+                self._values_pq = nm24_prefill_layout(self.values)
+            else:
+                # the prefill kernels read each block k-contiguous per output column
+                self._values_pq = self.values.transpose(1, 2).contiguous()
         return pp
 
     def rows(self, x: torch.Tensor) -> torch.Tensor:

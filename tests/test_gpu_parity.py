@@ -21,7 +21,7 @@ from oracle import slr_oracle as orc  # noqa: E402
 from slr_cases import TOL, err, make_problem, make_x, oracle_y, sparse_bsr_tensor, to_dev  # noqa: E402
 
 import ssalaad_amd  # noqa: E402
-from ssalaad_amd import LRSLinear, _runtime  # noqa: E402
+from ssalaad_amd import LRSLinear, _lib, _runtime  # noqa: E402
 from ssalaad_amd.ls_linear import latent_wait_status  # noqa: E402
 
 pytestmark = pytest.mark.gpu
@@ -710,3 +710,56 @@ def test_nm24_llama7b_ffn_shape_decode(gpu_device):
     assert err(y, orc.slr_linear(x, A, B, S, b)) <= 1e-2
     assert torch.equal(y, y2)
     assert latent_wait_status(gpu_device) == 0
+
+
+# ------------------------------------------------- 2:4 at prefill sizes --
+# From ssl_prefill_min_rows() token rows 2:4 calls run the prefill row kernel
+# on v_smfmac_f32_16x16x64 (the weights' kept values and positions as the
+# sparse A operand, x as B, tiles transposed to features × tokens); the
+# latent and the low-rank steps are the dense MFMA steps of the same kernel.
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("shape", [(256, 192, 64), (100, 200, 24), (320, 1024, 128)])
+@pytest.mark.parametrize("tile_mode", [0, 1, 2], ids=["auto", "narrow", "tall"])
+@pytest.mark.parametrize("M", [128, 600])
+def test_nm24_prefill_matches_oracle(dtype, shape, tile_mode, M, gpu_device):
+    n, m, r = shape
+    lib = _lib.load()
+    assert lib.ssl_nm24_takes_prefill(M, -(-n // 32), _lib.dtype_code(dtype)) == 1
+    mod, (A, B, S, b) = _nm_module(n, m, r, dtype, gpu_device, seed=n + m + M + tile_mode)
+    x = np.random.default_rng(M + 1).standard_normal((M, m))
+    x = torch.from_numpy(x).to(dtype).double().numpy()
+    xt = to_dev(x, dtype, gpu_device)
+    _lib.check(lib.ssl_debug_set(_lib.DEBUG_PREFILL_TILE, tile_mode), "ssl_debug_set")
+    try:
+        y1, y2 = mod(xt), mod(xt)
+        torch.cuda.synchronize()
+    finally:
+        lib.ssl_debug_set(_lib.DEBUG_PREFILL_TILE, 0)
+    assert err(y1, orc.slr_linear(x, A, B, S, b)) <= TOL[dtype]
+    assert torch.equal(y1, y2)
+
+
+def test_nm24_prefill_grouped_launch(gpu_device):
+    dtype = torch.bfloat16
+    mods = [_nm_module(n, 320, r, dtype, gpu_device, seed=17 + n) for n, r in ((96, 32), (200, 64), (64, 16))]
+    grp = ssalaad_amd.LRSLinearGroup(*[md for md, _ in mods])
+    x = np.random.default_rng(19).standard_normal((300, 320))
+    x = torch.from_numpy(x).to(dtype).double().numpy()
+    ys = grp(to_dev(x, dtype, gpu_device))
+    torch.cuda.synchronize()
+    for y, (_, (A, B, S, b)) in zip(ys, mods):
+        assert err(y, orc.slr_linear(x, A, B, S, b)) <= 1e-2
+
+
+def test_nm24_llama7b_ffn_shape_at_2048_tokens_every_row(gpu_device):
+    """11008×4096 bf16, rank 256, 2:4 S, 2048 tokens: the structured-sparse row
+    kernel, every output row against the oracle."""
+    mod, (A, B, S, b) = _nm_module(11008, 4096, 256, torch.bfloat16, gpu_device, seed=41,
+                                   bias=False)
+    x = np.random.default_rng(5).standard_normal((2048, 4096))
+    x = torch.from_numpy(x).to(torch.bfloat16).double().numpy()
+    y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, orc.slr_linear(x, A, B, S, b)) <= 1e-2

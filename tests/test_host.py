@@ -180,3 +180,38 @@ def test_decode_engine_rejects_head_widths_without_a_kernel():
         "max_position_embeddings": 16, "hidden_act": "silu"})
     with pytest.raises(NotImplementedError, match="head_dim 48"):
         DecodeEngine(model, max_batch=1, max_context=4)
+
+
+def test_nm24_prefill_layout_decodes_to_the_same_matrix():
+    """The 2:4 blocks in the prefill row kernel's layout (values per output
+    column, position nibbles per group) hold exactly the packed matrix: decoded
+    independently here from the layout include/ssalaad_amd.h documents."""
+    import numpy as np
+
+    from ssalaad_amd.artifact import _nm24_pack, nm24_prefill_layout
+
+    g = torch.Generator().manual_seed(3)
+    n, m = 70, 100
+    count = torch.randint(0, 3, (n, m // 4), generator=g)
+    order = torch.rand(n, m // 4, 4, generator=g).argsort(-1).argsort(-1)
+    keep = order < count[..., None]
+    S = (torch.randn(n, m // 4, 4, generator=g) * keep).reshape(n, m).to(torch.bfloat16)
+    pk = _nm24_pack(S)
+    pf = nm24_prefill_layout(pk["blocks"])
+    assert pf.shape == (pk["blocks"].shape[0], ssalaad_amd._lib.load().ssl_nm24_prefill_block_bytes())
+    crow, col = pk["crow"].numpy(), pk["col"].numpy()
+    D = np.zeros((pk["NB"] * 32, pk["NBK"] * 32), np.float32)
+    for by in range(pk["NB"]):
+        for k in range(crow[by], crow[by + 1]):
+            vals = pf[k, :1024].view(torch.bfloat16).float().numpy().reshape(32, 2, 8)
+            idx = pf[k, 1024:].view(torch.int32).numpy().astype(np.int64) & 0xFFFFFFFF
+            for j in range(32):
+                for h in range(2):
+                    for q in range(4):
+                        nib = (int(idx[j]) >> (16 * h + 4 * q)) & 0xF
+                        i0, i1 = nib & 3, nib >> 2
+                        assert i0 < i1
+                        kk = col[k] * 32 + 16 * h + 4 * q
+                        D[by * 32 + j, kk + i0] += vals[j, h, 2 * q]
+                        D[by * 32 + j, kk + i1] += vals[j, h, 2 * q + 1]
+    assert np.array_equal(D[:n, :m], S.float().numpy())
