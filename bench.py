@@ -170,20 +170,36 @@ def algorithmic_bytes(mod, M: int, e: int) -> dict:
 # -------------------------------------------------------------- GPU leg --
 
 
-def run_gpu(args):
+def build_layers(args):
+    """The LLaMA-1B projection stack: args.layers × 7 SLR linears (bf16, r 256,
+    32×32 blocks at 50%), seeded."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(args.seed)
+    t0 = time.time()
+    layers = []
+    for li in range(args.layers):
+        layers.append([(name, make_linear(n, m, 256, 32, 0.5, gen, dev, torch.bfloat16))
+                       for name, n, m in llama1b_shapes()])
+    torch.cuda.synchronize()
+    _log(f"[bench] built {args.layers}x7 SLR linears in {time.time() - t0:.1f}s")
+    return layers
+
+
+def run_gpu(args, layers=None, M=None, steps=None):
+    """One step = every launch of the stack at M token rows (args.batch by
+    default), replayed from a HIP graph unless --eager."""
     import torch
 
     dev = torch.device("cuda:0")
     dtype = torch.bfloat16
     e = 2
-    gen = torch.Generator().manual_seed(args.seed)
-    M, r, p, d = args.batch, 256, 32, 0.5
-    t0 = time.time()
-    layers = []
-    for li in range(args.layers):
-        layers.append([(name, make_linear(n, m, r, p, d, gen, dev, dtype)) for name, n, m in llama1b_shapes()])
-    torch.cuda.synchronize()
-    _log(f"[bench] built {args.layers}x7 SLR linears in {time.time() - t0:.1f}s")
+    M = args.batch if M is None else M
+    steps = args.steps if steps is None else steps
+    gen = torch.Generator().manual_seed(args.seed + 7)
+    if layers is None:
+        layers = build_layers(args)
     h, f = 2048, 5461
     xh = torch.randn(M, h, generator=gen).to(dtype).to(dev)
     xo = torch.randn(M, h, generator=gen).to(dtype).to(dev)
@@ -232,11 +248,11 @@ def run_gpu(args):
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         ev0.record(s)
-        for _ in range(args.steps):
+        for _ in range(steps):
             run()
         ev1.record(s)
         torch.cuda.synchronize()
-    ms_step = ev0.elapsed_time(ev1) / args.steps
+    ms_step = ev0.elapsed_time(ev1) / steps
     n_lin = len(mods)
     n_launch = len(calls)
     total_bytes = sum(b["total"] for b in bytes_)
@@ -624,19 +640,42 @@ def copy_probe(mib: int, reps: int) -> None:
 
 
 def measured_traffic():
-    """HBM bytes per launch of the dominant kernel, from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE per dispatch, calibrated on a plain copy),
-    or None when there is none."""
+    """HBM bytes per launch of the dominant kernel from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, calibrated on a plain copy)
+    and the source revision the counters were measured at; None when absent."""
+    out = {"bytes": None, "revision": None}
     path = ROOT / "profiles" / "slr_kernel_llama1b_decode_counters.md"
     if not path.exists():
-        return None
+        return out
     for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":", 1)[1].strip())
-    return None
+            out["bytes"] = int(line.split(":", 1)[1].strip())
+        elif line.startswith("measured_at_revision:"):
+            out["revision"] = line.split(":", 1)[1].strip()
+    return out
 
 
 # -------------------------------------------------------------- CPU leg --
+
+
+def cpu_model() -> str | None:
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def run_cpu(args):
@@ -711,6 +750,7 @@ def run_cpu(args):
         value=M / t_step,
         unit="tok/s",
         cores=cores,
+        cpu_model=cpu_model(),
         kind=kind,
         sample=(f"one layer's 7 linears (2048/5461-wide, r256, 32x32@50%), fp32, batch {M}, "
                 f"median of {reps} runs = {t_layer * 1e3:.2f} ms, scaled x{args.layers} layers"),
@@ -727,6 +767,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-details", action="store_true",
+                    help="time only the headline batch (skip M=1, M=4 and the 2048-token prefill)")
     ap.add_argument("--eager", action="store_true",
                     help="launch eagerly instead of replaying a HIP graph (default workload, "
                          "llama7b_ffn_decode and llama7b_ffn_decode_nm24)")
@@ -757,13 +799,32 @@ def main():
         print(json.dumps(line), flush=True)
         return
     _log("[bench] GPU leg")
-    g = run_gpu(args)
+    layers = build_layers(args)
+    g = run_gpu(args, layers)
     _log(f"[bench] GPU: {g['ms_step']:.3f} ms/step, {g['tok_s']:.0f} tok/s")
+    # the other decode batches and the 2048-token prefill of the same stack
+    more = {}
+    for M in (() if args.no_details else (1, 4)):
+        gm = run_gpu(args, layers, M=M, steps=max(5, args.steps // 2))
+        more[f"decode_M{M}"] = {
+            "tok_s": round(gm["tok_s"], 1), "ms_per_step": round(gm["ms_step"], 4),
+            "avg_launch_us": round(gm["avg_launch_us"], 3),
+            "hbm_frac": round(gm["achieved_gbs"] / HBM_PEAK_GBS, 4)}
+        _log(f"[bench] decode M={M}: {gm['ms_step']:.3f} ms/step")
+    if not args.no_details:
+        gp = run_gpu(args, layers, M=2048, steps=max(3, args.steps // 10))
+        more["prefill_2048"] = {
+            "tok_s": round(gp["tok_s"], 1), "ms_per_step": round(gp["ms_step"], 4),
+            "TFLOPs": round(gp["step_tflops"], 2),
+            "mfma_frac": round(gp["step_tflops"] / 2500.0, 4)}
+        _log(f"[bench] prefill 2048: {gp['ms_step']:.3f} ms/step")
+    del layers
     cpu = None
     if not args.no_cpu:
         _log("[bench] CPU baseline leg")
         cpu = run_cpu(args)
         _log(f"[bench] CPU: {cpu['value']:.1f} tok/s on {cpu['cores']} cores ({cpu['kind']})")
+    traffic = measured_traffic()
     line = {
         "metric": METRIC,
         "value": round(g["tok_s"], 1),
@@ -796,13 +857,15 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(g["achieved_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(),
-            "kernel": "slr_kernel<bf16,p32,MT1,fused>",
+            "traffic": traffic["bytes"],
+            "traffic_revision": traffic["revision"],
+            "kernel": "slr_kernel<1, 32, 8, 1, 1, 4, 0> (bf16, p 32, KE 8, MT 1, fused, UNR 4, BSR)",
             "avg_launch_us": round(g["avg_launch_us"], 3),
             "algorithmic_bytes_per_launch": int(g["bytes_per_launch"]),
         },
         "cpu_baseline": cpu,
         "details": {
+            **more,
             "step_TFLOPs": round(g["step_tflops"], 3),
             "bytes_per_step": int(g["total_bytes_per_step"]),
             "graph_matches_eager": g["graph_matches_eager"],
