@@ -85,7 +85,7 @@ struct Layout {
   int n_rt, n_kc_max, ku_total;
   int64_t cnt_total;  // int32 row counters: [MG][NB]
   int64_t n_sync;     // u64 handshake words: status, then (2 + n_rt) per token tile
-  int64_t t_part, t_final, part_main, total;
+  int64_t t_part, t_final, part_main, pf_cnt, total;
 };
 
 Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, int64_t n_slots,
@@ -102,19 +102,14 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   const int64_t rows = (int64_t)L.MG * 16 * L.MT;
   int64_t off = 0;
   L.t_part = off;
-  if (M >= kPrefillMinM) {
-    // the prefill latent GEMM's K-split partials, or the streaming kernel's
-    // (calls of this size may take either kernel)
-    int ks = prefill_latent_split(M, r_pad, m_pad, device_cus());
-    if (ks < L.n_kc_max) ks = L.n_kc_max;
-    if (ks > 1) off = align_up(off + 4 * (int64_t)ks * rows * r_pad, 256);
-  } else if (L.n_kc_max > 1) {
-    off = align_up(off + 4 * (int64_t)L.n_kc_max * rows * r_pad, 256);
-  }
+  if (L.n_kc_max > 1) off = align_up(off + 4 * (int64_t)L.n_kc_max * rows * r_pad, 256);
   L.t_final = off;
   off = align_up(off + (int64_t)elem_bytes(dtype) * rows * r_pad, 256);
   L.part_main = off;
   off = align_up(off + 4 * (int64_t)L.MG * n_slots * (16 * L.MT * p), 256);
+  // the prefill kernels' latent tile counters (one per kPrefillLatentRows rows)
+  L.pf_cnt = off;
+  if (M >= kPrefillMinM) off = align_up(off + 4 * ((M + kPrefillLatentRows - 1) / kPrefillLatentRows), 256);
   L.total = off;
   return L;
 }
@@ -381,8 +376,10 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
   const bool nm = s_format == SSL_S_NM24;
   if (nm ? ssl_nm24_takes_prefill(M, call_rows, dtype)
          : ssl_slr_takes_prefill(M, call_rows, block_p, block_q, dtype)) {
-    // Many token rows: the latent GEMM (K split, then combined), then the row
-    // GEMM over groups of block-rows (2:4: on the structured-sparse MFMA).
+    // Many token rows: one launch (after zeroing the latent tile counters)
+    // with the latent GEMM's workgroups first and the row GEMM's after them,
+    // over groups of block-rows (2:4: on the structured-sparse MFMA); a row
+    // workgroup's low-rank steps wait for its token rows' latent tiles.
     const int64_t blk_bytes = nm ? kNmPrefillBlockBytes : (int64_t)block_p * block_p * eb;
     const int cus = device_cus();
     PfArgs rows{}, lat{};
@@ -392,7 +389,13 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
     rows.M = lat.M = (int)M; rows.m = lat.m = (int)m; rows.m_pad = lat.m_pad = (int)m_pad;
     rows.mode = PF_FUSED;
     rows.n = lat.n = n_members;
-    const int64_t T128 = (M + 127) / 128;  // latent token tiles
+    rows.lbm = lat.lbm = kPrefillLatentRows;
+    const DebugKnobs& knobs = debug_knobs();
+    rows.polls = knobs.wait_polls > 0 ? (int)knobs.wait_polls : kSpinLimit;
+    // out of reach of any launch: a latent tile adds 1 to its counter
+    rows.wait_bias = knobs.wait_unreachable ? (1 << 30) : 0;
+    rows.status = members[0].status ? members[0].status : (uint64_t*)members[0].exchange;
+    const int64_t TL = (M + kPrefillLatentRows - 1) / kPrefillLatentRows;  // latent token tiles
     // one group size for the whole call, from all members' rows together
     int64_t total_rows = 0;
     for (int i = 0; i < n_members; ++i)
@@ -422,34 +425,21 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       pm.groups = mb.pf_groups; pm.steps = mb.pf_steps; pm.n_groups = (int)mb.pf_n_groups;
       pm.B = mb.B; pm.ldb = m_pad;
       pm.t = (char*)mb.workspace + L[i].t_final; pm.ldt = mb.r_pad;
-      pm.tpart = (float*)((char*)mb.workspace + L[i].t_part);
+      pm.tcnt = mb.r_pad > 0 ? (int32_t*)((char*)mb.workspace + L[i].pf_cnt) : nullptr;
       pm.r_pad = (int)mb.r_pad;
-      pm.ksplit = mb.r_pad > 0 ? prefill_latent_split(M, mb.r_pad, m_pad, cus) : 1;
       lat.mb[i] = pm;
       items += mb.pf_n_groups * T;
-      if (mb.r_pad > 0) litems += T128 * (mb.r_pad / 64) * pm.ksplit;
+      if (mb.r_pad > 0) litems += TL * (mb.r_pad / 64);
       if (items > 0x7fffffffLL / 8 || litems > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
     }
     rows.off[n_members] = (int)items;
     lat.off[n_members] = (int)litems;
     rows.items = (int)items;
     lat.items = (int)litems;
-    // combine workgroups (members with a split latent), offsets in member order
-    PfArgs comb = lat;
-    {
-      int64_t c = 0;
-      for (int i = 0; i < n_members; ++i) {
-        comb.off[i] = (int)c;
-        if (members[i].NB > 0 && members[i].r_pad > 0 && lat.mb[i].ksplit > 1)
-          c += (M * members[i].r_pad / 4 + 255) / 256;
-      }
-      comb.off[n_members] = (int)c;
-      comb.combine_items = (int)c;
-    }
     if (nm)
-      return check_hip(prefill_launch_fused_nm24(dtype, rows, lat, comb, (hipStream_t)stream),
+      return check_hip(prefill_launch_fused_nm24(dtype, rows, lat, (hipStream_t)stream),
                        "slr prefill launch (2:4)");
-    return check_hip(prefill_launch_fused(dtype, block_p, G, rows, lat, comb, (hipStream_t)stream),
+    return check_hip(prefill_launch_fused(dtype, block_p, G, rows, lat, (hipStream_t)stream),
                      "slr prefill launch");
   }
 

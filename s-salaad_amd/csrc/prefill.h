@@ -29,9 +29,9 @@ struct PfMember {
   int64_t ldb;
   void* t;              // latent [M][r_pad], activation dtype
   int64_t ldt;
-  float* tpart;         // latent split partials [ksplit][M][r_pad], fp32
+  int32_t* tcnt;        // latent tiles written, per latent token tile (zeroed before
+                        // the launch; the low-rank steps wait on them)
   int r_pad;
-  int ksplit;           // latent: K splits of this member
 };
 
 struct PfArgs {
@@ -42,10 +42,16 @@ struct PfArgs {
   int n;                // members
   int items;            // workgroups that do work
   int bm;               // rows kernels: token rows per tile (prefill_row_tile)
-  int combine_items;    // latent combine: workgroups
+  int lbm;              // token rows per latent tile (kPrefillLatentRows)
+  uint64_t* status;     // set to 1 when a bounded wait gives up
+  int polls;            // polls before a wait gives up
+  int wait_bias;        // added to every wait's target (test hook: out of reach)
   int off[5];           // first item of each member
   PfMember mb[4];
 };
+
+// Token rows per latent tile of the prefill kernels.
+constexpr int kPrefillLatentRows = 64;
 
 // Row-kernel tiles (token rows × output features): narrow 128 × 64, tall
 // 256 × 64 and wide 256 × 128; a workgroup owns BN / p block-rows.
@@ -53,19 +59,18 @@ struct PfArgs {
 int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus);
 // Token rows per row-kernel workgroup (128 or 256) for that group size.
 int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus);
-// K splits of the latent GEMM (about one workgroup per CU, ≥ 4 steps each, ≤ 16).
-int prefill_latent_split(int64_t M, int64_t r_pad, int64_t m_pad, int n_cus);
-
-// The fused SLR linear: the latent GEMM (`lat`, K split over lat.ksplit), its
-// combine (`comb`, when split) and the row GEMM (`rows`), in that order on
-// `stream`. dtype: SSL_BF16 or SSL_F16; P ∈ {16, 32, 64}; G = 128/P or 64/P.
+// The fused SLR linear in one launch (after a small kernel that zeroes the
+// latent tile counters): the latent GEMM's workgroups (`lat`, one per 64-token
+// × 64-rank tile over all of in_features) first in the grid, then the row
+// GEMM's (`rows`), whose low-rank steps wait for their token rows' latent
+// tiles. dtype: SSL_F32, SSL_BF16 or SSL_F16; P ∈ {16, 32, 64}; G = 64/P.
 hipError_t prefill_launch_fused(int dtype, int P, int G, const PfArgs& rows, const PfArgs& lat,
-                                const PfArgs& comb, hipStream_t stream);
+                                hipStream_t stream);
 // The fused SLR linear with 2:4 S (32×32 blocks in the row kernel's layout,
 // kNmPrefillBlockBytes each): latent, combine, then the row GEMM on
 // v_smfmac_f32_16x16x64. dtype: SSL_BF16 or SSL_F16; G = 2.
 hipError_t prefill_launch_fused_nm24(int dtype, const PfArgs& rows, const PfArgs& lat,
-                                     const PfArgs& comb, hipStream_t stream);
+                                     hipStream_t stream);
 constexpr int kNmPrefillBlockBytes = 32 * 2 * 16 + 32 * 4;
 // The in-place op: the row GEMM only (rows.mode = PF_OP).
 hipError_t prefill_launch_op(int dtype, int P, int G, const PfArgs& rows, hipStream_t stream);

@@ -162,6 +162,17 @@ __device__ __forceinline__ void dma16(const u32x4& r, uint32_t voff, uint32_t so
                : "s"(lds), "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff))
                : "m0");
 }
+// The same with the sc1 cache policy: device-coherent, for data another
+// workgroup of the launch wrote (the latent) that a stale cache line must not
+// hide.
+__device__ __forceinline__ void dma16_sc1(const u32x4& r, uint32_t voff, uint32_t soff,
+                                          uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen sc1 lds"
+               :
+               : "s"(lds), "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "m0");
+}
+
 // 4 bytes a lane: lane l writes LDS byte address lds + 4·l (active lanes only).
 __device__ __forceinline__ void dma4(const u32x4& r, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
@@ -198,6 +209,18 @@ __device__ __forceinline__ void barrier_only() {
 // contiguous direct-to-LDS writes cannot skip).
 __device__ __forceinline__ int lds_chunk(int R, int kc) { return R * kK + ((kc ^ (R & 7)) << 3); }
 
+// Cross-workgroup hand-over of the latent inside one launch. The latent's
+// workgroups store their tile with the sc1 cache policy (device-coherent),
+// wait for the stores to be acknowledged, and count the tile with a relaxed
+// agent-scope add; a row workgroup polls that count (bounded) before its
+// low-rank steps and reads the latent with sc1 loads. No cache-wide fence.
+constexpr int kSc1Policy = 16;
+__device__ __forceinline__ void st_sc1(const __amdgpu_buffer_rsrc_t& r, int off, float v, int eb,
+                                       uint32_t bits16) {
+  if (eb == 4) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kSc1Policy);
+  else __builtin_amdgcn_raw_buffer_store_b16((unsigned short)bits16, r, off, 0, kSc1Policy);
+}
+
 // Workgroups per compute unit that the stages' LDS allows (160 KiB per CU).
 constexpr int pf_occupancy(int BM, int BN, int S) {
   return (160 * 1024) / ((BM + BN) * kK * 2 * S) > 4 ? 4 : (160 * 1024) / ((BM + BN) * kK * 2 * S);
@@ -218,10 +241,8 @@ constexpr int pf_occupancy(int BM, int BN, int S) {
 // would otherwise reload them from the argument segment every step.
 // ---------------------------------------------------------------------------
 template <int DT, int KIND, int P, int BM, int BN, int WM, int WN, int S>
-__global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
-    PfArgs by_value) {
-  (void)by_value;
-  const PfArgs& a = *(const PfArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+__device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
+                                        uint16_t (*lds)[Tile<BM, BN, WM, WN>::LDS]) {
   using T = Tile<BM, BN, WM, WN>;
   constexpr int IA = T::IA, IB = T::IB, MTI = T::MTI, NTI = T::NTI;
   constexpr bool ROWS = KIND != K_LATENT;
@@ -246,19 +267,19 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   static_assert(NRV <= 64, "a record view is one word per lane");
   using MM = Mma<DT, DT == DT_F32 ? 4 : 8>;
   using Frag = typename MM::Frag;
-  __shared__ __align__(1024) uint16_t lds[S][T::LDS];
 
   // ---- which tile
-  const int items = (KIND == K_LATENT) ? (int)gridDim.x : a.items;
+  const int items = a.items;
   int item;
   if constexpr (KIND == K_LATENT) {
-    item = blockIdx.x;
+    item = bid;
+    if (item >= items) return;
   } else {  // XCD-major order
-    const int b = blockIdx.x;
     const int per_xcd = (items + kXcds - 1) / kXcds;
-    item = (b % kXcds) * per_xcd + b / kXcds;
+    item = (bid % kXcds) * per_xcd + bid / kXcds;
     if (item >= items) return;
   }
+  (void)n_bid;
   int mi = 0;
   while (mi + 1 < a.n && item >= a.off[mi + 1]) ++mi;
   const PfMember& mb = a.mb[mi];
@@ -268,17 +289,13 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   int m0, s_begin, s_end;            // token tile; step range
   int n_sp = 0;                      // sparse steps (rows kernels)
   const int32_t* gr = nullptr;       // group record: {step_begin, step_end, rows[G]}
-  int rt = 0, kspl = 0;              // latent: rank tile, K split
+  int rt = 0;                        // latent: rank tile
   if constexpr (KIND == K_LATENT) {
     const int n_rt = mb.r_pad / BN;
-    kspl = local % mb.ksplit;
-    const int tile = local / mb.ksplit;
-    rt = tile % n_rt;
-    m0 = (tile / n_rt) * BM;
-    const int units = a.m_pad / KS;
-    const int ku = (units + mb.ksplit - 1) / mb.ksplit;
-    s_begin = kspl * ku;
-    s_end = min(s_begin + ku, units);
+    rt = local % n_rt;
+    m0 = (local / n_rt) * BM;
+    s_begin = 0;
+    s_end = a.m_pad / KS;
   } else {
     const int tt = local / mb.n_groups, grp = local % mb.n_groups;
     m0 = tt * BM;
@@ -384,6 +401,29 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
     else return __builtin_amdgcn_ds_bpermute((w + e_t) * 4, rv);
   };
 
+  // ---- wait until the latent tiles of this tile's token rows are written
+  // (rows kernels with low-rank steps; one lane per wave polls, bounded)
+  auto wait_latent = [&]() {
+    if constexpr (LR) {
+      if (lane == 0) {
+        const int lbm = a.lbm, target = mb.r_pad / 64 + a.wait_bias, polls = a.polls;
+        const int lt1 = (min(m0 + BM, M) - 1) / lbm;
+        for (int lt = m0 / lbm; lt <= lt1; ++lt) {
+          int n = 0;
+          while (__hip_atomic_load(mb.tcnt + lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+                 target) {
+            __builtin_amdgcn_s_sleep(2);
+            if (++n > polls) {
+              __hip_atomic_store(a.status, (uint64_t)1, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+              break;
+            }
+          }
+        }
+      }
+    }
+  };
+
   // ---- issue the tile loads of step u (clamped past the end) into stage `k`
   // (rv: the step's record view); returns the step's mask (uniform).
   // `ragged` is set when an x chunk of the step is cut by in_features (those
@@ -444,8 +484,9 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
         }
       } else {
         const uint32_t k0b = (uint32_t)((u - n_sp) * KS * EB);  // ranks (K_ROWS_FUSED only)
+        if (u == n_sp) wait_latent();  // before the first load of t
 #pragma unroll
-        for (int i = 0; i < IA; ++i) dma16(tr, at_[i], k0b, la + i * kRowBytes32);
+        for (int i = 0; i < IA; ++i) dma16_sc1(tr, at_[i], k0b, la + i * kRowBytes32);
 #pragma unroll
         for (int i = 0; i < IB; ++i) dma16(ar, lroff[i], k0b, lb + i * kRowBytes32);
         mask = lr_mask;
@@ -574,10 +615,12 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   // stores below could otherwise alias the argument segment and force a
   // reload per store.
   if constexpr (KIND == K_LATENT) {
-    void* const t_out = mb.t;
-    float* const t_part = mb.tpart;
+    // the tile, rounded once to the activation dtype as F.linear's output is,
+    // stored device-coherently, then counted for its token rows
+    const __amdgpu_buffer_rsrc_t tr =
+        __builtin_amdgcn_make_buffer_rsrc(mb.t, (short)0, 0x7fffffff, 0x00020000);
     const int64_t ldt = mb.ldt;
-    const bool whole = mb.ksplit == 1;
+    int32_t* const tcnt = mb.tcnt;
 #pragma unroll
     for (int mt = 0; mt < MTI; ++mt)
 #pragma unroll
@@ -588,13 +631,14 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
         for (int nt = 0; nt < NTI; ++nt) {
           const int col = rt * BN + wn * T::TN + 16 * nt + c;
           const float v = acc[mt][nt][e];
-          if (whole) {
-            store_elem<DT>(t_out, (int64_t)r * ldt + col, v);
-          } else {
-            t_part[((int64_t)kspl * M + r) * ldt + col] = v;
-          }
+          st_sc1(tr, (int)(((int64_t)r * ldt + col) * EB), v, EB,
+                 EB == 2 ? to_bits<DT>(v) : 0u);
         }
       }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores acknowledged
+    __syncthreads();
+    if (tid == 0)
+      __hip_atomic_fetch_add(tcnt + m0 / BM, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else if constexpr (NM) {
     // lane (c, gq) holds features 4gq + e of feature tile nt for token 16·mt + c
     void* const y_out = mb.y;
@@ -648,34 +692,65 @@ __global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(
   }
 }
 
-// t = Σ_splits partials in split order, rounded once to the activation dtype.
-template <int DT>
-__global__ __launch_bounds__(kPfThreads) void pf_latent_combine(PfArgs by_value) {
+// The op's row kernel (no latent): the engine in a kernel of its own.
+template <int DT, int KIND, int P, int BM, int BN, int WM, int WN, int S>
+__global__ __launch_bounds__(kPfThreads, pf_occupancy(BM, BN, S)) void pf_gemm(PfArgs by_value) {
   (void)by_value;
   const PfArgs& a = *(const PfArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  __shared__ __align__(1024) uint16_t lds[S][Tile<BM, BN, WM, WN>::LDS];
+  pf_body<DT, KIND, P, BM, BN, WM, WN, S>(a, blockIdx.x, gridDim.x, lds);
+}
+
+// The fused linear in one launch: grid [latent workgroups (padded to a
+// multiple of kXcds)][row workgroups]. Latent workgroups come first in the
+// grid, so every tile a row workgroup waits for belongs to a workgroup
+// dispatched before it; they never wait themselves. One LDS allocation serves
+// both roles.
+constexpr int kLatentStages = 3;
+template <int BM, int BN, int WM, int WN>
+constexpr int fused_lds() {
+  return Tile<BM, BN, WM, WN>::LDS * 2 > Tile<kPrefillLatentRows, 64, 2, 2>::LDS * kLatentStages
+             ? Tile<BM, BN, WM, WN>::LDS * 2
+             : Tile<kPrefillLatentRows, 64, 2, 2>::LDS * kLatentStages;
+}
+template <int DT, int KIND, int P, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(kPfThreads, pf_occupancy(fused_lds<BM, BN, WM, WN>() / kK, 0, 1))
+void pf_fused(PfArgs rows_by_value, PfArgs lat_by_value) {
+  (void)rows_by_value;
+  (void)lat_by_value;
+  const PfArgs* args = (const PfArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  const PfArgs& rows = args[0];
+  const PfArgs& lat = args[1];
+  __shared__ __align__(1024) uint16_t raw[fused_lds<BM, BN, WM, WN>()];
+  const int nlat = (lat.items + kXcds - 1) / kXcds * kXcds;
   const int b = blockIdx.x;
-  int i = 0;
-  while (i + 1 < a.n && b >= a.off[i + 1]) ++i;
-  const PfMember& mb = a.mb[i];
-  const int64_t q = (int64_t)(b - a.off[i]) * kPfThreads + threadIdx.x;  // 4-element piece
-  const int64_t n = (int64_t)a.M * mb.ldt / 4;
-  if (q >= n) return;
-  const int64_t slab = (int64_t)a.M * mb.ldt;
-  float4 v = *(const float4*)(mb.tpart + 4 * q);
-  for (int k = 1; k < mb.ksplit; ++k) {
-    const float4 w = *(const float4*)(mb.tpart + k * slab + 4 * q);
-    v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+  if (b < nlat) {
+    using TL = Tile<kPrefillLatentRows, 64, 2, 2>;
+    pf_body<DT, K_LATENT, 64, kPrefillLatentRows, 64, 2, 2, kLatentStages>(
+        lat, b, nlat, reinterpret_cast<uint16_t(*)[TL::LDS]>(raw));
+  } else {
+    using TR = Tile<BM, BN, WM, WN>;
+    pf_body<DT, KIND, P, BM, BN, WM, WN, 2>(rows, b - nlat, (int)gridDim.x - nlat,
+                                            reinterpret_cast<uint16_t(*)[TR::LDS]>(raw));
   }
-  const float o[4] = {v.x, v.y, v.z, v.w};
-  st_w<DT, 4>(mb.t, 4 * q, o);
+}
+
+// Zero every member's latent tile counters (a fill kernel, so that the pair
+// of launches can be captured in a graph).
+__global__ __launch_bounds__(kPfThreads) void pf_zero_counts(PfArgs lat_by_value) {
+  (void)lat_by_value;
+  const PfArgs& a = *(const PfArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int n_lt = (a.M + a.lbm - 1) / a.lbm;
+  for (int i = threadIdx.x; i < a.n * n_lt; i += kPfThreads) {
+    int32_t* c = a.mb[i / n_lt].tcnt;
+    if (c) c[i % n_lt] = 0;
+  }
 }
 
 // Row-kernel tiles: tall 256 × 64 (waves 4 × 1, 64 × 64 each; 80 KiB of LDS,
 // two workgroups per compute unit) and narrow 128 × 64 (waves 2 × 2, 64 × 32
-// each; 48 KiB, three per compute unit), both with two stages. The latent uses
-// the narrow tile with three stages.
-constexpr int kLatentStages = 3;
-
+// each; 48 KiB), both with two stages. The latent's tiles are 64 tokens × 64
+// ranks (waves 2 × 2) with three stages.
 template <int DT, int KIND, int P>
 hipError_t launch_rows(const PfArgs& a, int G, hipStream_t s) {
   const int per_xcd = (a.items + kXcds - 1) / kXcds;
@@ -702,45 +777,35 @@ hipError_t launch_rows_p(const PfArgs& rows, int P, int G, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-template <int DT>
-hipError_t launch_latent(const PfArgs& lat, const PfArgs& comb, hipStream_t s) {
-  if (lat.items > 0) {
-    hipLaunchKernelGGL((pf_gemm<DT, K_LATENT, 64, 128, 64, 2, 2, kLatentStages>),
-                       dim3((unsigned)lat.items), dim3(kPfThreads), 0, s, lat);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (comb.combine_items > 0) {
-      hipLaunchKernelGGL((pf_latent_combine<DT>), dim3((unsigned)comb.combine_items),
-                         dim3(kPfThreads), 0, s, comb);
-      e = hipGetLastError();
-      if (e != hipSuccess) return e;
-    }
-  }
-  return hipSuccess;
-}
-
-template <int DT>
-hipError_t launch_fused(const PfArgs& rows, const PfArgs& lat, const PfArgs& comb, int P, int G,
-                        hipStream_t s) {
-  const hipError_t e = launch_latent<DT>(lat, comb, s);
+// Latent and rows in one launch (after zeroing the latent tile counters).
+template <int DT, int KIND, int P>
+hipError_t launch_fused_p(const PfArgs& rows, const PfArgs& lat, int G, hipStream_t s) {
+  if (G * P != 64) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(pf_zero_counts, dim3(1), dim3(kPfThreads), 0, s, lat);
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_rows_p<DT, K_ROWS_FUSED>(rows, P, G, s);
-}
-
-template <int DT>
-hipError_t launch_fused_nm24(const PfArgs& rows, const PfArgs& lat, const PfArgs& comb,
-                             hipStream_t s) {
-  hipError_t e = launch_latent<DT>(lat, comb, s);
-  if (e != hipSuccess || rows.items == 0) return e;
+  const int nlat = (lat.items + kXcds - 1) / kXcds * kXcds;
   const int per_xcd = (rows.items + kXcds - 1) / kXcds;
-  const dim3 grid((unsigned)(per_xcd * kXcds)), blk(kPfThreads);
+  const dim3 grid((unsigned)(nlat + per_xcd * kXcds)), blk(kPfThreads);
   if (rows.bm == 256)
-    hipLaunchKernelGGL((pf_gemm<DT, K_ROWS_NM, 32, 256, 64, 4, 1, 2>), grid, blk, 0, s, rows);
+    hipLaunchKernelGGL((pf_fused<DT, KIND, P, 256, 64, 4, 1>), grid, blk, 0, s, rows, lat);
   else if (rows.bm == 128)
-    hipLaunchKernelGGL((pf_gemm<DT, K_ROWS_NM, 32, 128, 64, 2, 2, 2>), grid, blk, 0, s, rows);
+    hipLaunchKernelGGL((pf_fused<DT, KIND, P, 128, 64, 2, 2>), grid, blk, 0, s, rows, lat);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_fused(const PfArgs& rows, const PfArgs& lat, int P, int G, hipStream_t s) {
+  switch (P) {
+    case 16: return launch_fused_p<DT, K_ROWS_FUSED, 16>(rows, lat, G, s);
+    case 32: return launch_fused_p<DT, K_ROWS_FUSED, 32>(rows, lat, G, s);
+    case 64:
+      if constexpr (DT != DT_F32) return launch_fused_p<DT, K_ROWS_FUSED, 64>(rows, lat, G, s);
+      break;
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -763,33 +828,21 @@ int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cu
   return (tall >= 2 * n_cus || tall >= narrow) ? 256 : 128;
 }
 
-int prefill_latent_split(int64_t M, int64_t r_pad, int64_t m_pad, int n_cus) {
-  // latent tiles are 128 tokens × 64 ranks; split K until about one workgroup
-  // per compute unit, keeping at least 4 steps (256 columns) per split
-  const int64_t tiles = ((M + 127) / 128) * (r_pad / 64);
-  if (tiles <= 0) return 1;
-  int64_t ks = n_cus / tiles;
-  const int64_t units = m_pad / 64;
-  if (ks > units / 4) ks = units / 4;
-  if (ks > 16) ks = 16;
-  return ks < 1 ? 1 : (int)ks;
-}
-
 hipError_t prefill_launch_fused(int dtype, int P, int G, const PfArgs& rows, const PfArgs& lat,
-                                const PfArgs& comb, hipStream_t stream) {
+                                hipStream_t stream) {
   switch (dtype) {
-    case SSL_BF16: return launch_fused<DT_BF16>(rows, lat, comb, P, G, stream);
-    case SSL_F16: return launch_fused<DT_F16>(rows, lat, comb, P, G, stream);
-    case SSL_F32: return launch_fused<DT_F32>(rows, lat, comb, P, G, stream);
+    case SSL_BF16: return launch_fused<DT_BF16>(rows, lat, P, G, stream);
+    case SSL_F16: return launch_fused<DT_F16>(rows, lat, P, G, stream);
+    case SSL_F32: return launch_fused<DT_F32>(rows, lat, P, G, stream);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t prefill_launch_fused_nm24(int dtype, const PfArgs& rows, const PfArgs& lat,
-                                     const PfArgs& comb, hipStream_t stream) {
+                                     hipStream_t stream) {
   switch (dtype) {
-    case SSL_BF16: return launch_fused_nm24<DT_BF16>(rows, lat, comb, stream);
-    case SSL_F16: return launch_fused_nm24<DT_F16>(rows, lat, comb, stream);
+    case SSL_BF16: return launch_fused_p<DT_BF16, K_ROWS_NM, 32>(rows, lat, 2, stream);
+    case SSL_F16: return launch_fused_p<DT_F16, K_ROWS_NM, 32>(rows, lat, 2, stream);
   }
   return hipErrorInvalidValue;
 }

@@ -309,9 +309,10 @@ def test_workspace_sizes_are_aligned_and_monotone():
     # ([MG][slots][16·MT][p]); each part 256-byte aligned
     assert a == 8 * 16 * 256 * 4 + 16 * 256 * 2
     assert b == a + 100 * 16 * 64 * 4
-    # 2048 rows take the prefill kernels: the latent GEMM's K-split fp32
-    # partials (4 splits on a 256-CU device, the count assumed without a GPU)
-    assert c == 4 * 2048 * 256 * 4 + 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4
+    # 2048 rows: no latent K split (the prefill kernels run the latent in the
+    # row launch, whole), the final latent, the split-row partials, then one
+    # latent tile counter per 64 rows (32 int32, 256-byte aligned)
+    assert c == 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4 + 256
     # counters: one per (token tile, block-row)
     assert lib.ssl_slr_counter_count(16, 172) == 172
     assert lib.ssl_slr_counter_count(2048, 172) == 32 * 172

@@ -45,12 +45,14 @@ def _counters_at_rest(dev) -> bool:
                if idx == dev.index)
 
 
-@pytest.mark.parametrize("M", [1, 16, 40])
+@pytest.mark.parametrize("M", [1, 16, 40, 600])
 def test_wait_give_up_is_reported_and_counters_net_to_zero(M, knobs, gpu_device, monkeypatch):
     """Every unit its own chunk: each row's finaliser waits for its other chunks
     and for the latent. With unreachable targets every wait gives up after 64
     polls; the status word says so, the late chunks' arrivals bring every row
-    counter back to zero, and the next normal calls are exact."""
+    counter back to zero, and the next normal calls are exact. At 600 rows the
+    call runs the prefill kernels, whose row workgroups wait for the latent
+    tiles of the same launch: the same give-up, the same recovery."""
     monkeypatch.setattr(_runtime, "_CHUNK_BYTES", 1)
     dtype = torch.bfloat16
     prob = make_problem(256, 1024, 96, 32, 0.4, dtype, seed=M, skew=True)
