@@ -32,8 +32,12 @@ headline):
   llama7b_ffn_decode   one 11008×4096 SLR linear (64×64 blocks at 50%, r 256,
                        bf16), --batch tokens (default 1), 8 weight copies
                        cycled in a HIP graph: GB/s of algorithmic bytes
-  llama7b_ffn_prefill  the same linear at 2048 tokens (latent GEMM, its
-                       combine, the row GEMM): TFLOP/s
+  llama7b_ffn_prefill  the same linear at 2048 tokens (one launch: the latent
+                       t = x·Bᵀ workgroups, then the row workgroups for
+                       x·Sᵀ + t·Aᵀ + b): TFLOP/s
+  llama7b_ffn_prefill_nm24  the 2:4 projection of llama7b_ffn_decode_nm24 at
+                       2048 tokens: TFLOP/s of the dense-equivalent work
+                       (x·Bᵀ, t·Aᵀ and the kept half of S)
   block_topk           the compression loop's block projection (project_S) of
                        an 11008×4096 fp32 matrix, 64×64 blocks, half kept:
                        GB/s of compulsory traffic
@@ -398,6 +402,27 @@ def run_workload(args) -> dict:
                     config={"workload": "llama7b_ffn_prefill", "n": n, "m": m, "rank": r,
                             "block": p, "block_density": 0.5, "batch_tokens": M,
                             "parallelism": "single_gpu"},
+                    roofline={"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
+                              "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4), "traffic": None,
+                              "flops_per_call": int(fl), "low_rank_flops": 2 * M * r * (m + n)})
+    if args.workload == "llama7b_ffn_prefill_nm24":
+        from ssalaad_amd import LRSLinear
+
+        M = args.batch if args.batch_set else 2048
+        grp = torch.rand(n, m // 4, 4, generator=gen).argsort(dim=-1).argsort(dim=-1) < 2
+        S = (torch.randn(n, m, generator=gen) * 0.02 * grp.reshape(n, m)).to(torch.bfloat16)
+        A = (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
+        B = (torch.randn(r, m, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
+        mod = LRSLinear(A, B, S.to(dev), in_features=m, out_features=n, nm_n=2, nm_m=4)
+        x = torch.randn(M, m, generator=gen).to(torch.bfloat16).to(dev)
+        us = _time_eager(lambda: mod(x), args.steps)
+        fl = 2 * M * r * (m + n) + 2 * M * n * (m // 2)
+        tf = fl / us / 1e6
+        return dict(base, metric="SLR-linear prefill TFLOP/s (LLaMA-7B FFN projection, 2:4 S)",
+                    value=round(tf, 1), unit="TFLOP/s", ms_per_step=round(us / 1e3, 5),
+                    dtype="bf16",
+                    config={"workload": "llama7b_ffn_prefill_nm24", "n": n, "m": m, "rank": r,
+                            "sparsity": "2:4", "batch_tokens": M, "parallelism": "single_gpu"},
                     roofline={"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
                               "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4), "traffic": None,
                               "flops_per_call": int(fl), "low_rank_flops": 2 * M * r * (m + n)})
@@ -778,7 +803,8 @@ def main():
                     help="only run a plain device copy of MIB MiB (counter calibration)")
     ap.add_argument("--workload", default="llama1b_decode",
                     choices=["llama1b_decode", "llama7b_ffn_decode", "llama7b_ffn_prefill",
-                             "llama7b_ffn_decode_nm24", "block_topk", "llama60m_forward",
+                             "llama7b_ffn_decode_nm24", "llama7b_ffn_prefill_nm24", "block_topk",
+                             "llama60m_forward",
                              "llama1b_decode_step", "sweep", "llama1b_prefill"])
     args = ap.parse_args()
     args.batch_set = args.batch is not None
