@@ -7,20 +7,27 @@ step = one pass of a batch through all 168 linears (y = x·Bᵀ·Aᵀ + x·Sᵀ)
 the projection work of one decode step. Weights (1.69 GB) exceed the 256 MB
 last-level cache, so every step streams them from HBM.
 
-Launches: the linears that read the same activation run as one launch of the
-fused kernel (LRSLinearGroup): q, k, v | o | gate, up | down, i.e. 4 launches
-per layer, 96 per step (--no-group: one launch per linear, 168 per step). Each
-linear is computed exactly as its own module computes it.
+Data flow: each layer's projections read what the previous one wrote, in
+the order of a decoder layer: q, k, v read the layer input; o reads q's output
+(attention's output in a model); gate and up read o's output (the normed
+residual); down reads gate's output (silu(gate)·up); the next layer reads
+down's output. So every projection waits for the one before it, as in decode.
+
+Launches: one chained launch per layer (LRSLinearChain: the stages q,k,v |
+o | gate,up | down in one launch, each waiting inside the launch for its
+input), 24 per step. --no-chain: the stages as grouped launches
+(LRSLinearGroup), 4 per layer, 96 per step; --no-group: one launch per
+linear, 168 per step.
 
 Timing: the step is captured once in a HIP graph and replayed; W untimed
 replays, then K replays bracketed by synchronize + HIP events on the replay
 stream. value = M·K / elapsed (tokens/s).
 
 roofline: every launch of the step is the fused kernel (latent, sparse blocks,
-t·Aᵀ and epilogue); its average launch duration = the HIP-event time of the
-graph replays / launches per step (gaps between launches included, so this
-slightly understates the kernel); achieved = algorithmic bytes per launch /
-that duration.
+t·Aᵀ and epilogue; chained: a layer's four stages); its average launch
+duration = the HIP-event time of the graph replays / launches per step (gaps
+between launches included, so this slightly understates the kernel);
+achieved = algorithmic bytes per launch / that duration.
 
 cpu_baseline: the reference AVX2 BSR kernel (oracle/_ref, compiled from the
 reference's own source) plus torch-CPU F.linear ×2 — the reference's CPU
@@ -80,6 +87,13 @@ for _p in (ROOT, ROOT / "s-salaad_amd"):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBS = 8000.0
+# the dominant kernel of the default workload's launches, by launch mode
+KERNEL_NAMES = {
+    "chain": "slr_chain_kernel<1, 32, 8, 1, 4, 0> (bf16, p 32, KE 8, MT 1, UNR 4, BSR): one "
+             "launch per layer, stages q,k,v | o | gate,up | down",
+    "groups": "slr_kernel<1, 32, 8, 1, 1, 4, 0> (bf16, p 32, KE 8, MT 1, fused, UNR 4, BSR)",
+    "linears": "slr_kernel<1, 32, 8, 1, 1, 4, 0> (bf16, p 32, KE 8, MT 1, fused, UNR 4, BSR)",
+}
 METRIC = "SLR-linear GB/s & TFLOP/s (% roofline); decode tok/s at LLaMA-1B shape"
 
 
@@ -205,29 +219,51 @@ def run_gpu(args, layers=None, M=None, steps=None):
     if layers is None:
         layers = build_layers(args)
     h, f = 2048, 5461
-    xh = torch.randn(M, h, generator=gen).to(dtype).to(dev)
-    xo = torch.randn(M, h, generator=gen).to(dtype).to(dev)
-    xd_buf = torch.zeros(M, 5504, dtype=dtype, device=dev)
-    xd_buf[:, :f] = torch.randn(M, f, generator=gen).to(dtype).to(dev)
-    xd = xd_buf[:, :f]
-    xin = {"q": xh, "k": xh, "v": xh, "o": xo, "gate": xh, "up": xh, "down": xd}
+    x0 = torch.randn(M, h, generator=gen).to(dtype).to(dev)
     mods = [(name, mod) for layer in layers for name, mod in layer]
     bytes_ = [algorithmic_bytes(mod, M, e) for _, mod in mods]
-    # launches: the linears that read the same activation go in one launch
-    # (q, k, v | o | gate, up | down) unless --no-group
-    from ssalaad_amd import LRSLinearGroup
+    from ssalaad_amd import LRSLinearChain, LRSLinearGroup
 
-    calls = []
+    # per layer: q,k,v (layer input) | o (q's output) | gate,up (o's output) |
+    # down (gate's output); the next layer reads down's output
+    chains = []
     for layer in layers:
         d = dict(layer)
-        sets = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
-        if args.no_group:
-            sets = [[name] for name, _ in layer]
-        for names in sets:
-            calls.append((LRSLinearGroup(*[d[nm] for nm in names]), xin[names[0]]))
+        chains.append(LRSLinearChain([[d["q"], d["k"], d["v"]], [d["o"]], [d["gate"], d["up"]],
+                                      [d["down"]]], sources=[d["q"], d["o"], d["gate"]]))
+    groups = [(LRSLinearGroup(*c.groups[0].members), c.groups[1].members[0],
+               LRSLinearGroup(*c.groups[2].members), c.groups[3].members[0]) for c in chains]
+    mode = "linears" if args.no_group else ("groups" if args.no_chain else "chain")
+
+    def layer_fwd(li, x):
+        """The layer's 7 outputs (q, k, v, o, gate, up, down)."""
+        if mode == "chain":
+            return [y for stage in chains[li](x) for y in stage]
+        d = dict(layers[li])
+        if mode == "groups":
+            g_qkv, m_o, g_gu, m_d = groups[li]
+            q, k, v = g_qkv(x)
+            o = m_o(q)
+            g, u = g_gu(o)
+            return [q, k, v, o, g, u, m_d(g)]
+        q, k, v = d["q"](x), d["k"](x), d["v"](x)
+        o = d["o"](q)
+        g, u = d["gate"](o), d["up"](o)
+        return [q, k, v, o, g, u, d["down"](g)]
 
     def step():
-        return [out for grp, x in calls for out in grp(x)]
+        outs, x = [], x0
+        for li in range(len(layers)):
+            ys = layer_fwd(li, x)
+            outs.append((x, ys))
+            x = ys[-1]
+        return outs
+
+    if mode == "chain":
+        st = [[m._kernel() for m in g.members] for g in chains[0].groups]
+        n_launch = len(layers) * (1 if chains[0]._chained(st, M) else 4)
+    else:
+        n_launch = len(layers) * (4 if mode == "groups" else 7)
 
     s = torch.cuda.Stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))
@@ -258,7 +294,6 @@ def run_gpu(args, layers=None, M=None, steps=None):
         torch.cuda.synchronize()
     ms_step = ev0.elapsed_time(ev1) / steps
     n_lin = len(mods)
-    n_launch = len(calls)
     total_bytes = sum(b["total"] for b in bytes_)
     total_flops = sum(b["flops"] for b in bytes_)
     avg_us = ms_step * 1e3 / n_launch
@@ -274,11 +309,13 @@ def run_gpu(args, layers=None, M=None, steps=None):
         n_linears=n_lin,
         n_launches=n_launch,
     )
-    # a parity spot check of one linear of the timed graph against a fresh call
-    name, mod = mods[-1]
-    ref = mod(xin[name])
+    # a parity spot check of the timed graph: the last layer recomputed eagerly
+    # from the input the graph gave it
+    x_last, ys_last = keep[-1]
+    ref = layer_fwd(len(layers) - 1, x_last)
     torch.cuda.synchronize()
-    res["graph_matches_eager"] = bool(torch.equal(keep[-1], ref))
+    res["graph_matches_eager"] = all(bool(torch.equal(a, b)) for a, b in zip(ys_last, ref))
+    res["mode"] = mode
     from ssalaad_amd.ls_linear import latent_wait_status
 
     with torch.cuda.stream(s):
@@ -797,6 +834,8 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="launch eagerly instead of replaying a HIP graph (default workload, "
                          "llama7b_ffn_decode and llama7b_ffn_decode_nm24)")
+    ap.add_argument("--no-chain", action="store_true",
+                    help="the four stages of a layer as grouped launches instead of one chained launch")
     ap.add_argument("--no-group", action="store_true",
                     help="one launch per linear instead of grouping q/k/v and gate/up")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -869,6 +908,7 @@ def main():
             "layers": args.layers,
             "linears_per_step": g["n_linears"],
             "launches_per_step": g["n_launches"],
+            "launch": g["mode"],
             "hidden": 2048,
             "ffn": 5461,
             "rank": 256,
@@ -885,7 +925,7 @@ def main():
             "frac": round(g["achieved_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": traffic["bytes"],
             "traffic_revision": traffic["revision"],
-            "kernel": "slr_kernel<1, 32, 8, 1, 1, 4, 0> (bf16, p 32, KE 8, MT 1, fused, UNR 4, BSR)",
+            "kernel": KERNEL_NAMES[g["mode"]],
             "avg_launch_us": round(g["avg_launch_us"], 3),
             "algorithmic_bytes_per_launch": int(g["bytes_per_launch"]),
         },

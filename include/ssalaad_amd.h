@@ -327,6 +327,50 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
                           int32_t block_p, int32_t block_q, int32_t dtype,
                           const ssl_slr_member* members, int32_t n_members, void* stream);
 
+/* Chained launch: up to 4 dependent stages of grouped SLR linears (up to 8
+ * linears in all) in ONE launch, e.g. a decoder layer's q,k,v -> o -> gate,up
+ * -> down projections at decode. Stage 0 reads the launch's input x; every
+ * later stage reads the output (y) of one member of an earlier stage, `src`,
+ * as it is written inside the launch: its workgroups start their weight loads,
+ * wait (bounded) until src has finished every output row tile of their token
+ * tile, then read x device-coherently. Each member is computed as
+ * ssl_slr_forward_group computes it for its stage's members alone (same plans
+ * and rounding points); stage 0 also takes the same latent split, so its
+ * outputs equal the grouped launch's bit for bit, while later stages compute
+ * each latent tile over all of in_features in one workgroup (the fp32 sums of
+ * t = x·Bᵀ then run in another order). Replaces nothing in the reference (its model calls
+ * every module on its own, ssalaad/efficient/model.py:41-57); it removes the
+ * kernel boundaries between a layer's projections, which dominate decode.
+ *
+ * Restrictions: bf16 or fp16; square 16/32/64 blocks or 2:4 storage; calls
+ * the streaming kernel takes (for every stage, ssl_slr_takes_prefill /
+ * ssl_nm24_takes_prefill is 0; otherwise SSL_ERR_UNSUPPORTED, and the caller
+ * launches the stages one by one). A src member's output is stored
+ * device-coherently and must lie within 2 GiB (M · ldy · element size).
+ * Stage `sync` words: ssl_slr_chain_sync_count(M) int32, zero at rest, owned
+ * by the stage; the launch returns them to zero (also after a wait that gave
+ * up, which the members' status word reports). Calls that share sync words,
+ * or any member's counters, exchange area or workspace, must be ordered on
+ * one stream. */
+#define SSL_MAX_CHAIN_STAGES 4
+typedef struct ssl_slr_stage {
+  const void* x;   /* stage 0: the launch's input; later stages: NULL or src's y */
+  int64_t ldx;     /* stage 0: x's row stride (later stages use src's ldy) */
+  int64_t m;       /* in_features of the stage's members (≤ src's NB · p) */
+  int64_t m_pad;   /* in_features padded to a multiple of 64 (B's row stride) */
+  int32_t first;   /* the stage's members: members[first .. first + count) */
+  int32_t count;
+  int32_t src;     /* later stages: index of the member whose output is x; -1 for stage 0 */
+  int32_t* sync;   /* later stages: ssl_slr_chain_sync_count(M) zeroed int32 words,
+                    * 256-byte aligned */
+  int64_t n_sync;
+} ssl_slr_stage;
+
+int64_t ssl_slr_chain_sync_count(int64_t M);
+int ssl_slr_forward_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,
+                          const ssl_slr_stage* stages, int32_t n_stages,
+                          const ssl_slr_member* members, int32_t n_members, void* stream);
+
 /* -------------------------------------------------------------------------
  * Block projection (device): keep the n_keep blocks of largest Frobenius norm.
  * Replaces ssalaad/inference/egar.py:296-317 (_project_S), the sparse step of

@@ -130,6 +130,81 @@ void latent_chunks(const Layout& L, int64_t n_stream, int64_t per_chunk, int* n_
   if (*n_kc < 1) *n_kc = 1;
 }
 
+// Checks of one member of a fused call, and its scratch layout. Returns
+// SSL_OK, or the status of the failure already recorded.
+int check_member(int i, const ssl_slr_member& mb, int64_t M, int64_t m_pad, int block_p,
+                 int block_q, int dtype, int s_format, Layout* L) {
+  const int eb = elem_bytes(dtype);
+  if (mb.NB < 0 || mb.r_pad < 0 || mb.n_chunks < 0 || mb.n_slots < 0 || mb.lr_wgs < 0)
+    return fail(SSL_ERR_INVALID, "linear %d: negative size", i);
+  if (mb.s_format != s_format)
+    return fail(SSL_ERR_INVALID, "linear %d: all linears of a call share the sparse storage", i);
+  if (mb.r_pad % 64) return fail(SSL_ERR_INVALID, "linear %d: r_pad must be a multiple of 64", i);
+  if (mb.nnz < 0 || !slab_count_ok(mb.nnz, block_q / (4 * stream_ke(dtype, block_q))))
+    return fail(SSL_ERR_UNSUPPORTED, "linear %d: too many blocks (%lld) for one call", i,
+                (long long)mb.nnz);
+  if (mb.NB == 0) {  // no output columns: nothing to launch for this linear
+    *L = slr_layout(M, 0, block_p, 0, m_pad, 0, dtype);
+    return SSL_OK;
+  }
+  if (mb.n_chunks == 0)
+    return fail(SSL_ERR_INVALID, "linear %d: empty plan for a non-empty output", i);
+  if ((mb.r_pad > 0) != (mb.lr_wgs > 0) || mb.lr_wgs > mb.n_chunks)
+    return fail(SSL_ERR_INVALID, "linear %d: lr_wgs must count the plan's chunks with low-rank units", i);
+  if (!mb.y || !mb.plan || (mb.r_pad > 0 && (!mb.A || !mb.B)))
+    return fail(SSL_ERR_INVALID, "linear %d: null pointer", i);
+  if (mb.ldy < mb.NB * block_p || !aligned(mb.y, 16) || (mb.ldy * eb) % 16)
+    return fail(SSL_ERR_INVALID, "linear %d: y rows must be 16-byte aligned and NB·p wide", i);
+  if ((mb.A && !aligned(mb.A, 16)) || (mb.B && !aligned(mb.B, 16)) ||
+      (mb.values && !aligned(mb.values, 16)))
+    return fail(SSL_ERR_INVALID, "linear %d: A, B and values must be 16-byte aligned", i);
+  *L = slr_layout(M, mb.NB, block_p, mb.r_pad, m_pad, mb.n_slots, dtype);
+  if (L->total > 0x7fffffffLL)
+    return fail(SSL_ERR_UNSUPPORTED,
+                "linear %d: workspace of %lld bytes exceeds 2 GiB; split the call by tokens", i,
+                (long long)L->total);
+  if (mb.workspace_bytes < L->total || !mb.workspace)
+    return fail(SSL_ERR_WORKSPACE, "linear %d: workspace of %lld bytes needed", i,
+                (long long)L->total);
+  if (!aligned(mb.workspace, 256))
+    return fail(SSL_ERR_WORKSPACE, "linear %d: workspace must be 256-byte aligned", i);
+  if (mb.n_counters < L->cnt_total || !mb.counters)
+    return fail(SSL_ERR_WORKSPACE, "linear %d: %lld zeroed counters needed", i,
+                (long long)L->cnt_total);
+  if (mb.exchange_bytes < 8 * L->n_sync || !mb.exchange)
+    return fail(SSL_ERR_WORKSPACE, "linear %d: exchange area of %lld bytes needed", i,
+                (long long)(8 * L->n_sync));
+  if (!aligned(mb.exchange, 256))
+    return fail(SSL_ERR_WORKSPACE, "linear %d: exchange area must be 256-byte aligned", i);
+  return SSL_OK;
+}
+
+// The streaming kernel's arguments for one member (a latent split of n_kc
+// chunks of ku_chunk units).
+void fill_args(SlrArgs& a, const ssl_slr_member& mb, const Layout& L, const void* x, int64_t ldx,
+               int64_t M, int64_t m, int64_t m_pad, int n_kc, int ku_chunk, int dtype,
+               int block_p, int block_q, int s_format) {
+  const DebugKnobs& knobs = debug_knobs();
+  char* ws = (char*)mb.workspace;
+  a.x = x; a.ldx = ldx; a.M = (int)M; a.m = (int)m;
+  a.y = mb.y; a.ldy = mb.ldy; a.col = mb.col; a.values = mb.values; a.plan = mb.plan;
+  a.n_chunks = (int)mb.n_chunks; a.NB = (int)mb.NB;
+  a.A = mb.A; a.lda = mb.r_pad; a.bias = mb.bias;
+  a.n_slots = mb.n_slots; a.part_main = (float*)(ws + L.part_main); a.cnt_main = mb.counters;
+  a.B = mb.B; a.ldb = m_pad; a.t = ws + L.t_final; a.ldt = mb.r_pad;
+  a.t_part = (float*)(ws + L.t_part);
+  a.MG = L.MG; a.n_rt = L.n_rt; a.n_kc = n_kc; a.ku_total = L.ku_total;
+  a.ku_chunk = ku_chunk;
+  a.n_lat_wgs = (int)((int64_t)L.n_rt * n_kc * L.MG);
+  a.sync = (u64*)mb.exchange; a.lr_wgs = (int)mb.lr_wgs; a.lat_weight = kLatentUnits / n_kc;
+  a.status = mb.status ? (u64*)mb.status : (u64*)mb.exchange;
+  set_block_shape(a, dtype, block_p, block_q, s_format);
+  a.wait_polls = knobs.wait_polls > 0 ? (int)knobs.wait_polls : kSpinLimit;
+  // out of reach of any launch: tickets and counters advance far less per launch
+  a.wait_bias = knobs.wait_unreachable ? (1 << 30) : 0;
+  a.dep = nullptr; a.dep_need = 0; a.dep_waiters = 0; a.done = nullptr; a.done_copies = 0;
+}
+
 }  // namespace
 }  // namespace ssl
 
@@ -325,47 +400,8 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
     return fail(SSL_ERR_UNSUPPORTED, "2:4 blocks are 32x32 with 16-bit activations");
   for (int i = 0; i < n_members; ++i) {
     const ssl_slr_member& mb = members[i];
-    if (mb.NB < 0 || mb.r_pad < 0 || mb.n_chunks < 0 || mb.n_slots < 0 || mb.lr_wgs < 0)
-      return fail(SSL_ERR_INVALID, "linear %d: negative size", i);
-    if (mb.s_format != s_format)
-      return fail(SSL_ERR_INVALID, "linear %d: all linears of a call share the sparse storage", i);
-    if (mb.r_pad % 64) return fail(SSL_ERR_INVALID, "linear %d: r_pad must be a multiple of 64", i);
-    if (mb.nnz < 0 || !slab_count_ok(mb.nnz, block_q / (4 * stream_ke(dtype, block_q))))
-      return fail(SSL_ERR_UNSUPPORTED, "linear %d: too many blocks (%lld) for one call", i,
-                  (long long)mb.nnz);
-    if (mb.NB == 0) {  // no output columns: nothing to launch for this linear
-      L[i] = slr_layout(M, 0, block_p, 0, m_pad, 0, dtype);
-      continue;
-    }
-    if (mb.n_chunks == 0)
-      return fail(SSL_ERR_INVALID, "linear %d: empty plan for a non-empty output", i);
-    if ((mb.r_pad > 0) != (mb.lr_wgs > 0) || mb.lr_wgs > mb.n_chunks)
-      return fail(SSL_ERR_INVALID, "linear %d: lr_wgs must count the plan's chunks with low-rank units", i);
-    if (!mb.y || !mb.plan || (mb.r_pad > 0 && (!mb.A || !mb.B)))
-      return fail(SSL_ERR_INVALID, "linear %d: null pointer", i);
-    if (mb.ldy < mb.NB * block_p || !aligned(mb.y, 16) || (mb.ldy * eb) % 16)
-      return fail(SSL_ERR_INVALID, "linear %d: y rows must be 16-byte aligned and NB·p wide", i);
-    if ((mb.A && !aligned(mb.A, 16)) || (mb.B && !aligned(mb.B, 16)) ||
-        (mb.values && !aligned(mb.values, 16)))
-      return fail(SSL_ERR_INVALID, "linear %d: A, B and values must be 16-byte aligned", i);
-    L[i] = slr_layout(M, mb.NB, block_p, mb.r_pad, m_pad, mb.n_slots, dtype);
-    if (L[i].total > 0x7fffffffLL)
-      return fail(SSL_ERR_UNSUPPORTED,
-                  "linear %d: workspace of %lld bytes exceeds 2 GiB; split the call by tokens", i,
-                  (long long)L[i].total);
-    if (mb.workspace_bytes < L[i].total || !mb.workspace)
-      return fail(SSL_ERR_WORKSPACE, "linear %d: workspace of %lld bytes needed", i,
-                  (long long)L[i].total);
-    if (!aligned(mb.workspace, 256))
-      return fail(SSL_ERR_WORKSPACE, "linear %d: workspace must be 256-byte aligned", i);
-    if (mb.n_counters < L[i].cnt_total || !mb.counters)
-      return fail(SSL_ERR_WORKSPACE, "linear %d: %lld zeroed counters needed", i,
-                  (long long)L[i].cnt_total);
-    if (mb.exchange_bytes < 8 * L[i].n_sync || !mb.exchange)
-      return fail(SSL_ERR_WORKSPACE, "linear %d: exchange area of %lld bytes needed", i,
-                  (long long)(8 * L[i].n_sync));
-    if (!aligned(mb.exchange, 256))
-      return fail(SSL_ERR_WORKSPACE, "linear %d: exchange area must be 256-byte aligned", i);
+    const int rc = check_member(i, mb, M, m_pad, block_p, block_q, dtype, s_format, &L[i]);
+    if (rc != SSL_OK) return rc;
     n_stream += (mb.NB > 0 ? mb.n_chunks : 0) * L[i].MG;
     rt_tiles += (int64_t)L[i].n_rt * L[i].MG;
   }
@@ -443,7 +479,6 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
                      "slr prefill launch");
   }
 
-  const DebugKnobs& knobs = debug_knobs();
   // One K split for the whole launch: latent and row workgroups of every
   // member resident at once.
   int n_kc = 1, ku_chunk = 1;
@@ -456,24 +491,8 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
     lat += (int64_t)L[i].n_rt * n_kc * L[i].MG;
     str += (mb.NB > 0 ? mb.n_chunks : 0) * L[i].MG;
     if (lat + str > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
-    char* ws = (char*)mb.workspace;
-    SlrArgs& a = g.m[i];
-    a.x = x; a.ldx = ldx; a.M = (int)M; a.m = (int)m;
-    a.y = mb.y; a.ldy = mb.ldy; a.col = mb.col; a.values = mb.values; a.plan = mb.plan;
-    a.n_chunks = (int)mb.n_chunks; a.NB = (int)mb.NB;
-    a.A = mb.A; a.lda = mb.r_pad; a.bias = mb.bias;
-    a.n_slots = mb.n_slots; a.part_main = (float*)(ws + L[i].part_main); a.cnt_main = mb.counters;
-    a.B = mb.B; a.ldb = m_pad; a.t = ws + L[i].t_final; a.ldt = mb.r_pad;
-    a.t_part = (float*)(ws + L[i].t_part);
-    a.MG = L[i].MG; a.n_rt = L[i].n_rt; a.n_kc = n_kc; a.ku_total = L[i].ku_total;
-    a.ku_chunk = ku_chunk;
-    a.n_lat_wgs = (int)((int64_t)L[i].n_rt * n_kc * L[i].MG);
-    a.sync = (u64*)mb.exchange; a.lr_wgs = (int)mb.lr_wgs; a.lat_weight = kLatentUnits / n_kc;
-    a.status = mb.status ? (u64*)mb.status : (u64*)mb.exchange;
-    set_block_shape(a, dtype, block_p, block_q, s_format);
-    a.wait_polls = knobs.wait_polls > 0 ? (int)knobs.wait_polls : kSpinLimit;
-    // out of reach of any launch: tickets and counters advance far less per launch
-    a.wait_bias = knobs.wait_unreachable ? (1 << 30) : 0;
+    fill_args(g.m[i], mb, L[i], x, ldx, M, m, m_pad, n_kc, ku_chunk, dtype, block_p, block_q,
+              s_format);
   }
   g.lat_off[n_members] = (int)lat;
   g.str_off[n_members] = (int)str;
@@ -500,6 +519,149 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
   mb.exchange = exchange; mb.exchange_bytes = exchange_bytes;
   mb.workspace = workspace; mb.workspace_bytes = workspace_bytes;
   return ssl_slr_forward_group(x, ldx, M, m, m_pad, block_p, block_q, dtype, &mb, 1, stream);
+}
+
+int64_t ssl_slr_chain_sync_count(int64_t M) {
+  if (M <= 0) return 0;
+  const int MT = tile_mt(M);
+  return (int64_t)kDepCopies * kDepSlotInts * ((M + 16 * MT - 1) / (16 * MT));
+}
+
+int ssl_slr_forward_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,
+                          const ssl_slr_stage* stages, int32_t n_stages,
+                          const ssl_slr_member* members, int32_t n_members, void* stream) {
+  clear_error();
+  if (dtype != SSL_BF16 && dtype != SSL_F16)
+    return fail(SSL_ERR_UNSUPPORTED, "chained launches take bf16 or fp16 activations");
+  if (n_stages < 1 || n_stages > SSL_MAX_CHAIN_STAGES || !stages)
+    return fail(SSL_ERR_INVALID, "a chained launch takes 1 to %d stages, got %d",
+                SSL_MAX_CHAIN_STAGES, n_stages);
+  if (n_members < 1 || n_members > kMaxChain || !members)
+    return fail(SSL_ERR_INVALID, "a chained launch takes 1 to %d linears, got %d", kMaxChain,
+                n_members);
+  const int s_format = members[0].s_format;
+  if (s_format == SSL_S_NM24) {
+    if (block_p != kNmBlock || block_q != kNmBlock)
+      return fail(SSL_ERR_UNSUPPORTED, "2:4 blocks are 32x32");
+  } else if (s_format != SSL_S_BSR) {
+    return fail(SSL_ERR_INVALID, "unknown sparse storage format %d", s_format);
+  } else if (block_p != block_q || (block_p != 16 && block_p != 32 && block_p != 64)) {
+    return fail(SSL_ERR_UNSUPPORTED, "chained launches take square blocks of 16, 32 or 64, got %dx%d",
+                block_p, block_q);
+  }
+  if (M < 0) return fail(SSL_ERR_INVALID, "negative size");
+  if (M == 0) return SSL_OK;
+  const int eb = elem_bytes(dtype);
+  const int64_t n_sync = ssl_slr_chain_sync_count(M);
+
+  // stages: contiguous member ranges in order; each later stage reads the
+  // output of one member of an earlier stage, and a member feeds at most one
+  int fed[kMaxChain] = {};
+  int next = 0;
+  for (int s = 0; s < n_stages; ++s) {
+    const ssl_slr_stage& st = stages[s];
+    if (st.first != next || st.count < 1 || st.first + st.count > n_members)
+      return fail(SSL_ERR_INVALID, "stage %d: its members must follow the previous stage's", s);
+    next = st.first + st.count;
+    if (st.m < 1 || st.m_pad % 64 || st.m_pad < st.m)
+      return fail(SSL_ERR_INVALID, "stage %d: m >= 1 and m_pad a multiple of 64 and >= m", s);
+    if (s == 0) {
+      if (st.src != -1) return fail(SSL_ERR_INVALID, "stage 0 reads the launch's input (src -1)");
+      if (!st.x || !aligned(st.x, 16) || st.ldx < st.m || (st.ldx * eb) % 16)
+        return fail(SSL_ERR_INVALID, "x rows must be 16-byte aligned and at least m wide");
+      continue;
+    }
+    if (st.src < 0 || st.src >= st.first)
+      return fail(SSL_ERR_INVALID, "stage %d: src must be a member of an earlier stage", s);
+    const ssl_slr_member& src = members[st.src];
+    if (fed[st.src]++) return fail(SSL_ERR_INVALID, "stage %d: member %d already feeds a stage", s, st.src);
+    if (src.NB * block_p < st.m)
+      return fail(SSL_ERR_INVALID, "stage %d: in_features %lld exceed member %d's %lld outputs", s,
+                  (long long)st.m, st.src, (long long)(src.NB * block_p));
+    if (st.x && st.x != src.y)
+      return fail(SSL_ERR_INVALID, "stage %d: x must be NULL (member %d's output)", s, st.src);
+    if (!st.sync || st.n_sync < n_sync || !aligned(st.sync, 256))
+      return fail(SSL_ERR_WORKSPACE, "stage %d: %lld zeroed sync words needed", s,
+                  (long long)n_sync);
+    if (M * src.ldy * eb > 0x7fffffffLL)
+      return fail(SSL_ERR_UNSUPPORTED, "stage %d: its input is beyond 2 GiB; split the call by tokens", s);
+  }
+  if (next != n_members) return fail(SSL_ERR_INVALID, "every member belongs to one stage");
+
+  ChainArgs c{};
+  Layout L[kMaxChain];
+  int64_t wg = 0;
+  int nseg = 0;
+  int MT = tile_mt(M);
+  for (int s = 0; s < n_stages; ++s) {
+    const ssl_slr_stage& st = stages[s];
+    const void* x = s == 0 ? st.x : members[st.src].y;
+    const int64_t ldx = s == 0 ? st.ldx : members[st.src].ldy;
+    int64_t n_stream = 0, rt_tiles = 0, rows = 0;
+    for (int i = st.first; i < st.first + st.count; ++i) {
+      const ssl_slr_member& mb = members[i];
+      const int rc = check_member(i, mb, M, st.m_pad, block_p, block_q, dtype, s_format, &L[i]);
+      if (rc != SSL_OK) return rc;
+      n_stream += (mb.NB > 0 ? mb.n_chunks : 0) * L[i].MG;
+      rt_tiles += (int64_t)L[i].n_rt * L[i].MG;
+      rows += mb.NB;
+    }
+    if (s_format == SSL_S_NM24 ? ssl_nm24_takes_prefill(M, rows, dtype)
+                               : ssl_slr_takes_prefill(M, rows, block_p, block_q, dtype))
+      return fail(SSL_ERR_UNSUPPORTED,
+                  "stage %d: a call of %lld token rows runs the prefill kernels; launch the "
+                  "stages one by one", s, (long long)M);
+    // Stage 0: the K split a grouped launch of its members would take (its
+    // results equal ssl_slr_forward_group's bit for bit). Later stages: one K
+    // chunk, so a latent tile is final without an exchange of partials (its
+    // B loads go out before the stage's input is ready, and the partial
+    // exchange would be one more hop after it): measured 4-5% per step at 1
+    // and 4 token rows, none at 16.
+    int n_kc = 1, ku_chunk = L[st.first].ku_total;
+    if (s == 0) latent_chunks(L[st.first], n_stream, rt_tiles, &n_kc, &ku_chunk);
+    // waiters of one token tile: every latent workgroup, then every row
+    // workgroup of the stage's members, numbered in that order
+    int waiters = 0;
+    for (int i = st.first; i < st.first + st.count; ++i) {
+      SlrArgs& a = c.m[i];
+      fill_args(a, members[i], L[i], x, ldx, M, st.m, st.m_pad, n_kc, ku_chunk, dtype, block_p,
+                block_q, s_format);
+      c.seg_start[nseg] = (int)wg;
+      c.seg_member[nseg] = i;
+      c.seg_rows[nseg++] = 0;
+      wg += (int64_t)L[i].n_rt * n_kc * L[i].MG;
+      a.dep_lat_base = waiters;
+      waiters += L[i].n_rt * n_kc;
+    }
+    for (int i = st.first; i < st.first + st.count; ++i) {
+      const ssl_slr_member& mb = members[i];
+      c.seg_start[nseg] = (int)wg;
+      c.seg_member[nseg] = i;
+      c.seg_rows[nseg++] = 1;
+      wg += (mb.NB > 0 ? mb.n_chunks : 0) * L[i].MG;
+      c.m[i].dep_row_base = waiters;
+      waiters += mb.NB > 0 ? (int)mb.n_chunks : 0;
+      if (wg > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
+    }
+    if (s > 0 && waiters > 0) {
+      // the stage waits for its source; the source counts its row tiles
+      for (int i = st.first; i < st.first + st.count; ++i) {
+        c.m[i].dep = st.sync;
+        c.m[i].dep_need = (int)members[st.src].NB;
+        c.m[i].dep_waiters = waiters;
+      }
+      c.m[st.src].done = st.sync;
+      c.m[st.src].done_copies = waiters < kDepCopies ? waiters : kDepCopies;
+    }
+  }
+  c.n_seg = nseg;
+  c.seg_start[nseg] = (int)wg;
+  if (wg == 0) return SSL_OK;
+  const int sf = s_format == SSL_S_NM24 ? SF_NM24 : SF_BSR;
+  hipError_t e = dtype == SSL_BF16
+                     ? chain_launch<DT_BF16>(sf, block_p, MT, c, wg, (hipStream_t)stream)
+                     : chain_launch<DT_F16>(sf, block_p, MT, c, wg, (hipStream_t)stream);
+  return check_hip(e, "slr chained launch");
 }
 
 }  // extern "C"

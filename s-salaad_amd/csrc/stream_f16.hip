@@ -11,4 +11,10 @@ hipError_t stream_launch<DT_F16>(int mode, int sf, int P, int KE, int MT, const 
   return stream_dispatch<DT_F16>(mode, sf, P, KE, MT, a, blocks, s);
 }
 
+template <>
+hipError_t chain_launch<DT_F16>(int sf, int P, int MT, const ChainArgs& a, int64_t blocks,
+                             hipStream_t s) {
+  return chain_dispatch<DT_F16>(sf, P, MT, a, blocks, s);
+}
+
 }  // namespace ssl

@@ -153,12 +153,12 @@ __device__ __forceinline__ void st_u64(u64* p, u64 v) {
 // timeout. The caller goes on either way, so every workgroup of the launch
 // still ends; a wait that gave up leaves its tile unreliable, which the status
 // word reports.
-template <typename T>
+template <typename T, int SLEEP = 2>
 __device__ __forceinline__ void wait_at_least(const T* flag, T target, u64* status, int polls) {
   int n = 0;
   while (__hip_atomic_load(const_cast<T*>(flag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
          target) {
-    __builtin_amdgcn_s_sleep(2);
+    __builtin_amdgcn_s_sleep(SLEEP);
     if (++n > polls) {
       st_u64(status, 1);
       break;
@@ -176,6 +176,72 @@ __device__ __forceinline__ typename Mma<DT, KE>::Frag ld_dev_frag(__amdgpu_buffe
   static_assert(sizeof(f) == 16, "fragment image");
   __builtin_memcpy(&f, &u, 16);
   return f;
+}
+
+// One KE-element fragment of x read device-coherently: in a chained launch x
+// is a row tile that another workgroup of the same launch wrote. `valid`
+// (0..KE) elements are read, the rest are zero.
+template <int DT, int KE>
+__device__ __forceinline__ typename Mma<DT, KE>::Frag ld_dev_kfrag(__amdgpu_buffer_rsrc_t r,
+                                                                   int byte_off, int valid) {
+  using F = typename Mma<DT, KE>::Frag;
+  constexpr int EB = Elem<DT>::bytes;
+  static_assert(sizeof(F) == KE * EB, "fragment image");
+  F f;
+  if (valid >= KE) {
+    if constexpr (KE * EB == 16) {
+      const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kSc1);
+      __builtin_memcpy(&f, &u, 16);
+    } else {
+      static_assert(KE * EB == 8, "8- or 16-byte fragments");
+      const auto u = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, kSc1);
+      __builtin_memcpy(&f, &u, 8);
+    }
+  } else if constexpr (DT == DT_F32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      f.f[e] = e < valid ? __uint_as_float(
+                               __builtin_amdgcn_raw_buffer_load_b32(r, byte_off + 4 * e, 0, kSc1))
+                         : 0.f;
+  } else {
+#pragma unroll
+    for (int d = 0; d < KE / 2; ++d) {
+      const uint32_t lo =
+          2 * d < valid ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, byte_off + 4 * d, 0, kSc1)
+                        : 0u;
+      const uint32_t hi = 2 * d + 1 < valid ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+                                                  r, byte_off + 4 * d + 2, 0, kSc1)
+                                            : 0u;
+      f.d[d] = lo | (hi << 16);
+    }
+  }
+  return f;
+}
+
+// W adjacent output elements stored device-coherently (a chained stage's
+// output, read by a later stage of the same launch).
+template <int DT, int W>
+__device__ __forceinline__ void st_w_dev(__amdgpu_buffer_rsrc_t r, int byte_off,
+                                         const float (&v)[W]) {
+  if constexpr (DT == DT_F32) {
+    st_dev_vec<W>(r, byte_off, v);
+  } else if constexpr (W == 1 || W == 3) {
+#pragma unroll
+    for (int i = 0; i < W; ++i)
+      __builtin_amdgcn_raw_buffer_store_b16((unsigned short)to_bits<DT>(v[i]), r, byte_off + 2 * i,
+                                            0, kSc1);
+  } else {
+    uint32_t w[W / 2];
+#pragma unroll
+    for (int i = 0; i < W / 2; ++i) w[i] = to_bits<DT>(v[2 * i]) | (to_bits<DT>(v[2 * i + 1]) << 16);
+    if constexpr (W == 4) {
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      const u32x2 u = {w[0], w[1]};
+      __builtin_amdgcn_raw_buffer_store_b64(u, r, byte_off, 0, kSc1);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b32(w[0], r, byte_off, 0, kSc1);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -314,7 +380,54 @@ struct SlrArgs {
   u64* status;
   int wait_polls;
   int wait_bias;
+  // Chained launches (slr_chain_kernel), where x is the output of a member of
+  // an earlier stage of the same launch. dep: that stage's words (below), zero
+  // at rest, or null when x is an input of the launch; dep_need: the source's
+  // row tiles per token tile (its NB); dep_waiters: workgroups of this stage
+  // per token tile. done: the words this member's finished row tiles are
+  // counted in (the dependent stage's dep), or null; a member with `done`
+  // stores its output device-coherently.
+  int* dep;
+  int dep_need;
+  int dep_waiters;
+  int dep_lat_base;  // this member's first latent / row workgroup among the
+  int dep_row_base;  // stage's waiters of one token tile
+  int* done;
+  int done_copies;   // copies of `done` that have waiters (min(kDepCopies, its stage's waiters))
 };
+
+// A stage's words, per token tile: kDepCopies copies of [finished row tiles of
+// the source | waiters passed], each copy in its own 512-byte slot (the finished
+// count at +0, the passed count at +256 bytes). A word that hundreds of
+// workgroups poll serialises their accesses (and the increments they wait for)
+// at one memory location: measured 5-8 µs per hand-over with one copy for
+// every stage. The source's row tiles add 1 to every copy; waiter w polls copy
+// w % kDepCopies (copies no waiter polls are left alone, so every copy nets
+// to zero in each launch).
+constexpr int kDepCopies = 16;
+constexpr int kDepSlotInts = 128;
+constexpr int kDepPassedInts = 64;
+constexpr int kDepSleep = 2;  // s_sleep between polls of a stage's input count
+
+// Chained stages: wait until the source member has finished every row tile of
+// token tile mg in this launch (one thread polls, the barrier releases the
+// workgroup); w is the workgroup's index among the stage's waiters of that
+// tile. The last waiter of a copy returns both of its words to zero by
+// subtracting what the launch adds to them, so they are zero at rest whatever
+// the order of arrivals, a wait that gave up included.
+__device__ __forceinline__ void wait_dep(const SlrArgs& a, int mg, int w) {
+  if (threadIdx.x == 0) {
+    const int c = w % kDepCopies;
+    const int n_c = a.dep_waiters / kDepCopies + (c < a.dep_waiters % kDepCopies ? 1 : 0);
+    int* word = a.dep + ((int64_t)mg * kDepCopies + c) * kDepSlotInts;
+    wait_at_least<int, kDepSleep>(word, a.dep_need + a.wait_bias, a.status, a.wait_polls);
+    if (rmw_add(word + kDepPassedInts, 1) == n_c - 1) {
+      rmw_add(word, -a.dep_need);
+      rmw_add(word + kDepPassedInts, -n_c);
+    }
+  }
+  __syncthreads();
+}
 
 __device__ __forceinline__ u64* tile_sync(const SlrArgs& a, int mg) {
   return a.sync + 1 + (int64_t)mg * (2 + a.n_rt);
@@ -323,7 +436,11 @@ __device__ __forceinline__ u64* tile_sync(const SlrArgs& a, int mg) {
 // ---------------------------------------------------------------------------
 // Latent workgroup: t[token tile, 16-rank tile rt] over all of in_features.
 // ---------------------------------------------------------------------------
-template <int DT, int MT>
+// CH (chained launches): 0 = an ordinary launch; 1 = a chained member whose x
+// is an input of the launch; 2 = a chained member whose x another stage of the
+// launch writes: its B loads go out before it waits for x, and x is read
+// device-coherently.
+template <int DT, int MT, int CH = 0>
 __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) {
   constexpr int KE = (DT == DT_F32) ? 4 : 8;
   using MM = Mma<DT, KE>;
@@ -341,34 +458,69 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
   const int64_t brow = (int64_t)(rt * 16 + c) * a.ldb;
   const int ub = kc * a.ku_chunk, ue = min(ub + a.ku_chunk, a.ku_total);
 
+  constexpr int EB = Elem<DT>::bytes;
   f32x4 acc[MT][1];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int u0 = ub + wid; u0 < ue; u0 += kSW * UNR) {
+  const auto xr = dev_rsrc(a.x);
+  // x fragments of K unit u for every token row tile
+  auto load_x = [&](int u, Frag(&xk)[MT]) {
+    const int kcol = u * KM + KE * g;
+    if (u * KM + KM <= a.m) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int64_t off = (int64_t)(m0 + min(mt * 16 + c, Mrem - 1)) * a.ldx + kcol;
+        if constexpr (CH == 2) xk[mt] = ld_dev_kfrag<DT, KE>(xr, (int)(off * EB), KE);
+        else xk[mt] = load_kfrag_full<DT, KE>(a.x, off);
+      }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int rr = mt * 16 + c;
+        const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
+        const int64_t off = (int64_t)(m0 + rr) * a.ldx + kcol;
+        if constexpr (CH == 2)
+          xk[mt] = (valid > 0) ? ld_dev_kfrag<DT, KE>(xr, (int)(off * EB), valid)
+                               : zero_frag<DT, KE>();
+        else
+          xk[mt] = (valid > 0) ? load_kfrag<DT, KE>(a.x, off, valid) : zero_frag<DT, KE>();
+      }
+    }
+  };
+
+  int u0 = ub + wid;
+  if constexpr (CH == 2) {
+    // B does not depend on x: the first batch's B loads go out before the wait.
+    Frag xf[UNR][MT];
+    Frag bf[UNR];
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int u = u0 + k * kSW;
+      if (u < ue) bf[k] = load_kfrag_full<DT, KE>(a.B, brow + u * KM + KE * g);
+    }
+    wait_dep(a, mg, a.dep_lat_base + wg % per_mg);
+#pragma unroll
+    for (int k = 0; k < UNR; ++k)
+      if (u0 + k * kSW < ue) load_x(u0 + k * kSW, xf[k]);
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      if (u0 + k * kSW < ue) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][0], xf[k][mt], bf[k]);
+      }
+    }
+    u0 += kSW * UNR;
+  }
+  for (; u0 < ue; u0 += kSW * UNR) {
     Frag xf[UNR][MT];
     Frag bf[UNR];
 #pragma unroll
     for (int k = 0; k < UNR; ++k) {
       const int u = u0 + k * kSW;
       if (u < ue) {
-        const int kcol = u * KM + KE * g;
-        if (u * KM + KM <= a.m) {
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            xf[k][mt] = load_kfrag_full<DT, KE>(
-                a.x, (int64_t)(m0 + min(mt * 16 + c, Mrem - 1)) * a.ldx + kcol);
-        } else {
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const int rr = mt * 16 + c;
-            const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
-            xf[k][mt] = (valid > 0)
-                            ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol, valid)
-                            : zero_frag<DT, KE>();
-          }
-        }
-        bf[k] = load_kfrag_full<DT, KE>(a.B, brow + kcol);
+        load_x(u, xf[k]);
+        bf[k] = load_kfrag_full<DT, KE>(a.B, brow + u * KM + KE * g);
       }
     }
 #pragma unroll
@@ -423,7 +575,6 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
   // Final latent tile, rounded once to the activation dtype as F.linear's
   // output is. Rows past M hold zeros (their x rows were read as zero).
   const auto tr = dev_rsrc(a.t);
-  constexpr int EB = Elem<DT>::bytes;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -449,7 +600,9 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
 // KE: k elements per lane of the sparse MFMA fragments (8 when q is a multiple
 // of 32 for 16-bit activations, else 4), so one K slab is KM = 4·KE block rows
 // and q (any multiple of KM) is a runtime value.
-template <int DT, int P, int KE, int MT, int MODE, int UNR, int SF>
+// CH: as for latent_wg (chained launches; 2 = x written by an earlier stage:
+// the first batch's weight loads go out before the wait for x).
+template <int DT, int P, int KE, int MT, int MODE, int UNR, int SF, int CH = 0>
 __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f32x4* red) {
   constexpr int W = P / 16;
   using MM = Mma<DT, KE>;
@@ -508,12 +661,9 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   // slab by slab before the first MFMA, so each slab waits only for its own data.
   const int nks = a.nks;
   const int vb = bb * nks, ve = be * nks;
-  for (int v0 = vb + wid; v0 < ve; v0 += kSW * UNR) {
-    Raw raw[UNR];
-    Frag xf[UNR][MT];
-    // the batch's column indices first, as scalar loads issued together
-    int colk[UNR];
-    int64_t voff[UNR];
+  const auto xr = dev_rsrc(a.x);
+  // the batch's column indices first, as scalar loads issued together
+  auto index = [&](int v0, int(&colk)[UNR], int64_t(&voff)[UNR]) {
 #pragma unroll
     for (int k = 0; k < UNR; ++k) {
       const int v = min(v0 + k * kSW, ve - 1);
@@ -522,42 +672,82 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
       colk[k] = ld_uniform(a.col, blk) * a.q + ks * KM;
       voff[k] = (int64_t)blk * a.blk_bytes + ks * a.slab_bytes;
     }
+  };
+  // x fragments of the slab at input column colk for every token row tile
+  auto load_x = [&](int colk, Frag(&xk)[MT]) {
+    const int kcol = colk + KE * g;
+    const bool full = colk + KM <= a.m;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int rr = mt * 16 + c;
+      if (full) {
+        const int64_t off = (int64_t)(m0 + min(rr, Mrem - 1)) * a.ldx + kcol;
+        if constexpr (CH == 2) xk[mt] = ld_dev_kfrag<DT, KE>(xr, (int)(off * EB), KE);
+        else xk[mt] = load_kfrag_full<DT, KE>(a.x, off);
+      } else {
+        const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
+        const int64_t off = (int64_t)(m0 + rr) * a.ldx + kcol;
+        if constexpr (CH == 2)
+          xk[mt] = (valid > 0) ? ld_dev_kfrag<DT, KE>(xr, (int)(off * EB), valid)
+                               : zero_frag<DT, KE>();
+        else
+          xk[mt] = (valid > 0) ? load_kfrag<DT, KE>(a.x, off, valid) : zero_frag<DT, KE>();
+      }
+    }
+  };
+  auto load_w = [&](int64_t voff, Raw& rk) {
+    const char* vb_ = (const char*)a.values + voff;
+    if constexpr (SF == SF_NM24) load_nm(rk, vb_, lane);
+    else load_vstep<DT, KE, W>(rk, vb_, P, 0, lane);
+  };
+  auto mma = [&](const Raw& rk, const Frag(&xk)[MT]) {
+#pragma unroll
+    for (int s = 0; s < W; ++s) {
+      Frag vf;
+      if constexpr (SF == SF_NM24) vf = nm_frag<DT>(rk, s);
+      else vf = vfrag<DT, KE, W>(rk, s);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][s], xk[mt], vf);
+    }
+  };
+
+  int v0 = vb + wid;
+  if constexpr (CH == 2) {
+    // The weights do not depend on x: the first batch's block loads go out
+    // before the wait for the stage's input.
+    Raw raw[UNR];
+    Frag xf[UNR][MT];
+    int colk[UNR];
+    int64_t voff[UNR];
+    if (v0 < ve) index(v0, colk, voff);
+#pragma unroll
+    for (int k = 0; k < UNR; ++k)
+      if (v0 + k * kSW < ve) load_w(voff[k], raw[k]);
+    wait_dep(a, mg, a.dep_row_base + chunk);
+#pragma unroll
+    for (int k = 0; k < UNR; ++k)
+      if (v0 + k * kSW < ve) load_x(colk[k], xf[k]);
+#pragma unroll
+    for (int k = 0; k < UNR; ++k)
+      if (v0 + k * kSW < ve) mma(raw[k], xf[k]);
+    v0 += kSW * UNR;
+  }
+  for (; v0 < ve; v0 += kSW * UNR) {
+    Raw raw[UNR];
+    Frag xf[UNR][MT];
+    int colk[UNR];
+    int64_t voff[UNR];
+    index(v0, colk, voff);
 #pragma unroll
     for (int k = 0; k < UNR; ++k) {
       if (v0 + k * kSW < ve) {
-        const char* vb_ = (const char*)a.values + voff[k];
-        const int kcol = colk[k] + KE * g;
-        const bool full = colk[k] + KM <= a.m;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int rr = mt * 16 + c;
-          if (full) {
-            xf[k][mt] =
-                load_kfrag_full<DT, KE>(a.x, (int64_t)(m0 + min(rr, Mrem - 1)) * a.ldx + kcol);
-          } else {
-            const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
-            xf[k][mt] = (valid > 0) ? load_kfrag<DT, KE>(a.x, (int64_t)(m0 + rr) * a.ldx + kcol,
-                                                         valid)
-                                    : zero_frag<DT, KE>();
-          }
-        }
-        if constexpr (SF == SF_NM24) load_nm(raw[k], vb_, lane);
-        else load_vstep<DT, KE, W>(raw[k], vb_, P, 0, lane);
+        load_x(colk[k], xf[k]);
+        load_w(voff[k], raw[k]);
       }
     }
 #pragma unroll
-    for (int k = 0; k < UNR; ++k) {
-      if (v0 + k * kSW < ve) {
-#pragma unroll
-        for (int s = 0; s < W; ++s) {
-          Frag vf;
-          if constexpr (SF == SF_NM24) vf = nm_frag<DT>(raw[k], s);
-          else vf = vfrag<DT, KE, W>(raw[k], s);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][s], xf[k][mt], vf);
-        }
-      }
-    }
+    for (int k = 0; k < UNR; ++k)
+      if (v0 + k * kSW < ve) mma(raw[k], xf[k]);
   }
 
   // ---- low-rank units: 32 ranks of A per unit, t·Aᵀ. One thread of the
@@ -653,6 +843,9 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   if constexpr (MODE == MODE_FUSED) {
     if (a.bias != nullptr) ld_w<DT, W>(a.bias, j0, bv);
   }
+  // a chained member another stage reads stores device-coherently
+  const bool dev_out = CH > 0 && a.done != nullptr;
+  const auto yr = dev_rsrc(a.y);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -669,9 +862,18 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
 #pragma unroll
           for (int s = 0; s < W; ++s) o[s] += acc[mt][s][e];
         }
-        st_w<DT, W>(a.y, off, o);
+        if (CH > 0 && dev_out) st_w_dev<DT, W>(yr, (int)(off * EB), o);
+        else st_w<DT, W>(a.y, off, o);
       }
     }
+  if constexpr (CH > 0) {
+    // count this row tile as finished once its stores are acknowledged
+    if (dev_out) {
+      wait_mem();
+      if (lane < a.done_copies)
+        rmw_add(a.done + ((int64_t)mg * kDepCopies + lane) * kDepSlotInts, 1);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -716,6 +918,51 @@ __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_ke
   stream_wg<DT, P, KE, MT, MODE, UNR, SF>(a, chunk, mg, red);
 }
 
+// ---------------------------------------------------------------------------
+// Chained launch: the linears of several dependent stages (e.g. a decoder
+// layer's q,k,v -> o -> gate,up -> down projections) in ONE launch. The grid is
+// the stages in order, each [latent workgroups][row workgroups] of its members
+// as in slr_kernel. A stage after the first reads the output of a member of an
+// earlier stage: its workgroups issue their first weight loads, then wait for
+// that member's row tiles of their token tile (SlrArgs::dep), then read x
+// device-coherently. Every wait is on workgroups earlier in the grid, which an
+// XCD dispatches first, so every wait ends; the weight streams of a stage
+// overlap the tail of the stage before it, and the launch pays one kernel
+// boundary instead of one per stage.
+// ---------------------------------------------------------------------------
+constexpr int kMaxChain = 8;  // members of a chained launch
+struct ChainArgs {
+  int n_seg;                         // grid segments, in grid order
+  int seg_start[2 * kMaxChain + 1];  // first workgroup of each segment, then the grid size
+  int seg_member[2 * kMaxChain];     // the member a segment belongs to
+  int seg_rows[2 * kMaxChain];       // 1: its row workgroups, 0: its latent workgroups
+  SlrArgs m[kMaxChain];
+};
+static_assert(sizeof(ChainArgs) <= 4096, "kernel arguments of a chained launch");
+
+template <int DT, int P, int KE, int MT, int UNR, int SF>
+__global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_chain_kernel(
+    ChainArgs c_by_value) {
+  (void)c_by_value;
+  const ChainArgs& g = *(const ChainArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  constexpr int W = P / 16;
+  constexpr int SLOTS = red_slots<MT, W>();
+  __shared__ f32x4 red[SLOTS * MT * W * kWave];
+  const int b = blockIdx.x;
+  int k = 0;
+  while (k + 1 < g.n_seg && b >= g.seg_start[k + 1]) ++k;
+  const SlrArgs& a = g.m[g.seg_member[k]];
+  const int lb = b - g.seg_start[k];
+  if (!g.seg_rows[k]) {
+    if (a.dep) latent_wg<DT, MT, 2>(a, lb, red);
+    else latent_wg<DT, MT, 1>(a, lb, red);
+    return;
+  }
+  const int mg = lb / a.n_chunks, chunk = lb % a.n_chunks;
+  if (a.dep) stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 2>(a, chunk, mg, red);
+  else stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 1>(a, chunk, mg, red);
+}
+
 // Slabs per wave per batch. The byte budget of the square-block kernels
 // (a 32-block row in one batch of the 8 waves for 32×32 and 64×64 blocks,
 // fewer units for wide tiles; 16-bit kernels with P ≤ 32 stay within 128 VGPRs,
@@ -744,6 +991,44 @@ hipError_t stream_launch_one(const GroupArgs& a, int64_t blocks, hipStream_t s) 
   hipLaunchKernelGGL((slr_kernel<DT, P, KE, MT, MODE, UNR, SF>), dim3((unsigned)blocks), dim3(kST),
                      0, s, a);
   return hipGetLastError();
+}
+
+// One chained launch for a 16-bit dtype; defined in stream_{bf16,f16}.hip.
+// Square blocks of 16, 32 or 64 (KE 4, 8, 8) or 2:4 blocks; MT ∈ {1, 2, 4}.
+template <int DT>
+hipError_t chain_launch(int sf, int P, int MT, const ChainArgs& a, int64_t blocks, hipStream_t s);
+
+template <int DT, int P, int KE, int MT, int SF>
+hipError_t chain_launch_one(const ChainArgs& a, int64_t blocks, hipStream_t s) {
+  constexpr int UNR = stream_unroll<DT, P, KE, MT>();
+  hipLaunchKernelGGL((slr_chain_kernel<DT, P, KE, MT, UNR, SF>), dim3((unsigned)blocks), dim3(kST),
+                     0, s, a);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t chain_dispatch(int sf, int P, int MT, const ChainArgs& a, int64_t blocks,
+                          hipStream_t s) {
+  static_assert(DT != DT_F32, "chained launches take 16-bit activations");
+#define SSL_CMT(PP, KK, SS)                                                 \
+  switch (MT) {                                                             \
+    case 1: return chain_launch_one<DT, PP, KK, 1, SS>(a, blocks, s);       \
+    case 2: return chain_launch_one<DT, PP, KK, 2, SS>(a, blocks, s);       \
+    case 4: return chain_launch_one<DT, PP, KK, 4, SS>(a, blocks, s);       \
+  }                                                                         \
+  return hipErrorInvalidValue;
+  if (sf == SF_NM24) {
+    if (P != kNmBlock) return hipErrorInvalidValue;
+    SSL_CMT(kNmBlock, 8, SF_NM24)
+  }
+  if (sf != SF_BSR) return hipErrorInvalidValue;
+  switch (P) {
+    case 16: { SSL_CMT(16, 4, SF_BSR) }
+    case 32: { SSL_CMT(32, 8, SF_BSR) }
+    case 64: { SSL_CMT(64, 8, SF_BSR) }
+  }
+  return hipErrorInvalidValue;
+#undef SSL_CMT
 }
 
 // The instantiation table of one dtype (expanded in its own file).

@@ -4,6 +4,7 @@ Drop-in for the S-SALAAD hot path:
   * torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_  (ssalaad_amd.addmm_inplace)
   * LRSLinear                                              (ssalaad_amd.ls_linear)
   * LRSLinearGroup: linears sharing an input in one launch (ssalaad_amd.ls_linear)
+  * LRSLinearChain: dependent stages of linears in one launch (ssalaad_amd.ls_linear)
   * dense_to_bsr / factor_from_svd                         (ssalaad_amd.artifact)
   * project_S / project_S_nm: the compression loop's sparse steps (ssalaad_amd.project)
   * save_artifact / load_artifact / build_efficient_model: bundles (ssalaad_amd.bundle)
@@ -18,12 +19,13 @@ from .addmm_inplace import SUPPORTED_BLOCK_SIZES, bsr_addmm_inplace_, get_tuned_
 from .artifact import dense_to_bsr, encode_for_kernels, factor_from_svd
 from .bundle import build_efficient_model, load_artifact, save_artifact
 from .decode import DecodeEngine, generate
-from .ls_linear import LRSLinear, LRSLinearGroup
+from .ls_linear import LRSLinear, LRSLinearChain, LRSLinearGroup
 from .project import block_topk, project_S, project_S_nm, project_nm
 
 __all__ = [
     "DecodeEngine",
     "LRSLinear",
+    "LRSLinearChain",
     "LRSLinearGroup",
     "SUPPORTED_BLOCK_SIZES",
     "block_topk",

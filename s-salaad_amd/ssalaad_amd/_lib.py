@@ -157,7 +157,27 @@ _SIGNATURES["ssl_slr_forward_group"] = (
      _c_i32, _c_p],
 )
 
+
+
+class SlrStage(ctypes.Structure):
+    """ssl_slr_stage: one stage of a chained launch."""
+
+    _fields_ = [
+        ("x", _c_p), ("ldx", _c_i64), ("m", _c_i64), ("m_pad", _c_i64), ("first", _c_i32),
+        ("count", _c_i32), ("src", _c_i32), ("sync", _c_p), ("n_sync", _c_i64),
+    ]
+
+
+_SIGNATURES["ssl_slr_chain_sync_count"] = (_c_i64, [_c_i64])
+_SIGNATURES["ssl_slr_forward_chain"] = (
+    ctypes.c_int,
+    [_c_i64, _c_i32, _c_i32, _c_i32, ctypes.POINTER(SlrStage), _c_i32, ctypes.POINTER(SlrMember),
+     _c_i32, _c_p],
+)
+
 MAX_GROUP = 4
+MAX_CHAIN = 8
+MAX_CHAIN_STAGES = 4
 
 _lib = None
 

@@ -204,6 +204,59 @@ class _KernelState:
         return _launch([self], x, [out_features])[0]
 
 
+def _members(states: list["_KernelState"], ys: list[torch.Tensor], M: int, G: int,
+             extra_counters: int = 0):
+    """The C-ABI member descriptors of a fused call of M token rows writing
+    `ys`, with workspaces and zero-at-rest counters from the stream's pools;
+    `extra_counters` more int32 counters follow the members' (their address is
+    returned too)."""
+    lib = _lib.load()
+    dev = ys[0].device
+    plans = [st.plan(M) for st in states]
+    ws_need = [_round_up(lib.ssl_slr_workspace_size(M, st.NB, st.p, st.r_pad, st.m_pad,
+                                                    pl.n_slots, st.dtype_code), 256)
+               for st, pl in zip(states, plans)]
+    cnt_need = [lib.ssl_slr_counter_count(M, st.NB) for st in states]
+    ws = _runtime.workspace(dev, sum(ws_need))
+    cnt = _runtime.counters(dev, sum(cnt_need) + extra_counters)
+    status = _runtime.status_word(dev).data_ptr()
+    members = (_lib.SlrMember * len(states))()
+    ws_off = cnt_off = 0
+    for i, (st, pl, y) in enumerate(zip(states, plans, ys)):
+        xch = pl.exchange(lib.ssl_slr_exchange_size(M, st.r_pad, st.m_pad, st.dtype_code))
+        mb = members[i]
+        mb.y, mb.ldy = y.data_ptr(), y.stride(0)
+        mb.A, mb.B, mb.bias = st.A.data_ptr(), st.B.data_ptr(), _lib.ptr(st.bias)
+        mb.col, mb.values = st.col.data_ptr(), st.values.data_ptr()
+        mb.plan, mb.n_chunks, mb.n_slots = pl.table.data_ptr(), pl.n_chunks, pl.n_slots
+        mb.lr_wgs, mb.NB, mb.r_pad = pl.lr_wgs, st.NB, st.r_pad
+        mb.counters = cnt.data_ptr() + 4 * cnt_off
+        mb.n_counters = cnt_need[i]
+        mb.exchange, mb.exchange_bytes = xch.data_ptr(), xch.numel()
+        mb.workspace = ws.data_ptr() + ws_off
+        mb.workspace_bytes = ws_need[i]
+        mb.nnz = st.nblk_total
+        mb.s_format = st.s_format
+        mb.status = status
+        if G:
+            pp = st.prefill_plan(G)
+            mb.pf_groups, mb.pf_steps = pp.groups.data_ptr(), pp.steps.data_ptr()
+            mb.pf_n_groups, mb.pf_group = pp.n_groups, pp.group
+            mb.values_pq = _lib.ptr(st._values_pq)
+        ws_off += ws_need[i]
+        cnt_off += cnt_need[i]
+    return members, cnt.data_ptr() + 4 * cnt_off
+
+
+def _outputs(states, ys, out_features, lead: tuple) -> list[torch.Tensor]:
+    outs = []
+    for st, y, n in zip(states, ys, out_features):
+        if st.n_pad != n:
+            y = y[:, :n]
+        outs.append(y.reshape(*lead, n))
+    return outs
+
+
 def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[int]):
     """One fused launch computing every state's linear of the same x."""
     st0 = states[0]
@@ -213,53 +266,16 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
     ys = [torch.empty(M, st.n_pad, dtype=x.dtype, device=x.device) for st in states]
     if M > 0:
         lib = _lib.load()
-        plans = [st.plan(M) for st in states]
-        ws_need = [_round_up(lib.ssl_slr_workspace_size(M, st.NB, st.p, st.r_pad, st.m_pad,
-                                                        pl.n_slots, st.dtype_code), 256)
-                   for st, pl in zip(states, plans)]
-        cnt_need = [lib.ssl_slr_counter_count(M, st.NB) for st in states]
-        ws = _runtime.workspace(x.device, sum(ws_need))
-        cnt = _runtime.counters(x.device, sum(cnt_need))
-        status = _runtime.status_word(x.device).data_ptr()
-        members = (_lib.SlrMember * len(states))()
-        ws_off = cnt_off = 0
         G = 0
         if st0.takes_prefill(M, sum(st.NB for st in states)):
             G = int(lib.ssl_prefill_group(M, sum(st.NB for st in states), st0.p, st0.q))
-        for i, (st, pl, y) in enumerate(zip(states, plans, ys)):
-            xch = pl.exchange(lib.ssl_slr_exchange_size(M, st.r_pad, st.m_pad, st.dtype_code))
-            mb = members[i]
-            mb.y, mb.ldy = y.data_ptr(), y.stride(0)
-            mb.A, mb.B, mb.bias = st.A.data_ptr(), st.B.data_ptr(), _lib.ptr(st.bias)
-            mb.col, mb.values = st.col.data_ptr(), st.values.data_ptr()
-            mb.plan, mb.n_chunks, mb.n_slots = pl.table.data_ptr(), pl.n_chunks, pl.n_slots
-            mb.lr_wgs, mb.NB, mb.r_pad = pl.lr_wgs, st.NB, st.r_pad
-            mb.counters = cnt.data_ptr() + 4 * cnt_off
-            mb.n_counters = cnt_need[i]
-            mb.exchange, mb.exchange_bytes = xch.data_ptr(), xch.numel()
-            mb.workspace = ws.data_ptr() + ws_off
-            mb.workspace_bytes = ws_need[i]
-            mb.nnz = st.nblk_total
-            mb.s_format = st.s_format
-            mb.status = status
-            if G:
-                pp = st.prefill_plan(G)
-                mb.pf_groups, mb.pf_steps = pp.groups.data_ptr(), pp.steps.data_ptr()
-                mb.pf_n_groups, mb.pf_group = pp.n_groups, pp.group
-                mb.values_pq = _lib.ptr(st._values_pq)
-            ws_off += ws_need[i]
-            cnt_off += cnt_need[i]
+        members, _ = _members(states, ys, M, G)
         rc = lib.ssl_slr_forward_group(
             x2.data_ptr(), x2.stride(0), M, st0.m, st0.m_pad, st0.p, st0.q, st0.dtype_code,
             members, len(states), _lib.stream_ptr(x.device),
         )
         _lib.check(rc, "ssl_slr_forward_group")
-    outs = []
-    for st, y, n in zip(states, ys, out_features):
-        if st.n_pad != n:
-            y = y[:, :n]
-        outs.append(y.reshape(*orig[:-1], n))
-    return outs
+    return _outputs(states, ys, out_features, orig[:-1])
 
 
 def latent_wait_status(device: torch.device) -> int:
@@ -540,3 +556,115 @@ class LRSLinearGroup(nn.Module):
             raise ValueError(f"input on {x.device}, weights on {first.A.device}")
         states = [mod._kernel() for mod in self.members]
         return tuple(_launch(states, x, [mod.out_features for mod in self.members]))
+
+
+class LRSLinearChain(nn.Module):
+    """Dependent stages of SLR linears computed in ONE launch at decode sizes.
+
+    `LRSLinearChain([[q, k, v], [o], [gate, up], [down]], sources=[q, o, gate])`
+    computes stage 0's members of the input x, then every later stage's
+    members of the output of its source (a member of an earlier stage), and
+    returns every member's output, stage by stage:
+    `((q(x), k(x), v(x)), (o(q(x)),), (gate(o(..)), up(o(..))), (down(gate(..)),))`.
+    Each output is what the module computes for that input (same plans and
+    rounding points); stage 0's equal the grouped launch's bit for bit, later
+    stages sum the latent t = x·Bᵀ over in_features in another fp32 order.
+
+    Calls the streaming kernel serves (decode sizes, 16-bit activations, square
+    16/32/64 or 2:4 blocks) run as one chained launch (ssl_slr_forward_chain):
+    a stage's workgroups load their weights while the stage before it
+    finishes, and wait for its output inside the launch instead of at a kernel
+    boundary. Other calls run the stages as grouped launches one after another.
+    The reference calls every module on its own (ssalaad/efficient/model.py:41-57).
+    """
+
+    def __init__(self, stages, sources) -> None:
+        super().__init__()
+        stages = [list(st) for st in stages]
+        sources = list(sources)
+        if not 1 <= len(stages) <= _lib.MAX_CHAIN_STAGES:
+            raise ValueError(f"a chain takes 1 to {_lib.MAX_CHAIN_STAGES} stages, got {len(stages)}")
+        if len(sources) != len(stages) - 1:
+            raise ValueError("every stage after the first needs one source module")
+        n = sum(len(st) for st in stages)
+        if not 1 <= n <= _lib.MAX_CHAIN:
+            raise ValueError(f"a chain takes 1 to {_lib.MAX_CHAIN} linears, got {n}")
+        self.groups = nn.ModuleList(LRSLinearGroup(*st) for st in stages)
+        first = stages[0][0]
+        flat = [mod for st in stages for mod in st]
+        for mod in flat:
+            if mod.A.dtype != first.A.dtype or mod.A.device != first.A.device:
+                raise ValueError("chain members must share dtype and device")
+            if (getattr(mod, "kind", "") == "nm") != (getattr(first, "kind", "") == "nm"):
+                raise ValueError("chain members must share the sparse storage (2:4 or blocks)")
+            if mod._kernel_block != first._kernel_block:
+                raise ValueError("chain members must share the kernel block shape")
+        self._src: list[tuple[int, int]] = []
+        used = set()
+        for s, src in enumerate(sources, start=1):
+            hit = [(si, mi) for si in range(s) for mi, mod in enumerate(stages[si]) if mod is src]
+            if len(hit) != 1:
+                raise ValueError(f"stage {s}'s source must be one member of an earlier stage")
+            if hit[0] in used:
+                raise ValueError(f"stage {s}'s source already feeds another stage")
+            used.add(hit[0])
+            if src.out_features != stages[s][0].in_features:
+                raise ValueError(f"stage {s} reads {stages[s][0].in_features} features, its source "
+                                 f"writes {src.out_features}")
+            self._src.append(hit[0])
+        self.in_features = first.in_features
+
+    def _chained(self, states, M: int) -> bool:
+        st0 = states[0][0]
+        if st0.elem != 2 or M <= 0:
+            return False
+        if st0.s_format == 0 and not (st0.p == st0.q and st0.p in (16, 32, 64)):
+            return False
+        return not any(sts[0].takes_prefill(M, sum(st.NB for st in sts)) for sts in states)
+
+    def forward(self, x: torch.Tensor) -> tuple[tuple[torch.Tensor, ...], ...]:
+        first = self.groups[0].members[0]
+        if x.dtype != first.A.dtype:
+            raise TypeError(f"input dtype {x.dtype} does not match the weights' {first.A.dtype}")
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"input has {x.shape[-1]} features, expected {self.in_features}")
+        if x.device != first.A.device:
+            raise ValueError(f"input on {x.device}, weights on {first.A.device}")
+        states = [[mod._kernel() for mod in grp.members] for grp in self.groups]
+        outf = [[mod.out_features for mod in grp.members] for grp in self.groups]
+        st0 = states[0][0]
+        lead = x.shape[:-1]
+        x2 = st0.rows(x)
+        M = x2.shape[0]
+        if not self._chained(states, M):
+            outs: list[list[torch.Tensor]] = []
+            for s, sts in enumerate(states):
+                xin = x if s == 0 else outs[self._src[s - 1][0]][self._src[s - 1][1]]
+                outs.append(_launch(sts, xin, outf[s]))
+            return tuple(tuple(o) for o in outs)
+        lib = _lib.load()
+        flat = [st for sts in states for st in sts]
+        ys = [torch.empty(M, st.n_pad, dtype=x.dtype, device=x.device) for st in flat]
+        n_sync = int(lib.ssl_slr_chain_sync_count(M))
+        # the stage words start 256-byte aligned (64 int32 of slack)
+        members, sync = _members(flat, ys, M, 0, extra_counters=n_sync * (len(states) - 1) + 64)
+        sync = (sync + 255) // 256 * 256
+        stages = (_lib.SlrStage * len(states))()
+        base = [0]
+        for sts in states:
+            base.append(base[-1] + len(sts))
+        for s, sts in enumerate(states):
+            sg = stages[s]
+            sg.m, sg.m_pad = sts[0].m, sts[0].m_pad
+            sg.first, sg.count = base[s], len(sts)
+            if s == 0:
+                sg.x, sg.ldx, sg.src = x2.data_ptr(), x2.stride(0), -1
+            else:
+                si, mi = self._src[s - 1]
+                sg.src = base[si] + mi
+                sg.sync, sg.n_sync = sync + 4 * n_sync * (s - 1), n_sync
+        rc = lib.ssl_slr_forward_chain(M, st0.p, st0.q, st0.dtype_code, stages, len(states),
+                                       members, len(flat), _lib.stream_ptr(x.device))
+        _lib.check(rc, "ssl_slr_forward_chain")
+        outs = _outputs(flat, ys, [n for o in outf for n in o], tuple(lead))
+        return tuple(tuple(outs[base[s]:base[s + 1]]) for s in range(len(states)))
