@@ -59,7 +59,8 @@ const char* ssl_last_error(void);
  *   SSL_DEBUG_PREFILL_TILE      0: the library picks the prefill row tile;
  *                               1: always the narrow tile (128 token rows ×
  *                               64 output features); 2: always the tall one
- *                               (256 × 64). Either also sends fp32 calls of
+ *                               (256 × 64); 3: always the short one (64 × 64).
+ *                               Any of them also sends fp32 calls of
  *                               ssl_prefill_min_rows() rows or more to the
  *                               prefill kernels whatever their size.
  *   SSL_DEBUG_WAIT_POLLS        polls before a bounded wait gives up (0: the

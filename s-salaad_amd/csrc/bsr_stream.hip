@@ -226,9 +226,10 @@ int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_
   if (M < kPrefillMinM || !prefill_block(block_p, block_q, dtype)) return 0;
   if (dtype == SSL_F32) {
     // fp32 runs 16 times fewer MFMA flops per cycle: the tiled kernels win once
-    // their grid fills the device; smaller calls keep the streaming kernel's
-    // finer split (LLaMA-60M shapes at 2048 rows: 512-wide outputs stream).
-    // A forced row tile (test hook) sends every such call to the tiled kernels.
+    // a grid of their narrow (128-row) tiles fills the device; smaller calls
+    // keep the streaming kernel's finer split (LLaMA-60M shapes at 2048 rows:
+    // 512-wide outputs stream, 30-39 µs either way). A forced row tile (test
+    // hook) sends every such call to the tiled kernels.
     if (debug_knobs().prefill_group != 0) return 1;
     const int64_t items = ((M + 127) / 128) * ((n_rows + 64 / block_p - 1) / (64 / block_p));
     return items >= device_cus() ? 1 : 0;
@@ -333,7 +334,7 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
     pm.y = out; pm.ldy = ldo; pm.values_pq = values_pq;
     pm.values_bytes = nnz * block_p * block_q * eb;
     pm.groups = pf_groups; pm.steps = pf_steps; pm.n_groups = (int)pf_n_groups;
-    rows.bm = prefill_row_tile(M, n_chunks, pf_group, block_p, device_cus());
+    rows.bm = prefill_row_tile(M, n_chunks, pf_group, block_p, device_cus(), dtype);
     const int64_t T = (M + rows.bm - 1) / rows.bm;
     if (pf_n_groups * T > 0x7fffffffLL / 8) return fail(SSL_ERR_INVALID, "grid too large");
     rows.items = (int)(pf_n_groups * T);
@@ -437,7 +438,7 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
     for (int i = 0; i < n_members; ++i)
       if (members[i].NB > 0) total_rows += members[i].n_chunks;
     const int G = prefill_group(M, total_rows, block_p, cus);
-    rows.bm = prefill_row_tile(M, total_rows, G, block_p, cus);
+    rows.bm = prefill_row_tile(M, total_rows, G, block_p, cus, dtype);
     int64_t items = 0, litems = 0;
     for (int i = 0; i < n_members; ++i) {
       const ssl_slr_member& mb = members[i];

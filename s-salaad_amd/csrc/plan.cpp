@@ -86,7 +86,7 @@ int ssl_debug_set(int32_t knob, int64_t value) {
   DebugKnobs& k = debug_knobs();
   switch (knob) {
     case SSL_DEBUG_PREFILL_TILE:
-      if (value < 0 || value > 2) return fail(SSL_ERR_INVALID, "prefill tile override must be 0, 1 or 2");
+      if (value < 0 || value > 3) return fail(SSL_ERR_INVALID, "prefill tile override must be 0 to 3");
       k.prefill_group = value;
       return SSL_OK;
     case SSL_DEBUG_WAIT_POLLS:

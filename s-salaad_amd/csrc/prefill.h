@@ -54,11 +54,11 @@ struct PfArgs {
 constexpr int kPrefillLatentRows = 64;
 
 // Row-kernel tiles (token rows × output features): narrow 128 × 64, tall
-// 256 × 64 and wide 256 × 128; a workgroup owns BN / p block-rows.
-// Block-rows per row-kernel workgroup (64/p or 128/p).
+// 256 × 64 and short 64 × 64; a workgroup owns 64 / p block-rows.
+// Block-rows per row-kernel workgroup (64/p).
 int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus);
-// Token rows per row-kernel workgroup (128 or 256) for that group size.
-int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus);
+// Token rows per row-kernel workgroup (64, 128 or 256) for that group size.
+int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus, int dtype);
 // The fused SLR linear in one launch (after a small kernel that zeroes the
 // latent tile counters): the latent GEMM's workgroups (`lat`, one per 64-token
 // × 64-rank tile over all of in_features) first in the grid, then the row

@@ -748,8 +748,9 @@ __global__ __launch_bounds__(kPfThreads) void pf_zero_counts(PfArgs lat_by_value
 }
 
 // Row-kernel tiles: tall 256 × 64 (waves 4 × 1, 64 × 64 each; 80 KiB of LDS,
-// two workgroups per compute unit) and narrow 128 × 64 (waves 2 × 2, 64 × 32
-// each; 48 KiB), both with two stages. The latent's tiles are 64 tokens × 64
+// two workgroups per compute unit), narrow 128 × 64 (waves 2 × 2, 64 × 32
+// each; 48 KiB) and short 64 × 64 (waves 2 × 2, 32 × 32 each), all with two
+// stages. The latent's tiles are 64 tokens × 64
 // ranks (waves 2 × 2) with three stages.
 template <int DT, int KIND, int P>
 hipError_t launch_rows(const PfArgs& a, int G, hipStream_t s) {
@@ -759,6 +760,8 @@ hipError_t launch_rows(const PfArgs& a, int G, hipStream_t s) {
     hipLaunchKernelGGL((pf_gemm<DT, KIND, P, 256, 64, 4, 1, 2>), grid, blk, 0, s, a);
   else if (G * P == 64 && a.bm == 128)
     hipLaunchKernelGGL((pf_gemm<DT, KIND, P, 128, 64, 2, 2, 2>), grid, blk, 0, s, a);
+  else if (G * P == 64 && a.bm == 64)
+    hipLaunchKernelGGL((pf_gemm<DT, KIND, P, 64, 64, 2, 2, 2>), grid, blk, 0, s, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -791,6 +794,8 @@ hipError_t launch_fused_p(const PfArgs& rows, const PfArgs& lat, int G, hipStrea
     hipLaunchKernelGGL((pf_fused<DT, KIND, P, 256, 64, 4, 1>), grid, blk, 0, s, rows, lat);
   else if (rows.bm == 128)
     hipLaunchKernelGGL((pf_fused<DT, KIND, P, 128, 64, 2, 2>), grid, blk, 0, s, rows, lat);
+  else if (rows.bm == 64)
+    hipLaunchKernelGGL((pf_fused<DT, KIND, P, 64, 64, 2, 2>), grid, blk, 0, s, rows, lat);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -815,16 +820,24 @@ int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus) {
   return 64 / block_p;
 }
 
-int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus) {
+int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus, int dtype) {
   (void)block_p;
   const int64_t forced = debug_knobs().prefill_group;  // test hook
   if (forced == 1) return 128;
   if (forced == 2) return 256;
+  if (forced == 3) return 64;
   // the tall tile (fewer re-reads of x and of the weights, more MFMA work per
   // LDS byte) unless it would leave compute units idle that the narrow one
-  // fills: it runs two workgroups per compute unit
+  // fills: it runs two workgroups per compute unit. fp32 steps are latency
+  // bound (a quarter of the k of a 16-bit step per load round trip): the short
+  // tile when the narrow one gives fewer than two workgroups per compute unit
+  // (LLaMA-60M gate at 2048 rows: 58 -> 50 µs; 16-bit calls gain nothing).
   const int64_t groups = (n_rows + group - 1) / group;
   const int64_t tall = ((M + 255) / 256) * groups, narrow = ((M + 127) / 128) * groups;
+  if (dtype == SSL_F32 && narrow < 2 * n_cus) return 64;
+  // (at 128 rows or fewer both give one tile per group, and the tall one's
+  // lower half would be rows past M: 7B FFN at 128 rows, 55.6 vs 41.0 µs)
+  if (M <= 128) return 128;
   return (tall >= 2 * n_cus || tall >= narrow) ? 256 : 128;
 }
 

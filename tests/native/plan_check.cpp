@@ -187,7 +187,7 @@ int main() {
   CHECK(ssl_plan_build(nullptr, nullptr, 0, 0, nullptr, 0, 16, 0, 0, nullptr, 0, &a, &b) ==
         SSL_ERR_INVALID);
   CHECK(ssl_debug_set(99, 0) == SSL_ERR_INVALID);
-  CHECK(ssl_debug_set(SSL_DEBUG_PREFILL_TILE, 3) == SSL_ERR_INVALID);
+  CHECK(ssl_debug_set(SSL_DEBUG_PREFILL_TILE, 4) == SSL_ERR_INVALID);
   CHECK(ssl_debug_set(SSL_DEBUG_PREFILL_TILE, 0) == SSL_OK);
   CHECK(ssl_last_error() != nullptr);
   if (g_fail) {

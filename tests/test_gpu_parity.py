@@ -721,7 +721,7 @@ def test_nm24_llama7b_ffn_shape_decode(gpu_device):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("shape", [(256, 192, 64), (100, 200, 24), (320, 1024, 128)])
-@pytest.mark.parametrize("tile_mode", [0, 1, 2], ids=["auto", "narrow", "tall"])
+@pytest.mark.parametrize("tile_mode", [0, 1, 2, 3], ids=["auto", "narrow", "tall", "short"])
 @pytest.mark.parametrize("M", [128, 600])
 def test_nm24_prefill_matches_oracle(dtype, shape, tile_mode, M, gpu_device):
     n, m, r = shape

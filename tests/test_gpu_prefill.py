@@ -1,9 +1,9 @@
 """The prefill row kernels (calls with many token rows, 16-bit activations),
 every tile configuration checked against the oracle on every output row.
 
-The row kernel has two tiles (token rows × output features, 64/p block-rows
-per workgroup): "narrow" (128 × 64) and "tall" (256 × 64); the library picks
-one per call. The test hook SSL_DEBUG_PREFILL_TILE
+The row kernel has three tiles (token rows × output features, 64/p block-rows
+per workgroup): "narrow" (128 × 64), "tall" (256 × 64) and "short" (64 × 64);
+the library picks one per call. The test hook SSL_DEBUG_PREFILL_TILE
 forces each tile on any shape, for the fused linear (PF_FUSED), the grouped
 launch and the in-place op (PF_OP). The full-size cases at the end run every
 tile at the benchmark shapes, checked on all rows.
@@ -25,9 +25,9 @@ from ssalaad_amd import _lib
 
 pytestmark = pytest.mark.gpu
 
-NARROW, TALL = 1, 2
-MODES = [NARROW, TALL]
-MODE_IDS = ["narrow", "tall"]
+NARROW, TALL, SHORT = 1, 2, 3
+MODES = [NARROW, TALL, SHORT]
+MODE_IDS = ["narrow", "tall", "short"]
 DT16 = [torch.bfloat16, torch.float16]
 
 
