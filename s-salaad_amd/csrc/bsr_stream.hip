@@ -85,6 +85,8 @@ struct Layout {
   int n_rt, n_kc_max, ku_total;
   int64_t cnt_total;  // int32 row counters: [MG][NB]
   int64_t n_sync;     // u64 handshake words: status, then (2 + n_rt) per token tile
+  int64_t fin_off;    // byte offset in the exchange area of the final-count copies
+  int64_t x_total;    // exchange area bytes
   int64_t t_part, t_final, part_main, pf_cnt, total;
 };
 
@@ -99,6 +101,8 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   L.n_kc_max = latent_split_max(M, m_pad);
   L.cnt_total = (int64_t)L.MG * NB;
   L.n_sync = 1 + (int64_t)L.MG * (2 + L.n_rt);
+  L.fin_off = align_up(8 * L.n_sync, 256);
+  L.x_total = L.fin_off + (L.n_rt > 0 ? 8LL * L.MG * kFinCopies * kFinSlotWords : 0);
   const int64_t rows = (int64_t)L.MG * 16 * L.MT;
   int64_t off = 0;
   L.t_part = off;
@@ -171,9 +175,9 @@ int check_member(int i, const ssl_slr_member& mb, int64_t M, int64_t m_pad, int 
   if (mb.n_counters < L->cnt_total || !mb.counters)
     return fail(SSL_ERR_WORKSPACE, "linear %d: %lld zeroed counters needed", i,
                 (long long)L->cnt_total);
-  if (mb.exchange_bytes < 8 * L->n_sync || !mb.exchange)
+  if (mb.exchange_bytes < L->x_total || !mb.exchange)
     return fail(SSL_ERR_WORKSPACE, "linear %d: exchange area of %lld bytes needed", i,
-                (long long)(8 * L->n_sync));
+                (long long)L->x_total);
   if (!aligned(mb.exchange, 256))
     return fail(SSL_ERR_WORKSPACE, "linear %d: exchange area must be 256-byte aligned", i);
   return SSL_OK;
@@ -197,6 +201,8 @@ void fill_args(SlrArgs& a, const ssl_slr_member& mb, const Layout& L, const void
   a.ku_chunk = ku_chunk;
   a.n_lat_wgs = (int)((int64_t)L.n_rt * n_kc * L.MG);
   a.sync = (u64*)mb.exchange; a.lr_wgs = (int)mb.lr_wgs; a.lat_weight = kLatentUnits / n_kc;
+  a.fin = (u64*)((char*)mb.exchange + L.fin_off);
+  a.tk_copies = mb.lr_wgs == mb.NB ? kFinCopies : 1;
   a.status = mb.status ? (u64*)mb.status : (u64*)mb.exchange;
   set_block_shape(a, dtype, block_p, block_q, s_format);
   a.wait_polls = knobs.wait_polls > 0 ? (int)knobs.wait_polls : kSpinLimit;
@@ -364,7 +370,7 @@ int64_t ssl_slr_counter_count(int64_t M, int64_t NB) {
 int64_t ssl_slr_exchange_size(int64_t M, int64_t r_pad, int64_t m_pad, int32_t dtype) {
   (void)m_pad;
   (void)dtype;
-  return align_up(8 * slr_layout(M, 0, 16, r_pad, 64, 0, SSL_BF16).n_sync, 256);
+  return slr_layout(M, 0, 16, r_pad, 64, 0, SSL_BF16).x_total;
 }
 
 int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r_pad,

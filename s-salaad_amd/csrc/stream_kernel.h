@@ -367,11 +367,19 @@ struct SlrArgs {
   int n_lat_wgs;    // latent workgroups at the start of the grid (n_rt·n_kc·MG)
   // Handshake words, all monotonic (never reset): sync[0] is the status (1 =
   // a wait gave up); token tile mg owns sync[1 + mg·(2 + n_rt) ...]:
-  //   [0] final latent tiles written (+1 per rank tile and launch)
-  //   [1] consumer tickets (+1 per consuming workgroup and launch)
+  //   [0], [1] unused
   //   [2 + rt] arrivals of rank tile rt's K chunks (+kLatentUnits/n_kc each,
   //       so every launch adds exactly kLatentUnits whatever its split)
+  // and, in fin's 512-byte slot (mg·kFinCopies + c), c < kFinCopies, copy c of
+  // token tile mg's count of final latent tiles written (word 0: +1 per rank
+  // tile and launch, to every copy) and consumer tickets (word kFinTicket: +1
+  // per consuming workgroup of copy c and launch). With tk_copies = kFinCopies
+  // (every block-row has exactly one consuming chunk, lr_wgs = NB) the
+  // consumers of block-row `row` use copy row % kFinCopies; otherwise every
+  // consumer takes its ticket from copy 0 and polls copy chunk % kFinCopies.
   u64* sync;
+  u64* fin;
+  int tk_copies;
   int lr_wgs;       // workgroups that consume the latent (per token tile)
   int lat_weight;   // kLatentUnits / n_kc
   // Bounded waits: where a timeout is reported (the caller's status word, or
@@ -431,6 +439,17 @@ __device__ __forceinline__ void wait_dep(const SlrArgs& a, int mg, int w) {
 
 __device__ __forceinline__ u64* tile_sync(const SlrArgs& a, int mg) {
   return a.sync + 1 + (int64_t)mg * (2 + a.n_rt);
+}
+
+// Copies of a token tile's final-latent count, each in its own 512-byte slot:
+// the count every consumer of the tile polls, so that the polls (and the
+// latent's increments behind them) spread over several memory locations
+// instead of queueing at one.
+constexpr int kFinCopies = 8;
+constexpr int kFinSlotWords = 64;
+constexpr int kFinTicket = 32;
+__device__ __forceinline__ u64* fin_copy(const SlrArgs& a, int mg, int c) {
+  return a.fin + ((int64_t)mg * kFinCopies + c) * kFinSlotWords;
 }
 
 // ---------------------------------------------------------------------------
@@ -589,7 +608,7 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
       }
     }
   wait_mem();
-  if (lane == 0) rmw_add64(sy, 1);
+  if (lane < kFinCopies) rmw_add64(fin_copy(a, mg, lane), 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -636,10 +655,12 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
 
   const bool used_t = (MODE == MODE_FUSED) && lb < le;
   // A consumer of the latent takes a ticket at once (its latency hides behind
-  // the row's loads). Launch k's consumers hold tickets k·lr_wgs ... and wait
-  // for (k + 1)·(latent workgroups) completions, so no counter is ever reset.
+  // the row's loads). Launch k's n consumers of a ticket copy hold its tickets
+  // k·n ... and wait for (k + 1)·n_rt final tiles, so no counter is ever reset.
   u64 ticket = 0;
-  if (used_t && threadIdx.x == 0) ticket = rmw_add64(tile_sync(a, mg) + 1, 1);
+  const bool per_row = a.tk_copies > 1;
+  const int tc = per_row ? row % kFinCopies : 0;
+  if (used_t && threadIdx.x == 0) ticket = rmw_add64(fin_copy(a, mg, tc) + kFinTicket, 1);
 
   // The wave's first low-rank unit of A does not depend on the latent: its
   // loads go out ahead of the sparse blocks.
@@ -756,8 +777,12 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   if constexpr (MODE == MODE_FUSED) {
     if (used_t) {
       if (threadIdx.x == 0) {
-        const u64 target = (ticket / (u64)a.lr_wgs + 1) * (u64)a.n_rt;
-        wait_at_least<u64>(tile_sync(a, mg), target + (u64)a.wait_bias, a.status, a.wait_polls);
+        // this copy's consumers per launch
+        const int n_tc =
+            per_row ? a.NB / kFinCopies + (tc < a.NB % kFinCopies ? 1 : 0) : a.lr_wgs;
+        const u64 target = (ticket / (u64)n_tc + 1) * (u64)a.n_rt;
+        wait_at_least<u64>(fin_copy(a, mg, per_row ? tc : chunk % kFinCopies),
+                           target + (u64)a.wait_bias, a.status, a.wait_polls);
       }
       __syncthreads();
       const auto tr = dev_rsrc(a.t);
