@@ -113,7 +113,9 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   off = align_up(off + 4 * (int64_t)L.MG * n_slots * (16 * L.MT * p), 256);
   // the prefill kernels' latent tile counters (one per kPrefillLatentRows rows)
   L.pf_cnt = off;
-  if (M >= kPrefillMinM) off = align_up(off + 4 * ((M + kPrefillLatentRows - 1) / kPrefillLatentRows), 256);
+  if (M >= kPrefillMinM)
+    off = align_up(off + 4LL * kPfCntCopies * kPfCntStride *
+                             ((M + kPrefillLatentRows - 1) / kPrefillLatentRows), 256);
   L.total = off;
   return L;
 }

@@ -10,6 +10,13 @@ namespace ssl {
 // Calls with at least this many token rows (and 16-bit activations) take the
 // LDS-tiled prefill kernels; fewer rows take the row-streaming decode kernel.
 constexpr int64_t kPrefillMinM = 128;
+// Copies of each latent tile counter, one per wave of a row workgroup, each in
+// its own 512-byte slot: every wave of every row workgroup of a token tile
+// polls its counter when it reaches its low-rank steps, and workgroups that
+// started together get there together; with one word those polls queue at one
+// memory location.
+constexpr int kPfCntCopies = 4;
+constexpr int kPfCntStride = 128;
 
 enum : int { PF_OP = 0, PF_FUSED = 1 };
 
@@ -29,8 +36,9 @@ struct PfMember {
   int64_t ldb;
   void* t;              // latent [M][r_pad], activation dtype
   int64_t ldt;
-  int32_t* tcnt;        // latent tiles written, per latent token tile (zeroed before
-                        // the launch; the low-rank steps wait on them)
+  int32_t* tcnt;        // latent tiles written, per latent token tile, in
+                        // kPfCntCopies copies kPfCntStride int32 apart (zeroed
+                        // before the launch; the low-rank steps wait on them)
   int r_pad;
 };
 

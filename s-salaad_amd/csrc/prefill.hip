@@ -410,7 +410,8 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
         const int lt1 = (min(m0 + BM, M) - 1) / lbm;
         for (int lt = m0 / lbm; lt <= lt1; ++lt) {
           int n = 0;
-          while (__hip_atomic_load(mb.tcnt + lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+          const int32_t* w = mb.tcnt + ((int64_t)lt * kPfCntCopies + wid % kPfCntCopies) * kPfCntStride;
+          while (__hip_atomic_load(const_cast<int32_t*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
                  target) {
             __builtin_amdgcn_s_sleep(2);
             if (++n > polls) {
@@ -637,8 +638,9 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
       }
     __builtin_amdgcn_s_waitcnt(0);  // this thread's stores acknowledged
     __syncthreads();
-    if (tid == 0)
-      __hip_atomic_fetch_add(tcnt + m0 / BM, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < kPfCntCopies)
+      __hip_atomic_fetch_add(tcnt + ((int64_t)(m0 / BM) * kPfCntCopies + tid) * kPfCntStride, 1,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else if constexpr (NM) {
     // lane (c, gq) holds features 4gq + e of feature tile nt for token 16·mt + c
     void* const y_out = mb.y;
@@ -740,10 +742,10 @@ void pf_fused(PfArgs rows_by_value, PfArgs lat_by_value) {
 __global__ __launch_bounds__(kPfThreads) void pf_zero_counts(PfArgs lat_by_value) {
   (void)lat_by_value;
   const PfArgs& a = *(const PfArgs*)__builtin_amdgcn_kernarg_segment_ptr();
-  const int n_lt = (a.M + a.lbm - 1) / a.lbm;
+  const int n_lt = (a.M + a.lbm - 1) / a.lbm * kPfCntCopies;  // counter copies per member
   for (int i = threadIdx.x; i < a.n * n_lt; i += kPfThreads) {
     int32_t* c = a.mb[i / n_lt].tcnt;
-    if (c) c[i % n_lt] = 0;
+    if (c) c[(int64_t)(i % n_lt) * kPfCntStride] = 0;
   }
 }
 

@@ -310,9 +310,9 @@ def test_workspace_sizes_are_aligned_and_monotone():
     assert a == 8 * 16 * 256 * 4 + 16 * 256 * 2
     assert b == a + 100 * 16 * 64 * 4
     # 2048 rows: no latent K split (the prefill kernels run the latent in the
-    # row launch, whole), the final latent, the split-row partials, then one
-    # latent tile counter per 64 rows (32 int32, 256-byte aligned)
-    assert c == 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4 + 256
+    # row launch, whole), the final latent, the split-row partials, then the
+    # latent tile counters: 4 copies of 512 bytes per 64 rows
+    assert c == 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4 + 32 * 4 * 512
     # counters: one per (token tile, block-row)
     assert lib.ssl_slr_counter_count(16, 172) == 172
     assert lib.ssl_slr_counter_count(2048, 172) == 32 * 172
