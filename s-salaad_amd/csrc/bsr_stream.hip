@@ -530,6 +530,10 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
   return ssl_slr_forward_group(x, ldx, M, m, m_pad, block_p, block_q, dtype, &mb, 1, stream);
 }
 
+// K units (of 32 in_features) per latent chunk in a chained stage after the
+// first: one batch of loads for each of the 8 waves.
+constexpr int kChainLatentUnits = 64;
+
 int64_t ssl_slr_chain_sync_count(int64_t M) {
   if (M <= 0) return 0;
   const int MT = tile_mt(M);
@@ -621,13 +625,23 @@ int ssl_slr_forward_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t d
                   "stage %d: a call of %lld token rows runs the prefill kernels; launch the "
                   "stages one by one", s, (long long)M);
     // Stage 0: the K split a grouped launch of its members would take (its
-    // results equal ssl_slr_forward_group's bit for bit). Later stages: one K
-    // chunk, so a latent tile is final without an exchange of partials (its
-    // B loads go out before the stage's input is ready, and the partial
-    // exchange would be one more hop after it): measured 4-5% per step at 1
-    // and 4 token rows, none at 16.
+    // results equal ssl_slr_forward_group's bit for bit). Later stages: K
+    // chunks of at most kChainLatentUnits units, one batch of loads per wave
+    // (its B loads go out before the stage's input is ready), so a latent
+    // over 2048 in_features is final without an exchange of partials:
+    // measured 4-5% per step at 1 and 4 token rows against the standalone
+    // split; the 5461-wide down projection takes three chunks (one chunk of
+    // 350 KB of loads per workgroup took 6.4 µs).
     int n_kc = 1, ku_chunk = L[st.first].ku_total;
-    if (s == 0) latent_chunks(L[st.first], n_stream, rt_tiles, &n_kc, &ku_chunk);
+    if (s == 0) {
+      latent_chunks(L[st.first], n_stream, rt_tiles, &n_kc, &ku_chunk);
+    } else {
+      n_kc = (L[st.first].ku_total + kChainLatentUnits - 1) / kChainLatentUnits;
+      if (n_kc > L[st.first].n_kc_max) n_kc = L[st.first].n_kc_max;
+      if (n_kc < 1) n_kc = 1;
+      ku_chunk = (L[st.first].ku_total + n_kc - 1) / n_kc;
+      n_kc = (L[st.first].ku_total + ku_chunk - 1) / ku_chunk;
+    }
     // waiters of one token tile: every latent workgroup, then every row
     // workgroup of the stage's members, numbered in that order
     int waiters = 0;
