@@ -14,10 +14,14 @@ residual); down reads gate's output (silu(gate)·up); the next layer reads
 down's output. So every projection waits for the one before it, as in decode.
 
 Launches: one chained launch per layer (LRSLinearChain: the stages q,k,v |
-o | gate,up | down in one launch, each waiting inside the launch for its
-input), 24 per step. --no-chain: the stages as grouped launches
-(LRSLinearGroup), 4 per layer, 96 per step; --no-group: one launch per
-linear, 168 per step.
+o | gate,up | down, each waiting inside the launch for its input), 24 per
+step. --stack: ONE launch for the 96 stages of all 24 layers (a prepared
+chain with its descriptor table in device memory; measured a few percent
+slower at 16 rows: later layers' workgroups, dispatched into whichever slots
+free up, crowd the compute units of the running stage); --no-chain: the
+stages as grouped launches (LRSLinearGroup), 4 per layer, 96 per step;
+--no-group: one launch per linear, 168 per step. Calls the chained kernel does
+not serve (the 2048-token prefill detail) run the stages as grouped launches.
 
 Timing: the step is captured once in a HIP graph and replayed; W untimed
 replays, then K replays bracketed by synchronize + HIP events on the replay
@@ -89,6 +93,8 @@ for _p in (ROOT, ROOT / "s-salaad_amd"):
 HBM_PEAK_GBS = 8000.0
 # the dominant kernel of the default workload's launches, by launch mode
 KERNEL_NAMES = {
+    "stack": "slr_chain_tab_kernel<1, 32, 8, 1, 4, 0> (bf16, p 32, KE 8, MT 1, UNR 4, BSR): one "
+             "launch per step, 96 stages (24 layers × q,k,v | o | gate,up | down)",
     "chain": "slr_chain_kernel<1, 32, 8, 1, 4, 0> (bf16, p 32, KE 8, MT 1, UNR 4, BSR): one "
              "launch per layer, stages q,k,v | o | gate,up | down",
     "groups": "slr_kernel<1, 32, 8, 1, 1, 4, 0> (bf16, p 32, KE 8, MT 1, fused, UNR 4, BSR)",
@@ -233,11 +239,24 @@ def run_gpu(args, layers=None, M=None, steps=None):
                                       [d["down"]]], sources=[d["q"], d["o"], d["gate"]]))
     groups = [(LRSLinearGroup(*c.groups[0].members), c.groups[1].members[0],
                LRSLinearGroup(*c.groups[2].members), c.groups[3].members[0]) for c in chains]
-    mode = "linears" if args.no_group else ("groups" if args.no_chain else "chain")
+    mode = ("linears" if args.no_group else "groups" if args.no_chain
+            else "stack" if args.stack else "chain")
+    stack = None
+    if mode == "stack":
+        stages, sources = [], []
+        for li, c in enumerate(chains):
+            if li > 0:
+                sources.append(chains[li - 1].groups[3].members[0])
+            stages += [list(g.members) for g in c.groups]
+            sources += [c.groups[0].members[0], c.groups[1].members[0], c.groups[2].members[0]]
+        stack = LRSLinearChain(stages, sources)
+        st = [[m._kernel() for m in g.members] for g in stack.groups]
+        if not stack._chained(st, M):
+            mode = "groups"  # prefill sizes: the stages one by one
 
     def layer_fwd(li, x):
         """The layer's 7 outputs (q, k, v, o, gate, up, down)."""
-        if mode == "chain":
+        if mode in ("chain", "stack"):
             return [y for stage in chains[li](x) for y in stage]
         d = dict(layers[li])
         if mode == "groups":
@@ -259,7 +278,14 @@ def run_gpu(args, layers=None, M=None, steps=None):
             x = ys[-1]
         return outs
 
-    if mode == "chain":
+    if mode == "stack":
+        prep = stack.prepare(x0)
+
+        def step():  # noqa: F811  (the whole stack in one launch)
+            return [y for stage in prep.run() for y in stage]
+
+        n_launch = 1
+    elif mode == "chain":
         st = [[m._kernel() for m in g.members] for g in chains[0].groups]
         n_launch = len(layers) * (1 if chains[0]._chained(st, M) else 4)
     else:
@@ -309,12 +335,17 @@ def run_gpu(args, layers=None, M=None, steps=None):
         n_linears=n_lin,
         n_launches=n_launch,
     )
-    # a parity spot check of the timed graph: the last layer recomputed eagerly
-    # from the input the graph gave it
-    x_last, ys_last = keep[-1]
-    ref = layer_fwd(len(layers) - 1, x_last)
-    torch.cuda.synchronize()
-    res["graph_matches_eager"] = all(bool(torch.equal(a, b)) for a, b in zip(ys_last, ref))
+    # a parity spot check of the timed graph: the whole stack (or its last
+    # layer, from the input the graph gave it) recomputed eagerly
+    if mode == "stack":
+        ref = [y for stage in stack(x0) for y in stage]
+        torch.cuda.synchronize()
+        res["graph_matches_eager"] = all(bool(torch.equal(a, b)) for a, b in zip(keep, ref))
+    else:
+        x_last, ys_last = keep[-1]
+        ref = layer_fwd(len(layers) - 1, x_last)
+        torch.cuda.synchronize()
+        res["graph_matches_eager"] = all(bool(torch.equal(a, b)) for a, b in zip(ys_last, ref))
     res["mode"] = mode
     from ssalaad_amd.ls_linear import latent_wait_status
 
@@ -834,6 +865,8 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="launch eagerly instead of replaying a HIP graph (default workload, "
                          "llama7b_ffn_decode and llama7b_ffn_decode_nm24)")
+    ap.add_argument("--stack", action="store_true",
+                    help="one chained launch for the whole stack instead of one per layer")
     ap.add_argument("--no-chain", action="store_true",
                     help="the four stages of a layer as grouped launches instead of one chained launch")
     ap.add_argument("--no-group", action="store_true",

@@ -372,6 +372,26 @@ int ssl_slr_forward_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t d
                           const ssl_slr_stage* stages, int32_t n_stages,
                           const ssl_slr_member* members, int32_t n_members, void* stream);
 
+/* A chained launch of many stages (up to SSL_MAX_CHAIN_TABLE linears and as
+ * many stages, e.g. every projection of every layer of a model's decode step
+ * in ONE launch, each layer's q,k,v a stage reading the previous layer's down
+ * projection), described by a table in device memory instead of kernel
+ * arguments. ssl_slr_chain_table_build checks the call exactly as
+ * ssl_slr_forward_chain does and writes the table (ssl_slr_chain_table_bytes,
+ * 16-byte aligned) into host memory; the caller copies it to device memory
+ * once, and ssl_slr_chain_table_launch launches it (table_dev must hold a copy
+ * of table_host). The table holds every pointer of the call (input, outputs,
+ * weights, scratch): a launch recomputes the same call on whatever those
+ * buffers hold, so it suits static-buffer decode loops and graph capture.
+ * Extends ssl_slr_forward_chain; no reference counterpart. */
+#define SSL_MAX_CHAIN_TABLE 256
+int64_t ssl_slr_chain_table_bytes(void);
+int ssl_slr_chain_table_build(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,
+                              const ssl_slr_stage* stages, int32_t n_stages,
+                              const ssl_slr_member* members, int32_t n_members, void* table,
+                              int64_t table_bytes);
+int ssl_slr_chain_table_launch(const void* table_host, const void* table_dev, void* stream);
+
 /* -------------------------------------------------------------------------
  * Block projection (device): keep the n_keep blocks of largest Frobenius norm.
  * Replaces ssalaad/inference/egar.py:296-317 (_project_S), the sparse step of

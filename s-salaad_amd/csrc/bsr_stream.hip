@@ -2,6 +2,10 @@
 // scratch layout and launch set-up of the C-ABI entry points. The kernels are
 // in stream_kernel.h, instantiated per dtype in stream_{bf16,f16,f32}.hip.
 
+#include <string.h>
+
+#include <vector>
+
 #include "abi_internal.h"
 #include "prefill.h"
 #include "stream_kernel.h"
@@ -212,6 +216,172 @@ void fill_args(SlrArgs& a, const ssl_slr_member& mb, const Layout& L, const void
   a.wait_bias = knobs.wait_unreachable ? (1 << 30) : 0;
   a.dep = nullptr; a.dep_need = 0; a.dep_waiters = 0; a.done = nullptr; a.done_copies = 0;
 }
+
+// K units (of 32 in_features) per latent chunk in a chained stage after the
+// first: one batch of loads for each of the 8 waves.
+constexpr int kChainLatentUnits = 64;
+
+// Checks a chained launch and fills its descriptor (c, zeroed by the caller,
+// with room for NMAX members); c->grid = 0 when there is nothing to launch.
+template <int NMAX>
+int build_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,
+                const ssl_slr_stage* stages, int32_t n_stages, const ssl_slr_member* members,
+                int32_t n_members, int max_stages, ChainDesc<NMAX>* c) {
+  if (dtype != SSL_BF16 && dtype != SSL_F16)
+    return fail(SSL_ERR_UNSUPPORTED, "chained launches take bf16 or fp16 activations");
+  if (n_stages < 1 || n_stages > max_stages || !stages)
+    return fail(SSL_ERR_INVALID, "a chained launch takes 1 to %d stages, got %d", max_stages,
+                n_stages);
+  if (n_members < 1 || n_members > NMAX || !members)
+    return fail(SSL_ERR_INVALID, "a chained launch takes 1 to %d linears, got %d", NMAX,
+                n_members);
+  const int s_format = members[0].s_format;
+  if (s_format == SSL_S_NM24) {
+    if (block_p != kNmBlock || block_q != kNmBlock)
+      return fail(SSL_ERR_UNSUPPORTED, "2:4 blocks are 32x32");
+  } else if (s_format != SSL_S_BSR) {
+    return fail(SSL_ERR_INVALID, "unknown sparse storage format %d", s_format);
+  } else if (block_p != block_q || (block_p != 16 && block_p != 32 && block_p != 64)) {
+    return fail(SSL_ERR_UNSUPPORTED, "chained launches take square blocks of 16, 32 or 64, got %dx%d",
+                block_p, block_q);
+  }
+  if (M < 0) return fail(SSL_ERR_INVALID, "negative size");
+  c->grid = 0;
+  if (M == 0) return SSL_OK;
+  if (M > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "too many token rows");
+  const int eb = elem_bytes(dtype);
+  const int64_t n_sync = ssl_slr_chain_sync_count(M);
+
+  // stages: contiguous member ranges in order; each later stage reads the
+  // output of one member of an earlier stage, and a member feeds at most one
+  std::vector<int> fed(n_members, 0);
+  int next = 0;
+  for (int s = 0; s < n_stages; ++s) {
+    const ssl_slr_stage& st = stages[s];
+    if (st.first != next || st.count < 1 || st.first + st.count > n_members)
+      return fail(SSL_ERR_INVALID, "stage %d: its members must follow the previous stage's", s);
+    next = st.first + st.count;
+    if (st.m < 1 || st.m_pad % 64 || st.m_pad < st.m)
+      return fail(SSL_ERR_INVALID, "stage %d: m >= 1 and m_pad a multiple of 64 and >= m", s);
+    if (s == 0) {
+      if (st.src != -1) return fail(SSL_ERR_INVALID, "stage 0 reads the launch's input (src -1)");
+      if (!st.x || !aligned(st.x, 16) || st.ldx < st.m || (st.ldx * eb) % 16)
+        return fail(SSL_ERR_INVALID, "x rows must be 16-byte aligned and at least m wide");
+      continue;
+    }
+    if (st.src < 0 || st.src >= st.first)
+      return fail(SSL_ERR_INVALID, "stage %d: src must be a member of an earlier stage", s);
+    const ssl_slr_member& src = members[st.src];
+    if (fed[st.src]++) return fail(SSL_ERR_INVALID, "stage %d: member %d already feeds a stage", s, st.src);
+    if (src.NB * block_p < st.m)
+      return fail(SSL_ERR_INVALID, "stage %d: in_features %lld exceed member %d's %lld outputs", s,
+                  (long long)st.m, st.src, (long long)(src.NB * block_p));
+    if (st.x && st.x != src.y)
+      return fail(SSL_ERR_INVALID, "stage %d: x must be NULL (member %d's output)", s, st.src);
+    if (!st.sync || st.n_sync < n_sync || !aligned(st.sync, 256))
+      return fail(SSL_ERR_WORKSPACE, "stage %d: %lld zeroed sync words needed", s,
+                  (long long)n_sync);
+    if (M * src.ldy * eb > 0x7fffffffLL)
+      return fail(SSL_ERR_UNSUPPORTED, "stage %d: its input is beyond 2 GiB; split the call by tokens", s);
+  }
+  if (next != n_members) return fail(SSL_ERR_INVALID, "every member belongs to one stage");
+
+  std::vector<Layout> L(n_members);
+  int64_t wg = 0;
+  int nseg = 0;
+  int MT = tile_mt(M);
+  for (int s = 0; s < n_stages; ++s) {
+    const ssl_slr_stage& st = stages[s];
+    const void* x = s == 0 ? st.x : members[st.src].y;
+    const int64_t ldx = s == 0 ? st.ldx : members[st.src].ldy;
+    int64_t n_stream = 0, rt_tiles = 0, rows = 0;
+    for (int i = st.first; i < st.first + st.count; ++i) {
+      const ssl_slr_member& mb = members[i];
+      const int rc = check_member(i, mb, M, st.m_pad, block_p, block_q, dtype, s_format, &L[i]);
+      if (rc != SSL_OK) return rc;
+      n_stream += (mb.NB > 0 ? mb.n_chunks : 0) * L[i].MG;
+      rt_tiles += (int64_t)L[i].n_rt * L[i].MG;
+      rows += mb.NB;
+    }
+    if (s_format == SSL_S_NM24 ? ssl_nm24_takes_prefill(M, rows, dtype)
+                               : ssl_slr_takes_prefill(M, rows, block_p, block_q, dtype))
+      return fail(SSL_ERR_UNSUPPORTED,
+                  "stage %d: a call of %lld token rows runs the prefill kernels; launch the "
+                  "stages one by one", s, (long long)M);
+    // Stage 0: the K split a grouped launch of its members would take (its
+    // results equal ssl_slr_forward_group's bit for bit). Later stages: K
+    // chunks of at most kChainLatentUnits units, one batch of loads per wave
+    // (its B loads go out before the stage's input is ready), so a latent
+    // over 2048 in_features is final without an exchange of partials:
+    // measured 4-5% per step at 1 and 4 token rows against the standalone
+    // split; the 5461-wide down projection takes three chunks (one chunk of
+    // 350 KB of loads per workgroup took 6.4 µs).
+    int n_kc = 1, ku_chunk = L[st.first].ku_total;
+    if (s == 0) {
+      latent_chunks(L[st.first], n_stream, rt_tiles, &n_kc, &ku_chunk);
+    } else {
+      n_kc = (L[st.first].ku_total + kChainLatentUnits - 1) / kChainLatentUnits;
+      if (n_kc > L[st.first].n_kc_max) n_kc = L[st.first].n_kc_max;
+      if (n_kc < 1) n_kc = 1;
+      ku_chunk = (L[st.first].ku_total + n_kc - 1) / n_kc;
+      n_kc = (L[st.first].ku_total + ku_chunk - 1) / ku_chunk;
+    }
+    // waiters of one token tile: every latent workgroup, then every row
+    // workgroup of the stage's members, numbered in that order
+    int waiters = 0;
+    for (int i = st.first; i < st.first + st.count; ++i) {
+      SlrArgs& a = c->m[i];
+      fill_args(a, members[i], L[i], x, ldx, M, st.m, st.m_pad, n_kc, ku_chunk, dtype, block_p,
+                block_q, s_format);
+      c->seg_start[nseg] = (int)wg;
+      c->seg_member[nseg] = i;
+      c->seg_rows[nseg++] = 0;
+      wg += (int64_t)L[i].n_rt * n_kc * L[i].MG;
+      a.dep_lat_base = waiters;
+      waiters += L[i].n_rt * n_kc;
+    }
+    for (int i = st.first; i < st.first + st.count; ++i) {
+      const ssl_slr_member& mb = members[i];
+      c->seg_start[nseg] = (int)wg;
+      c->seg_member[nseg] = i;
+      c->seg_rows[nseg++] = 1;
+      wg += (mb.NB > 0 ? mb.n_chunks : 0) * L[i].MG;
+      c->m[i].dep_row_base = waiters;
+      waiters += mb.NB > 0 ? (int)mb.n_chunks : 0;
+      if (wg > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
+    }
+    if (s > 0 && waiters > 0) {
+      // the stage waits for its source; the source counts its row tiles
+      for (int i = st.first; i < st.first + st.count; ++i) {
+        c->m[i].dep = st.sync;
+        c->m[i].dep_need = (int)members[st.src].NB;
+        c->m[i].dep_waiters = waiters;
+      }
+      c->m[st.src].done = st.sync;
+      c->m[st.src].done_copies = waiters < kDepCopies ? waiters : kDepCopies;
+    }
+  }
+  c->n_seg = nseg;
+  c->seg_start[nseg] = (int)wg;
+  c->grid = wg;
+  c->M = (int)M;
+  c->block_p = block_p;
+  c->dtype = dtype;
+  c->sf = s_format == SSL_S_NM24 ? SF_NM24 : SF_BSR;
+  (void)MT;
+  return SSL_OK;
+}
+
+template <int NMAX>
+int launch_chain(const ChainDesc<NMAX>& c, const ChainArgs* a, const ChainTab* tab,
+                 hipStream_t stream) {
+  const int MT = tile_mt(c.M);
+  hipError_t e = c.dtype == SSL_BF16
+                     ? chain_launch<DT_BF16>(c.sf, c.block_p, MT, a, tab, c.grid, stream)
+                     : chain_launch<DT_F16>(c.sf, c.block_p, MT, a, tab, c.grid, stream);
+  return check_hip(e, "slr chained launch");
+}
+
 
 }  // namespace
 }  // namespace ssl
@@ -530,10 +700,6 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
   return ssl_slr_forward_group(x, ldx, M, m, m_pad, block_p, block_q, dtype, &mb, 1, stream);
 }
 
-// K units (of 32 in_features) per latent chunk in a chained stage after the
-// first: one batch of loads for each of the 8 waves.
-constexpr int kChainLatentUnits = 64;
-
 int64_t ssl_slr_chain_sync_count(int64_t M) {
   if (M <= 0) return 0;
   const int MT = tile_mt(M);
@@ -544,147 +710,41 @@ int ssl_slr_forward_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t d
                           const ssl_slr_stage* stages, int32_t n_stages,
                           const ssl_slr_member* members, int32_t n_members, void* stream) {
   clear_error();
-  if (dtype != SSL_BF16 && dtype != SSL_F16)
-    return fail(SSL_ERR_UNSUPPORTED, "chained launches take bf16 or fp16 activations");
-  if (n_stages < 1 || n_stages > SSL_MAX_CHAIN_STAGES || !stages)
-    return fail(SSL_ERR_INVALID, "a chained launch takes 1 to %d stages, got %d",
-                SSL_MAX_CHAIN_STAGES, n_stages);
-  if (n_members < 1 || n_members > kMaxChain || !members)
-    return fail(SSL_ERR_INVALID, "a chained launch takes 1 to %d linears, got %d", kMaxChain,
-                n_members);
-  const int s_format = members[0].s_format;
-  if (s_format == SSL_S_NM24) {
-    if (block_p != kNmBlock || block_q != kNmBlock)
-      return fail(SSL_ERR_UNSUPPORTED, "2:4 blocks are 32x32");
-  } else if (s_format != SSL_S_BSR) {
-    return fail(SSL_ERR_INVALID, "unknown sparse storage format %d", s_format);
-  } else if (block_p != block_q || (block_p != 16 && block_p != 32 && block_p != 64)) {
-    return fail(SSL_ERR_UNSUPPORTED, "chained launches take square blocks of 16, 32 or 64, got %dx%d",
-                block_p, block_q);
-  }
-  if (M < 0) return fail(SSL_ERR_INVALID, "negative size");
-  if (M == 0) return SSL_OK;
-  const int eb = elem_bytes(dtype);
-  const int64_t n_sync = ssl_slr_chain_sync_count(M);
-
-  // stages: contiguous member ranges in order; each later stage reads the
-  // output of one member of an earlier stage, and a member feeds at most one
-  int fed[kMaxChain] = {};
-  int next = 0;
-  for (int s = 0; s < n_stages; ++s) {
-    const ssl_slr_stage& st = stages[s];
-    if (st.first != next || st.count < 1 || st.first + st.count > n_members)
-      return fail(SSL_ERR_INVALID, "stage %d: its members must follow the previous stage's", s);
-    next = st.first + st.count;
-    if (st.m < 1 || st.m_pad % 64 || st.m_pad < st.m)
-      return fail(SSL_ERR_INVALID, "stage %d: m >= 1 and m_pad a multiple of 64 and >= m", s);
-    if (s == 0) {
-      if (st.src != -1) return fail(SSL_ERR_INVALID, "stage 0 reads the launch's input (src -1)");
-      if (!st.x || !aligned(st.x, 16) || st.ldx < st.m || (st.ldx * eb) % 16)
-        return fail(SSL_ERR_INVALID, "x rows must be 16-byte aligned and at least m wide");
-      continue;
-    }
-    if (st.src < 0 || st.src >= st.first)
-      return fail(SSL_ERR_INVALID, "stage %d: src must be a member of an earlier stage", s);
-    const ssl_slr_member& src = members[st.src];
-    if (fed[st.src]++) return fail(SSL_ERR_INVALID, "stage %d: member %d already feeds a stage", s, st.src);
-    if (src.NB * block_p < st.m)
-      return fail(SSL_ERR_INVALID, "stage %d: in_features %lld exceed member %d's %lld outputs", s,
-                  (long long)st.m, st.src, (long long)(src.NB * block_p));
-    if (st.x && st.x != src.y)
-      return fail(SSL_ERR_INVALID, "stage %d: x must be NULL (member %d's output)", s, st.src);
-    if (!st.sync || st.n_sync < n_sync || !aligned(st.sync, 256))
-      return fail(SSL_ERR_WORKSPACE, "stage %d: %lld zeroed sync words needed", s,
-                  (long long)n_sync);
-    if (M * src.ldy * eb > 0x7fffffffLL)
-      return fail(SSL_ERR_UNSUPPORTED, "stage %d: its input is beyond 2 GiB; split the call by tokens", s);
-  }
-  if (next != n_members) return fail(SSL_ERR_INVALID, "every member belongs to one stage");
-
   ChainArgs c{};
-  Layout L[kMaxChain];
-  int64_t wg = 0;
-  int nseg = 0;
-  int MT = tile_mt(M);
-  for (int s = 0; s < n_stages; ++s) {
-    const ssl_slr_stage& st = stages[s];
-    const void* x = s == 0 ? st.x : members[st.src].y;
-    const int64_t ldx = s == 0 ? st.ldx : members[st.src].ldy;
-    int64_t n_stream = 0, rt_tiles = 0, rows = 0;
-    for (int i = st.first; i < st.first + st.count; ++i) {
-      const ssl_slr_member& mb = members[i];
-      const int rc = check_member(i, mb, M, st.m_pad, block_p, block_q, dtype, s_format, &L[i]);
-      if (rc != SSL_OK) return rc;
-      n_stream += (mb.NB > 0 ? mb.n_chunks : 0) * L[i].MG;
-      rt_tiles += (int64_t)L[i].n_rt * L[i].MG;
-      rows += mb.NB;
-    }
-    if (s_format == SSL_S_NM24 ? ssl_nm24_takes_prefill(M, rows, dtype)
-                               : ssl_slr_takes_prefill(M, rows, block_p, block_q, dtype))
-      return fail(SSL_ERR_UNSUPPORTED,
-                  "stage %d: a call of %lld token rows runs the prefill kernels; launch the "
-                  "stages one by one", s, (long long)M);
-    // Stage 0: the K split a grouped launch of its members would take (its
-    // results equal ssl_slr_forward_group's bit for bit). Later stages: K
-    // chunks of at most kChainLatentUnits units, one batch of loads per wave
-    // (its B loads go out before the stage's input is ready), so a latent
-    // over 2048 in_features is final without an exchange of partials:
-    // measured 4-5% per step at 1 and 4 token rows against the standalone
-    // split; the 5461-wide down projection takes three chunks (one chunk of
-    // 350 KB of loads per workgroup took 6.4 µs).
-    int n_kc = 1, ku_chunk = L[st.first].ku_total;
-    if (s == 0) {
-      latent_chunks(L[st.first], n_stream, rt_tiles, &n_kc, &ku_chunk);
-    } else {
-      n_kc = (L[st.first].ku_total + kChainLatentUnits - 1) / kChainLatentUnits;
-      if (n_kc > L[st.first].n_kc_max) n_kc = L[st.first].n_kc_max;
-      if (n_kc < 1) n_kc = 1;
-      ku_chunk = (L[st.first].ku_total + n_kc - 1) / n_kc;
-      n_kc = (L[st.first].ku_total + ku_chunk - 1) / ku_chunk;
-    }
-    // waiters of one token tile: every latent workgroup, then every row
-    // workgroup of the stage's members, numbered in that order
-    int waiters = 0;
-    for (int i = st.first; i < st.first + st.count; ++i) {
-      SlrArgs& a = c.m[i];
-      fill_args(a, members[i], L[i], x, ldx, M, st.m, st.m_pad, n_kc, ku_chunk, dtype, block_p,
-                block_q, s_format);
-      c.seg_start[nseg] = (int)wg;
-      c.seg_member[nseg] = i;
-      c.seg_rows[nseg++] = 0;
-      wg += (int64_t)L[i].n_rt * n_kc * L[i].MG;
-      a.dep_lat_base = waiters;
-      waiters += L[i].n_rt * n_kc;
-    }
-    for (int i = st.first; i < st.first + st.count; ++i) {
-      const ssl_slr_member& mb = members[i];
-      c.seg_start[nseg] = (int)wg;
-      c.seg_member[nseg] = i;
-      c.seg_rows[nseg++] = 1;
-      wg += (mb.NB > 0 ? mb.n_chunks : 0) * L[i].MG;
-      c.m[i].dep_row_base = waiters;
-      waiters += mb.NB > 0 ? (int)mb.n_chunks : 0;
-      if (wg > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
-    }
-    if (s > 0 && waiters > 0) {
-      // the stage waits for its source; the source counts its row tiles
-      for (int i = st.first; i < st.first + st.count; ++i) {
-        c.m[i].dep = st.sync;
-        c.m[i].dep_need = (int)members[st.src].NB;
-        c.m[i].dep_waiters = waiters;
-      }
-      c.m[st.src].done = st.sync;
-      c.m[st.src].done_copies = waiters < kDepCopies ? waiters : kDepCopies;
-    }
-  }
-  c.n_seg = nseg;
-  c.seg_start[nseg] = (int)wg;
-  if (wg == 0) return SSL_OK;
-  const int sf = s_format == SSL_S_NM24 ? SF_NM24 : SF_BSR;
-  hipError_t e = dtype == SSL_BF16
-                     ? chain_launch<DT_BF16>(sf, block_p, MT, c, wg, (hipStream_t)stream)
-                     : chain_launch<DT_F16>(sf, block_p, MT, c, wg, (hipStream_t)stream);
-  return check_hip(e, "slr chained launch");
+  if (int rc = build_chain<kMaxChain>(M, block_p, block_q, dtype, stages, n_stages, members,
+                                      n_members, SSL_MAX_CHAIN_STAGES, &c))
+    return rc;
+  if (c.grid == 0) return SSL_OK;
+  return launch_chain(c, &c, nullptr, (hipStream_t)stream);
+}
+
+int64_t ssl_slr_chain_table_bytes(void) { return (int64_t)sizeof(ChainTab); }
+
+int ssl_slr_chain_table_build(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,
+                              const ssl_slr_stage* stages, int32_t n_stages,
+                              const ssl_slr_member* members, int32_t n_members, void* table,
+                              int64_t table_bytes) {
+  clear_error();
+  if (!table || table_bytes < (int64_t)sizeof(ChainTab) || !aligned(table, 16))
+    return fail(SSL_ERR_WORKSPACE, "a chain table needs %lld bytes, 16-byte aligned",
+                (long long)sizeof(ChainTab));
+  ChainTab* c = (ChainTab*)table;
+  memset(c, 0, sizeof(ChainTab));
+  return build_chain<kMaxChainTab>(M, block_p, block_q, dtype, stages, n_stages, members,
+                                   n_members, kMaxChainTab, c);
+}
+
+int ssl_slr_chain_table_launch(const void* table_host, const void* table_dev, void* stream) {
+  clear_error();
+  if (!table_host || !table_dev || !aligned(table_dev, 16))
+    return fail(SSL_ERR_INVALID, "a chain table launch needs the host table and its device copy "
+                "(16-byte aligned)");
+  const ChainTab& c = *(const ChainTab*)table_host;
+  if (c.grid <= 0) return SSL_OK;
+  if ((c.dtype != SSL_BF16 && c.dtype != SSL_F16) || c.M <= 0 || c.n_seg <= 0 ||
+      c.n_seg > 2 * kMaxChainTab)
+    return fail(SSL_ERR_INVALID, "not a chain table (build it with ssl_slr_chain_table_build)");
+  return launch_chain(c, nullptr, (const ChainTab*)table_dev, (hipStream_t)stream);
 }
 
 }  // extern "C"

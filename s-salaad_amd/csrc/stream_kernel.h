@@ -955,30 +955,36 @@ __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_ke
 // overlap the tail of the stage before it, and the launch pays one kernel
 // boundary instead of one per stage.
 // ---------------------------------------------------------------------------
-constexpr int kMaxChain = 8;  // members of a chained launch
-struct ChainArgs {
-  int n_seg;                         // grid segments, in grid order
-  int seg_start[2 * kMaxChain + 1];  // first workgroup of each segment, then the grid size
-  int seg_member[2 * kMaxChain];     // the member a segment belongs to
-  int seg_rows[2 * kMaxChain];       // 1: its row workgroups, 0: its latent workgroups
-  SlrArgs m[kMaxChain];
+constexpr int kMaxChain = 8;       // members of a chained launch described in its kernel arguments
+constexpr int kMaxChainTab = 256;  // members of one described by a table in device memory
+template <int NMAX>
+struct ChainDesc {
+  // the launch it describes (read by the host when launching from a table)
+  int64_t grid;                 // workgroups
+  int M, block_p, dtype, sf;    // token rows, kernel block width, SSL dtype, SF_*
+  int n_seg;                    // grid segments, in grid order
+  int seg_start[2 * NMAX + 1];  // first workgroup of each segment, then the grid size
+  int seg_member[2 * NMAX];     // the member a segment belongs to
+  int seg_rows[2 * NMAX];       // 1: its row workgroups, 0: its latent workgroups
+  SlrArgs m[NMAX];
 };
+using ChainArgs = ChainDesc<kMaxChain>;
+using ChainTab = ChainDesc<kMaxChainTab>;
 static_assert(sizeof(ChainArgs) <= 4096, "kernel arguments of a chained launch");
 
-template <int DT, int P, int KE, int MT, int UNR, int SF>
-__global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_chain_kernel(
-    ChainArgs c_by_value) {
-  (void)c_by_value;
-  const ChainArgs& g = *(const ChainArgs*)__builtin_amdgcn_kernarg_segment_ptr();
-  constexpr int W = P / 16;
-  constexpr int SLOTS = red_slots<MT, W>();
-  __shared__ f32x4 red[SLOTS * MT * W * kWave];
+template <int DT, int P, int KE, int MT, int UNR, int SF, int NMAX>
+__device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4* red) {
   const int b = blockIdx.x;
-  int k = 0;
-  while (k + 1 < g.n_seg && b >= g.seg_start[k + 1]) ++k;
-  const SlrArgs& a = g.m[g.seg_member[k]];
-  const int lb = b - g.seg_start[k];
-  if (!g.seg_rows[k]) {
+  // the last segment starting at or before b (empty segments share a start)
+  int lo = 0, hi = g.n_seg - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (b >= g.seg_start[mid]) lo = mid;
+    else hi = mid - 1;
+  }
+  const SlrArgs& a = g.m[g.seg_member[lo]];
+  const int lb = b - g.seg_start[lo];
+  if (!g.seg_rows[lo]) {
     if (a.dep) latent_wg<DT, MT, 2>(a, lb, red);
     else latent_wg<DT, MT, 1>(a, lb, red);
     return;
@@ -986,6 +992,28 @@ __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_ch
   const int mg = lb / a.n_chunks, chunk = lb % a.n_chunks;
   if (a.dep) stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 2>(a, chunk, mg, red);
   else stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 1>(a, chunk, mg, red);
+}
+
+template <int DT, int P, int KE, int MT, int UNR, int SF>
+__global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_chain_kernel(
+    ChainArgs c_by_value) {
+  (void)c_by_value;
+  constexpr int W = P / 16;
+  __shared__ f32x4 red[red_slots<MT, W>() * MT * W * kWave];
+  chain_wg<DT, P, KE, MT, UNR, SF, kMaxChain>(
+      *(const ChainArgs*)__builtin_amdgcn_kernarg_segment_ptr(), red);
+}
+
+// The same with the descriptor in device memory (many stages, e.g. every
+// layer of a model in one launch). Read through the constant address space,
+// as kernel arguments are: scalar loads of uniform words.
+typedef const __attribute__((address_space(4))) ChainTab* ChainTabPtr;
+template <int DT, int P, int KE, int MT, int UNR, int SF>
+__global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_chain_tab_kernel(
+    ChainTabPtr tab) {
+  constexpr int W = P / 16;
+  __shared__ f32x4 red[red_slots<MT, W>() * MT * W * kWave];
+  chain_wg<DT, P, KE, MT, UNR, SF, kMaxChainTab>(*(const ChainTab*)tab, red);
 }
 
 // Slabs per wave per batch. The byte budget of the square-block kernels
@@ -1020,26 +1048,33 @@ hipError_t stream_launch_one(const GroupArgs& a, int64_t blocks, hipStream_t s) 
 
 // One chained launch for a 16-bit dtype; defined in stream_{bf16,f16}.hip.
 // Square blocks of 16, 32 or 64 (KE 4, 8, 8) or 2:4 blocks; MT ∈ {1, 2, 4}.
+// `a` is the descriptor in kernel arguments, or else `tab` one in device memory.
 template <int DT>
-hipError_t chain_launch(int sf, int P, int MT, const ChainArgs& a, int64_t blocks, hipStream_t s);
+hipError_t chain_launch(int sf, int P, int MT, const ChainArgs* a, const ChainTab* tab,
+                        int64_t blocks, hipStream_t s);
 
 template <int DT, int P, int KE, int MT, int SF>
-hipError_t chain_launch_one(const ChainArgs& a, int64_t blocks, hipStream_t s) {
+hipError_t chain_launch_one(const ChainArgs* a, const ChainTab* tab, int64_t blocks,
+                            hipStream_t s) {
   constexpr int UNR = stream_unroll<DT, P, KE, MT>();
-  hipLaunchKernelGGL((slr_chain_kernel<DT, P, KE, MT, UNR, SF>), dim3((unsigned)blocks), dim3(kST),
-                     0, s, a);
+  if (a)
+    hipLaunchKernelGGL((slr_chain_kernel<DT, P, KE, MT, UNR, SF>), dim3((unsigned)blocks),
+                       dim3(kST), 0, s, *a);
+  else
+    hipLaunchKernelGGL((slr_chain_tab_kernel<DT, P, KE, MT, UNR, SF>), dim3((unsigned)blocks),
+                       dim3(kST), 0, s, (ChainTabPtr)tab);
   return hipGetLastError();
 }
 
 template <int DT>
-hipError_t chain_dispatch(int sf, int P, int MT, const ChainArgs& a, int64_t blocks,
-                          hipStream_t s) {
+hipError_t chain_dispatch(int sf, int P, int MT, const ChainArgs* a, const ChainTab* tab,
+                          int64_t blocks, hipStream_t s) {
   static_assert(DT != DT_F32, "chained launches take 16-bit activations");
 #define SSL_CMT(PP, KK, SS)                                                 \
   switch (MT) {                                                             \
-    case 1: return chain_launch_one<DT, PP, KK, 1, SS>(a, blocks, s);       \
-    case 2: return chain_launch_one<DT, PP, KK, 2, SS>(a, blocks, s);       \
-    case 4: return chain_launch_one<DT, PP, KK, 4, SS>(a, blocks, s);       \
+    case 1: return chain_launch_one<DT, PP, KK, 1, SS>(a, tab, blocks, s);  \
+    case 2: return chain_launch_one<DT, PP, KK, 2, SS>(a, tab, blocks, s);  \
+    case 4: return chain_launch_one<DT, PP, KK, 4, SS>(a, tab, blocks, s);  \
   }                                                                         \
   return hipErrorInvalidValue;
   if (sf == SF_NM24) {

@@ -19,7 +19,7 @@ from .addmm_inplace import SUPPORTED_BLOCK_SIZES, bsr_addmm_inplace_, get_tuned_
 from .artifact import dense_to_bsr, encode_for_kernels, factor_from_svd
 from .bundle import build_efficient_model, load_artifact, save_artifact
 from .decode import DecodeEngine, generate
-from .ls_linear import LRSLinear, LRSLinearChain, LRSLinearGroup
+from .ls_linear import LRSLinear, LRSLinearChain, LRSLinearGroup, PreparedChain
 from .project import block_topk, project_S, project_S_nm, project_nm
 
 __all__ = [
@@ -27,6 +27,7 @@ __all__ = [
     "LRSLinear",
     "LRSLinearChain",
     "LRSLinearGroup",
+    "PreparedChain",
     "SUPPORTED_BLOCK_SIZES",
     "block_topk",
     "build_efficient_model",

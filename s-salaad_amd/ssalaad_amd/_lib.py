@@ -169,6 +169,13 @@ class SlrStage(ctypes.Structure):
 
 
 _SIGNATURES["ssl_slr_chain_sync_count"] = (_c_i64, [_c_i64])
+_SIGNATURES["ssl_slr_chain_table_bytes"] = (_c_i64, [])
+_SIGNATURES["ssl_slr_chain_table_build"] = (
+    ctypes.c_int,
+    [_c_i64, _c_i32, _c_i32, _c_i32, ctypes.POINTER(SlrStage), _c_i32, ctypes.POINTER(SlrMember),
+     _c_i32, _c_p, _c_i64],
+)
+_SIGNATURES["ssl_slr_chain_table_launch"] = (ctypes.c_int, [_c_p, _c_p, _c_p])
 _SIGNATURES["ssl_slr_forward_chain"] = (
     ctypes.c_int,
     [_c_i64, _c_i32, _c_i32, _c_i32, ctypes.POINTER(SlrStage), _c_i32, ctypes.POINTER(SlrMember),
@@ -178,6 +185,7 @@ _SIGNATURES["ssl_slr_forward_chain"] = (
 MAX_GROUP = 4
 MAX_CHAIN = 8
 MAX_CHAIN_STAGES = 4
+MAX_CHAIN_TABLE = 256
 
 _lib = None
 

@@ -575,6 +575,10 @@ class LRSLinearChain(nn.Module):
     a stage's workgroups load their weights while the stage before it
     finishes, and wait for its output inside the launch instead of at a kernel
     boundary. Other calls run the stages as grouped launches one after another.
+    Up to 4 stages of up to 8 linears in all travel in the kernel arguments;
+    longer chains (every layer of a model, up to 256 linears) use a descriptor
+    table in device memory, uploaded on each call, and `prepare` builds one
+    once for fixed buffers (graph capture, static decode loops).
     The reference calls every module on its own (ssalaad/efficient/model.py:41-57).
     """
 
@@ -582,13 +586,15 @@ class LRSLinearChain(nn.Module):
         super().__init__()
         stages = [list(st) for st in stages]
         sources = list(sources)
-        if not 1 <= len(stages) <= _lib.MAX_CHAIN_STAGES:
-            raise ValueError(f"a chain takes 1 to {_lib.MAX_CHAIN_STAGES} stages, got {len(stages)}")
+        if not stages:
+            raise ValueError("a chain takes at least one stage")
         if len(sources) != len(stages) - 1:
             raise ValueError("every stage after the first needs one source module")
         n = sum(len(st) for st in stages)
-        if not 1 <= n <= _lib.MAX_CHAIN:
-            raise ValueError(f"a chain takes 1 to {_lib.MAX_CHAIN} linears, got {n}")
+        if not 1 <= n <= _lib.MAX_CHAIN_TABLE:
+            raise ValueError(f"a chain takes 1 to {_lib.MAX_CHAIN_TABLE} linears, got {n}")
+        if any(len(st) > _lib.MAX_GROUP for st in stages):
+            raise ValueError(f"a stage takes 1 to {_lib.MAX_GROUP} linears")
         self.groups = nn.ModuleList(LRSLinearGroup(*st) for st in stages)
         first = stages[0][0]
         flat = [mod for st in stages for mod in st]
@@ -613,6 +619,38 @@ class LRSLinearChain(nn.Module):
                                  f"writes {src.out_features}")
             self._src.append(hit[0])
         self.in_features = first.in_features
+        self._table_dev: torch.Tensor | None = None
+
+    def _descriptors(self, states, x2: torch.Tensor, ys: list[torch.Tensor], M: int):
+        """The C-ABI member and stage descriptors of a chained call writing ys."""
+        lib = _lib.load()
+        flat = [st for sts in states for st in sts]
+        n_sync = int(lib.ssl_slr_chain_sync_count(M))
+        # the stage words start 256-byte aligned (64 int32 of slack)
+        members, sync = _members(flat, ys, M, 0, extra_counters=n_sync * (len(states) - 1) + 64)
+        sync = (sync + 255) // 256 * 256
+        stages = (_lib.SlrStage * len(states))()
+        base = [0]
+        for sts in states:
+            base.append(base[-1] + len(sts))
+        for s, sts in enumerate(states):
+            sg = stages[s]
+            sg.m, sg.m_pad = sts[0].m, sts[0].m_pad
+            sg.first, sg.count = base[s], len(sts)
+            if s == 0:
+                sg.x, sg.ldx, sg.src = x2.data_ptr(), x2.stride(0), -1
+            else:
+                si, mi = self._src[s - 1]
+                sg.src = base[si] + mi
+                sg.sync, sg.n_sync = sync + 4 * n_sync * (s - 1), n_sync
+        return members, stages, base
+
+    def prepare(self, x: torch.Tensor) -> "PreparedChain":
+        """The chain over the fixed input buffer `x`: its descriptor table is
+        built and uploaded once, and every PreparedChain.run() recomputes every
+        output from what x holds then, into the same output tensors (a decode
+        loop with static buffers, or a HIP graph capture of run())."""
+        return PreparedChain(self, x)
 
     def _chained(self, states, M: int) -> bool:
         st0 = states[0][0]
@@ -642,29 +680,92 @@ class LRSLinearChain(nn.Module):
                 xin = x if s == 0 else outs[self._src[s - 1][0]][self._src[s - 1][1]]
                 outs.append(_launch(sts, xin, outf[s]))
             return tuple(tuple(o) for o in outs)
-        lib = _lib.load()
         flat = [st for sts in states for st in sts]
         ys = [torch.empty(M, st.n_pad, dtype=x.dtype, device=x.device) for st in flat]
-        n_sync = int(lib.ssl_slr_chain_sync_count(M))
-        # the stage words start 256-byte aligned (64 int32 of slack)
-        members, sync = _members(flat, ys, M, 0, extra_counters=n_sync * (len(states) - 1) + 64)
-        sync = (sync + 255) // 256 * 256
-        stages = (_lib.SlrStage * len(states))()
-        base = [0]
-        for sts in states:
-            base.append(base[-1] + len(sts))
-        for s, sts in enumerate(states):
-            sg = stages[s]
-            sg.m, sg.m_pad = sts[0].m, sts[0].m_pad
-            sg.first, sg.count = base[s], len(sts)
-            if s == 0:
-                sg.x, sg.ldx, sg.src = x2.data_ptr(), x2.stride(0), -1
-            else:
-                si, mi = self._src[s - 1]
-                sg.src = base[si] + mi
-                sg.sync, sg.n_sync = sync + 4 * n_sync * (s - 1), n_sync
-        rc = lib.ssl_slr_forward_chain(M, st0.p, st0.q, st0.dtype_code, stages, len(states),
-                                       members, len(flat), _lib.stream_ptr(x.device))
-        _lib.check(rc, "ssl_slr_forward_chain")
+        members, stages, base = self._descriptors(states, x2, ys, M)
+        lib = _lib.load()
+        st0 = states[0][0]
+        if len(states) <= _lib.MAX_CHAIN_STAGES and len(flat) <= _lib.MAX_CHAIN:
+            rc = lib.ssl_slr_forward_chain(M, st0.p, st0.q, st0.dtype_code, stages, len(states),
+                                           members, len(flat), _lib.stream_ptr(x.device))
+            _lib.check(rc, "ssl_slr_forward_chain")
+        else:
+            host = _ChainTable(x.device)
+            host.build(M, st0, stages, len(states), members, len(flat))
+            dev = self._table_dev
+            if dev is None or dev.device != x.device or dev.numel() < host.nbytes:
+                dev = self._table_dev = torch.empty(host.nbytes, dtype=torch.uint8, device=x.device)
+            dev.copy_(host.array)  # from pageable memory: ordered before the launch
+            host.launch(dev, x.device)
         outs = _outputs(flat, ys, [n for o in outf for n in o], tuple(lead))
         return tuple(tuple(outs[base[s]:base[s + 1]]) for s in range(len(states)))
+
+
+class _ChainTable:
+    """A chained launch's descriptor table in (16-byte aligned) host memory."""
+
+    def __init__(self, device: torch.device) -> None:
+        lib = _lib.load()
+        self.nbytes = int(lib.ssl_slr_chain_table_bytes())
+        self._buf = np.zeros(self.nbytes + 16, dtype=np.uint8)
+        off = (-self._buf.ctypes.data) % 16
+        self._np = self._buf[off:off + self.nbytes]
+        self.array = torch.from_numpy(self._np)
+        self.device = device
+
+    def build(self, M, st0, stages, n_stages, members, n_members) -> None:
+        rc = _lib.load().ssl_slr_chain_table_build(M, st0.p, st0.q, st0.dtype_code, stages,
+                                                   n_stages, members, n_members,
+                                                   self._np.ctypes.data, self.nbytes)
+        _lib.check(rc, "ssl_slr_chain_table_build")
+
+    def launch(self, dev: torch.Tensor, device: torch.device) -> None:
+        rc = _lib.load().ssl_slr_chain_table_launch(self._np.ctypes.data, dev.data_ptr(),
+                                                    _lib.stream_ptr(device))
+        _lib.check(rc, "ssl_slr_chain_table_launch")
+
+
+class PreparedChain:
+    """An LRSLinearChain bound to a fixed input buffer and its own output
+    buffers, with its descriptor table built and in device memory: run()
+    launches the whole chain (one launch, whatever its number of stages) and
+    returns the outputs, stage by stage, as the chain's forward would. Each
+    run() overwrites the outputs of the previous one. The buffers' contents
+    may change between runs; their addresses may not. The table holds the
+    kernel views of the weights as prepare() found them: after a module's
+    weights change, prepare again (run(check=True) raises if they did)."""
+
+    def __init__(self, chain: LRSLinearChain, x: torch.Tensor) -> None:
+        first = chain.groups[0].members[0]
+        if x.dtype != first.A.dtype or x.device != first.A.device:
+            raise ValueError("x must have the weights' dtype and device")
+        if x.dim() != 2 or x.shape[-1] != chain.in_features:
+            raise ValueError(f"x must be [M, {chain.in_features}]")
+        if x.stride(-1) != 1 or x.data_ptr() % 16 or (x.stride(0) * x.element_size()) % 16:
+            raise ValueError("x rows must be contiguous and 16-byte aligned")
+        states = [[mod._kernel() for mod in grp.members] for grp in chain.groups]
+        M = x.shape[0]
+        if not chain._chained(states, M):
+            raise ValueError(f"calls of {M} token rows run the stages one by one; prepare serves "
+                             "the chained launch (decode sizes, 16-bit activations)")
+        self.x = x
+        self._keys = [[st.key for st in sts] for sts in states]
+        self._chain = chain
+        flat = [st for sts in states for st in sts]
+        self._ys = [torch.empty(M, st.n_pad, dtype=x.dtype, device=x.device) for st in flat]
+        members, stages, base = chain._descriptors(states, x, self._ys, M)
+        self._host = _ChainTable(x.device)
+        self._host.build(M, states[0][0], stages, len(states), members, len(flat))
+        self._dev = self._host.array.to(x.device)
+        outf = [[mod.out_features for mod in grp.members] for grp in chain.groups]
+        outs = _outputs(flat, self._ys, [n for o in outf for n in o], (M,))
+        self.outputs = tuple(tuple(outs[base[s]:base[s + 1]]) for s in range(len(states)))
+        self.n_stages, self.n_linears = len(states), len(flat)
+
+    def run(self, check: bool = False) -> tuple[tuple[torch.Tensor, ...], ...]:
+        if check:
+            keys = [[mod._weights_key() for mod in grp.members] for grp in self._chain.groups]
+            if keys != self._keys:
+                raise RuntimeError("the chain's weights changed since prepare(); prepare it again")
+        self._host.launch(self._dev, self.x.device)
+        return self.outputs

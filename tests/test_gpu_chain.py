@@ -255,3 +255,92 @@ def test_chain_rejects_bad_stages(gpu_device):
     with pytest.raises(ValueError):  # q already feeds o
         ssalaad_amd.LRSLinearChain([[mods["q"]], [mods["o"]], [mods["k"]]],
                                    sources=[mods["q"], mods["q"]])
+
+
+# ------------------------------------------ many stages: descriptor table --
+
+
+def _stack(layers):
+    """Every layer's four stages in one chain; layer l's q,k,v read layer l-1's
+    down output."""
+    stages, sources = [], []
+    for li, mods in enumerate(layers):
+        if li > 0:
+            sources.append(layers[li - 1]["down"])
+        stages += [[mods["q"], mods["k"], mods["v"]], [mods["o"]], [mods["gate"], mods["up"]],
+                   [mods["down"]]]
+        sources += [mods["q"], mods["o"], mods["gate"]]
+    return ssalaad_amd.LRSLinearChain(stages, sources)
+
+
+@pytest.mark.parametrize("M", [1, 16, 40])
+def test_stack_of_layers_in_one_launch(M, gpu_device):
+    """Three layers (12 stages, 21 linears) in one launch with the descriptor
+    table: every linear against the oracle on the input it read; forward (table
+    uploaded per call) and a prepared chain agree bit for bit; repeated runs
+    agree; the stage words net to zero."""
+    dtype = torch.bfloat16
+    layers = [_layer(256, 688, 64, 32, dtype, gpu_device, seed=300 + 10 * li, pad=True)
+              for li in range(3)]
+    chain = _stack([mods for _, mods in layers])
+    x = to_dev(make_x(layers[0][0]["q"], M), dtype, gpu_device)
+    ys = _flat(chain(x))
+    assert len(ys) == 21
+    x_p = x.clone()
+    prep = chain.prepare(x_p)
+    ys_p = _flat(prep.run(check=True))
+    ys_p2 = [y.clone() for y in ys_p]
+    _flat(prep.run())
+    torch.cuda.synchronize()
+    for i, (a, b, c) in enumerate(zip(ys, ys_p2, ys_p)):
+        assert torch.equal(a, b) and torch.equal(b, c), i
+    xin = x
+    for li, (probs, _) in enumerate(layers):
+        part = ys[7 * li:7 * li + 7]
+        _check_against_oracle(probs, xin, part, dtype)
+        xin = part[-1]
+    q, k, v = ssalaad_amd.LRSLinearGroup(*[layers[0][1][n] for n in ("q", "k", "v")])(x)
+    torch.cuda.synchronize()
+    assert torch.equal(ys[0], q) and torch.equal(ys[1], k) and torch.equal(ys[2], v)
+    assert latent_wait_status(gpu_device) == 0
+    assert _words_at_rest(gpu_device)
+
+
+def test_prepared_stack_graph_replays(gpu_device):
+    """A prepared two-layer stack captured in a HIP graph and replayed with new
+    input contents: every replay equals the chain's forward on that input."""
+    dtype = torch.bfloat16
+    layers = [_layer(256, 512, 64, 32, dtype, gpu_device, seed=400 + 10 * li) for li in range(2)]
+    chain = _stack([mods for _, mods in layers])
+    M = 16
+    x_static = to_dev(make_x(layers[0][0]["q"], M, seed=0), dtype, gpu_device)
+    prep = chain.prepare(x_static)
+    s = torch.cuda.Stream(gpu_device)
+    s.wait_stream(torch.cuda.current_stream(gpu_device))
+    with torch.cuda.stream(s):
+        prep.run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            outs = _flat(prep.run())
+    torch.cuda.synchronize()
+    for rep in range(3):
+        x_new = to_dev(make_x(layers[0][0]["q"], M, seed=rep + 1), dtype, gpu_device)
+        x_static.copy_(x_new)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        want = _flat(chain(x_new))
+        torch.cuda.synchronize()
+        for i, (y, w) in enumerate(zip(outs, want)):
+            assert torch.equal(y, w), (rep, i)
+    assert _words_at_rest(gpu_device)
+
+
+def test_prepare_rejects_prefill_sized_calls(gpu_device):
+    dtype = torch.bfloat16
+    probs, mods = _layer(256, 512, 64, 32, dtype, gpu_device, seed=12)
+    x = to_dev(make_x(probs["q"], 600), dtype, gpu_device)
+    with pytest.raises(ValueError):
+        _chain(mods).prepare(x)
