@@ -737,7 +737,7 @@ def measured_traffic():
     summary (FETCH_SIZE + WRITE_SIZE per dispatch, calibrated on a plain copy)
     and the source revision the counters were measured at; None when absent."""
     out = {"bytes": None, "revision": None}
-    path = ROOT / "profiles" / "slr_kernel_llama1b_decode_counters.md"
+    path = ROOT / "profiles" / "slr_chain_kernel_llama1b_decode_counters.md"
     if not path.exists():
         return out
     for line in path.read_text().splitlines():
@@ -922,7 +922,8 @@ def main():
         _log("[bench] CPU baseline leg")
         cpu = run_cpu(args)
         _log(f"[bench] CPU: {cpu['value']:.1f} tok/s on {cpu['cores']} cores ({cpu['kind']})")
-    traffic = measured_traffic()
+    # the counters were measured for the default launch mode's kernel
+    traffic = measured_traffic() if g["mode"] == "chain" else {"bytes": None, "revision": None}
     line = {
         "metric": METRIC,
         "value": round(g["tok_s"], 1),
