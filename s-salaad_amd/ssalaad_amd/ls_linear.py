@@ -121,8 +121,13 @@ class _KernelState:
         out[: t.shape[0], : t.shape[1]] = t
         return out
 
-    def plan(self, M: int) -> _runtime.DevicePlan:
-        key = 0 if M > 64 else 1
+    def plan(self, M: int, launch: tuple[int, int] | None = None) -> _runtime.DevicePlan:
+        """The work plan for calls of M token rows; `launch` = (block-rows, 16-rank
+        latent tiles) of every linear sharing the launch (None: this one alone),
+        which the 2:4 row split budgets the free workgroup slots against."""
+        if launch is None:
+            launch = (self.NB, self.r_pad // 16)
+        key = (0 if M > 64 else 1, launch if self.s_format == 1 else None)
         pl = self._plans.get(key)
         if pl is None:
             total = self.nblk_total * self.block_q + self.NB * self.lr_units * 32
@@ -131,7 +136,7 @@ class _KernelState:
             # a skewed structure whose longest row the default target leaves whole
             skewed = (costs.size > 0 and costs.max() > _runtime._BALANCE_SKEW * costs.mean()
                       and (target == 0 or costs.max() <= target))
-            if key == 1 and self.s_format == 0 and (self.p in _runtime._BALANCE_P or skewed):
+            if key[0] == 1 and self.s_format == 0 and (self.p in _runtime._BALANCE_P or skewed):
                 # split the longest rows into the workgroup slots left free
                 n_cu = torch.cuda.get_device_properties(self.device).multi_processor_count
                 per_cu = 2 if (self.p <= 32 and self.elem == 2) else 1
@@ -140,15 +145,17 @@ class _KernelState:
                 if bal:
                     target = min(target, bal) if target else bal
             n_split = 0
-            if key == 1 and self.s_format == 1 and self.lr_units > 0:
+            if key[0] == 1 and self.s_format == 1 and self.lr_units > 0:
                 # 2:4 rows are all alike: split the last rows in two, as many as
                 # the free slots take (the balancing budget above), when that
                 # is at most half of them (7B FFN at one token tile: 344 rows,
-                # 104 split; 24.5 -> 22.0 µs)
+                # 104 split; 24.5 -> 22.0 µs). The slots are those the whole
+                # launch leaves free; this linear takes its share of them.
                 n_cu = torch.cuda.get_device_properties(self.device).multi_processor_count
-                free = (n_cu * 2 - _runtime._BALANCE_LATENT_MIN * (self.r_pad // 16)) - self.NB
-                if 0 < free <= self.NB // 2:
-                    n_split = free
+                rows, lat_tiles = launch
+                free = (n_cu * 2 - _runtime._BALANCE_LATENT_MIN * lat_tiles) - rows
+                if 0 < free <= rows // 2:
+                    n_split = free * self.NB // rows
             if n_split:
                 table, n_chunks, n_slots = _runtime.partial_split_plan(
                     self.crow_h, self.col_h, self.NBK, self.block_q, self.lr_units, n_split)
@@ -204,15 +211,31 @@ class _KernelState:
         return _launch([self], x, [out_features])[0]
 
 
+def _launch_shares(states, stages) -> list[tuple[int, int] | None]:
+    """Per state: (block-rows, latent tiles) of the launch it shares (its stage
+    of `stages` member counts, or all of `states` when stages is None), or None
+    for a linear alone."""
+    counts = stages if stages is not None else [len(states)]
+    out, i = [], 0
+    for n in counts:
+        part = states[i:i + n]
+        share = (sum(st.NB for st in part), sum(st.r_pad // 16 for st in part)) if n > 1 else None
+        out += [share] * n
+        i += n
+    return out
+
+
 def _members(states: list["_KernelState"], ys: list[torch.Tensor], M: int, G: int,
-             extra_counters: int = 0):
+             extra_counters: int = 0, stages: list[int] | None = None):
     """The C-ABI member descriptors of a fused call of M token rows writing
     `ys`, with workspaces and zero-at-rest counters from the stream's pools;
     `extra_counters` more int32 counters follow the members' (their address is
-    returned too)."""
+    returned too). `stages`: member counts of a chained launch's stages."""
     lib = _lib.load()
     dev = ys[0].device
-    plans = [st.plan(M) for st in states]
+    # the 2:4 row split budgets the slots of each launch (a grouped launch, or a
+    # chained launch's stage) as a whole
+    plans = [st.plan(M, launch) for st, launch in zip(states, _launch_shares(states, stages))]
     ws_need = [_round_up(lib.ssl_slr_workspace_size(M, st.NB, st.p, st.r_pad, st.m_pad,
                                                     pl.n_slots, st.dtype_code), 256)
                for st, pl in zip(states, plans)]
@@ -627,7 +650,8 @@ class LRSLinearChain(nn.Module):
         flat = [st for sts in states for st in sts]
         n_sync = int(lib.ssl_slr_chain_sync_count(M))
         # the stage words start 256-byte aligned (64 int32 of slack)
-        members, sync = _members(flat, ys, M, 0, extra_counters=n_sync * (len(states) - 1) + 64)
+        members, sync = _members(flat, ys, M, 0, extra_counters=n_sync * (len(states) - 1) + 64,
+                                 stages=[len(sts) for sts in states])
         sync = (sync + 255) // 256 * 256
         stages = (_lib.SlrStage * len(states))()
         base = [0]

@@ -18,7 +18,7 @@ sys.path.insert(0, str(ROOT / "tests" / "golden"))
 
 from golden_inputs import CASES, make_case  # noqa: E402
 from oracle import slr_oracle as orc  # noqa: E402
-from slr_cases import TOL, err, make_problem, make_x, oracle_y, sparse_bsr_tensor, to_dev  # noqa: E402
+from slr_cases import TOL, err, make_problem, make_x, oracle_y, round_to, sparse_bsr_tensor, to_dev  # noqa: E402
 
 import ssalaad_amd  # noqa: E402
 from ssalaad_amd import LRSLinear, _lib, _runtime  # noqa: E402
@@ -694,6 +694,28 @@ def test_nm24_group_and_mixing_rules(gpu_device):
     blk = _module(make_problem(96, 160, 8, 32, 0.5, dtype, seed=3), gpu_device)
     with pytest.raises(ValueError, match="sparse storage"):
         ssalaad_amd.LRSLinearGroup(mods[0], blk)
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_nm24_llama7b_gate_up_group_decode(M, gpu_device):
+    """The 7B gate and up projections with 2:4 S in one grouped launch: the row
+    split budgets the slots the whole launch leaves free (none here: 688
+    block-rows for 512 slots), and both outputs match the oracle."""
+    dtype = torch.bfloat16
+    pairs = [_nm_module(11008, 4096, 256, dtype, gpu_device, seed=41 + i, bias=False) for i in range(2)]
+    grp = ssalaad_amd.LRSLinearGroup(*[m for m, _ in pairs])
+    x = round_to(np.random.default_rng(M).standard_normal((M, 4096)), dtype)
+    ys = grp(to_dev(x, dtype, gpu_device))
+    torch.cuda.synchronize()
+    states = [m._kernel() for m, _ in pairs]
+    share = (sum(st.NB for st in states), sum(st.r_pad // 16 for st in states))
+    for st in states:
+        pl = st.plan(M, share)
+        assert pl.n_chunks == st.NB  # no row split inside the group
+    assert states[0].plan(M).n_chunks > states[0].NB  # alone, some rows split
+    for y, (_, (A, B, S, b)) in zip(ys, pairs):
+        assert err(y, orc.slr_linear(x, A, B, S, b)) <= TOL[dtype]
+    assert latent_wait_status(gpu_device) == 0
 
 
 def test_nm24_llama7b_ffn_shape_decode(gpu_device):
