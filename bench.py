@@ -436,26 +436,35 @@ def run_workload(args) -> dict:
 
         M = args.batch if args.batch_set else 1
         mods = []
-        for _ in range(8):
+        for _ in range(8):  # --pair: four (gate, up) pairs in grouped launches
             grp = torch.rand(n, m // 4, 4, generator=gen).argsort(dim=-1).argsort(dim=-1) < 2
             S = (torch.randn(n, m, generator=gen) * 0.02 * grp.reshape(n, m)).to(torch.bfloat16)
             A = (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
             B = (torch.randn(r, m, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
             mods.append(LRSLinear(A, B, S.to(dev), in_features=m, out_features=n, nm_n=2, nm_m=4))
         x = torch.randn(M, m, generator=gen).to(torch.bfloat16).to(dev)
-        sts = [md._kernel() for md in mods]
-        us = _time_calls([lambda st=st: st.forward(x, n) for st in sts], args.steps, args.eager)
         b = 2 * M * (m + n) + 2 * r * (n + m) + 2 * (n * m // 2) + n * m // 8
+        if args.pair:
+            from ssalaad_amd import LRSLinearGroup
+
+            grps = [LRSLinearGroup(mods[2 * i], mods[2 * i + 1]) for i in range(4)]
+            us = _time_calls([lambda g=g: g(x) for g in grps], args.steps, args.eager)
+            b = 2 * b - 2 * M * m  # two projections, one read of x
+        else:
+            sts = [md._kernel() for md in mods]
+            us = _time_calls([lambda st=st: st.forward(x, n) for st in sts], args.steps, args.eager)
         gbs = b / us / 1e3
         return dict(base, metric="SLR-linear decode GB/s (LLaMA-7B FFN projection, 2:4 S)",
                     value=round(gbs, 1), unit="GB/s", ms_per_step=round(us / 1e3, 5), dtype="bf16",
                     config={"workload": "llama7b_ffn_decode_nm24", "n": n, "m": m, "rank": r,
                             "sparsity": "2:4", "batch_tokens": M, "weight_copies": 8,
+                            "linears_per_launch": 2 if args.pair else 1,
                             "parallelism": "single_gpu"},
                     roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                               "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                               "traffic": None, "algorithmic_bytes_per_launch": int(b),
-                              "stored_bytes_per_launch": int(2 * r * (n + m) + (n // 32) * (m // 32) * 1280),
+                              "stored_bytes_per_launch": int((2 if args.pair else 1) * (
+                                  2 * r * (n + m) + (n // 32) * (m // 32) * 1280)),
                               "avg_launch_us": round(us, 3)})
     if args.workload == "llama7b_ffn_prefill":
         M = args.batch if args.batch_set else 2048
@@ -865,6 +874,8 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="launch eagerly instead of replaying a HIP graph (default workload, "
                          "llama7b_ffn_decode and llama7b_ffn_decode_nm24)")
+    ap.add_argument("--pair", action="store_true",
+                    help="llama7b_ffn_decode_nm24: the projections in grouped pairs (gate, up)")
     ap.add_argument("--stack", action="store_true",
                     help="one chained launch for the whole stack instead of one per layer")
     ap.add_argument("--no-chain", action="store_true",
