@@ -87,11 +87,13 @@ bool supported_dtype(int dt) { return dt == SSL_F32 || dt == SSL_BF16 || dt == S
 struct Layout {
   int MT, MG;
   int n_rt, n_kc_max, ku_total;
-  int64_t cnt_total;  // int32 row counters: [MG][NB]
+  int64_t cnt_total;  // int32 counters: row counters [MG][NB], then (prefill) the
+                      // latent tile counters' slots from index pf_cnt
   int64_t n_sync;     // u64 handshake words: status, then (2 + n_rt) per token tile
   int64_t fin_off;    // byte offset in the exchange area of the final-count copies
   int64_t x_total;    // exchange area bytes
-  int64_t t_part, t_final, part_main, pf_cnt, total;
+  int64_t pf_cnt;     // first int32 counter of the prefill latent tile counters
+  int64_t t_part, t_final, part_main, total;  // workspace byte offsets, size
 };
 
 Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, int64_t n_slots,
@@ -104,6 +106,13 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   L.ku_total = (int)(m_pad / KM);
   L.n_kc_max = latent_split_max(M, m_pad);
   L.cnt_total = (int64_t)L.MG * NB;
+  // the prefill kernels' latent tile counters: per kPrefillLatentRows token
+  // rows, kPfCntCopies slots of kPfCntStride int32 (the tiles written, and the
+  // waiters that have passed), zero at rest like the row counters
+  L.pf_cnt = align_up(L.cnt_total, kPfCntStride);
+  if (M >= kPrefillMinM)
+    L.cnt_total = L.pf_cnt + (int64_t)kPfCntCopies * kPfCntStride *
+                                 ((M + kPrefillLatentRows - 1) / kPrefillLatentRows);
   L.n_sync = 1 + (int64_t)L.MG * (2 + L.n_rt);
   L.fin_off = align_up(8 * L.n_sync, 256);
   L.x_total = L.fin_off + (L.n_rt > 0 ? 8LL * L.MG * kFinCopies * kFinSlotWords : 0);
@@ -115,11 +124,6 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   off = align_up(off + (int64_t)elem_bytes(dtype) * rows * r_pad, 256);
   L.part_main = off;
   off = align_up(off + 4 * (int64_t)L.MG * n_slots * (16 * L.MT * p), 256);
-  // the prefill kernels' latent tile counters (one per kPrefillLatentRows rows)
-  L.pf_cnt = off;
-  if (M >= kPrefillMinM)
-    off = align_up(off + 4LL * kPfCntCopies * kPfCntStride *
-                             ((M + kPrefillLatentRows - 1) / kPrefillLatentRows), 256);
   L.total = off;
   return L;
 }
@@ -591,7 +595,7 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
   const bool nm = s_format == SSL_S_NM24;
   if (nm ? ssl_nm24_takes_prefill(M, call_rows, dtype)
          : ssl_slr_takes_prefill(M, call_rows, block_p, block_q, dtype)) {
-    // Many token rows: one launch (after zeroing the latent tile counters)
+    // Many token rows: one launch
     // with the latent GEMM's workgroups first and the row GEMM's after them,
     // over groups of block-rows (2:4: on the structured-sparse MFMA); a row
     // workgroup's low-rank steps wait for its token rows' latent tiles.
@@ -640,7 +644,7 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       pm.groups = mb.pf_groups; pm.steps = mb.pf_steps; pm.n_groups = (int)mb.pf_n_groups;
       pm.B = mb.B; pm.ldb = m_pad;
       pm.t = (char*)mb.workspace + L[i].t_final; pm.ldt = mb.r_pad;
-      pm.tcnt = mb.r_pad > 0 ? (int32_t*)((char*)mb.workspace + L[i].pf_cnt) : nullptr;
+      pm.tcnt = mb.r_pad > 0 ? mb.counters + L[i].pf_cnt : nullptr;
       pm.r_pad = (int)mb.r_pad;
       lat.mb[i] = pm;
       items += mb.pf_n_groups * T;

@@ -15,8 +15,13 @@ constexpr int64_t kPrefillMinM = 128;
 // polls its counter when it reaches its low-rank steps, and workgroups that
 // started together get there together; with one word those polls queue at one
 // memory location.
+// A slot's word 0 counts the latent tiles written for its token tile, word
+// kPfDepartWord the waiters that have passed; the last waiter returns both to
+// zero, so the slots (in the call's zero-at-rest counters) need no clearing
+// between launches.
 constexpr int kPfCntCopies = 4;
 constexpr int kPfCntStride = 128;
+constexpr int kPfDepartWord = 32;
 
 enum : int { PF_OP = 0, PF_FUSED = 1 };
 
@@ -37,8 +42,8 @@ struct PfMember {
   void* t;              // latent [M][r_pad], activation dtype
   int64_t ldt;
   int32_t* tcnt;        // latent tiles written, per latent token tile, in
-                        // kPfCntCopies copies kPfCntStride int32 apart (zeroed
-                        // before the launch; the low-rank steps wait on them)
+                        // kPfCntCopies copies kPfCntStride int32 apart (zero at
+                        // rest; the low-rank steps wait on them)
   int r_pad;
 };
 
@@ -67,8 +72,7 @@ constexpr int kPrefillLatentRows = 64;
 int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus);
 // Token rows per row-kernel workgroup (64, 128 or 256) for that group size.
 int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus, int dtype);
-// The fused SLR linear in one launch (after a small kernel that zeroes the
-// latent tile counters): the latent GEMM's workgroups (`lat`, one per 64-token
+// The fused SLR linear in one launch: the latent GEMM's workgroups (`lat`, one per 64-token
 // × 64-rank tile over all of in_features) first in the grid, then the row
 // GEMM's (`rows`), whose low-rank steps wait for their token rows' latent
 // tiles. dtype: SSL_F32, SSL_BF16 or SSL_F16; P ∈ {16, 32, 64}; G = 64/P.

@@ -402,7 +402,13 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
   };
 
   // ---- wait until the latent tiles of this tile's token rows are written
-  // (rows kernels with low-rank steps; one lane per wave polls, bounded)
+  // (rows kernels with low-rank steps; one lane per wave polls its copy,
+  // bounded). Past each wait the wave counts itself in the slot's departures
+  // (the old value comes back while the low-rank steps run); the last of the
+  // tile's waiters on that copy returns both words to zero at the end.
+  int departed[BM / kPrefillLatentRows];
+#pragma unroll
+  for (int i = 0; i < BM / kPrefillLatentRows; ++i) departed[i] = -1;
   auto wait_latent = [&]() {
     if constexpr (LR) {
       if (lane == 0) {
@@ -420,6 +426,9 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
               break;
             }
           }
+          departed[lt - m0 / lbm] =
+              __hip_atomic_fetch_add(const_cast<int32_t*>(w) + kPfDepartWord, 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
@@ -430,8 +439,8 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
   // `ragged` is set when an x chunk of the step is cut by in_features (those
   // chunks are fixed up once they landed); `xcol` is then this lane's first x
   // column in the step.
-  auto fetch = [&](int u, int k, int rv, int& ragged, int& xcol) -> int {
-    u = min(u, U - 1);
+  auto fetch = [&](int u_in, int k, int rv, int& ragged, int& xcol) -> int {
+    const int u = min(u_in, U - 1);
     int mask;
     const uint32_t la = la0 + (uint32_t)k * kStageBytes, lb = lb0 + (uint32_t)k * kStageBytes;
     if constexpr (KIND == K_LATENT) {
@@ -485,7 +494,9 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
         }
       } else {
         const uint32_t k0b = (uint32_t)((u - n_sp) * KS * EB);  // ranks (K_ROWS_FUSED only)
-        if (u == n_sp) wait_latent();  // before the first load of t
+        // before the first load of t; once (fetches past the end repeat the last
+        // step, which is step n_sp itself when there is one low-rank step)
+        if (u_in == n_sp) wait_latent();
 #pragma unroll
         for (int i = 0; i < IA; ++i) dma16_sc1(tr, at_[i], k0b, la + i * kRowBytes32);
 #pragma unroll
@@ -692,6 +703,23 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
         }
     }
   }
+  if constexpr (LR) {
+    // the last waiter of a latent tile's copy: every latent tile of that copy
+    // has been counted (n_rt) and every waiter has departed (n_groups), so
+    // subtracting both leaves the slot at zero for the next launch (also after
+    // a wait that gave up: the counts still arrive within the launch)
+    if (lane == 0) {
+      const int lt0 = m0 / a.lbm, lt1 = (min(m0 + BM, M) - 1) / a.lbm;
+      for (int lt = lt0; lt <= lt1; ++lt) {
+        if (departed[lt - lt0] == mb.n_groups - 1) {
+          int32_t* w = mb.tcnt + ((int64_t)lt * kPfCntCopies + wid % kPfCntCopies) * kPfCntStride;
+          __hip_atomic_fetch_add(w, -(mb.r_pad / 64), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_add(w + kPfDepartWord, -mb.n_groups, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+  }
 }
 
 // The op's row kernel (no latent): the engine in a kernel of its own.
@@ -737,18 +765,6 @@ void pf_fused(PfArgs rows_by_value, PfArgs lat_by_value) {
   }
 }
 
-// Zero every member's latent tile counters (a fill kernel, so that the pair
-// of launches can be captured in a graph).
-__global__ __launch_bounds__(kPfThreads) void pf_zero_counts(PfArgs lat_by_value) {
-  (void)lat_by_value;
-  const PfArgs& a = *(const PfArgs*)__builtin_amdgcn_kernarg_segment_ptr();
-  const int n_lt = (a.M + a.lbm - 1) / a.lbm * kPfCntCopies;  // counter copies per member
-  for (int i = threadIdx.x; i < a.n * n_lt; i += kPfThreads) {
-    int32_t* c = a.mb[i / n_lt].tcnt;
-    if (c) c[(int64_t)(i % n_lt) * kPfCntStride] = 0;
-  }
-}
-
 // Row-kernel tiles: tall 256 × 64 (waves 4 × 1, 64 × 64 each; 80 KiB of LDS,
 // two workgroups per compute unit), narrow 128 × 64 (waves 2 × 2, 64 × 32
 // each; 48 KiB) and short 64 × 64 (waves 2 × 2, 32 × 32 each), all with two
@@ -782,13 +798,10 @@ hipError_t launch_rows_p(const PfArgs& rows, int P, int G, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-// Latent and rows in one launch (after zeroing the latent tile counters).
+// Latent and rows in one launch.
 template <int DT, int KIND, int P>
 hipError_t launch_fused_p(const PfArgs& rows, const PfArgs& lat, int G, hipStream_t s) {
   if (G * P != 64) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(pf_zero_counts, dim3(1), dim3(kPfThreads), 0, s, lat);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
   const int nlat = (lat.items + kXcds - 1) / kXcds * kXcds;
   const int per_xcd = (rows.items + kXcds - 1) / kXcds;
   const dim3 grid((unsigned)(nlat + per_xcd * kXcds)), blk(kPfThreads);

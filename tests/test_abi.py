@@ -310,12 +310,15 @@ def test_workspace_sizes_are_aligned_and_monotone():
     assert a == 8 * 16 * 256 * 4 + 16 * 256 * 2
     assert b == a + 100 * 16 * 64 * 4
     # 2048 rows: no latent K split (the prefill kernels run the latent in the
-    # row launch, whole), the final latent, the split-row partials, then the
-    # latent tile counters: 4 copies of 512 bytes per 64 rows
-    assert c == 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4 + 32 * 4 * 512
-    # counters: one per (token tile, block-row)
+    # row launch, whole), the final latent and the split-row partials
+    assert c == 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4
+    # counters: one per (token tile, block-row); from 128 rows (the prefill
+    # kernels) then, 128-aligned, 4 slots of 128 per 64 rows: the latent tiles
+    # written and the waiters passed, zero at rest like the row counters
     assert lib.ssl_slr_counter_count(16, 172) == 172
-    assert lib.ssl_slr_counter_count(2048, 172) == 32 * 172
+    assert lib.ssl_slr_counter_count(64, 172) == 172
+    assert lib.ssl_slr_counter_count(2048, 172) == 5504 + 32 * 4 * 128
+    assert lib.ssl_slr_counter_count(256, 172) == 4 * 172 + 80 + 4 * 4 * 128
     # exchange: the plan's uint64 handshake words (status, then per token tile
     # the latent-ready and ticket words and one arrival word per 16-rank
     # tile), 256-byte aligned

@@ -47,6 +47,29 @@ def _group_of(M, rows, p):
     return int(_lib.load().ssl_prefill_group(M, rows, p, p))
 
 
+@pytest.mark.parametrize("r", [40, 64, 130], ids=["r40", "r64", "r130"])
+@pytest.mark.parametrize("mode", MODES, ids=MODE_IDS)
+def test_latent_tile_counters_return_to_zero(r, mode, tile, gpu_device):
+    """The latent tile counters live in the call's zero-at-rest counters: the
+    last waiter of each tile returns them to zero, with no clearing launch.
+    One low-rank step (r_pad 64: fetches past the end repeat the step that
+    waits) must count each wave once; three calls in a row, each exact, and
+    the counters back at zero after each."""
+    from ssalaad_amd import _runtime
+
+    tile(mode)
+    dtype = torch.bfloat16
+    prob = make_problem(10 * 64, 7 * 64, r, 64, 0.5, dtype, seed=r + mode, bias=True)
+    mod = make_module(prob, gpu_device)
+    for M in (200, 333, 128):
+        x_np = make_x(prob, M, seed=M)
+        y = mod(to_dev(x_np, dtype, gpu_device))
+        torch.cuda.synchronize()
+        assert err(y, oracle_y(prob, x_np)) <= TOL[dtype], M
+        assert all(int(buf.abs().max()) == 0 for (idx, _), buf in _runtime._COUNTERS.items()
+                   if idx == gpu_device.index), M
+
+
 @pytest.mark.parametrize("dtype", DT16, ids=["bf16", "f16"])
 @pytest.mark.parametrize("p", [16, 32, 64])
 @pytest.mark.parametrize("mode", MODES, ids=MODE_IDS)
