@@ -398,11 +398,13 @@ int64_t ssl_prefill_min_rows(void) { return kPrefillMinM; }
 
 // Which kernels a fused call with block storage takes. The prefill kernels
 // from kPrefillMinM token rows (fp32: when their grid fills the device),
-// except where the 16-bit streaming kernel (one weight pass per 64-row token tile, the re-reads served
-// by the caches) measured faster on MI355X: blocks of 32×32 or less up to 512
-// rows (LLaMA-1B gate 5461×2048 at 128 / 256 / 512 rows: 34.2 / 41.8 / 65.5 µs
-// prefill, 24.5 / 35.6 / 55.1 streaming), and calls of fewer than 100
-// block-rows up to 128 rows (4096×4096 with 64×64 blocks: 40.7 -> 31.9 µs).
+// except where the 16-bit streaming kernel (one weight pass per 64-row token
+// tile, the re-reads served by the caches) measured faster on MI355X: 16×16
+// blocks up to 512 rows, 32×32 blocks below 512 rows when the call has fewer
+// than 100 block-rows or at most 128 rows (LLaMA-1B down 2048×5461 at 128 / 256 / 384 rows: streaming
+// 38.4 / 51.6 / 53.5 µs, prefill 54.9 / 57.3 / 58.8; its gate 5461×2048, 171
+// block-rows, at 256 / 384 / 512 rows: prefill 29.8 / 33.6 / 34.7, streaming
+// 34.7 / 46.3 / 53.0), and calls of fewer than 100 block-rows up to 128 rows.
 int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q,
                               int32_t dtype) {
   if (M < kPrefillMinM || !prefill_block(block_p, block_q, dtype)) return 0;
@@ -416,7 +418,9 @@ int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_
     const int64_t items = ((M + 127) / 128) * ((n_rows + 64 / block_p - 1) / (64 / block_p));
     return items >= device_cus() ? 1 : 0;
   }
-  if (block_p <= 32 && M <= 512) return 0;
+  if (debug_knobs().prefill_group != 0) return 1;  // a forced row tile (test hook)
+  if (block_p == 16 && M <= 512) return 0;
+  if (block_p == 32 && M < 512 && (M <= kPrefillMinM || n_rows < 100)) return 0;
   if (M <= kPrefillMinM && n_rows < 100) return 0;
   return 1;
 }
@@ -516,7 +520,7 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
     pm.y = out; pm.ldy = ldo; pm.values_pq = values_pq;
     pm.values_bytes = nnz * block_p * block_q * eb;
     pm.groups = pf_groups; pm.steps = pf_steps; pm.n_groups = (int)pf_n_groups;
-    rows.bm = prefill_row_tile(M, n_chunks, pf_group, block_p, device_cus(), dtype);
+    rows.bm = prefill_row_tile(M, n_chunks, pf_group, block_p, device_cus(), dtype, 0);
     const int64_t T = (M + rows.bm - 1) / rows.bm;
     if (pf_n_groups * T > 0x7fffffffLL / 8) return fail(SSL_ERR_INVALID, "grid too large");
     rows.items = (int)(pf_n_groups * T);
@@ -620,7 +624,10 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
     for (int i = 0; i < n_members; ++i)
       if (members[i].NB > 0) total_rows += members[i].n_chunks;
     const int G = prefill_group(M, total_rows, block_p, cus);
-    rows.bm = prefill_row_tile(M, total_rows, G, block_p, cus, dtype);
+    int64_t lat_wgs = 0;
+    for (int i = 0; i < n_members; ++i)
+      if (members[i].NB > 0 && members[i].r_pad > 0) lat_wgs += TL * (members[i].r_pad / 64);
+    rows.bm = prefill_row_tile(M, total_rows, G, block_p, cus, dtype, lat_wgs);
     int64_t items = 0, litems = 0;
     for (int i = 0; i < n_members; ++i) {
       const ssl_slr_member& mb = members[i];

@@ -70,8 +70,10 @@ constexpr int kPrefillLatentRows = 64;
 // 256 × 64 and short 64 × 64; a workgroup owns 64 / p block-rows.
 // Block-rows per row-kernel workgroup (64/p).
 int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus);
-// Token rows per row-kernel workgroup (64, 128 or 256) for that group size.
-int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus, int dtype);
+// Token rows per row-kernel workgroup (64, 128 or 256) for that group size;
+// lat_items: the latent's workgroups in the same launch.
+int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus, int dtype,
+                     int64_t lat_items);
 // The fused SLR linear in one launch: the latent GEMM's workgroups (`lat`, one per 64-token
 // × 64-rank tile over all of in_features) first in the grid, then the row
 // GEMM's (`rows`), whose low-rank steps wait for their token rows' latent

@@ -835,25 +835,34 @@ int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus) {
   return 64 / block_p;
 }
 
-int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus, int dtype) {
+int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus, int dtype,
+                     int64_t lat_items) {
   (void)block_p;
   const int64_t forced = debug_knobs().prefill_group;  // test hook
   if (forced == 1) return 128;
   if (forced == 2) return 256;
   if (forced == 3) return 64;
-  // the tall tile (fewer re-reads of x and of the weights, more MFMA work per
-  // LDS byte) unless it would leave compute units idle that the narrow one
-  // fills: it runs two workgroups per compute unit. fp32 steps are latency
-  // bound (a quarter of the k of a 16-bit step per load round trip): the short
-  // tile when the narrow one gives fewer than two workgroups per compute unit
-  // (LLaMA-60M gate at 2048 rows: 58 -> 50 µs; 16-bit calls gain nothing).
   const int64_t groups = (n_rows + group - 1) / group;
   const int64_t tall = ((M + 255) / 256) * groups, narrow = ((M + 127) / 128) * groups;
+  // fp32 steps are latency bound (a quarter of the k of a 16-bit step per load
+  // round trip): the short tile when the narrow one gives fewer than two
+  // workgroups per compute unit (LLaMA-60M gate at 2048 rows: 58 -> 50 µs).
   if (dtype == SSL_F32 && narrow < 2 * n_cus) return 64;
-  // (at 128 rows or fewer both give one tile per group, and the tall one's
-  // lower half would be rows past M: 7B FFN at 128 rows, 55.6 vs 41.0 µs)
-  if (M <= 128) return 128;
-  return (tall >= 2 * n_cus || tall >= narrow) ? 256 : 128;
+  // A small grid: the short tile (64 × 64), twice the workgroups of the narrow
+  // one (2048×2048 with 32×32 blocks at 256 rows: 26.0 -> 22.7 µs; 4096×4096
+  // with 64×64 at 128 rows: 34.4 -> 31.7 µs).
+  if (narrow < n_cus / 2) return 64;
+  if (M <= 128) return 128;  // one token tile either way; the tall one's lower half past M
+  // Rounds of the whole grid (the latent's workgroups included) at the tile's
+  // workgroups per compute unit, the tall tile (80 KiB of LDS: 2) against the
+  // narrow one (48 KiB: 3); a round of tall workgroups moves 40 KiB a step per
+  // workgroup against 24 and measured about 1.3 narrow rounds. 7B FFN
+  // 11008×4096 at 768 / 1024 rows: narrow 78.8 / 92.9 µs, tall 87.3 / 96.7; at
+  // 1280: tall 103.5, narrow 115.4; 4096×11008 at 1536 rows: tall 123.2, narrow
+  // 169.8 (its narrow grid overflows one round).
+  const int64_t rt = (tall + lat_items + 2 * n_cus - 1) / (2 * n_cus);
+  const int64_t rn = (narrow + lat_items + 3 * n_cus - 1) / (3 * n_cus);
+  return 13 * rt <= 10 * rn ? 256 : 128;
 }
 
 hipError_t prefill_launch_fused(int dtype, int P, int G, const PfArgs& rows, const PfArgs& lat,

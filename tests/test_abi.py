@@ -367,7 +367,8 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     tp = lambda M, rows, p, dt=_lib.SSL_BF16, q=None: lib.ssl_slr_takes_prefill(
         M, rows, p, p if q is None else q, dt)
     assert tp(127, 500, 64) == 0 and tp(128, 172, 64) == 1 and tp(128, 64, 64) == 0
-    assert tp(129, 64, 64) == 1 and tp(512, 500, 32) == 0 and tp(513, 500, 32) == 1
+    assert tp(129, 64, 64) == 1 and tp(512, 500, 32) == 1 and tp(511, 64, 32) == 0
+    assert tp(300, 500, 32) == 1 and tp(128, 500, 32) == 0 and tp(512, 500, 16) == 0
     assert tp(300, 500, 16) == 0 and tp(2048, 64, 32) == 1 and tp(4096, 500, 64, _lib.SSL_F32) == 0
     assert lib.ssl_prefill_group(4096, 172, 64, 64) == 1  # 64 output features per row tile
     # the prefill kernels take square 16/32/64 blocks; other shapes stream
