@@ -403,12 +403,8 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
 
   // ---- wait until the latent tiles of this tile's token rows are written
   // (rows kernels with low-rank steps; one lane per wave polls its copy,
-  // bounded). Past each wait the wave counts itself in the slot's departures
-  // (the old value comes back while the low-rank steps run); the last of the
-  // tile's waiters on that copy returns both words to zero at the end.
-  int departed[BM / kPrefillLatentRows];
-#pragma unroll
-  for (int i = 0; i < BM / kPrefillLatentRows; ++i) departed[i] = -1;
+  // bounded). The wave counts itself in the slot's departures at its end; the
+  // last of the tile's waiters on that copy returns both words to zero.
   auto wait_latent = [&]() {
     if constexpr (LR) {
       if (lane == 0) {
@@ -426,9 +422,6 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
               break;
             }
           }
-          departed[lt - m0 / lbm] =
-              __hip_atomic_fetch_add(const_cast<int32_t*>(w) + kPfDepartWord, 1, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
@@ -704,15 +697,19 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
     }
   }
   if constexpr (LR) {
-    // the last waiter of a latent tile's copy: every latent tile of that copy
-    // has been counted (n_rt) and every waiter has departed (n_groups), so
-    // subtracting both leaves the slot at zero for the next launch (also after
-    // a wait that gave up: the counts still arrive within the launch)
+    // depart; the last waiter of a latent tile's copy: every latent tile of
+    // that copy has been counted (n_rt) and every waiter has departed
+    // (n_groups), so subtracting both leaves the slot at zero for the next
+    // launch (also after a wait that gave up: the counts still arrive within
+    // the launch). Counted here rather than past the wait, so that no returned
+    // value occupies a register through the low-rank steps.
     if (lane == 0) {
       const int lt0 = m0 / a.lbm, lt1 = (min(m0 + BM, M) - 1) / a.lbm;
       for (int lt = lt0; lt <= lt1; ++lt) {
-        if (departed[lt - lt0] == mb.n_groups - 1) {
-          int32_t* w = mb.tcnt + ((int64_t)lt * kPfCntCopies + wid % kPfCntCopies) * kPfCntStride;
+        int32_t* w = mb.tcnt + ((int64_t)lt * kPfCntCopies + wid % kPfCntCopies) * kPfCntStride;
+        const int old = __hip_atomic_fetch_add(w + kPfDepartWord, 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        if (old == mb.n_groups - 1) {
           __hip_atomic_fetch_add(w, -(mb.r_pad / 64), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_fetch_add(w + kPfDepartWord, -mb.n_groups, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
