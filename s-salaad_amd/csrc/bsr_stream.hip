@@ -410,12 +410,13 @@ int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_
   if (M < kPrefillMinM || !prefill_block(block_p, block_q, dtype)) return 0;
   if (dtype == SSL_F32) {
     // fp32 runs 16 times fewer MFMA flops per cycle: the tiled kernels win once
-    // a grid of their narrow (128-row) tiles fills the device; smaller calls
-    // keep the streaming kernel's finer split (LLaMA-60M shapes at 2048 rows:
-    // 512-wide outputs stream, 30-39 µs either way). A forced row tile (test
-    // hook) sends every such call to the tiled kernels.
+    // a grid of their short (64-row) tiles fills the device; smaller calls keep
+    // the streaming kernel's finer split (LLaMA-60M at 2048 rows: 512×512 31.1
+    // tiled vs 34.4 µs streaming, 512×1376 60.0 vs 59.7; the gate 1376×512 at
+    // 1024 rows 31.7 vs 38.5, at 512 rows 25.3 vs 26.1). A forced row tile
+    // (test hook) sends every such call to the tiled kernels.
     if (debug_knobs().prefill_group != 0) return 1;
-    const int64_t items = ((M + 127) / 128) * ((n_rows + 64 / block_p - 1) / (64 / block_p));
+    const int64_t items = ((M + 63) / 64) * ((n_rows + 64 / block_p - 1) / (64 / block_p));
     return items >= device_cus() ? 1 : 0;
   }
   if (debug_knobs().prefill_group != 0) return 1;  // a forced row tile (test hook)

@@ -370,6 +370,11 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     assert tp(129, 64, 64) == 1 and tp(512, 500, 32) == 1 and tp(511, 64, 32) == 0
     assert tp(300, 500, 32) == 1 and tp(128, 500, 32) == 0 and tp(512, 500, 16) == 0
     assert tp(300, 500, 16) == 0 and tp(2048, 64, 32) == 1 and tp(4096, 500, 64, _lib.SSL_F32) == 0
+    # fp32: when the short (64-row) tiles' grid fills the device (LLaMA-60M
+    # 512-wide projections at 2048 rows: 32 token tiles × 8 groups of two
+    # 32-row block-rows)
+    F32 = _lib.SSL_F32
+    assert tp(2048, 16, 32, F32) == 1 and tp(1024, 16, 32, F32) == 0 and tp(1024, 43, 32, F32) == 1
     assert lib.ssl_prefill_group(4096, 172, 64, 64) == 1  # 64 output features per row tile
     # the prefill kernels take square 16/32/64 blocks; other shapes stream
     assert tp(2048, 500, 32, q=64) == 0 and tp(2048, 500, 48) == 0
