@@ -15,7 +15,8 @@ All compute runs in the HIP kernels of libssalaad_amd.so; there is no CPU path.
 from __future__ import annotations
 
 from . import _lib
-from .addmm_inplace import SUPPORTED_BLOCK_SIZES, bsr_addmm_inplace_, get_tuned_config
+from .addmm_inplace import (SUPPORTED_BLOCK_SIZES, bsr_addmm_inplace_, get_tuned_config,
+                            prepare_bsr_addmm)
 from .artifact import dense_to_bsr, encode_for_kernels, factor_from_svd
 from .bundle import build_efficient_model, load_artifact, save_artifact
 from .decode import DecodeEngine, generate
@@ -32,6 +33,7 @@ __all__ = [
     "block_topk",
     "build_efficient_model",
     "bsr_addmm_inplace_",
+    "prepare_bsr_addmm",
     "dense_to_bsr",
     "encode_for_kernels",
     "factor_from_svd",

@@ -18,7 +18,11 @@ The per-structure work plan (which workgroup sums which blocks) is built on the
 host the first time a given crow/col/active_rows triple is seen and cached on the
 crow tensor object (keyed by the tensors' versions); building it validates the structure
 — monotone crow, col within range, active rows ascending — so the kernel never
-reads outside the tensors it is given.
+reads outside the tensors it is given. That first call copies the structure to the
+host (a synchronisation); `prepare_bsr_addmm` does it ahead of time, after which
+calls with that structure, including calls under HIP graph capture, touch only
+the device. A first call under capture raises (a copy to the host cannot be
+captured) instead of failing inside the capture.
 """
 
 from __future__ import annotations
@@ -61,6 +65,12 @@ _PLAN_ATTR = "_ssl_struct_plan"
 
 
 def _validated_host_structure(crow, col, active_rows, nnz_values, NB_K):
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            "the first call with a BSR structure builds its work plan from a host copy of the "
+            "structure, which a HIP graph cannot capture; call "
+            "ssalaad_amd.prepare_bsr_addmm(crow_indices, col_indices, values, active_rows, "
+            "in_features) once before capturing")
     crow_h = crow.detach().to("cpu", torch.int64).numpy()
     col_h = col.detach().to("cpu", torch.int64).numpy()
     act_h = active_rows.detach().to("cpu", torch.int64).numpy()
@@ -79,7 +89,8 @@ def _validated_host_structure(crow, col, active_rows, nnz_values, NB_K):
     return crow_h.astype(np.int32), act_h.astype(np.int32)
 
 
-def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_bytes):
+def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_bytes,
+              prefill=None):
     versions = (crow._version, col._version, active_rows._version, col.data_ptr(),
                 active_rows.data_ptr(), values.shape[0], NB_K)
     sp = getattr(crow, _PLAN_ATTR, None)
@@ -105,7 +116,9 @@ def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_by
     pf = None
     lib = _lib.load()
     dt = _lib.SSL_BF16 if elem_bytes == 2 else _lib.SSL_F32
-    if lib.ssl_bsr_addmm_takes_prefill(M, block_p, block_q, dt) and plan.n_chunks > 0:
+    if prefill is None:
+        prefill = bool(lib.ssl_bsr_addmm_takes_prefill(M, block_p, block_q, dt))
+    if prefill and plan.n_chunks > 0:
         # the prefill kernel's groups list the planned rows (active rows with blocks)
         G = int(lib.ssl_prefill_group(M, plan.n_chunks, block_p, block_q))
         step_cols = int(lib.ssl_prefill_step_cols(dt))
@@ -244,6 +257,55 @@ def bsr_addmm_inplace_(
     _lib.check(rc, "ssl_bsr_addmm_inplace")
     if target is not out_inplace:
         out_inplace.copy_(target)
+
+
+def prepare_bsr_addmm(
+    crow_indices: torch.Tensor,
+    col_indices: torch.Tensor,
+    values: torch.Tensor,
+    active_rows: torch.Tensor,
+    in_features: int,
+) -> None:
+    """Validate a BSR structure and build every per-structure object the op
+    caches for it (the kernels' block view, the decode and many-token work
+    plans, the prefill plan and the (nnz, p, q) copy of the values), so that
+    later calls with these tensors, unchanged, copy nothing to the host and can
+    be captured in a HIP graph. No counterpart in the reference, whose op has no
+    host-side plan. Raises as the op would for a bad structure."""
+    for name, t in (("crow_indices", crow_indices), ("col_indices", col_indices),
+                    ("active_rows", active_rows)):
+        if t.dtype != torch.int32 or t.dim() != 1:
+            raise TypeError(f"{name} must be a 1-D int32 tensor")
+    if values.dim() != 3 or values.dtype not in _TORCH_DTYPES:
+        raise ValueError("values must be (nnz, block_q, block_p) in float16/bfloat16/float32")
+    block_q, block_p = int(values.shape[1]), int(values.shape[2])
+    if block_p % BLOCK_MULTIPLE or block_q % BLOCK_MULTIPLE or block_p == 0 or block_q == 0:
+        raise ValueError(
+            f"The HIP BSR kernel requires block dimensions divisible by {BLOCK_MULTIPLE}, "
+            f"got {block_p}x{block_q}.")
+    if in_features % block_q:
+        raise ValueError(f"in_features={in_features} must be divisible by block_q={block_q}")
+    NB_K = in_features // block_q
+    if values.shape[0] == 0 or active_rows.numel() == 0:
+        _validated_host_structure(crow_indices, col_indices, active_rows, values.shape[0], NB_K)
+        return
+    P, Q = _reblock.kernel_block_shape(block_p, block_q)
+    if (P, Q) != (block_p, block_q):
+        crow_indices, col_indices, values, active_rows = _kernel_view(
+            crow_indices, col_indices, values, active_rows, block_p, block_q, P, Q, NB_K)
+        block_p, block_q, NB_K = P, Q, in_features // Q
+    eb = values.element_size()
+    dt = _lib.dtype_code(values.dtype)
+    lib = _lib.load()
+    can_prefill = bool(lib.ssl_bsr_addmm_takes_prefill(1 << 20, block_p, block_q, dt))
+    with torch.cuda.device(values.device):
+        for M, pf_wanted in ((1, False), (1 << 20, can_prefill)):
+            _, pf = _plan_for(crow_indices, col_indices, active_rows, values, NB_K, block_p,
+                              block_q, M, eb, prefill=pf_wanted)
+            if pf is not None:
+                vals = values if (values.is_contiguous() and values.data_ptr() % 16 == 0) \
+                    else values.contiguous()
+                _values_pq(values, vals)
 
 
 # Same library name, op name and schema as addmm_inplace.py:130-136, in a

@@ -286,6 +286,55 @@ def test_repeated_calls_and_graph_replays_are_bit_identical(gpu_device):
     assert latent_wait_status(gpu_device) == 0
 
 
+@pytest.mark.parametrize("p,q", [(64, 64), (32, 32), (128, 64)])
+def test_prepared_op_is_captured_in_a_graph(p, q, gpu_device):
+    """prepare_bsr_addmm builds the op's per-structure objects ahead of time;
+    calls with that structure at a decode and a prefill size (and a block shape
+    the kernels cut into sub-blocks) are then captured in one HIP graph without
+    a host copy (the op raises if it would make one), and every replay, with
+    eager work between, equals the eager op on the same tensors bit for bit.
+    Calls on copies of the structure size the stream's scratch pools first, so
+    the captured calls see only what prepare_bsr_addmm built."""
+    dtype, dev = torch.bfloat16, gpu_device
+    prob = make_problem(6 * p, 8 * q, 4, p, 0.5, dtype, seed=p + q, q=q)
+    crow32, col32, vt, act = orc.module_buffers(prob["crow"], prob["col"], prob["vals"])
+    crow, col, act_t = (torch.from_numpy(a).to(dev) for a in (crow32, col32, act))
+    vals = to_dev(vt, dtype, dev)
+    ssalaad_amd.prepare_bsr_addmm(crow, col, vals, act_t, prob["m"])
+    rng = np.random.default_rng(p * q)
+    xs = [to_dev(make_x(prob, M, seed=M), dtype, dev) for M in (16, 256)]
+    base = [to_dev(rng.standard_normal((M, prob["n"])), dtype, dev) for M in (16, 256)]
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):  # the stream's pools, through copies of the structure
+        c2, k2, v2, a2 = crow.clone(), col.clone(), vals.clone(), act_t.clone()
+        for b0, x in zip(base, xs):
+            _op(b0.clone(), x, c2, k2, v2, a2)
+    torch.cuda.synchronize()
+    outs = [b.clone() for b in base]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for o, x in zip(outs, xs):
+            _op(o, x, crow, col, vals, act_t)
+    want = [b.clone() for b in base]
+    with torch.cuda.stream(s):
+        for o, x in zip(want, xs):
+            _op(o, x, crow, col, vals, act_t)
+    torch.cuda.synchronize()
+    for w, x, M in zip(want, xs, (16, 256)):
+        ref = orc.bsr_addmm_inplace(base[0 if M == 16 else 1].double().cpu().numpy(),
+                                    x.double().cpu().numpy(), crow32, col32, vt, act)
+        assert err(w, ref) <= TOL[dtype]
+    for _ in range(3):
+        for o, b in zip(outs, base):
+            o.copy_(b)
+        torch.cuda.synchronize()  # eager work between replays
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(o, w) for o, w in zip(outs, want))
+
+
 def test_llama1b_down_proj_ragged_decode(gpu_device):
     """2048×5461 bf16 (in_features not a block multiple), 32×32 blocks, rank 256."""
     prob = make_problem(2048, 5461, 256, 32, 0.5, torch.bfloat16, seed=8, pad=True)

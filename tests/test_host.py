@@ -215,3 +215,17 @@ def test_nm24_prefill_layout_decodes_to_the_same_matrix():
                         D[by * 32 + j, kk + i0] += vals[j, h, 2 * q]
                         D[by * 32 + j, kk + i1] += vals[j, h, 2 * q + 1]
     assert np.array_equal(D[:n, :m], S.float().numpy())
+
+
+def test_first_op_call_under_graph_capture_raises(monkeypatch):
+    """The op's first call with a structure copies it to the host to build the
+    plan; under HIP graph capture it raises instead, naming prepare_bsr_addmm."""
+    import torch
+    from ssalaad_amd import addmm_inplace
+
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    crow = torch.tensor([0, 1], dtype=torch.int32)
+    col = torch.tensor([0], dtype=torch.int32)
+    act = torch.tensor([0], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="prepare_bsr_addmm"):
+        addmm_inplace._validated_host_structure(crow, col, act, 1, 1)
