@@ -68,11 +68,19 @@ const char* ssl_last_error(void);
  *   SSL_DEBUG_WAIT_UNREACHABLE  nonzero: every wait of the fused kernel targets
  *                               a count no launch reaches, so each gives up
  *                               after its polls and reports it.
+ *   SSL_DEBUG_PREFILL_SPLIT     0: the library decides whether a fused
+ *                               prefill call splits its row groups' sparse
+ *                               steps (and its latent's in_features) across
+ *                               workgroups; 1: never; 2 to 4: every fused
+ *                               prefill call splits its row groups in that
+ *                               many parts (when the caller's workspace holds
+ *                               the partial tiles).
  * Not for concurrent use with calls on other threads. */
 typedef enum {
   SSL_DEBUG_PREFILL_TILE = 0,
   SSL_DEBUG_WAIT_POLLS = 1,
-  SSL_DEBUG_WAIT_UNREACHABLE = 2
+  SSL_DEBUG_WAIT_UNREACHABLE = 2,
+  SSL_DEBUG_PREFILL_SPLIT = 3
 } ssl_debug_knob;
 int ssl_debug_set(int32_t knob, int64_t value);
 

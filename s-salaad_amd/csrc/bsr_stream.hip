@@ -93,7 +93,11 @@ struct Layout {
   int64_t fin_off;    // byte offset in the exchange area of the final-count copies
   int64_t x_total;    // exchange area bytes
   int64_t pf_cnt;     // first int32 counter of the prefill latent tile counters
-  int64_t t_part, t_final, part_main, total;  // workspace byte offsets, size
+  int64_t pf_rarrive; // first int32 counter of the prefill row parts' arrivals
+  int64_t t_part, t_final, part_main;  // workspace byte offsets
+  int64_t total_min;  // workspace bytes a call needs
+  int64_t pf_split;   // then (prefill) the partial tiles of split calls
+  int64_t total;      // workspace bytes with them (the size the query reports)
 };
 
 Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, int64_t n_slots,
@@ -110,9 +114,13 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   // rows, kPfCntCopies slots of kPfCntStride int32 (the tiles written, and the
   // waiters that have passed), zero at rest like the row counters
   L.pf_cnt = align_up(L.cnt_total, kPfCntStride);
-  if (M >= kPrefillMinM)
-    L.cnt_total = L.pf_cnt + (int64_t)kPfCntCopies * kPfCntStride *
-                                 ((M + kPrefillLatentRows - 1) / kPrefillLatentRows);
+  L.pf_rarrive = L.pf_cnt;
+  if (M >= kPrefillMinM) {
+    L.pf_rarrive = L.pf_cnt + (int64_t)kPfCntCopies * kPfCntStride *
+                                  ((M + kPrefillLatentRows - 1) / kPrefillLatentRows);
+    // one arrival word per (64-row token tile, block-row) bounds the row parts'
+    L.cnt_total = L.pf_rarrive + ((M + 63) / 64) * NB;
+  }
   L.n_sync = 1 + (int64_t)L.MG * (2 + L.n_rt);
   L.fin_off = align_up(8 * L.n_sync, 256);
   L.x_total = L.fin_off + (L.n_rt > 0 ? 8LL * L.MG * kFinCopies * kFinSlotWords : 0);
@@ -124,7 +132,9 @@ Layout slr_layout(int64_t M, int64_t NB, int p, int64_t r_pad, int64_t m_pad, in
   off = align_up(off + (int64_t)elem_bytes(dtype) * rows * r_pad, 256);
   L.part_main = off;
   off = align_up(off + 4 * (int64_t)L.MG * n_slots * (16 * L.MT * p), 256);
-  L.total = off;
+  L.total_min = off;
+  L.pf_split = off;
+  L.total = align_up(off + prefill_split_bytes(M, NB, p, m_pad, r_pad, dtype, device_cus()), 256);
   return L;
 }
 
@@ -177,9 +187,9 @@ int check_member(int i, const ssl_slr_member& mb, int64_t M, int64_t m_pad, int 
     return fail(SSL_ERR_UNSUPPORTED,
                 "linear %d: workspace of %lld bytes exceeds 2 GiB; split the call by tokens", i,
                 (long long)L->total);
-  if (mb.workspace_bytes < L->total || !mb.workspace)
+  if (mb.workspace_bytes < L->total_min || !mb.workspace)
     return fail(SSL_ERR_WORKSPACE, "linear %d: workspace of %lld bytes needed", i,
-                (long long)L->total);
+                (long long)L->total_min);
   if (!aligned(mb.workspace, 256))
     return fail(SSL_ERR_WORKSPACE, "linear %d: workspace must be 256-byte aligned", i);
   if (mb.n_counters < L->cnt_total || !mb.counters)
@@ -521,6 +531,7 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
     pm.y = out; pm.ldy = ldo; pm.values_pq = values_pq;
     pm.values_bytes = nnz * block_p * block_q * eb;
     pm.groups = pf_groups; pm.steps = pf_steps; pm.n_groups = (int)pf_n_groups;
+    pm.ksplit = 1;  // the op's row kernel runs whole row groups
     rows.bm = prefill_row_tile(M, n_chunks, pf_group, block_p, device_cus(), dtype, 0);
     const int64_t T = (M + rows.bm - 1) / rows.bm;
     if (pf_n_groups * T > 0x7fffffffLL / 8) return fail(SSL_ERR_INVALID, "grid too large");
@@ -558,6 +569,19 @@ int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r
                                int64_t m_pad, int64_t n_slots, int32_t dtype) {
   return slr_layout(M, NB, block_p, r_pad, m_pad, n_slots, dtype).total;
 }
+}  // extern "C"
+
+namespace ssl {
+// The workspace a call cannot do without (ssl_slr_workspace_size adds the room
+// for the partial tiles of split prefill calls, which a smaller workspace
+// forgoes).
+int64_t slr_workspace_min(int64_t M, int64_t NB, int32_t block_p, int64_t r_pad, int64_t m_pad,
+                          int64_t n_slots, int32_t dtype) {
+  return slr_layout(M, NB, block_p, r_pad, m_pad, n_slots, dtype).total_min;
+}
+}  // namespace ssl
+
+extern "C" {
 
 int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int64_t m_pad,
                           int32_t block_p, int32_t block_q, int32_t dtype,
@@ -629,6 +653,25 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
     for (int i = 0; i < n_members; ++i)
       if (members[i].NB > 0 && members[i].r_pad > 0) lat_wgs += TL * (members[i].r_pad / 64);
     rows.bm = prefill_row_tile(M, total_rows, G, block_p, cus, dtype, lat_wgs);
+    // K parts: when the row grid is small (prefill_row_split) and every
+    // member's workspace holds the partial tiles
+    int64_t items0 = 0, sp_steps = 0, n_grp = 0;
+    for (int i = 0; i < n_members; ++i)
+      if (members[i].NB > 0 && members[i].pf_n_groups > 0) {
+        items0 += members[i].pf_n_groups * ((M + rows.bm - 1) / rows.bm);
+        n_grp += members[i].pf_n_groups;
+        sp_steps += members[i].nnz * block_p / ssl_prefill_step_cols(dtype);
+      }
+    int ksplit = prefill_row_split(items0, n_grp > 0 ? sp_steps / n_grp : 0, cus, rows.bm);
+    for (int i = 0; i < n_members && ksplit > 1; ++i) {
+      const ssl_slr_member& mb = members[i];
+      if (mb.NB == 0) continue;
+      const int64_t need = (int64_t)ksplit * mb.pf_n_groups * ((M + rows.bm - 1) / rows.bm) *
+                           rows.bm * 64 * 4;
+      if (mb.workspace_bytes < L[i].total || mb.r_pad / 64 > 64 ||
+          need > prefill_split_bytes(M, mb.NB, block_p, m_pad, 0, dtype, cus))
+        ksplit = 1;
+    }
     int64_t items = 0, litems = 0;
     for (int i = 0; i < n_members; ++i) {
       const ssl_slr_member& mb = members[i];
@@ -654,9 +697,20 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       pm.t = (char*)mb.workspace + L[i].t_final; pm.ldt = mb.r_pad;
       pm.tcnt = mb.r_pad > 0 ? mb.counters + L[i].pf_cnt : nullptr;
       pm.r_pad = (int)mb.r_pad;
+      // the row parts' tiles first in the member's split region, then the latent's
+      const int64_t rows_bytes = prefill_split_bytes(M, mb.NB, block_p, m_pad, 0, dtype, cus);
+      pm.ksplit = ksplit;
+      pm.kchunk = 0;
+      pm.kpart = (float*)((char*)mb.workspace + L[i].pf_split);
+      pm.karrive = mb.counters + L[i].pf_rarrive;
       lat.mb[i] = pm;
-      items += mb.pf_n_groups * T;
-      if (mb.r_pad > 0) litems += TL * (mb.r_pad / 64);
+      const PfLatentSplit ls = ksplit > 1 ? prefill_latent_split(M, m_pad, mb.r_pad, dtype)
+                                          : PfLatentSplit{1, (int)(m_pad / ssl_prefill_step_cols(dtype))};
+      lat.mb[i].ksplit = ls.split;
+      lat.mb[i].kchunk = ls.chunk;
+      lat.mb[i].kpart = (float*)((char*)mb.workspace + L[i].pf_split + rows_bytes);
+      items += mb.pf_n_groups * T * ksplit;
+      if (mb.r_pad > 0) litems += TL * (mb.r_pad / 64) * ls.split;
       if (items > 0x7fffffffLL / 8 || litems > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
     }
     rows.off[n_members] = (int)items;

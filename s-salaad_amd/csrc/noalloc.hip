@@ -81,7 +81,9 @@ int ssl_slr_forward_noalloc(void* y, int64_t ldy, const void* x, int64_t ldx, co
   if (M == 0 || NB == 0) return SSL_OK;
   const int64_t n_cnt = ssl_slr_counter_count(M, NB);
   const int64_t x_bytes = ssl_slr_exchange_size(M, r_pad, m_pad, dtype);
-  const int64_t ws = ssl_slr_workspace_size(M, NB, block_p, r_pad, m_pad, n_slots, dtype);
+  // the workspace the call needs (the room for split prefill calls' partial
+  // tiles is used when the array holds it)
+  const int64_t ws = slr_workspace_min(M, NB, block_p, r_pad, m_pad, n_slots, dtype);
   if (4 * n_cnt > kNoAllocCounterBytes || x_bytes > kNoAllocExchangeBytes ||
       ws > kNoAllocWorkspaceBytes)
     return fail(SSL_ERR_CAPACITY,
@@ -105,7 +107,7 @@ int ssl_slr_forward_noalloc(void* y, int64_t ldy, const void* x, int64_t ldx, co
   if (int rc = check_hip(hipGetLastError(), "scratch clear launch")) return rc;
   return ssl_slr_forward(y, ldy, x, ldx, A, B, bias, col, values, plan, n_chunks, n_slots, lr_wgs,
                          M, m, m_pad, NB, r_pad, block_p, block_q, dtype, counters, n_cnt,
-                         exchange, x_bytes, workspace, ws, stream);
+                         exchange, x_bytes, workspace, kNoAllocWorkspaceBytes, stream);
 }
 
 }  // extern "C"

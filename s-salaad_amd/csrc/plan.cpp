@@ -96,6 +96,10 @@ int ssl_debug_set(int32_t knob, int64_t value) {
     case SSL_DEBUG_WAIT_UNREACHABLE:
       k.wait_unreachable = value != 0;
       return SSL_OK;
+    case SSL_DEBUG_PREFILL_SPLIT:
+      if (value < 0 || value > 4) return fail(SSL_ERR_INVALID, "prefill split override must be 0 to 4");
+      k.prefill_split = value;
+      return SSL_OK;
   }
   return fail(SSL_ERR_INVALID, "unknown debug knob %d", knob);
 }

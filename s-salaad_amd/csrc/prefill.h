@@ -45,6 +45,17 @@ struct PfMember {
                         // kPfCntCopies copies kPfCntStride int32 apart (zero at
                         // rest; the low-rank steps wait on them)
   int r_pad;
+  // K parts (prefill_row_split): rows kernels split a row group's sparse steps
+  // into ksplit parts (the last also takes the low-rank steps), the latent its
+  // in_features into ksplit chunks of kchunk steps; every part stores its fp32
+  // partial tile in kpart and counts itself, and the last to arrive sums the
+  // parts in part order (the same sum whichever arrives last) and goes on.
+  int ksplit, kchunk;
+  float* kpart;         // ksplit > 1: [tile][part][tile elements] fp32
+  int32_t* karrive;     // rows, ksplit > 1: parts arrived per (token tile,
+                        // group), zero at rest (the latent's arrivals use
+                        // words kPfLatArriveWord + rank tile of its tile
+                        // counters' first slot)
 };
 
 struct PfArgs {
@@ -65,6 +76,21 @@ struct PfArgs {
 
 // Token rows per latent tile of the prefill kernels.
 constexpr int kPrefillLatentRows = 64;
+constexpr int kPfLatArriveWord = 64;  // rank tiles ≤ 64 (r_pad ≤ 4096) for a latent split
+
+// K parts of a fused prefill call with few row workgroups: a grid of `items`
+// row workgroups under twice the CUs splits each row group's sparse steps in
+// up to 4 parts (at least 40 steps a part, `steps` the mean
+// per group), and then the latent's in_features too (prefill_latent_split),
+// so neither leaves the other's critical path. 1 = no split.
+int prefill_row_split(int64_t items, int64_t steps, int n_cus, int bm);
+struct PfLatentSplit {
+  int split, chunk;
+};
+PfLatentSplit prefill_latent_split(int64_t M, int64_t m_pad, int64_t r_pad, int dtype);
+// Workspace bytes the partial tiles of both splits may take for a member.
+int64_t prefill_split_bytes(int64_t M, int64_t NB, int block_p, int64_t m_pad, int64_t r_pad,
+                            int dtype, int n_cus);
 
 // Row-kernel tiles (token rows × output features): narrow 128 × 64, tall
 // 256 × 64 and short 64 × 64; a workgroup owns 64 / p block-rows.

@@ -215,6 +215,8 @@ __device__ __forceinline__ int lds_chunk(int R, int kc) { return R * kK + ((kc ^
 // agent-scope add; a row workgroup polls that count (bounded) before its
 // low-rank steps and reads the latent with sc1 loads. No cache-wide fence.
 constexpr int kSc1Policy = 16;
+// fp32 partial tile of a latent K chunk: 64 tokens × 64 ranks
+constexpr int kLatentPartFloats = kPrefillLatentRows * 64;
 __device__ __forceinline__ void st_sc1(const __amdgpu_buffer_rsrc_t& r, int off, float v, int eb,
                                        uint32_t bits16) {
   if (eb == 4) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kSc1Policy);
@@ -290,19 +292,28 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
   int n_sp = 0;                      // sparse steps (rows kernels)
   const int32_t* gr = nullptr;       // group record: {step_begin, step_end, rows[G]}
   int rt = 0;                        // latent: rank tile
+  const int ksplit = mb.ksplit;      // K parts of a tile (1: whole)
+  const int tile = local / ksplit;   // a tile's parts are adjacent items
+  const int kp = local - tile * ksplit;  // this workgroup's part
+  bool has_lr = LR;                  // rows: this part runs the low-rank steps
   if constexpr (KIND == K_LATENT) {
     const int n_rt = mb.r_pad / BN;
-    rt = local % n_rt;
-    m0 = (local / n_rt) * BM;
-    s_begin = 0;
-    s_end = a.m_pad / KS;
+    rt = tile % n_rt;
+    m0 = (tile / n_rt) * BM;
+    s_begin = kp * mb.kchunk;
+    s_end = min(a.m_pad / KS, s_begin + mb.kchunk);
   } else {
-    const int tt = local / mb.n_groups, grp = local % mb.n_groups;
+    const int tt = tile / mb.n_groups, grp = tile % mb.n_groups;
     m0 = tt * BM;
     gr = mb.groups + (int64_t)grp * (2 + G);
-    s_begin = ld_word(gr, 0);
-    n_sp = ld_word(gr, 1) - s_begin;
-    const int n_lr = LR ? mb.r_pad / KS : 0;
+    // part kp of the group's sparse steps; the last part also the low-rank ones
+    const int g0 = ld_word(gr, 0), n_all = ld_word(gr, 1) - g0;
+    const int chunk = (n_all + ksplit - 1) / ksplit;
+    const int b0 = min(kp * chunk, n_all), b1 = min(b0 + chunk, n_all);
+    s_begin = g0 + b0;
+    n_sp = b1 - b0;
+    has_lr = LR && kp == ksplit - 1;
+    const int n_lr = has_lr ? mb.r_pad / KS : 0;
     s_end = s_begin + n_sp + n_lr;
   }
   const int U = s_end - s_begin;
@@ -615,6 +626,87 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
   }
   wait_vmcnt<0>();  // no load may still be writing LDS when the workgroup ends
 
+  auto depart = [&]() {
+    if constexpr (LR) {
+      if (!has_lr) return;  // only the part that ran the low-rank steps waited
+      // depart; the last waiter of a latent tile's copy: every latent tile of
+      // that copy has been counted (n_rt) and every waiter has departed
+      // (n_groups), so subtracting both leaves the slot at zero for the next
+      // launch (also after a wait that gave up: the counts still arrive within
+      // the launch). Counted here rather than past the wait, so that no returned
+      // value occupies a register through the low-rank steps.
+      if (lane == 0) {
+        const int lt0 = m0 / a.lbm, lt1 = (min(m0 + BM, M) - 1) / a.lbm;
+        for (int lt = lt0; lt <= lt1; ++lt) {
+          int32_t* w = mb.tcnt + ((int64_t)lt * kPfCntCopies + wid % kPfCntCopies) * kPfCntStride;
+          const int old = __hip_atomic_fetch_add(w + kPfDepartWord, 1, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+          if (old == mb.n_groups - 1) {
+            __hip_atomic_fetch_add(w, -(mb.r_pad / 64), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(w + kPfDepartWord, -mb.n_groups, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+    }
+  };
+
+  // ---- K parts: this part's fp32 partial tile (each thread's accumulators,
+  // contiguous) stored device-coherently, then counted; the last part to
+  // arrive returns the count to zero, sums every part's tile in part order
+  // into acc and goes on to the epilogue (true); the others are done (false).
+  auto combine = [&](float* base, int32_t* arrive) -> bool {
+    constexpr int TF = MTI * NTI * 4 * kPfThreads;  // floats of a part's tile
+    const __amdgpu_buffer_rsrc_t pr =
+        __builtin_amdgcn_make_buffer_rsrc(base, (short)0, ksplit * TF * 4, 0x00020000);
+#pragma unroll
+    for (int mt = 0; mt < MTI; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTI; ++nt)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mt][nt]), pr,
+                                               ((kp * kPfThreads + tid) * MTI * NTI + mt * NTI + nt) * 16,
+                                               0, kSc1Policy);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores acknowledged
+    __syncthreads();                // (and every wave is past its last LDS read)
+    volatile int32_t* const flag = reinterpret_cast<volatile int32_t*>(&lds[0][0]);
+    if (tid == 0)
+      *flag = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (*flag != ksplit - 1) return false;
+    if (tid == 0) __hip_atomic_fetch_add(arrive, -ksplit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    f32x4 sum[MTI][NTI];
+#pragma unroll
+    for (int mt = 0; mt < MTI; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTI; ++nt) sum[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < ksplit; ++j) {
+#pragma unroll
+      for (int mt = 0; mt < MTI; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTI; ++nt)
+          sum[mt][nt] += (j == kp) ? acc[mt][nt]
+                                   : __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         pr, ((j * kPfThreads + tid) * MTI * NTI + mt * NTI + nt) * 16,
+                                         0, kSc1Policy));
+    }
+#pragma unroll
+    for (int mt = 0; mt < MTI; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NTI; ++nt) acc[mt][nt] = sum[mt][nt];
+    return true;
+  };
+  if constexpr (KIND == K_LATENT) {
+    if (ksplit > 1 &&
+        !combine(mb.kpart + (int64_t)tile * ksplit * kLatentPartFloats,
+                 mb.tcnt + (int64_t)(m0 / BM) * kPfCntCopies * kPfCntStride + kPfLatArriveWord + rt))
+      return;
+  } else if constexpr (BM < 256) {
+    if (ksplit > 1 && !combine(mb.kpart + (int64_t)tile * ksplit * (BM * BN), mb.karrive + tile)) {
+      depart();
+      return;
+    }
+  }
+
   // ---- epilogue: lane (c, gq) holds rows 16·mt + 4gq + e of column 16·nt + c.
   // The output pointers and strides are read into registers first: the
   // stores below could otherwise alias the argument segment and force a
@@ -696,27 +788,7 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
         }
     }
   }
-  if constexpr (LR) {
-    // depart; the last waiter of a latent tile's copy: every latent tile of
-    // that copy has been counted (n_rt) and every waiter has departed
-    // (n_groups), so subtracting both leaves the slot at zero for the next
-    // launch (also after a wait that gave up: the counts still arrive within
-    // the launch). Counted here rather than past the wait, so that no returned
-    // value occupies a register through the low-rank steps.
-    if (lane == 0) {
-      const int lt0 = m0 / a.lbm, lt1 = (min(m0 + BM, M) - 1) / a.lbm;
-      for (int lt = lt0; lt <= lt1; ++lt) {
-        int32_t* w = mb.tcnt + ((int64_t)lt * kPfCntCopies + wid % kPfCntCopies) * kPfCntStride;
-        const int old = __hip_atomic_fetch_add(w + kPfDepartWord, 1, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-        if (old == mb.n_groups - 1) {
-          __hip_atomic_fetch_add(w, -(mb.r_pad / 64), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_fetch_add(w + kPfDepartWord, -mb.n_groups, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-    }
-  }
+  depart();
 }
 
 // The op's row kernel (no latent): the engine in a kernel of its own.
@@ -826,6 +898,60 @@ hipError_t launch_fused(const PfArgs& rows, const PfArgs& lat, int P, int G, hip
 }
 
 }  // namespace
+
+// Parts of fewer steps lose more to the exchange of partial tiles (a store,
+// its acknowledgement, a count, a load: some µs) than they gain: 7B FFN
+// 11008×4096 (32 steps a group) at 256 rows 41.1 µs whole, 53.7 in two parts;
+// 4096×11008 (86 steps) 65.9 whole, 53.3 in two parts, 58.2 in three.
+constexpr int64_t kRowSplitMinSteps = 40;
+int prefill_row_split(int64_t items, int64_t steps, int n_cus, int bm) {
+  if (bm >= 256) return 1;  // the tall tile keeps its registers for its own steps
+  const int64_t forced = debug_knobs().prefill_split;  // test hook
+  if (forced == 1) return 1;
+  if (forced >= 2) return (int)forced;
+  if (items <= 0 || items >= 2 * (int64_t)n_cus) return 1;
+  int64_t k = (2 * (int64_t)n_cus + items - 1) / items;
+  if (k > 4) k = 4;
+  if (k > steps / kRowSplitMinSteps) k = steps / kRowSplitMinSteps;
+  return k < 2 ? 1 : (int)k;
+}
+
+// The latent's K chunks when the rows split: chunks of at least 16 steps, at
+// most 256 latent workgroups in all, at most 16 chunks a tile, at most 64 rank
+// tiles (their arrival words). LLaMA-7B FFN at 256 rows: 16 tiles; 4096
+// in_features (64 steps) in 4 chunks, 11008 (172 steps) in 11.
+PfLatentSplit prefill_latent_split(int64_t M, int64_t m_pad, int64_t r_pad, int dtype) {
+  const int64_t ks = dtype == SSL_F32 ? 32 : 64;  // in_features per step
+  const int64_t steps = m_pad / ks;
+  const int64_t tiles = (M + kPrefillLatentRows - 1) / kPrefillLatentRows * (r_pad / 64);
+  PfLatentSplit r{1, (int)steps};
+  if (tiles <= 0 || steps <= 16 || r_pad / 64 > 64) return r;
+  int64_t n = (steps + 15) / 16;
+  if (n > 256 / tiles) n = 256 / tiles;
+  if (n > 16) n = 16;
+  if (n <= 1) return r;
+  const int64_t chunk = (steps + n - 1) / n;
+  r.split = (int)((steps + chunk - 1) / chunk);
+  r.chunk = (int)chunk;
+  return r;
+}
+
+int64_t prefill_split_bytes(int64_t M, int64_t NB, int block_p, int64_t m_pad, int64_t r_pad,
+                            int dtype, int n_cus) {
+  if (M < kPrefillMinM || NB <= 0) return 0;
+  const int64_t groups = (NB + 64 / block_p - 1) / (64 / block_p);
+  // no split when even the tall tile's grid gives two workgroups per CU
+  if (((M + 255) / 256) * groups >= 2 * (int64_t)n_cus && debug_knobs().prefill_split == 0) return 0;
+  int64_t tiles = 4 * ((M + 63) / 64) * groups;  // part tiles: 4 parts of 64-row tiles at most
+  if (tiles > 4 * (int64_t)n_cus) tiles = 4 * (int64_t)n_cus;  // automatic splits: < 4 CUs' worth
+  const int64_t rows = tiles * 128 * 64 * 4;  // at most 128 × 64 fp32 a part
+  const PfLatentSplit ls = prefill_latent_split(M, m_pad, r_pad, dtype);
+  const int64_t lat = ls.split > 1 ? 4LL * kLatentPartFloats * ls.split *
+                                         ((M + kPrefillLatentRows - 1) / kPrefillLatentRows) *
+                                         (r_pad / 64)
+                                   : 0;
+  return rows + lat;
+}
 
 int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus) {
   (void)M; (void)n_rows; (void)n_cus;

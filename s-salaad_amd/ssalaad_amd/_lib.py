@@ -29,6 +29,7 @@ PLAN_STRIDE = 8
 DEBUG_PREFILL_TILE = 0
 DEBUG_WAIT_POLLS = 1
 DEBUG_WAIT_UNREACHABLE = 2
+DEBUG_PREFILL_SPLIT = 3
 
 _DTYPE_CODE = {torch.float32: SSL_F32, torch.bfloat16: SSL_BF16, torch.float16: SSL_F16}
 

@@ -312,13 +312,22 @@ def test_workspace_sizes_are_aligned_and_monotone():
     # 2048 rows: no latent K split (the prefill kernels run the latent in the
     # row launch, whole), the final latent and the split-row partials
     assert c == 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4
+    # 256 rows of 4096×11008 (64 block-rows): room for the split row groups'
+    # partial tiles (up to 4 parts of 64-row tiles, at most 4 per CU, 128 × 64
+    # fp32 each) and the latent's K chunks (172 steps in 11 chunks of 16, 16
+    # tiles of 64 × 64 fp32); calls whose tall grid fills the device reserve none
+    d = lib.ssl_slr_workspace_size(256, 64, 64, 256, 11008, 0, _lib.SSL_BF16)
+    assert d == 256 * 256 * 2 + 1024 * 128 * 64 * 4 + 11 * 16 * 64 * 64 * 4
+    assert lib.ssl_slr_workspace_size(8192, 64, 64, 256, 4096, 0, _lib.SSL_BF16) == 8192 * 256 * 2
     # counters: one per (token tile, block-row); from 128 rows (the prefill
     # kernels) then, 128-aligned, 4 slots of 128 per 64 rows: the latent tiles
     # written and the waiters passed, zero at rest like the row counters
     assert lib.ssl_slr_counter_count(16, 172) == 172
     assert lib.ssl_slr_counter_count(64, 172) == 172
-    assert lib.ssl_slr_counter_count(2048, 172) == 5504 + 32 * 4 * 128
-    assert lib.ssl_slr_counter_count(256, 172) == 4 * 172 + 80 + 4 * 4 * 128
+    # (and one arrival word per (64-row token tile, block-row) for the parts of
+    # split row groups)
+    assert lib.ssl_slr_counter_count(2048, 172) == 5504 + 32 * 4 * 128 + 32 * 172
+    assert lib.ssl_slr_counter_count(256, 172) == 4 * 172 + 80 + 4 * 4 * 128 + 4 * 172
     # exchange: the plan's uint64 handshake words (status, then per token tile
     # the latent-ready and ticket words and one arrival word per 16-rank
     # tile), 256-byte aligned

@@ -812,6 +812,29 @@ def test_nm24_prefill_matches_oracle(dtype, shape, tile_mode, M, gpu_device):
     assert torch.equal(y1, y2)
 
 
+@pytest.mark.parametrize("k", [2, 3])
+def test_nm24_prefill_split_row_groups(k, gpu_device):
+    """The 2:4 prefill kernel with its row groups' steps in k parts and the
+    latent's in_features in chunks (test hook), narrow and short tiles."""
+    lib = _lib.load()
+    n, m, r, dtype = 320, 2048, 128, torch.bfloat16
+    mod, (A, B, S, b) = _nm_module(n, m, r, dtype, gpu_device, seed=k)
+    x = np.random.default_rng(k).standard_normal((300, m))
+    x = torch.from_numpy(x).to(dtype).double().numpy()
+    xt = to_dev(x, dtype, gpu_device)
+    for tile in (1, 3):
+        _lib.check(lib.ssl_debug_set(_lib.DEBUG_PREFILL_TILE, tile), "ssl_debug_set")
+        _lib.check(lib.ssl_debug_set(_lib.DEBUG_PREFILL_SPLIT, k), "ssl_debug_set")
+        try:
+            y1, y2 = mod(xt), mod(xt)
+            torch.cuda.synchronize()
+        finally:
+            lib.ssl_debug_set(_lib.DEBUG_PREFILL_TILE, 0)
+            lib.ssl_debug_set(_lib.DEBUG_PREFILL_SPLIT, 0)
+        assert err(y1, orc.slr_linear(x, A, B, S, b)) <= TOL[dtype]
+        assert torch.equal(y1, y2)
+
+
 def test_nm24_prefill_grouped_launch(gpu_device):
     dtype = torch.bfloat16
     mods = [_nm_module(n, 320, r, dtype, gpu_device, seed=17 + n) for n, r in ((96, 32), (200, 64), (64, 16))]

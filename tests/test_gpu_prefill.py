@@ -129,6 +129,76 @@ def test_forced_tiles_inplace_op(dtype, p, mode, tile, gpu_device):
         assert np.array_equal(got[:, by * p:(by + 1) * p], out0[:, by * p:(by + 1) * p])
 
 
+# ------------------------------------------------------------ K parts --
+
+
+@pytest.fixture
+def split():
+    """Force the K parts of fused prefill calls (1: none, 2-4: that many)."""
+    lib = _lib.load()
+
+    def force(k):
+        _lib.check(lib.ssl_debug_set(_lib.DEBUG_PREFILL_SPLIT, k), "ssl_debug_set")
+
+    yield force
+    force(0)
+
+
+def _counters_at_rest(dev) -> bool:
+    from ssalaad_amd import _runtime
+
+    torch.cuda.synchronize()
+    return all(int(buf.abs().max()) == 0 for (idx, _), buf in _runtime._COUNTERS.items()
+               if idx == dev.index)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32],
+                         ids=["bf16", "f16", "f32"])
+@pytest.mark.parametrize("p", [16, 32, 64])
+@pytest.mark.parametrize("mode", [NARROW, SHORT], ids=["narrow", "short"])
+@pytest.mark.parametrize("k", [2, 3, 4])
+def test_split_row_groups_and_latent(dtype, p, mode, k, tile, split, gpu_device):
+    """Every row group's sparse steps in k parts (the last also runs the
+    low-rank steps) and the latent's in_features in chunks: the parts' fp32
+    tiles summed in part order by the last to arrive. Skewed rows (groups with
+    fewer sparse steps than parts), ragged token count, 5000 in_features (the
+    latent in several chunks): every row against the oracle, twice, and the
+    counters back at zero after each call."""
+    if dtype == torch.float32 and p == 64:
+        pytest.skip("fp32 prefill blocks are 16 or 32")
+    tile(mode)
+    split(k)
+    prob = make_problem(11 * p + 64, 5000, 128, p, 0.5, dtype, seed=7 * p + k + mode, skew=True,
+                        pad=True)
+    mod = make_module(prob, gpu_device)
+    for M in (333, 200):
+        x = make_x(prob, M, seed=M)
+        y = mod(to_dev(x, dtype, gpu_device))
+        torch.cuda.synchronize()
+        assert err(y, oracle_y(prob, x)) <= TOL[dtype], M
+        assert _counters_at_rest(gpu_device), M
+
+
+@pytest.mark.parametrize("k", [2, 4])
+def test_split_grouped_launch(k, tile, split, gpu_device):
+    """K parts in a grouped launch of three linears of different ranks and
+    shapes (every member's row groups in k parts, each latent in its own
+    chunks)."""
+    tile(NARROW)
+    split(k)
+    dtype, p = torch.bfloat16, 32
+    specs = [(5 * p, 64, 0.5), (3 * p, 192, 0.3), (7 * p, 128, 0.7)]
+    probs = [make_problem(n, 40 * p, r, p, d, dtype, seed=41 + i, skew=(i == 1))
+             for i, (n, r, d) in enumerate(specs)]
+    grp = ssalaad_amd.LRSLinearGroup(*[make_module(pr, gpu_device) for pr in probs])
+    x = make_x(probs[0], 300)
+    ys = grp(to_dev(x, dtype, gpu_device))
+    torch.cuda.synchronize()
+    for y, pr in zip(ys, probs):
+        assert err(y, oracle_y(pr, x)) <= TOL[dtype]
+    assert _counters_at_rest(gpu_device)
+
+
 # -------------------------------------------- full size, library's choice --
 
 
