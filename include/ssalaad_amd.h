@@ -10,7 +10,10 @@
  *             before the first call; every call that completes leaves it zero.
  *             Keep it for counters only (never alias it with data).
  *   workspace bytes sized by the *_workspace_size query (256-byte aligned); no
- *             initialisation needed.
+ *             initialisation needed. For ssl_slr_forward and its group, many-token
+ *             calls with a small grid may run their row groups in parts whose fp32
+ *             partial tiles take room the query includes; a workspace with less
+ *             (but at least what the call needs without them) runs them whole.
  * Calls that share scratch must be ordered (same stream); concurrent calls on the
  * same scratch race.
  *
