@@ -672,6 +672,24 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
           need > prefill_split_bytes(M, mb.NB, block_p, m_pad, 0, dtype, cus))
         ksplit = 1;
     }
+    // The split narrow grid, the latent's chunks included, against the tall
+    // tile's: 7B FFN 4096×11008 at 768 rows, 768 narrow parts and 240 latent
+    // chunks take two rounds, 192 tall workgroups one (105.3 -> 95.4 µs).
+    if (ksplit > 1 && rows.bm == 128 && knobs.prefill_split == 0) {
+      int64_t tall = 0, narrow = 0;
+      for (int i = 0; i < n_members; ++i) {
+        const ssl_slr_member& mb = members[i];
+        if (mb.NB == 0) continue;
+        tall += mb.pf_n_groups * ((M + 255) / 256);
+        narrow += mb.pf_n_groups * ((M + 127) / 128) * ksplit;
+        if (mb.r_pad > 0)
+          narrow += TL * (mb.r_pad / 64) * prefill_latent_split(M, m_pad, mb.r_pad, dtype).split;
+      }
+      if (prefill_rounds_prefer_tall(tall, narrow, cus)) {
+        rows.bm = 256;
+        ksplit = 1;
+      }
+    }
     int64_t items = 0, litems = 0;
     for (int i = 0; i < n_members; ++i) {
       const ssl_slr_member& mb = members[i];

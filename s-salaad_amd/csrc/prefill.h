@@ -100,6 +100,10 @@ int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus);
 // lat_items: the latent's workgroups in the same launch.
 int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cus, int dtype,
                      int64_t lat_items);
+// Whether `tall` workgroups of the tall tile (2 a compute unit) finish before
+// `narrow` workgroups of the narrow one (3 a compute unit, the latent's
+// included); false while a test forces the tile.
+bool prefill_rounds_prefer_tall(int64_t tall, int64_t narrow, int n_cus);
 // The fused SLR linear in one launch: the latent GEMM's workgroups (`lat`, one per 64-token
 // × 64-rank tile over all of in_features) first in the grid, then the row
 // GEMM's (`rows`), whose low-rank steps wait for their token rows' latent

@@ -976,16 +976,24 @@ int prefill_row_tile(int64_t M, int64_t n_rows, int group, int block_p, int n_cu
   // with 64×64 at 128 rows: 34.4 -> 31.7 µs).
   if (narrow < n_cus / 2) return 64;
   if (M <= 128) return 128;  // one token tile either way; the tall one's lower half past M
-  // Rounds of the whole grid (the latent's workgroups included) at the tile's
-  // workgroups per compute unit, the tall tile (80 KiB of LDS: 2) against the
-  // narrow one (48 KiB: 3); a round of tall workgroups moves 40 KiB a step per
-  // workgroup against 24 and measured about 1.3 narrow rounds. 7B FFN
-  // 11008×4096 at 768 / 1024 rows: narrow 78.8 / 92.9 µs, tall 87.3 / 96.7; at
-  // 1280: tall 103.5, narrow 115.4; 4096×11008 at 1536 rows: tall 123.2, narrow
-  // 169.8 (its narrow grid overflows one round).
-  const int64_t rt = (tall + lat_items + 2 * n_cus - 1) / (2 * n_cus);
-  const int64_t rn = (narrow + lat_items + 3 * n_cus - 1) / (3 * n_cus);
-  return 13 * rt <= 10 * rn ? 256 : 128;
+  // Rounds of the grid at the tile's workgroups per compute unit, the tall tile
+  // (80 KiB of LDS: 2) against the narrow one (48 KiB: 3); a round of tall
+  // workgroups moves 40 KiB a step per workgroup against 24 and costs about 1.2
+  // narrow rounds. The latent's workgroups (first in the grid, short) count
+  // against the narrow grid only: narrow rows that wait for their slots run a
+  // whole round late, tall ones about a latent's length. Min of 3 graph
+  // timings: 7B FFN 11008×4096 at 768 / 1024 rows narrow 78.5 / 92.0 µs, tall
+  // 86.7 / 96.0; at 1280 / 2048 / 3072 tall 100.8 / 154.5 / 231.2, narrow
+  // 114.1 / 168.1 / 245.4; 4096×11008 at 1536 / 2048 / 3072 rows tall 123.4 /
+  // 169.9 / 236.1, narrow 169.6 / 195.0 / 285.2.
+  return prefill_rounds_prefer_tall(tall, narrow + lat_items, n_cus) ? 256 : 128;
+}
+
+bool prefill_rounds_prefer_tall(int64_t tall, int64_t narrow, int n_cus) {
+  if (debug_knobs().prefill_group != 0) return false;  // a forced tile stays
+  const int64_t rt = (tall + 2 * n_cus - 1) / (2 * n_cus);
+  const int64_t rn = (narrow + 3 * n_cus - 1) / (3 * n_cus);
+  return 12 * rt <= 10 * rn;
 }
 
 hipError_t prefill_launch_fused(int dtype, int P, int G, const PfArgs& rows, const PfArgs& lat,
