@@ -662,7 +662,8 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
         n_grp += members[i].pf_n_groups;
         sp_steps += members[i].nnz * block_p / ssl_prefill_step_cols(dtype);
       }
-    int ksplit = prefill_row_split(items0, n_grp > 0 ? sp_steps / n_grp : 0, cus, rows.bm);
+    int ksplit = prefill_row_split(items0, n_grp > 0 ? sp_steps / n_grp : 0,
+                                   m_pad / ssl_prefill_step_cols(dtype), cus, rows.bm);
     for (int i = 0; i < n_members && ksplit > 1; ++i) {
       const ssl_slr_member& mb = members[i];
       if (mb.NB == 0) continue;

@@ -80,10 +80,13 @@ constexpr int kPfLatArriveWord = 64;  // rank tiles ≤ 64 (r_pad ≤ 4096) for 
 
 // K parts of a fused prefill call with few row workgroups: a grid of `items`
 // row workgroups under twice the CUs splits each row group's sparse steps in
-// up to 4 parts (at least 40 steps a part, `steps` the mean
-// per group), and then the latent's in_features too (prefill_latent_split),
-// so neither leaves the other's critical path. 1 = no split.
-int prefill_row_split(int64_t items, int64_t steps, int n_cus, int bm);
+// up to 4 parts (at least 40 steps a part, `steps` the mean per group, the
+// parts at most twice the CUs; past half the CUs' worth of groups only parts
+// of 64 steps or more, or when the latent's steps are 1.5 times the group's),
+// and then the latent's in_features too (prefill_latent_split), so neither
+// leaves the other's critical path. 1 = no split.
+// lat_steps: the latent's steps over in_features.
+int prefill_row_split(int64_t items, int64_t steps, int64_t lat_steps, int n_cus, int bm);
 struct PfLatentSplit {
   int split, chunk;
 };

@@ -904,16 +904,29 @@ hipError_t launch_fused(const PfArgs& rows, const PfArgs& lat, int P, int G, hip
 // 11008×4096 (32 steps a group) at 256 rows 41.1 µs whole, 53.7 in two parts;
 // 4096×11008 (86 steps) 65.9 whole, 53.3 in two parts, 58.2 in three.
 constexpr int64_t kRowSplitMinSteps = 40;
-int prefill_row_split(int64_t items, int64_t steps, int n_cus, int bm) {
+// Past half the CUs' worth of row groups, parts stack on compute units that
+// already run one: two parts pay only when each is long or the latent is what
+// they would otherwise wait for. Measured (whole -> auto parts, µs): 4096×11008
+// with 64×64 blocks (86 steps a group, 172-step latent) at 384 / 512 rows 66.1
+// -> 67.2 / 79.6 -> 66.7, at 640 (640 parts) 85.1 -> 96.9; with 16×16 (344
+// steps) at 512 134.5 -> 95.8; 2048×5461 with 32×32 (86 steps, 86-step latent)
+// at 512 / 640 / 768 rows 62.7 -> 56.1 / 65.2 -> 68.0 / 65.0 -> 70.6.
+constexpr int64_t kRowSplitLongSteps = 64;
+
+int prefill_row_split(int64_t items, int64_t steps, int64_t lat_steps, int n_cus, int bm) {
   if (bm >= 256) return 1;  // the tall tile keeps its registers for its own steps
   const int64_t forced = debug_knobs().prefill_split;  // test hook
   if (forced == 1) return 1;
   if (forced >= 2) return (int)forced;
-  if (items <= 0 || items >= 2 * (int64_t)n_cus) return 1;
-  int64_t k = (2 * (int64_t)n_cus + items - 1) / items;
+  const int64_t slots = 2 * (int64_t)n_cus;
+  if (items <= 0 || items >= slots) return 1;
+  int64_t k = (slots + items - 1) / items;
   if (k > 4) k = 4;
   if (k > steps / kRowSplitMinSteps) k = steps / kRowSplitMinSteps;
-  return k < 2 ? 1 : (int)k;
+  while (k >= 2 && k * items > slots) --k;
+  if (k < 2) return 1;
+  if (2 * items > n_cus && steps / k < kRowSplitLongSteps && 2 * lat_steps < 3 * steps) return 1;
+  return (int)k;
 }
 
 // The latent's K chunks when the rows split: chunks of at least 16 steps, at
