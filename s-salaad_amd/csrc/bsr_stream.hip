@@ -674,8 +674,8 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
         ksplit = 1;
     }
     // The split narrow grid, the latent's chunks included, against the tall
-    // tile's: 7B FFN 4096×11008 at 768 rows, 768 narrow parts and 240 latent
-    // chunks take two rounds, 192 tall workgroups one (105.3 -> 95.4 µs).
+    // tile's: at most twice the CUs in parts plus up to 256 latent chunks can
+    // overflow one round of 3 a CU on a device with fewer than 256 CUs.
     if (ksplit > 1 && rows.bm == 128 && knobs.prefill_split == 0) {
       int64_t tall = 0, narrow = 0;
       for (int i = 0; i < n_members; ++i) {

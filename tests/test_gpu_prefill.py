@@ -247,6 +247,39 @@ def test_llama7b_ffn_at_2048_tokens_every_row(mode, tile, gpu_device):
     assert err(y, oracle_y(prob, x)) <= 1e-2
 
 
+def test_llama7b_down_automatic_tile_and_parts_every_row(tile, split, gpu_device):
+    """4096×11008 bf16 (64×64 blocks at 50%: 86 sparse steps a row group, a
+    172-step latent), rank 256, on a 256-CU device. The library's own choice
+    at each token count equals, bit for bit, the forced configuration it should
+    take, and every row matches the oracle:
+      512 rows: 256 row groups' worth of narrow tiles in 2 parts (512 parts;
+                the latent is 1.5 times a group's steps), latent in chunks;
+      640 rows: 320 groups' worth of narrow tiles whole (640 parts would stack
+                three to a CU);
+      768 rows: 384 groups' worth of narrow tiles whole (768 parts would
+                stack three to a CU)."""
+    if torch.cuda.get_device_properties(gpu_device).multi_processor_count != 256:
+        pytest.skip("the choices checked are those of a 256-CU device")
+    prob = make_problem(4096, 11008, 256, 64, 0.5, torch.bfloat16, seed=23)
+    mod = make_module(prob, gpu_device)
+    x = make_x(prob, 768, seed=3)
+    want = oracle_y(prob, x)
+    for M, forced_tile, forced_parts in ((512, NARROW, 2), (640, NARROW, 1), (768, NARROW, 1)):
+        xt = to_dev(x[:M], torch.bfloat16, gpu_device)
+        y_auto = mod(xt)
+        tile(forced_tile)
+        split(forced_parts)
+        try:
+            y_forced = mod(xt)
+        finally:
+            tile(0)
+            split(0)
+        torch.cuda.synchronize()
+        assert torch.equal(y_auto, y_forced), M
+        assert err(y_auto, want[:M]) <= 1e-2, M
+        assert _counters_at_rest(gpu_device)
+
+
 # ------------------------------------------------------------------- fp32 --
 # fp32 calls run the same kernels with 32-column steps (128 bytes per tile
 # row, v_mfma_f32_16x16x4f32); 16×16 and 32×32 blocks (64-wide blocks stream).
