@@ -430,9 +430,14 @@ int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_
     return items >= device_cus() ? 1 : 0;
   }
   if (debug_knobs().prefill_group != 0) return 1;  // a forced row tile (test hook)
-  if (block_p == 16 && M <= 512) return 0;
-  if (block_p == 32 && M < 512 && (M <= kPrefillMinM || n_rows < 100)) return 0;
-  if (M <= kPrefillMinM && n_rows < 100) return 0;
+  // The streaming kernel keeps only one-token-tile calls with at most 2048
+  // output features: its finer K split wins there (2048×2048 and 2048×5461
+  // with 32×32 blocks at 128 rows: 26.9 / 39.4 µs streaming against 28.8 /
+  // 42.0). Everywhere else the tiled kernels, K parts included, win: 16×16
+  // blocks 2.2-4.3× (11008×4096 at 128 / 256 / 512 rows 109 / 196 / 372 ->
+  // 49 / 60 / 87 µs), 4096×11008 with 32×32 or 64×64 at 128 rows 82 / 64 ->
+  // 46 / 44, 4096×4096 with 64×64 at 128 rows 34.3 -> 31.0.
+  if (M <= kPrefillMinM && n_rows * block_p <= 2048) return 0;
   return 1;
 }
 

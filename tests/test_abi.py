@@ -371,14 +371,17 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     big = dict(M=4096, counters=P, n_counters=1 << 20)
     assert op(**big) == _lib.SSL_ERR_INVALID and b"prefill plan" in lib.ssl_last_error()
     assert lib.ssl_prefill_min_rows() == 128
-    # fused calls: streaming for small blocks up to 512 rows and for calls of
-    # fewer than 100 block-rows at 128 rows; fp32 always streams
+    # 16-bit fused calls: streaming below 128 rows, and at 128 rows for at
+    # most 2048 output features (block-rows × p); the tiled kernels otherwise,
+    # 16×16 blocks included
     tp = lambda M, rows, p, dt=_lib.SSL_BF16, q=None: lib.ssl_slr_takes_prefill(
         M, rows, p, p if q is None else q, dt)
-    assert tp(127, 500, 64) == 0 and tp(128, 172, 64) == 1 and tp(128, 64, 64) == 0
-    assert tp(129, 64, 64) == 1 and tp(512, 500, 32) == 1 and tp(511, 64, 32) == 0
-    assert tp(300, 500, 32) == 1 and tp(128, 500, 32) == 0 and tp(512, 500, 16) == 0
-    assert tp(300, 500, 16) == 0 and tp(2048, 64, 32) == 1 and tp(4096, 500, 64, _lib.SSL_F32) == 0
+    assert tp(127, 500, 64) == 0 and tp(128, 172, 64) == 1 and tp(128, 64, 64) == 1
+    assert tp(128, 32, 64) == 0 and tp(128, 64, 32) == 0 and tp(128, 65, 32) == 1
+    assert tp(128, 128, 16) == 0 and tp(128, 129, 16) == 1 and tp(129, 64, 32) == 1
+    assert tp(512, 500, 32) == 1 and tp(511, 64, 32) == 1 and tp(300, 500, 32) == 1
+    assert tp(128, 500, 32) == 1 and tp(512, 500, 16) == 1 and tp(300, 500, 16) == 1
+    assert tp(2048, 64, 32) == 1 and tp(4096, 500, 64, _lib.SSL_F32) == 0
     # fp32: when the short (64-row) tiles' grid fills the device (LLaMA-60M
     # 512-wide projections at 2048 rows: 32 token tiles × 8 groups of two
     # 32-row block-rows)
