@@ -280,6 +280,27 @@ def test_llama7b_down_automatic_tile_and_parts_every_row(tile, split, gpu_device
         assert _counters_at_rest(gpu_device)
 
 
+@pytest.mark.parametrize("n,m,p,M,tiled", [
+    (2048, 2048, 32, 128, False),   # one token tile, 2048 output features: streams
+    (2080, 2048, 32, 128, True),    # 65 block-rows: tiled
+    (4096, 2048, 16, 128, True),    # 16×16 blocks, one token tile: tiled
+    (4096, 2048, 16, 300, True),    # 16×16 blocks, ragged token tiles, K parts
+    (4096, 3072, 64, 128, True),
+], ids=["stream-2048x2048-p32", "tiled-2080-p32", "tiled-p16-128", "tiled-p16-300", "tiled-p64-128"])
+def test_automatic_routing_at_its_boundaries_every_row(n, m, p, M, tiled, gpu_device):
+    """The library's own stream-or-tile choice on both sides of its boundary
+    (128 rows, 2048 output features), every row against the oracle."""
+    lib = _lib.load()
+    prob = make_problem(n, m, 128, p, 0.5, torch.bfloat16, seed=n + M)
+    assert bool(lib.ssl_slr_takes_prefill(M, prob["NB"], p, p, _lib.SSL_BF16)) == tiled
+    mod = make_module(prob, gpu_device)
+    x = make_x(prob, M, seed=M)
+    y = mod(to_dev(x, torch.bfloat16, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= 1e-2
+    assert _counters_at_rest(gpu_device)
+
+
 # ------------------------------------------------------------------- fp32 --
 # fp32 calls run the same kernels with 32-column steps (128 bytes per tile
 # row, v_mfma_f32_16x16x4f32); 16×16 and 32×32 blocks (64-wide blocks stream).
