@@ -178,15 +178,15 @@ int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_
  * Blocks: p ∈ {16, 32, 48, 64} output features, q any multiple of 16 up to
  * 256 input features (square or not); dtype ∈ {f32, bf16, f16} for out, x and
  * values alike. `plan` is a device copy of a table from ssl_plan_build
- * (lr_units = 0). Calls for which ssl_bsr_addmm_takes_prefill(M, p, q, dtype)
- * is 1 run the prefill kernel instead: they need `pf_groups`/`pf_steps`
+ * (lr_units = 0). Calls for which ssl_bsr_addmm_takes_prefill(M, n_chunks, p, q,
+ * dtype) is 1 (n_chunks: the plan's, its rows at M > 64) run the prefill kernel instead: they need `pf_groups`/`pf_steps`
  * (device copies from ssl_prefill_plan_build with the same rows and group =
  * pf_group = ssl_prefill_group(M, rows, p, q)) and `values_pq`, the block
  * values in (nnz, p, q) order (each block transposed); other calls may pass
  * NULL/0 there.
  * ------------------------------------------------------------------------- */
-int32_t ssl_bsr_addmm_takes_prefill(int64_t M, int32_t block_p, int32_t block_q,
-                                    int32_t dtype);
+int32_t ssl_bsr_addmm_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p,
+                                    int32_t block_q, int32_t dtype);
 int64_t ssl_bsr_addmm_workspace_size(int64_t M, int64_t NB, int32_t block_p,
                                      int64_t n_slots);
 int64_t ssl_bsr_addmm_counter_count(int64_t M, int64_t NB);

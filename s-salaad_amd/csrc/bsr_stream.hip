@@ -458,11 +458,24 @@ int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p, int32_t bl
   return prefill_group(M, n_rows, block_p, device_cus());
 }
 
-int32_t ssl_bsr_addmm_takes_prefill(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype) {
+int32_t ssl_bsr_addmm_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q,
+                                    int32_t dtype) {
   // fp32: only under a forced row tile (test hook); the streaming kernel's
   // finer split is the default for the op
-  return M >= kPrefillMinM && prefill_block(block_p, block_q, dtype) &&
-         (dtype != SSL_F32 || debug_knobs().prefill_group != 0);
+  if (M < kPrefillMinM || !prefill_block(block_p, block_q, dtype)) return 0;
+  if (debug_knobs().prefill_group != 0) return 1;
+  if (dtype == SSL_F32) return 0;
+  // One token tile whose grid of short (64-row) tiles would fill at most half
+  // the CUs streams: the op's tiled kernel runs whole row groups (2048×5461
+  // with 32×32 blocks at 128 rows: 22.8 µs streaming, 36.0 tiled; 4096×4096
+  // and 4096×11008 with 64×64: 31.3 / 50.3 against 34.2 / 54.1), while
+  // 11008×4096 with 64×64 (172 groups) and 16×16 blocks tile (36.4 against
+  // 53.3, 51.5 against 109.4).
+  if (M <= kPrefillMinM && block_p >= 32) {
+    const int64_t per = 64 / block_p, groups = (n_rows + per - 1) / per;
+    if (4 * groups <= device_cus()) return 0;
+  }
+  return 1;
 }
 
 int64_t ssl_bsr_addmm_counter_count(int64_t M, int64_t NB) {
@@ -517,7 +530,7 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
 
   if (nnz < 0 || !slab_count_ok(nnz, block_q / (4 * stream_ke(dtype, block_q))))
     return fail(SSL_ERR_UNSUPPORTED, "too many blocks (%lld) for one call", (long long)nnz);
-  if (ssl_bsr_addmm_takes_prefill(M, block_p, block_q, dtype)) {
+  if (ssl_bsr_addmm_takes_prefill(M, n_chunks, block_p, block_q, dtype)) {
     if (!pf_groups || !pf_steps || pf_n_groups <= 0 || !values_pq)
       return fail(SSL_ERR_INVALID, "calls with %lld token rows need a prefill plan and (p, q) "
                   "ordered block values", (long long)M);

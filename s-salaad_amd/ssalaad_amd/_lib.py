@@ -68,7 +68,7 @@ _SIGNATURES = {
     "ssl_nm24_takes_prefill": (_c_i32, [_c_i64, _c_i64, _c_i32]),
     "ssl_prefill_group": (_c_i32, [_c_i64, _c_i64, _c_i32, _c_i32]),
     "ssl_slr_takes_prefill": (_c_i32, [_c_i64, _c_i64, _c_i32, _c_i32, _c_i32]),
-    "ssl_bsr_addmm_takes_prefill": (_c_i32, [_c_i64, _c_i32, _c_i32, _c_i32]),
+    "ssl_bsr_addmm_takes_prefill": (_c_i32, [_c_i64, _c_i64, _c_i32, _c_i32, _c_i32]),
     "ssl_slr_workspace_size": (_c_i64, [_c_i64, _c_i64, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32]),
     "ssl_slr_counter_count": (_c_i64, [_c_i64, _c_i64]),
     "ssl_slr_exchange_size": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i32]),

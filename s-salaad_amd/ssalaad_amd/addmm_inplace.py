@@ -117,7 +117,7 @@ def _plan_for(crow, col, active_rows, values, NB_K, block_p, block_q, M, elem_by
     lib = _lib.load()
     dt = _lib.SSL_BF16 if elem_bytes == 2 else _lib.SSL_F32
     if prefill is None:
-        prefill = bool(lib.ssl_bsr_addmm_takes_prefill(M, block_p, block_q, dt))
+        prefill = bool(lib.ssl_bsr_addmm_takes_prefill(M, plan.n_chunks, block_p, block_q, dt))
     if prefill and plan.n_chunks > 0:
         # the prefill kernel's groups list the planned rows (active rows with blocks)
         G = int(lib.ssl_prefill_group(M, plan.n_chunks, block_p, block_q))
@@ -297,7 +297,7 @@ def prepare_bsr_addmm(
     eb = values.element_size()
     dt = _lib.dtype_code(values.dtype)
     lib = _lib.load()
-    can_prefill = bool(lib.ssl_bsr_addmm_takes_prefill(1 << 20, block_p, block_q, dt))
+    can_prefill = bool(lib.ssl_bsr_addmm_takes_prefill(1 << 20, 1, block_p, block_q, dt))
     with torch.cuda.device(values.device):
         for M, pf_wanted in ((1, False), (1 << 20, can_prefill)):
             _, pf = _plan_for(crow_indices, col_indices, active_rows, values, NB_K, block_p,

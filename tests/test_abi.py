@@ -390,9 +390,13 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     assert lib.ssl_prefill_group(4096, 172, 64, 64) == 1  # 64 output features per row tile
     # the prefill kernels take square 16/32/64 blocks; other shapes stream
     assert tp(2048, 500, 32, q=64) == 0 and tp(2048, 500, 48) == 0
-    ap = lambda M, p, q, dt=_lib.SSL_BF16: lib.ssl_bsr_addmm_takes_prefill(M, p, q, dt)
-    assert ap(128, 64, 64) == 1 and ap(127, 64, 64) == 0 and ap(4096, 32, 64) == 0
-    assert ap(4096, 64, 64, _lib.SSL_F32) == 0
+    # the op: from 128 rows, except one token tile whose short-tile grid (64/p
+    # block-rows a group) fills at most a quarter of 256 CUs with 32/64-wide blocks
+    ap = lambda M, rows, p, q, dt=_lib.SSL_BF16: lib.ssl_bsr_addmm_takes_prefill(M, rows, p, q, dt)
+    assert ap(128, 172, 64, 64) == 1 and ap(127, 172, 64, 64) == 0 and ap(4096, 500, 32, 64) == 0
+    assert ap(4096, 500, 64, 64, _lib.SSL_F32) == 0 and ap(129, 1, 64, 64) == 1
+    assert ap(128, 64, 64, 64) == 0 and ap(128, 65, 64, 64) == 1 and ap(128, 128, 32, 32) == 0
+    assert ap(128, 129, 32, 32) == 1 and ap(128, 1, 16, 16) == 1
 
     # ssl_slr_forward with fake, aligned device pointers (every case below is
     # rejected on the host before any launch)
