@@ -129,6 +129,34 @@ def test_forced_tiles_inplace_op(dtype, p, mode, tile, gpu_device):
         assert np.array_equal(got[:, by * p:(by + 1) * p], out0[:, by * p:(by + 1) * p])
 
 
+@pytest.mark.parametrize("n,m,p", [(4096, 2048, 64), (6144, 2048, 64), (2048, 5461, 32),
+                                    (4160, 1024, 32), (1024, 1024, 16)],
+                         ids=["p64-64rows", "p64-96rows", "p32-64rows", "p32-130rows", "p16"])
+def test_inplace_op_automatic_routing_at_128_rows(n, m, p, gpu_device):
+    """The op's own stream-or-tile choice at one token tile pair (128 rows) on
+    both sides of its grid boundary: out += x·Sᵀ on the active rows, every
+    other row untouched."""
+    M, dtype = 128, torch.bfloat16
+    prob = make_problem(n, m, 4, p, 0.5, dtype, seed=n + p, pad=True)
+    crow32, col32, vt, act = orc.module_buffers(prob["crow"], prob["col"], prob["vals"])
+    x = make_x(prob, M, seed=7)
+    rng = np.random.default_rng(n)
+    out0 = torch.from_numpy(rng.standard_normal((M, prob["NB"] * p))).to(dtype).double().numpy()
+    xp = np.zeros((M, prob["NBK"] * p))
+    xp[:, :m] = x
+    want = orc.bsr_addmm_inplace(out0, xp, crow32, col32, vt, act)
+    dev = gpu_device
+    out = to_dev(out0, dtype, dev)
+    torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_(
+        out, to_dev(xp, dtype, dev), torch.from_numpy(crow32).to(dev),
+        torch.from_numpy(col32).to(dev), to_dev(vt, dtype, dev), torch.from_numpy(act).to(dev))
+    torch.cuda.synchronize()
+    assert err(out, want) <= TOL[dtype]
+    got = out.double().cpu().numpy()
+    for by in sorted(set(range(prob["NB"])) - set(act.tolist())):
+        assert np.array_equal(got[:, by * p:(by + 1) * p], out0[:, by * p:(by + 1) * p])
+
+
 # ------------------------------------------------------------ K parts --
 
 
