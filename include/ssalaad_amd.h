@@ -56,6 +56,19 @@ typedef enum { SSL_F32 = 0, SSL_BF16 = 1, SSL_F16 = 2 } ssl_dtype;
 int ssl_version(void);
 const char* ssl_last_error(void);
 
+/* A status word in host memory that kernels can write (no reference
+ * counterpart: the reference's kernels have no bounded waits to report). It
+ * allocates 256 bytes of pinned, coherent host memory, zeroed, that every GPU
+ * can address, and returns its host address and the device address kernels
+ * take (pass it as ssl_slr_member.status). A workgroup that gives up a bounded
+ * wait stores 1 into its first uint64, and the store is visible to the host
+ * as soon as it lands, so a host can check the word before each call with a
+ * plain read instead of a copy and a synchronisation. The memory lives until
+ * the process ends; the host clears the word itself. This is the one call of
+ * the library that allocates; it is made once per process or device, outside
+ * any graph capture. */
+int ssl_status_word_alloc(void** host_ptr, void** device_ptr);
+
 /* Test hooks (host-side process-wide settings read at each launch; no
  * reference counterpart). They exist so that tests can reach paths that a
  * healthy device never takes, with every kernel still ending normally:
@@ -157,11 +170,14 @@ int64_t ssl_prefill_min_rows(void);
 int32_t ssl_prefill_group(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q);
 /* 1 if a fused SLR call (ssl_slr_forward, ssl_slr_forward_group) with block
  * storage, M token rows and n_rows block-rows over all its linears takes the
- * prefill kernels (and so needs their plans), 0 if it streams. At least
- * ssl_prefill_min_rows() rows, except 32×32 or smaller 16-bit blocks up to
- * 512 rows and calls of fewer than 100 block-rows at the minimum row count;
- * fp32 calls only when the row kernel's grid fills the device. The in-place
- * op (ssl_bsr_addmm_inplace) keeps the plain threshold (fp32: streams). */
+ * prefill kernels (and so needs their plans), 0 if it streams. Only square
+ * 16/32/64 blocks (fp32: 16/32) take them, from ssl_prefill_min_rows() rows:
+ * 16-bit calls always, except calls of exactly that many rows (one token tile)
+ * with at most 2048 output features (n_rows · block_p ≤ 2048), which stream;
+ * fp32 calls when the grid of 64-row tiles, ceil(M / 64) · ceil(n_rows /
+ * (64 / block_p)) workgroups, reaches the device's compute-unit count. A
+ * forced row tile (SSL_DEBUG_PREFILL_TILE) sends every such call there. The
+ * in-place op decides with ssl_bsr_addmm_takes_prefill instead. */
 int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q,
                               int32_t dtype);
 
@@ -223,6 +239,9 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx,
  * uint64 is set to 1 if a workgroup gave up waiting (never expected; the host
  * may check it after synchronising). A zeroed area is always a valid state
  * (e.g. after growing it).
+ * Calls for which ssl_slr_takes_prefill(M, NB, block_p, block_q, dtype) is 1
+ * return SSL_ERR_INVALID before any launch: they need the prefill plans, which
+ * only ssl_slr_forward_group takes (the pf_* fields of ssl_slr_member).
  * ------------------------------------------------------------------------- */
 int64_t ssl_slr_workspace_size(int64_t M, int64_t NB, int32_t block_p, int64_t r_pad,
                                int64_t m_pad, int64_t n_slots, int32_t dtype);
@@ -251,8 +270,9 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
  * one another; calls that overlap on one GPU (other streams or threads) race on
  * the shared array. A wait that gave up is recorded in the first handshake word
  * (cleared by the next call). Same arguments, limits and results as
- * ssl_slr_forward otherwise (16-bit calls of ssl_prefill_min_rows() rows or
- * more need the prefill plans, which this entry point does not take). */
+ * ssl_slr_forward otherwise: calls for which ssl_slr_takes_prefill(M, NB,
+ * block_p, block_q, dtype) is 1 need the prefill plans, which this entry point
+ * does not take, and return SSL_ERR_INVALID before any launch. */
 int64_t ssl_slr_noalloc_scratch_bytes(void);
 int ssl_slr_forward_noalloc(void* y, int64_t ldy, const void* x, int64_t ldx, const void* A,
                             const void* B, const void* bias, const int32_t* col,
@@ -299,9 +319,9 @@ typedef struct ssl_slr_member {
    * (replaces the semi-structured S of ssalaad/efficient/ls_linear.py:167-219) */
   int32_t s_format;
   /* where a workgroup that gave up waiting records it (uint64, set to 1;
-   * device memory, never cleared by the library). NULL: the first uint64 of
-   * `exchange`. Sharing one word between every call lets a host check all of
-   * them at once. */
+   * device memory or the device address from ssl_status_word_alloc, never
+   * cleared by the library). NULL: the first uint64 of `exchange`. Sharing one
+   * word between every call lets a host check all of them at once. */
   uint64_t* status;
 } ssl_slr_member;
 

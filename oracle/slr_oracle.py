@@ -125,15 +125,18 @@ def module_buffers(crow, col, values):
 
 
 def bsr_to_dense(crow, col, values, n: int, m: int) -> np.ndarray:
-    """(crow, col, values (nnz, p, q)) -> dense (n, m) float64."""
+    """(crow, col, values (nnz, p, q)) -> dense (n, m) float64: block k of
+    block-row by (crow[by] <= k < crow[by+1]) lands at rows by·p.., columns
+    col[k]·q.. (the BSR layout of torch.sparse_bsr_tensor). n and m are
+    multiples of p and q."""
     values = np.asarray(values, dtype=np.float64)
+    crow = np.asarray(crow, dtype=np.int64)
     p, q = values.shape[1], values.shape[2]
-    S = np.zeros((n, m), dtype=np.float64)
-    for by in range(len(crow) - 1):
-        for ji in range(int(crow[by]), int(crow[by + 1])):
-            c = int(col[ji])
-            S[by * p : (by + 1) * p, c * q : (c + 1) * q] = values[ji]
-    return S
+    NB, NBK = n // p, m // q
+    rows = np.repeat(np.arange(len(crow) - 1), np.diff(crow))
+    S4 = np.zeros((NB, NBK, p, q), dtype=np.float64)
+    S4[rows, np.asarray(col, dtype=np.int64)] = values
+    return np.ascontiguousarray(S4.transpose(0, 2, 1, 3)).reshape(n, m)
 
 
 # -------------------------------------------------------------- arithmetic --

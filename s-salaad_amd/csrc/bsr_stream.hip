@@ -406,15 +406,11 @@ extern "C" {
 
 int64_t ssl_prefill_min_rows(void) { return kPrefillMinM; }
 
-// Which kernels a fused call with block storage takes. The prefill kernels
-// from kPrefillMinM token rows (fp32: when their grid fills the device),
-// except where the 16-bit streaming kernel (one weight pass per 64-row token
-// tile, the re-reads served by the caches) measured faster on MI355X: 16×16
-// blocks up to 512 rows, 32×32 blocks below 512 rows when the call has fewer
-// than 100 block-rows or at most 128 rows (LLaMA-1B down 2048×5461 at 128 / 256 / 384 rows: streaming
-// 38.4 / 51.6 / 53.5 µs, prefill 54.9 / 57.3 / 58.8; its gate 5461×2048, 171
-// block-rows, at 256 / 384 / 512 rows: prefill 29.8 / 33.6 / 34.7, streaming
-// 34.7 / 46.3 / 53.0), and calls of fewer than 100 block-rows up to 128 rows.
+// Which kernels a fused call with block storage takes: the prefill kernels
+// from kPrefillMinM token rows for the square blocks they run (fp32: when
+// their grid fills the device), except one-token-tile 16-bit calls with at
+// most 2048 output features, where the streaming kernel (one weight pass per
+// 64-row token tile) measured faster on MI355X.
 int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_t block_q,
                               int32_t dtype) {
   if (M < kPrefillMinM || !prefill_block(block_p, block_q, dtype)) return 0;
@@ -465,8 +461,8 @@ int32_t ssl_bsr_addmm_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, 
   if (M < kPrefillMinM || !prefill_block(block_p, block_q, dtype)) return 0;
   if (debug_knobs().prefill_group != 0) return 1;
   if (dtype == SSL_F32) return 0;
-  // One token tile whose grid of short (64-row) tiles would fill at most half
-  // the CUs streams: the op's tiled kernel runs whole row groups (2048×5461
+  // One token tile whose grid of short (64-row) tiles would fill at most a
+  // quarter of the CUs streams: the op's tiled kernel runs whole row groups (2048×5461
   // with 32×32 blocks at 128 rows: 22.8 µs streaming, 36.0 tiled; 4096×4096
   // and 4096×11008 with 64×64: 31.3 / 50.3 against 34.2 / 54.1), while
   // 11008×4096 with 64×64 (172 groups) and 16×16 blocks tile (36.4 against

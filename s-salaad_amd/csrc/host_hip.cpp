@@ -1,7 +1,12 @@
-// Host-side HIP helpers of the C ABI: error mapping and device queries.
+// Host-side HIP helpers of the C ABI: error mapping, device queries and the
+// status word's host memory.
+#include <string.h>
+
 #include "abi_internal.h"
 
 namespace ssl {
+
+constexpr size_t kStatusWordBytes = 256;
 
 int check_hip(hipError_t e, const char* what) {
   if (e == hipSuccess) return SSL_OK;
@@ -22,3 +27,31 @@ int device_cus() {
 }
 
 }  // namespace ssl
+
+using namespace ssl;
+
+extern "C" {
+
+int ssl_status_word_alloc(void** host_ptr, void** device_ptr) {
+  clear_error();
+  if (!host_ptr || !device_ptr) return fail(SSL_ERR_INVALID, "status word: null output pointer");
+  void* h = nullptr;
+  // coherent (fine-grained): a kernel's store reaches host memory without a
+  // cache write-back, so the host sees it as soon as it lands
+  if (int rc = check_hip(hipHostMalloc(&h, kStatusWordBytes,
+                                       hipHostMallocPortable | hipHostMallocMapped |
+                                           hipHostMallocCoherent),
+                         "status word allocation"))
+    return rc;
+  memset(h, 0, kStatusWordBytes);
+  void* d = nullptr;
+  if (int rc = check_hip(hipHostGetDevicePointer(&d, h, 0), "status word device address")) {
+    (void)hipHostFree(h);
+    return rc;
+  }
+  *host_ptr = h;
+  *device_ptr = d;
+  return SSL_OK;
+}
+
+}  // extern "C"

@@ -312,7 +312,9 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
     const int b0 = min(kp * chunk, n_all), b1 = min(b0 + chunk, n_all);
     s_begin = g0 + b0;
     n_sp = b1 - b0;
-    has_lr = LR && kp == ksplit - 1;
+    // a member with no low-rank factor (r_pad 0) has no latent tiles to wait
+    // for and no tile counters (tcnt is null): it neither waits nor departs
+    has_lr = LR && kp == ksplit - 1 && mb.r_pad > 0;
     const int n_lr = has_lr ? mb.r_pad / KS : 0;
     s_end = s_begin + n_sp + n_lr;
   }

@@ -20,7 +20,8 @@ from .addmm_inplace import (SUPPORTED_BLOCK_SIZES, bsr_addmm_inplace_, get_tuned
 from .artifact import dense_to_bsr, encode_for_kernels, factor_from_svd
 from .bundle import build_efficient_model, load_artifact, save_artifact
 from .decode import DecodeEngine, generate
-from .ls_linear import LRSLinear, LRSLinearChain, LRSLinearGroup, PreparedChain
+from .ls_linear import (LRSLinear, LRSLinearChain, LRSLinearGroup, PreparedChain,
+                        clear_wait_status, latent_wait_status)
 from .project import block_topk, project_S, project_S_nm, project_nm
 
 __all__ = [
@@ -33,12 +34,14 @@ __all__ = [
     "block_topk",
     "build_efficient_model",
     "bsr_addmm_inplace_",
+    "clear_wait_status",
     "prepare_bsr_addmm",
     "dense_to_bsr",
     "encode_for_kernels",
     "factor_from_svd",
     "generate",
     "get_tuned_config",
+    "latent_wait_status",
     "library_path",
     "load_artifact",
     "project_S",

@@ -42,6 +42,7 @@ _SIGNATURES = {
     "ssl_version": (ctypes.c_int, []),
     "ssl_last_error": (ctypes.c_char_p, []),
     "ssl_debug_set": (ctypes.c_int, [_c_i32, _c_i64]),
+    "ssl_status_word_alloc": (ctypes.c_int, [_c_p, _c_p]),
     "ssl_plan_build": (
         ctypes.c_int,
         [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_i64, _c_p, _c_i64, _c_p,

@@ -17,8 +17,11 @@ buffer and exchange area lives as long as the process (the pools grow
 geometrically, so the retired ones total less than the live one).
 
 Every fused call reports a bounded wait that gave up in one status word per
-device (`status_word`), which the host reads when it chooses to (a read
-synchronises; the decode engine mirrors it into host memory once per step).
+device (`status_word`). The word lives in pinned, coherent host memory that the
+kernels write through its device address, so the host reads it with a plain
+load: every call of the modules, groups, chains and the op checks it first
+(`check_status`) and raises once a give-up has landed, and the decode engine
+checks it before each step.
 """
 
 from __future__ import annotations
@@ -247,7 +250,7 @@ _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 _COUNTERS: dict[tuple[int, int], torch.Tensor] = {}
 # Outgrown pool buffers: kept for the life of the process (see the module doc).
 _RETIRED: list[torch.Tensor] = []
-_STATUS: dict[int, torch.Tensor] = {}
+_STATUS: dict[int, "StatusWord"] = {}
 
 
 def _key(device: torch.device) -> tuple[int, int]:
@@ -277,22 +280,66 @@ def counters(device: torch.device, count: int) -> torch.Tensor:
     return _grown(_COUNTERS, _key(device), count, torch.int32, device, 1 << 14)
 
 
-def status_word(device: torch.device) -> torch.Tensor:
-    """The device's wait-status word (int64 on the device): every fused call on
-    it sets the word to 1 when one of its workgroups gave up waiting (its output
-    is then unreliable). Zero until then; only `reset_status` clears it."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
+class StatusWord:
+    """A device's wait-status word: one uint64 of pinned, coherent host memory
+    (ssl_status_word_alloc) that the kernels set to 1 through `device_ptr`
+    when a workgroup gives up a bounded wait. The host reads and clears it
+    in place; it lives as long as the process."""
+
+    __slots__ = ("host_ptr", "device_ptr", "_word")
+
+    def __init__(self) -> None:
+        host, dev = ctypes.c_void_p(), ctypes.c_void_p()
+        rc = _lib.load().ssl_status_word_alloc(ctypes.byref(host), ctypes.byref(dev))
+        _lib.check(rc, "ssl_status_word_alloc")
+        self.host_ptr, self.device_ptr = host.value, dev.value
+        self._word = ctypes.c_uint64.from_address(self.host_ptr)
+
+    def read(self) -> int:
+        """The word as it stands (no synchronisation: a give-up of a call still
+        running shows once its store lands)."""
+        return int(self._word.value)
+
+    def clear(self) -> None:
+        self._word.value = 0
+
+
+def _index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def status_word(device: torch.device) -> StatusWord:
+    """The device's wait-status word, which every fused call on it reports into
+    (its output is unreliable once the word is set). Zero until then; only
+    `reset_status` clears it."""
+    idx = _index(device)
     w = _STATUS.get(idx)
     if w is None:
-        w = torch.zeros(1, dtype=torch.int64, device=torch.device("cuda", idx))
+        with torch.cuda.device(idx):
+            w = StatusWord()
         _STATUS[idx] = w
     return w
 
 
+def check_status(device: torch.device) -> None:
+    """Raise RuntimeError if a fused call on `device` gave up waiting (as far as
+    the host can see now, without synchronising)."""
+    w = _STATUS.get(_index(device))
+    if w is not None and w.read() != 0:
+        raise RuntimeError(
+            f"a fused SLR launch on cuda:{_index(device)} gave up waiting for another "
+            "workgroup (bounded wait), so outputs computed since then are unreliable; "
+            "call ssalaad_amd.clear_wait_status() before the next call")
+
+
 def read_status(device: torch.device) -> int:
-    """The device's wait status (synchronises with the device)."""
-    return int(status_word(device).item())
+    """The device's wait status once all its work has finished (synchronises)."""
+    torch.cuda.synchronize(device)
+    return status_word(device).read()
 
 
 def reset_status(device: torch.device) -> None:
-    status_word(device).zero_()
+    """Clear the device's wait status after all its work has finished
+    (synchronises, so no running call sets it again afterwards)."""
+    torch.cuda.synchronize(device)
+    status_word(device).clear()

@@ -201,6 +201,9 @@ def bsr_addmm_inplace_(
     devs = {t.device for t in (out_inplace, x, crow_indices, col_indices, values, active_rows)}
     if len(devs) != 1 or out_inplace.device.type != "cuda":
         raise ValueError("all tensors must be on one ROCm GPU device")
+    # The op's own kernels never wait on another workgroup; an earlier fused
+    # call on the device that gave up a wait makes its inputs unreliable.
+    _runtime.check_status(out_inplace.device)
     block_q = int(values.shape[1])
     block_p = int(values.shape[2])
     if block_p % BLOCK_MULTIPLE or block_q % BLOCK_MULTIPLE or block_p == 0 or block_q == 0:

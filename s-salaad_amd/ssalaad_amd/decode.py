@@ -132,12 +132,11 @@ class DecodeEngine:
         nc = self.lib.ssl_decode_attention_counter_count(max_batch, self.heads, self.kv_heads)
         self.attn_cnt = torch.zeros(max(nc, 1), dtype=torch.int32, device=dev)
         self.use_graphs = use_graphs
-        # Host mirror of the device's wait-status word, refreshed (one 8-byte
-        # copy, no synchronisation) after every step and checked before the
-        # next, so a fused launch whose wait gave up is reported one step late
-        # at no per-step cost.
-        self._status_dev = _runtime.status_word(dev)
-        self._status_host = torch.zeros(1, dtype=torch.int64, pin_memory=True)
+        # The device's wait-status word sits in host memory the kernels write
+        # directly: checked before every step with a plain read, so a fused
+        # launch whose wait gave up is reported by the first step that starts
+        # after its store landed, at no per-step cost.
+        self._status = _runtime.status_word(dev)
         self._stream = torch.cuda.Stream(dev)
         self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
 
@@ -192,10 +191,9 @@ class DecodeEngine:
 
     # ---------------------------------------------------------------- public
     def clear_status(self) -> None:
-        """Reset the device's wait-status word and this engine's host mirror of it."""
+        """Reset the device's wait-status word once this engine's work is done."""
         self._stream.synchronize()
         _runtime.reset_status(self.device)
-        self._status_host.zero_()
 
     @torch.no_grad()
     def step(self, tokens, positions) -> torch.Tensor:
@@ -210,7 +208,7 @@ class DecodeEngine:
         pos_h = positions.to("cpu")
         if int(pos_h.min()) < 0 or int(pos_h.max()) >= self.max_context:
             raise ValueError(f"positions must lie in [0, {self.max_context})")
-        if int(self._status_host[0]) != 0:
+        if self._status.read() != 0:
             raise RuntimeError(
                 "a fused SLR launch of an earlier step gave up waiting for another "
                 "workgroup (bounded wait); its logits are unreliable. Call clear_status() "
@@ -232,7 +230,6 @@ class DecodeEngine:
                 with torch.cuda.graph(g, stream=s):
                     gout = self._body(B)
                 self._graphs[B] = (g, gout)
-            self._status_host.copy_(self._status_dev, non_blocking=True)
         cur.wait_stream(s)
         return out
 

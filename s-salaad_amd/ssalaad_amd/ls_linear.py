@@ -242,7 +242,7 @@ def _members(states: list["_KernelState"], ys: list[torch.Tensor], M: int, G: in
     cnt_need = [lib.ssl_slr_counter_count(M, st.NB) for st in states]
     ws = _runtime.workspace(dev, sum(ws_need))
     cnt = _runtime.counters(dev, sum(cnt_need) + extra_counters)
-    status = _runtime.status_word(dev).data_ptr()
+    status = _runtime.status_word(dev).device_ptr
     members = (_lib.SlrMember * len(states))()
     ws_off = cnt_off = 0
     for i, (st, pl, y) in enumerate(zip(states, plans, ys)):
@@ -282,6 +282,7 @@ def _outputs(states, ys, out_features, lead: tuple) -> list[torch.Tensor]:
 
 def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[int]):
     """One fused launch computing every state's linear of the same x."""
+    _runtime.check_status(x.device)
     st0 = states[0]
     orig = x.shape
     x2 = st0.rows(x)
@@ -310,6 +311,17 @@ def latent_wait_status(device: torch.device) -> int:
     idx = device.index if device.index is not None else torch.cuda.current_device()
     words = [pl.wait_status() for pl in list(_runtime._PLANS) if pl.table.device.index == idx]
     return max(words + [_runtime.read_status(torch.device("cuda", idx))])
+
+
+def clear_wait_status(device: torch.device | None = None) -> None:
+    """Clear the wait status of `device` (the current device by default) after
+    its work has finished. Every module, group, chain and op call raises
+    RuntimeError while the status is set: a workgroup of an earlier call gave
+    up a bounded wait, so what was computed since then is unreliable.
+    Synchronises."""
+    if device is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    _runtime.reset_status(device)
 
 
 class _LRSLinearBase(nn.Module):
@@ -692,6 +704,7 @@ class LRSLinearChain(nn.Module):
             raise ValueError(f"input has {x.shape[-1]} features, expected {self.in_features}")
         if x.device != first.A.device:
             raise ValueError(f"input on {x.device}, weights on {first.A.device}")
+        _runtime.check_status(x.device)
         states = [[mod._kernel() for mod in grp.members] for grp in self.groups]
         outf = [[mod.out_features for mod in grp.members] for grp in self.groups]
         st0 = states[0][0]
@@ -787,6 +800,7 @@ class PreparedChain:
         self.n_stages, self.n_linears = len(states), len(flat)
 
     def run(self, check: bool = False) -> tuple[tuple[torch.Tensor, ...], ...]:
+        _runtime.check_status(self.x.device)
         if check:
             keys = [[mod._weights_key() for mod in grp.members] for grp in self._chain.groups]
             if keys != self._keys:

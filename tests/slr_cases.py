@@ -31,11 +31,10 @@ def make_problem(n, m, r, p, density, dtype, seed=0, skew=False, bias=True, pad=
         rows, cols = orc.random_block_structure(NB, NBK, density, rng)
     vals = rng.standard_normal((len(rows), p, q)) * 0.02
     # zero the padded rows/columns of edge blocks
-    for k, (br, bc) in enumerate(zip(rows, cols)):
-        if (br + 1) * p > n:
-            vals[k, n - br * p:, :] = 0
-        if (bc + 1) * q > m:
-            vals[k, :, m - bc * q:] = 0
+    if n % p:
+        vals[np.asarray(rows) == NB - 1, n % p:, :] = 0
+    if m % q:
+        vals[np.asarray(cols) == NBK - 1, :, m % q:] = 0
     vals = round_to(vals, dtype)
     crow, col, vals = orc.structure_to_bsr(rows, cols, NB, vals)
     A = round_to(rng.standard_normal((n, r)) * 0.02, dtype)
@@ -90,3 +89,31 @@ def make_module(prob, dev, bias=True):
         bias=to_dev(prob["bias"], dt, dev) if (bias and prob["bias"] is not None) else None,
         block_p=prob["p"], block_q=prob["q"],
     )
+
+
+def nm24_matrix(n, m, seed, dtype) -> np.ndarray:
+    """Random 2:4 S (0, 1 or 2 non-zeros in every group of four input features)."""
+    rng = np.random.default_rng(seed)
+    count = rng.choice(3, size=(n, m // 4), p=[0.15, 0.25, 0.6])        # kept per group
+    rank = np.argsort(rng.random((n, m // 4, 4)), axis=-1).argsort(axis=-1)  # random order
+    keep = rank < count[..., None]
+    S = (rng.standard_normal((n, m // 4, 4)) * 0.05 * keep).reshape(n, m)
+    return torch.from_numpy(S).to(dtype).double().numpy()
+
+
+def make_nm_module(n, m, r, dtype, dev, seed, bias=True):
+    """The package's LRSLinear with a 2:4 S, and its (A, B, S, bias) master copies."""
+    from ssalaad_amd import LRSLinear
+
+    rng = np.random.default_rng(seed + 1)
+    A = rng.standard_normal((n, r)) * 0.05
+    B = rng.standard_normal((r, m)) * 0.05
+    b = rng.standard_normal(n) * 0.1 if bias else None
+    A, B = (torch.from_numpy(t).to(dtype).double().numpy() for t in (A, B))
+    if b is not None:
+        b = torch.from_numpy(b).to(dtype).double().numpy()
+    S = nm24_matrix(n, m, seed, dtype)
+    mod = LRSLinear(to_dev(A, dtype, dev), to_dev(B, dtype, dev), to_dev(S, dtype, dev),
+                    in_features=m, out_features=n,
+                    bias=None if b is None else to_dev(b, dtype, dev), nm_n=2, nm_m=4)
+    return mod, (A, B, S, b)

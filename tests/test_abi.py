@@ -427,6 +427,21 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     assert b"exchange" in lib.ssl_last_error()
     # M = 0 is a no-op
     assert slr(M=0) == _lib.SSL_OK
+    # a call that ssl_slr_takes_prefill sends to the prefill kernels needs the
+    # prefill plans, which only the group entry point carries: an fp32 call
+    # whose 64-row tiles fill the device (2048 rows × 16 block-rows of 32)
+    M2, NB2, F32 = 2048, 16, _lib.SSL_F32
+    assert tp(M2, NB2, 32, F32) == 1
+    big = dict(M=M2, m=512, m_pad=512, ldx=512, ldy=512, NB=NB2, p=32, q=32, dtype=F32,
+               workspace=P, workspace_bytes=lib.ssl_slr_workspace_size(M2, NB2, 32, 64, 512, 0, F32),
+               counters=P, n_counters=lib.ssl_slr_counter_count(M2, NB2),
+               exchange=P, exchange_bytes=lib.ssl_slr_exchange_size(M2, 64, 512, F32))
+    assert slr(**big) == _lib.SSL_ERR_INVALID and b"prefill plan" in lib.ssl_last_error()
+    # the same call with a 16-bit dtype and with a row count the kernels stream
+    assert tp(M2, NB2, 32) == 1
+    assert slr(**{**big, "dtype": _lib.SSL_BF16}) == _lib.SSL_ERR_INVALID
+    assert b"prefill plan" in lib.ssl_last_error()
+    assert tp(1024, NB2, 32, F32) == 0
     # the group entry point: 1..4 members
     members = (_lib.SlrMember * 5)()
     rc = lib.ssl_slr_forward_group(P, 64, 1, 64, 64, 64, 64, _lib.SSL_BF16, members, 5, None)

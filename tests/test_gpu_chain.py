@@ -232,11 +232,13 @@ def test_chain_wait_give_up_is_reported_and_words_net_to_zero(M, knobs, gpu_devi
     _runtime.reset_status(gpu_device)
     knobs(_lib.DEBUG_WAIT_POLLS, 64)
     knobs(_lib.DEBUG_WAIT_UNREACHABLE, 1)
-    for _ in range(3):
+    for _ in range(3):  # give-ups on consecutive launches with the same words
         chain(x)
-    torch.cuda.synchronize()
-    assert latent_wait_status(gpu_device) == 1
-    assert _words_at_rest(gpu_device)
+        assert latent_wait_status(gpu_device) == 1
+        assert _words_at_rest(gpu_device)
+        with pytest.raises(RuntimeError, match="gave up waiting"):
+            chain(x)
+        _runtime.reset_status(gpu_device)
     knobs(_lib.DEBUG_WAIT_POLLS, 0)
     knobs(_lib.DEBUG_WAIT_UNREACHABLE, 0)
     _runtime.reset_status(gpu_device)

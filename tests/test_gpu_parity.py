@@ -18,7 +18,8 @@ sys.path.insert(0, str(ROOT / "tests" / "golden"))
 
 from golden_inputs import CASES, make_case  # noqa: E402
 from oracle import slr_oracle as orc  # noqa: E402
-from slr_cases import TOL, err, make_problem, make_x, oracle_y, round_to, sparse_bsr_tensor, to_dev  # noqa: E402
+from slr_cases import (TOL, err, make_nm_module, make_problem, make_x, nm24_matrix,  # noqa: E402
+                       oracle_y, round_to, sparse_bsr_tensor, to_dev)
 
 import ssalaad_amd  # noqa: E402
 from ssalaad_amd import LRSLinear, _lib, _runtime  # noqa: E402
@@ -655,29 +656,8 @@ def test_no_workgroup_gave_up_waiting_for_the_latent(gpu_device):
 # ------------------------------------------------------------ 2:4 (N:M) S --
 
 
-def _nm24(n, m, seed, dtype):
-    """Random 2:4 S (0, 1 or 2 non-zeros in every group of four input features)."""
-    rng = np.random.default_rng(seed)
-    count = rng.choice(3, size=(n, m // 4), p=[0.15, 0.25, 0.6])        # kept per group
-    rank = np.argsort(rng.random((n, m // 4, 4)), axis=-1).argsort(axis=-1)  # random order
-    keep = rank < count[..., None]
-    S = (rng.standard_normal((n, m // 4, 4)) * 0.05 * keep).reshape(n, m)
-    return torch.from_numpy(S).to(dtype).double().numpy()
-
-
-def _nm_module(n, m, r, dtype, dev, seed, bias=True):
-    rng = np.random.default_rng(seed + 1)
-    A = rng.standard_normal((n, r)) * 0.05
-    B = rng.standard_normal((r, m)) * 0.05
-    b = rng.standard_normal(n) * 0.1 if bias else None
-    A, B = (torch.from_numpy(t).to(dtype).double().numpy() for t in (A, B))
-    if b is not None:
-        b = torch.from_numpy(b).to(dtype).double().numpy()
-    S = _nm24(n, m, seed, dtype)
-    mod = LRSLinear(to_dev(A, dtype, dev), to_dev(B, dtype, dev), to_dev(S, dtype, dev),
-                    in_features=m, out_features=n,
-                    bias=None if b is None else to_dev(b, dtype, dev), nm_n=2, nm_m=4)
-    return mod, (A, B, S, b)
+_nm24 = nm24_matrix
+_nm_module = make_nm_module
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])

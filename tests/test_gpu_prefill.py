@@ -129,16 +129,25 @@ def test_forced_tiles_inplace_op(dtype, p, mode, tile, gpu_device):
         assert np.array_equal(got[:, by * p:(by + 1) * p], out0[:, by * p:(by + 1) * p])
 
 
-@pytest.mark.parametrize("n,m,p", [(4096, 2048, 64), (6144, 2048, 64), (2048, 5461, 32),
-                                    (4160, 1024, 32), (1024, 1024, 16)],
+@pytest.mark.parametrize("n,m,p,tiled", [(4096, 2048, 64, False), (6144, 2048, 64, True),
+                                          (2048, 5461, 32, False), (4160, 1024, 32, True),
+                                          (1024, 1024, 16, True)],
                          ids=["p64-64rows", "p64-96rows", "p32-64rows", "p32-130rows", "p16"])
-def test_inplace_op_automatic_routing_at_128_rows(n, m, p, gpu_device):
+def test_inplace_op_automatic_routing_at_128_rows(n, m, p, tiled, gpu_device):
     """The op's own stream-or-tile choice at one token tile pair (128 rows) on
     both sides of its grid boundary: out += x·Sᵀ on the active rows, every
-    other row untouched."""
+    other row untouched. The side each case takes is asserted: the op plans
+    its active rows that hold blocks, and on a 256-CU device one token tile
+    streams when those rows' 64-feature groups number at most a quarter of
+    the CUs (64 groups)."""
+    if torch.cuda.get_device_properties(gpu_device).multi_processor_count != 256:
+        pytest.skip("the sides checked are those of a 256-CU device")
     M, dtype = 128, torch.bfloat16
     prob = make_problem(n, m, 4, p, 0.5, dtype, seed=n + p, pad=True)
     crow32, col32, vt, act = orc.module_buffers(prob["crow"], prob["col"], prob["vals"])
+    planned = int(np.count_nonzero(np.diff(crow32)[act]))
+    lib = _lib.load()
+    assert bool(lib.ssl_bsr_addmm_takes_prefill(M, planned, p, p, _lib.SSL_BF16)) == tiled
     x = make_x(prob, M, seed=7)
     rng = np.random.default_rng(n)
     out0 = torch.from_numpy(rng.standard_normal((M, prob["NB"] * p))).to(dtype).double().numpy()

@@ -62,11 +62,14 @@ def test_wait_give_up_is_reported_and_counters_net_to_zero(M, knobs, gpu_device,
     _runtime.reset_status(gpu_device)
     knobs(_lib.DEBUG_WAIT_POLLS, 64)
     knobs(_lib.DEBUG_WAIT_UNREACHABLE, 1)
-    for _ in range(3):
+    for _ in range(3):  # give-ups on consecutive calls with one plan
         mod(x)
-    torch.cuda.synchronize()
-    assert latent_wait_status(gpu_device) == 1
-    assert _counters_at_rest(gpu_device)
+        assert latent_wait_status(gpu_device) == 1
+        assert _counters_at_rest(gpu_device)
+        # the module refuses to run again until the status is cleared
+        with pytest.raises(RuntimeError, match="gave up waiting"):
+            mod(x)
+        ssalaad_amd.clear_wait_status(gpu_device)
     knobs(_lib.DEBUG_WAIT_POLLS, 0)
     knobs(_lib.DEBUG_WAIT_UNREACHABLE, 0)
     _runtime.reset_status(gpu_device)
@@ -74,6 +77,52 @@ def test_wait_give_up_is_reported_and_counters_net_to_zero(M, knobs, gpu_device,
     torch.cuda.synchronize()
     for y in ys:
         assert err(y, want) <= TOL[dtype]
+    assert latent_wait_status(gpu_device) == 0
+    assert _counters_at_rest(gpu_device)
+
+
+def test_every_entry_point_raises_while_a_give_up_is_reported(knobs, gpu_device):
+    """A give-up forced on one module call (it still returns): once its store
+    has landed, the next call of any module, group, chain or the in-place op
+    on the device raises RuntimeError before launching anything, without the
+    caller synchronising or asking. After clear_wait_status every one of them
+    runs again and is exact."""
+    dtype = torch.bfloat16
+    prob = make_problem(256, 512, 64, 32, 0.5, dtype, seed=21)
+    mod, other = make_module(prob, gpu_device), make_module(prob, gpu_device)
+    nxt = make_module(make_problem(128, 256, 64, 32, 0.5, dtype, seed=22), gpu_device)
+    group = ssalaad_amd.LRSLinearGroup(mod, other)
+    chain = ssalaad_amd.LRSLinearChain([[mod], [nxt]], [mod])
+    x_np = make_x(prob, 4)
+    x = to_dev(x_np, dtype, gpu_device)
+    want = oracle_y(prob, x_np)
+    crow = torch.from_numpy(prob["crow"].astype(np.int32)).to(gpu_device)
+    col = torch.from_numpy(prob["col"].astype(np.int32)).to(gpu_device)
+    vt = mod.S_values
+    act = mod.S_active_rows
+    out = torch.zeros(4, 256, dtype=dtype, device=gpu_device)
+    calls = {
+        "module": lambda: mod(x),
+        "group": lambda: group(x),
+        "chain": lambda: chain(x),
+        "op": lambda: torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_(out, x, crow, col, vt, act),
+    }
+    ssalaad_amd.clear_wait_status(gpu_device)
+    knobs(_lib.DEBUG_WAIT_POLLS, 16)
+    knobs(_lib.DEBUG_WAIT_UNREACHABLE, 1)
+    mod(x)  # returns; its workgroups gave up
+    knobs(_lib.DEBUG_WAIT_POLLS, 0)
+    knobs(_lib.DEBUG_WAIT_UNREACHABLE, 0)
+    torch.cuda.synchronize()  # only so that the store has surely landed
+    for name, call in calls.items():
+        with pytest.raises(RuntimeError, match="gave up waiting"):
+            call()
+    ssalaad_amd.clear_wait_status(gpu_device)
+    for name, call in calls.items():
+        call()
+    torch.cuda.synchronize()
+    assert err(mod(x), want) <= TOL[dtype]
+    assert err(group(x)[1], want) <= TOL[dtype]
     assert latent_wait_status(gpu_device) == 0
     assert _counters_at_rest(gpu_device)
 
@@ -89,11 +138,15 @@ def test_decode_engine_raises_after_a_wait_gave_up(knobs, gpu_device):
     eng.step([1, 2], [0, 0])
     knobs(_lib.DEBUG_WAIT_POLLS, 16)
     knobs(_lib.DEBUG_WAIT_UNREACHABLE, 1)
-    eng.step([3, 4], [1, 1])       # its launches give up; reported at the next step
-    knobs(_lib.DEBUG_WAIT_POLLS, 0)
-    knobs(_lib.DEBUG_WAIT_UNREACHABLE, 0)
-    torch.cuda.synchronize()
     with pytest.raises(RuntimeError, match="gave up waiting"):
+        # its launches give up: an eager step's later launch may already see
+        # the report; the next step sees it at the latest
+        try:
+            eng.step([3, 4], [1, 1])
+        finally:
+            knobs(_lib.DEBUG_WAIT_POLLS, 0)
+            knobs(_lib.DEBUG_WAIT_UNREACHABLE, 0)
+        torch.cuda.synchronize()
         eng.step([5, 6], [2, 2])
     eng.clear_status()
     eng.step([5, 6], [2, 2])

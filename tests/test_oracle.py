@@ -239,6 +239,23 @@ def _random_slr(rng, n, m, r, block, density, bias=True):
     return A, B, crow, col, vals, b
 
 
+@pytest.mark.parametrize("pq", [(16, 16), (32, 16), (16, 48)])
+def test_bsr_to_dense_matches_torch_bsr_to_dense(pq):
+    """The oracle's densification against torch.sparse_bsr_tensor(...).to_dense()
+    on a structure with empty block-rows, a full block-row and repeated values."""
+    p, q = pq
+    rng = np.random.default_rng(p * 100 + q)
+    NB, NBK = 9, 7
+    counts = np.array([0, 3, 7, 0, 1, 5, 2, 0, 4])
+    crow = np.concatenate([[0], np.cumsum(counts)])
+    col = np.concatenate([np.sort(rng.permutation(NBK)[:c]) for c in counts]).astype(np.int64)
+    vals = rng.standard_normal((int(crow[-1]), p, q))
+    vals[2] = vals[1]
+    want = torch.sparse_bsr_tensor(torch.from_numpy(crow), torch.from_numpy(col),
+                                   torch.from_numpy(vals), size=(NB * p, NBK * q)).to_dense()
+    np.testing.assert_array_equal(orc.bsr_to_dense(crow, col, vals, NB * p, NBK * q), want.numpy())
+
+
 def test_slr_linear_matches_the_densified_weight():
     """y = x·(A·B + S)ᵀ + b with S densified independently (the bundle test's formula)."""
     rng = np.random.default_rng(21)
