@@ -46,6 +46,9 @@ headline):
   llama7b_ffn_prefill  the same linear at 2048 tokens (one launch: the latent
                        t = x·Bᵀ workgroups, then the row workgroups for
                        x·Sᵀ + t·Aᵀ + b): TFLOP/s
+  llama7b_lr_prefill   the low-rank share of that linear alone (S = 0: the
+                       two GEMMs x·Bᵀ and t·Aᵀ) at 2048 tokens: TFLOP/s, with
+                       torch's two F.linear calls on the same tensors beside it
   llama7b_ffn_prefill_nm24  the 2:4 projection of llama7b_ffn_decode_nm24 at
                        2048 tokens: TFLOP/s of the dense-equivalent work
                        (x·Bᵀ, t·Aᵀ and the kept half of S)
@@ -405,6 +408,39 @@ def _time_eager(fn, reps):
     return e0.elapsed_time(e1) * 1e3 / reps
 
 
+def eager_calls(layers, M: int, reps: int) -> dict:
+    """The drop-in path's per-call cost: module calls made one by one from
+    Python, as a Hugging Face forward makes them (LRSLinear.forward, eager),
+    against the same calls replayed from a HIP graph. The calls cycle through
+    the 24 layers' gate projections (5461×2048), so the weights stream from
+    HBM. host_issue_us is the host's time to issue one call (no waiting)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(M, 2048, generator=gen).to(torch.bfloat16).to(dev)
+    fns = [lambda md=dict(layer)["gate"]: md(x) for layer in layers]
+    graph_us = _time_graph(fns, reps)
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for f in fns:
+            f()
+    host = time.perf_counter() - t0
+    e1.record()
+    torch.cuda.synchronize()
+    calls = reps * len(fns)
+    eager_us = e0.elapsed_time(e1) * 1e3 / calls
+    return {"eager_call_us": round(eager_us, 3), "graph_call_us": round(graph_us, 3),
+            "host_issue_us": round(host * 1e6 / calls, 3),
+            "eager_overhead_us": round(eager_us - graph_us, 3)}
+
+
 def run_workload(args) -> dict:
     """The non-default workloads (see the module docstring)."""
     import torch
@@ -482,6 +518,42 @@ def run_workload(args) -> dict:
                     roofline={"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
                               "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4), "traffic": None,
                               "flops_per_call": int(fl), "low_rank_flops": 2 * M * r * (m + n)})
+    if args.workload == "llama7b_lr_prefill":
+        # The low-rank share of the same projection alone: S ≡ 0 gives the
+        # low-rank-only module (ls_linear.py:47-54), whose call is the two GEMMs
+        # t = x·Bᵀ, y = t·Aᵀ of ls_linear.py:131 in one launch. torch's own two
+        # F.linear calls (the library GEMMs the reference makes there) are timed
+        # on the same tensors beside it.
+        import torch.nn.functional as F
+
+        from ssalaad_amd import LRSLinear
+
+        M = args.batch if args.batch_set else 2048
+        A = (torch.randn(n, r, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
+        B = (torch.randn(r, m, generator=gen) * 0.02).to(torch.bfloat16).to(dev)
+        mod = LRSLinear(A, B, torch.zeros(n, m, dtype=torch.bfloat16, device=dev),
+                        in_features=m, out_features=n)
+        assert mod.kind == "lr_only"
+        x = torch.randn(M, m, generator=gen).to(torch.bfloat16).to(dev)
+        us = _time_graph([lambda: mod(x)], args.steps)
+        us_call = _time_eager(lambda: mod(x), args.steps)
+        us_lib = _time_graph([lambda: F.linear(F.linear(x, B), A)], args.steps)
+        fl = 2 * M * r * (m + n)
+        tf = fl / us / 1e6
+        byt = 2 * (M * (m + n) + r * (m + n))
+        return dict(base, metric="SLR-linear prefill low-rank share TFLOP/s (LLaMA-7B FFN "
+                    "projection, S = 0)",
+                    value=round(tf, 1), unit="TFLOP/s", ms_per_step=round(us / 1e3, 5),
+                    dtype="bf16",
+                    config={"workload": "llama7b_lr_prefill", "n": n, "m": m, "rank": r,
+                            "batch_tokens": M, "parallelism": "single_gpu"},
+                    roofline={"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
+                              "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4), "traffic": None,
+                              "flops_per_call": int(fl), "compulsory_bytes": int(byt),
+                              "hbm_frac_at_this_time": round(byt / us / 1e3 / HBM_PEAK_GBS, 4)},
+                    details={"call_us_eager": round(us_call, 3), "kernel_us_graph": round(us, 3),
+                             "torch_two_linears_us_graph": round(us_lib, 3),
+                             "torch_two_linears_TFLOPs": round(fl / us_lib / 1e6, 1)})
     if args.workload == "llama7b_ffn_prefill_nm24":
         from ssalaad_amd import LRSLinear
 
@@ -887,6 +959,7 @@ def main():
     ap.add_argument("--workload", default="llama1b_decode",
                     choices=["llama1b_decode", "llama7b_ffn_decode", "llama7b_ffn_prefill",
                              "llama7b_ffn_decode_nm24", "llama7b_ffn_prefill_nm24", "block_topk",
+                             "llama7b_lr_prefill",
                              "llama60m_forward",
                              "llama1b_decode_step", "sweep", "llama1b_prefill"])
     args = ap.parse_args()
@@ -920,6 +993,9 @@ def main():
             "avg_launch_us": round(gm["avg_launch_us"], 3),
             "hbm_frac": round(gm["achieved_gbs"] / HBM_PEAK_GBS, 4)}
         _log(f"[bench] decode M={M}: {gm['ms_step']:.3f} ms/step")
+    for M in (() if args.no_details else (1, 16)):
+        more[f"eager_gate_M{M}"] = eager_calls(layers, M, max(5, args.steps // 2))
+        _log(f"[bench] eager gate calls M={M}: {more[f'eager_gate_M{M}']}")
     if not args.no_details:
         gp = run_gpu(args, layers, M=2048, steps=max(3, args.steps // 10))
         more["prefill_2048"] = {

@@ -737,8 +737,20 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       pm.kpart = (float*)((char*)mb.workspace + L[i].pf_split);
       pm.karrive = mb.counters + L[i].pf_rarrive;
       lat.mb[i] = pm;
-      const PfLatentSplit ls = ksplit > 1 ? prefill_latent_split(M, m_pad, mb.r_pad, dtype)
-                                          : PfLatentSplit{1, (int)(m_pad / ssl_prefill_step_cols(dtype))};
+      const int64_t lat_steps = m_pad / ssl_prefill_step_cols(dtype);
+      PfLatentSplit ls{1, (int)lat_steps};
+      if (ksplit > 1) {
+        ls = prefill_latent_split(M, m_pad, mb.r_pad, dtype);
+      } else if (mb.r_pad > 0) {
+        // whole row groups: the latent splits when it is longer than their
+        // sparse steps and the workspace holds its partial tiles
+        const int64_t group_steps = mb.nnz * block_p / ssl_prefill_step_cols(dtype) /
+                                    (mb.pf_n_groups > 0 ? mb.pf_n_groups : 1);
+        ls = prefill_latent_split_whole(M, m_pad, mb.r_pad, dtype, group_steps, cus);
+        if (ls.split > 1 && mb.workspace_bytes < L[i].pf_split + rows_bytes +
+                                                     prefill_latent_part_bytes(M, mb.r_pad, ls.split))
+          ls = PfLatentSplit{1, (int)lat_steps};
+      }
       lat.mb[i].ksplit = ls.split;
       lat.mb[i].kchunk = ls.chunk;
       lat.mb[i].kpart = (float*)((char*)mb.workspace + L[i].pf_split + rows_bytes);

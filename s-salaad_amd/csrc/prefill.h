@@ -91,6 +91,13 @@ struct PfLatentSplit {
   int split, chunk;
 };
 PfLatentSplit prefill_latent_split(int64_t M, int64_t m_pad, int64_t r_pad, int dtype);
+// The latent's K chunks when the row groups run whole (no K parts): split when
+// the latent is longer than 1.5 times a group's sparse steps (`row_steps`, the
+// member's mean), into chunks about that long.
+PfLatentSplit prefill_latent_split_whole(int64_t M, int64_t m_pad, int64_t r_pad, int dtype,
+                                         int64_t row_steps, int n_cus);
+// Bytes of the latent's fp32 partial tiles in `split` chunks.
+int64_t prefill_latent_part_bytes(int64_t M, int64_t r_pad, int split);
 // Workspace bytes the partial tiles of both splits may take for a member.
 int64_t prefill_split_bytes(int64_t M, int64_t NB, int block_p, int64_t m_pad, int64_t r_pad,
                             int dtype, int n_cus);

@@ -80,6 +80,36 @@ __device__ __forceinline__ uint4 keep_first(uint4 v, int valid) {
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// 16 bytes of an activation-dtype array (16 / EB elements from element `off`,
+// 16-byte aligned) as fp32, and back (rounded once to the dtype).
+template <int DT>
+__device__ __forceinline__ void ld16(const void* base, int64_t off, float* v) {
+  if constexpr (DT == DT_F32) {
+    const float4 q = *(const float4*)((const float*)base + off);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else {
+    const uint4 q = *(const uint4*)((const uint16_t*)base + off);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = (uint16_t)(w[i] & 0xffffu), hi = (uint16_t)(w[i] >> 16);
+      v[2 * i] = DT == DT_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+      v[2 * i + 1] = DT == DT_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+    }
+  }
+}
+template <int DT>
+__device__ __forceinline__ void st16(void* base, int64_t off, const float* v) {
+  if constexpr (DT == DT_F32) {
+    *(float4*)((float*)base + off) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = to_bits<DT>(v[2 * i]) | (to_bits<DT>(v[2 * i + 1]) << 16);
+    *(uint4*)((uint16_t*)base + off) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // Element i of an activation-dtype array as fp32 bits stored back.
 template <int DT>
 __device__ __forceinline__ void store_elem(void* base, int64_t i, float v) {
@@ -739,55 +769,78 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
     if (tid < kPfCntCopies)
       __hip_atomic_fetch_add(tcnt + ((int64_t)(m0 / BM) * kPfCntCopies + tid) * kPfCntStride, 1,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else if constexpr (NM) {
-    // lane (c, gq) holds features 4gq + e of feature tile nt for token 16·mt + c
-    void* const y_out = mb.y;
-    const int64_t ldy = mb.ldy;
+  } else {
+    // Rows: the finished tile goes through LDS as fp32 ([BM token rows][BN + 4
+    // features], the bias added for the fused linear), then out 16 bytes per
+    // lane, consecutive lanes along a token row's features, so a wave writes
+    // whole 128-byte feature runs. (Stored straight from the MFMA layout, one
+    // 2-byte element per lane, a wave's store covered four rows in 32-byte
+    // pieces, and the epilogue took as long as four low-rank steps.)
+    constexpr int LDT = BN + 4;  // floats per staged row; the padding spreads the banks
+    static_assert(BM * LDT * 4 <= T::LDS * 2 * 2, "the staged tile fits in the stages' LDS");
+    float* const stg = reinterpret_cast<float*>(&lds[0][0]);
     const void* const bias = mb.bias;
+    __syncthreads();  // every wave is past its last read of the stages
 #pragma unroll
     for (int nt = 0; nt < NTI; ++nt) {
-      const int fl = wn * T::TN + 16 * nt + 4 * gq;
       const int row = ld_word(gr, 2 + (wn * T::TN + 16 * nt) / P);
       if (row < 0) continue;
-      const int col = row * P + fl % P;
-      float bv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (bias != nullptr) {
+      if constexpr (NM) {
+        // lane (c, gq) holds features 4gq + e of feature tile nt for token 16·mt + c
+        const int fl = wn * T::TN + 16 * nt + 4 * gq;
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (bias != nullptr) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bv[e] = load_scalar<DT>(bias, col + e);
-      }
+          for (int e = 0; e < 4; ++e) bv[e] = load_scalar<DT>(bias, row * P + fl % P + e);
+        }
 #pragma unroll
-      for (int mt = 0; mt < MTI; ++mt) {
-        const int r = m0 + wm * T::TM + 16 * mt + c;
-        if (r >= M) continue;
-        const float o[4] = {acc[mt][nt][0] + bv[0], acc[mt][nt][1] + bv[1], acc[mt][nt][2] + bv[2],
-                            acc[mt][nt][3] + bv[3]};
-        st_w<DT, 4>(y_out, (int64_t)r * ldy + col, o);
+        for (int mt = 0; mt < MTI; ++mt) {
+          float* const d = stg + (wm * T::TM + 16 * mt + c) * LDT + fl;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) d[e] = acc[mt][nt][e] + bv[e];
+        }
+      } else {
+        // lane (c, gq) holds token rows 16·mt + 4gq + e of feature 16·nt + c
+        const int f = wn * T::TN + 16 * nt + c;
+        float bv = 0.f;
+        if (KIND == K_ROWS_FUSED && bias != nullptr) bv = load_scalar<DT>(bias, row * P + f % P);
+#pragma unroll
+        for (int mt = 0; mt < MTI; ++mt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            stg[(wm * T::TM + 16 * mt + 4 * gq + e) * LDT + f] = acc[mt][nt][e] + bv;
       }
     }
-  } else {
+    __syncthreads();
     void* const y_out = mb.y;
     const int64_t ldy = mb.ldy;
-    const void* const bias = mb.bias;
+    constexpr int CO = 16 / EB;   // outputs per 16-byte store
+    constexpr int CPR = BN / CO;  // stores per token row of the tile
+    int srow[G];                  // the slots' block-rows (−1: absent)
 #pragma unroll
-    for (int nt = 0; nt < NTI; ++nt) {
-      const int f = wn * T::TN + 16 * nt + c;
-      const int row = ld_word(gr, 2 + (wn * T::TN + 16 * nt) / P);
+    for (int g = 0; g < G; ++g) srow[g] = ld_word(gr, 2 + g);
+    const int rows_here = min(BM, M - m0);
+    for (int q = tid; q < rows_here * CPR; q += kPfThreads) {
+      const int tr = q / CPR, f0 = (q % CPR) * CO;
+      int row = srow[0];
+#pragma unroll
+      for (int g = 1; g < G; ++g) row = (f0 / P == g) ? srow[g] : row;
       if (row < 0) continue;
-      const int col = row * P + f % P;
-      float bv = 0.f;
-      if (KIND == K_ROWS_FUSED && bias != nullptr) bv = load_scalar<DT>(bias, col);
+      const int64_t yi = (int64_t)(m0 + tr) * ldy + row * P + f0 % P;
+      float o[CO];
+      const float* const sp = stg + tr * LDT + f0;
 #pragma unroll
-      for (int mt = 0; mt < MTI; ++mt)
+      for (int i = 0; i < CO; i += 4) {
+        const float4 v = *(const float4*)(sp + i);
+        o[i] = v.x; o[i + 1] = v.y; o[i + 2] = v.z; o[i + 3] = v.w;
+      }
+      if constexpr (KIND == K_ROWS_OP) {  // the op accumulates onto out in fp32
+        float old[CO];
+        ld16<DT>(y_out, yi, old);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = m0 + wm * T::TM + 16 * mt + 4 * gq + e;
-          if (r >= M) continue;
-          const int64_t yi = (int64_t)r * ldy + col;
-          float o = acc[mt][nt][e];
-          if constexpr (KIND == K_ROWS_FUSED) o += bv;
-          else o += load_scalar<DT>(y_out, yi);
-          store_elem<DT>(y_out, yi, o);
-        }
+        for (int i = 0; i < CO; ++i) o[i] += old[i];
+      }
+      st16<DT>(y_out, yi, o);
     }
   }
   depart();
@@ -951,21 +1004,56 @@ PfLatentSplit prefill_latent_split(int64_t M, int64_t m_pad, int64_t r_pad, int 
   return r;
 }
 
+// The latent's K chunks when the row groups run whole. A row workgroup waits
+// for its token rows' latent tiles after its own sparse steps, so a latent
+// longer than that (a call with few blocks, or none: S = 0) is the rows'
+// critical path: its in_features split into chunks about a group's sparse
+// steps long (at least 16 steps), at most twice the CUs' worth of latent
+// workgroups, 16 chunks a tile and 64 rank tiles. Within 1.5 times a group's
+// steps the exchange of partials would cost more than it saves.
+PfLatentSplit prefill_latent_split_whole(int64_t M, int64_t m_pad, int64_t r_pad, int dtype,
+                                         int64_t row_steps, int n_cus) {
+  const int64_t ks = dtype == SSL_F32 ? 32 : 64;  // in_features per step
+  const int64_t steps = m_pad / ks;
+  const int64_t tiles = (M + kPrefillLatentRows - 1) / kPrefillLatentRows * (r_pad / 64);
+  PfLatentSplit r{1, (int)steps};
+  if (tiles <= 0 || r_pad / 64 > 64) return r;
+  const int64_t target = row_steps > 16 ? row_steps : 16;
+  if (2 * steps <= 3 * target) return r;
+  int64_t n = (steps + target - 1) / target;
+  if (n > 16) n = 16;
+  if (n > 2 * (int64_t)n_cus / tiles) n = 2 * (int64_t)n_cus / tiles;
+  if (n <= 1) return r;
+  const int64_t chunk = (steps + n - 1) / n;
+  r.split = (int)((steps + chunk - 1) / chunk);
+  r.chunk = (int)chunk;
+  return r;
+}
+
 int64_t prefill_split_bytes(int64_t M, int64_t NB, int block_p, int64_t m_pad, int64_t r_pad,
                             int dtype, int n_cus) {
   if (M < kPrefillMinM || NB <= 0) return 0;
   const int64_t groups = (NB + 64 / block_p - 1) / (64 / block_p);
-  // no split when even the tall tile's grid gives two workgroups per CU
-  if (((M + 255) / 256) * groups >= 2 * (int64_t)n_cus && debug_knobs().prefill_split == 0) return 0;
-  int64_t tiles = 4 * ((M + 63) / 64) * groups;  // part tiles: 4 parts of 64-row tiles at most
-  if (tiles > 4 * (int64_t)n_cus) tiles = 4 * (int64_t)n_cus;  // automatic splits: < 4 CUs' worth
-  const int64_t rows = tiles * 128 * 64 * 4;  // at most 128 × 64 fp32 a part
-  const PfLatentSplit ls = prefill_latent_split(M, m_pad, r_pad, dtype);
-  const int64_t lat = ls.split > 1 ? 4LL * kLatentPartFloats * ls.split *
-                                         ((M + kPrefillLatentRows - 1) / kPrefillLatentRows) *
-                                         (r_pad / 64)
-                                   : 0;
+  int64_t rows = 0;
+  // row parts only while even the tall tile's grid gives fewer than two
+  // workgroups per CU
+  if (((M + 255) / 256) * groups < 2 * (int64_t)n_cus || debug_knobs().prefill_split != 0) {
+    int64_t tiles = 4 * ((M + 63) / 64) * groups;  // part tiles: 4 parts of 64-row tiles at most
+    if (tiles > 4 * (int64_t)n_cus) tiles = 4 * (int64_t)n_cus;  // automatic splits: < 4 CUs' worth
+    rows = tiles * 128 * 64 * 4;  // at most 128 × 64 fp32 a part
+  }
+  // the latent's chunks: the most either policy takes (whole rows: a group
+  // without sparse steps)
+  int split = prefill_latent_split(M, m_pad, r_pad, dtype).split;
+  const int whole = prefill_latent_split_whole(M, m_pad, r_pad, dtype, 0, n_cus).split;
+  if (whole > split) split = whole;
+  const int64_t lat = split > 1 ? prefill_latent_part_bytes(M, r_pad, split) : 0;
   return rows + lat;
+}
+
+int64_t prefill_latent_part_bytes(int64_t M, int64_t r_pad, int split) {
+  return 4LL * kLatentPartFloats * split * ((M + kPrefillLatentRows - 1) / kPrefillLatentRows) *
+         (r_pad / 64);
 }
 
 int prefill_group(int64_t M, int64_t n_rows, int block_p, int n_cus) {

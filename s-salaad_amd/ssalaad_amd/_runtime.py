@@ -255,7 +255,7 @@ _STATUS: dict[int, "StatusWord"] = {}
 
 def _key(device: torch.device) -> tuple[int, int]:
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    return (idx, torch.cuda.current_stream(device).cuda_stream)
+    return (idx, torch._C._cuda_getCurrentRawStream(idx))
 
 
 def _grown(pool, key, n, dtype, device, minimum):

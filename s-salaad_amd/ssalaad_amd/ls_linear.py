@@ -111,6 +111,8 @@ class _KernelState:
         bq = getattr(mod, "block_q", None) or q
         self.NBK = -(-m // bq) * (bq // q)
         self._plans: dict[int, _runtime.DevicePlan] = {}
+        # fused calls led by this state: (M, stream, linears) -> _LaunchCall
+        self._calls: dict[tuple, "_LaunchCall"] = {}
         self._pf_plans: dict[int, _runtime.DevicePrefillPlan] = {}
         self._values_pq: torch.Tensor | None = None
 
@@ -225,50 +227,83 @@ def _launch_shares(states, stages) -> list[tuple[int, int] | None]:
     return out
 
 
+class _Descriptors:
+    """The C-ABI member descriptors of a fused call of M token rows over
+    `states`: plans, sizes and weight pointers are set once; `bind` points
+    them at the stream's scratch pools and the plans' exchange areas, `rebind`
+    repeats that only when one of those buffers was replaced (a pool that
+    grew), and the caller fills in each member's `y`. `extra_counters` more
+    int32 counters follow the members' (bind returns their address).
+    `stages`: member counts of a chained launch's stages."""
+
+    __slots__ = ("states", "M", "G", "plans", "ws_need", "cnt_need", "xch_need", "extra",
+                 "members", "_ws", "_cnt", "_xch", "_extra_ptr")
+
+    def __init__(self, states, M: int, G: int, extra_counters: int = 0,
+                 stages: list[int] | None = None) -> None:
+        lib = _lib.load()
+        self.states, self.M, self.G, self.extra = list(states), M, G, extra_counters
+        # the 2:4 row split budgets the slots of each launch (a grouped launch,
+        # or a chained launch's stage) as a whole
+        self.plans = [st.plan(M, launch) for st, launch in zip(states, _launch_shares(states, stages))]
+        self.ws_need = [_round_up(lib.ssl_slr_workspace_size(M, st.NB, st.p, st.r_pad, st.m_pad,
+                                                             pl.n_slots, st.dtype_code), 256)
+                        for st, pl in zip(states, self.plans)]
+        self.cnt_need = [int(lib.ssl_slr_counter_count(M, st.NB)) for st in states]
+        self.xch_need = [int(lib.ssl_slr_exchange_size(M, st.r_pad, st.m_pad, st.dtype_code))
+                         for st in states]
+        self.members = (_lib.SlrMember * len(states))()
+        for i, (st, pl) in enumerate(zip(states, self.plans)):
+            mb = self.members[i]
+            mb.A, mb.B, mb.bias = st.A.data_ptr(), st.B.data_ptr(), _lib.ptr(st.bias)
+            mb.col, mb.values = st.col.data_ptr(), st.values.data_ptr()
+            mb.plan, mb.n_chunks, mb.n_slots = pl.table.data_ptr(), pl.n_chunks, pl.n_slots
+            mb.lr_wgs, mb.NB, mb.r_pad = pl.lr_wgs, st.NB, st.r_pad
+            mb.n_counters = self.cnt_need[i]
+            mb.workspace_bytes = self.ws_need[i]
+            mb.nnz = st.nblk_total
+            mb.s_format = st.s_format
+            mb.ldy = st.n_pad
+            if G:
+                pp = st.prefill_plan(G)
+                mb.pf_groups, mb.pf_steps = pp.groups.data_ptr(), pp.steps.data_ptr()
+                mb.pf_n_groups, mb.pf_group = pp.n_groups, pp.group
+                mb.values_pq = _lib.ptr(st._values_pq)
+        self._ws = self._cnt = None
+        self._xch: list = [None] * len(states)
+        self._extra_ptr = 0
+
+    def bind(self, dev: torch.device) -> int:
+        ws = _runtime.workspace(dev, sum(self.ws_need))
+        cnt = _runtime.counters(dev, sum(self.cnt_need) + self.extra)
+        xch = [pl.exchange(nb) for pl, nb in zip(self.plans, self.xch_need)]
+        if (ws is not self._ws or cnt is not self._cnt
+                or any(a is not b for a, b in zip(xch, self._xch))):
+            status = _runtime.status_word(dev).device_ptr
+            ws_off = cnt_off = 0
+            for i, mb in enumerate(self.members):
+                mb.counters = cnt.data_ptr() + 4 * cnt_off
+                mb.exchange, mb.exchange_bytes = xch[i].data_ptr(), xch[i].numel()
+                mb.workspace = ws.data_ptr() + ws_off
+                mb.status = status
+                ws_off += self.ws_need[i]
+                cnt_off += self.cnt_need[i]
+            self._ws, self._cnt, self._xch = ws, cnt, xch
+            self._extra_ptr = cnt.data_ptr() + 4 * cnt_off
+        return self._extra_ptr
+
+
 def _members(states: list["_KernelState"], ys: list[torch.Tensor], M: int, G: int,
              extra_counters: int = 0, stages: list[int] | None = None):
     """The C-ABI member descriptors of a fused call of M token rows writing
     `ys`, with workspaces and zero-at-rest counters from the stream's pools;
     `extra_counters` more int32 counters follow the members' (their address is
     returned too). `stages`: member counts of a chained launch's stages."""
-    lib = _lib.load()
-    dev = ys[0].device
-    # the 2:4 row split budgets the slots of each launch (a grouped launch, or a
-    # chained launch's stage) as a whole
-    plans = [st.plan(M, launch) for st, launch in zip(states, _launch_shares(states, stages))]
-    ws_need = [_round_up(lib.ssl_slr_workspace_size(M, st.NB, st.p, st.r_pad, st.m_pad,
-                                                    pl.n_slots, st.dtype_code), 256)
-               for st, pl in zip(states, plans)]
-    cnt_need = [lib.ssl_slr_counter_count(M, st.NB) for st in states]
-    ws = _runtime.workspace(dev, sum(ws_need))
-    cnt = _runtime.counters(dev, sum(cnt_need) + extra_counters)
-    status = _runtime.status_word(dev).device_ptr
-    members = (_lib.SlrMember * len(states))()
-    ws_off = cnt_off = 0
-    for i, (st, pl, y) in enumerate(zip(states, plans, ys)):
-        xch = pl.exchange(lib.ssl_slr_exchange_size(M, st.r_pad, st.m_pad, st.dtype_code))
-        mb = members[i]
+    d = _Descriptors(states, M, G, extra_counters, stages)
+    extra = d.bind(ys[0].device)
+    for mb, y in zip(d.members, ys):
         mb.y, mb.ldy = y.data_ptr(), y.stride(0)
-        mb.A, mb.B, mb.bias = st.A.data_ptr(), st.B.data_ptr(), _lib.ptr(st.bias)
-        mb.col, mb.values = st.col.data_ptr(), st.values.data_ptr()
-        mb.plan, mb.n_chunks, mb.n_slots = pl.table.data_ptr(), pl.n_chunks, pl.n_slots
-        mb.lr_wgs, mb.NB, mb.r_pad = pl.lr_wgs, st.NB, st.r_pad
-        mb.counters = cnt.data_ptr() + 4 * cnt_off
-        mb.n_counters = cnt_need[i]
-        mb.exchange, mb.exchange_bytes = xch.data_ptr(), xch.numel()
-        mb.workspace = ws.data_ptr() + ws_off
-        mb.workspace_bytes = ws_need[i]
-        mb.nnz = st.nblk_total
-        mb.s_format = st.s_format
-        mb.status = status
-        if G:
-            pp = st.prefill_plan(G)
-            mb.pf_groups, mb.pf_steps = pp.groups.data_ptr(), pp.steps.data_ptr()
-            mb.pf_n_groups, mb.pf_group = pp.n_groups, pp.group
-            mb.values_pq = _lib.ptr(st._values_pq)
-        ws_off += ws_need[i]
-        cnt_off += cnt_need[i]
-    return members, cnt.data_ptr() + 4 * cnt_off
+    return d.members, extra
 
 
 def _outputs(states, ys, out_features, lead: tuple) -> list[torch.Tensor]:
@@ -280,24 +315,41 @@ def _outputs(states, ys, out_features, lead: tuple) -> list[torch.Tensor]:
     return outs
 
 
+_MAX_CALLS = 16  # cached launch descriptors per leading state
+
+
 def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[int]):
-    """One fused launch computing every state's linear of the same x."""
-    _runtime.check_status(x.device)
+    """One fused launch computing every state's linear of the same x.
+
+    The descriptors of a call (plans, sizes, weight pointers, prefill plans)
+    are built once per (token count, stream, linears) and kept on the leading
+    state, which is rebuilt whenever a module's weights change; a call fills
+    in x and the outputs only."""
+    dev = x.device
+    _runtime.check_status(dev)
     st0 = states[0]
     orig = x.shape
     x2 = st0.rows(x)
     M = x2.shape[0]
-    ys = [torch.empty(M, st.n_pad, dtype=x.dtype, device=x.device) for st in states]
+    ys = [torch.empty(M, st.n_pad, dtype=x.dtype, device=dev) for st in states]
     if M > 0:
         lib = _lib.load()
-        G = 0
-        if st0.takes_prefill(M, sum(st.NB for st in states)):
-            G = int(lib.ssl_prefill_group(M, sum(st.NB for st in states), st0.p, st0.q))
-        members, _ = _members(states, ys, M, G)
-        rc = lib.ssl_slr_forward_group(
-            x2.data_ptr(), x2.stride(0), M, st0.m, st0.m_pad, st0.p, st0.q, st0.dtype_code,
-            members, len(states), _lib.stream_ptr(x.device),
-        )
+        stream = _lib.stream_ptr(dev)
+        key = (M, stream, tuple(map(id, states)))
+        d = st0._calls.get(key)  # its states are held, so their ids are not reused
+        if d is None or any(a is not b for a, b in zip(d.states, states)):
+            G = 0
+            rows = sum(st.NB for st in states)
+            if st0.takes_prefill(M, rows):
+                G = int(lib.ssl_prefill_group(M, rows, st0.p, st0.q))
+            if len(st0._calls) >= _MAX_CALLS:
+                st0._calls.clear()
+            d = st0._calls[key] = _Descriptors(states, M, G)
+        d.bind(dev)
+        for mb, y in zip(d.members, ys):
+            mb.y = y.data_ptr()
+        rc = lib.ssl_slr_forward_group(x2.data_ptr(), x2.stride(0), M, st0.m, st0.m_pad, st0.p,
+                                       st0.q, st0.dtype_code, d.members, len(states), stream)
         _lib.check(rc, "ssl_slr_forward_group")
     return _outputs(states, ys, out_features, orig[:-1])
 

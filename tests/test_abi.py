@@ -309,9 +309,11 @@ def test_workspace_sizes_are_aligned_and_monotone():
     # ([MG][slots][16·MT][p]); each part 256-byte aligned
     assert a == 8 * 16 * 256 * 4 + 16 * 256 * 2
     assert b == a + 100 * 16 * 64 * 4
-    # 2048 rows: no latent K split (the prefill kernels run the latent in the
-    # row launch, whole), the final latent and the split-row partials
-    assert c == 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4
+    # 2048 rows: the final latent, the split-row partials and room for the
+    # latent's K chunks when the row groups run whole (4096 in_features, 64
+    # steps, in chunks of at least 16, at most twice the CUs' worth: 4 chunks
+    # of 32 token tiles × 4 rank tiles, 64 × 64 fp32 each)
+    assert c == 2048 * 256 * 2 + 32 * 10 * 64 * 64 * 4 + 4 * 32 * 4 * 64 * 64 * 4
     # 256 rows of 4096×11008 (64 block-rows): room for the split row groups'
     # partial tiles (up to 4 parts of 64-row tiles, at most 4 per CU, 128 × 64
     # fp32 each) and the latent's K chunks (172 steps in 11 chunks of 16, 16

@@ -25,7 +25,7 @@ import zlib
 import pytest
 import torch
 
-from slr_cases import TOL, err, make_module, make_problem, make_x, oracle_y, to_dev
+from slr_cases import TOL, err, make_module, make_problem, make_x, oracle_y, round_to, to_dev
 
 from ssalaad_amd import _runtime
 from ssalaad_amd.ls_linear import latent_wait_status
@@ -91,3 +91,35 @@ def test_skewed_structures(case, M, gpu_device):
     p, d = case
     _check(("skew", p, d), 4096, 11008, 128, p, d, True, M, gpu_device)
 
+
+
+@pytest.mark.parametrize("M", [128, 256, 2048])
+def test_low_rank_only_llama7b_ffn(M, gpu_device):
+    """S = 0 (the low-rank-only module, ssalaad/efficient/ls_linear.py:47-54) at
+    the 7B FFN shape: the latent over 4096 in_features is the rows' whole wait,
+    so it splits into K chunks whose fp32 partials are summed in chunk order."""
+    import numpy as np
+
+    from oracle import slr_oracle as orc
+    from ssalaad_amd import LRSLinear
+
+    n, m, r = 11008, 4096, 256
+    rng = np.random.default_rng(M)
+    A = round_to(rng.standard_normal((n, r)) * 0.02, torch.bfloat16)
+    B = round_to(rng.standard_normal((r, m)) * 0.02, torch.bfloat16)
+    b = round_to(rng.standard_normal(n) * 0.1, torch.bfloat16)
+    x = round_to(rng.standard_normal((M, m)), torch.bfloat16)
+    dev = gpu_device
+    mod = LRSLinear(to_dev(A, torch.bfloat16, dev), to_dev(B, torch.bfloat16, dev),
+                    torch.zeros(n, m, dtype=torch.bfloat16, device=dev), in_features=m,
+                    out_features=n, bias=to_dev(b, torch.bfloat16, dev))
+    assert mod.kind == "lr_only"
+    print(f"[config] lr-only 11008x4096 r256 M={M}", flush=True)
+    y1, y2 = mod(to_dev(x, torch.bfloat16, dev)), mod(to_dev(x, torch.bfloat16, dev))
+    torch.cuda.synchronize()
+    want = orc.slr_linear(x, A, B, np.zeros((n, m)), b)
+    assert err(y1, want) <= TOL[torch.bfloat16]
+    assert torch.equal(y1, y2)
+    assert latent_wait_status(dev) == 0
+    assert all(int(buf.abs().max()) == 0 for (idx, _), buf in _runtime._COUNTERS.items()
+               if idx == dev.index)
