@@ -155,6 +155,25 @@ int ssl_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB
  * ssl_prefill_step_ints is 0 otherwise). The structure is checked as for
  * ssl_plan_build. */
 int32_t ssl_prefill_step_ints(int32_t block_p, int32_t group, int32_t step_cols);
+/* Balanced K parts of a prefill plan's row groups (no reference counterpart:
+ * the reference walks each block-row serially,
+ * ssalaad/tilelang_sparse/addmm_inplace.py:74). A row workgroup runs its
+ * group's sparse steps in a row, so with a skewed structure (per-row block
+ * counts far from even) the longest group sets the time of a call whose row
+ * workgroups all fit on the device at once. From the group table of
+ * ssl_prefill_plan_build (n_groups records of 2 + group int32), this cuts every
+ * group into parts of about the mean group's steps (at least 32, at most 16
+ * parts a group), when the longest group holds more than twice that; else it
+ * returns no records (*n_parts = 0). Records are 8 int32 each, in group order:
+ * {group, step_begin, step_end, part, parts, first split part, 0, 0};
+ * *split_parts counts the parts of the groups cut in more than one. Call with
+ * NULL output for the counts. */
+int ssl_prefill_parts_build(const int32_t* groups_host, int64_t n_groups, int32_t group,
+                            int32_t* parts_out, int64_t parts_capacity, int64_t* n_parts,
+                            int64_t* split_parts);
+/* Workspace bytes the partial tiles of split_parts parts take in a call of M
+ * token rows (fp32 tiles of up to 128 token rows × 64 output features). */
+int64_t ssl_prefill_parts_bytes(int64_t M, int64_t split_parts);
 int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, int64_t NB,
                            int64_t NBK, const int32_t* rows_host, int64_t n_rows, int32_t block_p,
                            int32_t group, int32_t step_cols, int32_t* groups_out,
@@ -323,6 +342,18 @@ typedef struct ssl_slr_member {
    * cleared by the library). NULL: the first uint64 of `exchange`. Sharing one
    * word between every call lets a host check all of them at once. */
   uint64_t* status;
+  /* optional, prefill kernels with block storage: the part table of the
+   * prefill plan (a device copy of ssl_prefill_parts_build's records for the
+   * same pf_groups), NULL for none. A call whose row groups would otherwise
+   * run whole then gives each workgroup one record: the long groups of a
+   * skewed structure run in parts of about the mean group's steps, summed in
+   * part order by the last part to arrive. It needs ssl_prefill_parts_bytes(M,
+   * pf_split_parts) more workspace bytes past ssl_slr_workspace_size's; with
+   * less, or when the call splits every group evenly instead, the table is
+   * not used. */
+  const int32_t* pf_parts;
+  int64_t pf_n_parts;
+  int64_t pf_split_parts;
 } ssl_slr_member;
 
 typedef enum { SSL_S_BSR = 0, SSL_S_NM24 = 1 } ssl_s_format;

@@ -437,6 +437,11 @@ int32_t ssl_slr_takes_prefill(int64_t M, int64_t n_rows, int32_t block_p, int32_
   return 1;
 }
 
+int64_t ssl_prefill_parts_bytes(int64_t M, int64_t split_parts) {
+  if (M <= 0 || split_parts <= 0) return 0;
+  return align_up(split_parts * ((M + 127) / 128 * 128) * 64 * 4, 256);
+}
+
 int64_t ssl_nm24_block_bytes(void) { return kNmBlockBytes; }
 
 int64_t ssl_nm24_prefill_block_bytes(void) { return kNmPrefillBlockBytes; }
@@ -705,6 +710,24 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
         ksplit = 1;
       }
     }
+    // Part tables (skewed structures): when the groups run whole and the
+    // tall grid takes at most two rounds of the device, a member whose part
+    // table and partial tiles fit runs its long groups in parts. Partial
+    // tiles are kept for the narrow and short tiles only, so a tall call
+    // takes the narrow one.
+    bool parts = false;
+    if (ksplit == 1 && knobs.prefill_split == 0 && knobs.prefill_group != 2) {
+      int64_t tall = 0;
+      for (int i = 0; i < n_members; ++i)
+        if (members[i].NB > 0) tall += members[i].pf_n_groups * ((M + 255) / 256);
+      for (int i = 0; i < n_members && tall <= 4 * (int64_t)cus; ++i) {
+        const ssl_slr_member& mb = members[i];
+        if (mb.NB > 0 && mb.pf_parts && mb.pf_n_parts > 0 &&
+            mb.workspace_bytes >= L[i].total + ssl_prefill_parts_bytes(M, mb.pf_split_parts))
+          parts = true;
+      }
+      if (parts && rows.bm == 256) rows.bm = 128;
+    }
     int64_t items = 0, litems = 0;
     for (int i = 0; i < n_members; ++i) {
       const ssl_slr_member& mb = members[i];
@@ -737,6 +760,7 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       pm.kpart = (float*)((char*)mb.workspace + L[i].pf_split);
       pm.karrive = mb.counters + L[i].pf_rarrive;
       lat.mb[i] = pm;
+      lat.mb[i].parts = nullptr;
       const int64_t lat_steps = m_pad / ssl_prefill_step_cols(dtype);
       PfLatentSplit ls{1, (int)lat_steps};
       if (ksplit > 1) {
@@ -754,7 +778,19 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       lat.mb[i].ksplit = ls.split;
       lat.mb[i].kchunk = ls.chunk;
       lat.mb[i].kpart = (float*)((char*)mb.workspace + L[i].pf_split + rows_bytes);
-      items += mb.pf_n_groups * T * ksplit;
+      if (parts && mb.pf_parts && mb.pf_n_parts > 0 &&
+          mb.workspace_bytes >= L[i].total + ssl_prefill_parts_bytes(M, mb.pf_split_parts)) {
+        if (mb.pf_n_parts < mb.pf_n_groups || mb.pf_split_parts < 0 ||
+            mb.pf_split_parts > mb.pf_n_parts || mb.pf_n_parts > 0x7fffffffLL / 8)
+          return fail(SSL_ERR_INVALID, "linear %d: part table sizes do not fit its plan", i);
+        pm.parts = mb.pf_parts;
+        pm.n_parts = (int)mb.pf_n_parts;
+        pm.split_parts = (int)mb.pf_split_parts;
+        pm.kpart = (float*)((char*)mb.workspace + L[i].total);
+        items += mb.pf_n_parts * T;
+      } else {
+        items += mb.pf_n_groups * T * ksplit;
+      }
       if (mb.r_pad > 0) litems += TL * (mb.r_pad / 64) * ls.split;
       if (items > 0x7fffffffLL / 8 || litems > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "grid too large");
     }

@@ -26,6 +26,13 @@
 
 namespace ssl {
 
+// Part tables of prefill plans (ssl_prefill_parts_build): record size, the
+// shortest part worth its exchange of partial tiles, the most parts a group
+// takes.
+constexpr int64_t kPartRecordInts = 8;
+constexpr int64_t kPartMinSteps = 32;
+constexpr int64_t kMaxParts = 16;
+
 static thread_local std::string g_last_error;
 static DebugKnobs g_knobs{};
 
@@ -287,6 +294,60 @@ int ssl_prefill_plan_build(const int32_t* crow_host, const int32_t* col_host, in
   }
   *n_groups = ng;
   *n_steps = ns;
+  return SSL_OK;
+}
+
+int ssl_prefill_parts_build(const int32_t* groups_host, int64_t n_groups, int32_t group,
+                            int32_t* parts_out, int64_t parts_capacity, int64_t* n_parts,
+                            int64_t* split_parts) {
+  clear_error();
+  if (!n_parts || !split_parts || n_groups < 0 || group < 1 || group > 4 ||
+      (n_groups > 0 && !groups_host) || (parts_out && parts_capacity < 0))
+    return fail(SSL_ERR_INVALID, "invalid part table arguments");
+  *n_parts = 0;
+  *split_parts = 0;
+  const int64_t gstride = 2 + group;
+  int64_t total = 0, longest = 0, prev_end = 0;
+  for (int64_t g = 0; g < n_groups; ++g) {
+    const int64_t b = groups_host[g * gstride], e = groups_host[g * gstride + 1];
+    if (b != prev_end || e < b) return fail(SSL_ERR_INVALID, "group %lld: step ranges must tile the plan", (long long)g);
+    prev_end = e;
+    total += e - b;
+    if (e - b > longest) longest = e - b;
+  }
+  if (n_groups == 0) return SSL_OK;
+  // parts of about the mean group's steps (at least kPartMinSteps), only for
+  // structures whose longest group is more than twice that
+  const int64_t mean = (total + n_groups - 1) / n_groups;
+  const int64_t target = mean > kPartMinSteps ? mean : kPartMinSteps;
+  if (longest <= 2 * target) return SSL_OK;
+  int64_t np = 0, sp = 0;
+  for (int64_t g = 0; g < n_groups; ++g) {
+    const int64_t b = groups_host[g * gstride], n = groups_host[g * gstride + 1] - b;
+    int64_t k = (n + target - 1) / target;
+    if (k < 1) k = 1;
+    if (k > kMaxParts) k = kMaxParts;
+    const int64_t chunk = k > 1 ? (n + k - 1) / k : n;
+    if (k > 1) k = (n + chunk - 1) / chunk;
+    for (int64_t j = 0; j < k; ++j) {
+      if (parts_out) {
+        if (np >= parts_capacity) return fail(SSL_ERR_CAPACITY, "part table capacity exceeded");
+        int32_t* r = parts_out + np * kPartRecordInts;
+        const int64_t b0 = b + j * chunk, b1 = (b0 + chunk < b + n) ? b0 + chunk : b + n;
+        r[0] = (int32_t)g;
+        r[1] = (int32_t)b0;
+        r[2] = (int32_t)(k > 1 ? b1 : b + n);
+        r[3] = (int32_t)j;
+        r[4] = (int32_t)k;
+        r[5] = (int32_t)(k > 1 ? sp : 0);
+        r[6] = r[7] = 0;
+      }
+      ++np;
+    }
+    if (k > 1) sp += k;
+  }
+  *n_parts = np;
+  *split_parts = sp;
   return SSL_OK;
 }
 

@@ -56,6 +56,13 @@ struct PfMember {
                         // group), zero at rest (the latent's arrivals use
                         // words kPfLatArriveWord + rank tile of its tile
                         // counters' first slot)
+  // Rows: a part table (ssl_prefill_parts_build) instead of `ksplit` equal
+  // parts of every group: n_parts records per token tile, kPartInts int32
+  // each, {group, step_begin, step_end, part, parts, first split part}. The
+  // partial tiles of split groups sit at kpart [token tile][split_parts],
+  // the arrivals at karrive [token tile][group].
+  const int32_t* parts;
+  int n_parts, split_parts;
 };
 
 struct PfArgs {
@@ -73,6 +80,9 @@ struct PfArgs {
   int off[5];           // first item of each member
   PfMember mb[4];
 };
+
+// int32 per record of a prefill part table.
+constexpr int kPartInts = 8;
 
 // Token rows per latent tile of the prefill kernels.
 constexpr int kPrefillLatentRows = 64;

@@ -322,9 +322,11 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
   int n_sp = 0;                      // sparse steps (rows kernels)
   const int32_t* gr = nullptr;       // group record: {step_begin, step_end, rows[G]}
   int rt = 0;                        // latent: rank tile
-  const int ksplit = mb.ksplit;      // K parts of a tile (1: whole)
-  const int tile = local / ksplit;   // a tile's parts are adjacent items
-  const int kp = local - tile * ksplit;  // this workgroup's part
+  int ksplit = mb.ksplit;            // K parts of a tile (1: whole)
+  int tile = local / ksplit;         // a tile's parts are adjacent items
+  int kp = local - tile * ksplit;    // this workgroup's part
+  int64_t part_tile = (int64_t)tile * ksplit;  // rows: its parts' first partial tile
+  int arrive = tile;                 // rows: its parts' arrival word
   bool has_lr = LR;                  // rows: this part runs the low-rank steps
   if constexpr (KIND == K_LATENT) {
     const int n_rt = mb.r_pad / BN;
@@ -333,15 +335,33 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
     s_begin = kp * mb.kchunk;
     s_end = min(a.m_pad / KS, s_begin + mb.kchunk);
   } else {
-    const int tt = tile / mb.n_groups, grp = tile % mb.n_groups;
-    m0 = tt * BM;
-    gr = mb.groups + (int64_t)grp * (2 + G);
-    // part kp of the group's sparse steps; the last part also the low-rank ones
-    const int g0 = ld_word(gr, 0), n_all = ld_word(gr, 1) - g0;
-    const int chunk = (n_all + ksplit - 1) / ksplit;
-    const int b0 = min(kp * chunk, n_all), b1 = min(b0 + chunk, n_all);
-    s_begin = g0 + b0;
-    n_sp = b1 - b0;
+    int grp;
+    if (mb.parts != nullptr) {
+      // the member's part table (ssl_prefill_parts_build): per token tile,
+      // its records in turn, each a group's step range and its part of them
+      const int tt = local / mb.n_parts, j = local - tt * mb.n_parts;
+      const int32_t* pr = mb.parts + (int64_t)j * kPartInts;
+      grp = ld_word(pr, 0);
+      s_begin = ld_word(pr, 1);
+      n_sp = ld_word(pr, 2) - s_begin;
+      kp = ld_word(pr, 3);
+      ksplit = ld_word(pr, 4);
+      part_tile = (int64_t)tt * mb.split_parts + ld_word(pr, 5);
+      arrive = tt * mb.n_groups + grp;
+      m0 = tt * BM;
+      gr = mb.groups + (int64_t)grp * (2 + G);
+    } else {
+      const int tt = tile / mb.n_groups;
+      grp = tile % mb.n_groups;
+      m0 = tt * BM;
+      gr = mb.groups + (int64_t)grp * (2 + G);
+      // part kp of the group's sparse steps; the last part also the low-rank ones
+      const int g0 = ld_word(gr, 0), n_all = ld_word(gr, 1) - g0;
+      const int chunk = (n_all + ksplit - 1) / ksplit;
+      const int b0 = min(kp * chunk, n_all), b1 = min(b0 + chunk, n_all);
+      s_begin = g0 + b0;
+      n_sp = b1 - b0;
+    }
     // a member with no low-rank factor (r_pad 0) has no latent tiles to wait
     // for and no tile counters (tcnt is null): it neither waits nor departs
     has_lr = LR && kp == ksplit - 1 && mb.r_pad > 0;
@@ -733,7 +753,7 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
                  mb.tcnt + (int64_t)(m0 / BM) * kPfCntCopies * kPfCntStride + kPfLatArriveWord + rt))
       return;
   } else if constexpr (BM < 256) {
-    if (ksplit > 1 && !combine(mb.kpart + (int64_t)tile * ksplit * (BM * BN), mb.karrive + tile)) {
+    if (ksplit > 1 && !combine(mb.kpart + part_tile * (BM * BN), mb.karrive + arrive)) {
       depart();
       return;
     }

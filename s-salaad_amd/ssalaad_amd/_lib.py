@@ -64,6 +64,8 @@ _SIGNATURES = {
          _c_i64, _c_p, _c_p],
     ),
     "ssl_prefill_min_rows": (_c_i64, []),
+    "ssl_prefill_parts_build": (ctypes.c_int, [_c_p, _c_i64, _c_i32, _c_p, _c_i64, _c_p, _c_p]),
+    "ssl_prefill_parts_bytes": (_c_i64, [_c_i64, _c_i64]),
     "ssl_nm24_block_bytes": (_c_i64, []),
     "ssl_nm24_prefill_block_bytes": (_c_i64, []),
     "ssl_nm24_takes_prefill": (_c_i32, [_c_i64, _c_i64, _c_i32]),
@@ -150,6 +152,7 @@ class SlrMember(ctypes.Structure):
         ("exchange_bytes", _c_i64), ("workspace", _c_p), ("workspace_bytes", _c_i64),
         ("pf_groups", _c_p), ("pf_steps", _c_p), ("pf_n_groups", _c_i64), ("pf_group", _c_i32),
         ("nnz", _c_i64), ("values_pq", _c_p), ("s_format", _c_i32), ("status", _c_p),
+        ("pf_parts", _c_p), ("pf_n_parts", _c_i64), ("pf_split_parts", _c_i64),
     ]
 
 

@@ -186,17 +186,42 @@ def build_prefill_plan(
     return groups, steps, int(ng.value)
 
 
-class DevicePrefillPlan:
-    """A prefill plan (group table and step records) on one device."""
+def build_prefill_parts(groups: np.ndarray, n_groups: int, group: int):
+    """The part table of a prefill plan's groups (ssl_prefill_parts_build):
+    (records [n_parts, 8] int32, n_parts, split_parts), or None when the
+    groups are even enough to run whole."""
+    lib = _lib.load()
+    groups = np.ascontiguousarray(groups, dtype=np.int32)
+    n_parts, split = ctypes.c_int64(), ctypes.c_int64()
+    args = (groups.ctypes.data, n_groups, group)
+    rc = lib.ssl_prefill_parts_build(*args, None, 0, ctypes.byref(n_parts), ctypes.byref(split))
+    _lib.check(rc, "ssl_prefill_parts_build")
+    if n_parts.value == 0:
+        return None
+    table = np.zeros((n_parts.value, 8), dtype=np.int32)
+    rc = lib.ssl_prefill_parts_build(*args, table.ctypes.data, table.shape[0],
+                                     ctypes.byref(n_parts), ctypes.byref(split))
+    _lib.check(rc, "ssl_prefill_parts_build")
+    return table, int(n_parts.value), int(split.value)
 
-    __slots__ = ("groups", "steps", "n_groups", "group")
+
+class DevicePrefillPlan:
+    """A prefill plan (group table, step records and, for a skewed structure,
+    its part table) on one device."""
+
+    __slots__ = ("groups", "steps", "n_groups", "group", "parts", "n_parts", "split_parts")
 
     def __init__(self, groups: np.ndarray, steps: np.ndarray, n_groups: int, group: int,
-                 device: torch.device):
+                 device: torch.device, parts=None):
         self.groups = torch.from_numpy(groups).to(device)
         self.steps = torch.from_numpy(steps).to(device)
         self.n_groups = n_groups
         self.group = group
+        self.parts = self.n_parts = None
+        self.split_parts = 0
+        if parts is not None:
+            table, self.n_parts, self.split_parts = parts
+            self.parts = torch.from_numpy(table).to(device)
 
 
 _PLANS: "weakref.WeakSet[DevicePlan]" = weakref.WeakSet()

@@ -185,7 +185,10 @@ class _KernelState:
             step_cols = int(_lib.load().ssl_prefill_step_cols(self.dtype_code))
             groups, steps, ng = _runtime.build_prefill_plan(self.crow_h, self.col_h, self.NBK,
                                                             None, self.p, G, step_cols)
-            pp = _runtime.DevicePrefillPlan(groups, steps, ng, G, self.device)
+            # block storage: long groups of a skewed structure run in parts
+            parts = (_runtime.build_prefill_parts(groups, ng, G)
+                     if self.s_format == 0 and ng > 0 else None)
+            pp = _runtime.DevicePrefillPlan(groups, steps, ng, G, self.device, parts)
             self._pf_plans[G] = pp
         if self._values_pq is None and self.nblk_total > 0:
             if self.s_format == 1:
@@ -269,6 +272,13 @@ class _Descriptors:
                 mb.pf_groups, mb.pf_steps = pp.groups.data_ptr(), pp.steps.data_ptr()
                 mb.pf_n_groups, mb.pf_group = pp.n_groups, pp.group
                 mb.values_pq = _lib.ptr(st._values_pq)
+                if pp.parts is not None:
+                    # the parts' partial tiles follow the call's own workspace
+                    mb.pf_parts, mb.pf_n_parts = pp.parts.data_ptr(), pp.n_parts
+                    mb.pf_split_parts = pp.split_parts
+                    self.ws_need[i] += _round_up(
+                        int(lib.ssl_prefill_parts_bytes(M, pp.split_parts)), 256)
+                    mb.workspace_bytes = self.ws_need[i]
         self._ws = self._cnt = None
         self._xch: list = [None] * len(states)
         self._extra_ptr = 0

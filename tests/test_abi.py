@@ -564,3 +564,62 @@ def test_balanced_target_splits_only_the_longest_rows():
         assert all(spans[i][1] == spans[i + 1][0] for i in range(len(spans) - 1))
         assert (len(mine) > 1) == (costs[row] > t)
         assert sum(int(e - b) for b, e in mine[:, 3:5]) == 8
+
+
+def _parts(groups, group):
+    return _runtime.build_prefill_parts(np.asarray(groups, np.int32), len(groups), group)
+
+
+def _groups_of(steps, group=1):
+    """A group table whose group g holds steps[g] steps (rows are placeholders)."""
+    b = np.concatenate([[0], np.cumsum(steps)])
+    return [[b[g], b[g + 1]] + [g] * group for g in range(len(steps))]
+
+
+def test_part_table_cuts_only_the_long_groups_of_a_skewed_plan():
+    """Parts of about the mean group's steps (at least 32): every step of every
+    group exactly once, parts in group and step order, near-equal parts, the
+    split groups' partial tiles numbered contiguously in part order."""
+    rng = np.random.default_rng(3)
+    steps = np.concatenate([[172, 150, 100], rng.integers(0, 30, 61)])
+    for group in (1, 2, 4):
+        table, n_parts, split = _parts(_groups_of(steps, group), group)
+        mean = -(-int(steps.sum()) // len(steps))
+        target = max(32, mean)
+        covered = {}
+        nxt = 0
+        for g, b0, b1, k, nk, first, z0, z1 in table:
+            assert (z0, z1) == (0, 0)
+            covered.setdefault(int(g), []).append((int(k), int(nk), int(b0), int(b1), int(first)))
+        for g, recs in covered.items():
+            recs.sort()
+            nk = recs[0][1]
+            assert [r[0] for r in recs] == list(range(nk)) and all(r[1] == nk for r in recs)
+            b = int(np.sum(steps[:g]))
+            assert recs[0][2] == b and recs[-1][3] == b + steps[g]
+            for r0, r1 in zip(recs, recs[1:]):
+                assert r0[3] == r1[2]
+            lens = [r[3] - r[2] for r in recs]
+            assert nk == max(1, -(-int(steps[g]) // target)) or nk == 16
+            if nk > 1:
+                assert max(lens) - min(lens) <= max(lens) // 2 + 1
+                assert recs[0][4] == nxt and all(r[4] == nxt for r in recs)
+                nxt += nk
+        assert sorted(covered) == list(range(len(steps)))
+        assert n_parts == len(table) and split == nxt
+        assert [int(r[0]) for r in table] == sorted(int(r[0]) for r in table)  # group order
+
+
+def test_part_table_is_empty_for_even_plans_and_checks_its_input():
+    assert _parts(_groups_of([40, 41, 39, 80]), 1) is None            # longest ≤ 2 · mean
+    assert _parts(_groups_of([5, 6, 60]), 1) is None                   # ≤ 2 · 32
+    assert _parts([], 1) is None
+    t = _parts(_groups_of([0, 0, 0, 200], 2), 2)
+    assert t is not None and t[1] == 3 + 4 and t[2] == 4               # 200 in parts of the mean, 50
+    bad = _groups_of([10, 200])
+    bad[1][0] += 1                                                      # a gap between groups
+    with pytest.raises(ValueError, match="tile"):
+        _parts(bad, 1)
+    assert _lib.load().ssl_prefill_parts_bytes(2048, 10) == 10 * 2048 * 64 * 4
+    assert _lib.load().ssl_prefill_parts_bytes(300, 3) == 3 * 384 * 64 * 4
+    assert _lib.load().ssl_prefill_parts_bytes(300, 0) == 0

@@ -413,3 +413,35 @@ def test_fp32_llama60m_gate_at_2048_tokens_every_row(gpu_device):
     y = mod(to_dev(x, dt, gpu_device))
     torch.cuda.synchronize()
     assert err(y, oracle_y(prob, x)) <= TOL[dt]
+
+
+# ------------------------------------------------- skewed structures: parts --
+# Zipf(1.2) rows: the prefill plan's longest groups run in parts of about the
+# mean group's steps (ssl_prefill_parts_build), each part's fp32 tile summed in
+# part order by the last to arrive. 64 groups at 1900-2048 tokens: the tall
+# grid is one round of the device, so the parts run (narrow or short tiles).
+
+
+@pytest.mark.parametrize("p", [16, 32, 64])
+@pytest.mark.parametrize("mode", [0, NARROW, SHORT], ids=["auto", "narrow", "short"])
+@pytest.mark.parametrize("M", [2048, 1900])
+def test_skewed_groups_run_in_parts(p, mode, M, tile, gpu_device):
+    from ssalaad_amd import _runtime
+
+    if mode:
+        tile(mode)
+    dtype = torch.bfloat16
+    prob = make_problem(4096, 8192, 96, p, 0.1, dtype, seed=p + M, skew=True)
+    mod = make_module(prob, gpu_device)
+    st = mod._kernel()
+    pp = st.prefill_plan(int(_lib.load().ssl_prefill_group(M, st.NB, p, p)))
+    assert pp.parts is not None and pp.split_parts > 0
+    x_np = make_x(prob, M, seed=M)
+    print(f"[parts] p={p} tile={mode} M={M} parts={pp.n_parts} split={pp.split_parts}", flush=True)
+    y1 = mod(to_dev(x_np, dtype, gpu_device))
+    y2 = mod(to_dev(x_np, dtype, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y1, oracle_y(prob, x_np)) <= TOL[dtype]
+    assert torch.equal(y1, y2)
+    assert all(int(buf.abs().max()) == 0 for (idx, _), buf in _runtime._COUNTERS.items()
+               if idx == gpu_device.index)
