@@ -10,6 +10,10 @@ q / Q sub-blocks in column order (column col·(q/Q) + j). The sub-blocks tile
 the block exactly, so the product is the same sum with the same terms; only
 the order in which fp32 partial sums are added changes. Output columns are
 unchanged (kernel row r covers columns r·P … r·P + P − 1 = by·p + h·P …).
+
+The tiled kernels of many-token calls run square 16/32/64 blocks only; a call
+with other blocks (16×32, 48-wide, fp32 64×64, cut wide blocks) runs on the
+same matrix cut into the widest square blocks that tile its blocks exactly.
 """
 
 from __future__ import annotations
@@ -27,6 +31,22 @@ def kernel_block_shape(p: int, q: int) -> tuple[int, int]:
     P = next(w for w in KERNEL_P if p % w == 0)
     Q = q if q <= MAX_Q else max(d for d in range(16, MAX_Q + 1, 16) if q % d == 0)
     return P, Q
+
+
+def prefill_square(P: int, Q: int, elem_bytes: int) -> bool:
+    """Whether the tiled many-token kernels run (Q, P) blocks as they are:
+    square 16, 32 or 64 (fp32: 16 or 32)."""
+    return P == Q and P in (16, 32, 64) and not (elem_bytes == 4 and P == 64)
+
+
+def square_block(P: int, Q: int, elem_bytes: int) -> int:
+    """The widest square block the tiled kernels run (64, 32 or 16; fp32: 32
+    or 16) that tiles a (Q, P) block exactly; a many-token call with other
+    blocks runs on this re-blocked view of the same matrix."""
+    for s in (64, 32, 16):
+        if P % s == 0 and Q % s == 0 and not (elem_bytes == 4 and s == 64):
+            return s
+    return 0
 
 
 def reblock(crow_h: np.ndarray, col_h: np.ndarray, values: torch.Tensor, p: int, q: int,

@@ -62,6 +62,7 @@ class _StructPlan:
 
 
 _PLAN_ATTR = "_ssl_struct_plan"
+_PREFILL_MIN_ROWS = 128  # ssl_prefill_min_rows(): fewer token rows always stream
 
 
 def _validated_host_structure(crow, col, active_rows, nnz_values, NB_K):
@@ -138,11 +139,16 @@ _VIEW_ATTR = "_ssl_kernel_view"
 
 
 def _kernel_view(crow, col, values, active_rows, p, q, P, Q, NB_K):
-    """(crow, col, values, active_rows) of the same matrix in the (Q, P) blocks
-    the kernels run, cached on the values tensor while every input keeps its
-    identity and version. The structure is validated before it is cut."""
+    """(crow, col, values, active_rows) of the same matrix in (Q, P) blocks (the
+    blocks the kernels run, or the square ones of many-token calls), cached on
+    the values tensor per block shape while every input keeps its identity
+    and version. The structure is validated before it is cut."""
     key = tuple((t.data_ptr(), t._version) for t in (crow, col, values, active_rows))
-    hit = getattr(values, _VIEW_ATTR, None)
+    views = getattr(values, _VIEW_ATTR, None)
+    if views is None:
+        views = {}
+        setattr(values, _VIEW_ATTR, views)
+    hit = views.get((P, Q))
     if hit is not None and hit[0] == key:
         return hit[1]
     crow_h, act_h = _validated_host_structure(crow, col, active_rows, values.shape[0], NB_K)
@@ -151,7 +157,7 @@ def _kernel_view(crow, col, values, active_rows, p, q, P, Q, NB_K):
     dev = values.device
     view = (torch.from_numpy(crow2).to(dev), torch.from_numpy(col2).to(dev), vals2,
             torch.from_numpy(_reblock.reblock_rows(act_h, p // P)).to(dev))
-    setattr(values, _VIEW_ATTR, (key, view))
+    views[(P, Q)] = (key, view)
     return view
 
 
@@ -224,6 +230,17 @@ def bsr_addmm_inplace_(
     if M == 0 or values.shape[0] == 0 or active_rows.numel() == 0:
         return
     P, Q = _reblock.kernel_block_shape(block_p, block_q)
+    eb = out_inplace.element_size()
+    if M >= _PREFILL_MIN_ROWS and not _reblock.prefill_square(P, Q, eb):
+        # many tokens: blocks the tiled kernels do not run as they are go to
+        # the same matrix in square blocks when the tiled kernels take it there
+        s = _reblock.square_block(P, Q, eb)
+        rows = active_rows.numel() * (block_p // s) if s else 0
+        if s and _lib.load().ssl_bsr_addmm_takes_prefill(M, rows, s, s,
+                                                          _lib.dtype_code(out_inplace.dtype)):
+            view = _kernel_view(crow_indices, col_indices, values, active_rows, block_p,
+                                block_q, s, s, NB_K)
+            return bsr_addmm_inplace_(out_inplace, x, *view)
     if (P, Q) != (block_p, block_q):
         view = _kernel_view(crow_indices, col_indices, values, active_rows, block_p, block_q, P,
                             Q, NB_K)
@@ -293,11 +310,16 @@ def prepare_bsr_addmm(
         _validated_host_structure(crow_indices, col_indices, active_rows, values.shape[0], NB_K)
         return
     P, Q = _reblock.kernel_block_shape(block_p, block_q)
+    eb = values.element_size()
+    s = _reblock.square_block(P, Q, eb)
+    if not _reblock.prefill_square(P, Q, eb) and s:
+        # many-token calls run the square view: its plans too
+        prepare_bsr_addmm(*_kernel_view(crow_indices, col_indices, values, active_rows,
+                                        block_p, block_q, s, s, NB_K), in_features)
     if (P, Q) != (block_p, block_q):
         crow_indices, col_indices, values, active_rows = _kernel_view(
             crow_indices, col_indices, values, active_rows, block_p, block_q, P, Q, NB_K)
         block_p, block_q, NB_K = P, Q, in_features // Q
-    eb = values.element_size()
     dt = _lib.dtype_code(values.dtype)
     lib = _lib.load()
     can_prefill = bool(lib.ssl_bsr_addmm_takes_prefill(1 << 20, 1, block_p, block_q, dt))

@@ -31,6 +31,8 @@ Differences from the reference, all extensions:
 
 from __future__ import annotations
 
+import weakref
+
 import numpy as np
 import torch
 import torch.nn as nn
@@ -58,14 +60,17 @@ class _KernelState:
     load_state_dict or an in-place copy into A.
     """
 
-    def __init__(self, mod: "_LRSLinearBase", device: torch.device):
+    def __init__(self, mod: "_LRSLinearBase", device: torch.device,
+                 block: tuple[int, int] | None = None):
         dtype = mod.A.dtype
         self.key = mod._weights_key()
         self.device = device
         self.dtype_code = _lib.dtype_code(dtype)
         self.elem = torch.empty((), dtype=dtype).element_size()
         n, m, r = mod.out_features, mod.in_features, mod.r
-        p, q = mod._kernel_block
+        p, q = block if block is not None else mod._kernel_block
+        self._mod = weakref.ref(mod)
+        self._square: "_KernelState | None" = None
         self.p, self.q = p, q
         # kernel block-rows: a stored block-row of bp features is bp / p kernel rows
         bp = getattr(mod, "block_p", None) or p
@@ -201,6 +206,23 @@ class _KernelState:
                 self._values_pq = self.values.transpose(1, 2).contiguous()
         return pp
 
+    def prefill_view(self) -> "_KernelState | None":
+        """The same weights in the square blocks the tiled many-token kernels
+        run, when this view's blocks are not such (non-square, 48-wide, fp32
+        64×64, cut wide blocks): the blocks cut exactly into the widest square
+        blocks that tile them (_reblock.square_block), built on first use.
+        None when this view runs there as it is (or has no blocks)."""
+        if (self.s_format != 0 or self.nblk_total == 0
+                or _reblock.prefill_square(self.p, self.q, self.elem)):
+            return None
+        if self._square is None:
+            mod = self._mod()
+            s = _reblock.square_block(self.p, self.q, self.elem)
+            if mod is None or s == 0:
+                return None
+            self._square = _KernelState(mod, self.device, block=(s, s))
+        return self._square
+
     def rows(self, x: torch.Tensor) -> torch.Tensor:
         """x as [M, ·] with 16-byte aligned rows (copied into a padded buffer if not)."""
         x2 = x.reshape(-1, x.shape[-1])
@@ -326,6 +348,7 @@ def _outputs(states, ys, out_features, lead: tuple) -> list[torch.Tensor]:
 
 
 _MAX_CALLS = 16  # cached launch descriptors per leading state
+_PREFILL_MIN_ROWS = 128  # ssl_prefill_min_rows(): fewer token rows always stream
 
 
 def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[int]):
@@ -341,6 +364,14 @@ def _launch(states: list["_KernelState"], x: torch.Tensor, out_features: list[in
     orig = x.shape
     x2 = st0.rows(x)
     M = x2.shape[0]
+    if M >= _PREFILL_MIN_ROWS:
+        # many tokens with blocks the tiled kernels do not run as they are:
+        # the square view, when the tiled kernels take the call there
+        views = [st.prefill_view() for st in states]
+        if views[0] is not None and all(v is not None for v in views):
+            if views[0].takes_prefill(M, sum(v.NB for v in views)):
+                states = views
+                st0 = views[0]
     ys = [torch.empty(M, st.n_pad, dtype=x.dtype, device=dev) for st in states]
     if M > 0:
         lib = _lib.load()

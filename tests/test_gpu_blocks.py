@@ -167,3 +167,89 @@ def test_bundle_with_16x32_blocks_matches_the_dense_model(tmp_path, gpu_device):
         got = model(input_ids=ids.to(gpu_device)).logits.double()
     torch.cuda.synchronize()
     assert float((got - want).abs().max() / want.abs().max()) <= 1e-5
+
+
+# ----------------------------------------- many tokens: the square tiles --
+# The tiled kernels of many-token calls run square 16/32/64 blocks (fp32:
+# 16/32). Other blocks run on the same matrix cut into the widest square
+# blocks that tile them; every tile forced in turn, every row checked.
+
+PF_PQ = [(16, 32), (32, 16), (48, 48), (64, 32), (32, 64), (128, 320)]
+SQUARE = {(16, 32): 16, (32, 16): 16, (48, 48): 16, (64, 32): 32, (32, 64): 32, (128, 320): 32}
+
+
+@pytest.fixture
+def tile():
+    from ssalaad_amd import _lib
+
+    lib = _lib.load()
+
+    def force(mode):
+        _lib.check(lib.ssl_debug_set(_lib.DEBUG_PREFILL_TILE, mode), "ssl_debug_set")
+
+    yield force
+    force(0)
+
+
+@pytest.mark.parametrize("p,q", PF_PQ)
+@pytest.mark.parametrize("mode", [0, 1, 2, 3], ids=["auto", "narrow", "tall", "short"])
+@pytest.mark.parametrize("M", [300, 600])
+def test_module_many_tokens_runs_square_tiles(p, q, mode, M, tile, gpu_device):
+    tile(mode)
+    dtype = torch.bfloat16
+    prob = make_problem(12 * p, 10 * q, 64, p, 0.5, dtype, seed=p + q + M + mode, q=q,
+                        skew=(mode == 2))
+    mod = make_module(prob, gpu_device)
+    view = mod._kernel().prefill_view()
+    assert view is not None and view.p == view.q == SQUARE[(p, q)]
+    assert view.takes_prefill(M, view.NB)
+    x = make_x(prob, M, seed=M)
+    print(f"[square] {p}x{q} as {view.p} tile={mode} M={M}", flush=True)
+    y1, y2 = mod(to_dev(x, dtype, gpu_device)), mod(to_dev(x, dtype, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y1, oracle_y(prob, x)) <= TOL[dtype]
+    assert torch.equal(y1, y2)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 3], ids=["auto", "narrow", "short"])
+def test_module_fp32_64x64_runs_32x32_tiles(mode, tile, gpu_device):
+    """fp32 steps are 32 columns: 64×64 blocks run as four 32×32 blocks."""
+    tile(mode)
+    dtype = torch.float32
+    prob = make_problem(20 * 64, 8 * 64, 64, 64, 0.5, dtype, seed=5 + mode)
+    mod = make_module(prob, gpu_device)
+    view = mod._kernel().prefill_view()
+    assert view is not None and view.p == 32
+    M = 2048 if mode == 0 else 300
+    assert view.takes_prefill(M, view.NB)
+    x = make_x(prob, M, seed=M)
+    y = mod(to_dev(x, dtype, gpu_device))
+    torch.cuda.synchronize()
+    assert err(y, oracle_y(prob, x)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("p,q", [(16, 32), (48, 48), (64, 32), (128, 320)])
+@pytest.mark.parametrize("mode", [0, 1, 3], ids=["auto", "narrow", "short"])
+def test_op_many_tokens_runs_square_tiles(dtype, p, q, mode, tile, gpu_device):
+    tile(mode)
+    M = 600
+    prob = make_problem(9 * p, 6 * q, 4, p, 0.4, dtype, seed=p + q + mode, skew=True, q=q)
+    crow32, col32, vt, act = orc.module_buffers(prob["crow"], prob["col"], prob["vals"])
+    x = make_x(prob, M, seed=2)
+    rng = np.random.default_rng(M)
+    out0 = torch.from_numpy(rng.standard_normal((M, prob["n"]))).to(dtype).double().numpy()
+    want = orc.bsr_addmm_inplace(out0, x, crow32, col32, vt, act)
+    dev = gpu_device
+    out = to_dev(out0, dtype, dev)
+    values = to_dev(vt, dtype, dev)
+    torch.ops.ssalaad.tilelang_bsr_addmm_inplace_dense_(
+        out, to_dev(x, dtype, dev), torch.from_numpy(crow32).to(dev),
+        torch.from_numpy(col32).to(dev), values, torch.from_numpy(act).to(dev))
+    torch.cuda.synchronize()
+    assert err(out, want) <= TOL[dtype]
+    s = SQUARE[(p, q)]
+    assert any(pq == (s, s) for pq in getattr(values, "_ssl_kernel_view", {}))  # the square view ran
+    got = out.double().cpu().numpy()
+    for by in sorted(set(range(prob["NB"])) - set(act.tolist())):
+        assert np.array_equal(got[:, by * p:(by + 1) * p], out0[:, by * p:(by + 1) * p])

@@ -3,6 +3,7 @@ factory dispatch and validation messages, op registration and schema."""
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -229,3 +230,33 @@ def test_first_op_call_under_graph_capture_raises(monkeypatch):
     act = torch.tensor([0], dtype=torch.int32)
     with pytest.raises(RuntimeError, match="prepare_bsr_addmm"):
         addmm_inplace._validated_host_structure(crow, col, act, 1, 1)
+
+
+@pytest.mark.parametrize("p,q,elem,s", [(16, 32, 2, 16), (32, 16, 2, 16), (48, 48, 2, 16),
+                                        (64, 32, 2, 32), (128, 320, 2, 32), (128, 512, 2, 64), (96, 96, 2, 16),
+                                        (64, 64, 4, 32), (64, 192, 4, 32)])
+def test_square_view_is_the_same_matrix(p, q, elem, s):
+    """Many-token calls with blocks the tiled kernels do not run as they are use
+    the widest square block that tiles them (fp32 at most 32): the re-blocked
+    structure densifies to the same matrix, rows in order."""
+    from oracle import slr_oracle as orc
+    from ssalaad_amd import _reblock
+
+    P, Q = _reblock.kernel_block_shape(p, q)
+    assert not _reblock.prefill_square(P, Q, elem)
+    assert _reblock.square_block(P, Q, elem) == s
+    rng = np.random.default_rng(p + q)
+    NB, NBK = 5, 4
+    counts = np.array([2, 0, 4, 1, 3])
+    crow = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    col = np.concatenate([np.sort(rng.permutation(NBK)[:c]) for c in counts]).astype(np.int32)
+    vals = rng.standard_normal((int(crow[-1]), p, q))
+    vt = torch.from_numpy(vals.transpose(0, 2, 1).copy())               # stored (nnz, q, p)
+    crow2, col2, vt2 = _reblock.reblock(crow, col, vt, p, q, s, s)
+    dense = orc.bsr_to_dense(crow, col, vals, NB * p, NBK * q)
+    dense2 = orc.bsr_to_dense(crow2, col2, vt2.numpy().transpose(0, 2, 1), NB * p, NBK * q)
+    np.testing.assert_array_equal(dense, dense2)
+    assert crow2.shape[0] - 1 == NB * (p // s)
+    assert np.all(np.diff(crow2) >= 0) and crow2[-1] == col2.shape[0]
+    for r in range(NB * (p // s)):                                        # columns ascending
+        assert np.all(np.diff(col2[crow2[r]:crow2[r + 1]]) > 0)
