@@ -49,6 +49,9 @@ headline):
   llama7b_lr_prefill   the low-rank share of that linear alone (S = 0: the
                        two GEMMs x·Bᵀ and t·Aᵀ) at 2048 tokens: TFLOP/s, with
                        torch's two F.linear calls on the same tensors beside it
+  skew_prefill         one point of the skew sweep (4096x11008, r 128, Zipf(1.2)
+                       rows of --block blocks at --density, --batch tokens, 2048
+                       by default): TFLOP/s
   llama7b_ffn_prefill_nm24  the 2:4 projection of llama7b_ffn_decode_nm24 at
                        2048 tokens: TFLOP/s of the dense-equivalent work
                        (x·Bᵀ, t·Aᵀ and the kept half of S)
@@ -554,6 +557,25 @@ def run_workload(args) -> dict:
                     details={"call_us_eager": round(us_call, 3), "kernel_us_graph": round(us, 3),
                              "torch_two_linears_us_graph": round(us_lib, 3),
                              "torch_two_linears_TFLOPs": round(fl / us_lib / 1e6, 1)})
+    if args.workload == "skew_prefill":
+        # one point of the skew sweep: 4096x11008, r 128, Zipf(1.2) rows of
+        # --block blocks at --density mean density, --batch tokens (2048)
+        M = args.batch if args.batch_set else 2048
+        mod = make_linear(4096, 11008, 128, args.block, args.density, gen, dev, torch.bfloat16,
+                          skew=True)
+        x = torch.randn(M, 11008, generator=gen).to(torch.bfloat16).to(dev)
+        us = _time_eager(lambda: mod(x), args.steps)
+        fl = algorithmic_bytes(mod, M, 2)["flops"]
+        tf = fl / us / 1e6
+        return dict(base, metric="SLR-linear TFLOP/s, skewed (Zipf 1.2) block rows",
+                    value=round(tf, 1), unit="TFLOP/s", ms_per_step=round(us / 1e3, 5),
+                    dtype="bf16",
+                    config={"workload": "skew_prefill", "n": 4096, "m": 11008, "rank": 128,
+                            "block": args.block, "mean_block_density": args.density,
+                            "batch_tokens": M, "parallelism": "single_gpu"},
+                    roofline={"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
+                              "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4), "traffic": None,
+                              "flops_per_call": int(fl)})
     if args.workload == "llama7b_ffn_prefill_nm24":
         from ssalaad_amd import LRSLinear
 
@@ -954,12 +976,14 @@ def main():
                     help="the four stages of a layer as grouped launches instead of one chained launch")
     ap.add_argument("--no-group", action="store_true",
                     help="one launch per linear instead of grouping q/k/v and gate/up")
+    ap.add_argument("--block", type=int, default=16, help="skew_prefill: block size")
+    ap.add_argument("--density", type=float, default=0.5, help="skew_prefill: mean block density")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (counter calibration)")
     ap.add_argument("--workload", default="llama1b_decode",
                     choices=["llama1b_decode", "llama7b_ffn_decode", "llama7b_ffn_prefill",
                              "llama7b_ffn_decode_nm24", "llama7b_ffn_prefill_nm24", "block_topk",
-                             "llama7b_lr_prefill",
+                             "llama7b_lr_prefill", "skew_prefill",
                              "llama60m_forward",
                              "llama1b_decode_step", "sweep", "llama1b_prefill"])
     args = ap.parse_args()
