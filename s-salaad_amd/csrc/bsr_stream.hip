@@ -728,6 +728,27 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
       }
       if (parts && rows.bm == 256) rows.bm = 128;
     }
+    // Does the latent hold up rows that would otherwise start at once? Its
+    // workgroups come first in the grid and each takes a row workgroup's slot
+    // (LDS) until it ends: when the row grid fits one round of the device but
+    // not beside the latent, the rows pushed out wait for the whole latent,
+    // so it runs in short chunks (4096×11008 with Zipf 16×16 blocks at 50% and
+    // 2048 tokens: 64 rows started after the 173-step latent, at 67 µs).
+    bool lat_contends = false;
+    if (ksplit == 1) {
+      int64_t row_items = 0, lat_items = 0;
+      for (int i = 0; i < n_members; ++i) {
+        const ssl_slr_member& mb = members[i];
+        if (mb.NB == 0) continue;
+        const int64_t T = (M + rows.bm - 1) / rows.bm;
+        const bool mp = parts && mb.pf_parts && mb.pf_n_parts > 0 &&
+                        mb.workspace_bytes >= L[i].total + ssl_prefill_parts_bytes(M, mb.pf_split_parts);
+        row_items += (mp ? mb.pf_n_parts : mb.pf_n_groups) * T;
+        if (mb.r_pad > 0) lat_items += TL * (mb.r_pad / 64);
+      }
+      const int64_t slots = (rows.bm == 256 ? 2 : 3) * (int64_t)cus;
+      lat_contends = row_items <= slots && row_items + lat_items > slots;
+    }
     int64_t items = 0, litems = 0;
     for (int i = 0; i < n_members; ++i) {
       const ssl_slr_member& mb = members[i];
@@ -770,7 +791,8 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
         // sparse steps and the workspace holds its partial tiles
         const int64_t group_steps = mb.nnz * block_p / ssl_prefill_step_cols(dtype) /
                                     (mb.pf_n_groups > 0 ? mb.pf_n_groups : 1);
-        ls = prefill_latent_split_whole(M, m_pad, mb.r_pad, dtype, group_steps, cus);
+        ls = prefill_latent_split_whole(M, m_pad, mb.r_pad, dtype,
+                                        lat_contends ? group_steps / 8 : group_steps, cus);
         if (ls.split > 1 && mb.workspace_bytes < L[i].pf_split + rows_bytes +
                                                      prefill_latent_part_bytes(M, mb.r_pad, ls.split))
           ls = PfLatentSplit{1, (int)lat_steps};
