@@ -100,6 +100,23 @@ typedef enum {
 } ssl_debug_knob;
 int ssl_debug_set(int32_t knob, int64_t value);
 
+/* Device bounds checks (no reference counterpart): 1 in the library's checked
+ * build (compiled with SSL_DEVICE_CHECKS=1, libssalaad_amd_checked.so), 0 in
+ * the normal one. A checked build re-checks on the device every index the
+ * kernels read from a plan, a column array or a prefill group, step or part
+ * record; one outside what the call's plan can hold is dropped or clamped (the
+ * kernel still ends normally) and recorded as bit 8 + code of the call's
+ * status word (ssl_slr_member.status, or the plan's first exchange word):
+ * code 0 a streaming plan entry, 1 a column index (negative, or, for the
+ * in-place op, past x; the fused linear reads columns past in_features as
+ * zeros), 2 a prefill group's
+ * block-row, 3 a prefill step's x column or block, 4 a prefill part record.
+ * Calls that pass no status word (the in-place op) record in a word of the
+ * library's own, which ssl_debug_check_word returns and clears (synchronous;
+ * always 0 in the normal build, -1 on a HIP error). */
+int32_t ssl_device_checks(void);
+int64_t ssl_debug_check_word(void);
+
 /* -------------------------------------------------------------------------
  * Work plans (host side, integer only).
  *

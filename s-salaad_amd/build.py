@@ -5,7 +5,12 @@ one shared library exporting the C ABI declared in include/ssalaad_amd.h. The
 library is linked against the HIP runtime that PyTorch ships, so a process that
 imports torch first holds a single libamdhip64.
 
-Usage: python s-salaad_amd/build.py [-v]
+With --checked, the same sources are built with SSL_DEVICE_CHECKS=1 into
+`ssalaad_amd/libssalaad_amd_checked.so`: the kernels re-check every index they
+read from plans and records and report a bad one in the call's status word
+(ssl_device_checks). Load it with SSALAAD_AMD_LIB=<its path>.
+
+Usage: python s-salaad_amd/build.py [-v] [--checked]
 """
 
 from __future__ import annotations
@@ -21,6 +26,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 OUT = HERE / "ssalaad_amd" / "libssalaad_amd.so"
+OUT_CHECKED = HERE / "ssalaad_amd" / "libssalaad_amd_checked.so"
 BUILD_DIR = HERE / "_build"
 ARCH = "gfx950"
 
@@ -70,16 +76,19 @@ COMMON_FLAGS = [
 ]
 
 
-def build(verbose: bool = False, jobs: int = 8) -> Path:
+def build(verbose: bool = False, jobs: int = 8, checked: bool = False) -> Path:
     hipcc = _hipcc()
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    out = OUT_CHECKED if checked else OUT
+    build_dir = BUILD_DIR / "checked" if checked else BUILD_DIR
+    build_dir.mkdir(parents=True, exist_ok=True)
+    flags = COMMON_FLAGS + (["-DSSL_DEVICE_CHECKS=1"] if checked else [])
     sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     if not sources:
         raise RuntimeError("no sources under csrc/")
 
     def compile_one(src: Path) -> Path:
-        obj = BUILD_DIR / (src.name + ".o")
-        cmd = [hipcc, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+        obj = build_dir / (src.name + ".o")
+        cmd = [hipcc, *flags, "-c", str(src), "-o", str(obj)]
         if src.suffix == ".cpp":
             cmd[1:1] = ["-x", "hip"]
         t0 = time.time()
@@ -99,7 +108,7 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(sources)))) as ex:
         objs = list(ex.map(compile_one, sources))
 
-    tmp = OUT.with_name(OUT.name + ".tmp")
+    tmp = out.with_name(out.name + ".tmp")
     link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     tlib = _torch_lib()
     if tlib:
@@ -107,11 +116,11 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     res = subprocess.run(link, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
     if verbose:
-        print(f"[build] wrote {OUT}")
-    return OUT
+        print(f"[build] wrote {out}")
+    return out
 
 
 if __name__ == "__main__":
-    build(verbose="-v" in sys.argv)
+    build(verbose="-v" in sys.argv, checked="--checked" in sys.argv)

@@ -6,6 +6,11 @@
 
 #include "../../include/ssalaad_amd.h"
 
+// 1 in the library's checked build (device bounds checks; slr_common.h)
+#ifndef SSL_DEVICE_CHECKS
+#define SSL_DEVICE_CHECKS 0
+#endif
+
 namespace ssl {
 
 // Records `msg` as the thread's last error and returns `code`.

@@ -212,7 +212,7 @@ void fill_args(SlrArgs& a, const ssl_slr_member& mb, const Layout& L, const void
   char* ws = (char*)mb.workspace;
   a.x = x; a.ldx = ldx; a.M = (int)M; a.m = (int)m;
   a.y = mb.y; a.ldy = mb.ldy; a.col = mb.col; a.values = mb.values; a.plan = mb.plan;
-  a.n_chunks = (int)mb.n_chunks; a.NB = (int)mb.NB;
+  a.n_chunks = (int)mb.n_chunks; a.NB = (int)mb.NB; a.nnz = (int)mb.nnz;
   a.A = mb.A; a.lda = mb.r_pad; a.bias = mb.bias;
   a.n_slots = mb.n_slots; a.part_main = (float*)(ws + L.part_main); a.cnt_main = mb.counters;
   a.B = mb.B; a.ldb = m_pad; a.t = ws + L.t_final; a.ldt = mb.r_pad;
@@ -546,8 +546,9 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
     rows.x = x; rows.ldx = ldx; rows.M = (int)M; rows.m = (int)K; rows.m_pad = (int)K;
     rows.mode = PF_OP;
     rows.n = 1;
+    rows.status = (uint64_t*)check_word_ptr();
     PfMember& pm = rows.mb[0];
-    pm.y = out; pm.ldy = ldo; pm.values_pq = values_pq;
+    pm.y = out; pm.ldy = ldo; pm.values_pq = values_pq; pm.NB = (int)NB;
     pm.values_bytes = nnz * block_p * block_q * eb;
     pm.groups = pf_groups; pm.steps = pf_steps; pm.n_groups = (int)pf_n_groups;
     pm.ksplit = 1;  // the op's row kernel runs whole row groups
@@ -566,8 +567,9 @@ int ssl_bsr_addmm_inplace(void* out, int64_t ldo, const void* x, int64_t ldx, co
   SlrArgs& a = g.m[0];
   a.x = x; a.ldx = ldx; a.M = (int)M; a.m = (int)K;
   a.y = out; a.ldy = ldo; a.col = col; a.values = values; a.plan = plan;
-  a.n_chunks = (int)n_chunks; a.NB = (int)NB;
+  a.n_chunks = (int)n_chunks; a.NB = (int)NB; a.nnz = (int)nnz;
   a.n_slots = n_slots; a.part_main = (float*)workspace; a.cnt_main = counters;
+  a.status = check_word_ptr();  // the op never waits; a checked build reports there
   set_block_shape(a, dtype, block_p, block_q, SSL_S_BSR);
   return check_hip(dispatch(dtype, MODE_OP, SF_BSR, block_p, stream_ke(dtype, block_q), MT, g,
                             n_chunks * MG, (hipStream_t)stream),
@@ -766,7 +768,7 @@ int ssl_slr_forward_group(const void* x, int64_t ldx, int64_t M, int64_t m, int6
           mb.NB * block_p * mb.r_pad * eb > 0x7fffffffLL || M * mb.ldy * eb > 0x7fffffffLL ||
           (int64_t)mb.r_pad * m_pad * eb > 0x7fffffffLL)
         return fail(SSL_ERR_UNSUPPORTED, "linear %d: weights or output beyond 2 GiB", i);
-      pm.y = mb.y; pm.ldy = mb.ldy; pm.A = mb.A; pm.lda = mb.r_pad;
+      pm.y = mb.y; pm.ldy = mb.ldy; pm.A = mb.A; pm.lda = mb.r_pad; pm.NB = (int)mb.NB;
       pm.A_bytes = mb.NB * block_p * mb.r_pad * eb; pm.bias = mb.bias;
       pm.values_pq = mb.values_pq; pm.values_bytes = mb.nnz * blk_bytes;
       pm.groups = mb.pf_groups; pm.steps = mb.pf_steps; pm.n_groups = (int)mb.pf_n_groups;

@@ -26,11 +26,50 @@ int device_cus() {
   return cache[dev];
 }
 
+// The checked build's status word for calls that pass none (the in-place op,
+// which never waits): a file-scope device word, used through the address
+// hipGetSymbolAddress gives with the device current (the name is a host-side
+// stand-in in host code), once per device.
+#if SSL_DEVICE_CHECKS
+static __device__ unsigned long long check_word;
+#endif
+
+unsigned long long* check_word_ptr() {
+#if SSL_DEVICE_CHECKS
+  static unsigned long long* cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (!cache[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(check_word)) == hipSuccess) cache[dev] = (unsigned long long*)p;
+  }
+  return cache[dev];
+#else
+  return nullptr;
+#endif
+}
+
 }  // namespace ssl
 
 using namespace ssl;
 
 extern "C" {
+
+int64_t ssl_debug_check_word(void) {
+#if SSL_DEVICE_CHECKS
+  unsigned long long v = 0, zero = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(check_word), sizeof v, 0, hipMemcpyDeviceToHost) != hipSuccess)
+    return -1;
+  if (v != 0 &&
+      hipMemcpyToSymbol(HIP_SYMBOL(check_word), &zero, sizeof zero, 0, hipMemcpyHostToDevice) != hipSuccess)
+    return -1;
+  return (int64_t)v;
+#else
+  return 0;
+#endif
+}
+
+int32_t ssl_device_checks(void) { return SSL_DEVICE_CHECKS; }
 
 int ssl_status_word_alloc(void** host_ptr, void** device_ptr) {
   clear_error();

@@ -63,6 +63,7 @@ struct PfMember {
   // the arrivals at karrive [token tile][group].
   const int32_t* parts;
   int n_parts, split_parts;
+  int NB;               // block-rows (bounds the group records' rows)
 };
 
 struct PfArgs {

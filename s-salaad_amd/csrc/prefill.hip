@@ -346,7 +346,17 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
       n_sp = ld_word(pr, 2) - s_begin;
       kp = ld_word(pr, 3);
       ksplit = ld_word(pr, 4);
-      part_tile = (int64_t)tt * mb.split_parts + ld_word(pr, 5);
+      const int first = ld_word(pr, 5);
+#if SSL_DEVICE_CHECKS
+      if (!(grp >= 0 && grp < mb.n_groups && ksplit >= 1 && ksplit <= 16 && kp >= 0 &&
+            kp < ksplit && (ksplit == 1 || (first >= 0 && first + ksplit <= mb.split_parts)) &&
+            n_sp >= 0 && s_begin >= ld_word(mb.groups + (int64_t)grp * (2 + G), 0) &&
+            s_begin + n_sp <= ld_word(mb.groups + (int64_t)grp * (2 + G), 1))) {
+        if (threadIdx.x == 0) check_fail(a.status, kChkPart);
+        return;
+      }
+#endif
+      part_tile = (int64_t)tt * mb.split_parts + first;
       arrive = tt * mb.n_groups + grp;
       m0 = tt * BM;
       gr = mb.groups + (int64_t)grp * (2 + G);
@@ -362,6 +372,20 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
       s_begin = g0 + b0;
       n_sp = b1 - b0;
     }
+#if SSL_DEVICE_CHECKS
+    {
+      bool ok = true;
+#pragma unroll
+      for (int g2 = 0; g2 < G; ++g2) {
+        const int r = ld_word(gr, 2 + g2);
+        ok = ok && r >= -1 && r < mb.NB;
+      }
+      if (!ok) {
+        if (threadIdx.x == 0) check_fail(a.status, kChkGroupRow);
+        return;
+      }
+    }
+#endif
     // a member with no low-rank factor (r_pad 0) has no latent tiles to wait
     // for and no tile counters (tcnt is null): it neither waits nor departs
     has_lr = LR && kp == ksplit - 1 && mb.r_pad > 0;
@@ -513,7 +537,15 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
     } else {
       if (u < n_sp) {
         mask = view_word(rv, 0);
+#if SSL_DEVICE_CHECKS
+        int c = view_entry(rv, 1);  // first x column of this lane's entry, or −1
+        if (c >= a.m_pad) {
+          check_fail(a.status, kChkStep);
+          c = -1;
+        }
+#else
         const int c = view_entry(rv, 1);  // first x column of this lane's entry, or −1
+#endif
         const uint32_t xcb = c >= 0 ? (uint32_t)(c * EB) : kOob;
 #pragma unroll
         for (int i = 0; i < IA; ++i) dma16(xr, ax[i] + xcb, 0, la + i * kRowBytes32);
@@ -521,8 +553,18 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
           // this wave's 16 feature rows (slot wid / 2): lane l takes row l / 4,
           // entry (l % 4) / 2, half l % 2 of the values; lanes < 32 the
           // index word of row l / 2, entry l % 2
+#if SSL_DEVICE_CHECKS
+          int b0 = view_word(rv, 1 + E + (wid >> 1) * E);
+          int b1 = view_word(rv, 1 + E + (wid >> 1) * E + 1);
+          if ((int64_t)b0 * kNmPfBytes >= mb.values_bytes || (int64_t)b1 * kNmPfBytes >= mb.values_bytes) {
+            check_fail(a.status, kChkStep);
+            if ((int64_t)b0 * kNmPfBytes >= mb.values_bytes) b0 = -1;
+            if ((int64_t)b1 * kNmPfBytes >= mb.values_bytes) b1 = -1;
+          }
+#else
           const int b0 = view_word(rv, 1 + E + (wid >> 1) * E);
           const int b1 = view_word(rv, 1 + E + (wid >> 1) * E + 1);
+#endif
           const uint32_t kst = (uint32_t)k * kStageBytes;
           const int bv = (lane & 2) ? b1 : b0;
           const uint32_t jv = 16 * (wid & 1) + (lane >> 2);
@@ -536,7 +578,15 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
         } else {
 #pragma unroll
           for (int i = 0; i < IB; ++i) {
+#if SSL_DEVICE_CHECKS
+            int blk = view_entry(rv, 1 + E + i * E);
+            if ((int64_t)blk * (P * P * EB) >= mb.values_bytes) {
+              check_fail(a.status, kChkStep);
+              blk = -1;
+            }
+#else
             const int blk = view_entry(rv, 1 + E + i * E);
+#endif
             dma16(br, blk < 0 ? kOob : (uint32_t)blk * (uint32_t)(P * P * EB) + bconst[i], 0,
                   lb + i * kRowBytes32);
           }

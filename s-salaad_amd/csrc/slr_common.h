@@ -362,6 +362,35 @@ __device__ __forceinline__ int ld_uniform(const int32_t* p, int64_t i) {
 }
 
 // ---------------------------------------------------------------------------
+// Device bounds checks, compiled in by building with SSL_DEVICE_CHECKS=1 (the
+// library build's checked variant). The kernels index x, the block values and
+// their outputs with numbers read from device memory: plan entries, column
+// indices, prefill group, step and part records. The planners check them on
+// the host; a checked build checks them again where they are read. An index
+// outside what a plan can hold is recorded in the call's status word (bit
+// 8 + code, a plain store: the word may be host memory, where an atomic RMW
+// needs PCIe atomics) and the access it would drive is dropped or clamped, so
+// every kernel still ends normally. LDS offsets are compile-time expressions
+// of the tile shape, bounded by static assertions, and are not re-checked.
+// ---------------------------------------------------------------------------
+#ifndef SSL_DEVICE_CHECKS
+#define SSL_DEVICE_CHECKS 0
+#endif
+enum : int {
+  kChkPlan = 0,      // a streaming plan entry (row, block or unit range, parts, slot)
+  kChkColumn = 1,    // a block's column index
+  kChkGroupRow = 2,  // a prefill group record's block-row
+  kChkStep = 3,      // a prefill step record's x column or block index
+  kChkPart = 4,      // a prefill part record
+};
+template <typename U64>
+__device__ __forceinline__ void check_fail(U64* status, int code) {
+  static_assert(sizeof(U64) == 8, "a 64-bit status word");
+  if (status != nullptr)
+    __hip_atomic_store(status, (U64)1 << (8 + code), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // W adjacent elements in the activation dtype.
 // ---------------------------------------------------------------------------
 template <int DT, int W>

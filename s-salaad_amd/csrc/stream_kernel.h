@@ -340,6 +340,7 @@ struct SlrArgs {
   const int32_t* plan;
   int n_chunks;
   int NB;
+  int nnz;              // stored blocks (0: not given; bounds the plan's block ranges)
   // Sparse blocks are walked in K slabs of KM rows (the MFMA's k extent):
   // block b's slab ks is KM·p contiguous values at b·blk_bytes + ks·slab_bytes.
   int q;                // block_q: input features per block
@@ -644,6 +645,14 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   const int32_t* d = a.plan + (int64_t)chunk * SSL_PLAN_STRIDE;
   const int row = d[0], bb = d[1], be = d[2], lb = d[3], le = d[4], seq = d[5], nseq = d[6];
   const int slot = d[7];
+#if SSL_DEVICE_CHECKS
+  if (!(row >= 0 && row < a.NB && bb >= 0 && bb <= be && (a.nnz <= 0 || be <= a.nnz) &&
+        lb >= 0 && lb <= le && (int64_t)le * 32 <= a.lda && nseq >= 1 && seq >= 0 && seq < nseq &&
+        (nseq == 1 || (slot >= 0 && slot + nseq <= a.n_slots)))) {
+    if (threadIdx.x == 0) check_fail(a.status, kChkPlan);
+    return;  // the whole workgroup: the entry is uniform
+  }
+#endif
   const int m0 = mg * MT * 16;
   const int Mrem = min(a.M - m0, MT * 16);
 
@@ -690,7 +699,21 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
       const int v = min(v0 + k * kSW, ve - 1);
       const int blk = nks == 1 ? v : (int)__umulhi((uint32_t)v, a.nks_magic);
       const int ks = v - blk * nks;
+#if SSL_DEVICE_CHECKS
+      // The fused linear reads x through masks at in_features, so a block past
+      // it reads zeros (the padding of a ragged last block, or the all-padding
+      // sub-blocks cut from a deep one): there a column must only be
+      // non-negative with an offset in range. The op's x is exactly its
+      // block-columns wide.
+      int cb = ld_uniform(a.col, blk);
+      if (cb < 0 || (MODE == MODE_OP ? (int64_t)cb * a.q >= a.m : (int64_t)cb * a.q > 0x3fffffff)) {
+        if (lane == 0) check_fail(a.status, kChkColumn);
+        cb = 0;
+      }
+      colk[k] = cb * a.q + ks * KM;
+#else
       colk[k] = ld_uniform(a.col, blk) * a.q + ks * KM;
+#endif
       voff[k] = (int64_t)blk * a.blk_bytes + ks * a.slab_bytes;
     }
   };

@@ -13,7 +13,10 @@ from pathlib import Path
 
 import torch  # noqa: F401  (loads torch's libamdhip64 before ours)
 
-LIB_PATH = Path(__file__).resolve().parent / "libssalaad_amd.so"
+# SSALAAD_AMD_LIB selects another build of the same library, e.g. the device
+# bounds-check variant libssalaad_amd_checked.so next to this file.
+LIB_PATH = Path(os.environ.get("SSALAAD_AMD_LIB") or
+                Path(__file__).resolve().parent / "libssalaad_amd.so").resolve()
 
 SSL_OK = 0
 SSL_ERR_INVALID = 1
@@ -43,6 +46,8 @@ _SIGNATURES = {
     "ssl_last_error": (ctypes.c_char_p, []),
     "ssl_debug_set": (ctypes.c_int, [_c_i32, _c_i64]),
     "ssl_status_word_alloc": (ctypes.c_int, [_c_p, _c_p]),
+    "ssl_device_checks": (_c_i32, []),
+    "ssl_debug_check_word": (_c_i64, []),
     "ssl_plan_build": (
         ctypes.c_int,
         [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_i64, _c_p, _c_i64, _c_p,

@@ -351,6 +351,11 @@ def check_status(device: torch.device) -> None:
     the host can see now, without synchronising)."""
     w = _STATUS.get(_index(device))
     if w is not None and w.read() != 0:
+        if w.read() >> 8:
+            raise RuntimeError(
+                f"a device bounds check of a fused SLR launch on cuda:{_index(device)} failed "
+                f"(status word {w.read():#x}: bit 8 + code, see ssl_device_checks); call "
+                "ssalaad_amd.clear_wait_status() before the next call")
         raise RuntimeError(
             f"a fused SLR launch on cuda:{_index(device)} gave up waiting for another "
             "workgroup (bounded wait), so outputs computed since then are unreliable; "

@@ -24,3 +24,25 @@ def gpu_device():
     if not torch.cuda.is_available():
         pytest.fail("GPU test selected but no ROCm device is visible")
     return torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True)
+def _device_checks_record_nothing(request):
+    """Under the library's checked build (SSALAAD_AMD_LIB pointing at
+    libssalaad_amd_checked.so), every GPU test must leave no device
+    bounds-check record behind: neither in the devices' status words nor in the
+    library's own word for calls that pass none."""
+    yield
+    if request.node.get_closest_marker("gpu") is None:
+        return
+    from ssalaad_amd import _lib, _runtime
+
+    lib = _lib.load()
+    if not lib.ssl_device_checks():
+        return
+    import torch
+
+    torch.cuda.synchronize()
+    bad = {idx: hex(w.read()) for idx, w in _runtime._STATUS.items() if w.read() >> 8}
+    word = lib.ssl_debug_check_word()
+    assert not bad and word == 0, f"device bounds checks failed: status {bad}, op word {word:#x}"
