@@ -228,7 +228,7 @@ void fill_args(SlrArgs& a, const ssl_slr_member& mb, const Layout& L, const void
   a.wait_polls = knobs.wait_polls > 0 ? (int)knobs.wait_polls : kSpinLimit;
   // out of reach of any launch: tickets and counters advance far less per launch
   a.wait_bias = knobs.wait_unreachable ? (1 << 30) : 0;
-  a.dep = nullptr; a.dep_need = 0; a.dep_waiters = 0; a.done = nullptr; a.done_copies = 0;
+  a.dep = nullptr; a.dep_need = 0; a.dep_waiters = 0; a.done = nullptr;
 }
 
 // K units (of 32 in_features) per latent chunk in a chained stage after the
@@ -372,7 +372,6 @@ int build_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,
         c->m[i].dep_waiters = waiters;
       }
       c->m[st.src].done = st.sync;
-      c->m[st.src].done_copies = waiters < kDepCopies ? waiters : kDepCopies;
     }
   }
   c->n_seg = nseg;

@@ -245,18 +245,57 @@ __device__ __forceinline__ void st_w_dev(__amdgpu_buffer_rsrc_t r, int byte_off,
 }
 
 // ---------------------------------------------------------------------------
-// Deterministic tree reduction of the kSW wave tiles into wave 0's registers:
-// rounds of halving; in each round wave i (< half) adds wave i + half's tile,
-// passed through LDS in groups of SLOTS tiles.
+// Deterministic reduction of the kSW wave tiles into wave 0's registers. Tiles
+// of up to 4 KiB (MT·W ≤ 4: decode tiles of up to 64 output features) go
+// through LDS at once: waves 1..7 store, one barrier, wave 0 adds them in wave
+// order (measured: the three halving rounds' six barriers took about 0.6 µs of
+// a 7B decode launch's tail). Larger tiles take rounds of halving; in each
+// round wave i (< half) adds wave i + half's tile, passed through LDS in groups
+// of SLOTS tiles.
 // ---------------------------------------------------------------------------
 template <int MT, int W>
+constexpr bool flat_reduce() {
+  return MT * W <= 4;
+}
+template <int MT, int W>
 constexpr int red_slots() {
-  return MT * W <= 8 ? 4 : 2;  // LDS: SLOTS × MT·W KiB
+  return flat_reduce<MT, W>() ? kSW - 1 : (MT * W <= 8 ? 4 : 2);  // LDS: SLOTS × MT·W KiB
+}
+// The LDS a launch's reductions share: its row workgroups reduce MT·W tiles,
+// its latent workgroups MT·1 tiles (which may take the flat form where the row
+// tiles do not).
+template <int MT, int W>
+constexpr int red_len() {
+  constexpr int rows = red_slots<MT, W>() * MT * W * kWave;
+  constexpr int lat = red_slots<MT, 1>() * MT * kWave;
+  return rows > lat ? rows : lat;
 }
 
-template <int MT, int W>
-__device__ __forceinline__ void tree_reduce(f32x4 (&acc)[MT][W], f32x4* red, int wid, int lane) {
+template <int MT, int W, int NR>
+__device__ __forceinline__ void tree_reduce(f32x4 (&acc)[MT][W], f32x4 (&red)[NR], int wid, int lane) {
   constexpr int SLOTS = red_slots<MT, W>();
+  static_assert(SLOTS * MT * W * kWave <= NR, "the reduction's tiles fit the launch's LDS buffer");
+  if constexpr (flat_reduce<MT, W>()) {
+    if (wid > 0) {
+      f32x4* slot = red + (wid - 1) * (MT * W * kWave);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int s = 0; s < W; ++s) slot[(mt * W + s) * kWave + lane] = acc[mt][s];
+    }
+    __syncthreads();
+    if (wid == 0) {
+#pragma unroll
+      for (int k = 0; k < kSW - 1; ++k) {
+        const f32x4* slot = red + k * (MT * W * kWave);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int s = 0; s < W; ++s) acc[mt][s] += slot[(mt * W + s) * kWave + lane];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int half = kSW / 2; half >= 1; half /= 2) {
 #pragma unroll
@@ -402,55 +441,120 @@ struct SlrArgs {
   int dep_lat_base;  // this member's first latent / row workgroup among the
   int dep_row_base;  // stage's waiters of one token tile
   int* done;
-  int done_copies;   // copies of `done` that have waiters (min(kDepCopies, its stage's waiters))
 };
 
-// A stage's words, per token tile: kDepCopies copies of [finished row tiles of
-// the source | waiters passed], each copy in its own 512-byte slot (the finished
-// count at +0, the passed count at +256 bytes). A word that hundreds of
-// workgroups poll serialises their accesses (and the increments they wait for)
-// at one memory location: measured 5-8 µs per hand-over with one copy for
-// every stage. The source's row tiles add 1 to every copy; waiter w polls copy
-// w % kDepCopies (copies no waiter polls are left alone, so every copy nets
-// to zero in each launch).
+// A stage's words, per token tile: kDepCopies slots of 512 bytes. Slot c holds
+// at +0 the finished row tiles j of the source with j % kDepCopies == c, and at
+// +256 bytes the waiters w with w % kDepCopies == c that have passed; slot 0
+// also holds at +384 bytes the slots whose waiters have all passed. Same-address
+// atomics are served one after another (tens of ns each), so each finished row
+// tile makes ONE increment, spreading a source's NB increments over 16 words,
+// and a waiter reads all 16 counts with one 16-lane load. Measured on the 1B
+// layer: every row tile adding to 16 copies (each copy taking NB increments)
+// and each waiter taking a returning "passed" ticket before it went on cost
+// 1.1-2.8 µs per hand-over.
 constexpr int kDepCopies = 16;
 constexpr int kDepSlotInts = 128;
 constexpr int kDepPassedInts = 64;
-constexpr int kDepSleep = 2;  // s_sleep between polls of a stage's input count
+constexpr int kDepClosedInts = 96;
+constexpr int kDepSleep = 2;  // s_sleep between polls of a stage's input counts
+
+// Increments slot c's count takes per launch when n things are dealt out by
+// index modulo kDepCopies.
+__device__ __forceinline__ int dep_share(int n, int c) {
+  return n / kDepCopies + (c < n % kDepCopies ? 1 : 0);
+}
 
 // Chained stages: wait until the source member has finished every row tile of
-// token tile mg in this launch (one thread polls, the barrier releases the
-// workgroup); w is the workgroup's index among the stage's waiters of that
-// tile. The last waiter of a copy returns both of its words to zero by
-// subtracting what the launch adds to them, so they are zero at rest whatever
-// the order of arrivals, a wait that gave up included.
-__device__ __forceinline__ void wait_dep(const SlrArgs& a, int mg, int w) {
-  if (threadIdx.x == 0) {
-    const int c = w % kDepCopies;
-    const int n_c = a.dep_waiters / kDepCopies + (c < a.dep_waiters % kDepCopies ? 1 : 0);
-    int* word = a.dep + ((int64_t)mg * kDepCopies + c) * kDepSlotInts;
-    wait_at_least<int, kDepSleep>(word, a.dep_need + a.wait_bias, a.status, a.wait_polls);
-    if (rmw_add(word + kDepPassedInts, 1) == n_c - 1) {
-      rmw_add(word, -a.dep_need);
-      rmw_add(word + kDepPassedInts, -n_c);
+// token tile mg in this launch. Wave 0 polls the 16 counts, the barrier
+// releases the workgroup. The bookkeeping that returns the words to zero
+// (dep_close) runs when the workgroup ends, off the path to its output.
+__device__ __forceinline__ void wait_dep(const SlrArgs& a, int mg) {
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    const bool mine = lane < kDepCopies;
+    const int* word = a.dep + ((int64_t)mg * kDepCopies + (mine ? lane : 0)) * kDepSlotInts;
+    const int need = dep_share(a.dep_need, mine ? lane : 0) + a.wait_bias;
+    for (int n = 0;; ++n) {
+      const int v = mine ? __hip_atomic_load(const_cast<int*>(word), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT)
+                         : need;
+      if (__builtin_amdgcn_ballot_w64(v < need) == 0) break;
+      if (n >= a.wait_polls) {
+        if (lane == 0) st_u64(a.status, 1);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(kDepSleep);
     }
   }
   __syncthreads();
+}
+
+// Called once by each waiter (wave 0, after its workgroup's work): w is its
+// index among the stage's waiters of token tile mg. The waiter that passes last
+// subtracts what the launch added to every word, so the words are zero at rest
+// whatever the order of arrivals, a wait that gave up included.
+__device__ __forceinline__ void dep_close(const SlrArgs& a, int mg, int w) {
+  const int lane = threadIdx.x;
+  int* base = a.dep + (int64_t)mg * kDepCopies * kDepSlotInts;
+  const int c = w % kDepCopies;
+  int last = 0;
+  if (lane == 0) {
+    last = rmw_add(base + c * kDepSlotInts + kDepPassedInts, 1) == dep_share(a.dep_waiters, c) - 1;
+    if (last) {
+      const int slots = a.dep_waiters < kDepCopies ? a.dep_waiters : kDepCopies;
+      last = rmw_add(base + kDepClosedInts, 1) == slots - 1;
+    }
+  }
+  if (!__builtin_amdgcn_readfirstlane(last)) return;
+  if (lane < kDepCopies) {
+    const int slots = a.dep_waiters < kDepCopies ? a.dep_waiters : kDepCopies;
+    const int n_src = dep_share(a.dep_need, lane);
+    if (n_src) rmw_add(base + lane * kDepSlotInts, -n_src);
+    if (lane < slots) rmw_add(base + lane * kDepSlotInts + kDepPassedInts, -dep_share(a.dep_waiters, lane));
+    if (lane == 0) rmw_add(base + kDepClosedInts, -slots);
+  }
 }
 
 __device__ __forceinline__ u64* tile_sync(const SlrArgs& a, int mg) {
   return a.sync + 1 + (int64_t)mg * (2 + a.n_rt);
 }
 
-// Copies of a token tile's final-latent count, each in its own 512-byte slot:
-// the count every consumer of the tile polls, so that the polls (and the
-// latent's increments behind them) spread over several memory locations
-// instead of queueing at one.
+// A token tile's final-latent counts, in kFinCopies 512-byte slots: rank tile
+// rt adds 1 to slot rt % kFinCopies's count when its final tile is written (one
+// increment, so no count takes more than ceil(n_rt / 8) per launch), and a
+// consumer reads all 8 counts with one 8-lane load. Word kFinTicket of each slot
+// holds consumer tickets.
 constexpr int kFinCopies = 8;
 constexpr int kFinSlotWords = 64;
 constexpr int kFinTicket = 32;
 __device__ __forceinline__ u64* fin_copy(const SlrArgs& a, int mg, int c) {
   return a.fin + ((int64_t)mg * kFinCopies + c) * kFinSlotWords;
+}
+__device__ __forceinline__ int fin_share(int n, int c) {
+  return n / kFinCopies + (c < n % kFinCopies ? 1 : 0);
+}
+
+// Wave 0 of a consumer: wait until every rank tile of token tile mg has its
+// final latent of launch `launch` (counted from the consumer's ticket: every
+// launch adds fin_share(n_rt, c) to slot c, so launch k is complete when slot c
+// holds (k + 1)·fin_share(n_rt, c)).
+__device__ __forceinline__ void wait_fin(const SlrArgs& a, int mg, u64 launch) {
+  const int lane = threadIdx.x;
+  const bool mine = lane < kFinCopies;
+  const u64* word = fin_copy(a, mg, mine ? lane : 0);
+  const u64 need = (launch + 1) * (u64)fin_share(a.n_rt, mine ? lane : 0) + (u64)a.wait_bias;
+  for (int n = 0;; ++n) {
+    const u64 v = mine ? __hip_atomic_load(const_cast<u64*>(word), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT)
+                       : need;
+    if (__builtin_amdgcn_ballot_w64(v < need) == 0) break;
+    if (n >= a.wait_polls) {
+      if (lane == 0) st_u64(a.status, 1);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -460,8 +564,8 @@ __device__ __forceinline__ u64* fin_copy(const SlrArgs& a, int mg, int c) {
 // is an input of the launch; 2 = a chained member whose x another stage of the
 // launch writes: its B loads go out before it waits for x, and x is read
 // device-coherently.
-template <int DT, int MT, int CH = 0>
-__device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) {
+template <int DT, int MT, int CH = 0, int NR>
+__device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)[NR]) {
   constexpr int KE = (DT == DT_F32) ? 4 : 8;
   using MM = Mma<DT, KE>;
   using Frag = typename MM::Frag;
@@ -519,7 +623,7 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
       const int u = u0 + k * kSW;
       if (u < ue) bf[k] = load_kfrag_full<DT, KE>(a.B, brow + u * KM + KE * g);
     }
-    wait_dep(a, mg, a.dep_lat_base + wg % per_mg);
+    wait_dep(a, mg);
 #pragma unroll
     for (int k = 0; k < UNR; ++k)
       if (u0 + k * kSW < ue) load_x(u0 + k * kSW, xf[k]);
@@ -609,7 +713,7 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
       }
     }
   wait_mem();
-  if (lane < kFinCopies) rmw_add64(fin_copy(a, mg, lane), 1);
+  if (lane == 0) rmw_add64(fin_copy(a, mg, rt % kFinCopies), 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -622,8 +726,8 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4* red) 
 // and q (any multiple of KM) is a runtime value.
 // CH: as for latent_wg (chained launches; 2 = x written by an earlier stage:
 // the first batch's weight loads go out before the wait for x).
-template <int DT, int P, int KE, int MT, int MODE, int UNR, int SF, int CH = 0>
-__device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f32x4* red) {
+template <int DT, int P, int KE, int MT, int MODE, int UNR, int SF, int CH = 0, int NR>
+__device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f32x4 (&red)[NR]) {
   constexpr int W = P / 16;
   using MM = Mma<DT, KE>;
   using Frag = typename MM::Frag;
@@ -767,7 +871,7 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
 #pragma unroll
     for (int k = 0; k < UNR; ++k)
       if (v0 + k * kSW < ve) load_w(voff[k], raw[k]);
-    wait_dep(a, mg, a.dep_row_base + chunk);
+    wait_dep(a, mg);
 #pragma unroll
     for (int k = 0; k < UNR; ++k)
       if (v0 + k * kSW < ve) load_x(colk[k], xf[k]);
@@ -799,13 +903,12 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   // other waves, which then read it device-coherently.
   if constexpr (MODE == MODE_FUSED) {
     if (used_t) {
-      if (threadIdx.x == 0) {
-        // this copy's consumers per launch
-        const int n_tc =
-            per_row ? a.NB / kFinCopies + (tc < a.NB % kFinCopies ? 1 : 0) : a.lr_wgs;
-        const u64 target = (ticket / (u64)n_tc + 1) * (u64)a.n_rt;
-        wait_at_least<u64>(fin_copy(a, mg, per_row ? tc : chunk % kFinCopies),
-                           target + (u64)a.wait_bias, a.status, a.wait_polls);
+      if (threadIdx.x < kWave) {
+        // the ticket's launch: this copy's consumers per launch
+        const int n_tc = per_row ? fin_share(a.NB, tc) : a.lr_wgs;
+        const u64 tk = ((u64)__builtin_amdgcn_readfirstlane((uint32_t)(ticket >> 32)) << 32) |
+                       (u64)__builtin_amdgcn_readfirstlane((uint32_t)ticket);
+        wait_fin(a, mg, tk / (u64)n_tc);
       }
       __syncthreads();
       const auto tr = dev_rsrc(a.t);
@@ -918,8 +1021,7 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
     // count this row tile as finished once its stores are acknowledged
     if (dev_out) {
       wait_mem();
-      if (lane < a.done_copies)
-        rmw_add(a.done + ((int64_t)mg * kDepCopies + lane) * kDepSlotInts, 1);
+      if (lane == 0) rmw_add(a.done + ((int64_t)mg * kDepCopies + row % kDepCopies) * kDepSlotInts, 1);
     }
   }
 }
@@ -946,8 +1048,7 @@ __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_ke
   (void)g_by_value;
   const GroupArgs& g = *(const GroupArgs*)__builtin_amdgcn_kernarg_segment_ptr();
   constexpr int W = P / 16;
-  constexpr int SLOTS = red_slots<MT, W>();
-  __shared__ f32x4 red[SLOTS * MT * W * kWave];
+  __shared__ f32x4 red[red_len<MT, W>()];
   const int b = blockIdx.x;
   if constexpr (MODE == MODE_FUSED) {
     if (b < g.lat_total) {
@@ -995,8 +1096,8 @@ using ChainArgs = ChainDesc<kMaxChain>;
 using ChainTab = ChainDesc<kMaxChainTab>;
 static_assert(sizeof(ChainArgs) <= 4096, "kernel arguments of a chained launch");
 
-template <int DT, int P, int KE, int MT, int UNR, int SF, int NMAX>
-__device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4* red) {
+template <int DT, int P, int KE, int MT, int UNR, int SF, int NMAX, int NR>
+__device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4 (&red)[NR]) {
   const int b = blockIdx.x;
   // the last segment starting at or before b (empty segments share a start)
   int lo = 0, hi = g.n_seg - 1;
@@ -1008,13 +1109,22 @@ __device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4* red) {
   const SlrArgs& a = g.m[g.seg_member[lo]];
   const int lb = b - g.seg_start[lo];
   if (!g.seg_rows[lo]) {
-    if (a.dep) latent_wg<DT, MT, 2>(a, lb, red);
-    else latent_wg<DT, MT, 1>(a, lb, red);
+    if (a.dep) {
+      latent_wg<DT, MT, 2>(a, lb, red);
+      const int per_mg = a.n_rt * a.n_kc;
+      if (threadIdx.x < kWave) dep_close(a, lb / per_mg, a.dep_lat_base + lb % per_mg);
+    } else {
+      latent_wg<DT, MT, 1>(a, lb, red);
+    }
     return;
   }
   const int mg = lb / a.n_chunks, chunk = lb % a.n_chunks;
-  if (a.dep) stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 2>(a, chunk, mg, red);
-  else stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 1>(a, chunk, mg, red);
+  if (a.dep) {
+    stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 2>(a, chunk, mg, red);
+    if (threadIdx.x < kWave) dep_close(a, mg, a.dep_row_base + chunk);
+  } else {
+    stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 1>(a, chunk, mg, red);
+  }
 }
 
 template <int DT, int P, int KE, int MT, int UNR, int SF>
@@ -1022,7 +1132,7 @@ __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_ch
     ChainArgs c_by_value) {
   (void)c_by_value;
   constexpr int W = P / 16;
-  __shared__ f32x4 red[red_slots<MT, W>() * MT * W * kWave];
+  __shared__ f32x4 red[red_len<MT, W>()];
   chain_wg<DT, P, KE, MT, UNR, SF, kMaxChain>(
       *(const ChainArgs*)__builtin_amdgcn_kernarg_segment_ptr(), red);
 }
@@ -1035,7 +1145,7 @@ template <int DT, int P, int KE, int MT, int UNR, int SF>
 __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_chain_tab_kernel(
     ChainTabPtr tab) {
   constexpr int W = P / 16;
-  __shared__ f32x4 red[red_slots<MT, W>() * MT * W * kWave];
+  __shared__ f32x4 red[red_len<MT, W>()];
   chain_wg<DT, P, KE, MT, UNR, SF, kMaxChainTab>(*(const ChainTab*)tab, red);
 }
 
