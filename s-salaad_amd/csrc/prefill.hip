@@ -143,6 +143,51 @@ struct Tile {
   static constexpr int LDS = (BM + BN) * kK;  // elements per LDS stage (rows of 128 bytes)
 };
 
+// Row items of a member, in order: its token tiles in groups of TG; within a
+// group, its row groups (or part records) one after another, each with the
+// group's token tiles adjacent. The items of one XCD are a contiguous range,
+// so an XCD runs a block-row's token tiles together and its L2 serves the
+// block-row's weights to all of them. When D XCDs share a group of token
+// tiles, the row groups are dealt to them round-robin (XCD chunk c holds row
+// groups c, c + D, c + 2D, ...), so that long rows of a skewed structure
+// spread over the XCDs instead of filling one contiguous range.
+// Item t → token tile tt and row group / part record j of n per token tile.
+// Pairs of narrow (128-token) tiles, whose x panels stay in L2 together, when
+// the token tiles pair up evenly: the 7B FFN (11008×4096, 64×64 blocks) fetched
+// 119 → 75 MB per call beyond L2 at 256 tokens (60.6 MB compulsory) and ran
+// 81.0 / 99.9 / 145.3 → 78.3 / 97.5 / 141.0 µs at 768 / 1024 / 1536 tokens
+// (best of three interleaved runs). With the tall tile's 2 MB
+// panels the pairs evicted each other's x and skewed calls lost 3-6%, and an
+// odd token-tile count (384 tokens: a lone last tile) lost 8%: those keep one
+// token tile per group (TG = 1: the items in token-tile order).
+template <int BM>
+__device__ __forceinline__ void tile_of(int t, int n, int MG, int& tt, int& j) {
+  constexpr int TG = 2;
+  if (BM > 128 || MG % TG != 0) {
+    tt = t / n;
+    j = t - tt * n;
+    return;
+  }
+  const int blk = TG * n;
+  const int pg = t / blk, r = t - pg * blk;
+  const int tg = min(TG, MG - pg * TG);
+  const int q = r / tg;  // position of the row group within the token-tile group
+  tt = pg * TG + (r - q * tg);
+  const int n_pg = (MG + TG - 1) / TG;
+  const int D = max(1, min(n, kXcds / n_pg));  // XCDs sharing this group of token tiles
+  const int base = n / D, rem = n % D;         // chunks 0..rem-1 hold base + 1 row groups
+  int c, i;
+  if (q < rem * (base + 1)) {
+    c = q / (base + 1);
+    i = q - c * (base + 1);
+  } else {
+    const int q2 = q - rem * (base + 1);
+    c = rem + q2 / base;
+    i = q2 - (c - rem) * base;
+  }
+  j = c + i * D;
+}
+
 __device__ __forceinline__ int ld_word(const int32_t* p, int i) {
   return __builtin_amdgcn_readfirstlane(ld_uniform(p, i));
 }
@@ -339,7 +384,8 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
     if (mb.parts != nullptr) {
       // the member's part table (ssl_prefill_parts_build): per token tile,
       // its records in turn, each a group's step range and its part of them
-      const int tt = local / mb.n_parts, j = local - tt * mb.n_parts;
+      int tt, j;
+      tile_of<BM>(local, mb.n_parts, (M + BM - 1) / BM, tt, j);
       const int32_t* pr = mb.parts + (int64_t)j * kPartInts;
       grp = ld_word(pr, 0);
       s_begin = ld_word(pr, 1);
@@ -361,8 +407,8 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
       m0 = tt * BM;
       gr = mb.groups + (int64_t)grp * (2 + G);
     } else {
-      const int tt = tile / mb.n_groups;
-      grp = tile % mb.n_groups;
+      int tt;
+      tile_of<BM>(tile, mb.n_groups, (M + BM - 1) / BM, tt, grp);
       m0 = tt * BM;
       gr = mb.groups + (int64_t)grp * (2 + G);
       // part kp of the group's sparse steps; the last part also the low-rank ones
