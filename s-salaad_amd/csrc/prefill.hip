@@ -156,14 +156,19 @@ struct Tile {
 // the token tiles pair up evenly: the 7B FFN (11008×4096, 64×64 blocks) fetched
 // 119 → 75 MB per call beyond L2 at 256 tokens (60.6 MB compulsory) and ran
 // 81.0 / 99.9 / 145.3 → 78.3 / 97.5 / 141.0 µs at 768 / 1024 / 1536 tokens
-// (best of three interleaved runs). With the tall tile's 2 MB
-// panels the pairs evicted each other's x and skewed calls lost 3-6%, and an
-// odd token-tile count (384 tokens: a lone last tile) lost 8%: those keep one
-// token tile per group (TG = 1: the items in token-tile order).
-template <int BM>
-__device__ __forceinline__ void tile_of(int t, int n, int MG, int& tt, int& j) {
+// (best of three interleaved runs). Larger panels evict each other's x: with
+// the tall tile's 2 MB panels skewed calls lost 3-6%, and with the narrow
+// tile's 2.8 MB panels at 11008 input features the Zipf 10%-density calls
+// lost 12% (16×16 blocks, 176 → 198 µs) and 8% (32×32). An odd token-tile
+// count (384 tokens: a lone last tile) lost 8%. Those keep one token tile per
+// group (TG = 1: the items in token-tile order); pairs need narrow tiles, an
+// even token-tile count and panels of at most kPairPanelBytes.
+constexpr int64_t kPairPanelBytes = 1 << 20;
+
+template <int BM, int EB>
+__device__ __forceinline__ void tile_of(int t, int n, int MG, int m, int& tt, int& j) {
   constexpr int TG = 2;
-  if (BM > 128 || MG % TG != 0) {
+  if (BM > 128 || MG % TG != 0 || (int64_t)BM * m * EB > kPairPanelBytes) {
     tt = t / n;
     j = t - tt * n;
     return;
@@ -385,7 +390,7 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
       // the member's part table (ssl_prefill_parts_build): per token tile,
       // its records in turn, each a group's step range and its part of them
       int tt, j;
-      tile_of<BM>(local, mb.n_parts, (M + BM - 1) / BM, tt, j);
+      tile_of<BM, EB>(local, mb.n_parts, (M + BM - 1) / BM, m, tt, j);
       const int32_t* pr = mb.parts + (int64_t)j * kPartInts;
       grp = ld_word(pr, 0);
       s_begin = ld_word(pr, 1);
@@ -408,7 +413,7 @@ __device__ __forceinline__ void pf_body(const PfArgs& a, int bid, int n_bid,
       gr = mb.groups + (int64_t)grp * (2 + G);
     } else {
       int tt;
-      tile_of<BM>(tile, mb.n_groups, (M + BM - 1) / BM, tt, grp);
+      tile_of<BM, EB>(tile, mb.n_groups, (M + BM - 1) / BM, m, tt, grp);
       m0 = tt * BM;
       gr = mb.groups + (int64_t)grp * (2 + G);
       // part kp of the group's sparse steps; the last part also the low-rank ones
