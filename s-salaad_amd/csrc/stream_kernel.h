@@ -1050,19 +1050,31 @@ __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_ke
   constexpr int W = P / 16;
   __shared__ f32x4 red[red_len<MT, W>()];
   const int b = blockIdx.x;
+  // the member of workgroup b: every member's offsets in one batch of scalar
+  // loads and a chain of selects (no dependent loads before the work starts)
   if constexpr (MODE == MODE_FUSED) {
     if (b < g.lat_total) {
-      int i = 0;
-      while (i + 1 < g.n && b >= g.lat_off[i + 1]) ++i;
-      latent_wg<DT, MT>(g.m[i], b - g.lat_off[i], red);
+      int i = 0, off = g.lat_off[0];
+#pragma unroll
+      for (int k = 1; k < kMaxGroup; ++k) {
+        const bool in = k < g.n && b >= g.lat_off[k];
+        i = in ? k : i;
+        off = in ? g.lat_off[k] : off;
+      }
+      latent_wg<DT, MT>(g.m[i], b - off, red);
       return;
     }
   }
   const int sb = b - (MODE == MODE_FUSED ? g.lat_total : 0);
-  int i = 0;
-  while (i + 1 < g.n && sb >= g.str_off[i + 1]) ++i;
+  int i = 0, off = g.str_off[0];
+#pragma unroll
+  for (int k = 1; k < kMaxGroup; ++k) {
+    const bool in = k < g.n && sb >= g.str_off[k];
+    i = in ? k : i;
+    off = in ? g.str_off[k] : off;
+  }
   const SlrArgs& a = g.m[i];
-  const int lb = sb - g.str_off[i];
+  const int lb = sb - off;
   const int mg = lb / a.n_chunks, chunk = lb % a.n_chunks;
   stream_wg<DT, P, KE, MT, MODE, UNR, SF>(a, chunk, mg, red);
 }
@@ -1100,15 +1112,36 @@ template <int DT, int P, int KE, int MT, int UNR, int SF, int NMAX, int NR>
 __device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4 (&red)[NR]) {
   const int b = blockIdx.x;
   // the last segment starting at or before b (empty segments share a start)
-  int lo = 0, hi = g.n_seg - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (b >= g.seg_start[mid]) lo = mid;
-    else hi = mid - 1;
+  int member, rows, start;
+  if constexpr (2 * NMAX <= 16) {
+    // Kernel arguments: every segment's words in one batch of scalar loads and
+    // a chain of selects. A binary search's dependent loads, each a round trip
+    // to L2 on a cold scalar cache, put a workgroup's first work 1.0-1.6 µs
+    // after its first instruction.
+    member = g.seg_member[0];
+    rows = g.seg_rows[0];
+    start = g.seg_start[0];
+#pragma unroll
+    for (int i = 1; i < 2 * NMAX; ++i) {
+      const bool in = i < g.n_seg && b >= g.seg_start[i];
+      member = in ? g.seg_member[i] : member;
+      rows = in ? g.seg_rows[i] : rows;
+      start = in ? g.seg_start[i] : start;
+    }
+  } else {
+    int lo = 0, hi = g.n_seg - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (b >= g.seg_start[mid]) lo = mid;
+      else hi = mid - 1;
+    }
+    member = g.seg_member[lo];
+    rows = g.seg_rows[lo];
+    start = g.seg_start[lo];
   }
-  const SlrArgs& a = g.m[g.seg_member[lo]];
-  const int lb = b - g.seg_start[lo];
-  if (!g.seg_rows[lo]) {
+  const SlrArgs& a = g.m[member];
+  const int lb = b - start;
+  if (!rows) {
     if (a.dep) {
       latent_wg<DT, MT, 2>(a, lb, red);
       const int per_mg = a.n_rt * a.n_kc;
