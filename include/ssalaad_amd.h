@@ -91,12 +91,17 @@ int ssl_status_word_alloc(void** host_ptr, void** device_ptr);
  *                               prefill call splits its row groups in that
  *                               many parts (when the caller's workspace holds
  *                               the partial tiles).
+ *   SSL_DEBUG_CHAIN_FRAG        0: the library decides whether a chained launch
+ *                               of 32- or 64-wide blocks passes its stages'
+ *                               inputs in fragment order (ssl_slr_stage.xf);
+ *                               1: never (one-tile calls); 2: always.
  * Not for concurrent use with calls on other threads. */
 typedef enum {
   SSL_DEBUG_PREFILL_TILE = 0,
   SSL_DEBUG_WAIT_POLLS = 1,
   SSL_DEBUG_WAIT_UNREACHABLE = 2,
-  SSL_DEBUG_PREFILL_SPLIT = 3
+  SSL_DEBUG_PREFILL_SPLIT = 3,
+  SSL_DEBUG_CHAIN_FRAG = 4
 } ssl_debug_knob;
 int ssl_debug_set(int32_t knob, int64_t value);
 
@@ -444,9 +449,20 @@ typedef struct ssl_slr_stage {
   int32_t* sync;   /* later stages: ssl_slr_chain_sync_count(M) zeroed int32 words,
                     * 256-byte aligned */
   int64_t n_sync;
+  void* xf;        /* later stages of calls of 8 or more token rows with 32- or 64-wide
+                    * blocks (ignored otherwise, may be NULL then): room for a second
+                    * copy of src's output in MFMA-fragment order, which src writes and
+                    * this stage reads (contiguous 1 KiB loads instead of 16 row
+                    * segments): ssl_slr_chain_frag_bytes(M, src's NB · block_p) bytes,
+                    * 256-byte aligned, no initial contents needed */
+  int64_t xf_bytes;
 } ssl_slr_stage;
 
 int64_t ssl_slr_chain_sync_count(int64_t M);
+/* Bytes of a fragment-order copy (ssl_slr_stage.xf) of an M-row output with
+ * n_out features: 1 KiB per 16 token rows (in whole tiles of the call) and 32
+ * features. No reference counterpart (a layout of this library's kernels). */
+int64_t ssl_slr_chain_frag_bytes(int64_t M, int64_t n_out);
 int ssl_slr_forward_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,
                           const ssl_slr_stage* stages, int32_t n_stages,
                           const ssl_slr_member* members, int32_t n_members, void* stream);

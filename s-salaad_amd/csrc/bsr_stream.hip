@@ -234,6 +234,23 @@ void fill_args(SlrArgs& a, const ssl_slr_member& mb, const Layout& L, const void
 // K units (of 32 in_features) per latent chunk in a chained stage after the
 // first: one batch of loads for each of the 8 waves.
 constexpr int kChainLatentUnits = 64;
+// Token rows from which a chained launch of 32- or 64-wide blocks passes the
+// stages' inputs in fragment order (each wave reads a unit as one contiguous
+// 1 KiB load). Below it the 16-row tiles are mostly padding, and the rows
+// read by row segments (fewer bytes) were faster: LLaMA-1B layer stack at 1 /
+// 4 / 16 token rows 1274 / 4713 / 17.2 k tok/s by rows, 1176 / 4685 / 18.4 k
+// in fragment order.
+constexpr int64_t kChainFragMinM = 8;
+
+// Whether a chained launch's later stages read fragment-order inputs.
+bool chain_frag(int64_t M, int32_t block_p) {
+  if (block_p != 32 && block_p != 64) return false;
+  if (tile_mt(M) > 1) return true;  // taller tiles have only the fragment kernels
+  const int64_t k = debug_knobs().chain_frag;
+  if (k == 1) return false;
+  if (k == 2) return true;
+  return M >= kChainFragMinM;
+}
 
 // Checks a chained launch and fills its descriptor (c, zeroed by the caller,
 // with room for NMAX members); c->grid = 0 when there is nothing to launch.
@@ -297,6 +314,18 @@ int build_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,
                   (long long)n_sync);
     if (M * src.ldy * eb > 0x7fffffffLL)
       return fail(SSL_ERR_UNSUPPORTED, "stage %d: its input is beyond 2 GiB; split the call by tokens", s);
+    if (!st.xf && chain_frag(M, block_p))
+      return fail(SSL_ERR_WORKSPACE, "stage %d: %lld token rows of 32- or 64-wide blocks need xf "
+                  "(%lld bytes)", s, (long long)M,
+                  (long long)ssl_slr_chain_frag_bytes(M, src.NB * block_p));
+    if (st.xf) {
+      const int64_t need = ssl_slr_chain_frag_bytes(M, src.NB * block_p);
+      if (!aligned(st.xf, 256) || st.xf_bytes < need)
+        return fail(SSL_ERR_WORKSPACE, "stage %d: xf must be 256-byte aligned with %lld bytes", s,
+                    (long long)need);
+      if (need > 0x7fffffffLL)
+        return fail(SSL_ERR_UNSUPPORTED, "stage %d: its fragment copy is beyond 2 GiB", s);
+    }
   }
   if (next != n_members) return fail(SSL_ERR_INVALID, "every member belongs to one stage");
 
@@ -372,6 +401,17 @@ int build_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,
         c->m[i].dep_waiters = waiters;
       }
       c->m[st.src].done = st.sync;
+      // the source's output also in fragment order (whole 32-column units per
+      // row tile: 32- and 64-wide tiles)
+      if (chain_frag(M, block_p)) {
+        const int units = (int)(members[st.src].NB * block_p / 32);
+        for (int i = st.first; i < st.first + st.count; ++i) {
+          c->m[i].xf = st.xf;
+          c->m[i].xf_units = units;
+        }
+        c->m[st.src].yf = st.xf;
+        c->m[st.src].yf_units = units;
+      }
     }
   }
   c->n_seg = nseg;
@@ -381,6 +421,7 @@ int build_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,
   c->block_p = block_p;
   c->dtype = dtype;
   c->sf = s_format == SSL_S_NM24 ? SF_NM24 : SF_BSR;
+  c->fr = chain_frag(M, block_p) ? 1 : 0;
   (void)MT;
   return SSL_OK;
 }
@@ -390,8 +431,8 @@ int launch_chain(const ChainDesc<NMAX>& c, const ChainArgs* a, const ChainTab* t
                  hipStream_t stream) {
   const int MT = tile_mt(c.M);
   hipError_t e = c.dtype == SSL_BF16
-                     ? chain_launch<DT_BF16>(c.sf, c.block_p, MT, a, tab, c.grid, stream)
-                     : chain_launch<DT_F16>(c.sf, c.block_p, MT, a, tab, c.grid, stream);
+                     ? chain_launch<DT_BF16>(c.sf, c.block_p, MT, c.fr != 0, a, tab, c.grid, stream)
+                     : chain_launch<DT_F16>(c.sf, c.block_p, MT, c.fr != 0, a, tab, c.grid, stream);
   return check_hip(e, "slr chained launch");
 }
 
@@ -874,6 +915,13 @@ int64_t ssl_slr_chain_sync_count(int64_t M) {
   if (M <= 0) return 0;
   const int MT = tile_mt(M);
   return (int64_t)kDepCopies * kDepSlotInts * ((M + 16 * MT - 1) / (16 * MT));
+}
+
+int64_t ssl_slr_chain_frag_bytes(int64_t M, int64_t n_out) {
+  if (M <= 0 || n_out <= 0) return 0;
+  const int MT = tile_mt(M);
+  const int64_t tiles = (M + 16 * MT - 1) / (16 * MT) * MT;
+  return tiles * ((n_out + 31) / 32) * 1024;
 }
 
 int ssl_slr_forward_chain(int64_t M, int32_t block_p, int32_t block_q, int32_t dtype,

@@ -107,6 +107,10 @@ int ssl_debug_set(int32_t knob, int64_t value) {
       if (value < 0 || value > 4) return fail(SSL_ERR_INVALID, "prefill split override must be 0 to 4");
       k.prefill_split = value;
       return SSL_OK;
+    case SSL_DEBUG_CHAIN_FRAG:
+      if (value < 0 || value > 2) return fail(SSL_ERR_INVALID, "chain fragment override must be 0 to 2");
+      k.chain_frag = value;
+      return SSL_OK;
   }
   return fail(SSL_ERR_INVALID, "unknown debug knob %d", knob);
 }

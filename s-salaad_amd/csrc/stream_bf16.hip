@@ -12,9 +12,9 @@ hipError_t stream_launch<DT_BF16>(int mode, int sf, int P, int KE, int MT, const
 }
 
 template <>
-hipError_t chain_launch<DT_BF16>(int sf, int P, int MT, const ChainArgs* a, const ChainTab* tab,
-                             int64_t blocks, hipStream_t s) {
-  return chain_dispatch<DT_BF16>(sf, P, MT, a, tab, blocks, s);
+hipError_t chain_launch<DT_BF16>(int sf, int P, int MT, bool fr, const ChainArgs* a,
+                             const ChainTab* tab, int64_t blocks, hipStream_t s) {
+  return chain_dispatch<DT_BF16>(sf, P, MT, fr, a, tab, blocks, s);
 }
 
 }  // namespace ssl

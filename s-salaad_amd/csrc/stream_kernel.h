@@ -136,6 +136,8 @@ __device__ __forceinline__ void st_dev_vec(__amdgpu_buffer_rsrc_t r, int byte_of
 // All of this thread's earlier memory operations have completed (stores are
 // acknowledged by the device-coherent level).
 __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
+// the wave's LDS accesses completed (not its vector memory accesses)
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 typedef unsigned long long u64;
 constexpr int kLatentUnits = 840;  // divisible by every latent split 1..8
@@ -363,6 +365,32 @@ __device__ __forceinline__ void add_partial(f32x4 (&tot)[MT][W], const float* pa
     }
 }
 
+// The same for tiles in any register layout: every lane's accumulators whole,
+// lane-native (the TSZ floats of a tile are exactly MT·W f32x4 per lane).
+template <int MT, int W>
+__device__ __forceinline__ void store_partial_lanes(const f32x4 (&acc)[MT][W], float* part, int lane) {
+  const auto r = dev_rsrc(part);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int s = 0; s < W; ++s) {
+      const float v[4] = {acc[mt][s][0], acc[mt][s][1], acc[mt][s][2], acc[mt][s][3]};
+      st_dev_vec<4>(r, (((mt * W + s) * kWave + lane) * 4) * 4, v);
+    }
+}
+template <int MT, int W>
+__device__ __forceinline__ void add_partial_lanes(f32x4 (&tot)[MT][W], const float* part, int lane) {
+  const auto r = dev_rsrc(part);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int s = 0; s < W; ++s) {
+      float v[4];
+      ld_dev_vec<4>(r, (((mt * W + s) * kWave + lane) * 4) * 4, v);
+      tot[mt][s] += f32x4{v[0], v[1], v[2], v[3]};
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Kernel arguments (one struct for every mode).
 // ---------------------------------------------------------------------------
@@ -441,6 +469,17 @@ struct SlrArgs {
   int dep_lat_base;  // this member's first latent / row workgroup among the
   int dep_row_base;  // stage's waiters of one token tile
   int* done;
+  // Fragment-order copies (chained launches, 16-bit, 32- or 64-wide blocks).
+  // xf, when set, holds x's whole 32-column units as 1 KiB blocks in the order
+  // the MFMA fragments take them: block (mg·MT + mt)·xf_units + u, lane
+  // 16g + c's 16 bytes = row 16·mt + c of token tile mg, columns 32u + 8g ..
+  // 32u + 8g + 7. A wave then reads a unit with one contiguous 1 KiB load
+  // instead of 16 row segments. yf: where this member writes its own output
+  // in that order (yf_units units per token row tile), for the stage reading it.
+  const void* xf;
+  void* yf;
+  int xf_units;
+  int yf_units;
 };
 
 // A stage's words, per token tile: kDepCopies slots of 512 bytes. Slot c holds
@@ -564,7 +603,7 @@ __device__ __forceinline__ void wait_fin(const SlrArgs& a, int mg, u64 launch) {
 // is an input of the launch; 2 = a chained member whose x another stage of the
 // launch writes: its B loads go out before it waits for x, and x is read
 // device-coherently.
-template <int DT, int MT, int CH = 0, int NR>
+template <int DT, int MT, int CH = 0, bool FX = false, int NR>
 __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)[NR]) {
   constexpr int KE = (DT == DT_F32) ? 4 : 8;
   using MM = Mma<DT, KE>;
@@ -588,6 +627,10 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)
   for (int mt = 0; mt < MT; ++mt) acc[mt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const auto xr = dev_rsrc(a.x);
+  const auto xfr = dev_rsrc(a.xf);
+  // FX: whole units of x from its fragment-order copy (chained stages of
+  // 32- and 64-wide blocks, whose source writes one)
+  static_assert(!FX || (CH == 2 && DT != DT_F32 && KE == 8), "fragment-order x: 16-bit chains");
   // x fragments of K unit u for every token row tile
   auto load_x = [&](int u, Frag(&xk)[MT]) {
     const int kcol = u * KM + KE * g;
@@ -595,7 +638,10 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int64_t off = (int64_t)(m0 + min(mt * 16 + c, Mrem - 1)) * a.ldx + kcol;
-        if constexpr (CH == 2) xk[mt] = ld_dev_kfrag<DT, KE>(xr, (int)(off * EB), KE);
+        if constexpr (FX)
+          xk[mt] = ld_dev_kfrag<DT, KE>(xfr, (((mg * MT + mt) * a.xf_units + u) << 10) + lane * 16,
+                                        KE);
+        else if constexpr (CH == 2) xk[mt] = ld_dev_kfrag<DT, KE>(xr, (int)(off * EB), KE);
         else xk[mt] = load_kfrag_full<DT, KE>(a.x, off);
       }
     } else {
@@ -726,7 +772,8 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)
 // and q (any multiple of KM) is a runtime value.
 // CH: as for latent_wg (chained launches; 2 = x written by an earlier stage:
 // the first batch's weight loads go out before the wait for x).
-template <int DT, int P, int KE, int MT, int MODE, int UNR, int SF, int CH = 0, int NR>
+template <int DT, int P, int KE, int MT, int MODE, int UNR, int SF, int CH = 0, bool FR = false,
+          int NR>
 __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f32x4 (&red)[NR]) {
   constexpr int W = P / 16;
   using MM = Mma<DT, KE>;
@@ -796,6 +843,21 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   const int nks = a.nks;
   const int vb = bb * nks, ve = be * nks;
   const auto xr = dev_rsrc(a.x);
+  const auto xfr = dev_rsrc(a.xf);
+  // whole units of x from the fragment-order copy its source writes (chained
+  // stages, 16-bit, 32- and 64-wide blocks: KE = 8, KM = 32 and every slab's
+  // column is a multiple of 32)
+  constexpr bool kFragIn = FR && CH == 2 && DT != DT_F32 && (P == 32 || P == 64);
+  static_assert(!kFragIn || KE == 8, "fragment-order x: 32-column units");
+  // Chained 16-bit members with 32- or 64-wide tiles in the kernels that pass
+  // fragment-order inputs (FR) compute the transposed tile (features × tokens:
+  // the weights as the MFMA's first operand), so that lane (c, g) ends with 4W
+  // adjacent features, W·4g .. W·4g + 4W − 1, of token row 16·mt + c, element
+  // (s, e) being feature W·(4g + e) + s: its output row segment is one vector
+  // store, and for W = 2 it is exactly the lane's 16 bytes of the
+  // fragment-order copy (for W = 4, two of them). (At one token row, where
+  // FR kernels are not used, the transposed tile measured 4% slower.)
+  constexpr bool kSwap = FR && CH > 0 && MODE == MODE_FUSED && DT != DT_F32 && (P == 32 || P == 64);
   // the batch's column indices first, as scalar loads issued together
   auto index = [&](int v0, int(&colk)[UNR], int64_t(&voff)[UNR]) {
 #pragma unroll
@@ -830,7 +892,10 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
       const int rr = mt * 16 + c;
       if (full) {
         const int64_t off = (int64_t)(m0 + min(rr, Mrem - 1)) * a.ldx + kcol;
-        if constexpr (CH == 2) xk[mt] = ld_dev_kfrag<DT, KE>(xr, (int)(off * EB), KE);
+        if constexpr (kFragIn)
+          xk[mt] = ld_dev_kfrag<DT, KE>(
+              xfr, (((mg * MT + mt) * a.xf_units + (colk >> 5)) << 10) + lane * 16, KE);
+        else if constexpr (CH == 2) xk[mt] = ld_dev_kfrag<DT, KE>(xr, (int)(off * EB), KE);
         else xk[mt] = load_kfrag_full<DT, KE>(a.x, off);
       } else {
         const int valid = (rr < Mrem) ? min(KE, a.m - kcol) : 0;
@@ -855,7 +920,10 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
       if constexpr (SF == SF_NM24) vf = nm_frag<DT>(rk, s);
       else vf = vfrag<DT, KE, W>(rk, s);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][s], xk[mt], vf);
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (kSwap) MM::run(acc[mt][s], vf, xk[mt]);
+        else MM::run(acc[mt][s], xk[mt], vf);
+      }
     }
   };
 
@@ -934,7 +1002,10 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
 #pragma unroll
           for (int s = 0; s < W; ++s)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) ML::run(acc[mt][s], tf[ls][mt], af[ls][s]);
+            for (int mt = 0; mt < MT; ++mt) {
+              if constexpr (kSwap) ML::run(acc[mt][s], af[ls][s], tf[ls][mt]);
+              else ML::run(acc[mt][s], tf[ls][mt], af[ls][s]);
+            }
       }
     }
   }
@@ -951,7 +1022,8 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
       // the row's finaliser: wait for the other nseq - 1 chunks
       if (lane == 0) wait_at_least<int>(counter, nseq - 1 + a.wait_bias, a.status, a.wait_polls);
     } else {
-      store_partial<MT, W>(acc, part_base + (int64_t)seq * TSZ, Mrem, lane);
+      if constexpr (kSwap) store_partial_lanes<MT, W>(acc, part_base + (int64_t)seq * TSZ, lane);
+      else store_partial<MT, W>(acc, part_base + (int64_t)seq * TSZ, Mrem, lane);
       wait_mem();
       int old = 0;
       if (lane == 0) old = rmw_add(counter, 1);
@@ -972,7 +1044,8 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
 #pragma unroll
           for (int s = 0; s < W; ++s) tot[mt][s] += acc[mt][s];
       } else {
-        add_partial<MT, W>(tot, part_base + (int64_t)k * TSZ, Mrem, lane);
+        if constexpr (kSwap) add_partial_lanes<MT, W>(tot, part_base + (int64_t)k * TSZ, lane);
+        else add_partial<MT, W>(tot, part_base + (int64_t)k * TSZ, Mrem, lane);
       }
     }
 #pragma unroll
@@ -991,12 +1064,58 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   float bv[W];
 #pragma unroll
   for (int s = 0; s < W; ++s) bv[s] = 0.f;
-  if constexpr (MODE == MODE_FUSED) {
+  if constexpr (MODE == MODE_FUSED && !kSwap) {
     if (a.bias != nullptr) ld_w<DT, W>(a.bias, j0, bv);
   }
   // a chained member another stage reads stores device-coherently
   const bool dev_out = CH > 0 && a.done != nullptr;
   const auto yr = dev_rsrc(a.y);
+  if constexpr (kSwap) {
+    // transposed tile: lane (c, g) holds 4W adjacent features of token row
+    // 16·mt + c (see kSwap). Its row segment goes out as 16-byte stores, and
+    // a member another stage reads also writes it to the fragment-order copy
+    // (every token row of the tile, those past M included: finite, computed
+    // from copies of the last row), so the reader loads whole units.
+    constexpr int NF = 4 * W;  // features per lane
+    const int f0 = row * P + NF * g;
+    float bw[NF];
+#pragma unroll
+    for (int i = 0; i < NF; ++i) bw[i] = 0.f;
+    if (a.bias != nullptr) ld_w<DT, NF>(a.bias, f0, bw);
+    const bool frag_out = dev_out && a.yf != nullptr;
+    const auto fr = dev_rsrc(a.yf);
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int rr = mt * 16 + c;
+      uint32_t w[NF / 2];
+#pragma unroll
+      for (int i = 0; i < NF / 2; ++i) {
+        // features 2i and 2i + 1 of the lane: (s, e) = ((2i) % W, (2i) / W), ...
+        const int f_lo = 2 * i, f_hi = 2 * i + 1;
+        const float lo = acc[mt][f_lo % W][f_lo / W] + bw[f_lo];
+        const float hi = acc[mt][f_hi % W][f_hi / W] + bw[f_hi];
+        w[i] = to_bits<DT>(lo) | (to_bits<DT>(hi) << 16);
+      }
+#pragma unroll
+      for (int q = 0; q < NF / 8; ++q) {
+        const u32x4v v = {w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]};
+        if (rr < Mrem) {
+          const int64_t off = ((int64_t)(m0 + rr) * a.ldy + f0 + 8 * q) * EB;
+          if (dev_out) __builtin_amdgcn_raw_buffer_store_b128(v, yr, (int)off, 0, kSc1);
+          else *reinterpret_cast<u32x4v*>((char*)a.y + off) = v;
+        }
+        if (frag_out) {
+          // unit (row·P + NF·g + 8q) / 32 of the output, 8-column group
+          // ((NF·g + 8q) % 32) / 8 of it
+          const int col = NF * g + 8 * q;
+          const int unit = row * (P / 32) + col / 32, gg = (col % 32) / 8;
+          __builtin_amdgcn_raw_buffer_store_b128(
+              v, fr, (((mg * MT + mt) * a.yf_units + unit) << 10) + (16 * gg + c) * 16, 0, kSc1);
+        }
+      }
+    }
+  } else {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -1017,6 +1136,7 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
         else st_w<DT, W>(a.y, off, o);
       }
     }
+  }
   if constexpr (CH > 0) {
     // count this row tile as finished once its stores are acknowledged
     if (dev_out) {
@@ -1098,6 +1218,7 @@ struct ChainDesc {
   // the launch it describes (read by the host when launching from a table)
   int64_t grid;                 // workgroups
   int M, block_p, dtype, sf;    // token rows, kernel block width, SSL dtype, SF_*
+  int fr;                       // later stages read fragment-order copies (FR kernels)
   int n_seg;                    // grid segments, in grid order
   int seg_start[2 * NMAX + 1];  // first workgroup of each segment, then the grid size
   int seg_member[2 * NMAX];     // the member a segment belongs to
@@ -1108,7 +1229,7 @@ using ChainArgs = ChainDesc<kMaxChain>;
 using ChainTab = ChainDesc<kMaxChainTab>;
 static_assert(sizeof(ChainArgs) <= 4096, "kernel arguments of a chained launch");
 
-template <int DT, int P, int KE, int MT, int UNR, int SF, int NMAX, int NR>
+template <int DT, int P, int KE, int MT, int UNR, int SF, bool FR, int NMAX, int NR>
 __device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4 (&red)[NR]) {
   const int b = blockIdx.x;
   // the last segment starting at or before b (empty segments share a start)
@@ -1143,7 +1264,7 @@ __device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4 (&red)[
   const int lb = b - start;
   if (!rows) {
     if (a.dep) {
-      latent_wg<DT, MT, 2>(a, lb, red);
+      latent_wg<DT, MT, 2, FR && DT != DT_F32 && (P == 32 || P == 64)>(a, lb, red);
       const int per_mg = a.n_rt * a.n_kc;
       if (threadIdx.x < kWave) dep_close(a, lb / per_mg, a.dep_lat_base + lb % per_mg);
     } else {
@@ -1153,20 +1274,20 @@ __device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4 (&red)[
   }
   const int mg = lb / a.n_chunks, chunk = lb % a.n_chunks;
   if (a.dep) {
-    stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 2>(a, chunk, mg, red);
+    stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 2, FR>(a, chunk, mg, red);
     if (threadIdx.x < kWave) dep_close(a, mg, a.dep_row_base + chunk);
   } else {
-    stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 1>(a, chunk, mg, red);
+    stream_wg<DT, P, KE, MT, MODE_FUSED, UNR, SF, 1, FR>(a, chunk, mg, red);
   }
 }
 
-template <int DT, int P, int KE, int MT, int UNR, int SF>
+template <int DT, int P, int KE, int MT, int UNR, int SF, bool FR>
 __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_chain_kernel(
     ChainArgs c_by_value) {
   (void)c_by_value;
   constexpr int W = P / 16;
   __shared__ f32x4 red[red_len<MT, W>()];
-  chain_wg<DT, P, KE, MT, UNR, SF, kMaxChain>(
+  chain_wg<DT, P, KE, MT, UNR, SF, FR, kMaxChain>(
       *(const ChainArgs*)__builtin_amdgcn_kernarg_segment_ptr(), red);
 }
 
@@ -1174,12 +1295,12 @@ __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_ch
 // layer of a model in one launch). Read through the constant address space,
 // as kernel arguments are: scalar loads of uniform words.
 typedef const __attribute__((address_space(4))) ChainTab* ChainTabPtr;
-template <int DT, int P, int KE, int MT, int UNR, int SF>
+template <int DT, int P, int KE, int MT, int UNR, int SF, bool FR>
 __global__ __launch_bounds__(kST, (DT != DT_F32 && P <= 32) ? 4 : 2) void slr_chain_tab_kernel(
     ChainTabPtr tab) {
   constexpr int W = P / 16;
   __shared__ f32x4 red[red_len<MT, W>()];
-  chain_wg<DT, P, KE, MT, UNR, SF, kMaxChainTab>(*(const ChainTab*)tab, red);
+  chain_wg<DT, P, KE, MT, UNR, SF, FR, kMaxChainTab>(*(const ChainTab*)tab, red);
 }
 
 // Slabs per wave per batch. The byte budget of the square-block kernels
@@ -1216,32 +1337,39 @@ hipError_t stream_launch_one(const GroupArgs& a, int64_t blocks, hipStream_t s) 
 // Square blocks of 16, 32 or 64 (KE 4, 8, 8) or 2:4 blocks; MT ∈ {1, 2, 4}.
 // `a` is the descriptor in kernel arguments, or else `tab` one in device memory.
 template <int DT>
-hipError_t chain_launch(int sf, int P, int MT, const ChainArgs* a, const ChainTab* tab,
+hipError_t chain_launch(int sf, int P, int MT, bool fr, const ChainArgs* a, const ChainTab* tab,
                         int64_t blocks, hipStream_t s);
 
-template <int DT, int P, int KE, int MT, int SF>
+template <int DT, int P, int KE, int MT, int SF, bool FR>
 hipError_t chain_launch_one(const ChainArgs* a, const ChainTab* tab, int64_t blocks,
                             hipStream_t s) {
   constexpr int UNR = stream_unroll<DT, P, KE, MT>();
   if (a)
-    hipLaunchKernelGGL((slr_chain_kernel<DT, P, KE, MT, UNR, SF>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((slr_chain_kernel<DT, P, KE, MT, UNR, SF, FR>), dim3((unsigned)blocks),
                        dim3(kST), 0, s, *a);
   else
-    hipLaunchKernelGGL((slr_chain_tab_kernel<DT, P, KE, MT, UNR, SF>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((slr_chain_tab_kernel<DT, P, KE, MT, UNR, SF, FR>), dim3((unsigned)blocks),
                        dim3(kST), 0, s, (ChainTabPtr)tab);
   return hipGetLastError();
 }
 
+// fr: the stages after the first read their input from its fragment-order
+// copy (32- and 64-wide blocks). One-tile calls have both kernels; taller
+// ones (MT > 1) always read fragments, and 16-wide blocks never do.
 template <int DT>
-hipError_t chain_dispatch(int sf, int P, int MT, const ChainArgs* a, const ChainTab* tab,
+hipError_t chain_dispatch(int sf, int P, int MT, bool fr, const ChainArgs* a, const ChainTab* tab,
                           int64_t blocks, hipStream_t s) {
   static_assert(DT != DT_F32, "chained launches take 16-bit activations");
-#define SSL_CMT(PP, KK, SS)                                                 \
-  switch (MT) {                                                             \
-    case 1: return chain_launch_one<DT, PP, KK, 1, SS>(a, tab, blocks, s);  \
-    case 2: return chain_launch_one<DT, PP, KK, 2, SS>(a, tab, blocks, s);  \
-    case 4: return chain_launch_one<DT, PP, KK, 4, SS>(a, tab, blocks, s);  \
-  }                                                                         \
+#define SSL_CMT(PP, KK, SS)                                                               \
+  switch (MT) {                                                                           \
+    case 1:                                                                               \
+      return fr ? chain_launch_one<DT, PP, KK, 1, SS, true>(a, tab, blocks, s)            \
+                : chain_launch_one<DT, PP, KK, 1, SS, false>(a, tab, blocks, s);          \
+    case 2: if (fr) return chain_launch_one<DT, PP, KK, 2, SS, true>(a, tab, blocks, s); \
+      break;                                                                              \
+    case 4: if (fr) return chain_launch_one<DT, PP, KK, 4, SS, true>(a, tab, blocks, s); \
+      break;                                                                              \
+  }                                                                                       \
   return hipErrorInvalidValue;
   if (sf == SF_NM24) {
     if (P != kNmBlock) return hipErrorInvalidValue;
@@ -1249,7 +1377,14 @@ hipError_t chain_dispatch(int sf, int P, int MT, const ChainArgs* a, const Chain
   }
   if (sf != SF_BSR) return hipErrorInvalidValue;
   switch (P) {
-    case 16: { SSL_CMT(16, 4, SF_BSR) }
+    case 16:
+      if (fr) return hipErrorInvalidValue;
+      switch (MT) {
+        case 1: return chain_launch_one<DT, 16, 4, 1, SF_BSR, false>(a, tab, blocks, s);
+        case 2: return chain_launch_one<DT, 16, 4, 2, SF_BSR, false>(a, tab, blocks, s);
+        case 4: return chain_launch_one<DT, 16, 4, 4, SF_BSR, false>(a, tab, blocks, s);
+      }
+      return hipErrorInvalidValue;
     case 32: { SSL_CMT(32, 8, SF_BSR) }
     case 64: { SSL_CMT(64, 8, SF_BSR) }
   }

@@ -33,6 +33,7 @@ DEBUG_PREFILL_TILE = 0
 DEBUG_WAIT_POLLS = 1
 DEBUG_WAIT_UNREACHABLE = 2
 DEBUG_PREFILL_SPLIT = 3
+DEBUG_CHAIN_FRAG = 4
 
 _DTYPE_CODE = {torch.float32: SSL_F32, torch.bfloat16: SSL_BF16, torch.float16: SSL_F16}
 
@@ -175,10 +176,12 @@ class SlrStage(ctypes.Structure):
     _fields_ = [
         ("x", _c_p), ("ldx", _c_i64), ("m", _c_i64), ("m_pad", _c_i64), ("first", _c_i32),
         ("count", _c_i32), ("src", _c_i32), ("sync", _c_p), ("n_sync", _c_i64),
+        ("xf", _c_p), ("xf_bytes", _c_i64),
     ]
 
 
 _SIGNATURES["ssl_slr_chain_sync_count"] = (_c_i64, [_c_i64])
+_SIGNATURES["ssl_slr_chain_frag_bytes"] = (_c_i64, [_c_i64, _c_i64])
 _SIGNATURES["ssl_slr_chain_table_bytes"] = (_c_i64, [])
 _SIGNATURES["ssl_slr_chain_table_build"] = (
     ctypes.c_int,

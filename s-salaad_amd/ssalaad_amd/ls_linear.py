@@ -759,6 +759,7 @@ class LRSLinearChain(nn.Module):
                                  stages=[len(sts) for sts in states])
         sync = (sync + 255) // 256 * 256
         stages = (_lib.SlrStage * len(states))()
+        frags: list[torch.Tensor] = []
         base = [0]
         for sts in states:
             base.append(base[-1] + len(sts))
@@ -772,7 +773,15 @@ class LRSLinearChain(nn.Module):
                 si, mi = self._src[s - 1]
                 sg.src = base[si] + mi
                 sg.sync, sg.n_sync = sync + 4 * n_sync * (s - 1), n_sync
-        return members, stages, base
+                # room for the source's output in MFMA-fragment order (the
+                # stage then reads whole 1 KiB units)
+                src = states[si][mi]
+                nbytes = int(lib.ssl_slr_chain_frag_bytes(M, src.NB * src.p))
+                if nbytes > 0:
+                    buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=x2.device)
+                    frags.append(buf)
+                    sg.xf, sg.xf_bytes = (buf.data_ptr() + 255) // 256 * 256, nbytes
+        return members, stages, base, frags
 
     def prepare(self, x: torch.Tensor) -> "PreparedChain":
         """The chain over the fixed input buffer `x`: its descriptor table is
@@ -812,7 +821,7 @@ class LRSLinearChain(nn.Module):
             return tuple(tuple(o) for o in outs)
         flat = [st for sts in states for st in sts]
         ys = [torch.empty(M, st.n_pad, dtype=x.dtype, device=x.device) for st in flat]
-        members, stages, base = self._descriptors(states, x2, ys, M)
+        members, stages, base, frags = self._descriptors(states, x2, ys, M)
         lib = _lib.load()
         st0 = states[0][0]
         if len(states) <= _lib.MAX_CHAIN_STAGES and len(flat) <= _lib.MAX_CHAIN:
@@ -883,7 +892,7 @@ class PreparedChain:
         self._chain = chain
         flat = [st for sts in states for st in sts]
         self._ys = [torch.empty(M, st.n_pad, dtype=x.dtype, device=x.device) for st in flat]
-        members, stages, base = chain._descriptors(states, x, self._ys, M)
+        members, stages, base, self._frags = chain._descriptors(states, x, self._ys, M)
         self._host = _ChainTable(x.device)
         self._host.build(M, states[0][0], stages, len(states), members, len(flat))
         self._dev = self._host.array.to(x.device)

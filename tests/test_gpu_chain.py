@@ -217,6 +217,39 @@ def knobs():
     yield set_
     set_(_lib.DEBUG_WAIT_POLLS, 0)
     set_(_lib.DEBUG_WAIT_UNREACHABLE, 0)
+    set_(_lib.DEBUG_CHAIN_FRAG, 0)
+
+
+@pytest.mark.parametrize("p", [32, 64, "nm24"])
+@pytest.mark.parametrize("M", [3, 16])
+def test_chain_fragment_order_inputs_equal_row_order(p, M, knobs, gpu_device):
+    """A later stage of 32- or 64-wide blocks reads its input either by row
+    segments or from the copy in MFMA-fragment order its source writes (the
+    library picks by token rows; forced both ways here, at a size where it
+    picks each): the same bits either way, and the oracle's values."""
+    dtype = torch.bfloat16
+    if p == "nm24":
+        h, f = 256, 704
+        shapes = [(h, h), (h, h), (h, h), (h, h), (f, h), (f, h), (h, f)]
+        mods = {nm: _nm24_module(n, m, 64, dtype, gpu_device, seed=300 + i)
+                for i, (nm, (n, m)) in enumerate(zip(NAMES, shapes))}
+        probs = None
+        x = to_dev(np.random.default_rng(M).standard_normal((M, h)), dtype, gpu_device)
+    else:
+        probs, mods = _layer(256, 688, 64, p, dtype, gpu_device, seed=7 * p + M, pad=True)
+        x = to_dev(make_x(probs["q"], M), dtype, gpu_device)
+    chain = _chain(mods)
+    outs = {}
+    for mode in (1, 2, 0):  # rows, fragments, the library's choice
+        knobs(_lib.DEBUG_CHAIN_FRAG, mode)
+        outs[mode] = _check_chain(chain, mods, probs, x, dtype)
+    for nm, a, b, c in zip(NAMES, outs[1], outs[2], outs[0]):
+        assert torch.equal(a, b) and torch.equal(a, c), nm
+    if probs is None:
+        for nm, xin, y in zip(NAMES, _inputs(x, outs[0]), outs[0]):
+            assert err(y, mods[nm](xin).double().cpu().numpy()) <= TOL[dtype], nm
+    assert latent_wait_status(gpu_device) == 0
+    assert _words_at_rest(gpu_device)
 
 
 @pytest.mark.parametrize("M", [1, 40])
