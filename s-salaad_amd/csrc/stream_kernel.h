@@ -603,7 +603,11 @@ __device__ __forceinline__ void wait_fin(const SlrArgs& a, int mg, u64 launch) {
 // is an input of the launch; 2 = a chained member whose x another stage of the
 // launch writes: its B loads go out before it waits for x, and x is read
 // device-coherently.
-template <int DT, int MT, int CH = 0, bool FX = false, int NR>
+// TF: t written in fragment order (units of 32 ranks, 1 KiB per 16 token rows,
+// lane 16g + c's 16 bytes = token row c, ranks 8g .. 8g + 7 of the unit), the
+// tile computed transposed so that each lane holds 4 adjacent ranks of one
+// token row; the rows of an FR chained launch read t that way.
+template <int DT, int MT, int CH = 0, bool FX = false, bool TF = false, int NR>
 __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)[NR]) {
   constexpr int KE = (DT == DT_F32) ? 4 : 8;
   using MM = Mma<DT, KE>;
@@ -677,7 +681,10 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)
     for (int k = 0; k < UNR; ++k) {
       if (u0 + k * kSW < ue) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][0], xf[k][mt], bf[k]);
+        for (int mt = 0; mt < MT; ++mt) {
+          if constexpr (TF) MM::run(acc[mt][0], bf[k], xf[k][mt]);
+          else MM::run(acc[mt][0], xf[k][mt], bf[k]);
+        }
       }
     }
     u0 += kSW * UNR;
@@ -697,7 +704,10 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)
     for (int k = 0; k < UNR; ++k) {
       if (u0 + k * kSW < ue) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) MM::run(acc[mt][0], xf[k][mt], bf[k]);
+        for (int mt = 0; mt < MT; ++mt) {
+          if constexpr (TF) MM::run(acc[mt][0], bf[k], xf[k][mt]);
+          else MM::run(acc[mt][0], xf[k][mt], bf[k]);
+        }
       }
     }
   }
@@ -745,6 +755,24 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)
   // Final latent tile, rounded once to the activation dtype as F.linear's
   // output is. Rows past M hold zeros (their x rows were read as zero).
   const auto tr = dev_rsrc(a.t);
+  if constexpr (TF) {
+    static_assert(DT != DT_F32, "fragment-order t: 16-bit");
+    // lane (c, g): ranks rt·16 + 4g .. + 3 of token row 16·mt + c: 8 bytes of
+    // unit rt / 2, 8-rank group 2·(rt % 2) + g / 2, half g % 2
+    const int units = (int)(a.ldt >> 5);
+    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const u32x2v w = {to_bits<DT>(acc[mt][0][0]) | (to_bits<DT>(acc[mt][0][1]) << 16),
+                        to_bits<DT>(acc[mt][0][2]) | (to_bits<DT>(acc[mt][0][3]) << 16)};
+      const int off = (((mg * MT + mt) * units + (rt >> 1)) << 10) +
+                      (16 * (2 * (rt & 1) + (g >> 1)) + c) * 16 + (g & 1) * 8;
+      __builtin_amdgcn_raw_buffer_store_b64(w, tr, off, 0, kSc1);
+    }
+    wait_mem();
+    if (lane == 0) rmw_add64(fin_copy(a, mg, rt % kFinCopies), 1);
+    return;
+  }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -858,6 +886,9 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   // fragment-order copy (for W = 4, two of them). (At one token row, where
   // FR kernels are not used, the transposed tile measured 4% slower.)
   constexpr bool kSwap = FR && CH > 0 && MODE == MODE_FUSED && DT != DT_F32 && (P == 32 || P == 64);
+  // the latent of FR launches writes t in fragment order (latent_wg's TF)
+  constexpr bool kTFrag = kSwap;
+  static_assert(!kTFrag || NLS == 1, "fragment-order t: one fragment per 32-rank unit");
   // the batch's column indices first, as scalar loads issued together
   auto index = [&](int v0, int(&colk)[UNR], int64_t(&voff)[UNR]) {
 #pragma unroll
@@ -987,9 +1018,14 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
         for (int ls = 0; ls < NLS; ++ls) {
           const int kr = u * 32 + ls * ML::KM + KEL * g;
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            tf[ls][mt] = ld_dev_frag<DT, KEL>(
-                tr, (int)(((int64_t)(m0 + mt * 16 + c) * a.ldt + kr) * EB));
+          for (int mt = 0; mt < MT; ++mt) {
+            if constexpr (kTFrag)
+              tf[ls][mt] = ld_dev_frag<DT, KEL>(
+                  tr, (((mg * MT + mt) * (int)(a.ldt >> 5) + u) << 10) + lane * 16);
+            else
+              tf[ls][mt] = ld_dev_frag<DT, KEL>(
+                  tr, (int)(((int64_t)(m0 + mt * 16 + c) * a.ldt + kr) * EB));
+          }
 #pragma unroll
           for (int s = 0; s < W; ++s)
             af[ls][s] = (u == lb + wid)
@@ -1231,6 +1267,7 @@ static_assert(sizeof(ChainArgs) <= 4096, "kernel arguments of a chained launch")
 
 template <int DT, int P, int KE, int MT, int UNR, int SF, bool FR, int NMAX, int NR>
 __device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4 (&red)[NR]) {
+  constexpr bool kFrag = FR && DT != DT_F32 && (P == 32 || P == 64);
   const int b = blockIdx.x;
   // the last segment starting at or before b (empty segments share a start)
   int member, rows, start;
@@ -1264,11 +1301,11 @@ __device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4 (&red)[
   const int lb = b - start;
   if (!rows) {
     if (a.dep) {
-      latent_wg<DT, MT, 2, FR && DT != DT_F32 && (P == 32 || P == 64)>(a, lb, red);
+      latent_wg<DT, MT, 2, kFrag, kFrag>(a, lb, red);
       const int per_mg = a.n_rt * a.n_kc;
       if (threadIdx.x < kWave) dep_close(a, lb / per_mg, a.dep_lat_base + lb % per_mg);
     } else {
-      latent_wg<DT, MT, 1>(a, lb, red);
+      latent_wg<DT, MT, 1, false, kFrag>(a, lb, red);
     }
     return;
   }
