@@ -603,11 +603,13 @@ __device__ __forceinline__ void wait_fin(const SlrArgs& a, int mg, u64 launch) {
 // is an input of the launch; 2 = a chained member whose x another stage of the
 // launch writes: its B loads go out before it waits for x, and x is read
 // device-coherently.
-// TF: t written in fragment order (units of 32 ranks, 1 KiB per 16 token rows,
-// lane 16g + c's 16 bytes = token row c, ranks 8g .. 8g + 7 of the unit), the
-// tile computed transposed so that each lane holds 4 adjacent ranks of one
-// token row; the rows of an FR chained launch read t that way.
-template <int DT, int MT, int CH = 0, bool FX = false, bool TF = false, int NR>
+// TF (16-bit activations): t written in fragment order (units of 32 ranks,
+// 1 KiB per 16 token rows, lane 16g + c's 16 bytes = token row c, ranks
+// 8g .. 8g + 7 of the unit), the tile computed transposed so that each lane
+// holds 4 adjacent ranks of one token row and stores them at once; the row
+// workgroups then read each 32-rank unit of t with one contiguous load. (The
+// row order took 4 two-byte stores per lane and 16 row segments per load.)
+template <int DT, int MT, int CH = 0, bool FX = false, bool TF = (DT != DT_F32), int NR>
 __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)[NR]) {
   constexpr int KE = (DT == DT_F32) ? 4 : 8;
   using MM = Mma<DT, KE>;
@@ -886,8 +888,8 @@ __device__ __forceinline__ void stream_wg(const SlrArgs& a, int chunk, int mg, f
   // fragment-order copy (for W = 4, two of them). (At one token row, where
   // FR kernels are not used, the transposed tile measured 4% slower.)
   constexpr bool kSwap = FR && CH > 0 && MODE == MODE_FUSED && DT != DT_F32 && (P == 32 || P == 64);
-  // the latent of FR launches writes t in fragment order (latent_wg's TF)
-  constexpr bool kTFrag = kSwap;
+  // t in fragment order (latent_wg's TF) for 16-bit activations
+  constexpr bool kTFrag = MODE == MODE_FUSED && DT != DT_F32;
   static_assert(!kTFrag || NLS == 1, "fragment-order t: one fragment per 32-rank unit");
   // the batch's column indices first, as scalar loads issued together
   auto index = [&](int v0, int(&colk)[UNR], int64_t(&voff)[UNR]) {
@@ -1301,11 +1303,11 @@ __device__ __forceinline__ void chain_wg(const ChainDesc<NMAX>& g, f32x4 (&red)[
   const int lb = b - start;
   if (!rows) {
     if (a.dep) {
-      latent_wg<DT, MT, 2, kFrag, kFrag>(a, lb, red);
+      latent_wg<DT, MT, 2, kFrag>(a, lb, red);
       const int per_mg = a.n_rt * a.n_kc;
       if (threadIdx.x < kWave) dep_close(a, lb / per_mg, a.dep_lat_base + lb % per_mg);
     } else {
-      latent_wg<DT, MT, 1, false, kFrag>(a, lb, red);
+      latent_wg<DT, MT, 1>(a, lb, red);
     }
     return;
   }
