@@ -99,10 +99,11 @@ for _p in (ROOT, ROOT / "s-salaad_amd"):
 HBM_PEAK_GBS = 8000.0
 # the dominant kernel of the default workload's launches, by launch mode
 KERNEL_NAMES = {
-    "stack": "slr_chain_tab_kernel<1, 32, 8, 1, 4, 0> (bf16, p 32, KE 8, MT 1, UNR 4, BSR): one "
-             "launch per step, 96 stages (24 layers × q,k,v | o | gate,up | down)",
-    "chain": "slr_chain_kernel<1, 32, 8, 1, 4, 0> (bf16, p 32, KE 8, MT 1, UNR 4, BSR): one "
-             "launch per layer, stages q,k,v | o | gate,up | down",
+    "stack": "slr_chain_tab_kernel<1, 32, 8, 1, 4, 0, true> (bf16, p 32, KE 8, MT 1, UNR 4, BSR, "
+             "fragment-order stage inputs): one launch per step, 96 stages (24 layers × "
+             "q,k,v | o | gate,up | down)",
+    "chain": "slr_chain_kernel<1, 32, 8, 1, 4, 0, true> (bf16, p 32, KE 8, MT 1, UNR 4, BSR, "
+             "fragment-order stage inputs): one launch per layer, stages q,k,v | o | gate,up | down",
     "groups": "slr_kernel<1, 32, 8, 1, 1, 4, 0> (bf16, p 32, KE 8, MT 1, fused, UNR 4, BSR)",
     "linears": "slr_kernel<1, 32, 8, 1, 1, 4, 0> (bf16, p 32, KE 8, MT 1, fused, UNR 4, BSR)",
 }
