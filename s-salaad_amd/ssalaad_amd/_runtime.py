@@ -59,6 +59,14 @@ def plan_target_cost(total_cost: int, block_p: int, elem_bytes: int, M: int) -> 
 # is the number of latent K chunks the balancing leaves room for.
 _BALANCE_MIN_ROW_BYTES = 128 * 1024
 _BALANCE_LATENT_MIN = 4
+# With 64-wide blocks (one workgroup per compute unit) the chunks may exceed
+# the slots the latent leaves free by an eighth of the compute units: the
+# latent's workgroups end well before the longest rows, and the chunks
+# dispatched into their slots still finish first. LLaMA-7B FFN decode
+# (11008×4096, 8 weight copies): 16.4 → 15.9 µs at 1 token row, 17.3-17.9 →
+# 17.0-17.1 at 16 (4096×11008: 19.95 → 19.5 / unchanged); a quarter of the
+# compute units: 19.4 / 22.3 µs, the late chunks become the stragglers.
+_BALANCE_EXTRA_P64 = 8  # extra chunks: compute units / this
 # Block sizes it applies to: at p = 32 (two workgroups per compute unit,
 # shorter rows) the split rows' exchange costs more than the straggler. At
 # p = 16 a row of small blocks streams slowly on one workgroup (a 4096-row

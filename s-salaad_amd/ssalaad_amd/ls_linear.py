@@ -147,7 +147,8 @@ class _KernelState:
                 # split the longest rows into the workgroup slots left free
                 n_cu = torch.cuda.get_device_properties(self.device).multi_processor_count
                 per_cu = 2 if (self.p <= 32 and self.elem == 2) else 1
-                bal = _runtime.balanced_target(costs, self.p * self.elem, n_cu * per_cu,
+                extra = n_cu // _runtime._BALANCE_EXTRA_P64 if self.p == 64 else 0
+                bal = _runtime.balanced_target(costs, self.p * self.elem, n_cu * per_cu + extra,
                                                self.r_pad // 16)
                 if bal:
                     target = min(target, bal) if target else bal
