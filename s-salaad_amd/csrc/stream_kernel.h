@@ -136,8 +136,6 @@ __device__ __forceinline__ void st_dev_vec(__amdgpu_buffer_rsrc_t r, int byte_of
 // All of this thread's earlier memory operations have completed (stores are
 // acknowledged by the device-coherent level).
 __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
-// the wave's LDS accesses completed (not its vector memory accesses)
-__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 typedef unsigned long long u64;
 constexpr int kLatentUnits = 840;  // divisible by every latent split 1..8
@@ -755,7 +753,8 @@ __device__ __forceinline__ void latent_wg(const SlrArgs& a, int wg, f32x4 (&red)
     for (int mt = 0; mt < MT; ++mt) acc[mt][0] = tot[mt];
   }
   // Final latent tile, rounded once to the activation dtype as F.linear's
-  // output is. Rows past M hold zeros (their x rows were read as zero).
+  // output is. Rows past M hold finite values no output uses (their x rows
+  // were read as copies of the last row, or as zeros past in_features).
   const auto tr = dev_rsrc(a.t);
   if constexpr (TF) {
     static_assert(DT != DT_F32, "fragment-order t: 16-bit");
