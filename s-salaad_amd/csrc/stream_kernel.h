@@ -485,12 +485,14 @@ struct SlrArgs {
 // +256 bytes the waiters w with w % kDepCopies == c that have passed; slot 0
 // also holds at +384 bytes the slots whose waiters have all passed. Same-address
 // atomics are served one after another (tens of ns each), so each finished row
-// tile makes ONE increment, spreading a source's NB increments over 16 words,
-// and a waiter reads all 16 counts with one 16-lane load. Measured on the 1B
-// layer: every row tile adding to 16 copies (each copy taking NB increments)
-// and each waiter taking a returning "passed" ticket before it went on cost
-// 1.1-2.8 µs per hand-over.
-constexpr int kDepCopies = 16;
+// tile makes ONE increment, spreading a source's NB increments over 64 words,
+// and a waiter reads all 64 counts with one load (a lane each). Measured on
+// the 1B layer: every row tile adding to 16 copies (each copy taking NB
+// increments) and each waiter taking a returning "passed" ticket before it went
+// on cost 1.1-2.8 µs per hand-over; one increment per tile over 16 / 32 / 64
+// words: 18.67 k / 19.06 k / 19.11 k tok/s (1282 / 1312 / 1318 at one token row).
+constexpr int kDepCopies = 64;
+static_assert(kDepCopies <= 64, "a waiter polls the copies with one lane each");
 constexpr int kDepSlotInts = 128;
 constexpr int kDepPassedInts = 64;
 constexpr int kDepClosedInts = 96;
@@ -503,7 +505,7 @@ __device__ __forceinline__ int dep_share(int n, int c) {
 }
 
 // Chained stages: wait until the source member has finished every row tile of
-// token tile mg in this launch. Wave 0 polls the 16 counts, the barrier
+// token tile mg in this launch. Wave 0 polls the kDepCopies counts, the barrier
 // releases the workgroup. The bookkeeping that returns the words to zero
 // (dep_close) runs when the workgroup ends, off the path to its output.
 __device__ __forceinline__ void wait_dep(const SlrArgs& a, int mg) {
