@@ -302,8 +302,8 @@ int ssl_slr_forward(void* y, int64_t ldy, const void* x, int64_t ldx, const void
  * under HIP graph capture, tight serving loops, hosts that forbid hipMalloc).
  * The counters, handshake words and workspace come from a file-scope device
  * array of ssl_slr_noalloc_scratch_bytes() (16 MiB) that each GPU the library
- * runs on holds until the process ends: at most 256 KiB of row counters, 256
- * KiB of handshake words and 15.5 MiB of workspace, as the *_counter_count,
+ * runs on holds until the process ends: at most 256 KiB of row counters, 512
+ * KiB of handshake words and 15.25 MiB of workspace, as the *_counter_count,
  * *_exchange_size and *_workspace_size queries compute them for the call;
  * beyond that the call returns SSL_ERR_CAPACITY before any launch. Each call
  * first clears the counters and handshake words it uses (a fill kernel on

@@ -24,7 +24,7 @@ namespace {
 
 constexpr int64_t kNoAllocScratchBytes = 16LL << 20;
 constexpr int64_t kNoAllocCounterBytes = 256LL << 10;   // 65,536 int32 row counters
-constexpr int64_t kNoAllocExchangeBytes = 256LL << 10;  // 32,768 uint64 handshake words
+constexpr int64_t kNoAllocExchangeBytes = 512LL << 10;  // 65,536 uint64 handshake words
 constexpr int64_t kNoAllocWorkspaceBytes =
     kNoAllocScratchBytes - kNoAllocCounterBytes - kNoAllocExchangeBytes;
 

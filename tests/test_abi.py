@@ -333,10 +333,10 @@ def test_workspace_sizes_are_aligned_and_monotone():
     # exchange: the plan's uint64 handshake words (status, then per token tile
     # the latent-ready and ticket words and one arrival word per 16-rank
     # tile), 256-byte aligned
-    # handshake words 8·(1 + MG·(2 + r/16)) rounded up to 256 bytes, then 8
+    # handshake words 8·(1 + MG·(2 + r/16)) rounded up to 256 bytes, then 16
     # copies of 512 bytes per token tile of the final-latent count
-    assert lib.ssl_slr_exchange_size(16, 256, 4096, _lib.SSL_BF16) == 256 + 4096
-    assert lib.ssl_slr_exchange_size(2048, 256, 4096, _lib.SSL_BF16) == 4864 + 32 * 4096
+    assert lib.ssl_slr_exchange_size(16, 256, 4096, _lib.SSL_BF16) == 256 + 8192
+    assert lib.ssl_slr_exchange_size(2048, 256, 4096, _lib.SSL_BF16) == 4864 + 32 * 8192
     assert lib.ssl_slr_exchange_size(16, 0, 4096, _lib.SSL_BF16) == 256
     assert lib.ssl_bsr_addmm_counter_count(16, 172) == 172
     assert lib.ssl_bsr_addmm_counter_count(65, 172) == 2 * 172

@@ -77,7 +77,7 @@ def test_no_alloc_entry_point_matches_the_scratch_entry_point(dtype, gpu_device,
 def test_no_alloc_entry_point_rejects_calls_beyond_its_scratch(gpu_device):
     lib = _lib.load()
     assert lib.ssl_slr_noalloc_scratch_bytes() == 16 << 20
-    # 64 token rows of a rank-65536 latent need far more than 15.5 MiB of
+    # 64 token rows of a rank-65536 latent need far more than 15.25 MiB of
     # workspace; the call is refused before any pointer is used or any launch
     R = 1 << 16
     assert lib.ssl_slr_workspace_size(64, 4, 32, R, 8192, 0, _lib.SSL_BF16) > (16 << 20)
