@@ -566,6 +566,31 @@ def test_balanced_target_splits_only_the_longest_rows():
         assert sum(int(e - b) for b, e in mine[:, 3:5]) == 8
 
 
+def test_chain_fragment_copy_sizes():
+    """Room for a chained stage's input in fragment order: 1 KiB per 16 token
+    rows (whole tiles of the call's tile height) and 32 features, rounded up."""
+    lib = _lib.load()
+    assert lib.ssl_slr_chain_frag_bytes(16, 2048) == 64 * 1024
+    assert lib.ssl_slr_chain_frag_bytes(1, 2048) == 64 * 1024  # one 16-row tile
+    assert lib.ssl_slr_chain_frag_bytes(16, 5472) == 171 * 1024
+    assert lib.ssl_slr_chain_frag_bytes(16, 5461) == 171 * 1024  # 32-feature units, rounded up
+    tiles = lib.ssl_slr_chain_frag_bytes(40, 256) // (8 * 1024)
+    assert tiles >= 3 and tiles * 8 * 1024 == lib.ssl_slr_chain_frag_bytes(40, 256)
+    assert lib.ssl_slr_chain_frag_bytes(0, 2048) == 0
+    assert lib.ssl_slr_chain_frag_bytes(16, 0) == 0
+
+
+def test_balanced_target_extra_chunks_for_64_wide_rows():
+    """With 64-wide blocks the decode balancing may use an eighth of the
+    compute units beyond the free slots: more rows split than without."""
+    rng = np.random.default_rng(1)
+    costs = rng.binomial(64, 0.5, size=172).astype(np.int64) * 64 + 8 * 32
+    base = _runtime.balanced_target(costs, 128, 256, 16)
+    wide = _runtime.balanced_target(costs, 128, 256 + 256 // _runtime._BALANCE_EXTRA_P64, 16)
+    assert 0 < wide < base
+    assert np.ceil(costs / wide).sum() <= 256 + 32 - _runtime._BALANCE_LATENT_MIN * 16
+
+
 def _parts(groups, group):
     return _runtime.build_prefill_parts(np.asarray(groups, np.int32), len(groups), group)
 
