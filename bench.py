@@ -1018,6 +1018,16 @@ def main():
             "avg_launch_us": round(gm["avg_launch_us"], 3),
             "hbm_frac": round(gm["achieved_gbs"] / HBM_PEAK_GBS, 4)}
         _log(f"[bench] decode M={M}: {gm['ms_step']:.3f} ms/step")
+    if not args.no_details and g["mode"] == "chain":
+        # the same step as ONE chained launch over all 24 layers (the layers
+        # chain directly here; a decoder runs attention and norms between them)
+        import copy
+        a1 = copy.copy(args)
+        a1.stack = True
+        gs = run_gpu(a1, layers, steps=max(5, args.steps // 2))
+        more["stack_M16"] = {"tok_s": round(gs["tok_s"], 1), "ms_per_step": round(gs["ms_step"], 4),
+                             "launches_per_step": gs["n_launches"]}
+        _log(f"[bench] one launch for the stack: {gs['ms_step']:.3f} ms/step")
     for M in (() if args.no_details else (1, 16)):
         more[f"eager_gate_M{M}"] = eager_calls(layers, M, max(5, args.steps // 2))
         _log(f"[bench] eager gate calls M={M}: {more[f'eager_gate_M{M}']}")
