@@ -449,7 +449,7 @@ typedef struct ssl_slr_stage {
   int32_t* sync;   /* later stages: ssl_slr_chain_sync_count(M) zeroed int32 words,
                     * 256-byte aligned */
   int64_t n_sync;
-  void* xf;        /* later stages of calls of 8 or more token rows with 32- or 64-wide
+  void* xf;        /* later stages of calls of 6 or more token rows with 32- or 64-wide
                     * blocks (ignored otherwise, may be NULL then): room for a second
                     * copy of src's output in MFMA-fragment order, which src writes and
                     * this stage reads (contiguous 1 KiB loads instead of 16 row

@@ -237,10 +237,10 @@ constexpr int kChainLatentUnits = 64;
 // Token rows from which a chained launch of 32- or 64-wide blocks passes the
 // stages' inputs in fragment order (each wave reads a unit as one contiguous
 // 1 KiB load). Below it the 16-row tiles are mostly padding, and the rows
-// read by row segments (fewer bytes) were faster: LLaMA-1B layer stack at 1 /
-// 4 / 16 token rows 1274 / 4713 / 17.2 k tok/s by rows, 1176 / 4685 / 18.4 k
-// in fragment order.
-constexpr int64_t kChainFragMinM = 8;
+// read by row segments (fewer bytes) were faster: LLaMA-1B layer stack at 2 /
+// 4 / 6 token rows 2608 / 4977 / 7362 tok/s by rows, 2499 / 4963 / 7412 in
+// fragment order (16 rows: 17.2 k by rows, 18.4 k in fragment order).
+constexpr int64_t kChainFragMinM = 6;
 
 // Whether a chained launch's later stages read fragment-order inputs.
 bool chain_frag(int64_t M, int32_t block_p) {
