@@ -601,12 +601,16 @@ def run_workload(args) -> dict:
     if args.workload == "block_topk":
         import ssalaad_amd
 
+        if args.block_set:
+            p = args.block
+            if n % p or m % p:
+                raise SystemExit(f"--block {p} does not divide {n}x{m}")
         Mt = torch.randn(n, m, generator=gen).to(dev)
         keep = (n // p) * (m // p) // 2
         us = _time_eager(lambda: ssalaad_amd.block_topk(Mt, keep, p, p), args.steps)
         b = n * m * 4 * 3 + (n // p) * (m // p) * 5  # read twice, write fp32 once; norms + flags
         gbs = b / us / 1e3
-        return dict(base, metric="block projection GB/s (project_S, 11008x4096 fp32)",
+        return dict(base, metric=f"block projection GB/s (project_S, 11008x4096 fp32, {p}x{p} blocks)",
                     value=round(gbs, 1), unit="GB/s", ms_per_step=round(us / 1e3, 5), dtype="f32",
                     config={"workload": "block_topk", "n": n, "m": m, "block": p,
                             "blocks_kept": keep, "parallelism": "single_gpu"},
@@ -977,7 +981,9 @@ def main():
                     help="the four stages of a layer as grouped launches instead of one chained launch")
     ap.add_argument("--no-group", action="store_true",
                     help="one launch per linear instead of grouping q/k/v and gate/up")
-    ap.add_argument("--block", type=int, default=16, help="skew_prefill: block size")
+    ap.add_argument("--block", type=int, default=None,
+                    help="skew_prefill: block size (default 16); block_topk: square block size "
+                         "(default 64)")
     ap.add_argument("--density", type=float, default=0.5, help="skew_prefill: mean block density")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (counter calibration)")
@@ -991,6 +997,9 @@ def main():
     args.batch_set = args.batch is not None
     if args.batch is None:
         args.batch = 16
+    args.block_set = args.block is not None
+    if args.block is None:
+        args.block = 16
     if args.copy_probe:
         copy_probe(args.copy_probe, max(1, args.steps))
         return

@@ -95,13 +95,16 @@ int ssl_status_word_alloc(void** host_ptr, void** device_ptr);
  *                               of 32- or 64-wide blocks passes its stages'
  *                               inputs in fragment order (ssl_slr_stage.xf);
  *                               1: never (one-tile calls); 2: always.
+ *   SSL_DEBUG_TOPK_GROUPS       0: ssl_block_topk picks its select; 1: one
+ *                               workgroup; 2: many workgroups.
  * Not for concurrent use with calls on other threads. */
 typedef enum {
   SSL_DEBUG_PREFILL_TILE = 0,
   SSL_DEBUG_WAIT_POLLS = 1,
   SSL_DEBUG_WAIT_UNREACHABLE = 2,
   SSL_DEBUG_PREFILL_SPLIT = 3,
-  SSL_DEBUG_CHAIN_FRAG = 4
+  SSL_DEBUG_CHAIN_FRAG = 4,
+  SSL_DEBUG_TOPK_GROUPS = 5
 } ssl_debug_knob;
 int ssl_debug_set(int32_t knob, int64_t value);
 
@@ -500,10 +503,15 @@ int ssl_slr_chain_table_launch(const void* table_host, const void* table_dev, vo
  * order: deterministic, where torch.topk leaves the order unspecified.
  * `norms` (NB·NBK fp32) and `keep` (NB·NBK bytes) are device arrays the call
  * fills; `out` ([NB·p, ldo] fp32) may be NULL to get the mask only.
+ * `workspace` (ssl_block_topk_workspace_size(NB·NBK) bytes, 16-byte aligned,
+ * no initial contents) holds the select's histograms and counts when many
+ * workgroups share it; calls that share a workspace must be ordered.
  * ------------------------------------------------------------------------- */
+int64_t ssl_block_topk_workspace_size(int64_t n_blocks);
 int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t block_p,
                    int32_t block_q, int32_t dtype, int64_t n_keep, float* norms, uint8_t* keep,
-                   float* out, int64_t ldo, void* stream);
+                   float* out, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                   void* stream);
 
 /* -------------------------------------------------------------------------
  * ssl_project_nm — N:M projection of a dense matrix.

@@ -31,6 +31,7 @@ struct DebugKnobs {
   int64_t wait_unreachable;  // nonzero: every wait's target is out of reach
   int64_t prefill_split;     // 0: the library's choice; 1: never; 2-4: that many parts
   int64_t chain_frag;        // 0: the library's choice; 1: never; 2: always (32/64-wide)
+  int64_t topk_groups;       // 0: the library's choice; 1: one workgroup; 2: many
 };
 DebugKnobs& debug_knobs();
 

@@ -28,12 +28,36 @@ __device__ __forceinline__ float elem_f32(const void* base, int64_t i) {
   else return f16_to_f32(((const uint16_t*)base)[i]);
 }
 
+// The many-workgroup select's workspace (32-bit words): per pass (one 8-bit
+// digit of the key each, most significant first) a 256-bin histogram and an
+// arrival count; per pass boundary the select's state {prefix, mask, need, eq}
+// (boundary 0: nothing chosen yet, need = n_keep; boundary 4: the threshold
+// key T, with need and eq the number of keys equal to T still to keep and
+// present); per workgroup its own last-pass histogram, whose bin of T counts
+// the keys equal to T in its range, for the ordered pass. The norms' launch
+// zeroes the shared part, so each call starts from zero whatever the last call
+// left.
+constexpr int kSelPasses = 4;
+constexpr int kWsHist = 0;  // [pass][256]
+constexpr int kWsTicket = kWsHist + 256 * kSelPasses;
+constexpr int kWsState = kWsTicket + 8;
+constexpr int kWsGroupHist = kWsState + 4 * (kSelPasses + 1) + 4;
+constexpr int kMaxSelGroups = 1024;
+static_assert(kWsGroupHist % 4 == 0, "per-group histograms start on a 16-byte boundary");
+
+__device__ __forceinline__ void sel_ws_init(uint32_t* ws, int n_keep) {
+  for (int i = threadIdx.x; i < kWsGroupHist; i += blockDim.x)
+    ws[i] = i == kWsState + 2 ? (uint32_t)n_keep : 0u;
+}
+
 // One wave per block: the fp32 sum of squares (lane-strided partial sums, then a
 // fixed butterfly, so repeated runs give identical bits).
 template <int DT>
 __global__ __launch_bounds__(kThreads) void block_sumsq_kernel(const void* S, int64_t lds, int NB,
                                                                int NBK, int p, int q, bool vec,
-                                                               float* norms) {
+                                                               float* norms, uint32_t* sel_ws,
+                                                               int n_keep) {
+  if (sel_ws && blockIdx.x == 0) sel_ws_init(sel_ws, n_keep);
   const int lane = threadIdx.x & 63;
   const int64_t blk = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (blk >= (int64_t)NB * NBK) return;
@@ -82,14 +106,114 @@ __global__ __launch_bounds__(kThreads) void block_sumsq_kernel(const void* S, in
   if (lane == 0) norms[blk] = acc;
 }
 
+// Small blocks (at most 64 pieces of 16 bytes, e.g. 16×16 fp32, 8×8): lanes-per-
+// block L, the next power of two of the piece count; a wave takes 64 / L blocks
+// a round and kSmallRounds rounds with every load in flight at once. Each lane
+// sums its piece in the order above and the L lanes of a block reduce with
+// the last log2(L) steps of the same butterfly (the wider steps above would
+// add lanes that hold +0), so the sums are bit-identical to the kernel above.
+constexpr int kSmallRounds = 4;
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void block_sumsq_small_kernel(
+    const void* S, int64_t lds, int64_t nblocks, int NBK, int p, int q, int L, float* norms,
+    uint32_t* sel_ws, int n_keep) {
+  if (sel_ws && blockIdx.x == 0) sel_ws_init(sel_ws, n_keep);
+  constexpr int EB = Elem<DT>::bytes, VE = 16 / EB;
+  const int lane = threadIdx.x & 63;
+  const int per_round = kWave / L, cpr = q / VE, pieces = p * cpr;
+  const int gi = lane / L, li = lane % L;
+  const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int64_t blk0 = wave * (kSmallRounds * per_round) + gi;
+  uint4 v4[kSmallRounds];
+#pragma unroll
+  for (int u = 0; u < kSmallRounds; ++u) {
+    const int64_t blk = blk0 + (int64_t)u * per_round;
+    v4[u] = make_uint4(0, 0, 0, 0);
+    if (li < pieces && blk < nblocks) {
+      const int by = (int)(blk / NBK), bc = (int)(blk % NBK);
+      const int i = li / cpr, j = (li % cpr) * VE;
+      const int64_t off = (int64_t)by * p * lds + (int64_t)bc * q + (int64_t)i * lds + j;
+      v4[u] = *(const uint4*)((const char*)S + off * EB);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kSmallRounds; ++u) {
+    float acc = 0.f;
+    const uint32_t w[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      if constexpr (DT == DT_F32) {
+        const float v = __uint_as_float(w[h]);
+        acc = fmaf(v, v, acc);
+      } else {
+        const float lo = DT == DT_BF16 ? bf16_to_f32(w[h] & 0xffffu) : f16_to_f32(w[h] & 0xffffu);
+        const float hi = DT == DT_BF16 ? bf16_to_f32(w[h] >> 16) : f16_to_f32(w[h] >> 16);
+        acc = fmaf(lo, lo, acc);
+        acc = fmaf(hi, hi, acc);
+      }
+    }
+    for (int off = L >> 1; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+    const int64_t blk = blk0 + (int64_t)u * per_round;
+    if (li == 0 && blk < nblocks) norms[blk] = acc;
+  }
+}
+
 __device__ __forceinline__ uint32_t norm_key(float v) {
   const uint32_t b = __float_as_uint(v);
   return (b & 0x7fffffffu) > 0x7f800000u ? kNanKey : b;
 }
 
+// hist[d] += 1 for each lane with `in`. Norms of one matrix mostly share their
+// leading digits, so a wave's lanes usually land in one bin; then one lane adds
+// the wave's count instead of 64 lanes contending for one LDS word.
+__device__ __forceinline__ void hist_add(int* hist, bool in, uint32_t d) {
+  const unsigned long long act = __ballot(in);
+  if (act == 0ull) return;
+  const int first = __ffsll((long long)act) - 1;
+  const uint32_t d0 = (uint32_t)__shfl((int)d, first, kWave);
+  if (__ballot(in && d == d0) == act) {
+    if ((int)(threadIdx.x & 63) == first) atomicAdd(&hist[d0], __popcll(act));
+  } else if (in) {
+    atomicAdd(&hist[d], 1);
+  }
+}
+
+// The digit of the need-th largest key among those matching the prefix, from
+// a 256-bin histogram read by one wave (lane l: bins 4l .. 4l + 3). Returns the
+// lane's result in d, cum (keys above bin d) and cnt (keys in bin d); exactly
+// one lane's bins hold it (returns true).
+__device__ __forceinline__ bool find_digit(const int (&h)[4], int need0, int& d, int& cum,
+                                           int& cnt) {
+  const int lane = threadIdx.x & 63;
+  const int sum4 = h[0] + h[1] + h[2] + h[3];
+  int incl = sum4;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int v = __shfl_down(incl, off, kWave);
+    if (lane + off < kWave) incl += v;
+  }
+  const int above = incl - sum4;
+  if (!(above < need0 && need0 <= incl)) return false;
+  cum = above;
+  d = 4 * lane;
+  cnt = h[0];
+#pragma unroll
+  for (int b = 3; b >= 0; --b) {
+    if (cum + h[b] >= need0) {
+      d = 4 * lane + b;
+      cnt = h[b];
+      break;
+    }
+    cum += h[b];
+  }
+  return true;
+}
+
 // Single workgroup: keep[b] = 1 for the n_keep largest keys (ties: lowest b first).
 // STAGED: the keys are copied into LDS once (n ≤ kLdsKeys) and every pass reads them there.
 constexpr int kLdsKeys = 15360;  // 60 KiB of keys: within 64 KiB of LDS with the rest
+constexpr int64_t kSelOneGroupMax = kLdsKeys;  // more keys: the many-workgroup select
 
 template <bool STAGED>
 __global__ __launch_bounds__(kSelThreads) void block_topk_kernel(const float* norms, int n,
@@ -117,41 +241,21 @@ __global__ __launch_bounds__(kSelThreads) void block_topk_kernel(const float* no
     for (int d = t; d < 256; d += kSelThreads) hist[d] = 0;
     __syncthreads();
     const uint32_t prefix = s_prefix, mask = s_mask;
-    for (int i = t; i < n; i += kSelThreads) {
-      const uint32_t k = key_at(i);
-      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1);
+    for (int i0 = 0; i0 < n; i0 += kSelThreads) {
+      const int i = i0 + t;
+      const uint32_t k = i < n ? key_at(i) : 0u;
+      hist_add(hist, i < n && (k & mask) == prefix, (k >> shift) & 255u);
     }
     __syncthreads();
     if (t < kWave) {
-      // The digit of the need-th largest key among those matching the prefix.
-      // Lane l holds bins 4l .. 4l + 3; a suffix sum over the lanes gives the
-      // count above each lane's bins, and exactly one lane's bins contain it.
+      int h[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) h[b] = hist[4 * t + b];
       const int need0 = s_need;
-      int h[4], sum4 = 0;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        h[b] = hist[4 * t + b];
-        sum4 += h[b];
-      }
-      int incl = sum4;  // Σ of lanes t .. 63
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const int v = __shfl_down(incl, off, kWave);
-        if (t + off < kWave) incl += v;
-      }
-      const int above = incl - sum4;
-      if (above < need0 && need0 <= incl) {
-        int cum = above, d = 4 * t;
-#pragma unroll
-        for (int b = 3; b >= 0; --b) {
-          if (cum + h[b] >= need0) {
-            d = 4 * t + b;
-            break;
-          }
-          cum += h[b];
-        }
+      int d, cum, cnt;
+      if (find_digit(h, need0, d, cum, cnt)) {
         s_need = need0 - cum;
-        s_eq = hist[d];  // keys matching the prefix so far (after the last digit: equal to T)
+        s_eq = cnt;  // keys matching the prefix so far (after the last digit: equal to T)
         s_prefix = prefix | ((uint32_t)d << shift);
         s_mask = mask | (255u << shift);
       }
@@ -188,6 +292,187 @@ __global__ __launch_bounds__(kSelThreads) void block_topk_kernel(const float* no
     taken += chunk_total;
     __syncthreads();
   }
+}
+
+// ---------------------------------------------------------------------------
+// Many-workgroup select, for more keys than one workgroup reads quickly. Four
+// 8-bit digit passes, each a launch over every key: group g
+// counts the digits of its range [g·chunk, (g+1)·chunk) that match the prefix
+// chosen so far into an LDS histogram, adds it to the pass's histogram in the
+// workspace, and the group that arrives last picks the pass's digit for the
+// next launch. The last pass also leaves each group's own histogram. Then the
+// marking launch keeps every key above T, and, when only some of the keys
+// equal to T are kept, each group ranks its keys equal to T in block order
+// from the count of them in the groups before it.
+// ---------------------------------------------------------------------------
+constexpr int kSelGroupThreads = 256;
+constexpr int kSelUnroll = 32;       // keys per thread per round, loaded together
+constexpr int kSelGroupKeys = kSelGroupThreads * kSelUnroll;  // keys per workgroup (one round),
+                                                              // up to kMaxSelGroups groups
+constexpr int kTiePer = 32;          // contiguous keys per thread in the ordered pass
+static_assert(kSelGroupThreads == 256, "one histogram bin per thread");
+
+__device__ __forceinline__ void group_range(int64_t n, int chunk, int64_t& i0, int64_t& i1) {
+  i0 = (int64_t)blockIdx.x * chunk;
+  i1 = i0 + chunk < n ? i0 + chunk : n;
+}
+
+// Block-wide exclusive prefix of v over the workgroup's 256 threads; total in tot.
+__device__ __forceinline__ int group_exclusive(int v, int& tot, int* s_wave) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int u = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += u;
+  }
+  if (lane == kWave - 1) s_wave[w] = incl;
+  __syncthreads();
+  int before = 0;
+  tot = 0;
+#pragma unroll
+  for (int x = 0; x < kSelGroupThreads / kWave; ++x) {
+    const int c = s_wave[x];
+    if (x < w) before += c;
+    tot += c;
+  }
+  __syncthreads();
+  return before + incl - v;
+}
+
+template <int PS>
+__global__ __launch_bounds__(kSelGroupThreads) void topk_hist_kernel(const float* norms, int n,
+                                                                     int chunk, uint32_t* ws) {
+  constexpr int SHIFT = 24 - 8 * PS;
+  __shared__ int hist[256];
+  __shared__ int s_wave[kSelGroupThreads / kWave];
+  __shared__ int s_last;
+  const int t = threadIdx.x;
+  int64_t i0, i1;
+  group_range(n, chunk, i0, i1);
+  // The first round's keys are requested before the histogram is cleared, so
+  // their round trip overlaps the state's and the barrier.
+  constexpr int64_t kStep = kSelGroupThreads * kSelUnroll;
+  uint32_t k[kSelUnroll];
+  auto load_round = [&](int64_t b) {
+#pragma unroll
+    for (int u = 0; u < kSelUnroll; ++u) {
+      const int64_t i = b + u * kSelGroupThreads + t;
+      k[u] = i < i1 ? norm_key(norms[i]) : 0u;
+    }
+  };
+  load_round(i0);
+  hist[t] = 0;
+  const uint32_t* st = ws + kWsState + 4 * PS;
+  const uint32_t prefix = st[0], mask = st[1];
+  __syncthreads();
+  for (int64_t b = i0; b < i1; b += kStep) {
+#pragma unroll
+    for (int u = 0; u < kSelUnroll; ++u) {
+      const int64_t i = b + u * kSelGroupThreads + t;
+      hist_add(hist, i < i1 && (k[u] & mask) == prefix, (k[u] >> SHIFT) & 255u);
+    }
+    if (b + kStep < i1) load_round(b + kStep);
+  }
+  __syncthreads();
+  int* gh = (int*)ws + kWsHist + 256 * PS;
+  const int mine = hist[t];
+  if (mine) __hip_atomic_fetch_add(gh + t, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // this group's keys per last digit, for the ranks of keys equal to T
+  if constexpr (PS == kSelPasses - 1) ws[kWsGroupHist + (int64_t)blockIdx.x * 256 + t] = mine;
+  // The adds are acknowledged before this group's arrival is counted, so the
+  // group that counts last reads every group's adds.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0)
+    s_last = __hip_atomic_fetch_add((int*)ws + kWsTicket + PS, 1, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (!s_last || t >= kWave) return;
+  int h[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    h[b] = __hip_atomic_load(gh + 4 * t + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int need0 = (int)st[2];
+  int d, cum, cnt;
+  if (find_digit(h, need0, d, cum, cnt)) {
+    uint32_t* nx = ws + kWsState + 4 * (PS + 1);
+    nx[0] = prefix | ((uint32_t)d << SHIFT);
+    nx[1] = mask | (255u << SHIFT);
+    nx[2] = (uint32_t)(need0 - cum);
+    nx[3] = (uint32_t)cnt;
+  }
+}
+
+// Ordered pass over [i0, i1): thread t takes kTiePer consecutive keys of each
+// slice of kSelGroupThreads·kTiePer; keys equal to T are ranked in block order
+// from `base`, and kept while their rank is below need.
+__device__ __forceinline__ void tie_pass(const float* norms, int64_t i0, int64_t i1, uint32_t T,
+                                         int need, int base, uint8_t* keep, int* s_wave) {
+  for (int64_t s0 = i0; s0 < i1; s0 += kSelGroupThreads * kTiePer) {
+    const int64_t a = s0 + (int64_t)threadIdx.x * kTiePer;
+    uint32_t k[kTiePer];
+    int c = 0;
+#pragma unroll
+    for (int u = 0; u < kTiePer; ++u) {
+      k[u] = a + u < i1 ? norm_key(norms[a + u]) : 0u;
+      c += (a + u < i1 && k[u] == T) ? 1 : 0;
+    }
+    int tot;
+    int r = base + group_exclusive(c, tot, s_wave);
+#pragma unroll
+    for (int u = 0; u < kTiePer; ++u) {
+      if (a + u < i1) {
+        const bool eq = k[u] == T;
+        keep[a + u] = (k[u] > T || (eq && r < need)) ? 1 : 0;
+        r += eq ? 1 : 0;
+      }
+    }
+    base += tot;
+  }
+}
+
+// keep[i] for the group's range: fill ≥ 0 writes that value (n_keep ≤ 0 or
+// ≥ n), else the select's result.
+__global__ __launch_bounds__(kSelGroupThreads) void topk_mark_kernel(const float* norms, int n,
+                                                                     int chunk, const uint32_t* ws,
+                                                                     int fill, uint8_t* keep) {
+  __shared__ int s_wave[kSelGroupThreads / kWave];
+  const int t = threadIdx.x;
+  int64_t i0, i1;
+  group_range(n, chunk, i0, i1);
+  if (fill >= 0) {
+    for (int64_t i = i0 + t; i < i1; i += kSelGroupThreads) keep[i] = (uint8_t)fill;
+    return;
+  }
+  const uint32_t* st = ws + kWsState + 4 * kSelPasses;
+  const uint32_t T = st[0];
+  const int need = (int)st[2];
+  if (st[2] == st[3]) {
+    // every key equal to T is kept: no ranks needed
+    for (int64_t b = i0; b < i1; b += kSelGroupThreads * kSelUnroll) {
+      uint32_t k[kSelUnroll];
+#pragma unroll
+      for (int u = 0; u < kSelUnroll; ++u) {
+        const int64_t i = b + u * kSelGroupThreads + t;
+        k[u] = i < i1 ? norm_key(norms[i]) : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < kSelUnroll; ++u) {
+        const int64_t i = b + u * kSelGroupThreads + t;
+        if (i < i1) keep[i] = k[u] >= T ? 1 : 0;
+      }
+    }
+    return;
+  }
+  // keys equal to T in the ranges of the groups before this one
+  const uint32_t d = T & 255u;
+  int before = 0;
+  for (int g = t; g < (int)blockIdx.x; g += kSelGroupThreads)
+    before += (int)ws[kWsGroupHist + (int64_t)g * 256 + d];
+  int tot;
+  group_exclusive(before, tot, s_wave);
+  tie_pass(norms, i0, i1, T, need, tot, keep, s_wave);
 }
 
 // out[i, j] = input as fp32 where block (i / p, j / q) is kept, else 0.
@@ -265,9 +550,22 @@ using namespace ssl;
 
 extern "C" {
 
+// Workgroups of the many-workgroup select: kSelGroupKeys keys each, at most
+// kMaxSelGroups (then more keys each).
+static int64_t select_groups(int64_t n_blocks) {
+  return std::min<int64_t>((n_blocks + kSelGroupKeys - 1) / kSelGroupKeys, kMaxSelGroups);
+}
+
+int64_t ssl_block_topk_workspace_size(int64_t n_blocks) {
+  if (n_blocks <= 0) return 0;
+  const int64_t words = kWsGroupHist + select_groups(n_blocks) * 256;
+  return (words * 4 + 255) / 256 * 256;
+}
+
 int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t block_p,
                    int32_t block_q, int32_t dtype, int64_t n_keep, float* norms, uint8_t* keep,
-                   float* out, int64_t ldo, void* stream) {
+                   float* out, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                   void* stream) {
   clear_error();
   if (block_p <= 0 || block_q <= 0 || NB < 0 || NBK < 0) return fail(SSL_ERR_INVALID, "bad sizes");
   if (dtype != SSL_F32 && dtype != SSL_BF16 && dtype != SSL_F16)
@@ -279,6 +577,9 @@ int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t 
   if (lds < NBK * block_q) return fail(SSL_ERR_INVALID, "lds smaller than the row");
   if (!S || !norms || !keep) return fail(SSL_ERR_INVALID, "null pointer");
   if (out && ldo < NBK * block_q) return fail(SSL_ERR_INVALID, "ldo smaller than the row");
+  if (!workspace || workspace_bytes < ssl_block_topk_workspace_size(nblocks) ||
+      (uintptr_t)workspace % 16 != 0)
+    return fail(SSL_ERR_WORKSPACE, "block projection workspace missing, small or not 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   const unsigned grid = (unsigned)((nblocks + kWaves - 1) / kWaves);
   const int n = (int)(NB * block_p), m = (int)(NBK * block_q);
@@ -289,15 +590,51 @@ int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t 
   // 16-byte pieces of the input: aligned base, row stride and block rows
   const bool vec_in = ((uintptr_t)S % 16 == 0) && (lds * eb) % 16 == 0 && (block_q * eb) % 16 == 0;
   const bool vec_out = out && ((uintptr_t)out % 16 == 0) && ldo % 4 == 0;
+  // The select: one workgroup over keys staged in its LDS, or many workgroups
+  // over kSelGroupKeys keys each (four histogram launches and the marking).
+  const int64_t knob = debug_knobs().topk_groups;
+  const bool many = knob == 2 || (knob == 0 && nblocks > kSelOneGroupMax);
+  const bool fill = keep_n <= 0 || keep_n >= nblocks;
+  const int groups = (int)select_groups(nblocks);
+  const int chunk = (int)((nblocks + groups - 1) / groups);
+  uint32_t* ws = (uint32_t*)workspace;
+  // blocks of at most 64 pieces of 16 bytes: several blocks per wave
+  const int64_t pieces = vec_in ? (int64_t)block_p * (block_q * eb / 16) : 0;
+  const bool small = vec_in && pieces <= kWave;
+  int lanes = 1;
+  while (small && lanes < pieces) lanes <<= 1;
+  const int64_t small_blocks = (int64_t)kSmallRounds * (kWave / lanes);  // per wave
+  const int64_t small_waves = small ? (nblocks + small_blocks - 1) / small_blocks : 0;
+  const unsigned small_grid = (unsigned)((small_waves + kWaves - 1) / kWaves);
+  uint32_t* init_ws = many && !fill ? ws : nullptr;
 #define SSL_PROJECT(DTC)                                                                       \
-  hipLaunchKernelGGL(block_sumsq_kernel<DTC>, dim3(grid), dim3(kThreads), 0, s, S, lds, (int)NB, \
-                     (int)NBK, block_p, block_q, vec_in, norms);                                \
-  if (nblocks <= kLdsKeys)                                                                       \
+  if (small)                                                                                    \
+    hipLaunchKernelGGL(block_sumsq_small_kernel<DTC>, dim3(small_grid), dim3(kThreads), 0, s, S, \
+                       lds, nblocks, (int)NBK, block_p, block_q, lanes, norms, init_ws, keep_n); \
+  else                                                                                          \
+    hipLaunchKernelGGL(block_sumsq_kernel<DTC>, dim3(grid), dim3(kThreads), 0, s, S, lds,        \
+                       (int)NB, (int)NBK, block_p, block_q, vec_in, norms, init_ws, keep_n);    \
+  if (!many && nblocks <= kLdsKeys)                                                              \
     hipLaunchKernelGGL(block_topk_kernel<true>, dim3(1), dim3(kSelThreads),                      \
                        (unsigned)(4 * nblocks), s, norms, (int)nblocks, keep_n, keep);           \
-  else                                                                                          \
+  else if (!many)                                                                               \
     hipLaunchKernelGGL(block_topk_kernel<false>, dim3(1), dim3(kSelThreads), 0, s, norms,        \
                        (int)nblocks, keep_n, keep);                                             \
+  else if (fill)                                                                                \
+    hipLaunchKernelGGL(topk_mark_kernel, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,      \
+                       (int)nblocks, chunk, ws, keep_n > 0 ? 1 : 0, keep);                      \
+  else {                                                                                        \
+    hipLaunchKernelGGL(topk_hist_kernel<0>, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,   \
+                       (int)nblocks, chunk, ws);                                                \
+    hipLaunchKernelGGL(topk_hist_kernel<1>, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,   \
+                       (int)nblocks, chunk, ws);                                                \
+    hipLaunchKernelGGL(topk_hist_kernel<2>, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,   \
+                       (int)nblocks, chunk, ws);                                                \
+    hipLaunchKernelGGL(topk_hist_kernel<3>, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,   \
+                       (int)nblocks, chunk, ws);                                                \
+    hipLaunchKernelGGL(topk_mark_kernel, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,      \
+                       (int)nblocks, chunk, ws, -1, keep);                                      \
+  }                                                                                             \
   if (out)                                                                                      \
     hipLaunchKernelGGL(block_mask_kernel<DTC>, mgrid, dim3(kThreads), 0, s, S, lds, n, m,        \
                        block_p, block_q, (int)NBK, keep, out, ldo, vec_out);

@@ -111,6 +111,10 @@ int ssl_debug_set(int32_t knob, int64_t value) {
       if (value < 0 || value > 2) return fail(SSL_ERR_INVALID, "chain fragment override must be 0 to 2");
       k.chain_frag = value;
       return SSL_OK;
+    case SSL_DEBUG_TOPK_GROUPS:
+      if (value < 0 || value > 2) return fail(SSL_ERR_INVALID, "select override must be 0 to 2");
+      k.topk_groups = value;
+      return SSL_OK;
   }
   return fail(SSL_ERR_INVALID, "unknown debug knob %d", knob);
 }

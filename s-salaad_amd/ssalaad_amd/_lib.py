@@ -34,6 +34,7 @@ DEBUG_WAIT_POLLS = 1
 DEBUG_WAIT_UNREACHABLE = 2
 DEBUG_PREFILL_SPLIT = 3
 DEBUG_CHAIN_FRAG = 4
+DEBUG_TOPK_GROUPS = 5
 
 _DTYPE_CODE = {torch.float32: SSL_F32, torch.bfloat16: SSL_BF16, torch.float16: SSL_F16}
 
@@ -93,10 +94,11 @@ _SIGNATURES = {
         [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p],
     ),
+    "ssl_block_topk_workspace_size": (_c_i64, [_c_i64]),
     "ssl_block_topk": (
         ctypes.c_int,
         [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_p, _c_p, _c_p, _c_i64,
-         _c_p],
+         _c_p, _c_i64, _c_p],
     ),
     "ssl_project_nm": (
         ctypes.c_int,

@@ -41,11 +41,13 @@ def block_topk(M: torch.Tensor, n_keep: int, block_p: int, block_q: int):
     out = torch.empty(n, m, dtype=torch.float32, device=dev)
     if rb * cb > 0:
         lib = _lib.load()
+        ws_bytes = lib.ssl_block_topk_workspace_size(rb * cb)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
             rc = lib.ssl_block_topk(
                 M.data_ptr(), M.stride(0), rb, cb, block_p, block_q, dt, int(n_keep),
                 norms.data_ptr(), keep.data_ptr(), out.data_ptr(), out.stride(0),
-                _lib.stream_ptr(dev),
+                ws.data_ptr(), ws_bytes, _lib.stream_ptr(dev),
             )
         _lib.check(rc, "ssl_block_topk")
     return (out, keep[: rb * cb].view(rb, cb).bool(), norms[: rb * cb].view(rb, cb))

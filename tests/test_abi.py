@@ -469,13 +469,20 @@ def test_encoder_rejects_bad_arguments():
 def test_block_topk_rejects_bad_arguments_before_any_launch():
     lib = _lib.load()
     fake = 256  # never dereferenced: every call below fails its argument checks first
-    assert lib.ssl_block_topk(fake, 64, 2, 2, 0, 32, _lib.SSL_F32, 1, fake, fake, None, 0, None) == 1
-    assert lib.ssl_block_topk(fake, 32, 2, 2, 32, 32, _lib.SSL_F32, 1, fake, fake, None, 0, None) == 1
-    assert lib.ssl_block_topk(fake, 64, 2, 2, 32, 32, 7, 1, fake, fake, None, 0, None) == 2
-    assert lib.ssl_block_topk(None, 64, 2, 2, 32, 32, _lib.SSL_BF16, 1, fake, fake, None, 0, None) == 1
-    assert lib.ssl_block_topk(fake, 64, 2, 2, 32, 32, _lib.SSL_BF16, 1, fake, fake, fake, 16, None) == 1
+    ws = lib.ssl_block_topk_workspace_size(4)
+    assert ws >= 4096 and ws % 256 == 0 and lib.ssl_block_topk_workspace_size(0) == 0
+    assert lib.ssl_block_topk(fake, 64, 2, 2, 0, 32, _lib.SSL_F32, 1, fake, fake, None, 0, fake, ws, None) == 1
+    assert lib.ssl_block_topk(fake, 32, 2, 2, 32, 32, _lib.SSL_F32, 1, fake, fake, None, 0, fake, ws, None) == 1
+    assert lib.ssl_block_topk(fake, 64, 2, 2, 32, 32, 7, 1, fake, fake, None, 0, fake, ws, None) == 2
+    assert lib.ssl_block_topk(None, 64, 2, 2, 32, 32, _lib.SSL_BF16, 1, fake, fake, None, 0, fake, ws, None) == 1
+    assert lib.ssl_block_topk(fake, 64, 2, 2, 32, 32, _lib.SSL_BF16, 1, fake, fake, fake, 16, fake, ws, None) == 1
     assert b"ldo" in lib.ssl_last_error()
-    assert lib.ssl_block_topk(fake, 64, 0, 2, 32, 32, _lib.SSL_BF16, 1, None, None, None, 0, None) == 0
+    # the select's workspace: missing, short, misaligned
+    assert lib.ssl_block_topk(fake, 64, 2, 2, 32, 32, _lib.SSL_BF16, 1, fake, fake, None, 0, None, ws, None) == 3
+    assert lib.ssl_block_topk(fake, 64, 2, 2, 32, 32, _lib.SSL_BF16, 1, fake, fake, None, 0, fake, ws - 4, None) == 3
+    assert lib.ssl_block_topk(fake, 64, 2, 2, 32, 32, _lib.SSL_BF16, 1, fake, fake, None, 0, fake + 4, ws, None) == 3
+    assert b"workspace" in lib.ssl_last_error()
+    assert lib.ssl_block_topk(fake, 64, 0, 2, 32, 32, _lib.SSL_BF16, 1, None, None, None, 0, None, 0, None) == 0
 
 
 def test_decode_entry_points_reject_bad_arguments_before_any_launch():

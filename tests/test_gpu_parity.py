@@ -499,25 +499,39 @@ def _separated(n, m, p, q, seed):
     return blk.reshape(n, m)
 
 
+@pytest.fixture(params=[0, 2], ids=["select_auto", "select_many_groups"])
+def select_path(request):
+    """The block projection's select: the library's choice (one workgroup at
+    these sizes) or forced onto the many-workgroup launches."""
+    lib = _lib.load()
+    _lib.check(lib.ssl_debug_set(_lib.DEBUG_TOPK_GROUPS, request.param), "ssl_debug_set")
+    yield request.param
+    _lib.check(lib.ssl_debug_set(_lib.DEBUG_TOPK_GROUPS, 0), "ssl_debug_set")
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("shape", [(64, 96, 16, 16), (128, 128, 32, 32), (256, 512, 64, 64),
                                    (48, 40, 8, 4), (12, 20, 1, 1)])
-def test_project_S_matches_oracle(dtype, shape, gpu_device):
+def test_project_S_matches_oracle(dtype, shape, select_path, gpu_device):
     """Keep mask and kept values exact (the values are the input as fp32)."""
     n, m, p, q = shape
     M = _separated(n, m, p, q, seed=n * 7 + m)
     Md = torch.from_numpy(M).to(dtype)
     Mq = Md.float().numpy()                      # the input as the kernel sees it
     total = (n // p) * (m // q)
+    blk = Mq.astype(np.float64).reshape(n // p, p, m // q, q)
+    want_norms = (blk * blk).sum(axis=(1, 3))
     for n_keep in (-3, 0, 1, total // 2, total - 1, total, total + 5):
-        out, keep, _ = ssalaad_amd.block_topk(Md.to(gpu_device), n_keep, p, q)
+        out, keep, norms = ssalaad_amd.block_topk(Md.to(gpu_device), n_keep, p, q)
         torch.cuda.synchronize()
         want, want_keep = orc.project_blocks(Mq, n_keep, p, q)
         assert np.array_equal(keep.cpu().numpy(), want_keep), n_keep
         assert np.array_equal(out.cpu().numpy(), want), n_keep
+        # fp32 sums of p·q squares against float64 ones
+        np.testing.assert_allclose(norms.cpu().numpy(), want_norms, rtol=2e-6 * p * q ** 0.5)
 
 
-def test_project_S_ties_nan_and_inf(gpu_device):
+def test_project_S_ties_nan_and_inf(select_path, gpu_device):
     M = np.ones((8, 12), np.float32)             # twelve equal 2×4 blocks (4 × 3)
     out = ssalaad_amd.project_S(torch.from_numpy(M).to(gpu_device), 5, 2, 4)
     keep = (out.cpu().numpy().reshape(4, 2, 3, 4) != 0).any(axis=(1, 3)).reshape(-1)
@@ -532,6 +546,44 @@ def test_project_S_ties_nan_and_inf(gpu_device):
         got = out.cpu().numpy()
         assert np.array_equal(np.isnan(got), np.isnan(want))
         assert np.array_equal(np.nan_to_num(got, nan=7.0), np.nan_to_num(want, nan=7.0))
+
+
+@pytest.mark.parametrize("n_keep_frac", [0.0, 0.3, 0.5, 0.9, 1.0])
+@pytest.mark.parametrize("shape", [(1024, 1024, 2, 2), (2048, 1536, 4, 4), (300, 700, 1, 1)])
+def test_project_S_ties_across_workgroups(shape, n_keep_frac, select_path, gpu_device):
+    """Small-integer blocks: every norm is an exact integer in both fp32 and the
+    oracle's float64, so thousands of blocks tie at the threshold, spread over
+    the ranges of many select workgroups (up to 196608 blocks here). The kept
+    ones are the lowest block indices among the tied, as in the oracle."""
+    n, m, p, q = shape
+    rng = np.random.default_rng(n + m + int(100 * n_keep_frac))
+    M = rng.integers(-2, 3, size=(n, m)).astype(np.float32)
+    M[rng.random((n, m)) < 0.3] = 0.0
+    total = (n // p) * (m // q)
+    n_keep = int(total * n_keep_frac)
+    out, keep, norms = ssalaad_amd.block_topk(torch.from_numpy(M).to(gpu_device), n_keep, p, q)
+    torch.cuda.synchronize()
+    want, want_keep = orc.project_blocks(M, n_keep, p, q)
+    assert np.array_equal(keep.cpu().numpy(), want_keep)
+    assert np.array_equal(out.cpu().numpy(), want)
+    blk = M.astype(np.float64).reshape(n // p, p, m // q, q)
+    assert np.array_equal(norms.cpu().numpy(), (blk * blk).sum(axis=(1, 3)).astype(np.float32))
+
+
+def test_project_S_many_groups_repeat_and_shrink(gpu_device):
+    """Calls in a row on one stream reuse nothing of the last call's select:
+    a large call, then a smaller one with a different threshold, then the large
+    one again."""
+    cases = [(2048, 2048, 2, 2, 0.4), (512, 768, 2, 2, 0.7), (2048, 2048, 2, 2, 0.4)]
+    rng = np.random.default_rng(5)
+    for n, m, p, q, frac in cases:
+        M = rng.integers(-3, 4, size=(n, m)).astype(np.float32)
+        total = (n // p) * (m // q)
+        out, keep, _ = ssalaad_amd.block_topk(torch.from_numpy(M).to(gpu_device), int(total * frac), p, q)
+        torch.cuda.synchronize()
+        want, want_keep = orc.project_blocks(M, int(total * frac), p, q)
+        assert np.array_equal(keep.cpu().numpy(), want_keep), (n, m)
+        assert np.array_equal(out.cpu().numpy(), want), (n, m)
 
 
 def test_project_S_rejects_bad_arguments(gpu_device):
@@ -561,9 +613,10 @@ def test_project_then_encode_gives_the_reference_structure(gpu_device):
     assert crow[-1] == total - 1                 # the kept subnormal block is dropped
 
 
-def test_project_S_llama7b_ffn_shape(gpu_device):
-    """11008×4096 fp32, 64×64 blocks, half of them kept."""
-    n, m, p = 11008, 4096, 64
+@pytest.mark.parametrize("p", [64, 16, 8])
+def test_project_S_llama7b_ffn_shape(p, gpu_device):
+    """11008×4096 fp32, p×p blocks (11008 to 704512 of them), half kept."""
+    n, m = 11008, 4096
     M = _separated(n, m, p, p, seed=23)
     total = (n // p) * (m // p)
     out, keep, _ = ssalaad_amd.block_topk(torch.from_numpy(M).to(gpu_device), total // 2, p, p)
