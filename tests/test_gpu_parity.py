@@ -553,7 +553,7 @@ def test_project_S_ties_nan_and_inf(select_path, gpu_device):
 def test_project_S_ties_across_workgroups(shape, n_keep_frac, select_path, gpu_device):
     """Small-integer blocks: every norm is an exact integer in both fp32 and the
     oracle's float64, so thousands of blocks tie at the threshold, spread over
-    the ranges of many select workgroups (up to 196608 blocks here). The kept
+    the ranges of many select workgroups (up to 262144 blocks here). The kept
     ones are the lowest block indices among the tied, as in the oracle."""
     n, m, p, q = shape
     rng = np.random.default_rng(n + m + int(100 * n_keep_frac))
