@@ -476,19 +476,39 @@ __global__ __launch_bounds__(kSelGroupThreads) void topk_mark_kernel(const float
 }
 
 // out[i, j] = input as fp32 where block (i / p, j / q) is kept, else 0.
+// vin: every run of 4 elements starting at a multiple of 4 lies in one block
+// and is aligned to 4 elements, so it is one vector load (16 bytes of fp32,
+// 8 of 16-bit values) under one keep flag.
 template <int DT>
 __global__ __launch_bounds__(kThreads) void block_mask_kernel(const void* S, int64_t lds, int n,
                                                               int m, int p, int q, int NBK,
                                                               const uint8_t* keep, float* out,
-                                                              int64_t ldo, bool vec) {
+                                                              int64_t ldo, bool vec, bool vin) {
   for (int i = blockIdx.y; i < n; i += gridDim.y) {
     const uint8_t* krow = keep + (int64_t)(i / p) * NBK;
     for (int j0 = 4 * (blockIdx.x * kThreads + threadIdx.x); j0 < m; j0 += 4 * gridDim.x * kThreads) {
       float v[4];
+      if (vin && j0 + 4 <= m) {
+        v[0] = v[1] = v[2] = v[3] = 0.f;
+        if (krow[j0 / q]) {
+          const int64_t e = (int64_t)i * lds + j0;
+          if constexpr (DT == DT_F32) {
+            const float4 f = *(const float4*)((const float*)S + e);
+            v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+          } else {
+            const uint2 h = *(const uint2*)((const uint16_t*)S + e);
+            v[0] = DT == DT_BF16 ? bf16_to_f32(h.x & 0xffffu) : f16_to_f32(h.x & 0xffffu);
+            v[1] = DT == DT_BF16 ? bf16_to_f32(h.x >> 16) : f16_to_f32(h.x >> 16);
+            v[2] = DT == DT_BF16 ? bf16_to_f32(h.y & 0xffffu) : f16_to_f32(h.y & 0xffffu);
+            v[3] = DT == DT_BF16 ? bf16_to_f32(h.y >> 16) : f16_to_f32(h.y >> 16);
+          }
+        }
+      } else {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int j = j0 + u;
-        v[u] = (j < m && krow[j / q]) ? elem_f32<DT>(S, (int64_t)i * lds + j) : 0.f;
+        for (int u = 0; u < 4; ++u) {
+          const int j = j0 + u;
+          v[u] = (j < m && krow[j / q]) ? elem_f32<DT>(S, (int64_t)i * lds + j) : 0.f;
+        }
       }
       if (vec && j0 + 4 <= m) {
         *(float4*)(out + (int64_t)i * ldo + j0) = make_float4(v[0], v[1], v[2], v[3]);
@@ -590,6 +610,7 @@ int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t 
   // 16-byte pieces of the input: aligned base, row stride and block rows
   const bool vec_in = ((uintptr_t)S % 16 == 0) && (lds * eb) % 16 == 0 && (block_q * eb) % 16 == 0;
   const bool vec_out = out && ((uintptr_t)out % 16 == 0) && ldo % 4 == 0;
+  const bool vec_mask_in = ((uintptr_t)S % (4 * eb) == 0) && lds % 4 == 0 && block_q % 4 == 0;
   // The select: one workgroup over keys staged in its LDS, or many workgroups
   // over kSelGroupKeys keys each (four histogram launches and the marking).
   const int64_t knob = debug_knobs().topk_groups;
@@ -637,7 +658,7 @@ int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t 
   }                                                                                             \
   if (out)                                                                                      \
     hipLaunchKernelGGL(block_mask_kernel<DTC>, mgrid, dim3(kThreads), 0, s, S, lds, n, m,        \
-                       block_p, block_q, (int)NBK, keep, out, ldo, vec_out);
+                       block_p, block_q, (int)NBK, keep, out, ldo, vec_out, vec_mask_in);
   switch (dtype) {
     case SSL_F32: SSL_PROJECT(DT_F32) break;
     case SSL_BF16: SSL_PROJECT(DT_BF16) break;
