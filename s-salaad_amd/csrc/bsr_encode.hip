@@ -49,52 +49,6 @@ __global__ __launch_bounds__(kThreads) void bsr_flag_kernel(const void* S, int64
   if (lane == 0) flags[blk] = (uint8_t)((!any_nan && any_nz) ? 1 : 0);
 }
 
-// Single workgroup: crow (exclusive scan of per-row counts), active rows, totals.
-__global__ __launch_bounds__(kThreads) void bsr_scan_kernel(const uint8_t* flags, int NB, int NBK,
-                                                            int32_t* crow, int32_t* active,
-                                                            int32_t* totals) {
-  __shared__ int s_nnz[kThreads], s_act[kThreads];
-  const int t = threadIdx.x;
-  const int R = (NB + kThreads - 1) / kThreads;
-  const int r0 = min(t * R, NB), r1 = min(r0 + R, NB);
-  auto count = [&](int by) {
-    int n = 0;
-    const uint8_t* f = flags + (int64_t)by * NBK;
-    for (int j = 0; j < NBK; ++j) n += f[j];
-    return n;
-  };
-  int nnz = 0, act = 0;
-  for (int by = r0; by < r1; ++by) {
-    const int n = count(by);
-    nnz += n;
-    act += (n > 0);
-  }
-  s_nnz[t] = nnz;
-  s_act[t] = act;
-  __syncthreads();
-  if (t == 0) {
-    int a = 0, b = 0;
-    for (int i = 0; i < kThreads; ++i) {
-      const int x = s_nnz[i], y = s_act[i];
-      s_nnz[i] = a;
-      s_act[i] = b;
-      a += x;
-      b += y;
-    }
-    crow[NB] = a;
-    totals[0] = a;
-    totals[1] = b;
-  }
-  __syncthreads();
-  int off = s_nnz[t], aoff = s_act[t];
-  for (int by = r0; by < r1; ++by) {
-    const int n = count(by);
-    crow[by] = off;
-    if (n > 0) active[aoff++] = by;
-    off += n;
-  }
-}
-
 // One workgroup per block-row: col indices and value copies of the kept blocks.
 template <int DT>
 __global__ __launch_bounds__(kThreads) void bsr_fill_kernel(const void* S, int64_t lds, int NBK,
@@ -149,6 +103,242 @@ __global__ __launch_bounds__(kThreads) void bsr_fill_kernel(const void* S, int64
   }
 }
 
+// ---------------------------------------------------------------------------
+// Vector paths, for blocks whose rows are whole 16-byte pieces (S, lds and q
+// aligned to 16 bytes). The keep rule and the copies are the ones above.
+// ---------------------------------------------------------------------------
+constexpr int kFlagRounds = 4;   // blocks per lane group and wave, small blocks
+constexpr int kScanThreads = 1024;
+constexpr int kScanKeep = 16;    // row counts a scan thread keeps in registers
+
+// L lanes per block (the piece count's next power of two, at most 64), 64 / L
+// blocks per wave and round; a lane tests pieces li, li + L, ... of its block,
+// four loads at a time.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void bsr_flag_vec_kernel(const void* S, int64_t lds,
+                                                                int64_t nblocks, int NBK, int p,
+                                                                int q, int L, int rounds,
+                                                                uint8_t* flags) {
+  using T = typename Bits<DT>::T;
+  constexpr int EB = (int)sizeof(T), VE = 16 / EB;
+  const int lane = threadIdx.x & 63;
+  const int per_round = kWave / L, cpr = q / VE, pieces = p * cpr;
+  const int gi = lane / L, li = lane % L;
+  const unsigned long long gmask = (L == kWave ? ~0ull : ((1ull << L) - 1ull)) << (gi * L);
+  const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  for (int r = 0; r < rounds; ++r) {
+    const int64_t blk = (wave * rounds + r) * per_round + gi;
+    bool nan = false, nz = false;
+    if (blk < nblocks) {
+      const int by = (int)(blk / NBK), bc = (int)(blk % NBK);
+      const char* base = (const char*)S + ((int64_t)by * p * lds + (int64_t)bc * q) * EB;
+      for (int x0 = li; x0 < pieces; x0 += 4 * L) {
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int x = x0 + u * L;
+          v[u] = make_uint4(0, 0, 0, 0);
+          if (x < pieces)
+            v[u] = *(const uint4*)(base + ((int64_t)(x / cpr) * lds + (x % cpr) * VE) * EB);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            if constexpr (DT == DT_F32) {
+              nan |= Bits<DT>::is_nan(w[h]);
+              nz |= !Bits<DT>::is_zero(w[h]);
+            } else {
+              const T lo = (T)(w[h] & 0xffffu), hi = (T)(w[h] >> 16);
+              nan |= Bits<DT>::is_nan(lo) || Bits<DT>::is_nan(hi);
+              nz |= !Bits<DT>::is_zero(lo) || !Bits<DT>::is_zero(hi);
+            }
+          }
+        }
+      }
+    }
+    const unsigned long long bn = __ballot(nan) & gmask, bz = __ballot(nz) & gmask;
+    if (li == 0 && blk < nblocks) flags[blk] = (uint8_t)((bn == 0ull && bz != 0ull) ? 1 : 0);
+  }
+}
+
+// One wave per block-row: crow[by] = its number of kept blocks (the scan below
+// turns the counts into offsets in place).
+__global__ __launch_bounds__(kThreads) void bsr_rowcount_kernel(const uint8_t* flags, int NB,
+                                                                int NBK, int32_t* crow) {
+  const int lane = threadIdx.x & 63;
+  const int64_t by = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (by >= NB) return;
+  const uint8_t* f = flags + by * NBK;
+  int c = 0;
+  for (int j0 = 0; j0 < NBK; j0 += 4 * kWave) {
+    uint8_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + u * kWave + lane;
+      v[u] = j < NBK ? f[j] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) c += __popcll(__ballot(v[u] != 0));
+  }
+  if (lane == 0) crow[by] = c;
+}
+
+// Single workgroup: row counts → crow offsets (in place), active rows, totals.
+// Thread t owns rows [t·R, (t+1)·R); it reads them all before the scan and
+// writes only its own rows after it.
+__global__ __launch_bounds__(kScanThreads) void bsr_scan_counts_kernel(int NB, int32_t* crow,
+                                                                       int32_t* active,
+                                                                       int32_t* totals) {
+  __shared__ int s_w[kScanThreads / kWave][2];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int R = (NB + kScanThreads - 1) / kScanThreads;
+  const int r0 = min(t * R, NB), r1 = min(r0 + R, NB);
+  int cnt[kScanKeep];
+  int nnz = 0, act = 0;
+#pragma unroll
+  for (int k = 0; k < kScanKeep; ++k) {
+    cnt[k] = r0 + k < r1 ? crow[r0 + k] : 0;
+    nnz += cnt[k];
+    act += cnt[k] > 0;
+  }
+  for (int by = r0 + kScanKeep; by < r1; ++by) {
+    const int c = crow[by];
+    nnz += c;
+    act += c > 0;
+  }
+  // inclusive scans of (nnz, act) over the wave, then over the waves
+  int in = nnz, ia = act;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int a = __shfl_up(in, off, kWave), b = __shfl_up(ia, off, kWave);
+    if (lane >= off) in += a, ia += b;
+  }
+  if (lane == kWave - 1) s_w[w][0] = in, s_w[w][1] = ia;
+  __syncthreads();
+  int bn = 0, ba = 0, tn = 0, ta = 0;
+  for (int x = 0; x < kScanThreads / kWave; ++x) {
+    if (x < w) bn += s_w[x][0], ba += s_w[x][1];
+    tn += s_w[x][0];
+    ta += s_w[x][1];
+  }
+  int off = bn + in - nnz, aoff = ba + ia - act;
+#pragma unroll
+  for (int k = 0; k < kScanKeep; ++k) {
+    if (r0 + k < r1) {
+      crow[r0 + k] = off;
+      if (cnt[k] > 0) active[aoff++] = r0 + k;
+      off += cnt[k];
+    }
+  }
+  for (int by = r0 + kScanKeep; by < r1; ++by) {
+    const int c = crow[by];
+    crow[by] = off;
+    if (c > 0) active[aoff++] = by;
+    off += c;
+  }
+  if (t == kScanThreads - 1) {
+    crow[NB] = tn;
+    totals[0] = tn;
+    totals[1] = ta;
+  }
+}
+
+// One workgroup per block-row, one wave per kept block (four at a time): the
+// (p, q) copy in 16-byte pieces, the (q, p) copy in 16-byte pieces of VE
+// consecutive rows of one column (VT: p a multiple of VE).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void bsr_fill_vec_kernel(const void* S, int64_t lds, int NBK,
+                                                                int p, int q,
+                                                                const uint8_t* flags,
+                                                                const int32_t* crow, int32_t* col,
+                                                                void* vbsr, void* vt) {
+  using T = typename Bits<DT>::T;
+  constexpr int EB = (int)sizeof(T), VE = 16 / EB;
+  constexpr int SEG = 1024;
+  __shared__ int s_cols[SEG];
+  __shared__ int s_cnt[kThreads];
+  __shared__ int s_nseg;
+  const int by = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const uint8_t* f = flags + (int64_t)by * NBK;
+  const int cpr = q / VE, pieces = p * cpr, tpc = p / VE, tpieces = q * tpc;
+  int base = crow[by];
+  for (int c0 = 0; c0 < NBK; c0 += SEG) {
+    const int cn = min(SEG, NBK - c0);
+    const int j0 = c0 + 4 * t;
+    int mine = 0;
+    for (int j = j0; j < min(j0 + 4, c0 + cn); ++j) mine += f[j];
+    s_cnt[t] = mine;
+    __syncthreads();
+    if (t == 0) {
+      int a = 0;
+      for (int i = 0; i < kThreads; ++i) {
+        const int x = s_cnt[i];
+        s_cnt[i] = a;
+        a += x;
+      }
+      s_nseg = a;
+    }
+    __syncthreads();
+    int pos = s_cnt[t];
+    for (int j = j0; j < min(j0 + 4, c0 + cn); ++j)
+      if (f[j]) s_cols[pos++] = j;
+    __syncthreads();
+    const int nseg = s_nseg;
+    for (int k = w; k < nseg; k += kWaves) {
+      const int bc = s_cols[k];
+      const int64_t dst = (int64_t)base + k;
+      if (lane == 0) col[dst] = bc;
+      const char* src = (const char*)S + ((int64_t)by * p * lds + (int64_t)bc * q) * EB;
+      if (vbsr) {
+        char* d = (char*)vbsr + dst * p * q * EB;
+        for (int x0 = lane; x0 < pieces; x0 += 4 * kWave) {
+          uint4 v[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int x = x0 + u * kWave;
+            v[u] = make_uint4(0, 0, 0, 0);
+            if (x < pieces) v[u] = *(const uint4*)(src + ((int64_t)(x / cpr) * lds + (x % cpr) * VE) * EB);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int x = x0 + u * kWave;
+            if (x < pieces) *(uint4*)(d + (int64_t)x * 16) = v[u];
+          }
+        }
+      }
+      if (vt) {
+        char* d = (char*)vt + dst * p * q * EB;
+        for (int y0 = lane; y0 < tpieces; y0 += 4 * kWave) {
+          uint32_t wv[4][4];  // the piece's 16 bytes, packed as loaded
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int y = y0 + u * kWave;
+            const bool in = y < tpieces;
+            const int j = in ? y / tpc : 0, i0 = in ? (y % tpc) * VE : 0;
+#pragma unroll
+            for (int e = 0; e < VE; ++e) {
+              const uint32_t b = in ? (uint32_t)((const T*)src)[(int64_t)(i0 + e) * lds + j] : 0u;
+              if constexpr (VE == 4) wv[u][e] = b;
+              else if (e & 1) wv[u][e >> 1] |= b << 16;
+              else wv[u][e >> 1] = b;
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int y = y0 + u * kWave;
+            if (y < tpieces)
+              *(uint4*)(d + (int64_t)y * 16) = make_uint4(wv[u][0], wv[u][1], wv[u][2], wv[u][3]);
+          }
+        }
+      }
+    }
+    base += nseg;
+    __syncthreads();
+  }
+}
+
 }  // namespace
 }  // namespace ssl
 
@@ -167,7 +357,26 @@ int ssl_bsr_encode_count(const void* S, int64_t lds, int64_t NB, int64_t NBK, in
   if (NB * NBK > 0x7fffffffLL) return fail(SSL_ERR_INVALID, "too many blocks");
   hipStream_t s = (hipStream_t)stream;
   const int64_t nblocks = NB * NBK;
-  if (nblocks > 0) {
+  const int eb = (dtype == SSL_F32) ? 4 : 2;
+  const bool vec = ((uintptr_t)S % 16 == 0) && (lds * eb) % 16 == 0 && (block_q * eb) % 16 == 0;
+  if (nblocks > 0 && vec && (dtype == SSL_F32 || dtype == SSL_BF16 || dtype == SSL_F16)) {
+    const int64_t pieces = (int64_t)block_p * (block_q * eb / 16);
+    int L = 1;
+    while (L < pieces && L < kWave) L <<= 1;
+    const int rounds = L < kWave ? kFlagRounds : 1;
+    const int64_t per_wave = (int64_t)(kWave / L) * rounds;
+    const int64_t waves = (nblocks + per_wave - 1) / per_wave;
+    const unsigned grid = (unsigned)((waves + kWaves - 1) / kWaves);
+#define SSL_FLAG_VEC(DTC)                                                                        \
+  hipLaunchKernelGGL(bsr_flag_vec_kernel<DTC>, dim3(grid), dim3(kThreads), 0, s, S, lds, nblocks, \
+                     (int)NBK, block_p, block_q, L, rounds, flags)
+    if (dtype == SSL_F32) SSL_FLAG_VEC(DT_F32);
+    else if (dtype == SSL_BF16) SSL_FLAG_VEC(DT_BF16);
+    else SSL_FLAG_VEC(DT_F16);
+#undef SSL_FLAG_VEC
+    int rc = check_hip(hipGetLastError(), "bsr flag launch");
+    if (rc) return rc;
+  } else if (nblocks > 0) {
     const unsigned grid = (unsigned)((nblocks + kWaves - 1) / kWaves);
     switch (dtype) {
       case SSL_F32:
@@ -190,8 +399,11 @@ int ssl_bsr_encode_count(const void* S, int64_t lds, int64_t NB, int64_t NBK, in
   } else if (!(dtype == SSL_F32 || dtype == SSL_BF16 || dtype == SSL_F16)) {
     return fail(SSL_ERR_UNSUPPORTED, "unsupported dtype %d", dtype);
   }
-  hipLaunchKernelGGL(bsr_scan_kernel, dim3(1), dim3(kThreads), 0, s, flags, (int)NB, (int)NBK,
-                     crow, active_rows, totals);
+  if (NB > 0)
+    hipLaunchKernelGGL(bsr_rowcount_kernel, dim3((unsigned)((NB + kWaves - 1) / kWaves)),
+                       dim3(kThreads), 0, s, flags, (int)NB, (int)NBK, crow);
+  hipLaunchKernelGGL(bsr_scan_counts_kernel, dim3(1), dim3(kScanThreads), 0, s, (int)NB, crow,
+                     active_rows, totals);
   return check_hip(hipGetLastError(), "bsr scan launch");
 }
 
@@ -204,6 +416,20 @@ int ssl_bsr_encode_fill(const void* S, int64_t lds, int64_t NB, int64_t NBK, int
   if (NB == 0 || NBK == 0) return SSL_OK;
   if (!S || !flags || !crow || !col) return fail(SSL_ERR_INVALID, "null pointer");
   hipStream_t s = (hipStream_t)stream;
+  const int eb = (dtype == SSL_F32) ? 4 : 2;
+  const bool vec = ((uintptr_t)S % 16 == 0) && (lds * eb) % 16 == 0 &&
+                   (block_q * eb) % 16 == 0 && (uintptr_t)values_bsr % 16 == 0 &&
+                   (!values_t || ((uintptr_t)values_t % 16 == 0 && (block_p * eb) % 16 == 0));
+  if (vec && (dtype == SSL_F32 || dtype == SSL_BF16 || dtype == SSL_F16)) {
+#define SSL_FILL_VEC(DTC)                                                                         \
+  hipLaunchKernelGGL(bsr_fill_vec_kernel<DTC>, dim3((unsigned)NB), dim3(kThreads), 0, s, S, lds,   \
+                     (int)NBK, block_p, block_q, flags, crow, col, values_bsr, values_t)
+    if (dtype == SSL_F32) SSL_FILL_VEC(DT_F32);
+    else if (dtype == SSL_BF16) SSL_FILL_VEC(DT_BF16);
+    else SSL_FILL_VEC(DT_F16);
+#undef SSL_FILL_VEC
+    return check_hip(hipGetLastError(), "bsr fill launch");
+  }
   switch (dtype) {
     case SSL_F32:
       hipLaunchKernelGGL(bsr_fill_kernel<DT_F32>, dim3((unsigned)NB), dim3(kThreads), 0, s, S, lds,

@@ -531,11 +531,15 @@ __global__ __launch_bounds__(kThreads) void block_mask_kernel(const void* S, int
 // every NaN folded above +inf; equal keys go to the lower index. One thread
 // per group; NMM ≥ nm_m bounds the unrolled group.
 // ---------------------------------------------------------------------------
-template <int DT, int NMM>
+// VEC (nm_m == NMM, every group aligned in R, out and keep): the group is read
+// with 16-byte (or, for four 16-bit values, 8-byte) loads and written with
+// 16-byte stores of out and one store of its NMM keep bytes.
+template <int DT, int NMM, bool VEC>
 __global__ __launch_bounds__(kThreads) void nm_project_kernel(const void* R, int64_t ldr, int n,
                                                               int groups_per_row, int nm_n,
                                                               int nm_m, float* out, int64_t ldo,
                                                               uint8_t* keep, int64_t ldk) {
+  constexpr int EB = Elem<DT>::bytes;
   const int64_t total = (int64_t)n * groups_per_row;
   for (int64_t g = (int64_t)blockIdx.x * kThreads + threadIdx.x; g < total;
        g += (int64_t)gridDim.x * kThreads) {
@@ -543,22 +547,76 @@ __global__ __launch_bounds__(kThreads) void nm_project_kernel(const void* R, int
     const int64_t c0 = (g % groups_per_row) * nm_m;
     float v[NMM];
     uint32_t key[NMM];
+    if constexpr (VEC) {
+      constexpr int W = NMM * EB / 4;  // 32-bit words of the group
+      uint32_t w[W];
+      const char* src = (const char*)R + (row * ldr + c0) * EB;
+      if constexpr (W % 4 == 0) {
 #pragma unroll
-    for (int j = 0; j < NMM; ++j) {
-      v[j] = j < nm_m ? elem_f32<DT>(R, row * ldr + c0 + j) : 0.f;
-      const uint32_t b = __float_as_uint(v[j]) & 0x7fffffffu;
-      key[j] = j < nm_m ? (b > 0x7f800000u ? kNanKey : b) : 0u;
+        for (int x = 0; x < W / 4; ++x) {
+          const uint4 q = ((const uint4*)src)[x];
+          w[4 * x] = q.x, w[4 * x + 1] = q.y, w[4 * x + 2] = q.z, w[4 * x + 3] = q.w;
+        }
+      } else {
+        const uint2 q = *(const uint2*)src;
+        w[0] = q.x, w[1] = q.y;
+      }
+#pragma unroll
+      for (int j = 0; j < NMM; ++j) {
+        if constexpr (DT == DT_F32) v[j] = __uint_as_float(w[j]);
+        else {
+          const uint32_t h = (w[j / 2] >> (16 * (j & 1))) & 0xffffu;
+          v[j] = DT == DT_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NMM; ++j) v[j] = j < nm_m ? elem_f32<DT>(R, row * ldr + c0 + j) : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < NMM; ++j) {
-      if (j >= nm_m) break;
+      const uint32_t b = __float_as_uint(v[j]) & 0x7fffffffu;
+      key[j] = j < nm_m ? (b > 0x7f800000u ? kNanKey : b) : 0u;
+    }
+    float o[NMM];
+    uint8_t kb[NMM];
+#pragma unroll
+    for (int j = 0; j < NMM; ++j) {
       int rank = 0;
 #pragma unroll
       for (int k = 0; k < NMM; ++k)
         rank += (k < nm_m && (key[k] > key[j] || (key[k] == key[j] && k < j))) ? 1 : 0;
       const bool kept = rank < nm_n;
-      out[row * ldo + c0 + j] = v[j] * (kept ? 1.f : 0.f);
-      if (keep) keep[row * ldk + c0 + j] = kept ? 1 : 0;
+      o[j] = v[j] * (kept ? 1.f : 0.f);
+      kb[j] = kept ? 1 : 0;
+    }
+    if constexpr (VEC) {
+      float4* dst = (float4*)(out + row * ldo + c0);
+#pragma unroll
+      for (int x = 0; x < NMM / 4; ++x)
+        dst[x] = make_float4(o[4 * x], o[4 * x + 1], o[4 * x + 2], o[4 * x + 3]);
+      if (keep) {
+        uint32_t kw[NMM / 4];
+#pragma unroll
+        for (int x = 0; x < NMM / 4; ++x)
+          kw[x] = kb[4 * x] | (kb[4 * x + 1] << 8) | (kb[4 * x + 2] << 16) |
+                  ((uint32_t)kb[4 * x + 3] << 24);
+        uint8_t* kd = keep + row * ldk + c0;
+        if constexpr (NMM == 4) *(uint32_t*)kd = kw[0];
+        else if constexpr (NMM == 8) *(uint2*)kd = make_uint2(kw[0], kw[1]);
+        else {
+#pragma unroll
+          for (int x = 0; x < NMM / 16; ++x)
+            ((uint4*)kd)[x] = make_uint4(kw[4 * x], kw[4 * x + 1], kw[4 * x + 2], kw[4 * x + 3]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NMM; ++j) {
+        if (j >= nm_m) break;
+        out[row * ldo + c0 + j] = o[j];
+        if (keep) keep[row * ldk + c0 + j] = kb[j];
+      }
     }
   }
 }
@@ -689,9 +747,24 @@ int ssl_project_nm(const void* R, int64_t ldr, int64_t n, int64_t m, int32_t nm_
   const unsigned grid = (unsigned)(want < 8192 ? want : 8192);
   hipStream_t s = (hipStream_t)stream;
   const int gpr = (int)(m / nm_m);
-#define SSL_NM(DTC, NMM)                                                                     \
-  hipLaunchKernelGGL((nm_project_kernel<DTC, NMM>), dim3(grid), dim3(kThreads), 0, s, R, ldr, \
-                     (int)n, gpr, nm_n, nm_m, out, ldo, keep, ldk)
+  // Whole aligned groups: nm_m a power of two from 4, every group's start in R
+  // aligned to its own size (at most 16 bytes), out rows to 16 bytes, keep
+  // rows to the group's byte count (at most 16).
+  const int eb = elem_bytes(dtype);
+  const bool pow2 = nm_m == 4 || nm_m == 8 || nm_m == 16 || nm_m == 32;
+  const int64_t ga = std::min<int64_t>((int64_t)nm_m * eb, 16), ka = std::min(nm_m, 16);
+  const bool vec = pow2 && (uintptr_t)R % ga == 0 && (ldr * eb) % ga == 0 &&
+                   (uintptr_t)out % 16 == 0 && ldo % 4 == 0 &&
+                   (!keep || ((uintptr_t)keep % ka == 0 && ldk % ka == 0));
+#define SSL_NM(DTC, NMM)                                                                       \
+  do {                                                                                          \
+    if (vec && nm_m == NMM)                                                                     \
+      hipLaunchKernelGGL((nm_project_kernel<DTC, NMM, true>), dim3(grid), dim3(kThreads), 0, s,   \
+                         R, ldr, (int)n, gpr, nm_n, nm_m, out, ldo, keep, ldk);                 \
+    else                                                                                        \
+      hipLaunchKernelGGL((nm_project_kernel<DTC, NMM, false>), dim3(grid), dim3(kThreads), 0, s,  \
+                         R, ldr, (int)n, gpr, nm_n, nm_m, out, ldo, keep, ldk);                 \
+  } while (0)
 #define SSL_NM_DT(DTC)                   \
   if (nm_m <= 4) SSL_NM(DTC, 4);         \
   else if (nm_m <= 8) SSL_NM(DTC, 8);    \
