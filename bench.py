@@ -56,8 +56,16 @@ headline):
                        2048 tokens: TFLOP/s of the dense-equivalent work
                        (x·Bᵀ, t·Aᵀ and the kept half of S)
   block_topk           the compression loop's block projection (project_S) of
-                       an 11008×4096 fp32 matrix, 64×64 blocks, half kept:
-                       GB/s of compulsory traffic
+                       an 11008×4096 fp32 matrix, 64×64 blocks (--block P for
+                       P×P), half kept: GB/s of compulsory traffic
+  dense_to_bsr         the encoder (encode_for_kernels: flags, row counts,
+                       crow, col and (q, p) values) of an 11008×4096 bf16
+                       matrix with half of its 64×64 blocks (--block P) zero:
+                       GB/s of compulsory traffic (read the matrix, write the
+                       kept blocks)
+  project_nm           the compression loop's N:M projection (project_S_nm,
+                       2:4) of an 11008×4096 fp32 matrix: GB/s of compulsory
+                       traffic (read it, write fp32 and the keep bytes)
   llama7b_ffn_decode_nm24  the same projection with 2:4 S (two of every four
                        input features kept, N(0, 0.02)) instead of blocks:
                        GB/s of algorithmic bytes (values plus 4-bit
@@ -617,6 +625,41 @@ def run_workload(args) -> dict:
                     roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                               "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                               "traffic": None, "bytes_per_call": int(b)})
+    if args.workload == "dense_to_bsr":
+        from ssalaad_amd.artifact import encode_for_kernels
+
+        p = args.block if args.block_set else 64
+        if n % p or m % p:
+            raise SystemExit(f"--block {p} does not divide {n}x{m}")
+        keep_blocks = torch.rand(n // p, m // p, generator=gen) < 0.5
+        mask = keep_blocks.repeat_interleave(p, 0).repeat_interleave(p, 1)
+        St = (torch.randn(n, m, generator=gen) * mask).to(torch.bfloat16).to(dev)
+        kept = int(keep_blocks.sum())
+        us = _time_eager(lambda: encode_for_kernels(St, p, p), args.steps)
+        b = n * m * 2 + kept * p * p * 2 + kept * 4 + (n // p + 1) * 4
+        gbs = b / us / 1e3
+        return dict(base, metric=f"BSR encode GB/s (encode_for_kernels, 11008x4096 bf16, {p}x{p} blocks)",
+                    value=round(gbs, 1), unit="GB/s", ms_per_step=round(us / 1e3, 5),
+                    dtype="bf16",
+                    config={"workload": "dense_to_bsr", "n": n, "m": m, "block": p,
+                            "blocks_kept": kept, "parallelism": "single_gpu"},
+                    roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                              "traffic": None, "bytes_per_call": int(b)})
+    if args.workload == "project_nm":
+        import ssalaad_amd
+
+        Rt = torch.randn(n, m, generator=gen).to(dev)
+        us = _time_eager(lambda: ssalaad_amd.project_nm(Rt, 2, 4), args.steps)
+        b = n * m * (4 + 4 + 1)  # read fp32, write fp32 and the keep bytes
+        gbs = b / us / 1e3
+        return dict(base, metric="N:M projection GB/s (project_nm 2:4, 11008x4096 fp32)",
+                    value=round(gbs, 1), unit="GB/s", ms_per_step=round(us / 1e3, 5), dtype="f32",
+                    config={"workload": "project_nm", "n": n, "m": m, "nm": "2:4",
+                            "parallelism": "single_gpu"},
+                    roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                              "traffic": None, "bytes_per_call": int(b)})
     if args.workload == "llama60m_forward":
         from ssalaad_amd import LRSLinear
         from ssalaad_amd.bundle import build_model_from_config
@@ -990,6 +1033,7 @@ def main():
     ap.add_argument("--workload", default="llama1b_decode",
                     choices=["llama1b_decode", "llama7b_ffn_decode", "llama7b_ffn_prefill",
                              "llama7b_ffn_decode_nm24", "llama7b_ffn_prefill_nm24", "block_topk",
+                             "dense_to_bsr", "project_nm",
                              "llama7b_lr_prefill", "skew_prefill",
                              "llama60m_forward",
                              "llama1b_decode_step", "sweep", "llama1b_prefill"])

@@ -126,6 +126,43 @@ __global__ __launch_bounds__(kThreads) void bsr_flag_vec_kernel(const void* S, i
   const int gi = lane / L, li = lane % L;
   const unsigned long long gmask = (L == kWave ? ~0ull : ((1ull << L) - 1ull)) << (gi * L);
   const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  auto test = [&](const uint4& v, bool& nan, bool& nz) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      if constexpr (DT == DT_F32) {
+        nan |= Bits<DT>::is_nan(w[h]);
+        nz |= !Bits<DT>::is_zero(w[h]);
+      } else {
+        const T lo = (T)(w[h] & 0xffffu), hi = (T)(w[h] >> 16);
+        nan |= Bits<DT>::is_nan(lo) || Bits<DT>::is_nan(hi);
+        nz |= !Bits<DT>::is_zero(lo) || !Bits<DT>::is_zero(hi);
+      }
+    }
+  };
+  if (pieces <= L && rounds == kFlagRounds) {
+    // at most one piece per lane and block: every round's load in flight at once
+    uint4 v[kFlagRounds];
+#pragma unroll
+    for (int r = 0; r < kFlagRounds; ++r) {
+      const int64_t blk = (wave * kFlagRounds + r) * per_round + gi;
+      v[r] = make_uint4(0, 0, 0, 0);
+      if (blk < nblocks && li < pieces) {
+        const int by = (int)(blk / NBK), bc = (int)(blk % NBK);
+        const char* base = (const char*)S + ((int64_t)by * p * lds + (int64_t)bc * q) * EB;
+        v[r] = *(const uint4*)(base + ((int64_t)(li / cpr) * lds + (li % cpr) * VE) * EB);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kFlagRounds; ++r) {
+      const int64_t blk = (wave * kFlagRounds + r) * per_round + gi;
+      bool nan = false, nz = false;
+      test(v[r], nan, nz);
+      const unsigned long long bn = __ballot(nan) & gmask, bz = __ballot(nz) & gmask;
+      if (li == 0 && blk < nblocks) flags[blk] = (uint8_t)((bn == 0ull && bz != 0ull) ? 1 : 0);
+    }
+    return;
+  }
   for (int r = 0; r < rounds; ++r) {
     const int64_t blk = (wave * rounds + r) * per_round + gi;
     bool nan = false, nz = false;
@@ -142,20 +179,7 @@ __global__ __launch_bounds__(kThreads) void bsr_flag_vec_kernel(const void* S, i
             v[u] = *(const uint4*)(base + ((int64_t)(x / cpr) * lds + (x % cpr) * VE) * EB);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-          for (int h = 0; h < 4; ++h) {
-            if constexpr (DT == DT_F32) {
-              nan |= Bits<DT>::is_nan(w[h]);
-              nz |= !Bits<DT>::is_zero(w[h]);
-            } else {
-              const T lo = (T)(w[h] & 0xffffu), hi = (T)(w[h] >> 16);
-              nan |= Bits<DT>::is_nan(lo) || Bits<DT>::is_nan(hi);
-              nz |= !Bits<DT>::is_zero(lo) || !Bits<DT>::is_zero(hi);
-            }
-          }
-        }
+        for (int u = 0; u < 4; ++u) test(v[u], nan, nz);
       }
     }
     const unsigned long long bn = __ballot(nan) & gmask, bz = __ballot(nz) & gmask;
@@ -245,9 +269,12 @@ __global__ __launch_bounds__(kScanThreads) void bsr_scan_counts_kernel(int NB, i
   }
 }
 
-// One workgroup per block-row, one wave per kept block (four at a time): the
-// (p, q) copy in 16-byte pieces, the (q, p) copy in 16-byte pieces of VE
-// consecutive rows of one column (VT: p a multiple of VE).
+// gridDim.y workgroups per block-row, one wave per kept block (four at a time): the
+// (p, q) copy in 16-byte pieces; the (q, p) copy through LDS, in slabs of SR
+// rows (a multiple of VE, at most 8 KiB of the block per wave): the slab's
+// pieces are stored row-major, then each lane gathers VE consecutive rows of
+// one column and stores them as one 16-byte piece (VT needs p a multiple of VE
+// and q at most 512, so that a slab holds at least VE rows).
 template <int DT>
 __global__ __launch_bounds__(kThreads) void bsr_fill_vec_kernel(const void* S, int64_t lds, int NBK,
                                                                 int p, int q,
@@ -256,13 +283,16 @@ __global__ __launch_bounds__(kThreads) void bsr_fill_vec_kernel(const void* S, i
                                                                 void* vbsr, void* vt) {
   using T = typename Bits<DT>::T;
   constexpr int EB = (int)sizeof(T), VE = 16 / EB;
-  constexpr int SEG = 1024;
+  constexpr int SEG = 1024, kSlabBytes = 8192;
   __shared__ int s_cols[SEG];
   __shared__ int s_cnt[kThreads];
   __shared__ int s_nseg;
+  __shared__ uint4 s_slab[kWaves][kSlabBytes / 16];
   const int by = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
   const uint8_t* f = flags + (int64_t)by * NBK;
-  const int cpr = q / VE, pieces = p * cpr, tpc = p / VE, tpieces = q * tpc;
+  const int cpr = q / VE, pieces = p * cpr;
+  const int SR = min(p, kSlabBytes / (q * EB) / VE * VE);
+  const T* tile = (const T*)s_slab[w];
   int base = crow[by];
   for (int c0 = 0; c0 < NBK; c0 += SEG) {
     const int cn = min(SEG, NBK - c0);
@@ -286,12 +316,16 @@ __global__ __launch_bounds__(kThreads) void bsr_fill_vec_kernel(const void* S, i
       if (f[j]) s_cols[pos++] = j;
     __syncthreads();
     const int nseg = s_nseg;
-    for (int k = w; k < nseg; k += kWaves) {
-      const int bc = s_cols[k];
+    // rounds of four blocks, the same count in every wave (the slab barriers);
+    // workgroup z of the row takes rounds z, z + gridDim.y, ...
+    for (int k0 = blockIdx.y * kWaves; k0 < nseg; k0 += kWaves * gridDim.y) {
+      const int k = k0 + w;
+      const bool active = k < nseg;
+      const int bc = active ? s_cols[k] : 0;
       const int64_t dst = (int64_t)base + k;
-      if (lane == 0) col[dst] = bc;
       const char* src = (const char*)S + ((int64_t)by * p * lds + (int64_t)bc * q) * EB;
-      if (vbsr) {
+      if (active && lane == 0) col[dst] = bc;
+      if (active && vbsr) {
         char* d = (char*)vbsr + dst * p * q * EB;
         for (int x0 = lane; x0 < pieces; x0 += 4 * kWave) {
           uint4 v[4];
@@ -310,27 +344,39 @@ __global__ __launch_bounds__(kThreads) void bsr_fill_vec_kernel(const void* S, i
       }
       if (vt) {
         char* d = (char*)vt + dst * p * q * EB;
-        for (int y0 = lane; y0 < tpieces; y0 += 4 * kWave) {
-          uint32_t wv[4][4];  // the piece's 16 bytes, packed as loaded
+        for (int r0 = 0; r0 < p; r0 += SR) {
+          const int nr = min(SR, p - r0), spieces = nr * cpr, tpc = nr / VE;
+          if (active) {
+            for (int x0 = lane; x0 < spieces; x0 += 4 * kWave) {
+              uint4 v[4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int y = y0 + u * kWave;
-            const bool in = y < tpieces;
-            const int j = in ? y / tpc : 0, i0 = in ? (y % tpc) * VE : 0;
+              for (int u = 0; u < 4; ++u) {
+                const int x = x0 + u * kWave;
+                v[u] = make_uint4(0, 0, 0, 0);
+                if (x < spieces)
+                  v[u] = *(const uint4*)(src + ((int64_t)(r0 + x / cpr) * lds + (x % cpr) * VE) * EB);
+              }
 #pragma unroll
-            for (int e = 0; e < VE; ++e) {
-              const uint32_t b = in ? (uint32_t)((const T*)src)[(int64_t)(i0 + e) * lds + j] : 0u;
-              if constexpr (VE == 4) wv[u][e] = b;
-              else if (e & 1) wv[u][e >> 1] |= b << 16;
-              else wv[u][e >> 1] = b;
+              for (int u = 0; u < 4; ++u)
+                if (x0 + u * kWave < spieces) s_slab[w][x0 + u * kWave] = v[u];
             }
           }
+          __syncthreads();
+          if (active) {
+            for (int y = lane; y < q * tpc; y += kWave) {
+              const int j = y / tpc, i0 = (y % tpc) * VE;
+              uint32_t wv[4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int y = y0 + u * kWave;
-            if (y < tpieces)
-              *(uint4*)(d + (int64_t)y * 16) = make_uint4(wv[u][0], wv[u][1], wv[u][2], wv[u][3]);
+              for (int e = 0; e < VE; ++e) {
+                const uint32_t b = (uint32_t)tile[(i0 + e) * q + j];
+                if constexpr (VE == 4) wv[e] = b;
+                else if (e & 1) wv[e >> 1] |= b << 16;
+                else wv[e >> 1] = b;
+              }
+              *(uint4*)(d + ((int64_t)j * p + r0 + i0) * EB) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+            }
           }
+          __syncthreads();
         }
       }
     }
@@ -419,11 +465,15 @@ int ssl_bsr_encode_fill(const void* S, int64_t lds, int64_t NB, int64_t NBK, int
   const int eb = (dtype == SSL_F32) ? 4 : 2;
   const bool vec = ((uintptr_t)S % 16 == 0) && (lds * eb) % 16 == 0 &&
                    (block_q * eb) % 16 == 0 && (uintptr_t)values_bsr % 16 == 0 &&
-                   (!values_t || ((uintptr_t)values_t % 16 == 0 && (block_p * eb) % 16 == 0));
+                   (!values_t || ((uintptr_t)values_t % 16 == 0 && (block_p * eb) % 16 == 0 &&
+                                  block_q <= 512));  // a slab holds 16 bytes of rows per column
   if (vec && (dtype == SSL_F32 || dtype == SSL_BF16 || dtype == SSL_F16)) {
+    // enough workgroups for about four per compute unit, at most 8 per block-row
+    const int64_t want = (4 * (int64_t)device_cus() + NB - 1) / NB;
+    const unsigned split = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, 8));
 #define SSL_FILL_VEC(DTC)                                                                         \
-  hipLaunchKernelGGL(bsr_fill_vec_kernel<DTC>, dim3((unsigned)NB), dim3(kThreads), 0, s, S, lds,   \
-                     (int)NBK, block_p, block_q, flags, crow, col, values_bsr, values_t)
+  hipLaunchKernelGGL(bsr_fill_vec_kernel<DTC>, dim3((unsigned)NB, split), dim3(kThreads), 0, s, S, \
+                     lds, (int)NBK, block_p, block_q, flags, crow, col, values_bsr, values_t)
     if (dtype == SSL_F32) SSL_FILL_VEC(DT_F32);
     else if (dtype == SSL_BF16) SSL_FILL_VEC(DT_BF16);
     else SSL_FILL_VEC(DT_F16);

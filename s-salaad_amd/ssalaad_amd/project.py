@@ -50,7 +50,8 @@ def block_topk(M: torch.Tensor, n_keep: int, block_p: int, block_q: int):
                 ws.data_ptr(), ws_bytes, _lib.stream_ptr(dev),
             )
         _lib.check(rc, "ssl_block_topk")
-    return (out, keep[: rb * cb].view(rb, cb).bool(), norms[: rb * cb].view(rb, cb))
+    # the kernels write keep bytes of exactly 0 and 1: a bool view, no copy
+    return (out, keep[: rb * cb].view(rb, cb).view(torch.bool), norms[: rb * cb].view(rb, cb))
 
 
 def project_S(M: torch.Tensor, n_keep: int, block_p: int, block_q: int) -> torch.Tensor:
@@ -83,7 +84,7 @@ def project_nm(R: torch.Tensor, nm_n: int, nm_m: int):
                                     _lib.dtype_code(R.dtype), out.data_ptr(), out.stride(0),
                                     keep.data_ptr(), keep.stride(0), _lib.stream_ptr(R.device))
         _lib.check(rc, "ssl_project_nm")
-    return out, keep.bool()
+    return out, keep.view(torch.bool)  # keep bytes of exactly 0 and 1
 
 
 def project_S_nm(R: torch.Tensor, nm_n: int, nm_m: int) -> torch.Tensor:

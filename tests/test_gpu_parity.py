@@ -653,7 +653,7 @@ def _special_matrix(n, m, p, q, dtype, seed):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
-@pytest.mark.parametrize("pq", [(16, 16), (32, 32), (64, 64), (16, 32)])
+@pytest.mark.parametrize("pq", [(16, 16), (32, 32), (64, 64), (16, 32), (32, 16), (64, 32), (8, 128)])
 def test_encoder_structure_is_bit_exact(dtype, pq, gpu_device):
     p, q = pq
     S = _special_matrix(6 * p, 9 * q, p, q, dtype, seed=p + q)
