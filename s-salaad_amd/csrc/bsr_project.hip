@@ -29,25 +29,19 @@ __device__ __forceinline__ float elem_f32(const void* base, int64_t i) {
 }
 
 // The many-workgroup select's workspace (32-bit words): per pass (one 8-bit
-// digit of the key each, most significant first) a 256-bin histogram and an
-// arrival count; per pass boundary the select's state {prefix, mask, need, eq}
-// (boundary 0: nothing chosen yet, need = n_keep; boundary 4: the threshold
-// key T, with need and eq the number of keys equal to T still to keep and
-// present); per workgroup its own last-pass histogram, whose bin of T counts
-// the keys equal to T in its range, for the ordered pass. The norms' launch
-// zeroes the shared part, so each call starts from zero whatever the last call
-// left.
+// digit of the key each, most significant first) a 256-bin histogram, then
+// per workgroup its own last-pass histogram, whose bin of the threshold key T
+// counts the keys equal to T in its range, for the ordered pass. The norms'
+// launch zeroes the pass histograms, so each call starts from zero whatever
+// the last call left.
 constexpr int kSelPasses = 4;
 constexpr int kWsHist = 0;  // [pass][256]
-constexpr int kWsTicket = kWsHist + 256 * kSelPasses;
-constexpr int kWsState = kWsTicket + 8;
-constexpr int kWsGroupHist = kWsState + 4 * (kSelPasses + 1) + 4;
+constexpr int kWsGroupHist = kWsHist + 256 * kSelPasses;
 constexpr int kMaxSelGroups = 1024;
 static_assert(kWsGroupHist % 4 == 0, "per-group histograms start on a 16-byte boundary");
 
-__device__ __forceinline__ void sel_ws_init(uint32_t* ws, int n_keep) {
-  for (int i = threadIdx.x; i < kWsGroupHist; i += blockDim.x)
-    ws[i] = i == kWsState + 2 ? (uint32_t)n_keep : 0u;
+__device__ __forceinline__ void sel_ws_init(uint32_t* ws) {
+  for (int i = threadIdx.x; i < kWsGroupHist; i += blockDim.x) ws[i] = 0u;
 }
 
 // One wave per block: the fp32 sum of squares (lane-strided partial sums, then a
@@ -55,9 +49,8 @@ __device__ __forceinline__ void sel_ws_init(uint32_t* ws, int n_keep) {
 template <int DT>
 __global__ __launch_bounds__(kThreads) void block_sumsq_kernel(const void* S, int64_t lds, int NB,
                                                                int NBK, int p, int q, bool vec,
-                                                               float* norms, uint32_t* sel_ws,
-                                                               int n_keep) {
-  if (sel_ws && blockIdx.x == 0) sel_ws_init(sel_ws, n_keep);
+                                                               float* norms, uint32_t* sel_ws) {
+  if (sel_ws && blockIdx.x == 0) sel_ws_init(sel_ws);
   const int lane = threadIdx.x & 63;
   const int64_t blk = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (blk >= (int64_t)NB * NBK) return;
@@ -117,8 +110,8 @@ constexpr int kSmallRounds = 4;
 template <int DT>
 __global__ __launch_bounds__(kThreads) void block_sumsq_small_kernel(
     const void* S, int64_t lds, int64_t nblocks, int NBK, int p, int q, int L, float* norms,
-    uint32_t* sel_ws, int n_keep) {
-  if (sel_ws && blockIdx.x == 0) sel_ws_init(sel_ws, n_keep);
+    uint32_t* sel_ws) {
+  if (sel_ws && blockIdx.x == 0) sel_ws_init(sel_ws);
   constexpr int EB = Elem<DT>::bytes, VE = 16 / EB;
   const int lane = threadIdx.x & 63;
   const int per_round = kWave / L, cpr = q / VE, pieces = p * cpr;
@@ -340,18 +333,58 @@ __device__ __forceinline__ int group_exclusive(int v, int& tot, int* s_wave) {
   return before + incl - v;
 }
 
+// The select's state after `passes` passes, from the finished histograms of
+// those passes (earlier launches): wave 0 repeats the digit search of each
+// pass in order, every workgroup the same way, and writes {prefix, mask, need,
+// eq} to st. Reading the histograms costs one round trip, which the caller
+// overlaps with its own key loads.
+__device__ __forceinline__ void sel_state(const uint32_t* ws, int passes, int n_keep,
+                                          uint32_t* st) {
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x >= kWave) return;
+  int h[kSelPasses][4];
+#pragma unroll
+  for (int ps = 0; ps < kSelPasses; ++ps)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      h[ps][b] = ps < passes ? (int)ws[kWsHist + 256 * ps + 4 * lane + b] : 0;
+  uint32_t prefix = 0u, mask = 0u;
+  int need = n_keep, eq = 0;
+#pragma unroll
+  for (int ps = 0; ps < kSelPasses; ++ps) {
+    if (ps >= passes) break;
+    int d = 0, cum = 0, cnt = 0;
+    const bool found = find_digit(h[ps], need, d, cum, cnt);
+    const int src = __ffsll((long long)__ballot(found)) - 1;
+    d = __shfl(d, src, kWave);
+    cum = __shfl(cum, src, kWave);
+    cnt = __shfl(cnt, src, kWave);
+    const int shift = 24 - 8 * ps;
+    prefix |= (uint32_t)d << shift;
+    mask |= 255u << shift;
+    need -= cum;
+    eq = cnt;
+  }
+  if (lane == 0) {
+    st[0] = prefix;
+    st[1] = mask;
+    st[2] = (uint32_t)need;
+    st[3] = (uint32_t)eq;
+  }
+}
+
 template <int PS>
 __global__ __launch_bounds__(kSelGroupThreads) void topk_hist_kernel(const float* norms, int n,
-                                                                     int chunk, uint32_t* ws) {
+                                                                     int chunk, int n_keep,
+                                                                     uint32_t* ws) {
   constexpr int SHIFT = 24 - 8 * PS;
   __shared__ int hist[256];
-  __shared__ int s_wave[kSelGroupThreads / kWave];
-  __shared__ int s_last;
+  __shared__ uint32_t s_st[4];
   const int t = threadIdx.x;
   int64_t i0, i1;
   group_range(n, chunk, i0, i1);
-  // The first round's keys are requested before the histogram is cleared, so
-  // their round trip overlaps the state's and the barrier.
+  // The first round's keys are requested first, so their round trip overlaps
+  // the state's (the earlier passes' histograms) and the barrier.
   constexpr int64_t kStep = kSelGroupThreads * kSelUnroll;
   uint32_t k[kSelUnroll];
   auto load_round = [&](int64_t b) {
@@ -363,9 +396,10 @@ __global__ __launch_bounds__(kSelGroupThreads) void topk_hist_kernel(const float
   };
   load_round(i0);
   hist[t] = 0;
-  const uint32_t* st = ws + kWsState + 4 * PS;
-  const uint32_t prefix = st[0], mask = st[1];
+  if constexpr (PS > 0) sel_state(ws, PS, n_keep, s_st);
+  else if (t == 0) s_st[0] = s_st[1] = 0u;
   __syncthreads();
+  const uint32_t prefix = s_st[0], mask = s_st[1];
   for (int64_t b = i0; b < i1; b += kStep) {
 #pragma unroll
     for (int u = 0; u < kSelUnroll; ++u) {
@@ -375,33 +409,12 @@ __global__ __launch_bounds__(kSelGroupThreads) void topk_hist_kernel(const float
     if (b + kStep < i1) load_round(b + kStep);
   }
   __syncthreads();
-  int* gh = (int*)ws + kWsHist + 256 * PS;
   const int mine = hist[t];
-  if (mine) __hip_atomic_fetch_add(gh + t, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (mine)
+    __hip_atomic_fetch_add((int*)ws + kWsHist + 256 * PS + t, mine, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
   // this group's keys per last digit, for the ranks of keys equal to T
   if constexpr (PS == kSelPasses - 1) ws[kWsGroupHist + (int64_t)blockIdx.x * 256 + t] = mine;
-  // The adds are acknowledged before this group's arrival is counted, so the
-  // group that counts last reads every group's adds.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (t == 0)
-    s_last = __hip_atomic_fetch_add((int*)ws + kWsTicket + PS, 1, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
-  __syncthreads();
-  if (!s_last || t >= kWave) return;
-  int h[4];
-#pragma unroll
-  for (int b = 0; b < 4; ++b)
-    h[b] = __hip_atomic_load(gh + 4 * t + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int need0 = (int)st[2];
-  int d, cum, cnt;
-  if (find_digit(h, need0, d, cum, cnt)) {
-    uint32_t* nx = ws + kWsState + 4 * (PS + 1);
-    nx[0] = prefix | ((uint32_t)d << SHIFT);
-    nx[1] = mask | (255u << SHIFT);
-    nx[2] = (uint32_t)(need0 - cum);
-    nx[3] = (uint32_t)cnt;
-  }
 }
 
 // Ordered pass over [i0, i1): thread t takes kTiePer consecutive keys of each
@@ -435,9 +448,11 @@ __device__ __forceinline__ void tie_pass(const float* norms, int64_t i0, int64_t
 // keep[i] for the group's range: fill ≥ 0 writes that value (n_keep ≤ 0 or
 // ≥ n), else the select's result.
 __global__ __launch_bounds__(kSelGroupThreads) void topk_mark_kernel(const float* norms, int n,
-                                                                     int chunk, const uint32_t* ws,
-                                                                     int fill, uint8_t* keep) {
+                                                                     int chunk, int n_keep,
+                                                                     const uint32_t* ws, int fill,
+                                                                     uint8_t* keep) {
   __shared__ int s_wave[kSelGroupThreads / kWave];
+  __shared__ uint32_t s_st[4];
   const int t = threadIdx.x;
   int64_t i0, i1;
   group_range(n, chunk, i0, i1);
@@ -445,10 +460,11 @@ __global__ __launch_bounds__(kSelGroupThreads) void topk_mark_kernel(const float
     for (int64_t i = i0 + t; i < i1; i += kSelGroupThreads) keep[i] = (uint8_t)fill;
     return;
   }
-  const uint32_t* st = ws + kWsState + 4 * kSelPasses;
-  const uint32_t T = st[0];
-  const int need = (int)st[2];
-  if (st[2] == st[3]) {
+  sel_state(ws, kSelPasses, n_keep, s_st);
+  __syncthreads();
+  const uint32_t T = s_st[0];
+  const int need = (int)s_st[2];
+  if (s_st[2] == s_st[3]) {
     // every key equal to T is kept: no ranks needed
     for (int64_t b = i0; b < i1; b += kSelGroupThreads * kSelUnroll) {
       uint32_t k[kSelUnroll];
@@ -689,10 +705,10 @@ int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t 
 #define SSL_PROJECT(DTC)                                                                       \
   if (small)                                                                                    \
     hipLaunchKernelGGL(block_sumsq_small_kernel<DTC>, dim3(small_grid), dim3(kThreads), 0, s, S, \
-                       lds, nblocks, (int)NBK, block_p, block_q, lanes, norms, init_ws, keep_n); \
+                       lds, nblocks, (int)NBK, block_p, block_q, lanes, norms, init_ws);         \
   else                                                                                          \
     hipLaunchKernelGGL(block_sumsq_kernel<DTC>, dim3(grid), dim3(kThreads), 0, s, S, lds,        \
-                       (int)NB, (int)NBK, block_p, block_q, vec_in, norms, init_ws, keep_n);    \
+                       (int)NB, (int)NBK, block_p, block_q, vec_in, norms, init_ws);            \
   if (!many && nblocks <= kLdsKeys)                                                              \
     hipLaunchKernelGGL(block_topk_kernel<true>, dim3(1), dim3(kSelThreads),                      \
                        (unsigned)(4 * nblocks), s, norms, (int)nblocks, keep_n, keep);           \
@@ -701,18 +717,18 @@ int ssl_block_topk(const void* S, int64_t lds, int64_t NB, int64_t NBK, int32_t 
                        (int)nblocks, keep_n, keep);                                             \
   else if (fill)                                                                                \
     hipLaunchKernelGGL(topk_mark_kernel, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,      \
-                       (int)nblocks, chunk, ws, keep_n > 0 ? 1 : 0, keep);                      \
+                       (int)nblocks, chunk, keep_n, ws, keep_n > 0 ? 1 : 0, keep);              \
   else {                                                                                        \
     hipLaunchKernelGGL(topk_hist_kernel<0>, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,   \
-                       (int)nblocks, chunk, ws);                                                \
+                       (int)nblocks, chunk, keep_n, ws);                                        \
     hipLaunchKernelGGL(topk_hist_kernel<1>, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,   \
-                       (int)nblocks, chunk, ws);                                                \
+                       (int)nblocks, chunk, keep_n, ws);                                        \
     hipLaunchKernelGGL(topk_hist_kernel<2>, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,   \
-                       (int)nblocks, chunk, ws);                                                \
+                       (int)nblocks, chunk, keep_n, ws);                                        \
     hipLaunchKernelGGL(topk_hist_kernel<3>, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,   \
-                       (int)nblocks, chunk, ws);                                                \
+                       (int)nblocks, chunk, keep_n, ws);                                        \
     hipLaunchKernelGGL(topk_mark_kernel, dim3(groups), dim3(kSelGroupThreads), 0, s, norms,      \
-                       (int)nblocks, chunk, ws, -1, keep);                                      \
+                       (int)nblocks, chunk, keep_n, ws, -1, keep);                              \
   }                                                                                             \
   if (out)                                                                                      \
     hipLaunchKernelGGL(block_mask_kernel<DTC>, mgrid, dim3(kThreads), 0, s, S, lds, n, m,        \
