@@ -334,7 +334,8 @@ __device__ __forceinline__ int group_exclusive(int v, int& tot, int* s_wave) {
 }
 
 // The select's state after `passes` passes, from the finished histograms of
-// those passes (earlier launches): wave 0 repeats the digit search of each
+// those passes (earlier launches, read device-coherently like the atomics
+// that built them): wave 0 repeats the digit search of each
 // pass in order, every workgroup the same way, and writes {prefix, mask, need,
 // eq} to st. Reading the histograms costs one round trip, which the caller
 // overlaps with its own key loads.
@@ -347,7 +348,9 @@ __device__ __forceinline__ void sel_state(const uint32_t* ws, int passes, int n_
   for (int ps = 0; ps < kSelPasses; ++ps)
 #pragma unroll
     for (int b = 0; b < 4; ++b)
-      h[ps][b] = ps < passes ? (int)ws[kWsHist + 256 * ps + 4 * lane + b] : 0;
+      h[ps][b] = ps < passes ? __hip_atomic_load((const int*)ws + kWsHist + 256 * ps + 4 * lane + b,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : 0;
   uint32_t prefix = 0u, mask = 0u;
   int need = n_keep, eq = 0;
 #pragma unroll
