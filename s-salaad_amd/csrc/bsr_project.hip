@@ -45,7 +45,9 @@ __device__ __forceinline__ void sel_ws_init(uint32_t* ws) {
 }
 
 // One wave per block: the fp32 sum of squares (lane-strided partial sums, then a
-// fixed butterfly, so repeated runs give identical bits).
+// fixed butterfly, so repeated runs give identical bits). A lane takes pieces
+// lane, lane + 64, ... in that order, kSumsqUnroll loads at a time.
+constexpr int kSumsqUnroll = 8;
 template <int DT>
 __global__ __launch_bounds__(kThreads) void block_sumsq_kernel(const void* S, int64_t lds, int NB,
                                                                int NBK, int p, int q, bool vec,
@@ -61,17 +63,17 @@ __global__ __launch_bounds__(kThreads) void block_sumsq_kernel(const void* S, in
   if (vec) {
     // pieces of VE elements: cpr per block row, all rows
     const int cpr = q / VE, pieces = p * cpr;
-    for (int idx0 = lane; idx0 < pieces; idx0 += 4 * kWave) {
-      uint4 v4[4];
+    for (int idx0 = lane; idx0 < pieces; idx0 += kSumsqUnroll * kWave) {
+      uint4 v4[kSumsqUnroll];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kSumsqUnroll; ++u) {
         const int idx = idx0 + u * kWave;
         const int i = idx / cpr, j = (idx % cpr) * VE;
         v4[u] = idx < pieces ? *(const uint4*)((const char*)S + (base + (int64_t)i * lds + j) * EB)
                              : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kSumsqUnroll; ++u) {
         const uint32_t w[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
