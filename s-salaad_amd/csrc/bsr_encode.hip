@@ -269,9 +269,10 @@ __global__ __launch_bounds__(kScanThreads) void bsr_scan_counts_kernel(int NB, i
   }
 }
 
-// gridDim.y workgroups per block-row, one wave per kept block (four at a time): the
-// (p, q) copy in 16-byte pieces; the (q, p) copy through LDS, in slabs of SR
-// rows (a multiple of VE, at most 8 KiB of the block per wave): the slab's
+// gridDim.y workgroups per block-row, each wave BPW kept blocks a round (small
+// blocks) or one: the (p, q) copy in 16-byte pieces; the (q, p) copy through
+// LDS, whole small blocks or slabs of SR rows (a multiple of VE, at most 8 KiB
+// of the block per wave): the slab's
 // pieces are stored row-major, then each lane gathers VE consecutive rows of
 // one column and stores them as one 16-byte piece (VT needs p a multiple of VE
 // and q at most 512, so that a slab holds at least VE rows).
@@ -291,7 +292,11 @@ __global__ __launch_bounds__(kThreads) void bsr_fill_vec_kernel(const void* S, i
   const int by = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
   const uint8_t* f = flags + (int64_t)by * NBK;
   const int cpr = q / VE, pieces = p * cpr;
-  const int SR = min(p, kSlabBytes / (q * EB) / VE * VE);
+  // Blocks of at most half a slab: BPW whole blocks per wave and round, one
+  // slab each; larger blocks: one block per wave, in slabs of SR rows.
+  const int blk_bytes = p * q * EB;
+  const int BPW = blk_bytes <= kSlabBytes / 2 ? min(16, kSlabBytes / blk_bytes) : 1;
+  const int SR = BPW > 1 ? p : min(p, kSlabBytes / (q * EB) / VE * VE);
   const T* tile = (const T*)s_slab[w];
   int base = crow[by];
   for (int c0 = 0; c0 < NBK; c0 += SEG) {
@@ -316,65 +321,74 @@ __global__ __launch_bounds__(kThreads) void bsr_fill_vec_kernel(const void* S, i
       if (f[j]) s_cols[pos++] = j;
     __syncthreads();
     const int nseg = s_nseg;
-    // rounds of four blocks, the same count in every wave (the slab barriers);
-    // workgroup z of the row takes rounds z, z + gridDim.y, ...
-    for (int k0 = blockIdx.y * kWaves; k0 < nseg; k0 += kWaves * gridDim.y) {
-      const int k = k0 + w;
-      const bool active = k < nseg;
-      const int bc = active ? s_cols[k] : 0;
-      const int64_t dst = (int64_t)base + k;
-      const char* src = (const char*)S + ((int64_t)by * p * lds + (int64_t)bc * q) * EB;
-      if (active && lane == 0) col[dst] = bc;
-      if (active && vbsr) {
-        char* d = (char*)vbsr + dst * p * q * EB;
-        for (int x0 = lane; x0 < pieces; x0 += 4 * kWave) {
+    // rounds of 4·BPW blocks, the same count in every wave (the slab barriers);
+    // workgroup z of the row takes rounds z, z + gridDim.y, ...; wave w takes
+    // the round's blocks kw .. kw + nb - 1
+    for (int k0 = blockIdx.y * kWaves * BPW; k0 < nseg; k0 += kWaves * BPW * gridDim.y) {
+      const int kw = k0 + w * BPW;
+      const int nb = max(0, min(BPW, nseg - kw));
+      auto src_of = [&](int bi) {
+        return (const char*)S + ((int64_t)by * p * lds + (int64_t)s_cols[kw + bi] * q) * EB;
+      };
+      if (lane < nb) col[(int64_t)base + kw + lane] = s_cols[kw + lane];
+      if (vbsr) {
+        const int total = nb * pieces;
+        for (int x0 = lane; x0 < total; x0 += 4 * kWave) {
           uint4 v[4];
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int x = x0 + u * kWave;
             v[u] = make_uint4(0, 0, 0, 0);
-            if (x < pieces) v[u] = *(const uint4*)(src + ((int64_t)(x / cpr) * lds + (x % cpr) * VE) * EB);
+            if (x < total) {
+              const int bi = x / pieces, xx = x % pieces;
+              v[u] = *(const uint4*)(src_of(bi) + ((int64_t)(xx / cpr) * lds + (xx % cpr) * VE) * EB);
+            }
           }
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int x = x0 + u * kWave;
-            if (x < pieces) *(uint4*)(d + (int64_t)x * 16) = v[u];
+            if (x < total) {
+              const int bi = x / pieces, xx = x % pieces;
+              *(uint4*)((char*)vbsr + ((int64_t)base + kw + bi) * blk_bytes + (int64_t)xx * 16) = v[u];
+            }
           }
         }
       }
       if (vt) {
-        char* d = (char*)vt + dst * p * q * EB;
         for (int r0 = 0; r0 < p; r0 += SR) {
           const int nr = min(SR, p - r0), spieces = nr * cpr, tpc = nr / VE;
-          if (active) {
-            for (int x0 = lane; x0 < spieces; x0 += 4 * kWave) {
-              uint4 v[4];
+          const int total = nb * spieces;  // at most kSlabBytes / 16 pieces
+          for (int x0 = lane; x0 < total; x0 += 4 * kWave) {
+            uint4 v[4];
 #pragma unroll
-              for (int u = 0; u < 4; ++u) {
-                const int x = x0 + u * kWave;
-                v[u] = make_uint4(0, 0, 0, 0);
-                if (x < spieces)
-                  v[u] = *(const uint4*)(src + ((int64_t)(r0 + x / cpr) * lds + (x % cpr) * VE) * EB);
+            for (int u = 0; u < 4; ++u) {
+              const int x = x0 + u * kWave;
+              v[u] = make_uint4(0, 0, 0, 0);
+              if (x < total) {
+                const int bi = x / spieces, xx = x % spieces;
+                v[u] = *(const uint4*)(src_of(bi) + ((int64_t)(r0 + xx / cpr) * lds + (xx % cpr) * VE) * EB);
               }
-#pragma unroll
-              for (int u = 0; u < 4; ++u)
-                if (x0 + u * kWave < spieces) s_slab[w][x0 + u * kWave] = v[u];
             }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              if (x0 + u * kWave < total) s_slab[w][x0 + u * kWave] = v[u];
           }
           __syncthreads();
-          if (active) {
-            for (int y = lane; y < q * tpc; y += kWave) {
-              const int j = y / tpc, i0 = (y % tpc) * VE;
-              uint32_t wv[4];
+          const int tp = q * tpc, ttotal = nb * tp;
+          for (int y = lane; y < ttotal; y += kWave) {
+            const int bi = y / tp, yy = y % tp;
+            const int j = yy / tpc, i0 = (yy % tpc) * VE;
+            const T* tb = tile + bi * (nr * q);
+            uint32_t wv[4];
 #pragma unroll
-              for (int e = 0; e < VE; ++e) {
-                const uint32_t b = (uint32_t)tile[(i0 + e) * q + j];
-                if constexpr (VE == 4) wv[e] = b;
-                else if (e & 1) wv[e >> 1] |= b << 16;
-                else wv[e >> 1] = b;
-              }
-              *(uint4*)(d + ((int64_t)j * p + r0 + i0) * EB) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+            for (int e = 0; e < VE; ++e) {
+              const uint32_t bits = (uint32_t)tb[(i0 + e) * q + j];
+              if constexpr (VE == 4) wv[e] = bits;
+              else if (e & 1) wv[e >> 1] |= bits << 16;
+              else wv[e >> 1] = bits;
             }
+            *(uint4*)((char*)vt + ((int64_t)base + kw + bi) * blk_bytes + ((int64_t)j * p + r0 + i0) * EB) =
+                make_uint4(wv[0], wv[1], wv[2], wv[3]);
           }
           __syncthreads();
         }
