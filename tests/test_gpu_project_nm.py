@@ -88,6 +88,20 @@ def test_project_nm_reference_case_and_strided_input(gpu_device):
     assert _bits_equal(out.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("nm_n,nm_m", [(2, 4), (4, 8), (8, 16)])
+def test_project_nm_misaligned_rows_take_the_scalar_path(nm_n, nm_m, gpu_device):
+    """Groups that start 8 bytes past a 16-byte boundary (an fp32 view from
+    column 2, rows of 3·nm_m + 6 columns) take the per-element path, with the
+    same results."""
+    big = torch.randn(33, 3 * nm_m + 6, device=gpu_device)
+    view = big[:, 2:2 + 3 * nm_m]
+    assert view.data_ptr() % 16 != 0
+    out, keep = ssalaad_amd.project_nm(view, nm_n, nm_m)
+    want, wmask = orc.project_nm(view.cpu().numpy(), nm_n, nm_m)
+    assert np.array_equal(keep.cpu().numpy(), wmask)
+    assert _bits_equal(out.cpu().numpy(), want)
+
+
 def test_project_nm_rejects_what_the_reference_rejects(gpu_device):
     R = torch.randn(4, 10, device=gpu_device)
     with pytest.raises(RuntimeError, match="invalid for input of size"):
